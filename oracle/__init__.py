@@ -1,0 +1,311 @@
+"""CPU oracle for the chromoFold hot path — TEST INFRASTRUCTURE ONLY.
+
+ctypes bindings over ``oracle/liboracle.so`` (built from ``oracle/*.cpp`` by ``oracle/Makefile``). Only
+``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import this package, and only
+as the checker or the timed CPU baseline; the product package ``chromofold_amd`` never imports it.
+
+Each wrapper names the reference function it restates; the C++ sources carry the file:line citations.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_DIR = os.path.join(HERE, "_ref")
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle library missing: {LIB_PATH} (run `make -C oracle`)")
+        _lib = C.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+P = C.c_void_p
+I32, I64, U32 = C.c_int32, C.c_int64, C.c_uint32
+
+
+def _ptr(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+class OrRrrw(C.Structure):
+    _fields_ = [("classes", P), ("offsets", P), ("rank_a", P), ("rank_d", P), ("off_a", P), ("off_d", P),
+                ("offbase", P), ("zeros", P), ("bits", C.c_int), ("cwords", C.c_int), ("nsb", C.c_int),
+                ("na", C.c_int)]
+
+
+class OrFm(C.Structure):
+    _fields_ = [("w", OrRrrw), ("C", P), ("mwords", P), ("msb", P), ("sval", P), ("sigma", C.c_int),
+                ("n", C.c_int), ("sa_sample", C.c_int)]
+
+
+def _declare(L):
+    sig = {
+        "or_rrr_tables": (None, [P, P]),
+        "or_num_threads": (C.c_int, []),
+        "or_set_threads": (None, [C.c_int]),
+        "or_rrrw_build": (P, [P, I64, C.c_int]),
+        "or_rrrw_info": (None, [P, P]),
+        "or_rrrw_copy": (None, [P] * 9),
+        "or_rrrw_free": (None, [P]),
+        "or_rrrw_rank1": (C.c_int, [P, C.c_int, C.c_int]),
+        "or_rrrw_access": (None, [P, P, P, I64]),
+        "or_rrrw_rank": (None, [P, P, P, P, I64]),
+        "or_suffix_array_doubling": (None, [P, I32, P]),
+        "or_suffix_array_radix": (None, [P, I32, P]),
+        "or_fm_build": (I32, [P, P, I32, I32, I32, P, P, P, P]),
+        "or_fm_ranges": (None, [P, P, P, P, P, P, I64]),
+        "or_fm_count": (None, [P, P, P, P, P, I64]),
+        "or_fm_locate": (None, [P, P, P, I64]),
+        "or_naive_positions": (I64, [P, I64, P, C.c_int, P, I64]),
+        "or_packed_build": (None, [P, I64, C.c_int, P, P, P]),
+        "or_packed_access": (None, [P, P, P, C.c_int, C.c_int, C.c_int, P, P, I64]),
+        "or_packed_rank": (None, [P, P, P, C.c_int, C.c_int, C.c_int, P, P, P, I64]),
+        "or_packed_rank1": (C.c_int, [P, P, C.c_int]),
+        "or_rrr_rank1": (None, [P, P, P, P, P, P, I64]),
+        "or_rrr_plane_build": (P, [P, I64]),
+        "or_rrr_plane_info": (None, [P, P]),
+        "or_rrr_plane_copy": (None, [P, P, P, P, P]),
+        "or_rrr_plane_free": (None, [P]),
+        "or_rrr_decode_all": (None, [P, P, I64, I64, P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name, None)
+        if fn is None:
+            continue
+        fn.restype = res
+        fn.argtypes = args
+
+
+def set_threads(t: int) -> None:
+    lib().or_set_threads(int(t))
+
+
+def num_threads() -> int:
+    return int(lib().or_num_threads())
+
+
+def rrr_tables() -> tuple[np.ndarray, np.ndarray]:
+    """binom[16*16] and width[16] (reference tools/build_index.cpp:31-42)."""
+    b = np.zeros(256, np.int32)
+    w = np.zeros(16, np.int32)
+    lib().or_rrr_tables(_ptr(b), _ptr(w))
+    return b, w
+
+
+# ------------------------------------------------------------------ RRR wavelet matrix
+@dataclass
+class RrrwArrays:
+    """Host arrays of an RRR wavelet matrix, field-for-field the cf_rrrw_view / .cfrw payload."""
+    bits: int
+    cwords: int
+    nsb: int
+    na: int
+    classes: np.ndarray
+    offsets: np.ndarray
+    rank_a: np.ndarray
+    rank_d: np.ndarray
+    off_a: np.ndarray
+    off_d: np.ndarray
+    offbase: np.ndarray
+    zeros: np.ndarray
+    rrr_bytes: int = 0
+
+    def view(self) -> OrRrrw:
+        return OrRrrw(_ptr(self.classes), _ptr(self.offsets), _ptr(self.rank_a), _ptr(self.rank_d),
+                      _ptr(self.off_a), _ptr(self.off_d), _ptr(self.offbase), _ptr(self.zeros),
+                      self.bits, self.cwords, self.nsb, self.na)
+
+
+def rrrw_build(tokens: np.ndarray, bits: int) -> RrrwArrays:
+    """RRR wavelet matrix of `tokens` (reference tools/build_index.cpp:172-218)."""
+    tok = np.ascontiguousarray(tokens, dtype=np.uint32)
+    L = lib()
+    h = L.or_rrrw_build(_ptr(tok), tok.size, bits)
+    info = np.zeros(10, np.int64)
+    L.or_rrrw_info(h, _ptr(info))
+    b, cw, nsb, na, ow, ncls, nra, nrd, rb = (int(x) for x in info[:9])
+    a = RrrwArrays(b, cw, nsb, na, np.zeros(ncls, np.uint32), np.zeros(ow, np.uint32), np.zeros(nra, np.int32),
+                   np.zeros(nrd, np.uint16), np.zeros(nra, np.int32), np.zeros(nrd, np.uint16),
+                   np.zeros(b, np.int32), np.zeros(b, np.int32), rb)
+    L.or_rrrw_copy(h, _ptr(a.classes), _ptr(a.offsets), _ptr(a.rank_a), _ptr(a.rank_d), _ptr(a.off_a),
+                   _ptr(a.off_d), _ptr(a.offbase), _ptr(a.zeros))
+    L.or_rrrw_free(h)
+    return a
+
+
+def rrrw_access(w: RrrwArrays, pos: np.ndarray) -> np.ndarray:
+    pos = np.ascontiguousarray(pos, np.uint32)
+    out = np.zeros(pos.size, np.uint32)
+    v = w.view()
+    lib().or_rrrw_access(C.byref(v), _ptr(pos), _ptr(out), pos.size)
+    return out
+
+
+def rrrw_rank(w: RrrwArrays, sym: np.ndarray, pos: np.ndarray) -> np.ndarray:
+    sym = np.ascontiguousarray(sym, np.uint32)
+    pos = np.ascontiguousarray(pos, np.uint32)
+    out = np.zeros(pos.size, np.uint32)
+    v = w.view()
+    lib().or_rrrw_rank(C.byref(v), _ptr(sym), _ptr(pos), _ptr(out), pos.size)
+    return out
+
+
+# ------------------------------------------------------------------ suffix array / FM-index
+def suffix_array(s: np.ndarray, method: str = "radix") -> np.ndarray:
+    s = np.ascontiguousarray(s, np.int32)
+    sa = np.zeros(s.size, np.int32)
+    fn = lib().or_suffix_array_radix if method == "radix" else lib().or_suffix_array_doubling
+    fn(_ptr(s), s.size, _ptr(sa))
+    return sa
+
+
+@dataclass
+class FmArrays:
+    w: RrrwArrays
+    C: np.ndarray
+    mwords: np.ndarray
+    msb: np.ndarray
+    sval: np.ndarray
+    sigma: int
+    n: int
+    sa_sample: int
+
+    def view(self) -> OrFm:
+        return OrFm(self.w.view(), _ptr(self.C), _ptr(self.mwords), _ptr(self.msb), _ptr(self.sval), self.sigma,
+                    self.n, self.sa_sample)
+
+
+def fm_text(tokens: np.ndarray) -> np.ndarray:
+    """s = (tokens + 1) ++ [0] (reference tools/build_index.cpp:369-371)."""
+    s = np.empty(tokens.size + 1, np.int32)
+    s[:-1] = np.asarray(tokens, np.int64) + 1
+    s[-1] = 0
+    return s
+
+
+def fm_build(tokens: np.ndarray, sa_sample: int, sa: np.ndarray | None = None) -> tuple[FmArrays, np.ndarray]:
+    """Full FM build: SA -> BWT -> RRR wavelet -> C/marks/msb/sval (reference build_index.cpp:368-469)."""
+    s = fm_text(tokens)
+    n = s.size
+    if sa is None:
+        sa = suffix_array(s)
+    bwt = s[(sa.astype(np.int64) - 1) % n].astype(np.int32)
+    sigma = int(bwt.max()) + 1
+    bits = max(1, int(sigma - 1).bit_length())
+    w = rrrw_build(bwt.astype(np.uint32), bits)
+    nw = (n + 31) // 32
+    nb = (nw + 7) // 8
+    Ct = np.zeros(sigma, np.int32)
+    mw = np.zeros(nw, np.uint32)
+    msb = np.zeros(nb + 1, np.int32)
+    sval = np.zeros(n // sa_sample + 2, np.int32)
+    ns = lib().or_fm_build(_ptr(sa), _ptr(bwt), n, sigma, sa_sample, _ptr(Ct), _ptr(mw), _ptr(msb), _ptr(sval))
+    return FmArrays(w, Ct, mw, msb, sval[:ns].copy(), sigma, n, sa_sample), bwt
+
+
+def fm_ranges(f: FmArrays, pat: np.ndarray, pstart: np.ndarray, plen: np.ndarray):
+    lo = np.zeros(pstart.size, np.int32)
+    hi = np.zeros(pstart.size, np.int32)
+    v = f.view()
+    lib().or_fm_ranges(C.byref(v), _ptr(pat), _ptr(pstart), _ptr(plen), _ptr(lo), _ptr(hi), pstart.size)
+    return lo, hi
+
+
+def fm_count(f: FmArrays, pat: np.ndarray, pstart: np.ndarray, plen: np.ndarray) -> np.ndarray:
+    out = np.zeros(pstart.size, np.uint32)
+    v = f.view()
+    lib().or_fm_count(C.byref(v), _ptr(pat), _ptr(pstart), _ptr(plen), _ptr(out), pstart.size)
+    return out
+
+
+def fm_locate(f: FmArrays, rows: np.ndarray) -> np.ndarray:
+    rows = np.ascontiguousarray(rows, np.int32)
+    out = np.zeros(rows.size, np.int32)
+    v = f.view()
+    lib().or_fm_locate(C.byref(v), _ptr(rows), _ptr(out), rows.size)
+    return out
+
+
+def naive_positions(seq: np.ndarray, pat: np.ndarray, cap: int = 1 << 20) -> np.ndarray:
+    seq = np.ascontiguousarray(seq, np.int32)
+    pat = np.ascontiguousarray(pat, np.int32)
+    out = np.zeros(cap, np.int32)
+    k = lib().or_naive_positions(_ptr(seq), seq.size, _ptr(pat), pat.size, _ptr(out), cap)
+    return out[:min(k, cap)].copy()
+
+
+def naive_count(seq: np.ndarray, pat: np.ndarray) -> int:
+    seq = np.ascontiguousarray(seq, np.int32)
+    pat = np.ascontiguousarray(pat, np.int32)
+    return int(lib().or_naive_positions(_ptr(seq), seq.size, _ptr(pat), pat.size, None, 0))
+
+
+# ------------------------------------------------------------------ packed wavelet / RRR bitvector
+def packed_build(tokens: np.ndarray, levels: int):
+    tok = np.ascontiguousarray(tokens, np.uint32)
+    n = tok.size
+    nwords = (n + 31) // 32
+    nblocks = (nwords + 7) // 8
+    bp = np.zeros(levels * nwords, np.uint32)
+    sb = np.zeros(levels * (nblocks + 1), np.int32)
+    z = np.zeros(levels, np.int32)
+    lib().or_packed_build(_ptr(tok), n, levels, _ptr(bp), _ptr(sb), _ptr(z))
+    return bp, sb, z, nwords, nblocks
+
+
+def packed_access(bp, sb, z, levels, nwords, nblocks, pos):
+    pos = np.ascontiguousarray(pos, np.uint32)
+    out = np.zeros(pos.size, np.uint32)
+    lib().or_packed_access(_ptr(bp), _ptr(sb), _ptr(z), levels, nwords, nblocks, _ptr(pos), _ptr(out), pos.size)
+    return out
+
+
+def packed_rank(bp, sb, z, levels, nwords, nblocks, sym, pos):
+    sym = np.ascontiguousarray(sym, np.uint32)
+    pos = np.ascontiguousarray(pos, np.uint32)
+    out = np.zeros(pos.size, np.uint32)
+    lib().or_packed_rank(_ptr(bp), _ptr(sb), _ptr(z), levels, nwords, nblocks, _ptr(sym), _ptr(pos), _ptr(out),
+                         pos.size)
+    return out
+
+
+def rrr_rank1(classes, offsets, sbrank, sboff, pos) -> np.ndarray:
+    pos = np.ascontiguousarray(pos, np.uint32)
+    out = np.zeros(pos.size, np.uint32)
+    lib().or_rrr_rank1(_ptr(classes), _ptr(offsets), _ptr(sbrank), _ptr(sboff), _ptr(pos), _ptr(out), pos.size)
+    return out
+
+
+def rrr_plane_build(bits01: np.ndarray):
+    b = np.ascontiguousarray(bits01, np.uint8)
+    L = lib()
+    h = L.or_rrr_plane_build(_ptr(b), b.size)
+    info = np.zeros(7, np.int64)
+    L.or_rrr_plane_info(h, _ptr(info))
+    nblocks, nsb, cwords, owords = (int(x) for x in info[:4])
+    cls = np.zeros(cwords, np.uint32)
+    off = np.zeros(owords, np.uint32)
+    sbr = np.zeros(nsb + 1, np.int32)
+    sbo = np.zeros(nsb + 1, np.int32)
+    L.or_rrr_plane_copy(h, _ptr(cls), _ptr(off), _ptr(sbr), _ptr(sbo))
+    L.or_rrr_plane_free(h)
+    return dict(nblocks=nblocks, nsb=nsb, cwords=cwords, owords=owords, class_bits=int(info[4]),
+                offset_bits=int(info[5]), zeros=int(info[6]), classes=cls, offsets=off, sbrank=sbr, sboff=sbo)
+
+
+def rrr_decode_all(classes, offsets, nblocks: int, off_base_bit: int = 0) -> np.ndarray:
+    out = np.zeros(nblocks * 15, np.uint8)
+    lib().or_rrr_decode_all(_ptr(classes), _ptr(offsets), nblocks, off_base_bit, _ptr(out))
+    return out
