@@ -1,0 +1,118 @@
+// cf_device.hpp — device-side building blocks shared by the gfx950 kernels of libchromofold.
+//
+// Everything here is written for the CDNA4 wave64 execution model: lane masks are 64-bit, cross-lane sums use
+// ballot/mbcnt, and tables that every lane indexes at random are either compile-time constants (read through the
+// scalar or vector cache) or staged into LDS by the kernel that needs them.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "chromofold/chromofold.h"
+
+namespace cfd {
+
+// ------------------------------------------------------------------------------------------------ launch helpers
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Status of the launch just issued: a launch-configuration error is reported synchronously as CF_ERR_CUDA
+// (the name is kept for ABI compatibility; it means "the HIP runtime rejected the call").
+inline cf_status launch_status() { return hipPeekAtLastError() == hipSuccess ? CF_OK : CF_ERR_CUDA; }
+
+inline unsigned grid_for(size_t work, unsigned per_block) {
+  return static_cast<unsigned>((work + per_block - 1) / per_block);
+}
+
+// ------------------------------------------------------------------------------------------------ RRR constants
+// T = 15-bit blocks, S = 64 blocks per rank superblock, K = 32 superblocks per int32 anchor. These are baked into
+// the .cfrw/.cffm formats (reference include/chromofold/detail/rrr_wavelet_device.cuh:16-18).
+constexpr int kRrrT = 15;
+constexpr int kRrrS = 64;
+constexpr int kRrrK = 32;
+
+struct RrrTables {
+  // width[k] = ceil(log2 C(15,k)), 0 when C(15,k) <= 1 — the enumerative-offset width of a class-k block.
+  int width[16];
+  // base[k] = sum_{j<k} C(15,j): start of class k inside the unrank table.
+  int base[17];
+  // unrank[base[k] + r] = the 15-bit word with k ones whose combinatorial-number-system rank is r
+  // (rank = sum over set bit positions c, taken in increasing order with i = 1..k, of C(c, i)).
+  uint16_t unrank[1 << kRrrT];
+};
+
+constexpr int64_t binom_ce(int n, int k) {
+  if (k < 0 || k > n) return 0;
+  int64_t r = 1;
+  for (int i = 1; i <= k; ++i) r = r * (n - k + i) / i;
+  return r;
+}
+
+constexpr RrrTables make_rrr_tables() {
+  RrrTables t{};
+  int64_t C[16][16] = {};
+  for (int n = 0; n < 16; ++n) {
+    C[n][0] = 1;
+    for (int k = 1; k <= n; ++k) C[n][k] = C[n - 1][k - 1] + C[n - 1][k];
+  }
+  int at = 0;
+  for (int k = 0; k <= 15; ++k) {
+    const int64_t c = C[kRrrT][k];
+    int w = 0;
+    while ((int64_t(1) << w) < c) ++w;
+    t.width[k] = c > 1 ? w : 0;
+    t.base[k] = at;
+    at += static_cast<int>(c);
+  }
+  t.base[16] = at;
+  // Enumerate every 15-bit word once and drop it at its class/rank slot: the rank of a word with set positions
+  // c_1 < c_2 < ... < c_k is sum_i C(c_i, i) (the encoder's formula, reference tools/build_index.cpp:90-148).
+  for (int word = 0; word < (1 << kRrrT); ++word) {
+    int k = 0;
+    int64_t r = 0;
+    for (int c = 0; c < kRrrT; ++c)
+      if ((word >> c) & 1) {
+        ++k;
+        r += C[c][k];
+      }
+    t.unrank[t.base[k] + r] = static_cast<uint16_t>(word);
+  }
+  return t;
+}
+
+// Widths packed 4 bits per class (class 0 in the low nibble); lets a lane look a width up without memory.
+constexpr uint64_t make_width_nibbles() {
+  const RrrTables t = make_rrr_tables();
+  uint64_t v = 0;
+  for (int k = 0; k < 16; ++k) v |= static_cast<uint64_t>(t.width[k]) << (4 * k);
+  return v;
+}
+
+constexpr uint64_t kWidthNibbles = make_width_nibbles();
+
+// Sum of the 8 nibbles of x (8 block classes in one class word).
+__device__ __forceinline__ int nibble_sum(uint32_t x) {
+  // popcount of each bit plane weighted by its bit value
+  return __popc(x & 0x11111111u) + 2 * __popc(x & 0x22222222u) + 4 * __popc(x & 0x44444444u) +
+         8 * __popc(x & 0x88888888u);
+}
+
+// Sum over the 8 nibbles k of x of width[k]. width is symmetric (width[k] == width[15-k]) so it is a function of
+// m = min(k, 15-k) in 0..7: width = 4[m>=1] + 3[m>=2] + 2[m>=3] + 2[m>=4] + [m>=5] + [m>=6]. Each indicator is
+// counted across all 8 nibbles at once: (m + 8 - t) has its nibble bit 3 set exactly when m >= t.
+__device__ __forceinline__ int nibble_width_sum(uint32_t x) {
+  const uint32_t hi = (x >> 3) & 0x11111111u;     // 1 in every nibble whose class is >= 8
+  const uint32_t m = (x ^ (hi * 15u)) & 0x77777777u;  // min(k, 15-k) per nibble
+  const uint32_t H = 0x88888888u;
+  int s = 4 * __popc((m + 0x77777777u) & H);  // m >= 1
+  s += 3 * __popc((m + 0x66666666u) & H);     // m >= 2
+  s += 2 * __popc((m + 0x55555555u) & H);     // m >= 3
+  s += 2 * __popc((m + 0x44444444u) & H);     // m >= 4
+  s += __popc((m + 0x33333333u) & H);         // m >= 5
+  s += __popc((m + 0x22222222u) & H);         // m >= 6
+  return s;
+}
+
+__device__ __forceinline__ int width_of(int k) { return static_cast<int>((kWidthNibbles >> (4 * k)) & 15u); }
+
+}  // namespace cfd

@@ -1,0 +1,107 @@
+// rrr_core.hpp — per-lane RRR wavelet-matrix primitives (rank1 of one level, access, rank), shared by the
+// wavelet kernels and the FM-index kernels.
+//
+// Semantics follow reference include/chromofold/detail/rrr_wavelet_device.cuh:40-149 exactly (same samples, same
+// class stream, same LSB-first offset stream, same enumerative code); the arithmetic is reorganised for gfx950
+// (SWAR class-word scan, table unrank) as described in rrr_wavelet.hip.
+#pragma once
+
+#include "chromofold/chromofold_search.h"
+#include "cf_device.hpp"
+
+namespace cfr {
+
+// One copy per code object; 64 KiB unrank table + widths + class bases, all fixed by the RRR format.
+static __device__ const cfd::RrrTables kTab = cfd::make_rrr_tables();
+
+// LSB-first read of `w` bits at bit position `at` (may straddle two words; the offset stream carries two words of
+// padding per level so the second read is always in bounds). reference rrr_wavelet_device.cuh:30-38.
+__device__ __forceinline__ uint32_t read_bits(const uint32_t *__restrict__ s, int64_t at, int w) {
+  const int64_t wi = at >> 5;
+  const int b = static_cast<int>(at & 31);
+  const uint32_t lo = s[wi];
+  const uint32_t hi = (b + w > 32) ? s[wi + 1] : 0u;
+  const uint64_t both = (static_cast<uint64_t>(hi) << 32) | lo;
+  return static_cast<uint32_t>(both >> b) & ((1u << w) - 1u);
+}
+
+// rank1 of level `lvl` over [0, pos); with kBit also the plane bit at pos (the access primitive, one block decode
+// serving both). reference rrr_wavelet_device.cuh:56-113.
+template <bool kBit>
+__device__ __forceinline__ int rank1_lvl(const cf_rrrw_view &v, int lvl, int pos, int *bit) {
+  const uint32_t *__restrict__ cls = v.classes + static_cast<size_t>(lvl) * v.cwords;
+  const size_t srow = static_cast<size_t>(lvl) * (v.nsb + 1);
+  const size_t arow = static_cast<size_t>(lvl) * v.na;
+  const int blk = pos / cfd::kRrrT;
+  const int b = pos - blk * cfd::kRrrT;
+  const int sbi = blk >> 6;  // / kRrrS
+  const int a = sbi >> 5;    // / kRrrK
+  int r = v.rank_a[arow + a] + static_cast<int>(v.rank_d[srow + sbi]);
+  int obit = v.off_a[arow + a] + static_cast<int>(v.off_d[srow + sbi]);
+
+  // class words of superblock sbi: blocks [sbi*64 + 8w, +8) live in word sbi*8 + w
+  const uint32_t *__restrict__ cw = cls + (static_cast<size_t>(sbi) << 3);
+  const int nblk = blk - (sbi << 6);  // blocks to sum before the target block, 0..63
+  const int full = nblk >> 3, rem = nblk & 7;
+  int csum = 0, wsum = 0;
+  uint32_t target_word = 0;
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    if (w <= full) {
+      uint32_t x = cw[w];
+      if (w == full) {
+        target_word = x;
+        x &= rem ? ((1u << (4 * rem)) - 1u) : 0u;
+      }
+      csum += cfd::nibble_sum(x);
+      wsum += cfd::nibble_width_sum(x);
+    }
+  }
+  r += csum;
+  if (kBit || b > 0) {
+    const int k = static_cast<int>((target_word >> (4 * rem)) & 15u);
+    const int w = cfd::width_of(k);
+    const uint32_t off = w ? read_bits(v.offsets, static_cast<int64_t>(v.offbase[lvl]) + obit + wsum, w) : 0u;
+    const uint32_t word = kTab.unrank[kTab.base[k] + off];
+    r += __popc(word & ((1u << b) - 1u));
+    if (kBit) *bit = static_cast<int>((word >> b) & 1u);
+  }
+  return r;
+}
+
+// token at position i: one block decode per level (reference rrr_wavelet_device.cuh:117-134)
+template <int LEVELS>
+__device__ __forceinline__ uint32_t access_one(const cf_rrrw_view &v, int i) {
+  const int L = LEVELS > 0 ? LEVELS : v.bits;
+  uint32_t val = 0;
+  for (int lvl = 0; lvl < L; ++lvl) {
+    int bit = 0;
+    const int r = rank1_lvl<true>(v, lvl, i, &bit);
+    val = (val << 1) | static_cast<uint32_t>(bit);
+    i = bit ? v.zeros[lvl] + r : i - r;
+  }
+  return val;
+}
+
+// occurrences of c in [0, i): two rank1 per level narrowing [p, q) (reference rrr_wavelet_device.cuh:137-149).
+// Once the interval is empty every later level keeps it empty, so the walk stops early with the same answer.
+template <int LEVELS>
+__device__ __forceinline__ uint32_t rank_one(const cf_rrrw_view &v, int c, int i) {
+  const int L = LEVELS > 0 ? LEVELS : v.bits;
+  int p = 0, q = i;
+  for (int lvl = 0; lvl < L; ++lvl) {
+    if (p >= q) break;
+    const int rp = rank1_lvl<false>(v, lvl, p, nullptr);
+    const int rq = rank1_lvl<false>(v, lvl, q, nullptr);
+    if ((c >> (L - 1 - lvl)) & 1) {
+      p = v.zeros[lvl] + rp;
+      q = v.zeros[lvl] + rq;
+    } else {
+      p -= rp;
+      q -= rq;
+    }
+  }
+  return static_cast<uint32_t>(q - p);
+}
+
+}  // namespace cfr
