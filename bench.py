@@ -93,6 +93,86 @@ def bench_rrr(steps: int, warmup: int, cpu: bool = True) -> dict:
     return res
 
 
+# ------------------------------------------------------------------------------------------------ paged KV (C4)
+def bench_kv(steps: int, warmup: int, context: int = 32768, batch: int = 32, codec: int = 2, cpu: bool = True,
+             check_seqs: int = 2) -> dict:
+    import torch
+    from chromofold_amd import kv, synth
+
+    H, QH, D = 8, 32, 128
+    gqa = QH // H
+    rng = np.random.default_rng(synth.SEED_C4)
+    t0 = time.perf_counter()
+    # synthetic K/V ~ N(0,1), one sequence at a time (host memory stays ~0.3 GB per sequence)
+    seeds = rng.integers(0, 2 ** 63, size=batch)
+
+    def source(s):
+        g = np.random.default_rng(int(seeds[s]))
+        return (g.standard_normal((H, context, D), dtype=np.float32),
+                g.standard_normal((H, context, D), dtype=np.float32))
+
+    tables = None
+    if codec == kv.CODEC_RANS_HYBRID:
+        K0, V0 = source(0)
+        tables = np.concatenate([t for h in range(H) for t in (kv.build_table(K0[h, :1024].reshape(-1, 16, D)),
+                                                               kv.build_table(V0[h, :1024].reshape(-1, 16, D)))])
+        del K0, V0
+    kvb = kv.build_batched(codec, source, batch, H, np.full(batch, context, np.uint32), D, tables, "cuda:0",
+                           keep_host=cpu or check_seqs > 0)
+    t_build = time.perf_counter() - t0
+    q = rng.standard_normal((batch, QH, D), dtype=np.float32)
+    qp = np.full(batch, context - 1, np.uint32)
+    sc = 1.0 / np.sqrt(D)
+    dq = torch.from_numpy(q).to("cuda:0")
+    dqp = torch.from_numpy(qp.view(np.int32)).to("cuda:0")
+    out = torch.empty_like(dq)
+    desc = kvb.desc(dq, out, dqp, sc)
+    kvb.attention(dq, out, dqp, sc, desc=desc)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    res = {"build_s": t_build, "pool_bytes": kvb.pool_bytes}
+    cpu_s = None
+    if check_seqs > 0:  # correctness gate on a few sequences (fp64 oracle on the oracle-decoded pages)
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        from kv_helpers import normwise_err
+        import oracle as O
+        errs = []
+        tc0 = time.perf_counter()
+        for s in range(check_seqs):
+            pages = []
+            for h in range(H):
+                for p in range(context // 16):
+                    off = int(kvb.host_offsets[s, h, p]) * 16
+                    ks, vs, ksc, vsc, _ = O.kv_decode_page(kvb.host_pool[off:off + 8192], kvb.host_tables, h, D)
+                    pages.append((h, 16 * p, (ks.astype(np.float32) - 128) * ksc,
+                                  (vs.astype(np.float32) - 128) * vsc))
+            ref, _ = O.paged_attention_f64(q[s], QH, H, D, gqa, context - 1, 0, sc, pages)
+            errs.append(normwise_err(got[s], ref))
+        cpu_s = (time.perf_counter() - tc0) / check_seqs
+        res["max_normwise_err"] = max(errs)
+        assert max(errs) <= 1e-3, errs
+    wall, per = _events_time(lambda: kvb.attention(dq, out, dqp, sc, desc=desc), steps, warmup)
+    t_step = float(np.mean(per)) * 1e-3
+    # algorithmic bytes per step: every visible page blob (payload + header + states), tables once, page table,
+    # queries and outputs
+    table_bytes = 0 if tables is None else tables.size
+    step_bytes = kvb.pool_bytes + table_bytes + batch * H * (context // 16) * 4 + 2 * q.nbytes
+    values = 2 * batch * H * context * D
+    res.update({
+        "tokens_per_s": batch / t_step, "ms_per_step": wall / steps, "kernel_ms": t_step * 1e3,
+        "bits_per_value": kvb.pool_bytes * 8.0 / values,
+        "ratio_vs_bf16": (values * 2.0) / kvb.pool_bytes,
+        "roofline": {"bound": "hbm", "achieved": step_bytes / t_step / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": step_bytes / t_step / 1e9 / HBM_PEAK_GBS, "traffic": None},
+        "step_bytes": step_bytes,
+    })
+    if cpu_s is not None:
+        res["cpu_baseline"] = {"value": 1.0 / cpu_s, "unit": "tokens/s", "cores": 1, "kind": "port",
+                               "sample": f"{check_seqs} sequences x 1 decode token at {context} context: oracle "
+                                         f"page decode + fp64 paged attention (32 q heads), single thread"}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -108,6 +188,24 @@ def main() -> int:
 
     import torch
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.workload in ("auto", "kv"):
+        kvr = bench_kv(args.steps, args.warmup, cpu=not args.no_cpu, check_seqs=0 if args.no_cpu else 2)
+        rrr = bench_rrr(args.steps, args.warmup, cpu=not args.no_cpu)
+        secondary = {k: v for k, v in kvr.items() if k not in ("roofline", "cpu_baseline", "tokens_per_s")}
+        secondary["wavelet_rank_mqs"] = rrr["rank_mqs"]
+        secondary["wavelet_access_mqs"] = rrr["access_mqs"]
+        secondary["wavelet_rank_roofline_frac"] = rrr["rank_roofline"]["frac"]
+        secondary["wavelet_cpu_baseline"] = rrr.get("cpu_baseline")
+        line = {
+            "metric": METRIC, "value": kvr["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": kvr["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "u8->f16 MFMA, f32 accumulate", "data": "synthetic (seeded N(0,1) K/V)",
+            "config": {"workload": "paged-KV decode, rANS-hybrid int8 pages, 32 seqs x 32768 ctx, 32 q / 8 kv heads, "
+                                   "head_dim 128, 16-token pages, 1 layer, 1 decode token per seq"},
+            "roofline": kvr["roofline"], "cpu_baseline": kvr.get("cpu_baseline"), "secondary": secondary,
+        }
+        print(json.dumps(line))
+        return 0
     rrr = bench_rrr(args.steps, args.warmup, cpu=not args.no_cpu)
     line = {
         "metric": METRIC, "value": rrr["rank_mqs"], "unit": "Mq/s", "n_gpus": 1, "steps": args.steps,

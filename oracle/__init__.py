@@ -79,6 +79,16 @@ def _declare(L):
         "or_rrr_plane_copy": (None, [P, P, P, P, P]),
         "or_rrr_plane_free": (None, [P]),
         "or_rrr_decode_all": (None, [P, P, I64, I64, P]),
+        "or_kv_fixture_quantize": (None, [P, P, U32, U32, U32, P, P, P, P, P, P]),
+        "or_pack_fixed": (None, [P, C.c_uint64, U32, P]),
+        "or_huffman_decode": (None, [P, P, C.c_int, I64, I64, P]),
+        "or_rans_block_decode": (None, [P, P, P, P, P, P, C.c_int, C.c_int, P]),
+        "or_paged_attention_f64": (C.c_int, [P, U32, U32, U32, U32, U32, U32, C.c_float, U32, P, P, P, P, P, P,
+                                             P, P, U32, U32, P]),
+        "or_dense_attention_f64": (None, [P, U32, P, P, U32, C.c_float, P]),
+        "or_kv_decode_page": (C.c_int, [P, P, U32, P, P, P, P, P]),
+        "or_kv_quantize_page_absmax": (None, [P, U32, P, P]),
+        "or_softmax_merge": (None, [P, P, P, C.c_double, C.c_double, P, U32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name, None)
@@ -308,4 +318,99 @@ def rrr_plane_build(bits01: np.ndarray):
 def rrr_decode_all(classes, offsets, nblocks: int, off_base_bit: int = 0) -> np.ndarray:
     out = np.zeros(nblocks * 15, np.uint8)
     lib().or_rrr_decode_all(_ptr(classes), _ptr(offsets), nblocks, off_base_bit, _ptr(out))
+    return out
+
+
+# ------------------------------------------------------------------ paged KV
+def kv_decode_page(blob: np.ndarray, tables: np.ndarray | None, head: int, head_dim: int):
+    """Decode one kv_codec_ext page blob -> (k_sym [16, D], v_sym [16, D], k_scale, v_scale, token_count)."""
+    blob = np.ascontiguousarray(blob, np.uint8)
+    ks = np.zeros((16, head_dim), np.uint8)
+    vs = np.zeros((16, head_dim), np.uint8)
+    ksc, vsc, tc = C.c_float(0), C.c_float(0), C.c_uint32(0)
+    tab = None if tables is None else np.ascontiguousarray(tables, np.uint8)
+    rc = lib().or_kv_decode_page(_ptr(blob), _ptr(tab), head, _ptr(ks), _ptr(vs), C.byref(ksc), C.byref(vsc),
+                                 C.byref(tc))
+    if rc != 0:
+        raise ValueError("page blob failed to decode")
+    return ks, vs, ksc.value, vsc.value, tc.value
+
+
+def kv_quantize_absmax(x: np.ndarray):
+    x = np.ascontiguousarray(x, np.float32)
+    sym = np.zeros(x.size, np.uint8)
+    sc = C.c_float(0)
+    lib().or_kv_quantize_page_absmax(_ptr(x), x.size, _ptr(sym), C.byref(sc))
+    return sym.reshape(x.shape), sc.value
+
+
+def kv_fixture_quantize(k: np.ndarray, v: np.ndarray, bits: int):
+    """reference kv_gpu_fixture encode_page quantiser: (k_sym, v_sym, k_scales[D], v_scales[T], k_deq, v_deq)."""
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    T, D = k.shape
+    out = [np.zeros((T, D), np.uint8), np.zeros((T, D), np.uint8), np.zeros(D, np.float32), np.zeros(T, np.float32),
+           np.zeros((T, D), np.float32), np.zeros((T, D), np.float32)]
+    lib().or_kv_fixture_quantize(_ptr(k), _ptr(v), T, D, bits, *[_ptr(a) for a in out])
+    return tuple(out)
+
+
+def pack_fixed(sym: np.ndarray, bits: int) -> np.ndarray:
+    sym = np.ascontiguousarray(sym, np.uint8).ravel()
+    words = np.zeros((sym.size * bits + 31) // 32, np.uint32)
+    lib().or_pack_fixed(_ptr(sym), sym.size, bits, _ptr(words))
+    return words
+
+
+def huffman_decode(words, lut, maxlen: int, pos: int, n: int) -> np.ndarray:
+    out = np.zeros(n, np.int32)
+    lib().or_huffman_decode(_ptr(np.ascontiguousarray(words, np.uint32)), _ptr(np.ascontiguousarray(lut, np.int32)),
+                            maxlen, pos, n, _ptr(out))
+    return out
+
+
+def rans_block_decode(data, byte_off, state0, slot2sym, freq, cum, block: int, n: int) -> np.ndarray:
+    out = np.zeros(n, np.int32)
+    a = [np.ascontiguousarray(data, np.uint8), np.ascontiguousarray(byte_off, np.int32),
+         np.ascontiguousarray(state0, np.uint32), np.ascontiguousarray(slot2sym, np.int32),
+         np.ascontiguousarray(freq, np.int32), np.ascontiguousarray(cum, np.int32)]
+    lib().or_rans_block_decode(*[_ptr(x) for x in a], block, n, _ptr(out))
+    return out
+
+
+def paged_attention_f64(q, q_heads, kv_heads, D, gqa, query_token, window, scale, pages, tail=None):
+    """pages: list of (kv_head, token_begin, K [n, D], V [n, D]) dequantised; tail: (token_begin, K [n, kvh, D],
+    V [n, kvh, D]) or None. Returns (out [q_heads, D], number of heads with no visible token)."""
+    q = np.ascontiguousarray(q, np.float32)
+    n = len(pages)
+    kvh = np.array([p[0] for p in pages], np.uint32)
+    tok0 = np.array([p[1] for p in pages], np.uint32)
+    ntok = np.array([p[2].shape[0] for p in pages], np.uint32)
+    off = np.zeros(n, np.uint64)
+    if n:
+        off[1:] = np.cumsum(ntok[:-1])
+        K = np.ascontiguousarray(np.concatenate([p[2] for p in pages]), np.float32)
+        V = np.ascontiguousarray(np.concatenate([p[3] for p in pages]), np.float32)
+    else:
+        K = V = np.zeros((1, D), np.float32)
+    if tail is not None:
+        t0, tk, tv = tail
+        tk = np.ascontiguousarray(tk, np.float32)
+        tv = np.ascontiguousarray(tv, np.float32)
+        tn = tk.shape[0]
+    else:
+        t0, tk, tv, tn = 0, None, None, 0
+    out = np.zeros((q_heads, D), np.float32)
+    empty = lib().or_paged_attention_f64(_ptr(q), q_heads, kv_heads, D, gqa, query_token, window, scale, n,
+                                         _ptr(kvh), _ptr(tok0), _ptr(ntok), _ptr(off), _ptr(K), _ptr(V), _ptr(tk),
+                                         _ptr(tv), t0, tn, _ptr(out))
+    return out, empty
+
+
+def dense_attention_f64(q, k, v, scale):
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    out = np.zeros(q.shape[-1], np.float32)
+    lib().or_dense_attention_f64(_ptr(q), q.shape[-1], _ptr(k), _ptr(v), k.shape[0], scale, _ptr(out))
     return out

@@ -1,1 +1,282 @@
-// oracle_kv.cpp — TEST INFRASTRUCTURE ONLY (see oracle_succinct.cpp header). KV quantizer and attention oracle.
+// oracle_kv.cpp — TEST INFRASTRUCTURE ONLY (see oracle_succinct.cpp header). CPU restatements for the paged-KV
+// path, used as the checker of the HIP kernels; never linked into libchromofold.so.
+//
+//   fixture quantiser + fixed-width packing   reference src/runtime/kv_gpu_fixture.cpp:12-95
+//   paged attention, fp64 online softmax      reference src/runtime/kv_reference.cpp:50-67,164-243 and the GPU
+//                                             seam semantics of src/cuda/paged_kv_attention.cu:41-176 (window,
+//                                             GQA h / gqa_group_size, active tail, no visible token -> zeros)
+//   online-softmax state merge                reference src/runtime/kv_runtime.cpp:179-254
+//   canonical Huffman LUT decode              reference include/chromofold/detail/block_huffman_device.cuh:12-19
+//   block rANS decode                         reference src/cuda/rans.cu:16-26
+//   RANS_HYBRID / INT8 page decode            the byte format written out in include/chromofold/kv_codec_ext.h
+//                                             (this project's codec; restated here from the format text, not
+//                                             from the product encoder, so a format slip shows as a mismatch)
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <limits>
+#include <vector>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+extern "C" {
+
+// ---------------------------------------------------------------------------------------- fixture quantiser
+// K per-channel scale, V per-token scale, both max|x|/qmax (0 -> 1.0); sym = clamp(lrint(x/s), -(qmax+1), qmax)
+// + zp; fixed-width MSB-first packing, block offsets every block_size symbols. Outputs: syms [T*D] (K then V),
+// scales (K [D] then V [T]), dequantised values (K then V).
+void or_kv_fixture_quantize(const float *k, const float *v, uint32_t T, uint32_t D, uint32_t bits, uint8_t *k_sym,
+                            uint8_t *v_sym, float *k_scales, float *v_scales, float *k_deq, float *v_deq) {
+  const int qmax = (1 << (bits - 1)) - 1, zp = 1 << (bits - 1);
+  for (uint32_t d = 0; d < D; ++d) {
+    float m = 0.0f;
+    for (uint32_t t = 0; t < T; ++t) m = std::max(m, std::fabs(k[(size_t)t * D + d]));
+    k_scales[d] = m == 0.0f ? 1.0f : m / (float)qmax;
+  }
+  for (uint32_t t = 0; t < T; ++t) {
+    float m = 0.0f;
+    for (uint32_t d = 0; d < D; ++d) m = std::max(m, std::fabs(v[(size_t)t * D + d]));
+    v_scales[t] = m == 0.0f ? 1.0f : m / (float)qmax;
+  }
+  for (uint32_t t = 0; t < T; ++t)
+    for (uint32_t d = 0; d < D; ++d) {
+      const size_t i = (size_t)t * D + d;
+      const int qk = std::clamp((int)std::lrint(k[i] / k_scales[d]), -(qmax + 1), qmax);
+      const int qv = std::clamp((int)std::lrint(v[i] / v_scales[t]), -(qmax + 1), qmax);
+      k_sym[i] = (uint8_t)(qk + zp);
+      v_sym[i] = (uint8_t)(qv + zp);
+      k_deq[i] = (float)qk * k_scales[d];
+      v_deq[i] = (float)qv * v_scales[t];
+    }
+}
+
+// MSB-first fixed-width packing (reference kv_gpu_fixture.cpp:31-41); words must be zeroed, n*bits/32 rounded up.
+void or_pack_fixed(const uint8_t *sym, uint64_t n, uint32_t bits, uint32_t *words) {
+  for (uint64_t i = 0; i < n; ++i) {
+    const uint64_t bit = i * bits;
+    words[bit >> 5] |= (uint32_t)(sym[i] & ((1u << bits) - 1u)) << ((32u - bits) - (uint32_t)(bit & 31u));
+  }
+}
+
+// canonical-Huffman LUT decode of n symbols starting at bit `pos` (reference block_huffman_device.cuh:12-19:
+// read maxlen bits MSB-first, lut[look] = sym | len << 8)
+void or_huffman_decode(const uint32_t *words, const int32_t *lut, int maxlen, int64_t pos, int64_t n,
+                       int32_t *out) {
+  for (int64_t i = 0; i < n; ++i) {
+    int look = 0;
+    for (int b = 0; b < maxlen; ++b) {
+      const int64_t w = pos + b;
+      look = (look << 1) | (int)((words[w >> 5] >> (31 - (w & 31))) & 1u);
+    }
+    const int e = lut[look];
+    out[i] = e & 0xff;
+    pos += e >> 8;
+  }
+}
+
+// block rANS decode (reference src/cuda/rans.cu:16-36): M = 4096, L = 2^23, byte renorm ascending
+void or_rans_block_decode(const uint8_t *data, const int32_t *byte_off, const uint32_t *state0,
+                          const int32_t *slot2sym, const int32_t *freq, const int32_t *cum, int block, int n,
+                          int32_t *out) {
+  const int nb = (n + block - 1) / block;
+  for (int b = 0; b < nb; ++b) {
+    int pos = byte_off[b];
+    uint32_t x = state0[b];
+    const int cnt = std::min(block, n - b * block);
+    for (int j = 0; j < cnt; ++j) {
+      const int slot = (int)(x & 4095u);
+      const int s = slot2sym[slot];
+      x = (uint32_t)freq[s] * (x >> 12) + (uint32_t)(slot - cum[s]);
+      while (x < (1u << 23)) x = (x << 8) | data[pos++];
+      out[b * block + j] = s;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------- paged attention
+// One query row per call. Pages: for page p, kv head kvh[p], tokens [tok0[p], tok0[p]+ntok[p]), dequantised K/V
+// at k + off[p]*D ([ntok, D] row-major). Tail: [tail_n, kv_heads, D] starting at tail_tok0. Output [q_heads, D].
+// Returns the number of heads that had no visible token (their output is zero, as the GPU seam writes).
+int or_paged_attention_f64(const float *q, uint32_t q_heads, uint32_t kv_heads, uint32_t D, uint32_t gqa,
+                           uint32_t query_token, uint32_t window, float scale, uint32_t npages,
+                           const uint32_t *kvh, const uint32_t *tok0, const uint32_t *ntok, const uint64_t *off,
+                           const float *k, const float *v, const float *tail_k, const float *tail_v,
+                           uint32_t tail_tok0, uint32_t tail_n, float *out) {
+  const uint32_t lo = (window == 0 || query_token + 1 <= window) ? 0u : query_token + 1 - window;
+  int empty = 0;
+  for (uint32_t h = 0; h < q_heads; ++h) {
+    const uint32_t kh = h / gqa;
+    const float *qq = q + (size_t)h * D;
+    double m = -std::numeric_limits<double>::infinity(), den = 0.0;
+    std::vector<double> w(D, 0.0);
+    auto add = [&](const float *kr, const float *vr) {
+      double dot = 0.0;
+      for (uint32_t d = 0; d < D; ++d) dot += (double)qq[d] * kr[d];
+      const double s = dot * scale;
+      const double nm = std::max(m, s);
+      const double a = den == 0.0 ? 0.0 : std::exp(m - nm), b = std::exp(s - nm);
+      den = den * a + b;
+      for (uint32_t d = 0; d < D; ++d) w[d] = w[d] * a + (double)vr[d] * b;
+      m = nm;
+    };
+    for (uint32_t p = 0; p < npages; ++p) {
+      if (kvh[p] != kh) continue;
+      for (uint32_t t = 0; t < ntok[p]; ++t) {
+        const uint32_t tok = tok0[p] + t;
+        if (tok < lo || tok > query_token) continue;
+        add(k + (off[p] + t) * D, v + (off[p] + t) * D);
+      }
+    }
+    for (uint32_t t = 0; t < tail_n; ++t) {
+      const uint32_t tok = tail_tok0 + t;
+      if (tok < lo || tok > query_token) continue;
+      add(tail_k + ((size_t)t * kv_heads + kh) * D, tail_v + ((size_t)t * kv_heads + kh) * D);
+    }
+    for (uint32_t d = 0; d < D; ++d) out[(size_t)h * D + d] = den > 0.0 ? (float)(w[d] / den) : 0.0f;
+    if (den == 0.0) ++empty;
+  }
+  return empty;
+}
+
+// Dense attention of one query row against contiguous K/V [T, D] of one kv head (all tokens < T visible
+// up to query_token): the closed form the paged result must equal (reference tests/kv_reference_test.cpp:47-120).
+void or_dense_attention_f64(const float *q, uint32_t D, const float *k, const float *v, uint32_t T, float scale,
+                            float *out) {
+  double m = -std::numeric_limits<double>::infinity();
+  std::vector<double> s(T);
+  for (uint32_t t = 0; t < T; ++t) {
+    double dot = 0.0;
+    for (uint32_t d = 0; d < D; ++d) dot += (double)q[d] * k[(size_t)t * D + d];
+    s[t] = dot * scale;
+    m = std::max(m, s[t]);
+  }
+  double den = 0.0;
+  std::vector<double> w(D, 0.0);
+  for (uint32_t t = 0; t < T; ++t) {
+    const double e = std::exp(s[t] - m);
+    den += e;
+    for (uint32_t d = 0; d < D; ++d) w[d] += e * v[(size_t)t * D + d];
+  }
+  for (uint32_t d = 0; d < D; ++d) out[d] = (float)(w[d] / den);
+}
+
+// ---------------------------------------------------------------------------------------- kv_codec_ext pages
+// Decode one INT8 / RANS_HYBRID page blob into symbols [16, D] for K and V (token-major) plus the two scales.
+// tables: table blobs (16 KiB each); the K stream uses tables[2*head], V uses tables[2*head+1].
+// Returns 0 on success, -1 on a format inconsistency (bad codec, stream over/under-run, final state != 2^16).
+int or_kv_decode_page(const uint8_t *blob, const uint8_t *tables, uint32_t head, uint8_t *k_sym, uint8_t *v_sym,
+                      float *k_scale, float *v_scale, uint32_t *token_count) {
+  uint32_t codec;
+  uint16_t kw, vw, tc, D;
+  std::memcpy(&codec, blob, 4);
+  std::memcpy(&kw, blob + 4, 2);
+  std::memcpy(&vw, blob + 6, 2);
+  std::memcpy(k_scale, blob + 8, 4);
+  std::memcpy(v_scale, blob + 12, 4);
+  std::memcpy(&tc, blob + 16, 2);
+  std::memcpy(&D, blob + 18, 2);
+  *token_count = tc;
+  const uint32_t nq = D / 4;
+  // symbol of lane t, quad q, position i -> (token, dim)
+  auto where = [&](bool is_v, uint32_t t, uint32_t q, uint32_t i, uint32_t *tok, uint32_t *dim) {
+    if (!is_v) {
+      *tok = t;
+      *dim = 4 * q + i;
+    } else {
+      const uint32_t per = D / 16;
+      *tok = 4 * (q / per) + i;
+      *dim = t + 16 * (q % per);
+    }
+  };
+  if (codec == 1) {  // INT8: word (q*16 + t) = 4 bytes of quad q of lane t
+    for (int s = 0; s < 2; ++s) {
+      const uint8_t *b = blob + 32 + (size_t)s * 16 * D;
+      uint8_t *out = s ? v_sym : k_sym;
+      for (uint32_t q = 0; q < nq; ++q)
+        for (uint32_t t = 0; t < 16; ++t)
+          for (uint32_t i = 0; i < 4; ++i) {
+            uint32_t tok, dim;
+            where(s == 1, t, q, i, &tok, &dim);
+            out[(size_t)tok * D + dim] = b[(q * 16 + t) * 4 + i];
+          }
+    }
+    return 0;
+  }
+  if (codec != 2) return -1;
+  const uint32_t nlow = 3 * (D / 16) * 16;
+  const uint32_t *states = reinterpret_cast<const uint32_t *>(blob + 32);
+  const uint32_t *lows = reinterpret_cast<const uint32_t *>(blob + 160);
+  const uint16_t *words = reinterpret_cast<const uint16_t *>(blob + 160 + 2 * (size_t)nlow * 4);
+  for (int s = 0; s < 2; ++s) {
+    const uint8_t *tab = tables + (size_t)(2 * head + s) * 16384;
+    const uint16_t *w = words + (s ? kw : 0);
+    const uint32_t nw = s ? vw : kw;
+    uint32_t x[16];
+    for (int t = 0; t < 16; ++t) x[t] = states[s * 16 + t];
+    uint32_t cur = 0;
+    uint8_t *out = s ? v_sym : k_sym;
+    for (uint32_t q = 0; q < nq; ++q) {
+      uint32_t j[16];
+      for (uint32_t t = 0; t < 16; ++t) {  // all lanes decode step q
+        uint32_t lo;
+        const uint32_t slot = x[t] & 2047u;
+        std::memcpy(&lo, tab + 8 * slot, 4);
+        const uint32_t f = (lo & 2047u) + 1, cs = (lo >> 11) & 2047u;
+        j[t] = (lo >> 22) & 255u;
+        x[t] = f * (x[t] >> 11) + cs;
+      }
+      for (uint32_t t = 0; t < 16; ++t)  // renormalisation reads in lane order
+        if (x[t] < 65536u) {
+          if (cur >= nw) return -1;
+          x[t] = (x[t] << 16) | w[cur++];
+        }
+      for (uint32_t t = 0; t < 16; ++t) {
+        const uint32_t g = q / 4, qd = q % 4;
+        const uint32_t *lw = lows + (size_t)s * nlow;
+        const uint32_t n = lw[(g * 3 + (qd >> 1)) * 16 + t], c = lw[(g * 3 + 2) * 16 + t];
+        for (uint32_t i = 0; i < 4; ++i) {
+          const uint32_t low = ((n >> (8 * i + 4 * (qd & 1))) & 15u) | (((c >> (8 * i + 2 * qd)) & 3u) << 4);
+          const uint32_t hi = (j[t] >> (2 * i)) & 3u;
+          uint32_t tok, dim;
+          where(s == 1, t, q, i, &tok, &dim);
+          out[(size_t)tok * D + dim] = (uint8_t)((hi << 6) | low);
+        }
+      }
+    }
+    if (cur != nw) return -1;
+    for (int t = 0; t < 16; ++t)
+      if (x[t] != 65536u) return -1;
+  }
+  return 0;
+}
+
+// per-page-per-head absmax int8 quantiser of the benchmark configuration (scale = max|x|/127, 0 -> 1;
+// sym = clamp(lrint(x / scale), -128, 127) + 128) — the kv_gpu_fixture convention with one scale per page.
+void or_kv_quantize_page_absmax(const float *x, uint32_t n, uint8_t *sym, float *scale) {
+  float m = 0.0f;
+  for (uint32_t i = 0; i < n; ++i) m = std::max(m, std::fabs(x[i]));
+  *scale = m == 0.0f ? 1.0f : m / 127.0f;
+  for (uint32_t i = 0; i < n; ++i) sym[i] = (uint8_t)(std::clamp(std::lrint(x[i] / *scale), -128L, 127L) + 128);
+}
+
+// ---------------------------------------------------------------------------------------- online softmax
+// (m, l, acc[D]) merge as reference kv_runtime.cpp:219-243 (returns merged state in dst)
+void or_softmax_merge(double *dst_m, double *dst_l, double *dst_acc, double src_m, double src_l,
+                      const double *src_acc, uint32_t D) {
+  if (src_l == 0.0) return;
+  if (*dst_l == 0.0) {
+    *dst_m = src_m;
+    *dst_l = src_l;
+    std::memcpy(dst_acc, src_acc, sizeof(double) * D);
+    return;
+  }
+  const double nm = std::max(*dst_m, src_m), a = std::exp(*dst_m - nm), b = std::exp(src_m - nm);
+  *dst_l = *dst_l * a + src_l * b;
+  for (uint32_t d = 0; d < D; ++d) dst_acc[d] = dst_acc[d] * a + src_acc[d] * b;
+  *dst_m = nm;
+}
+
+}  // extern "C"

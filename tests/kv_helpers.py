@@ -1,0 +1,47 @@
+"""Shared builders for the paged-KV tests: synthetic sequences, expected outputs from the fp64 CPU oracle."""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle as O
+
+
+def make_seqs(seq_tokens, kv_heads, D, seed, scale_spread=False):
+    rng = np.random.default_rng(seed)
+    data = []
+    for s, T in enumerate(seq_tokens):
+        K = rng.standard_normal((kv_heads, T, D)).astype(np.float32)
+        V = rng.standard_normal((kv_heads, T, D)).astype(np.float32)
+        if scale_spread:  # channels / tokens of very different magnitude (outlier channels, tiny tokens)
+            K *= rng.choice([0.01, 1.0, 30.0], size=(1, 1, D)).astype(np.float32)
+            V *= rng.choice([1e-3, 1.0, 8.0], size=(1, T, 1)).astype(np.float32)
+        data.append((K, V))
+    return data
+
+
+def oracle_batched(kv, data, queries, query_pos, softmax_scale, gqa):
+    """fp64 reference over the values the decoder must reproduce: every page blob is decoded by the oracle's own
+    decoder (which also checks the stream), dequantised as (sym - 128) * scale."""
+    S, H = kv.seq_count, kv.kv_heads
+    D = kv.head_dim
+    out = np.zeros((S, H * gqa, D), np.float32)
+    for s in range(S):
+        T = int(data[s][0].shape[1])
+        visible = min(T, int(query_pos[s]) + 1)
+        npg = (visible + 15) // 16
+        pages = []
+        for h in range(H):
+            for p in range(npg):
+                off = int(kv.host_offsets[s, h, p]) * 16
+                ks, vs, ksc, vsc, tc = O.kv_decode_page(kv.host_pool[off:off + 8192], kv.host_tables, h, D)
+                n = min(16, T - 16 * p)
+                assert tc == n
+                pages.append((h, 16 * p, (ks[:n].astype(np.float32) - 128) * ksc,
+                              (vs[:n].astype(np.float32) - 128) * vsc))
+        o, empty = O.paged_attention_f64(queries[s], H * gqa, H, D, gqa, int(query_pos[s]), 0, softmax_scale, pages)
+        out[s] = o
+    return out
+
+
+def normwise_err(got, ref):
+    return float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))

@@ -1,0 +1,107 @@
+"""GPU parity of the batched compressed paged-KV decode (cf_kv_paged_attention_batched_async) against the fp64 CPU
+oracle evaluated on the oracle-decoded pages. Tolerance (north star): normwise relative error <= 1e-3 with fp32
+accumulation; f16 operands with hi/lo-split queries keep it near 3e-4 (P in f16)."""
+import numpy as np
+import pytest
+
+from kv_helpers import make_seqs, normwise_err, oracle_batched
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def _run(dev, codec, seq_tokens, kv_heads, gqa, D, seed, query_pos=None, splits=(0,), shared=None,
+         scale_spread=False):
+    import torch
+    from chromofold_amd import kv
+    data = make_seqs(seq_tokens, kv_heads, D, seed, scale_spread)
+    tables = None
+    if codec == kv.CODEC_RANS_HYBRID:
+        parts = []
+        for h in range(kv_heads):
+            K = data[0][0][h][: (data[0][0].shape[1] // 16) * 16].reshape(-1, 16, D)[:32]
+            V = data[0][1][h][: (data[0][1].shape[1] // 16) * 16].reshape(-1, 16, D)[:32]
+            parts += [kv.build_table(K), kv.build_table(V)]
+        tables = np.concatenate(parts)
+    if shared:
+        for s, (donor, pages) in shared.items():  # the shared prefix really is the donor's data
+            n = pages * 16
+            data[s][0][:, :n] = data[donor][0][:, :n]
+            data[s][1][:, :n] = data[donor][1][:, :n]
+    S = len(seq_tokens)
+    kvb = kv.build_batched(codec, lambda s: data[s], S, kv_heads, np.array(seq_tokens), D, tables, dev,
+                           keep_host=True, shared=shared)
+    rng = np.random.default_rng(seed + 1)
+    q = rng.standard_normal((S, kv_heads * gqa, D)).astype(np.float32)
+    qp = np.array([t - 1 for t in seq_tokens] if query_pos is None else query_pos, np.uint32)
+    sc = 1.0 / np.sqrt(D)
+    ref = oracle_batched(kvb, data, q, qp, sc, gqa)
+    dq = torch.from_numpy(q).to(dev)
+    dqp = torch.from_numpy(qp.view(np.int32)).to(dev)
+    for sp in splits:
+        out = torch.full_like(dq, float("nan"))
+        kvb.attention(dq, out, dqp, sc, splits=sp)
+        got = out.cpu().numpy()
+        assert np.isfinite(got).all()
+        err = normwise_err(got, ref)
+        assert err <= TOL, (codec, sp, err)
+    return kvb
+
+
+@pytest.mark.parametrize("codec", [1, 2])
+@pytest.mark.parametrize("D", [128, 64])
+def test_batched_ragged(dev, codec, D):
+    # ragged lengths: partial last pages, a single-token sequence, lengths not multiples of 64 tokens
+    _run(dev, codec, [1, 16, 17, 100, 255, 640, 1029], 2, 4, D, seed=5 + D, splits=(0, 1, 3))
+
+
+@pytest.mark.parametrize("codec", [1, 2])
+def test_batched_causal_query_pos(dev, codec):
+    # query positions inside the context: tokens after query_pos are masked
+    _run(dev, codec, [300, 300, 64], 3, 4, 128, seed=9, query_pos=[0, 150, 63], splits=(0, 2))
+
+
+@pytest.mark.parametrize("gqa", [1, 2, 4])
+def test_batched_gqa(dev, gqa):
+    _run(dev, 2, [200, 333], 2, gqa, 128, seed=13 + gqa)
+
+
+def test_batched_shared_prefix(dev):
+    # sequences 1..3 reuse sequence 0's first 8 pages (refcounted prefix blobs)
+    _run(dev, 2, [256, 200, 300, 129], 2, 4, 128, seed=21, shared={1: (0, 8), 2: (0, 8), 3: (0, 8)})
+
+
+def test_batched_value_spread(dev):
+    # outlier channels and tiny / huge tokens: per-page absmax keeps decode exact, output within tolerance
+    _run(dev, 2, [512, 96], 2, 4, 128, seed=33, scale_spread=True)
+
+
+def test_batched_llama_shape_4k(dev):
+    """C4 shape at 4k context with 4 sequences (32 q heads, 8 kv heads, hd 128)."""
+    _run(dev, 2, [4096] * 4, 8, 4, 128, seed=0xC4, splits=(0,))
+
+
+def test_batched_rejects_bad_desc(dev):
+    import ctypes as C
+    import torch
+    from chromofold_amd import _abi as A
+    from chromofold_amd import kv
+    kvb = _run(dev, 1, [32], 1, 4, 128, seed=1)
+    q = torch.zeros((1, 4, 128), device=dev)
+    o = torch.zeros_like(q)
+    qp = torch.zeros(1, dtype=torch.int32, device=dev)
+    d = kvb.desc(q, o, qp, 0.1)
+    L = A.lib()
+    for field, val, st in [("struct_size", 8, 1), ("abi_version", 99, 1), ("codec", 7, 2), ("head_dim", 96, 2),
+                           ("query_head_count", 5, 2), ("queries", None, 1)]:
+        bad = kv.cf_kv_batched_desc.from_buffer_copy(d)
+        setattr(bad, field, val)
+        assert L.cf_kv_paged_attention_batched_async(C.byref(bad), None) == st, field

@@ -1,0 +1,103 @@
+"""CPU tests of the KV page codecs (kv_codec_ext.h): the library's host encoder against the oracle's independent
+decoder written from the format text. Decode must be bit-exact: every symbol equals the absmax quantiser's symbol
+(the quantiser itself is checked against a numpy closed form), scales equal, and every rANS stream ends exactly at
+its word count with all 16 states back at 2^16."""
+import numpy as np
+import pytest
+
+import oracle as O
+
+
+@pytest.fixture(scope="module")
+def kv():
+    from chromofold_amd import kv
+    return kv
+
+
+def _absmax_closed_form(x):
+    m = np.abs(x).max()
+    s = np.float32(1.0) if m == 0 else np.float32(m) / np.float32(127.0)
+    return (np.clip(np.rint(x / s), -128, 127) + 128).astype(np.uint8), s
+
+
+def test_absmax_quantiser_closed_form():
+    rng = np.random.default_rng(0)
+    for x in [rng.standard_normal((16, 128)).astype(np.float32), np.zeros((16, 64), np.float32),
+              np.full((3, 128), -2.5, np.float32), (rng.standard_normal((16, 128)) * 1e-30).astype(np.float32)]:
+        sym, sc = O.kv_quantize_absmax(x)
+        sym2, sc2 = _absmax_closed_form(x)
+        assert sc == sc2 and np.array_equal(sym, sym2)
+    # round half to even on exact halves: scale 1 (max 127) and values k + 0.5
+    x = np.array([127.0, 0.5, 1.5, 2.5, -0.5, -1.5], np.float32)
+    sym, sc = O.kv_quantize_absmax(x)
+    assert sc == 1.0 and list(sym.astype(int) - 128) == [127, 0, 2, 2, 0, -2]
+
+
+@pytest.mark.parametrize("codec", [1, 2])
+@pytest.mark.parametrize("D", [64, 128])
+def test_page_roundtrip(kv, codec, D):
+    rng = np.random.default_rng(D + codec)
+    n = 40
+    K = rng.standard_normal((n, 16, D)).astype(np.float32)
+    V = rng.standard_normal((n, 16, D)).astype(np.float32)
+    K[3] = 0.0                                   # all-zero page (scale 1, every symbol 128)
+    V[4] *= 1e4                                  # large magnitudes
+    K[5, :, 7] = 50.0                            # one outlier channel
+    V[6] = np.sign(V[6])                         # two-valued page
+    K[7] = np.linspace(-1, 1, 16 * D, dtype=np.float32).reshape(16, D)
+    tc = np.full(n, 16, np.uint32)
+    tc[8], tc[9] = 1, 11                         # partial pages (padded with symbol 128)
+    heads = (np.arange(n) % 3).astype(np.uint32)
+    tables = None
+    if codec == 2:
+        tables = np.concatenate([kv.build_table(K[h::3][:5]) if s == 0 else kv.build_table(V[h::3][:5])
+                                 for h in range(3) for s in range(2)])
+    blob, offs = kv.encode_pages(codec, K, V, D, tables, heads, tc)
+    assert blob.size % 16 == 0 and (offs[1:] > offs[:-1]).all()
+    for p in range(n):
+        o = int(offs[p]) * 16
+        ks, vs, ksc, vsc, t = O.kv_decode_page(blob[o:o + 8192], tables, int(heads[p]), D)
+        assert t == tc[p]
+        ek, eks = O.kv_quantize_absmax(K[p, :t])
+        ev, evs = O.kv_quantize_absmax(V[p, :t])
+        assert ksc == eks and vsc == evs
+        assert np.array_equal(ks[:t], ek) and np.array_equal(vs[:t], ev), p
+        assert (ks[t:] == 128).all() and (vs[t:] == 128).all()
+
+
+def test_rans_compression_near_entropy(kv):
+    """On N(0,1) pages the RANS_HYBRID blob is within 0.1 b/value of the int8 symbol entropy plus the fixed
+    per-page overhead (header + 32 states = 160 B) — i.e. the coder itself loses almost nothing."""
+    rng = np.random.default_rng(11)
+    n, D = 256, 128
+    K = rng.standard_normal((n, 16, D)).astype(np.float32)
+    V = rng.standard_normal((n, 16, D)).astype(np.float32)
+    tables = np.concatenate([kv.build_table(K[:64]), kv.build_table(V[:64])])
+    blob, _ = kv.encode_pages(2, K, V, D, tables)
+    syms = np.concatenate([O.kv_quantize_absmax(K[p])[0].ravel() for p in range(n)] +
+                          [O.kv_quantize_absmax(V[p])[0].ravel() for p in range(n)])
+    c = np.bincount(syms, minlength=256).astype(np.float64)
+    pr = c[c > 0] / c.sum()
+    h0 = -(pr * np.log2(pr)).sum()
+    bits_per_value = blob.size * 8 / (2 * n * 16 * D)
+    overhead = 160 * 8 / (2 * 16 * D)
+    assert bits_per_value < h0 + overhead + 0.25, (bits_per_value, h0, overhead)
+    assert bits_per_value < 8.0  # smaller than the raw int8 page
+
+
+def test_table_every_symbol_codable(kv):
+    hist = np.zeros((1, 16, 64), np.float32)  # all-zero sample -> joint symbol 0xAA only
+    t = kv.build_table(hist)
+    lo = t.view(np.uint32)[0::2]
+    f = (lo & 2047) + 1
+    cs = (lo >> 11) & 2047
+    j = (lo >> 22) & 255
+    starts = cs == 0
+    assert starts.sum() == 256 and sorted(j[starts]) == list(range(256))
+    assert f[starts].sum() == 2048
+    # a page whose high parts never occurred in the sample still codes and decodes
+    rng = np.random.default_rng(3)
+    K = (rng.standard_normal((2, 16, 64)) * 3).astype(np.float32)
+    blob, offs = kv.encode_pages(2, K, K, 64, np.concatenate([t, t]))
+    ks, vs, *_ = O.kv_decode_page(blob, np.concatenate([t, t]), 0, 64)
+    assert np.array_equal(ks, O.kv_quantize_absmax(K[0])[0])
