@@ -134,18 +134,14 @@ def bench_kv(steps: int, warmup: int, context: int = 32768, batch: int = 32, cod
     cpu_s = None
     if check_seqs > 0:  # correctness gate on a few sequences (fp64 oracle on the oracle-decoded pages)
         sys.path.insert(0, os.path.join(ROOT, "tests"))
-        from kv_helpers import normwise_err
+        from kv_helpers import decoded_pages, normwise_err
         import oracle as O
         errs = []
         tc0 = time.perf_counter()
         for s in range(check_seqs):
             pages = []
             for h in range(H):
-                for p in range(context // 16):
-                    off = int(kvb.host_offsets[s, h, p]) * 16
-                    ks, vs, ksc, vsc, _ = O.kv_decode_page(kvb.host_pool[off:off + 8192], kvb.host_tables, h, D)
-                    pages.append((h, 16 * p, (ks.astype(np.float32) - 128) * ksc,
-                                  (vs.astype(np.float32) - 128) * vsc))
+                pages += [(h, t0, k, v) for t0, k, v in decoded_pages(kvb, s, h, context)]
             ref, _ = O.paged_attention_f64(q[s], QH, H, D, gqa, context - 1, 0, sc, pages)
             errs.append(normwise_err(got[s], ref))
         cpu_s = (time.perf_counter() - tc0) / check_seqs
@@ -156,7 +152,7 @@ def bench_kv(steps: int, warmup: int, context: int = 32768, batch: int = 32, cod
     # algorithmic bytes per step: every visible page blob (payload + header + states), tables once, page table,
     # queries and outputs
     table_bytes = 0 if tables is None else tables.size
-    step_bytes = kvb.pool_bytes + table_bytes + batch * H * (context // 16) * 4 + 2 * q.nbytes
+    step_bytes = kvb.pool_bytes + table_bytes + batch * H * (context // 64) * 4 + 2 * q.nbytes
     values = 2 * batch * H * context * D
     res.update({
         "tokens_per_s": batch / t_step, "ms_per_step": wall / steps, "kernel_ms": t_step * 1e3,

@@ -20,6 +20,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <utility>
 
 #include "cf_device.hpp"
 #include "chromofold/kv_codec_ext.h"
@@ -49,48 +50,57 @@ __device__ __forceinline__ float4_t mfma4(half4_t a, half4_t b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 0, 0, 0);
 }
 
-// low-part byte word of quad qd (0..3) of a 16-value group from its three bit-sliced words
-__device__ __forceinline__ uint32_t lows_of(uint32_t n0, uint32_t n1, uint32_t c, int qd) {
-  const uint32_t n = (qd < 2) ? n0 : n1;
-  const uint32_t nib = (qd & 1) ? ((n >> 4) & 0x0F0F0F0Fu) : (n & 0x0F0F0F0Fu);
-  const uint32_t cr = ((c >> (2 * qd)) << 4) & 0x30303030u;
-  return nib | cr;
+// Symbol bytes of quad qd (0..3) of a 16-value low-part group: nibbles from n0/n1, bits 4-5 from the crumb word
+// c, bits 6-7 from the spread high parts (two bit-field inserts).
+template <int QD>
+__device__ __forceinline__ uint32_t quad_bytes(uint32_t n0, uint32_t n1, uint32_t c, uint32_t spread) {
+  const uint32_t nsrc = QD == 0 ? n0 : QD == 1 ? (n0 >> 4) : QD == 2 ? n1 : (n1 >> 4);
+  const uint32_t cs = QD == 0 ? (c << 4) : QD == 1 ? (c << 2) : QD == 2 ? c : (c >> 2);
+  const uint32_t r = (nsrc & 0x0F0F0F0Fu) | (cs & 0xF0F0F0F0u);
+  return (spread & 0xC0C0C0C0u) | (r & 0x3F3F3F3Fu);
 }
 
-struct PageRef {
-  const uint8_t *blob;  // nullptr when the group has no page this iteration
-  uint32_t kw, vw;      // word counts
-  float ks, vs;
-  uint32_t tok0;        // first token index of the page
-  uint32_t ntok;        // tokens present in the page
-};
+// One interleaved-rANS step of the 64-lane stream: x = lane state, cur = wave-uniform word cursor, words = the
+// stream staged in LDS, last = highest valid word index (reads of lanes that do not renormalise are clamped).
+// Returns the slot entry (f | c << 11 | j << 22).
+__device__ __forceinline__ uint32_t rans_step(const uint32_t *__restrict__ tab, uint32_t &x, uint32_t &cur,
+                                              const uint16_t *__restrict__ words, uint32_t last) {
+  const uint32_t e = tab[x & (kSlots - 1)];
+  x = __umul24(e & (kSlots - 1), x >> CF_KV_RANS_PROB_BITS) + ((e >> 11) & (kSlots - 1));
+  const bool need = x < 65536u;
+  const uint64_t m = __builtin_amdgcn_ballot_w64(need);
+  const uint32_t idx = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+  const uint32_t w = words[min(cur + idx, last)];
+  x = need ? ((x << 16) | w) : x;
+  cur += static_cast<uint32_t>(__builtin_popcountll(m));
+  return e;
+}
 
-// rANS step for one quad. x: lane state; cursor: word index of the group's shared stream (group-uniform).
-__device__ __forceinline__ uint32_t rans_quad(const uint2 *__restrict__ tab, uint32_t &x, uint32_t &cursor,
-                                              const uint16_t *__restrict__ words, bool active, int gshift,
-                                              uint32_t below) {
-  const uint2 e = tab[x & (kSlots - 1)];
-  const uint32_t f = (e.x & (kSlots - 1)) + 1u;
-  const uint32_t cs = (e.x >> 11) & (kSlots - 1);
-  x = f * (x >> CF_KV_RANS_PROB_BITS) + cs;
-  const bool need = active && x < 65536u;
-  const uint64_t m = __ballot(need);
-  const uint32_t gm = static_cast<uint32_t>(m >> gshift) & 0xFFFFu;
-  if (need) x = (x << 16) | words[cursor + __popc(gm & below)];
-  cursor += __popc(gm);
-  return e.y;  // spread high parts
+constexpr int kHdr = 64;  // group header bytes
+
+// per-wave LDS buffer: the K and V word streams of one group (RANS) — also reused for the wave's final partial
+template <int D>
+constexpr int buf_u32() {
+  constexpr int words = 2 * ((D / 4) * 64 * CF_KV_RANS_PROB_BITS / 16 + 64);  // worst case K + V words
+  constexpr int red = kGqa * (D + 2);
+  return (words + 1) / 2 > red ? (words + 1) / 2 : red;
 }
 
 template <int D, int CODEC>
 __global__ __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_batched_desc d, uint32_t splits,
                                                               float *__restrict__ partial) {
-  constexpr int NQ = D / 4;        // quads per lane per stream
-  constexpr int NG = D / 16;       // low-part groups per lane
-  constexpr int LOWS = 3 * NG * 16;  // u32 words of one stream's low parts
-  __shared__ uint2 s_tab[2][CODEC == CF_KV_CODEC_RANS_HYBRID ? kSlots : 1];
-  __shared__ _Float16 s_q[2][kGqa][D];         // query heads, hi and lo f16 parts (softmax scale folded in)
-  __shared__ _Float16 s_p[kWaves][4][kGqa][16];  // per wave: [page group][head][token] probabilities * v_scale
-  __shared__ float s_red[kWaves][kGqa * (D + 2)];
+  constexpr int NQ = D / 4;          // quads per lane per stream
+  constexpr int NG = D / 16;         // low-part groups per lane
+  constexpr int LOWS = 3 * NG * 64;  // u32 words of one stream's low parts
+  constexpr bool RANS = CODEC == CF_KV_CODEC_RANS_HYBRID;
+  constexpr int BUF = buf_u32<D>();
+  constexpr uint32_t LAST = 2 * BUF - 1;
+  __shared__ uint32_t s_tab[2][RANS ? kSlots : 1];   // slot entries: f | c << 11 | j << 22
+  __shared__ uint32_t s_spread[RANS ? 256 : 1];      // joint symbol -> high parts at bits 6-7 of each byte
+  __shared__ _Float16 s_q[2][kGqa][D];               // query heads, f16 hi and lo parts (softmax scale folded in)
+  __shared__ _Float16 s_p[kWaves][4][kGqa][16];      // per wave: [page][head][token] probability * v_scale
+  __shared__ uint32_t s_buf[kWaves][BUF];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int G = lane >> 4, t = lane & 15;
@@ -98,12 +108,19 @@ __global__ __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_batched_desc
   const uint32_t gqa = d.query_head_count / d.kv_head_count;
 
   // ---- stage tables and queries
-  if constexpr (CODEC == CF_KV_CODEC_RANS_HYBRID) {
+  if constexpr (RANS) {
     const uint2 *tk = reinterpret_cast<const uint2 *>(d.tables + static_cast<size_t>(2 * head) * CF_KV_RANS_TABLE_BYTES);
     const uint2 *tv = tk + kSlots;
     for (uint32_t i = threadIdx.x; i < kSlots; i += kThreads) {
-      s_tab[0][i] = tk[i];
-      s_tab[1][i] = tv[i];
+      s_tab[0][i] = tk[i].x;
+      s_tab[1][i] = tv[i].x;
+    }
+    if (threadIdx.x < 256) {
+      const uint32_t j = threadIdx.x;
+      uint32_t v = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v |= ((j >> (2 * i)) & 3u) << (8 * i + 6);
+      s_spread[j] = v;
     }
   }
   for (int i = threadIdx.x; i < kGqa * D; i += kThreads) {
@@ -117,23 +134,39 @@ __global__ __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_batched_desc
   }
   __syncthreads();
 
-  // per-head sum of the query operand as the MFMA sees it (hi + lo), for the 1152 offset fold; every lane keeps
-  // all heads (no cross-lane read later inside lane-divergent code)
-  float qsum[kGqa];
+  // Query operands held in registers for the whole kernel: lane (block b = lane/4, row i = lane%4) keeps head i's
+  // dims of quad 16c + b; the K MFMA of quad q broadcasts block q%16's A operand to all 16 blocks (CBSZ 4).
+  constexpr int NC = NQ / 16 > 0 ? NQ / 16 : 1;
+  half4_t qhi[NC], qlo[NC];
 #pragma unroll
-  for (int h = 0; h < kGqa; ++h) {
-    qsum[h] = 0.0f;
-    for (int dd = 0; dd < D; ++dd) qsum[h] += static_cast<float>(s_q[0][h][dd]) + static_cast<float>(s_q[1][h][dd]);
+  for (int c = 0; c < NC; ++c) {
+    const int qd = 16 * c + (lane >> 2);
+    qhi[c] = (4 * qd < D) ? *reinterpret_cast<const half4_t *>(&s_q[0][lane & 3][4 * qd]) : half4_t{0, 0, 0, 0};
+    qlo[c] = (4 * qd < D) ? *reinterpret_cast<const half4_t *>(&s_q[1][lane & 3][4 * qd]) : half4_t{0, 0, 0, 0};
+  }
+  // per-head sum of the query operand as the MFMA sees it, for the 1152 offset fold (lanes 16h.. reduce head h)
+  float qsum[kGqa];
+  {
+    float part = 0.0f;
+    const int h = lane >> 4;
+#pragma unroll
+    for (int k = 0; k < D / 16; ++k) {
+      const int dd = (lane & 15) * (D / 16) + k;
+      part += static_cast<float>(s_q[0][h][dd]) + static_cast<float>(s_q[1][h][dd]);
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) part += __shfl_xor(part, o);
+#pragma unroll
+    for (int hh = 0; hh < kGqa; ++hh) qsum[hh] = __shfl(part, 16 * hh);
   }
 
   const uint32_t ntok_seq = d.seq_tokens[seq];
   const uint32_t qpos = d.query_pos[seq];
   const uint32_t visible = min(ntok_seq, qpos + 1);  // tokens [0, visible) are attended
-  const uint32_t npages = min((visible + 15) / 16, d.max_pages);
-  const uint32_t nquads = (npages + 3) / 4;
-  const uint32_t per = (nquads + splits - 1) / splits;
-  const uint32_t qa = min(nquads, split * per), qb = min(nquads, qa + per);
-  const uint32_t *prow = d.page_offsets + (static_cast<size_t>(seq) * d.kv_head_count + head) * d.max_pages;
+  const uint32_t ngroups = min((visible + 63) / 64, d.max_groups);
+  const uint32_t per = (ngroups + splits - 1) / splits;
+  const uint32_t ga = min(ngroups, split * per), gb = min(ngroups, ga + per);
+  const uint32_t *grow = d.group_offsets + (static_cast<size_t>(seq) * d.kv_head_count + head) * d.max_groups;
 
   float m_run[kGqa], l_run[kGqa], corr[kGqa];
   float4_t acc_v[D / 16];
@@ -146,71 +179,74 @@ __global__ __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_batched_desc
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) acc_v[i] = float4_t{0, 0, 0, 0};
 
-  const int gshift = 16 * G;
-  const uint32_t below = (1u << t) - 1u;
+  uint32_t *buf = s_buf[wave];
+  const uint16_t *wk = reinterpret_cast<const uint16_t *>(buf);
 
-  for (uint32_t qi = qa + wave; qi < qb; qi += kWaves) {
-    // ---- page of this lane group
-    PageRef pg{};
-    const uint32_t p = 4 * qi + G;
-    if (p < npages) {
-      pg.blob = d.pool + static_cast<size_t>(prow[p]) * 16;
-      const cf_kv_rans_page_header *hd = reinterpret_cast<const cf_kv_rans_page_header *>(pg.blob);
-      pg.kw = hd->k_word_count;
-      pg.vw = hd->v_word_count;
-      pg.ks = hd->k_scale;
-      pg.vs = hd->v_scale;
-      pg.tok0 = 16 * p;
-      pg.ntok = min(16u, visible - 16 * p);
+  for (uint32_t gi = ga + wave; gi < gb; gi += kWaves) {
+    const uint8_t *blob = d.pool + static_cast<size_t>(grow[gi]) * 16;
+    const uint32_t cnt = *reinterpret_cast<const uint32_t *>(blob + 4);
+    const uint32_t kw = cnt & 0xFFFFu, vw = cnt >> 16;
+    const uint32_t tcG = reinterpret_cast<const uint16_t *>(blob + 8)[G];
+    const float ks = reinterpret_cast<const float *>(blob + 32)[G];
+    const float vs = reinterpret_cast<const float *>(blob + 48)[G];
+    const uint32_t tok = 64 * gi + 16 * G + t;
+
+    if constexpr (RANS) {  // word streams -> LDS (coalesced u32 copy)
+      const uint32_t *src = reinterpret_cast<const uint32_t *>(blob + kHdr + 512 + 2 * LOWS * 4);
+      const uint32_t n32 = (kw + vw + 1) / 2;
+      for (uint32_t i = lane; i < n32; i += 64) buf[i] = src[i];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    const bool active = pg.blob != nullptr;
 
-    // ---- K phase: scores of token t of page G for the 4 heads
+    // ---- K and V streams decoded together (two independent rANS chains per lane). K quads feed the score MFMAs
+    // immediately; V quads stay packed (4 symbol bytes per register) until the probabilities exist.
     float4_t sa = {0, 0, 0, 0}, sb = {0, 0, 0, 0};
-    if constexpr (CODEC == CF_KV_CODEC_RANS_HYBRID) {
-      const uint32_t *st = active ? reinterpret_cast<const uint32_t *>(pg.blob + 32) : nullptr;
-      const uint32_t *lows = active ? reinterpret_cast<const uint32_t *>(pg.blob + 160) : nullptr;
-      const uint16_t *words = active ? reinterpret_cast<const uint16_t *>(pg.blob + 160 + 2 * LOWS * 4) : nullptr;
-      uint32_t x = active ? st[t] : 0u, cur = 0;
-#pragma unroll 2
-      for (int g = 0; g < NG; ++g) {
-        uint32_t n0 = 0, n1 = 0, c = 0;
-        if (active) {
-          n0 = lows[(g * 3 + 0) * 16 + t];
-          n1 = lows[(g * 3 + 1) * 16 + t];
-          c = lows[(g * 3 + 2) * 16 + t];
-        }
+    uint32_t vb[NQ];
+    {
+      const uint32_t *st = reinterpret_cast<const uint32_t *>(blob + kHdr);
+      const uint32_t *lowk = reinterpret_cast<const uint32_t *>(blob + kHdr + 512);
+      const uint32_t *raw = reinterpret_cast<const uint32_t *>(blob + kHdr);
+      uint32_t xk = RANS ? st[lane] : 0u, xv = RANS ? st[64 + lane] : 0u;
+      uint32_t ck = 0, cv = kw;
+      uint32_t kl[3] = {0, 0, 0}, vl[3] = {0, 0, 0};
+      [&]<int... Q>(std::integer_sequence<int, Q...>) {
+        (
+            [&] {
+              constexpr int q = Q, g = q / 4, qd = q % 4;
+              uint32_t kbytes, vbytes;
+              if constexpr (RANS) {
+                if constexpr (qd == 0) {
 #pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          const uint32_t hi = rans_quad(s_tab[0], x, cur, words, active, gshift, below);
-          const uint32_t bytes = active ? (lows_of(n0, n1, c, qd) | hi) : 0x80808080u;
-          const half4_t bk = bytes_to_half4(bytes);
-          const int q = 4 * g + qd;
-          const half4_t a_hi = *reinterpret_cast<const half4_t *>(&s_q[0][lane & 3][4 * q]);
-          const half4_t a_lo = *reinterpret_cast<const half4_t *>(&s_q[1][lane & 3][4 * q]);
-          sa = mfma4(a_hi, bk, sa);
-          sb = mfma4(a_lo, bk, sb);
-        }
-      }
-    } else {  // CF_KV_CODEC_INT8
-      const uint32_t *kb = active ? reinterpret_cast<const uint32_t *>(pg.blob + 32) : nullptr;
-#pragma unroll 4
-      for (int q = 0; q < NQ; ++q) {
-        const uint32_t bytes = active ? kb[q * 16 + t] : 0x80808080u;
-        const half4_t bk = bytes_to_half4(bytes);
-        const half4_t a_hi = *reinterpret_cast<const half4_t *>(&s_q[0][lane & 3][4 * q]);
-        const half4_t a_lo = *reinterpret_cast<const half4_t *>(&s_q[1][lane & 3][4 * q]);
-        sa = mfma4(a_hi, bk, sa);
-        sb = mfma4(a_lo, bk, sb);
-      }
+                  for (int w = 0; w < 3; ++w) {
+                    kl[w] = lowk[(g * 3 + w) * 64 + lane];
+                    vl[w] = lowk[LOWS + (g * 3 + w) * 64 + lane];
+                  }
+                }
+                const uint32_t ek = rans_step(s_tab[0], xk, ck, wk, LAST);
+                const uint32_t ev = rans_step(s_tab[1], xv, cv, wk, LAST);
+                kbytes = quad_bytes<qd>(kl[0], kl[1], kl[2], s_spread[ek >> 22]);
+                vbytes = quad_bytes<qd>(vl[0], vl[1], vl[2], s_spread[ev >> 22]);
+              } else {
+                kbytes = raw[q * 64 + lane];
+                vbytes = raw[NQ * 64 + q * 64 + lane];
+              }
+              vb[q] = vbytes;
+              const half4_t bk = bytes_to_half4(kbytes);
+              sa = __builtin_amdgcn_mfma_f32_4x4x4f16(qhi[q / 16], bk, sa, 4, q % 16, 0);
+              sb = __builtin_amdgcn_mfma_f32_4x4x4f16(qlo[q / 16], bk, sb, 4, q % 16, 0);
+            }(),
+            ...);
+      }(std::make_integer_sequence<int, NQ>{});
     }
 
     // ---- online softmax over the wavefront's 64 tokens
-    const bool tok_ok = active && static_cast<uint32_t>(t) < pg.ntok;
+    const bool tok_ok = static_cast<uint32_t>(t) < tcG && tok < visible;
     float s[kGqa], mx[kGqa];
 #pragma unroll
     for (int h = 0; h < kGqa; ++h) {
-      s[h] = tok_ok ? (sa[h] + sb[h] - kOffset * qsum[h]) * pg.ks : -INFINITY;
+      s[h] = tok_ok ? (sa[h] + sb[h] - kOffset * qsum[h]) * ks : -INFINITY;
       mx[h] = s[h];
     }
 #pragma unroll
@@ -224,7 +260,7 @@ __global__ __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_batched_desc
       alpha[h] = (m_run[h] == -INFINITY) ? 0.0f : __expf(m_run[h] - mn);
       const float pr = tok_ok ? __expf(s[h] - mn) : 0.0f;
       l_run[h] = l_run[h] * alpha[h] + pr;
-      const _Float16 pv = static_cast<_Float16>(pr * (active ? pg.vs : 0.0f));
+      const _Float16 pv = static_cast<_Float16>(pr * vs);
       s_p[wave][G][h][t] = pv;
       corr[h] = corr[h] * alpha[h] + kOffset * static_cast<float>(pv);
       m_run[h] = mn;
@@ -233,50 +269,20 @@ __global__ __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_batched_desc
     for (int i = 0; i < D / 16; ++i)
 #pragma unroll
       for (int h = 0; h < kGqa; ++h) acc_v[i][h] *= alpha[h];
-    __builtin_amdgcn_wave_barrier();  // s_p written by this wave only; LDS ops of a wave complete in order
-
-    // ---- V phase: out[h][t + 16i] += sum over tokens of p * v
-    if constexpr (CODEC == CF_KV_CODEC_RANS_HYBRID) {
-      const uint32_t *st = active ? reinterpret_cast<const uint32_t *>(pg.blob + 32 + 64) : nullptr;
-      const uint32_t *lows = active ? reinterpret_cast<const uint32_t *>(pg.blob + 160 + LOWS * 4) : nullptr;
-      const uint16_t *words =
-          active ? reinterpret_cast<const uint16_t *>(pg.blob + 160 + 2 * LOWS * 4) + pg.kw : nullptr;
-      uint32_t x = active ? st[t] : 0u, cur = 0;
-#pragma unroll 1
-      for (int tq = 0; tq < 4; ++tq) {
-        const half4_t pa = *reinterpret_cast<const half4_t *>(&s_p[wave][G][lane & 3][4 * tq]);
-#pragma unroll
-        for (int gg = 0; gg < NG / 4; ++gg) {
-          const int g = tq * (NG / 4) + gg;  // low-part group: quads 4g .. 4g+3 of this lane
-          uint32_t n0 = 0, n1 = 0, c = 0;
-          if (active) {
-            n0 = lows[(g * 3 + 0) * 16 + t];
-            n1 = lows[(g * 3 + 1) * 16 + t];
-            c = lows[(g * 3 + 2) * 16 + t];
-          }
-#pragma unroll
-          for (int qd = 0; qd < 4; ++qd) {
-            const uint32_t hi = rans_quad(s_tab[1], x, cur, words, active, gshift, below);
-            const uint32_t bytes = active ? (lows_of(n0, n1, c, qd) | hi) : 0x80808080u;
-            const int i = 4 * gg + qd;  // dim index: lane dim t + 16 i
-            acc_v[i] = mfma4(pa, bytes_to_half4(bytes), acc_v[i]);
-          }
-        }
-      }
-    } else {
-      const uint32_t *vb = active ? reinterpret_cast<const uint32_t *>(pg.blob + 32 + 16 * D) : nullptr;
-#pragma unroll 1
-      for (int tq = 0; tq < 4; ++tq) {
-        const half4_t pa = *reinterpret_cast<const half4_t *>(&s_p[wave][G][lane & 3][4 * tq]);
-#pragma unroll
-        for (int i = 0; i < D / 16; ++i) {
-          const int q = tq * (D / 16) + i;
-          const uint32_t bytes = active ? vb[q * 16 + t] : 0x80808080u;
-          acc_v[i] = mfma4(pa, bytes_to_half4(bytes), acc_v[i]);
-        }
-      }
-    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- V MFMAs: out[h][t + 16i] += sum over the quad's 4 tokens of p * v
+#pragma unroll
+    for (int tq = 0; tq < 4; ++tq) {
+      const half4_t pa = *reinterpret_cast<const half4_t *>(&s_p[wave][G][lane & 3][4 * tq]);
+#pragma unroll
+      for (int i = 0; i < D / 16; ++i) acc_v[i] = mfma4(pa, bytes_to_half4(vb[tq * (D / 16) + i]), acc_v[i]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 
   // ---- reduce the wavefront: sum the 4 page groups (lanes t, t+16, t+32, t+48), l and corr over all lanes
@@ -296,8 +302,8 @@ __global__ __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_batched_desc
       l_run[h] += __shfl_xor(l_run[h], o);
       corr[h] += __shfl_xor(corr[h], o);
     }
-  // wave partial -> LDS: [h][D] acc (minus offset correction), then m, l
-  float *red = s_red[wave];
+  // wave partial -> the wave's LDS buffer: [h][D] acc (minus offset correction), then m, l
+  float *red = reinterpret_cast<float *>(buf);
   if (lane < 16) {
 #pragma unroll
     for (int i = 0; i < D / 16; ++i)
@@ -314,15 +320,16 @@ __global__ __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_batched_desc
   for (int i = threadIdx.x; i < kGqa * D; i += kThreads) {
     const int h = i / D, dd = i % D;
     float m = -INFINITY;
-    for (int w = 0; w < kWaves; ++w) m = fmaxf(m, s_red[w][h * (D + 2) + D]);
+    for (int w = 0; w < kWaves; ++w) m = fmaxf(m, reinterpret_cast<const float *>(s_buf[w])[h * (D + 2) + D]);
     float l = 0.0f, o = 0.0f;
     if (m != -INFINITY)
       for (int w = 0; w < kWaves; ++w) {
-        const float mw = s_red[w][h * (D + 2) + D];
+        const float *rw = reinterpret_cast<const float *>(s_buf[w]);
+        const float mw = rw[h * (D + 2) + D];
         if (mw == -INFINITY) continue;
         const float sc = __expf(mw - m);
-        l += s_red[w][h * (D + 2) + D + 1] * sc;
-        o += s_red[w][h * (D + 2) + dd] * sc;
+        l += rw[h * (D + 2) + D + 1] * sc;
+        o += rw[h * (D + 2) + dd] * sc;
       }
     if (splits == 1) {
       if (static_cast<uint32_t>(h) < gqa)
@@ -364,9 +371,8 @@ __global__ __launch_bounds__(kGqa * D) void kv_merge_kernel(cf_kv_batched_desc d
 uint32_t choose_splits(const cf_kv_batched_desc *d) {
   if (d->splits) return d->splits;
   const uint32_t units = d->seq_count * d->kv_head_count;
-  const uint32_t quads = (d->max_pages + 3) / 4;
   uint32_t s = (2048 + units - 1) / units;           // aim at ~2048 workgroups (8 per CU)
-  s = std::min<uint32_t>(s, std::max<uint32_t>(1, quads / kWaves));  // keep >= one quad per wavefront
+  s = std::min<uint32_t>(s, std::max<uint32_t>(1, d->max_groups / kWaves));  // keep >= one group per wavefront
   return std::max<uint32_t>(1, std::min<uint32_t>(s, 64));
 }
 
@@ -375,7 +381,7 @@ uint32_t choose_splits(const cf_kv_batched_desc *d) {
 extern "C" cf_status cf_kv_validate_batched_desc(const cf_kv_batched_desc *d) {
   if (!d || d->struct_size != sizeof(cf_kv_batched_desc) || d->abi_version != CF_KV_EXT_ABI_VERSION)
     return CF_ERR_INVALID_ARGUMENT;
-  if (!d->pool || !d->page_offsets || !d->seq_tokens || !d->query_pos || !d->queries || !d->output ||
+  if (!d->pool || !d->group_offsets || !d->seq_tokens || !d->query_pos || !d->queries || !d->output ||
       d->seq_count == 0 || d->kv_head_count == 0 || d->query_head_count == 0 ||
       d->query_head_count % d->kv_head_count != 0 || !std::isfinite(d->softmax_scale))
     return CF_ERR_INVALID_ARGUMENT;

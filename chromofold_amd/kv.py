@@ -5,7 +5,7 @@ Two entry points are mirrored:
     device pool, per-(sequence, head) page tables, split-context workspace) — the benchmark path;
   * the legacy single-sequence seam cf_kv_paged_attention_async of include/chromofold/kv_cuda.h (see legacy.py).
 
-Encoding happens on the host through the library's C encoder (cf_kv_encode_pages); pools, page tables, queries
+Encoding happens on the host through the library's C encoder (cf_kv_encode_groups); pools, page tables, queries
 and outputs live in HBM as torch tensors. Every launch goes through libchromofold.so.
 """
 from __future__ import annotations
@@ -21,23 +21,25 @@ from . import _abi as A
 CODEC_INT8, CODEC_RANS_HYBRID = 1, 2
 PAGE_TOKENS = 16
 TABLE_BYTES = 16384
-EXT_ABI_VERSION = 1
+EXT_ABI_VERSION = 2
+GROUP_PAGES = 4
+GROUP_TOKENS = PAGE_TOKENS * GROUP_PAGES
 
 
 class cf_kv_batched_desc(C.Structure):
     _fields_ = [("struct_size", A.U32), ("abi_version", A.U32), ("codec", A.U32), ("seq_count", A.U32),
-                ("kv_head_count", A.U32), ("query_head_count", A.U32), ("head_dim", A.U32), ("max_pages", A.U32),
-                ("pool", A.P), ("page_offsets", A.P), ("seq_tokens", A.P), ("query_pos", A.P), ("tables", A.P),
+                ("kv_head_count", A.U32), ("query_head_count", A.U32), ("head_dim", A.U32), ("max_groups", A.U32),
+                ("pool", A.P), ("group_offsets", A.P), ("seq_tokens", A.P), ("query_pos", A.P), ("tables", A.P),
                 ("queries", A.P), ("output", A.P), ("softmax_scale", A.F32), ("splits", A.U32),
                 ("workspace", A.P), ("workspace_bytes", A.U64)]
 
 
-A.declare("cf_kv_encode_pages", A.I32, [A.U32, A.P, A.P, A.U64, A.P, A.U32, A.P, A.P, A.P, A.U64, A.U64, A.P,
-                                        A.P, A.U32])
-A.declare("cf_kv_encode_page", A.I32, [A.U32, A.P, A.P, A.U32, A.U32, A.P, A.P, A.U32, A.U32, A.P, A.U64, A.P])
+A.declare("cf_kv_encode_groups", A.I32, [A.U32, A.P, A.P, A.U64, A.P, A.P, A.P, A.U32, A.P, A.P, A.P, A.U64, A.U64,
+                                         A.P, A.P, A.U32])
+A.declare("cf_kv_encode_group", A.I32, [A.U32, A.P, A.P, A.U32, A.P, A.U32, A.P, A.P, A.U32, A.U32, A.P, A.U64, A.P])
 A.declare("cf_kv_rans_build_table", A.I32, [A.P, A.P])
 A.declare("cf_kv_rans_page_histogram", A.I32, [A.P, A.U32, A.U32, A.P])
-A.declare("cf_kv_page_blob_max_bytes", A.U64, [A.U32, A.U32])
+A.declare("cf_kv_group_blob_max_bytes", A.U64, [A.U32, A.U32])
 A.declare("cf_kv_batched_workspace_bytes", A.U64, [A.P])
 A.declare("cf_kv_validate_batched_desc", A.I32, [A.P])
 A.declare("cf_kv_paged_attention_batched_async", A.I32, [A.P, A.P])
@@ -59,23 +61,26 @@ def build_table(pages: np.ndarray) -> np.ndarray:
     return out
 
 
-def encode_pages(codec: int, keys: np.ndarray, values: np.ndarray, head_dim: int, tables: np.ndarray | None,
-                 heads: np.ndarray | None = None, token_counts: np.ndarray | None = None,
-                 threads: int = 0) -> tuple[np.ndarray, np.ndarray]:
-    """Encode page-major pages keys/values [n, 16, D] -> (blob bytes, offsets/16 relative to the blob start)."""
+def encode_groups(codec: int, keys: np.ndarray, values: np.ndarray, head_dim: int, tables: np.ndarray | None,
+                  first_page: np.ndarray, page_counts: np.ndarray, heads: np.ndarray | None = None,
+                  token_counts: np.ndarray | None = None, threads: int = 0) -> tuple[np.ndarray, np.ndarray]:
+    """Encode page groups of page-major pages keys/values [n_pages, 16, D] -> (blob bytes, offsets/16)."""
     L = A.lib()
     keys = np.ascontiguousarray(keys, np.float32)
     values = np.ascontiguousarray(values, np.float32)
-    n = keys.shape[0]
-    cap = int(L.cf_kv_page_blob_max_bytes(codec, head_dim)) * n
+    first_page = np.ascontiguousarray(first_page, np.uint64)
+    page_counts = np.ascontiguousarray(page_counts, np.uint32)
+    n = first_page.size
+    cap = int(L.cf_kv_group_blob_max_bytes(codec, head_dim)) * n
     pool = np.zeros(cap, np.uint8)
     offs = np.zeros(n, np.uint32)
     end = C.c_uint64(0)
     hd = None if heads is None else np.ascontiguousarray(heads, np.uint32)
     tc = None if token_counts is None else np.ascontiguousarray(token_counts, np.uint32)
-    st = L.cf_kv_encode_pages(codec, _np_ptr(keys), _np_ptr(values), n, _np_ptr(tc), head_dim, _np_ptr(tables),
-                              _np_ptr(hd), _np_ptr(pool), cap, 0, _np_ptr(offs), C.byref(end), threads)
-    A.check(st, "cf_kv_encode_pages")
+    st = L.cf_kv_encode_groups(codec, _np_ptr(keys), _np_ptr(values), n, _np_ptr(first_page), _np_ptr(page_counts),
+                               _np_ptr(tc), head_dim, _np_ptr(tables), _np_ptr(hd), _np_ptr(pool), cap, 0,
+                               _np_ptr(offs), C.byref(end), threads)
+    A.check(st, "cf_kv_encode_groups")
     return pool[:end.value], offs
 
 
@@ -86,9 +91,9 @@ class BatchedKv:
     seq_count: int
     kv_heads: int
     head_dim: int
-    max_pages: int
+    max_groups: int
     pool: torch.Tensor                 # uint8 [bytes]
-    page_offsets: torch.Tensor         # int32 [S, H, max_pages] (u32 bits)
+    group_offsets: torch.Tensor        # int32 [S, H, max_groups] (u32 bits)
     seq_tokens: torch.Tensor           # int32 [S]
     tables: torch.Tensor | None        # uint8 [2H * 16 KiB]
     host_pool: np.ndarray | None = None
@@ -111,9 +116,9 @@ class BatchedKv:
         d.kv_head_count = self.kv_heads
         d.query_head_count = queries.shape[1]
         d.head_dim = self.head_dim
-        d.max_pages = self.max_pages
+        d.max_groups = self.max_groups
         d.pool = self.pool.data_ptr()
-        d.page_offsets = self.page_offsets.data_ptr()
+        d.group_offsets = self.group_offsets.data_ptr()
         d.seq_tokens = self.seq_tokens.data_ptr()
         d.query_pos = query_pos.data_ptr()
         d.tables = None if self.tables is None else self.tables.data_ptr()
@@ -139,44 +144,51 @@ class BatchedKv:
 def build_batched(codec: int, kv_source, seq_count: int, kv_heads: int, seq_tokens: np.ndarray, head_dim: int,
                   tables: np.ndarray | None, device="cuda", keep_host: bool = False,
                   shared: dict | None = None) -> BatchedKv:
-    """Encode and upload pages. kv_source(s) -> (K, V) fp32 arrays [kv_heads, T_s, D] for sequence s.
-    `shared` optionally maps sequence s -> (donor sequence, prefix pages): the first `prefix pages` pages of s are
+    """Encode and upload page groups. kv_source(s) -> (K, V) fp32 arrays [kv_heads, T_s, D] for sequence s.
+    `shared` optionally maps sequence s -> (donor sequence, prefix groups): the first `prefix groups` groups of s are
     the donor's blobs (no copy), modelling refcounted shared-prefix pages."""
     seq_tokens = np.asarray(seq_tokens, np.uint32)
-    max_pages = int((seq_tokens.max() + PAGE_TOKENS - 1) // PAGE_TOKENS)
-    offsets = np.zeros((seq_count, kv_heads, max_pages), np.uint32)
+    max_groups = int((seq_tokens.max() + GROUP_TOKENS - 1) // GROUP_TOKENS)
+    offsets = np.zeros((seq_count, kv_heads, max_groups), np.uint32)
     blobs, at = [], 0
     for s in range(seq_count):
         T = int(seq_tokens[s])
         npg = (T + PAGE_TOKENS - 1) // PAGE_TOKENS
-        share = (shared or {}).get(s)
+        ngr = (npg + GROUP_PAGES - 1) // GROUP_PAGES
         first = 0
+        share = (shared or {}).get(s)
         if share is not None:
             donor, first = share
             offsets[s, :, :first] = offsets[donor, :, :first]
+        if first >= ngr:
+            continue
         K, V = kv_source(s)
         pad = npg * PAGE_TOKENS - T
         if pad:
             K = np.concatenate([K, np.zeros((kv_heads, pad, head_dim), np.float32)], 1)
             V = np.concatenate([V, np.zeros((kv_heads, pad, head_dim), np.float32)], 1)
-        Kp = K[:, first * PAGE_TOKENS:].reshape(kv_heads * (npg - first), PAGE_TOKENS, head_dim)
-        Vp = V[:, first * PAGE_TOKENS:].reshape(kv_heads * (npg - first), PAGE_TOKENS, head_dim)
-        heads = np.repeat(np.arange(kv_heads, dtype=np.uint32), npg - first)
-        tc = np.full(kv_heads * (npg - first), PAGE_TOKENS, np.uint32)
+        p0 = first * GROUP_PAGES
+        Kp = np.ascontiguousarray(K[:, p0 * PAGE_TOKENS:]).reshape(kv_heads * (npg - p0), PAGE_TOKENS, head_dim)
+        Vp = np.ascontiguousarray(V[:, p0 * PAGE_TOKENS:]).reshape(kv_heads * (npg - p0), PAGE_TOKENS, head_dim)
+        tc = np.full((kv_heads, npg - p0), PAGE_TOKENS, np.uint32)
         if pad:
-            tc.reshape(kv_heads, npg - first)[:, -1] = PAGE_TOKENS - pad
-        if Kp.shape[0]:
-            blob, offs = encode_pages(codec, Kp, Vp, head_dim, tables, heads, tc)
-            offsets[s, :, first:npg] = (offs + at // 16).reshape(kv_heads, npg - first)
-            blobs.append(blob)
-            at += blob.size
+            tc[:, -1] = PAGE_TOKENS - pad
+        gl = np.arange(first, ngr)
+        first_page = (np.arange(kv_heads)[:, None] * (npg - p0) + (gl[None, :] - first) * GROUP_PAGES).ravel()
+        page_counts = np.broadcast_to(np.minimum(GROUP_PAGES, npg - gl * GROUP_PAGES)[None, :],
+                                      (kv_heads, gl.size)).ravel()
+        heads = np.repeat(np.arange(kv_heads, dtype=np.uint32), gl.size)
+        blob, offs = encode_groups(codec, Kp, Vp, head_dim, tables, first_page, page_counts, heads, tc.ravel())
+        offsets[s, :, first:ngr] = (offs + at // 16).reshape(kv_heads, gl.size)
+        blobs.append(blob)
+        at += blob.size
     host_pool = np.concatenate(blobs) if blobs else np.zeros(16, np.uint8)
     assert at // 16 < 2 ** 32
     pool = torch.from_numpy(host_pool).to(device)
     t_off = torch.from_numpy(offsets.view(np.int32)).to(device)
     t_tok = torch.from_numpy(seq_tokens.view(np.int32)).to(device)
     t_tab = None if tables is None else torch.from_numpy(np.ascontiguousarray(tables).ravel()).to(device)
-    kv = BatchedKv(codec, seq_count, kv_heads, head_dim, max_pages, pool, t_off, t_tok, t_tab)
+    kv = BatchedKv(codec, seq_count, kv_heads, head_dim, max_groups, pool, t_off, t_tok, t_tab)
     if keep_host:
         kv.host_pool, kv.host_offsets, kv.host_tables = host_pool, offsets, tables
     return kv

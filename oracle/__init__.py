@@ -86,7 +86,7 @@ def _declare(L):
         "or_paged_attention_f64": (C.c_int, [P, U32, U32, U32, U32, U32, U32, C.c_float, U32, P, P, P, P, P, P,
                                              P, P, U32, U32, P]),
         "or_dense_attention_f64": (None, [P, U32, P, P, U32, C.c_float, P]),
-        "or_kv_decode_page": (C.c_int, [P, P, U32, P, P, P, P, P]),
+        "or_kv_decode_group": (C.c_int, [P, P, U32, P, P, P, P, P]),
         "or_kv_quantize_page_absmax": (None, [P, U32, P, P]),
         "or_softmax_merge": (None, [P, P, P, C.c_double, C.c_double, P, U32]),
     }
@@ -322,18 +322,20 @@ def rrr_decode_all(classes, offsets, nblocks: int, off_base_bit: int = 0) -> np.
 
 
 # ------------------------------------------------------------------ paged KV
-def kv_decode_page(blob: np.ndarray, tables: np.ndarray | None, head: int, head_dim: int):
-    """Decode one kv_codec_ext page blob -> (k_sym [16, D], v_sym [16, D], k_scale, v_scale, token_count)."""
+def kv_decode_group(blob: np.ndarray, tables: np.ndarray | None, head: int, head_dim: int):
+    """Decode one kv_codec_ext group blob -> (k_sym [4, 16, D], v_sym [4, 16, D], k_scales[4], v_scales[4],
+    token_counts[4])."""
     blob = np.ascontiguousarray(blob, np.uint8)
-    ks = np.zeros((16, head_dim), np.uint8)
-    vs = np.zeros((16, head_dim), np.uint8)
-    ksc, vsc, tc = C.c_float(0), C.c_float(0), C.c_uint32(0)
+    ks = np.zeros((4, 16, head_dim), np.uint8)
+    vs = np.zeros((4, 16, head_dim), np.uint8)
+    ksc = np.zeros(4, np.float32)
+    vsc = np.zeros(4, np.float32)
+    tc = np.zeros(4, np.uint32)
     tab = None if tables is None else np.ascontiguousarray(tables, np.uint8)
-    rc = lib().or_kv_decode_page(_ptr(blob), _ptr(tab), head, _ptr(ks), _ptr(vs), C.byref(ksc), C.byref(vsc),
-                                 C.byref(tc))
+    rc = lib().or_kv_decode_group(_ptr(blob), _ptr(tab), head, _ptr(ks), _ptr(vs), _ptr(ksc), _ptr(vsc), _ptr(tc))
     if rc != 0:
-        raise ValueError("page blob failed to decode")
-    return ks, vs, ksc.value, vsc.value, tc.value
+        raise ValueError("group blob failed to decode")
+    return ks, vs, ksc, vsc, tc
 
 
 def kv_quantize_absmax(x: np.ndarray):

@@ -164,91 +164,82 @@ void or_dense_attention_f64(const float *q, uint32_t D, const float *k, const fl
 }
 
 // ---------------------------------------------------------------------------------------- kv_codec_ext pages
-// Decode one INT8 / RANS_HYBRID page blob into symbols [16, D] for K and V (token-major) plus the two scales.
-// tables: table blobs (16 KiB each); the K stream uses tables[2*head], V uses tables[2*head+1].
-// Returns 0 on success, -1 on a format inconsistency (bad codec, stream over/under-run, final state != 2^16).
-int or_kv_decode_page(const uint8_t *blob, const uint8_t *tables, uint32_t head, uint8_t *k_sym, uint8_t *v_sym,
-                      float *k_scale, float *v_scale, uint32_t *token_count) {
+// Decode one INT8 / RANS_HYBRID page-group blob into symbols [4 pages][16 tokens][D] for K and V (token-major)
+// plus per-page scales and token counts. tables: table blobs (16 KiB each); K uses tables[2*head], V
+// tables[2*head+1]. Returns 0 on success, -1 on a format inconsistency (bad codec, stream over/under-run, a final
+// state != 2^16).
+int or_kv_decode_group(const uint8_t *blob, const uint8_t *tables, uint32_t head, uint8_t *k_sym, uint8_t *v_sym,
+                       float *k_scale, float *v_scale, uint32_t *token_count) {
   uint32_t codec;
-  uint16_t kw, vw, tc, D;
+  uint16_t kw, vw, tc[4], D, npg;
   std::memcpy(&codec, blob, 4);
   std::memcpy(&kw, blob + 4, 2);
   std::memcpy(&vw, blob + 6, 2);
-  std::memcpy(k_scale, blob + 8, 4);
-  std::memcpy(v_scale, blob + 12, 4);
-  std::memcpy(&tc, blob + 16, 2);
-  std::memcpy(&D, blob + 18, 2);
-  *token_count = tc;
-  const uint32_t nq = D / 4;
-  // symbol of lane t, quad q, position i -> (token, dim)
-  auto where = [&](bool is_v, uint32_t t, uint32_t q, uint32_t i, uint32_t *tok, uint32_t *dim) {
-    if (!is_v) {
-      *tok = t;
-      *dim = 4 * q + i;
-    } else {
-      const uint32_t per = D / 16;
-      *tok = 4 * (q / per) + i;
-      *dim = t + 16 * (q % per);
-    }
+  std::memcpy(tc, blob + 8, 8);
+  std::memcpy(&D, blob + 16, 2);
+  std::memcpy(&npg, blob + 18, 2);
+  std::memcpy(k_scale, blob + 32, 16);
+  std::memcpy(v_scale, blob + 48, 16);
+  for (int g = 0; g < 4; ++g) token_count[g] = tc[g];
+  const uint32_t nq = D / 4, page = 16u * D;
+  // lane L (page L/16, t = L%16), quad q, position i -> flat index into [4][16][D]
+  auto where = [&](bool is_v, uint32_t L, uint32_t q, uint32_t i) -> size_t {
+    const uint32_t G = L / 16, t = L % 16;
+    if (!is_v) return (size_t)G * page + (size_t)t * D + 4 * q + i;
+    const uint32_t per = D / 16;
+    return (size_t)G * page + (size_t)(4 * (q / per) + i) * D + t + 16 * (q % per);
   };
-  if (codec == 1) {  // INT8: word (q*16 + t) = 4 bytes of quad q of lane t
+  if (codec == 1) {  // INT8: word (q*64 + L) = 4 bytes of quad q of lane L
     for (int s = 0; s < 2; ++s) {
-      const uint8_t *b = blob + 32 + (size_t)s * 16 * D;
+      const uint8_t *b = blob + 64 + (size_t)s * 64 * D;
       uint8_t *out = s ? v_sym : k_sym;
       for (uint32_t q = 0; q < nq; ++q)
-        for (uint32_t t = 0; t < 16; ++t)
-          for (uint32_t i = 0; i < 4; ++i) {
-            uint32_t tok, dim;
-            where(s == 1, t, q, i, &tok, &dim);
-            out[(size_t)tok * D + dim] = b[(q * 16 + t) * 4 + i];
-          }
+        for (uint32_t L = 0; L < 64; ++L)
+          for (uint32_t i = 0; i < 4; ++i) out[where(s == 1, L, q, i)] = b[(q * 64 + L) * 4 + i];
     }
     return 0;
   }
   if (codec != 2) return -1;
-  const uint32_t nlow = 3 * (D / 16) * 16;
-  const uint32_t *states = reinterpret_cast<const uint32_t *>(blob + 32);
-  const uint32_t *lows = reinterpret_cast<const uint32_t *>(blob + 160);
-  const uint16_t *words = reinterpret_cast<const uint16_t *>(blob + 160 + 2 * (size_t)nlow * 4);
+  const uint32_t nlow = 3 * (D / 16) * 64;
+  const uint32_t *states = reinterpret_cast<const uint32_t *>(blob + 64);
+  const uint32_t *lows = reinterpret_cast<const uint32_t *>(blob + 576);
+  const uint16_t *words = reinterpret_cast<const uint16_t *>(blob + 576 + 2 * (size_t)nlow * 4);
   for (int s = 0; s < 2; ++s) {
     const uint8_t *tab = tables + (size_t)(2 * head + s) * 16384;
     const uint16_t *w = words + (s ? kw : 0);
     const uint32_t nw = s ? vw : kw;
-    uint32_t x[16];
-    for (int t = 0; t < 16; ++t) x[t] = states[s * 16 + t];
+    uint32_t x[64];
+    for (int L = 0; L < 64; ++L) x[L] = states[s * 64 + L];
     uint32_t cur = 0;
     uint8_t *out = s ? v_sym : k_sym;
+    const uint32_t *lw = lows + (size_t)s * nlow;
     for (uint32_t q = 0; q < nq; ++q) {
-      uint32_t j[16];
-      for (uint32_t t = 0; t < 16; ++t) {  // all lanes decode step q
+      uint32_t j[64];
+      for (uint32_t L = 0; L < 64; ++L) {  // all lanes decode quad q
         uint32_t lo;
-        const uint32_t slot = x[t] & 2047u;
-        std::memcpy(&lo, tab + 8 * slot, 4);
-        const uint32_t f = (lo & 2047u) + 1, cs = (lo >> 11) & 2047u;
-        j[t] = (lo >> 22) & 255u;
-        x[t] = f * (x[t] >> 11) + cs;
+        std::memcpy(&lo, tab + 8 * (x[L] & 2047u), 4);
+        const uint32_t f = lo & 2047u, c = (lo >> 11) & 2047u;
+        j[L] = (lo >> 22) & 255u;
+        x[L] = f * (x[L] >> 11) + c;
       }
-      for (uint32_t t = 0; t < 16; ++t)  // renormalisation reads in lane order
-        if (x[t] < 65536u) {
+      for (uint32_t L = 0; L < 64; ++L)  // renormalisation reads in ascending lane order
+        if (x[L] < 65536u) {
           if (cur >= nw) return -1;
-          x[t] = (x[t] << 16) | w[cur++];
+          x[L] = (x[L] << 16) | w[cur++];
         }
-      for (uint32_t t = 0; t < 16; ++t) {
-        const uint32_t g = q / 4, qd = q % 4;
-        const uint32_t *lw = lows + (size_t)s * nlow;
-        const uint32_t n = lw[(g * 3 + (qd >> 1)) * 16 + t], c = lw[(g * 3 + 2) * 16 + t];
+      const uint32_t g = q / 4, qd = q % 4;
+      for (uint32_t L = 0; L < 64; ++L) {
+        const uint32_t n = lw[(g * 3 + (qd >> 1)) * 64 + L], c = lw[(g * 3 + 2) * 64 + L];
         for (uint32_t i = 0; i < 4; ++i) {
           const uint32_t low = ((n >> (8 * i + 4 * (qd & 1))) & 15u) | (((c >> (8 * i + 2 * qd)) & 3u) << 4);
-          const uint32_t hi = (j[t] >> (2 * i)) & 3u;
-          uint32_t tok, dim;
-          where(s == 1, t, q, i, &tok, &dim);
-          out[(size_t)tok * D + dim] = (uint8_t)((hi << 6) | low);
+          const uint32_t hi = (j[L] >> (2 * i)) & 3u;
+          out[where(s == 1, L, q, i)] = (uint8_t)((hi << 6) | low);
         }
       }
     }
     if (cur != nw) return -1;
-    for (int t = 0; t < 16; ++t)
-      if (x[t] != 65536u) return -1;
+    for (int L = 0; L < 64; ++L)
+      if (x[L] != 65536u) return -1;
   }
   return 0;
 }

@@ -19,25 +19,36 @@ def make_seqs(seq_tokens, kv_heads, D, seed, scale_spread=False):
     return data
 
 
+def decoded_pages(kv, s, h, T):
+    """(token_begin, K, V) dequantised pages of sequence s, head h, decoded by the oracle from the host pool."""
+    D = kv.head_dim
+    out = []
+    for g in range((T + 63) // 64):
+        off = int(kv.host_offsets[s, h, g]) * 16
+        ks, vs, ksc, vsc, tc = O.kv_decode_group(kv.host_pool[off:off + 65536], kv.host_tables, h, D)
+        for G in range(4):
+            p = 4 * g + G
+            n = min(16, T - 16 * p)
+            if n <= 0:
+                assert tc[G] == 0
+                continue
+            assert tc[G] == n, (s, h, g, G, tc[G], n)
+            out.append((16 * p, (ks[G, :n].astype(np.float32) - 128) * ksc[G],
+                        (vs[G, :n].astype(np.float32) - 128) * vsc[G]))
+    return out
+
+
 def oracle_batched(kv, data, queries, query_pos, softmax_scale, gqa):
-    """fp64 reference over the values the decoder must reproduce: every page blob is decoded by the oracle's own
+    """fp64 reference over the values the decoder must reproduce: every group blob is decoded by the oracle's own
     decoder (which also checks the stream), dequantised as (sym - 128) * scale."""
     S, H = kv.seq_count, kv.kv_heads
     D = kv.head_dim
     out = np.zeros((S, H * gqa, D), np.float32)
     for s in range(S):
         T = int(data[s][0].shape[1])
-        visible = min(T, int(query_pos[s]) + 1)
-        npg = (visible + 15) // 16
         pages = []
         for h in range(H):
-            for p in range(npg):
-                off = int(kv.host_offsets[s, h, p]) * 16
-                ks, vs, ksc, vsc, tc = O.kv_decode_page(kv.host_pool[off:off + 8192], kv.host_tables, h, D)
-                n = min(16, T - 16 * p)
-                assert tc == n
-                pages.append((h, 16 * p, (ks[:n].astype(np.float32) - 128) * ksc,
-                              (vs[:n].astype(np.float32) - 128) * vsc))
+            pages += [(h, t0, k, v) for t0, k, v in decoded_pages(kv, s, h, T)]
         o, empty = O.paged_attention_f64(queries[s], H * gqa, H, D, gqa, int(query_pos[s]), 0, softmax_scale, pages)
         out[s] = o
     return out

@@ -32,8 +32,8 @@ def _run(dev, codec, seq_tokens, kv_heads, gqa, D, seed, query_pos=None, splits=
             parts += [kv.build_table(K), kv.build_table(V)]
         tables = np.concatenate(parts)
     if shared:
-        for s, (donor, pages) in shared.items():  # the shared prefix really is the donor's data
-            n = pages * 16
+        for s, (donor, groups) in shared.items():  # the shared prefix really is the donor's data
+            n = groups * 64
             data[s][0][:, :n] = data[donor][0][:, :n]
             data[s][1][:, :n] = data[donor][1][:, :n]
     S = len(seq_tokens)
@@ -75,8 +75,8 @@ def test_batched_gqa(dev, gqa):
 
 
 def test_batched_shared_prefix(dev):
-    # sequences 1..3 reuse sequence 0's first 8 pages (refcounted prefix blobs)
-    _run(dev, 2, [256, 200, 300, 129], 2, 4, 128, seed=21, shared={1: (0, 8), 2: (0, 8), 3: (0, 8)})
+    # sequences 1..3 reuse sequence 0's first 2 page groups = 128 tokens (refcounted prefix blobs)
+    _run(dev, 2, [256, 200, 300, 129], 2, 4, 128, seed=21, shared={1: (0, 2), 2: (0, 2), 3: (0, 2)})
 
 
 def test_batched_value_spread(dev):
