@@ -30,6 +30,11 @@ namespace {
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
+// Occupancy floor for the compiler (3 wavefronts per SIMD: <= 168 VGPRs); the LDS footprint below allows 3
+// four-wavefront workgroups per CU.
+#ifndef CF_KV_WPE
+#define CF_KV_WPE 3
+#endif
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kGqa = 4;            // MFMA rows: query heads of one KV head (gqa < 4 pads with zero queries)
@@ -60,67 +65,162 @@ __device__ __forceinline__ uint32_t quad_bytes(uint32_t n0, uint32_t n1, uint32_
   return (spread & 0xC0C0C0C0u) | (r & 0x3F3F3F3Fu);
 }
 
-// One interleaved-rANS step of the 64-lane stream: x = lane state, cur = wave-uniform word cursor, words = the
-// stream staged in LDS, last = highest valid word index (reads of lanes that do not renormalise are clamped).
-// Returns the slot entry (f | c << 11 | j << 22).
-__device__ __forceinline__ uint32_t rans_step(const uint32_t *__restrict__ tab, uint32_t &x, uint32_t &cur,
-                                              const uint16_t *__restrict__ words, uint32_t last) {
-  const uint32_t e = tab[x & (kSlots - 1)];
-  x = __umul24(e & (kSlots - 1), x >> CF_KV_RANS_PROB_BITS) + ((e >> 11) & (kSlots - 1));
+// One interleaved-rANS step of the 64-lane stream. x = lane state; wbase = wave-uniform address of the current
+// word (cursor) in the stream staged in LDS (or global memory for oversized groups). The slot entry e is
+// {f | c << 16, spread high parts}. Returns the spread high parts of the decoded joint symbol.
+template <typename WordPtr>
+__device__ __forceinline__ uint32_t rans_step(const uint2 *__restrict__ tab, uint32_t &x, WordPtr &wbase) {
+  const uint2 e = tab[x & (kSlots - 1)];
+  x = __umul24(e.x & 0xFFFFu, x >> CF_KV_RANS_PROB_BITS) + (e.x >> 16);
   const bool need = x < 65536u;
   const uint64_t m = __builtin_amdgcn_ballot_w64(need);
   const uint32_t idx = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
                                                  __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
-  const uint32_t w = words[min(cur + idx, last)];
-  x = need ? ((x << 16) | w) : x;
-  cur += static_cast<uint32_t>(__builtin_popcountll(m));
-  return e;
+  const uint32_t w = wbase[idx];  // lanes that do not renormalise read a harmless in-bounds word
+  x = __builtin_amdgcn_perm(x, w, need ? 0x05040100u : 0x07060504u);  // (x << 16) | w  or  x
+  wbase += __builtin_popcountll(m);
+  return e.y;
 }
 
-constexpr int kHdr = 64;  // group header bytes
+constexpr int kHdr = 64;                 // group header bytes
+constexpr uint32_t kCapWords = CF_KV_RANS_MAX_GROUP_WORDS;  // K+V words staged in LDS per wavefront
+constexpr uint32_t kSlackWords = 64;     // reads past the last word by non-renormalising lanes stay in the buffer
 
-// per-wave LDS buffer: the K and V word streams of one group (RANS) — also reused for the wave's final partial
 template <int D>
 constexpr int buf_u32() {
-  constexpr int words = 2 * ((D / 4) * 64 * CF_KV_RANS_PROB_BITS / 16 + 64);  // worst case K + V words
+  constexpr int words = (kCapWords + kSlackWords) / 2;
   constexpr int red = kGqa * (D + 2);
-  return (words + 1) / 2 > red ? (words + 1) / 2 : red;
+  return words > red ? words : red;
 }
 
 template <int D, int CODEC>
-__global__ __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_batched_desc d, uint32_t splits,
-                                                              float *__restrict__ partial) {
-  constexpr int NQ = D / 4;          // quads per lane per stream
-  constexpr int NG = D / 16;         // low-part groups per lane
-  constexpr int LOWS = 3 * NG * 64;  // u32 words of one stream's low parts
+struct GroupCtx {
+  static constexpr int NQ = D / 4, NG = D / 16, LOWS = 3 * NG * 64;
+};
+
+// Decode one page group (K scores, softmax, V accumulation) with the word streams read through `words`
+// (LDS staging buffer or the blob in HBM).
+template <int D, int CODEC, typename WordPtr>
+__device__ __forceinline__ void group_body(const uint8_t *__restrict__ blob, WordPtr wk, uint32_t kw,
+                                           const uint2 (*__restrict__ s_tab)[kSlots], const half4_t *qhi,
+                                           const half4_t *qlo, const float *qsum, _Float16 (*s_pw)[kGqa][16],
+                                           int lane, bool tok_ok, float ks, float vs, float *m_run, float *l_run,
+                                           float *corr, float4_t *acc_v) {
+  constexpr int NQ = D / 4, LOWS = 3 * (D / 16) * 64;
+  constexpr bool RANS = CODEC == CF_KV_CODEC_RANS_HYBRID;
+  const int G = lane >> 4, t = lane & 15;
+  float4_t sa = {0, 0, 0, 0}, sb = {0, 0, 0, 0};
+  uint32_t vb[NQ];
+  {
+    const uint32_t *st = reinterpret_cast<const uint32_t *>(blob + kHdr);
+    const uint32_t *lowk = reinterpret_cast<const uint32_t *>(blob + kHdr + 512);
+    const uint32_t *raw = reinterpret_cast<const uint32_t *>(blob + kHdr);
+    uint32_t xk = RANS ? st[lane] : 0u, xv = RANS ? st[64 + lane] : 0u;
+    WordPtr wv = wk + kw;
+    uint32_t kl[3] = {0, 0, 0}, vl[3] = {0, 0, 0};
+    [&]<int... Q>(std::integer_sequence<int, Q...>) {
+      (
+          [&] {
+            constexpr int q = Q, g = q / 4, qd = q % 4;
+            uint32_t kbytes, vbytes;
+            if constexpr (RANS) {
+              if constexpr (qd == 0) {
+#pragma unroll
+                for (int w = 0; w < 3; ++w) {
+                  kl[w] = lowk[(g * 3 + w) * 64 + lane];
+                  vl[w] = lowk[LOWS + (g * 3 + w) * 64 + lane];
+                }
+              }
+              const uint32_t hk = rans_step(s_tab[0], xk, wk);
+              const uint32_t hv = rans_step(s_tab[1], xv, wv);
+              kbytes = quad_bytes<qd>(kl[0], kl[1], kl[2], hk);
+              vbytes = quad_bytes<qd>(vl[0], vl[1], vl[2], hv);
+            } else {
+              kbytes = raw[q * 64 + lane];
+              vbytes = raw[NQ * 64 + q * 64 + lane];
+            }
+            vb[q] = vbytes;
+            const half4_t bk = bytes_to_half4(kbytes);
+            sa = __builtin_amdgcn_mfma_f32_4x4x4f16(qhi[q / 16], bk, sa, 4, q % 16, 0);
+            sb = __builtin_amdgcn_mfma_f32_4x4x4f16(qlo[q / 16], bk, sb, 4, q % 16, 0);
+          }(),
+          ...);
+    }(std::make_integer_sequence<int, NQ>{});
+  }
+
+  // ---- online softmax over the wavefront's 64 tokens (one running max per head for all four pages)
+  float s[kGqa], mx[kGqa];
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) {
+    s[h] = tok_ok ? (sa[h] + sb[h] - kOffset * qsum[h]) * ks : -INFINITY;
+    mx[h] = s[h];
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) mx[h] = fmaxf(mx[h], __shfl_xor(mx[h], o));
+  float alpha[kGqa];
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) {
+    const float mn = fmaxf(m_run[h], mx[h]);
+    alpha[h] = (m_run[h] == -INFINITY) ? 0.0f : __expf(m_run[h] - mn);
+    const float pr = tok_ok ? __expf(s[h] - mn) : 0.0f;
+    l_run[h] = l_run[h] * alpha[h] + pr;
+    const _Float16 pv = static_cast<_Float16>(pr * vs);
+    s_pw[G][h][t] = pv;
+    corr[h] = corr[h] * alpha[h] + kOffset * static_cast<float>(pv);
+    m_run[h] = mn;
+  }
+#pragma unroll
+  for (int i = 0; i < D / 16; ++i)
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) acc_v[i][h] *= alpha[h];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // ---- V MFMAs: out[h][t + 16i] += sum over the quad's 4 tokens of p * v
+#pragma unroll
+  for (int tq = 0; tq < 4; ++tq) {
+    const half4_t pa = *reinterpret_cast<const half4_t *>(&s_pw[G][lane & 3][4 * tq]);
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) acc_v[i] = mfma4(pa, bytes_to_half4(vb[tq * (D / 16) + i]), acc_v[i]);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+#if CF_KV_WPE > 0
+#define CF_KV_OCC __attribute__((amdgpu_waves_per_eu(CF_KV_WPE, 8)))
+#else
+#define CF_KV_OCC
+#endif
+
+template <int D, int CODEC>
+__global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_batched_desc d, uint32_t splits,
+                                                                         float *__restrict__ partial) {
+  constexpr int NQ = D / 4;
+  constexpr int LOWS = 3 * (D / 16) * 64;  // u32 words of one stream's low parts
   constexpr bool RANS = CODEC == CF_KV_CODEC_RANS_HYBRID;
   constexpr int BUF = buf_u32<D>();
-  constexpr uint32_t LAST = 2 * BUF - 1;
-  __shared__ uint32_t s_tab[2][RANS ? kSlots : 1];   // slot entries: f | c << 11 | j << 22
-  __shared__ uint32_t s_spread[RANS ? 256 : 1];      // joint symbol -> high parts at bits 6-7 of each byte
-  __shared__ _Float16 s_q[2][kGqa][D];               // query heads, f16 hi and lo parts (softmax scale folded in)
-  __shared__ _Float16 s_p[kWaves][4][kGqa][16];      // per wave: [page][head][token] probability * v_scale
-  __shared__ uint32_t s_buf[kWaves][BUF];
+  __shared__ uint2 s_tab[RANS ? 2 : 1][kSlots];     // {f | c << 16, spread high parts} per slot, K and V tables
+  __shared__ _Float16 s_p[kWaves][4][kGqa][16];     // per wave: [page][head][token] probability * v_scale
+  __shared__ uint32_t s_buf[kWaves][BUF];           // per wave: staged words; query staging and partials alias it
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int G = lane >> 4, t = lane & 15;
   const uint32_t split = blockIdx.x, head = blockIdx.y, seq = blockIdx.z;
   const uint32_t gqa = d.query_head_count / d.kv_head_count;
+  static_assert(2 * kGqa * D * 2 <= kWaves * BUF * 4, "query staging must fit the word buffers");
+  _Float16(*s_q)[kGqa][D] = reinterpret_cast<_Float16(*)[kGqa][D]>(&s_buf[0][0]);
 
   // ---- stage tables and queries
   if constexpr (RANS) {
     const uint2 *tk = reinterpret_cast<const uint2 *>(d.tables + static_cast<size_t>(2 * head) * CF_KV_RANS_TABLE_BYTES);
-    const uint2 *tv = tk + kSlots;
-    for (uint32_t i = threadIdx.x; i < kSlots; i += kThreads) {
-      s_tab[0][i] = tk[i].x;
-      s_tab[1][i] = tv[i].x;
-    }
-    if (threadIdx.x < 256) {
-      const uint32_t j = threadIdx.x;
-      uint32_t v = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v |= ((j >> (2 * i)) & 3u) << (8 * i + 6);
-      s_spread[j] = v;
+    for (uint32_t i = threadIdx.x; i < 2 * kSlots; i += kThreads) {
+      const uint2 e = tk[i];  // K table then V table (adjacent blobs)
+      s_tab[i / kSlots][i % kSlots] = uint2{(e.x & 2047u) | (((e.x >> 11) & 2047u) << 16), e.y};
     }
   }
   for (int i = threadIdx.x; i < kGqa * D; i += kThreads) {
@@ -159,6 +259,7 @@ __global__ __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_batched_desc
 #pragma unroll
     for (int hh = 0; hh < kGqa; ++hh) qsum[hh] = __shfl(part, 16 * hh);
   }
+  __syncthreads();  // s_q (aliasing the word buffers) is dead from here on
 
   const uint32_t ntok_seq = d.seq_tokens[seq];
   const uint32_t qpos = d.query_pos[seq];
@@ -180,8 +281,6 @@ __global__ __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_batched_desc
   for (int i = 0; i < D / 16; ++i) acc_v[i] = float4_t{0, 0, 0, 0};
 
   uint32_t *buf = s_buf[wave];
-  const uint16_t *wk = reinterpret_cast<const uint16_t *>(buf);
-
   for (uint32_t gi = ga + wave; gi < gb; gi += kWaves) {
     const uint8_t *blob = d.pool + static_cast<size_t>(grow[gi]) * 16;
     const uint32_t cnt = *reinterpret_cast<const uint32_t *>(blob + 4);
@@ -189,100 +288,22 @@ __global__ __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_batched_desc
     const uint32_t tcG = reinterpret_cast<const uint16_t *>(blob + 8)[G];
     const float ks = reinterpret_cast<const float *>(blob + 32)[G];
     const float vs = reinterpret_cast<const float *>(blob + 48)[G];
-    const uint32_t tok = 64 * gi + 16 * G + t;
-
-    if constexpr (RANS) {  // word streams -> LDS (coalesced u32 copy)
+    const bool tok_ok = static_cast<uint32_t>(t) < tcG && 64 * gi + 16 * G + t < visible;
+    const uint32_t gcodec = *reinterpret_cast<const uint32_t *>(blob);  // wave-uniform
+    if (RANS && gcodec == CF_KV_CODEC_RANS_HYBRID) {
+      // stage both word streams in LDS (coalesced u32 copy); the encoder guarantees kw + vw <= kCapWords
       const uint32_t *src = reinterpret_cast<const uint32_t *>(blob + kHdr + 512 + 2 * LOWS * 4);
-      const uint32_t n32 = (kw + vw + 1) / 2;
+      const uint32_t n32 = (min(kw + vw, kCapWords) + 1) / 2;
       for (uint32_t i = lane; i < n32; i += 64) buf[i] = src[i];
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      group_body<D, CF_KV_CODEC_RANS_HYBRID>(blob, reinterpret_cast<const uint16_t *>(buf), kw, s_tab, qhi, qlo,
+                                             qsum, s_p[wave], lane, tok_ok, ks, vs, m_run, l_run, corr, acc_v);
+    } else {  // raw int8 group (the INT8 codec, or the raw fallback of a high-entropy group)
+      group_body<D, CF_KV_CODEC_INT8>(blob, static_cast<const uint16_t *>(nullptr), 0, s_tab, qhi, qlo, qsum,
+                                      s_p[wave], lane, tok_ok, ks, vs, m_run, l_run, corr, acc_v);
     }
-
-    // ---- K and V streams decoded together (two independent rANS chains per lane). K quads feed the score MFMAs
-    // immediately; V quads stay packed (4 symbol bytes per register) until the probabilities exist.
-    float4_t sa = {0, 0, 0, 0}, sb = {0, 0, 0, 0};
-    uint32_t vb[NQ];
-    {
-      const uint32_t *st = reinterpret_cast<const uint32_t *>(blob + kHdr);
-      const uint32_t *lowk = reinterpret_cast<const uint32_t *>(blob + kHdr + 512);
-      const uint32_t *raw = reinterpret_cast<const uint32_t *>(blob + kHdr);
-      uint32_t xk = RANS ? st[lane] : 0u, xv = RANS ? st[64 + lane] : 0u;
-      uint32_t ck = 0, cv = kw;
-      uint32_t kl[3] = {0, 0, 0}, vl[3] = {0, 0, 0};
-      [&]<int... Q>(std::integer_sequence<int, Q...>) {
-        (
-            [&] {
-              constexpr int q = Q, g = q / 4, qd = q % 4;
-              uint32_t kbytes, vbytes;
-              if constexpr (RANS) {
-                if constexpr (qd == 0) {
-#pragma unroll
-                  for (int w = 0; w < 3; ++w) {
-                    kl[w] = lowk[(g * 3 + w) * 64 + lane];
-                    vl[w] = lowk[LOWS + (g * 3 + w) * 64 + lane];
-                  }
-                }
-                const uint32_t ek = rans_step(s_tab[0], xk, ck, wk, LAST);
-                const uint32_t ev = rans_step(s_tab[1], xv, cv, wk, LAST);
-                kbytes = quad_bytes<qd>(kl[0], kl[1], kl[2], s_spread[ek >> 22]);
-                vbytes = quad_bytes<qd>(vl[0], vl[1], vl[2], s_spread[ev >> 22]);
-              } else {
-                kbytes = raw[q * 64 + lane];
-                vbytes = raw[NQ * 64 + q * 64 + lane];
-              }
-              vb[q] = vbytes;
-              const half4_t bk = bytes_to_half4(kbytes);
-              sa = __builtin_amdgcn_mfma_f32_4x4x4f16(qhi[q / 16], bk, sa, 4, q % 16, 0);
-              sb = __builtin_amdgcn_mfma_f32_4x4x4f16(qlo[q / 16], bk, sb, 4, q % 16, 0);
-            }(),
-            ...);
-      }(std::make_integer_sequence<int, NQ>{});
-    }
-
-    // ---- online softmax over the wavefront's 64 tokens
-    const bool tok_ok = static_cast<uint32_t>(t) < tcG && tok < visible;
-    float s[kGqa], mx[kGqa];
-#pragma unroll
-    for (int h = 0; h < kGqa; ++h) {
-      s[h] = tok_ok ? (sa[h] + sb[h] - kOffset * qsum[h]) * ks : -INFINITY;
-      mx[h] = s[h];
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1)
-#pragma unroll
-      for (int h = 0; h < kGqa; ++h) mx[h] = fmaxf(mx[h], __shfl_xor(mx[h], o));
-    float alpha[kGqa];
-#pragma unroll
-    for (int h = 0; h < kGqa; ++h) {
-      const float mn = fmaxf(m_run[h], mx[h]);
-      alpha[h] = (m_run[h] == -INFINITY) ? 0.0f : __expf(m_run[h] - mn);
-      const float pr = tok_ok ? __expf(s[h] - mn) : 0.0f;
-      l_run[h] = l_run[h] * alpha[h] + pr;
-      const _Float16 pv = static_cast<_Float16>(pr * vs);
-      s_p[wave][G][h][t] = pv;
-      corr[h] = corr[h] * alpha[h] + kOffset * static_cast<float>(pv);
-      m_run[h] = mn;
-    }
-#pragma unroll
-    for (int i = 0; i < D / 16; ++i)
-#pragma unroll
-      for (int h = 0; h < kGqa; ++h) acc_v[i][h] *= alpha[h];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    // ---- V MFMAs: out[h][t + 16i] += sum over the quad's 4 tokens of p * v
-#pragma unroll
-    for (int tq = 0; tq < 4; ++tq) {
-      const half4_t pa = *reinterpret_cast<const half4_t *>(&s_p[wave][G][lane & 3][4 * tq]);
-#pragma unroll
-      for (int i = 0; i < D / 16; ++i) acc_v[i] = mfma4(pa, bytes_to_half4(vb[tq * (D / 16) + i]), acc_v[i]);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 
   // ---- reduce the wavefront: sum the 4 page groups (lanes t, t+16, t+32, t+48), l and corr over all lanes

@@ -261,7 +261,9 @@ extern "C" cf_status cf_kv_encode_group(uint32_t codec, const float *keys, const
     }
     rans_encode(s ? tv : tk, joint, nq, states[s], &words[s]);
   }
-  if (words[0].size() > 0xFFFF || words[1].size() > 0xFFFF) return CF_ERR_UNSUPPORTED;
+  if (words[0].size() + words[1].size() > CF_KV_RANS_MAX_GROUP_WORDS)  // raw fallback (see kv_codec_ext.h)
+    return cf_kv_encode_group(CF_KV_CODEC_INT8, keys, values, page_count, token_counts, head_dim, nullptr, nullptr,
+                              k_table_index, v_table_index, blob, capacity, blob_bytes);
   h.k_word_count = static_cast<uint16_t>(words[0].size());
   h.v_word_count = static_cast<uint16_t>(words[1].size());
   uint64_t at = 0;

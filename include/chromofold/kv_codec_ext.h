@@ -52,6 +52,10 @@
  *   lo = f | c << 11 | j << 22     (every symbol has f >= 1, so f <= 1793 fits 11 bits)
  *   hi = spread(j) = sum_i ((j >> 2i) & 3) << (8i + 6)
  * The batched launch uses table 2h for the K streams and 2h+1 for the V streams of KV head h.
+ *
+ * Raw fallback: a group whose K + V rANS words would exceed CF_KV_RANS_MAX_GROUP_WORDS (data the tables do not
+ * fit, e.g. near-uniform high parts) is stored as an INT8 group instead (its header says so); a RANS_HYBRID pool
+ * may therefore hold both kinds and the decoder dispatches per group.
  * ------------------------------------------------------------------------------------------------------------ */
 #ifndef CHROMOFOLD_KV_CODEC_EXT_H
 #define CHROMOFOLD_KV_CODEC_EXT_H
@@ -73,6 +77,7 @@ extern "C" {
 #define CF_KV_RANS_PROB_BITS 11u
 #define CF_KV_RANS_LANES 64u
 #define CF_KV_RANS_TABLE_BYTES 16384u
+#define CF_KV_RANS_MAX_GROUP_WORDS 2048u
 
 typedef struct cf_kv_group_header {
     uint32_t codec;            /* CF_KV_CODEC_* */
