@@ -1,0 +1,140 @@
+// fm_search.hip — FM-index backward search (count / SA ranges) and locate over the RRR-compressed BWT, gfx950.
+//
+// Replaces reference src/cuda/fm_search.cu:10-89 and include/chromofold/detail/fm_search_device.cuh:31-62 behind
+// the unchanged cf_fm_* C ABI. One lane per pattern (count/ranges) or per occurrence (locate), like the
+// reference, with two algebraic savings that keep the results bit-identical:
+//   * backward search computes rank(c, lo) and rank(c, hi) in one walk sharing the start-of-c chain
+//     (3 rank1 per wavelet level instead of 4);
+//   * the LF step of locate takes c = BWT[p] and rank(c, p) from one walk (2 rank1 per level instead of 3).
+// Out-of-alphabet pattern symbols empty the range; locate returns (SA[sample] + steps) mod n in 64-bit.
+#include "chromofold/chromofold_search.h"
+#include "cf_device.hpp"
+#include "packed_core.hpp"
+#include "rrr_core.hpp"
+
+namespace {
+
+constexpr unsigned kThreads = 256;
+
+// reference fm_search_device.cuh:31-48
+template <int LEVELS>
+__device__ __forceinline__ void backward(const cf_fm_view &v, const int32_t *__restrict__ pat, int st, int len,
+                                         int &lo, int &hi) {
+  lo = 0;
+  hi = v.n;
+  for (int k = len - 1; k >= 0; --k) {
+    const int c = pat[st + k];
+    if (c < 0 || c >= v.sigma) {
+      lo = hi = 0;
+      continue;
+    }
+    if (lo < hi) {
+      int rl, rh;
+      cfr::rank_pair<LEVELS>(v.w, c, lo, hi, rl, rh);
+      lo = v.C[c] + rl;
+      hi = v.C[c] + rh;
+    }
+  }
+}
+
+template <int LEVELS>
+__global__ __launch_bounds__(kThreads) void fm_count_kernel(cf_fm_view v, const int32_t *__restrict__ pat,
+                                                            const int32_t *__restrict__ pstart,
+                                                            const int32_t *__restrict__ plen,
+                                                            uint32_t *__restrict__ out, size_t npat) {
+  const size_t t = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+  if (t >= npat) return;
+  int lo, hi;
+  backward<LEVELS>(v, pat, pstart[t], plen[t], lo, hi);
+  out[t] = static_cast<uint32_t>(hi - lo);
+}
+
+template <int LEVELS>
+__global__ __launch_bounds__(kThreads) void fm_ranges_kernel(cf_fm_view v, const int32_t *__restrict__ pat,
+                                                             const int32_t *__restrict__ pstart,
+                                                             const int32_t *__restrict__ plen,
+                                                             int32_t *__restrict__ lo_out,
+                                                             int32_t *__restrict__ hi_out, size_t npat) {
+  const size_t t = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+  if (t >= npat) return;
+  int lo, hi;
+  backward<LEVELS>(v, pat, pstart[t], plen[t], lo, hi);
+  lo_out[t] = lo;
+  hi_out[t] = hi;
+}
+
+// reference fm_search_device.cuh:52-62
+template <int LEVELS>
+__device__ __forceinline__ int32_t locate_one(const cf_fm_view &v, int p) {
+  int steps = 0;
+  while (!((v.mwords[p >> 5] >> (p & 31)) & 1u)) {
+    int c;
+    const int r = cfr::access_rank<LEVELS>(v.w, p, c);
+    p = v.C[c] + r;
+    ++steps;
+  }
+  const int idx = cfp::rank1(v.mwords, v.msb, p);
+  return static_cast<int32_t>((static_cast<int64_t>(v.sval[idx]) + steps) % v.n);
+}
+
+template <int LEVELS>
+__global__ __launch_bounds__(kThreads) void fm_locate_kernel(cf_fm_view v, const int32_t *__restrict__ rows,
+                                                             int32_t *__restrict__ out, size_t nocc) {
+  const size_t t = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
+  if (t >= nocc) return;
+  out[t] = locate_one<LEVELS>(v, rows[t]);
+}
+
+#define CF_FM_DISPATCH(LAUNCH) \
+  switch (v.w.bits) {         \
+    case 7: LAUNCH(7); break;  \
+    case 15: LAUNCH(15); break; \
+    case 16: LAUNCH(16); break; \
+    default: LAUNCH(0); break; \
+  }
+
+}  // namespace
+
+extern "C" cf_status cf_fm_count_async(cf_fm_view v, const int32_t *pat, const int32_t *pstart, const int32_t *plen,
+                                       uint32_t *out, size_t npat, void *stream) {
+  // reference src/cuda/fm_search.cu:53: null classes / pattern arrays / output rejected before any device call
+  if (!v.w.classes || !pat || !pstart || !plen || !out) return CF_ERR_INVALID_ARGUMENT;
+  if (npat == 0) return CF_OK;
+  if (v.w.bits <= 0 || v.w.bits > 31 || v.n <= 0) return CF_ERR_INVALID_ARGUMENT;
+  const hipStream_t s = cfd::as_stream(stream);
+  const unsigned blocks = cfd::grid_for(npat, kThreads);
+#define CF_LAUNCH(L) fm_count_kernel<L><<<blocks, kThreads, 0, s>>>(v, pat, pstart, plen, out, npat)
+  CF_FM_DISPATCH(CF_LAUNCH)
+#undef CF_LAUNCH
+  return cfd::launch_status();
+}
+
+extern "C" cf_status cf_fm_ranges_async(cf_fm_view v, const int32_t *pat, const int32_t *pstart,
+                                        const int32_t *plen, int32_t *lo_out, int32_t *hi_out, size_t npat,
+                                        void *stream) {
+  // reference src/cuda/fm_search.cu:67
+  if (!v.w.classes || !pat || !pstart || !plen || !lo_out || !hi_out) return CF_ERR_INVALID_ARGUMENT;
+  if (npat == 0) return CF_OK;
+  if (v.w.bits <= 0 || v.w.bits > 31 || v.n <= 0) return CF_ERR_INVALID_ARGUMENT;
+  const hipStream_t s = cfd::as_stream(stream);
+  const unsigned blocks = cfd::grid_for(npat, kThreads);
+#define CF_LAUNCH(L) fm_ranges_kernel<L><<<blocks, kThreads, 0, s>>>(v, pat, pstart, plen, lo_out, hi_out, npat)
+  CF_FM_DISPATCH(CF_LAUNCH)
+#undef CF_LAUNCH
+  return cfd::launch_status();
+}
+
+extern "C" cf_status cf_fm_locate_async(cf_fm_view v, const int32_t *r_in, int32_t *out, size_t nocc,
+                                        void *stream) {
+  // reference src/cuda/fm_search.cu:80
+  if (!v.w.classes || !r_in || !out) return CF_ERR_INVALID_ARGUMENT;
+  if (nocc == 0) return CF_OK;
+  if (v.w.bits <= 0 || v.w.bits > 31 || v.n <= 0 || !v.mwords || !v.msb || !v.sval || !v.C)
+    return CF_ERR_INVALID_ARGUMENT;
+  const hipStream_t s = cfd::as_stream(stream);
+  const unsigned blocks = cfd::grid_for(nocc, kThreads);
+#define CF_LAUNCH(L) fm_locate_kernel<L><<<blocks, kThreads, 0, s>>>(v, r_in, out, nocc)
+  CF_FM_DISPATCH(CF_LAUNCH)
+#undef CF_LAUNCH
+  return cfd::launch_status();
+}

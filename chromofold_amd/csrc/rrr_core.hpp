@@ -104,4 +104,52 @@ __device__ __forceinline__ uint32_t rank_one(const cf_rrrw_view &v, int c, int i
   return static_cast<uint32_t>(q - p);
 }
 
+// rank(c, lo) and rank(c, hi) together: both walks share the start-of-c chain p (its rank1 is computed once),
+// so a backward-search step costs 3 rank1 per level instead of 4. Identical results to two rank_one calls.
+template <int LEVELS>
+__device__ __forceinline__ void rank_pair(const cf_rrrw_view &v, int c, int lo, int hi, int &rlo, int &rhi) {
+  const int L = LEVELS > 0 ? LEVELS : v.bits;
+  int p = 0, a = lo, b = hi;
+  for (int lvl = 0; lvl < L; ++lvl) {
+    const int rp = rank1_lvl<false>(v, lvl, p, nullptr);
+    const int ra = rank1_lvl<false>(v, lvl, a, nullptr);
+    const int rb = rank1_lvl<false>(v, lvl, b, nullptr);
+    if ((c >> (L - 1 - lvl)) & 1) {
+      p = v.zeros[lvl] + rp;
+      a = v.zeros[lvl] + ra;
+      b = v.zeros[lvl] + rb;
+    } else {
+      p -= rp;
+      a -= ra;
+      b -= rb;
+    }
+  }
+  rlo = a - p;
+  rhi = b - p;
+}
+
+// One LF-mapping step: c = BWT[i] and rank(c, i) in a single walk. The access walk of i follows exactly the bits
+// of c, so it IS the rank walk of position i for symbol c; only the start-of-c chain p needs its own rank1.
+// Returns rank(c, i) (so LF(i) = C[c] + rank) and writes c. Two rank1 per level instead of three.
+template <int LEVELS>
+__device__ __forceinline__ int access_rank(const cf_rrrw_view &v, int i, int &c_out) {
+  const int L = LEVELS > 0 ? LEVELS : v.bits;
+  int p = 0, c = 0;
+  for (int lvl = 0; lvl < L; ++lvl) {
+    int bit = 0;
+    const int ri = rank1_lvl<true>(v, lvl, i, &bit);
+    const int rp = rank1_lvl<false>(v, lvl, p, nullptr);
+    c = (c << 1) | bit;
+    if (bit) {
+      i = v.zeros[lvl] + ri;
+      p = v.zeros[lvl] + rp;
+    } else {
+      i -= ri;
+      p -= rp;
+    }
+  }
+  c_out = c;
+  return i - p;
+}
+
 }  // namespace cfr

@@ -100,3 +100,63 @@ def to_u32(t: torch.Tensor) -> np.ndarray:
 
 def u32_dev(a, device="cuda") -> torch.Tensor:
     return _dev(np.asarray(a, dtype=np.uint32), device)
+
+
+A.declare("cf_suffix_array_workspace_bytes", A.U64, [A.I32, A.I32])
+A.declare("cf_suffix_array", A.I32, [A.P, A.I32, A.I32, A.P, A.P, A.U64, A.P])
+
+
+@dataclass
+class FmIndex:
+    """Device-resident FM-index (the cf_fm_view arrays): RRR wavelet of the BWT + C table + sampled SA."""
+    w: RrrWaveletIndex
+    sigma: int
+    n: int
+    sa_sample: int
+    tensors: dict
+
+    @classmethod
+    def from_host(cls, arrays, device="cuda") -> "FmIndex":
+        """`arrays` has the .cffm payload: an RRR wavelet (attribute `w` or the wavelet keys) plus C, mwords, msb,
+        sval, sigma, n, sa_sample."""
+        get = (lambda k: arrays[k]) if isinstance(arrays, dict) else (lambda k: getattr(arrays, k))
+        w = RrrWaveletIndex.from_host(arrays if isinstance(arrays, dict) else arrays.w, device)
+        t = {k: _dev(np.asarray(get(k)), device) for k in ["C", "mwords", "msb", "sval"]}
+        return cls(w, int(get("sigma")), int(get("n")), int(get("sa_sample")), t)
+
+    def view(self) -> A.cf_fm_view:
+        t = self.tensors
+        return A.cf_fm_view(self.w.view(), _ptr(t["C"]), _ptr(t["mwords"]), _ptr(t["msb"]), _ptr(t["sval"]),
+                            self.sigma, self.n, self.sa_sample)
+
+    def count(self, pat: torch.Tensor, pstart: torch.Tensor, plen: torch.Tensor, stream=None) -> torch.Tensor:
+        out = torch.empty(pstart.numel(), dtype=torch.int32, device=pstart.device)
+        A.check(A.lib().cf_fm_count_async(self.view(), _ptr(pat), _ptr(pstart), _ptr(plen), _ptr(out),
+                                          pstart.numel(), stream_ptr(stream)), "cf_fm_count_async")
+        return out
+
+    def ranges(self, pat, pstart, plen, stream=None):
+        lo = torch.empty(pstart.numel(), dtype=torch.int32, device=pstart.device)
+        hi = torch.empty_like(lo)
+        A.check(A.lib().cf_fm_ranges_async(self.view(), _ptr(pat), _ptr(pstart), _ptr(plen), _ptr(lo), _ptr(hi),
+                                           pstart.numel(), stream_ptr(stream)), "cf_fm_ranges_async")
+        return lo, hi
+
+    def locate(self, rows: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+        out = torch.empty_like(rows, dtype=torch.int32) if out is None else out
+        A.check(A.lib().cf_fm_locate_async(self.view(), _ptr(rows), _ptr(out), rows.numel(), stream_ptr(stream)),
+                "cf_fm_locate_async")
+        return out
+
+
+def gpu_suffix_array(s: torch.Tensor, stream=None) -> torch.Tensor:
+    """Suffix array of the int32 device text `s` (sentinel-terminated) via cf_suffix_array."""
+    n = s.numel()
+    mx = int(s.max().item())
+    wsb = int(A.lib().cf_suffix_array_workspace_bytes(n, mx))
+    if wsb == 0:
+        raise A.CfError(A.CF_ERR_UNSUPPORTED, "cf_suffix_array_workspace_bytes")
+    ws = torch.empty(wsb, dtype=torch.uint8, device=s.device)
+    sa = torch.empty(n, dtype=torch.int32, device=s.device)
+    A.check(A.lib().cf_suffix_array(_ptr(s), n, mx, _ptr(sa), _ptr(ws), wsb, stream_ptr(stream)), "cf_suffix_array")
+    return sa
