@@ -1,0 +1,99 @@
+"""Builders of reference-format KV pages for the legacy-seam tests: fixed-width pages exactly as the reference's
+encoder writes them (src/runtime/kv_gpu_fixture.cpp:20-95, via the oracle's restatement) and canonical
+length-limited Huffman pages (the reference decoder's LUT format, include/chromofold/detail/block_huffman_device.cuh;
+its encoder lived in the absent warp_compress prototype, so this test-side encoder is checked by round trip
+through the oracle's LUT decoder)."""
+from __future__ import annotations
+
+import heapq
+
+import numpy as np
+
+import oracle as O
+from chromofold_amd.legacy import HostPage
+
+
+def fixed_page(k, v, kv_head, token_begin, bits, block=64):
+    """Reference fixture page: K per-channel / V per-token scales, fixed-width MSB-first, degenerate LUT."""
+    ks, vs, ksc, vsc, kd, vd = O.kv_fixture_quantize(k, v, bits)
+    n = ks.size
+    boff = (np.arange(0, n, block, dtype=np.int64) * bits).astype(np.int32)
+    lut = np.array([s | (bits << 8) for s in range(1 << bits)], np.int32)
+    page = HostPage(kv_head, token_begin, k.shape[0], k.shape[1], O.pack_fixed(ks, bits), boff, lut, ksc,
+                    O.pack_fixed(vs, bits), boff.copy(), lut.copy(), vsc, block, bits, bits, 1 << (bits - 1), bits)
+    return page, kd, vd
+
+
+def huffman_lengths(freq, maxlen):
+    """Huffman code lengths, then length-limited: clamp to maxlen and lengthen the deepest shorter codes until the
+    Kraft sum is <= 1 (every symbol with nonzero frequency gets a code)."""
+    syms = [s for s in range(len(freq)) if freq[s] > 0]
+    if len(syms) == 1:
+        L = np.zeros(len(freq), np.int32)
+        L[syms[0]] = 1
+        return L
+    heap = [(int(freq[s]), i, [s]) for i, s in enumerate(syms)]
+    heapq.heapify(heap)
+    depth = np.zeros(len(freq), np.int32)
+    uid = len(heap)
+    while len(heap) > 1:
+        f1, _, a = heapq.heappop(heap)
+        f2, _, b = heapq.heappop(heap)
+        for s in a + b:
+            depth[s] += 1
+        heapq.heappush(heap, (f1 + f2, uid, a + b))
+        uid += 1
+    L = np.minimum(depth, maxlen)
+    L[[s for s in range(len(freq)) if freq[s] == 0]] = 0
+    while sum(2.0 ** -int(l) for l in L if l) > 1.0:
+        cand = [s for s in range(len(freq)) if 0 < L[s] < maxlen]
+        s = max(cand, key=lambda x: (L[x], -freq[x]))
+        L[s] += 1
+    return L
+
+
+def canonical_codes(L):
+    order = sorted([s for s in range(len(L)) if L[s] > 0], key=lambda s: (L[s], s))
+    codes, code, prev = {}, 0, 0
+    for s in order:
+        code <<= (L[s] - prev)
+        codes[s] = (code, int(L[s]))
+        prev = L[s]
+        code += 1
+    return codes
+
+
+def huffman_stream(sym, codes, maxlen, block):
+    """MSB-first bit stream + bit offsets of every block + LUT (lut[look] = sym | len << 8)."""
+    bits, boff = [], []
+    for i, s in enumerate(sym):
+        if i % block == 0:
+            boff.append(len(bits))
+        c, l = codes[int(s)]
+        bits.extend((c >> (l - 1 - j)) & 1 for j in range(l))
+    bits.extend([0] * (maxlen + 32))
+    bits.extend([0] * (-len(bits) % 32))
+    nw = (len(bits) + 31) // 32
+    arr = np.array(bits[:nw * 32], np.uint64).reshape(nw, 32)
+    words = (arr << np.arange(31, -1, -1, dtype=np.uint64)).sum(1).astype(np.uint32)
+    lut = np.zeros(1 << maxlen, np.int32)
+    for s, (c, l) in codes.items():
+        base = c << (maxlen - l)
+        lut[base:base + (1 << (maxlen - l))] = s | (l << 8)
+    return words, np.array(boff, np.int32), lut
+
+
+def huffman_page(k, v, kv_head, token_begin, bits=8, maxlen=12, block=64):
+    """Fixture quantisation, then canonical Huffman per stream (variable-length codes, fixed_code_length 0)."""
+    ks, vs, ksc, vsc, kd, vd = O.kv_fixture_quantize(k, v, bits)
+    out = []
+    for sym in (ks.ravel(), vs.ravel()):
+        freq = np.bincount(sym, minlength=1 << bits)
+        codes = canonical_codes(huffman_lengths(freq, maxlen))
+        w, b, lut = huffman_stream(sym, codes, maxlen, block)
+        assert np.array_equal(O.huffman_decode(w, lut, maxlen, 0, sym.size), sym)  # round trip
+        out.append((w, b, lut))
+    (kw, kb, kl), (vw, vb, vl) = out
+    page = HostPage(kv_head, token_begin, k.shape[0], k.shape[1], kw, kb, kl, ksc, vw, vb, vl, vsc, block, maxlen,
+                    maxlen, 1 << (bits - 1), 0)
+    return page, kd, vd

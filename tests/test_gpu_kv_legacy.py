@@ -1,0 +1,121 @@
+"""GPU parity of the reference seam cf_kv_paged_attention_async on reference-format pages.
+
+Mirrors the reference's GPU tests: tests/paged_kv_cuda_correctness.cu (single int4 page, smooth data, max abs
+error <= 2e-4 against a CPU attention over the encoder's dequantised values), tests/adapter_attention_test.cu
+(head_dim {32, 64, 96, 128} x {int4, int8}, 2 KV heads, 14 query heads, 70 tokens = sealed pages + dense active
+tail, seed 9001) and tests/kv_reference_test.cpp (page-order invariance, GQA + tail, empty visible set -> 0).
+Huffman-coded pages (variable-length codes, rows starting mid-block) exercise the LUT decoder the reference's
+warp kernel cannot take. Reference = fp64 oracle over the same dequantised values."""
+import numpy as np
+import pytest
+
+import oracle as O
+from legacy_helpers import fixed_page, huffman_page
+
+pytestmark = pytest.mark.gpu
+ABS_TOL = 2e-4
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def _run(dev, pages_deq, host_pages, q, kv_heads, gqa, qtok0, scale, window=0, tail=None):
+    import torch
+    from chromofold_amd.legacy import PagedKv
+    pk = PagedKv(host_pages, str(dev))
+    dq = torch.from_numpy(q).to(dev)
+    active = None
+    if tail is not None:
+        active = (tail[0], torch.from_numpy(tail[1]).to(dev), torch.from_numpy(tail[2]).to(dev))
+    got = pk.attention(dq, kv_heads, gqa, qtok0, scale, window, active).cpu().numpy()
+    ref = np.zeros_like(q)
+    for r in range(q.shape[0]):
+        ref[r], _ = O.paged_attention_f64(q[r], q.shape[1], kv_heads, q.shape[2], gqa, qtok0 + r, window, scale,
+                                          pages_deq, tail)
+    return got, ref
+
+
+def test_single_int4_page_smooth_data(dev):
+    """reference tests/paged_kv_cuda_correctness.cu: 128 tokens x 64 dims, one page, int4."""
+    T, D = 128, 64
+    t = np.arange(T, dtype=np.float32)[:, None]
+    d = np.arange(D, dtype=np.float32)[None, :]
+    k = (np.sin(0.03 * t + 0.11 * d) + 0.25 * np.cos(0.07 * d)).astype(np.float32)
+    v = (np.cos(0.05 * t - 0.13 * d) * 0.8).astype(np.float32)
+    page, kd, vd = fixed_page(k, v, 0, 0, 4)
+    q = np.random.default_rng(1).standard_normal((4, 1, D)).astype(np.float32)
+    got, ref = _run(dev, [(0, 0, kd, vd)], [page], q, 1, 1, T - 4, 1 / np.sqrt(D))
+    assert np.abs(got - ref).max() <= ABS_TOL
+
+
+@pytest.mark.parametrize("hd", [32, 64, 96, 128])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_adapter_matrix_pages_plus_tail(dev, hd, bits):
+    """reference tests/adapter_attention_test.cu:22-111: kvh 2, qh 14 (gqa 7), 70 tokens -> 2 sealed 32-token
+    pages per head + a 6-token dense fp32 tail, several query rows."""
+    rng = np.random.default_rng(9001)
+    kvh, gqa, N, P = 2, 7, 70, 32
+    K = rng.standard_normal((kvh, N, hd)).astype(np.float32)
+    V = rng.standard_normal((kvh, N, hd)).astype(np.float32)
+    pages, deq = [], []
+    for h in range(kvh):
+        for p0 in range(0, (N // P) * P, P):
+            page, kd, vd = fixed_page(K[h, p0:p0 + P], V[h, p0:p0 + P], h, p0, bits)
+            pages.append(page)
+            deq.append((h, p0, kd, vd))
+    t0 = (N // P) * P
+    tail = (t0, np.ascontiguousarray(K[:, t0:].transpose(1, 0, 2)), np.ascontiguousarray(V[:, t0:].transpose(1, 0, 2)))
+    q = rng.standard_normal((3, kvh * gqa, hd)).astype(np.float32)
+    got, ref = _run(dev, deq, pages, q, kvh, gqa, N - 3, 1 / np.sqrt(hd), tail=tail)
+    assert np.abs(got - ref).max() <= ABS_TOL, np.abs(got - ref).max()
+
+
+@pytest.mark.parametrize("hd,maxlen", [(96, 12), (128, 16), (64, 9)])
+def test_huffman_pages_mid_block_rows(dev, hd, maxlen):
+    """Variable-length (canonical Huffman) pages: rows of 96 dims start mid-way through 64-symbol blocks, so the
+    decoder must skip-decode from the block offsets; maxlen 16 exercises the LUT-in-HBM path."""
+    rng = np.random.default_rng(hd + maxlen)
+    kvh, gqa, T = 2, 4, 96
+    pages, deq = [], []
+    for h in range(kvh):
+        for p0 in (0, 40):
+            n = 40 if p0 == 0 else 56
+            k = (rng.standard_normal((n, hd)) ** 3).astype(np.float32)  # peaky -> short codes for small values
+            v = rng.standard_normal((n, hd)).astype(np.float32)
+            page, kd, vd = huffman_page(k, v, h, p0, 8, maxlen)
+            pages.append(page)
+            deq.append((h, p0, kd, vd))
+    q = rng.standard_normal((2, kvh * gqa, hd)).astype(np.float32)
+    got, ref = _run(dev, deq, pages, q, kvh, gqa, T - 2, 1 / np.sqrt(hd))
+    assert np.abs(got - ref).max() <= ABS_TOL
+
+
+def test_page_order_window_and_empty(dev):
+    """Shuffled page order gives the same result; a causal window; a query with no visible token -> zeros
+    (the GPU convention; the CPU reference throws, reference kv_reference.cpp:235)."""
+    import torch
+    from chromofold_amd.legacy import PagedKv
+    rng = np.random.default_rng(5)
+    hd, kvh, gqa = 64, 2, 2
+    pages, deq = [], []
+    for h in range(kvh):
+        for p0 in range(0, 128, 16):
+            k = rng.standard_normal((16, hd)).astype(np.float32)
+            v = rng.standard_normal((16, hd)).astype(np.float32)
+            page, kd, vd = fixed_page(k, v, h, 100 + p0, 8)
+            pages.append(page)
+            deq.append((h, 100 + p0, kd, vd))
+    order = rng.permutation(len(pages))
+    q = rng.standard_normal((2, kvh * gqa, hd)).astype(np.float32)
+    a, ref = _run(dev, deq, pages, q, kvh, gqa, 200, 0.125, window=37)
+    b, _ = _run(dev, [deq[i] for i in order], [pages[i] for i in order], q, kvh, gqa, 200, 0.125, window=37)
+    assert np.abs(a - ref).max() <= ABS_TOL and np.abs(b - ref).max() <= ABS_TOL
+    # query token before every page: nothing visible -> zeros
+    pk = PagedKv(pages, str(dev))
+    out = pk.attention(torch.from_numpy(q).to(dev), kvh, gqa, 10, 0.125).cpu().numpy()
+    assert (out == 0).all()
