@@ -416,3 +416,88 @@ def dense_attention_f64(q, k, v, scale):
     out = np.zeros(q.shape[-1], np.float32)
     lib().or_dense_attention_f64(_ptr(q), q.shape[-1], _ptr(k), _ptr(v), k.shape[0], scale, _ptr(out))
     return out
+
+
+# ------------------------------------------------------------------ the reference's own CPU code (oracle/_ref)
+# Built by `make -C oracle ref` from the reference sources where /root/reference is mounted; absent elsewhere.
+_ref = None
+
+
+def ref_lib() -> C.CDLL | None:
+    """oracle/_ref/libcfref.so (reference kv_gpu_fixture/kv_reference/kv_runtime behind ref_shim.cpp) or None."""
+    global _ref
+    path = os.path.join(REF_DIR, "libcfref.so")
+    if _ref is None and os.path.exists(path):
+        _ref = C.CDLL(path)
+        _ref.cfref_fixture_page.restype = C.c_int
+        _ref.cfref_fixture_page.argtypes = [C.c_int, P, P, U32, U32, U32, U32, U32] + [P] * 8 + [U32, P, U32, P]
+        _ref.cfref_seal_dequant.restype = C.c_int
+        _ref.cfref_seal_dequant.argtypes = [P, P, U32, U32, U32, U32, P, P]
+        _ref.cfref_paged_attention.restype = C.c_int
+        _ref.cfref_paged_attention.argtypes = [P, U32, U32, U32, U32, U32, C.c_float, U32, P, P, P, P, P, P, P, P,
+                                               U32, U32, P]
+    return _ref
+
+
+def ref_build_index() -> str | None:
+    """Path of oracle/_ref/build_index (reference tools/build_index.cpp compiled from its source) or None."""
+    path = os.path.join(REF_DIR, "build_index")
+    return path if os.path.exists(path) else None
+
+
+def ref_fixture_page(bits: int, k: np.ndarray, v: np.ndarray, kv_head: int = 0, block: int = 64):
+    """reference gpu_fixture::encode_int{4,8}_page -> dict of its words, scales, dequantised values, offsets."""
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    T, D = k.shape
+    cap = (T * D * 8 + 31) // 32 + 4
+    capb = T * D // block + 4
+    out = dict(kw=np.zeros(cap, np.uint32), vw=np.zeros(cap, np.uint32), ks=np.zeros(D, np.float32),
+               vs=np.zeros(T, np.float32), kdeq=np.zeros((T, D), np.float32), vdeq=np.zeros((T, D), np.float32),
+               kboff=np.zeros(capb, np.int32), vboff=np.zeros(capb, np.int32))
+    lut = np.zeros(256, np.int32)
+    cnt = np.zeros(6, np.uint32)
+    rc = ref_lib().cfref_fixture_page(bits, _ptr(k), _ptr(v), T, D, kv_head, block, cap,
+                                      *[_ptr(out[n]) for n in ["kw", "vw", "ks", "vs", "kdeq", "vdeq", "kboff",
+                                                               "vboff"]], capb, _ptr(lut), 256, _ptr(cnt))
+    if rc != 0:
+        raise ValueError("reference encoder rejected the page")
+    out["kw"], out["vw"] = out["kw"][:cnt[0]], out["vw"][:cnt[1]]
+    out["kboff"], out["vboff"] = out["kboff"][:cnt[2]], out["vboff"][:cnt[3]]
+    out["lut"], out["zero_point"] = lut[:cnt[4]], int(cnt[5])
+    return out
+
+
+def ref_seal_dequant(k: np.ndarray, v: np.ndarray, token_begin: int, kv_head: int):
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    T, D = k.shape
+    kd, vd = np.zeros((T, D), np.float32), np.zeros((T, D), np.float32)
+    if ref_lib().cfref_seal_dequant(_ptr(k), _ptr(v), token_begin, T, kv_head, D, _ptr(kd), _ptr(vd)) != 0:
+        raise ValueError("reference seal rejected the page")
+    return kd, vd
+
+
+def ref_paged_attention(q, q_heads, kv_heads, D, query_token, window, scale, pages, tail=None):
+    """reference::paged_attention over int4 pages sealed from raw (kv_head, token_begin, K, V) and an optional
+    (token_begin, K [n, kvh, D], V [n, kvh, D]) tail. Returns out [q_heads, D], or None if the reference threw."""
+    q = np.ascontiguousarray(q, np.float32)
+    n = len(pages)
+    kvh = np.array([p[0] for p in pages], np.uint32)
+    tok0 = np.array([p[1] for p in pages], np.uint32)
+    ntok = np.array([p[2].shape[0] for p in pages], np.uint32)
+    off = np.zeros(max(n, 1), np.uint64)
+    if n:
+        off[1:n] = np.cumsum(ntok[:-1])
+    K = np.ascontiguousarray(np.concatenate([p[2] for p in pages]) if n else np.zeros((1, D)), np.float32)
+    V = np.ascontiguousarray(np.concatenate([p[3] for p in pages]) if n else np.zeros((1, D)), np.float32)
+    t0, tk, tv, tn = 0, None, None, 0
+    if tail is not None:
+        t0, tk, tv = tail
+        tk, tv = np.ascontiguousarray(tk, np.float32), np.ascontiguousarray(tv, np.float32)
+        tn = tk.shape[0]
+    out = np.zeros((q_heads, D), np.float32)
+    rc = ref_lib().cfref_paged_attention(_ptr(q), q_heads, kv_heads, D, query_token, window, scale, n, _ptr(kvh),
+                                         _ptr(tok0), _ptr(ntok), _ptr(off), _ptr(K), _ptr(V), _ptr(tk), _ptr(tv),
+                                         t0, tn, _ptr(out))
+    return out if rc == 0 else None
