@@ -27,6 +27,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the dominant kernel, from rocprofv3 FETCH_SIZE + WRITE_SIZE runs calibrated on a copy of
+# known size (profiles/kv_batched_c4_32k.md): only quoted for the workload shape it was measured on.
+MEASURED_TRAFFIC = {("kv", 32768, 32): 2.139e9}
 METRIC = "compressed-KV attn decode tokens/s + HBM GB/s fraction; wavelet rank Mq/s"
 
 
@@ -46,6 +49,17 @@ def _events_time(fn, steps: int, warmup: int):
     wall_ms = (time.perf_counter() - t0) * 1e3
     per = [a.elapsed_time(b) for a, b in evs]
     return wall_ms, per
+
+
+def bench_copy(steps: int, warmup: int, nbytes: int = 1 << 30) -> dict:
+    """Device-to-device copy of `nbytes` (torch's copy kernel): the measured stream-copy peak the HBM fractions are
+    also quoted against, and the known-size kernel that FETCH_SIZE / WRITE_SIZE counters are calibrated on."""
+    import torch
+    src = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda:0")
+    dst = torch.empty_like(src)
+    _, per = _events_time(lambda: dst.copy_(src), steps, warmup)
+    t = float(np.median(per)) * 1e-3
+    return {"copy_bytes": nbytes, "copy_ms": t * 1e3, "stream_copy_gbs": 2.0 * nbytes / t / 1e9}
 
 
 # ------------------------------------------------------------------------------------------------ RRR wavelet (C1)
@@ -159,7 +173,8 @@ def bench_kv(steps: int, warmup: int, context: int = 32768, batch: int = 32, cod
         "bits_per_value": kvb.pool_bytes * 8.0 / values,
         "ratio_vs_bf16": (values * 2.0) / kvb.pool_bytes,
         "roofline": {"bound": "hbm", "achieved": step_bytes / t_step / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": step_bytes / t_step / 1e9 / HBM_PEAK_GBS, "traffic": None},
+                     "frac": step_bytes / t_step / 1e9 / HBM_PEAK_GBS,
+                     "traffic": MEASURED_TRAFFIC.get(("kv", context, batch))},
         "step_bytes": step_bytes,
     })
     if cpu_s is not None:
@@ -174,7 +189,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="auto", choices=["auto", "kv", "rrr"])
+    ap.add_argument("--workload", default="auto", choices=["auto", "kv", "rrr", "copy"])
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -184,6 +199,13 @@ def main() -> int:
 
     import torch
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.workload == "copy":
+        cp = bench_copy(args.steps, args.warmup)
+        print(json.dumps({"metric": "device-to-device copy GB/s", "value": cp["stream_copy_gbs"], "unit": "GB/s",
+                          "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": cp["copy_ms"],
+                          "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
+                          "data": "synthetic", "config": {"workload": f"torch copy_ of {cp['copy_bytes']} B"}}))
+        return 0
     if args.workload in ("auto", "kv"):
         kvr = bench_kv(args.steps, args.warmup, cpu=not args.no_cpu, check_seqs=0 if args.no_cpu else 2)
         rrr = bench_rrr(args.steps, args.warmup, cpu=not args.no_cpu)
@@ -192,6 +214,9 @@ def main() -> int:
         secondary["wavelet_access_mqs"] = rrr["access_mqs"]
         secondary["wavelet_rank_roofline_frac"] = rrr["rank_roofline"]["frac"]
         secondary["wavelet_cpu_baseline"] = rrr.get("cpu_baseline")
+        cp = bench_copy(10, 2)
+        secondary["stream_copy_gbs"] = cp["stream_copy_gbs"]
+        secondary["roofline_frac_of_stream_copy"] = kvr["roofline"]["achieved"] / cp["stream_copy_gbs"]
         line = {
             "metric": METRIC, "value": kvr["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": kvr["ms_per_step"], "higher_is_better": True, "scaling": "weak",

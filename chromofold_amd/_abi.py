@@ -76,6 +76,18 @@ _SIGS: dict[str, tuple] = {
     "cf_fm_count_async": (I32, [cf_fm_view, P, P, P, P, SZ, P]),
     "cf_fm_ranges_async": (I32, [cf_fm_view, P, P, P, P, P, SZ, P]),
     "cf_fm_locate_async": (I32, [cf_fm_view, P, P, SZ, P]),
+    # chromofold_extra.h (the reference's benchmark-level entry points)
+    "cf_rank2_async": (I32, [cf_wavelet_view, P, P, C.c_int, C.c_int, P, P, P, SZ, P]),
+    "cf_embedding_gather_tpq_async": (I32, [cf_wavelet_view, P, U32, P, P, SZ, P]),
+    "cf_rrr_rank_async": (I32, [P, P, P, P, P, P, P, P, SZ, P]),
+    "cf_delta_fetch_async": (I32, [P, C.c_int, P, P, P, P, P, P, P, SZ, P]),
+    "cf_sparse_gather_fused_async": (I32, [cf_rrrw_view, P, C.c_int, P, P, SZ, P]),
+    "cf_sparse_decode_all_async": (I32, [cf_rrrw_view, P, SZ, P]),
+    "cf_sparse_gather_async": (I32, [P, P, C.c_int, P, P, SZ, P]),
+    "cf_rans_decode_async": (I32, [P, P, P, P, P, P, C.c_int, C.c_int, P, P]),
+    "cf_fused_matmul_async": (I32, [P, P, P, C.c_int, C.c_int, P, P, C.c_int, C.c_int, C.c_int, F32, C.c_int, P]),
+    "cf_dense_matmul_async": (I32, [P, P, P, C.c_int, C.c_int, P, P, P, C.c_int, C.c_int, C.c_int, F32, C.c_int,
+                                    P]),
     # kv_cuda.h
     "cf_kv_validate_paged_attention_desc": (I32, [P]),
     "cf_kv_paged_attention_async": (I32, [P, P]),

@@ -153,3 +153,46 @@ __device__ __forceinline__ int access_rank(const cf_rrrw_view &v, int i, int &c_
 }
 
 }  // namespace cfr
+
+namespace cfr {
+
+// rank1 over [0, pos) of a single RRR bitvector with one-level samples: sbrank[sbi] set bits and sboff[sbi] offset
+// bit position at the start of superblock sbi (64 blocks). Semantics of reference src/cuda/rrr.cu:38-57; the class
+// scan and the unrank use the same SWAR word scan and table as the wavelet levels.
+__device__ __forceinline__ int rank1_plain(const uint32_t *__restrict__ cls, const uint32_t *__restrict__ offsets,
+                                           const int32_t *__restrict__ sbrank, const int32_t *__restrict__ sboff,
+                                           int pos) {
+  const int blk = pos / cfd::kRrrT;
+  const int b = pos - blk * cfd::kRrrT;
+  const int sbi = blk >> 6;
+  int r = sbrank[sbi];
+  const int obit = sboff[sbi];
+  const uint32_t *__restrict__ cw = cls + (static_cast<size_t>(sbi) << 3);
+  const int nblk = blk - (sbi << 6);
+  const int full = nblk >> 3, rem = nblk & 7;
+  int csum = 0, wsum = 0;
+  uint32_t target_word = 0;
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    if (w <= full && (w < full || rem || b)) {  // the target block's word is read only when it is needed
+      uint32_t x = cw[w];
+      if (w == full) {
+        target_word = x;
+        x &= rem ? ((1u << (4 * rem)) - 1u) : 0u;
+      }
+      csum += cfd::nibble_sum(x);
+      wsum += cfd::nibble_width_sum(x);
+    }
+  }
+  r += csum;
+  if (b > 0) {
+    const int k = static_cast<int>((target_word >> (4 * rem)) & 15u);
+    const int w = cfd::width_of(k);
+    const uint32_t off = w ? read_bits(offsets, static_cast<int64_t>(obit) + wsum, w) : 0u;
+    const uint32_t word = kTab.unrank[kTab.base[k] + off];
+    r += __popc(word & ((1u << b) - 1u));
+  }
+  return r;
+}
+
+}  // namespace cfr

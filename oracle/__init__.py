@@ -86,6 +86,7 @@ def _declare(L):
         "or_paged_attention_f64": (C.c_int, [P, U32, U32, U32, U32, U32, U32, C.c_float, U32, P, P, P, P, P, P,
                                              P, P, U32, U32, P]),
         "or_dense_attention_f64": (None, [P, U32, P, P, U32, C.c_float, P]),
+        "or_kv_window_attention_f64": (None, [P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, P]),
         "or_kv_decode_group": (C.c_int, [P, P, U32, P, P, P, P, P]),
         "or_kv_quantize_page_absmax": (None, [P, U32, P, P]),
         "or_softmax_merge": (None, [P, P, P, C.c_double, C.c_double, P, U32]),
@@ -416,6 +417,23 @@ def dense_attention_f64(q, k, v, scale):
     out = np.zeros(q.shape[-1], np.float32)
     lib().or_dense_attention_f64(_ptr(q), q.shape[-1], _ptr(k), _ptr(v), k.shape[0], scale, _ptr(out))
     return out
+
+
+def kv_window_attention_f64(K, V, Q, nq: int, window: int, sscale: float) -> np.ndarray:
+    """reference fused_kv_attention.cu:27-65 over dequantised K/V [seq, dim] (fp64 accumulation)."""
+    K, V, Q = (np.ascontiguousarray(a, np.float32) for a in (K, V, Q))
+    seq, dim = K.shape
+    out = np.zeros((nq, dim), np.float32)
+    lib().or_kv_window_attention_f64(_ptr(K), _ptr(V), _ptr(Q), seq, dim, nq, window, sscale, _ptr(out))
+    return out
+
+
+def qmatmul_f64(x: np.ndarray, sym: np.ndarray, scale, zero) -> np.ndarray:
+    """reference fused_matmul.cu:17-38: y[b, m] = sum_k x[b, k] * ((q[m, k] - zero) * scale), in float64. `scale` is
+    a scalar (per tensor) or an array broadcastable to q (e.g. per (row, 64-column block) scales repeated over the
+    block)."""
+    w = (sym.astype(np.float64) - zero) * np.asarray(scale, np.float64)
+    return (np.asarray(x, np.float64) @ w.T).astype(np.float64)
 
 
 # ------------------------------------------------------------------ the reference's own CPU code (oracle/_ref)

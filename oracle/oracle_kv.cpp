@@ -163,6 +163,18 @@ void or_dense_attention_f64(const float *q, uint32_t D, const float *k, const fl
   for (uint32_t d = 0; d < D; ++d) out[d] = (float)(w[d] / den);
 }
 
+// Causal-windowed attention of reference src/cuda/fused_kv_attention.cu:27-65 over dequantised rows K/V [seq, dim]:
+// query i attends rows [max(0, i - window + 1), i], i.e. the dense attention above over that slice.
+void or_kv_window_attention_f64(const float *K, const float *V, const float *Q, int seq, int dim, int nq, int window,
+                                float sscale, float *out) {
+  (void)seq;
+  for (int i = 0; i < nq; ++i) {
+    const int lo = std::max(0, i - window + 1);
+    or_dense_attention_f64(Q + (size_t)i * dim, (uint32_t)dim, K + (size_t)lo * dim, V + (size_t)lo * dim,
+                           (uint32_t)(i - lo + 1), sscale, out + (size_t)i * dim);
+  }
+}
+
 // ---------------------------------------------------------------------------------------- kv_codec_ext pages
 // Decode one INT8 / RANS_HYBRID page-group blob into symbols [4 pages][16 tokens][D] for K and V (token-major)
 // plus per-page scales and token counts. tables: table blobs (16 KiB each); K uses tables[2*head], V

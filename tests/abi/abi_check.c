@@ -1,0 +1,93 @@
+/* abi_check.c — compiled by tests/test_abi.py with plain `gcc -std=c99` against the public headers and linked
+ * with libchromofold.so: the public headers are valid C, every declaration links, and the NULL-argument contract
+ * holds (each call below is rejected on the host before any device call, so no GPU is needed). Prints one line per
+ * check; exit status 0 = all passed. */
+#include <stdio.h>
+#include <string.h>
+
+#include "chromofold/chromofold.h"
+#include "chromofold/chromofold_extra.h"
+#include "chromofold/chromofold_index.h"
+#include "chromofold/chromofold_qw.h"
+#include "chromofold/chromofold_search.h"
+#include "chromofold/kv_codec_ext.h"
+#include "chromofold/kv_cuda.h"
+#include "chromofold/kv_runtime.h"
+
+static int failures = 0;
+
+static void expect(const char *what, int got, int want) {
+  printf("%-40s %d %s\n", what, got, got == want ? "ok" : "FAIL");
+  if (got != want) ++failures;
+}
+
+int main(void) {
+  cf_wavelet_view wv;
+  cf_rrrw_view rv;
+  cf_fm_view fv;
+  memset(&wv, 0, sizeof wv);
+  memset(&rv, 0, sizeof rv);
+  memset(&fv, 0, sizeof fv);
+  const int INV = CF_ERR_INVALID_ARGUMENT;
+  printf("sizeof cf_wavelet_view %zu\n", sizeof(cf_wavelet_view));
+  printf("sizeof cf_rrrw_view %zu\n", sizeof(cf_rrrw_view));
+  printf("sizeof cf_fm_view %zu\n", sizeof(cf_fm_view));
+  printf("sizeof cf_kv_device_page %zu\n", sizeof(cf_kv_device_page));
+  printf("sizeof cf_kv_paged_attention_desc %zu\n", sizeof(cf_kv_paged_attention_desc));
+  printf("sizeof cf_kv_batched_desc %zu\n", sizeof(cf_kv_batched_desc));
+  printf("sizeof cf_qw_matrix %zu\n", sizeof(cf_qw_matrix));
+  /* chromofold.h */
+  expect("cf_access_async", cf_access_async(wv, NULL, NULL, 1, NULL), INV);
+  expect("cf_rank_async", cf_rank_async(wv, NULL, NULL, NULL, 1, NULL), INV);
+  expect("cf_embedding_gather_async", cf_embedding_gather_async(wv, NULL, 1, NULL, NULL, 1, NULL), INV);
+  expect("cf_kv_attn_fused_async", cf_kv_attn_fused_async(NULL, NULL, NULL, 0, NULL, NULL, NULL, 0, NULL, NULL,
+                                                          NULL, NULL, 0, 0, 0, 0, 0, 0, 0.0f, NULL), INV);
+  expect("cf_kv_attn_dense_async", cf_kv_attn_dense_async(NULL, NULL, NULL, 0, NULL, NULL, NULL, 0, NULL, NULL,
+                                                          NULL, NULL, NULL, NULL, 0, 0, 0, 0, 0, 0, 0.0f, NULL), INV);
+  /* chromofold_search.h */
+  expect("cf_rrrw_access_async", cf_rrrw_access_async(rv, NULL, NULL, 1, NULL), INV);
+  expect("cf_rrrw_rank_async", cf_rrrw_rank_async(rv, NULL, NULL, NULL, 1, NULL), INV);
+  expect("cf_fm_count_async", cf_fm_count_async(fv, NULL, NULL, NULL, NULL, 1, NULL), INV);
+  expect("cf_fm_ranges_async", cf_fm_ranges_async(fv, NULL, NULL, NULL, NULL, NULL, 1, NULL), INV);
+  expect("cf_fm_locate_async", cf_fm_locate_async(fv, NULL, NULL, 1, NULL), INV);
+  /* chromofold_extra.h */
+  expect("cf_rank2_async", cf_rank2_async(wv, NULL, NULL, 1, 8, NULL, NULL, NULL, 1, NULL), INV);
+  expect("cf_embedding_gather_tpq_async", cf_embedding_gather_tpq_async(wv, NULL, 1, NULL, NULL, 1, NULL), INV);
+  expect("cf_rrr_rank_async", cf_rrr_rank_async(NULL, NULL, NULL, NULL, NULL, NULL, NULL, NULL, 1, NULL), INV);
+  expect("cf_delta_fetch_async",
+         cf_delta_fetch_async(NULL, 0, NULL, NULL, NULL, NULL, NULL, NULL, NULL, 1, NULL), INV);
+  expect("cf_sparse_gather_fused_async", cf_sparse_gather_fused_async(rv, NULL, 1, NULL, NULL, 1, NULL), INV);
+  expect("cf_sparse_decode_all_async", cf_sparse_decode_all_async(rv, NULL, 1, NULL), INV);
+  expect("cf_sparse_gather_async", cf_sparse_gather_async(NULL, NULL, 1, NULL, NULL, 1, NULL), INV);
+  expect("cf_rans_decode_async", cf_rans_decode_async(NULL, NULL, NULL, NULL, NULL, NULL, 64, 1, NULL, NULL), INV);
+  expect("cf_fused_matmul_async",
+         cf_fused_matmul_async(NULL, NULL, NULL, 8, 64, NULL, NULL, 1, 1, 1, 1.0f, 8, NULL), INV);
+  expect("cf_dense_matmul_async",
+         cf_dense_matmul_async(NULL, NULL, NULL, 8, 64, NULL, NULL, NULL, 1, 1, 1, 1.0f, 8, NULL), INV);
+  /* chromofold_index.h */
+  expect("cf_suffix_array", cf_suffix_array(NULL, 4, 3, NULL, NULL, 0, NULL), INV);
+  expect("cf_suffix_array_workspace_bytes(0)", (int)cf_suffix_array_workspace_bytes(0, 1), 0);
+  /* chromofold_qw.h */
+  expect("cf_qw_validate", cf_qw_validate(NULL), INV);
+  expect("cf_qw_matmul_async", cf_qw_matmul_async(NULL, NULL, NULL, 1, NULL), INV);
+  expect("cf_qw_quantize_int4", cf_qw_quantize_int4(NULL, 1, 1, NULL, NULL), INV);
+  expect("cf_qw_huffman_plan", (int)cf_qw_huffman_plan(NULL, 1, 1, NULL), 0);
+  expect("cf_qw_huffman_encode", cf_qw_huffman_encode(NULL, 1, 1, NULL, NULL, 0, NULL), INV);
+  /* kv_cuda.h */
+  expect("cf_kv_validate_paged_attention_desc", cf_kv_validate_paged_attention_desc(NULL), INV);
+  expect("cf_kv_paged_attention_async", cf_kv_paged_attention_async(NULL, NULL), INV);
+  /* kv_codec_ext.h */
+  expect("cf_kv_validate_batched_desc", cf_kv_validate_batched_desc(NULL), INV);
+  expect("cf_kv_paged_attention_batched_async", cf_kv_paged_attention_batched_async(NULL, NULL), INV);
+  /* kv_runtime.h */
+  expect("cf_kv_validate_page", cf_kv_validate_page(NULL), INV);
+  expect("cf_kv_validate_layout", cf_kv_validate_layout(NULL), INV);
+  expect("cf_kv_page_resident_bytes", cf_kv_page_resident_bytes(NULL, NULL), INV);
+  expect("cf_kv_cache_memory_stats", cf_kv_cache_memory_stats(NULL, NULL), INV);
+  expect("cf_online_softmax_init", cf_online_softmax_init(NULL, NULL, 1), INV);
+  expect("cf_online_softmax_accumulate", cf_online_softmax_accumulate(NULL, 0.0, NULL), INV);
+  expect("cf_online_softmax_merge", cf_online_softmax_merge(NULL, NULL), INV);
+  expect("cf_online_softmax_finalize", cf_online_softmax_finalize(NULL, NULL), INV);
+  printf("%s (%d failure%s)\n", failures ? "FAIL" : "PASS", failures, failures == 1 ? "" : "s");
+  return failures ? 1 : 0;
+}

@@ -97,3 +97,62 @@ def huffman_page(k, v, kv_head, token_begin, bits=8, maxlen=12, block=64):
     page = HostPage(kv_head, token_begin, k.shape[0], k.shape[1], kw, kb, kl, ksc, vw, vb, vl, vsc, block, maxlen,
                     maxlen, 1 << (bits - 1), 0)
     return page, kd, vd
+
+
+def huffman_stream_np(sym, lengths, maxlen, block):
+    """Vectorised twin of huffman_stream for large inputs: canonical codes from `lengths` (per symbol value), MSB-first
+    packing, bit offset of every block, LUT. Codes of different symbols never share bits, so OR-packing is a sum."""
+    sym = np.asarray(sym).ravel().astype(np.int64)
+    codes = canonical_codes(lengths)
+    cv = np.zeros(len(lengths), np.uint64)
+    cl = np.zeros(len(lengths), np.int64)
+    for s, (c, l) in codes.items():
+        cv[s], cl[s] = c, l
+    L = cl[sym]
+    assert (L > 0).all(), "symbol without a code"
+    pos = np.concatenate([[0], np.cumsum(L)[:-1]])
+    nbits = int(pos[-1] + L[-1]) if sym.size else 0
+    nw = (nbits + maxlen + 64) // 32 + 1
+    wide = np.zeros(nw + 1, np.uint64)  # 64-bit accumulation of each code's window [word, word + 1]
+    w0 = pos >> 5
+    shift = (64 - L - (pos & 31)).astype(np.uint64)
+    v = cv[sym] << shift
+    hi, lo = (v >> np.uint64(32)), (v & np.uint64(0xFFFFFFFF))
+    np.add.at(wide, w0, hi)
+    np.add.at(wide, w0 + 1, lo)
+    words = wide[:nw].astype(np.uint32)
+    boff = pos[::block].astype(np.int32)
+    lut = np.zeros(1 << maxlen, np.int32)
+    for s, (c, l) in codes.items():
+        base = c << (maxlen - l)
+        lut[base:base + (1 << (maxlen - l))] = s | (l << 8)
+    return words, boff, lut
+
+
+def rans_encode_blocks(sym, freq, block):
+    """Block rANS encoder for the reference decoder format (src/cuda/rans.cu:11-50: M = 4096, L = 2^23, 32-bit
+    state, byte renormalisation read upward): each block encoded backwards, its bytes stored in read order.
+    Returns data, byte_off, state0, slot2sym, freq, cum."""
+    sym = np.asarray(sym, np.int64)
+    freq = np.asarray(freq, np.int64)
+    assert freq.sum() == 4096
+    cum = np.concatenate([[0], np.cumsum(freq)[:-1]])
+    slot2sym = np.repeat(np.arange(freq.size), freq).astype(np.int32)
+    L = 1 << 23
+    data, boff, st0 = [], [], []
+    for b0 in range(0, sym.size, block):
+        x = L
+        out = []
+        for s in sym[b0:b0 + block][::-1]:
+            f, c = int(freq[s]), int(cum[s])
+            xmax = ((L >> 12) << 8) * f
+            while x >= xmax:
+                out.append(x & 0xFF)
+                x >>= 8
+            x = ((x // f) << 12) + (x % f) + c
+        boff.append(len(data))
+        data.extend(out[::-1])
+        st0.append(x)
+    data.extend([0] * 8)
+    return (np.array(data, np.uint8), np.array(boff, np.int32), np.array(st0, np.uint32), slot2sym,
+            freq.astype(np.int32), cum.astype(np.int32))
