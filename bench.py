@@ -65,18 +65,20 @@ def bench_copy(steps: int, warmup: int, nbytes: int = 1 << 30) -> dict:
 # ------------------------------------------------------------------------------------------------ RRR wavelet (C1)
 def bench_rrr(steps: int, warmup: int, cpu: bool = True) -> dict:
     import torch
-    import oracle as O
     from chromofold_amd import synth
-    from chromofold_amd.search import RrrWaveletIndex, to_u32, u32_dev
+    from chromofold_amd.search import build_rrrw, to_u32, u32_dev
 
     n, vocab, nq = 1 << 20, 32000, 1 << 20
     tok = synth.zipf_tokens(n, vocab, 1.1, synth.SEED_C1)
-    w = O.rrrw_build(tok, 15)  # index construction is offline (the reference's CPU builder's job)
-    idx = RrrWaveletIndex.from_host(w, "cuda:0")
+    dtok = torch.from_numpy(tok.view(np.int32)).to("cuda:0")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    idx, lay = build_rrrw(dtok, 15)  # on-device index construction (cf_rrrw_build)
+    t_build = time.perf_counter() - t0
     pos, c, i = synth.rrr_queries(tok, nq, vocab, synth.SEED_C1 + 1)
     dpos, dc, di = u32_dev(pos), u32_dev(c), u32_dev(i)
     out = torch.empty(nq, dtype=torch.int32, device="cuda:0")
-    # correctness gate before timing (bit-exact vs closed form for access, oracle for rank)
+    # correctness gate before timing: access against the token array itself (closed form)
     idx.access_into(dpos, out)
     assert np.array_equal(to_u32(out), tok[pos]), "access mismatch"
     idx.rank_into(dc, di, out)
@@ -94,9 +96,13 @@ def bench_rrr(steps: int, warmup: int, cpu: bool = True) -> dict:
         "rank_wall_ms_per_step": wall_r / steps,
         "rank_roofline": {"bound": "hbm", "achieved": bytes_rank / t_rank / 1e9, "peak": HBM_PEAK_GBS,
                           "unit": "GB/s", "frac": bytes_rank / t_rank / 1e9 / HBM_PEAK_GBS, "traffic": None},
+        "access_gbs": bytes_acc / t_acc / 1e9,
         "index_bytes": idx.device_bytes(), "bits_per_token": idx.device_bytes() * 8.0 / n,
+        "gpu_index_build_ms": t_build * 1e3,
     }
     if cpu:
+        import oracle as O
+        w = O.rrrw_build(tok, 15)  # the CPU baseline's own index (byte-identical to the GPU build)
         th = O.num_threads()
         t0 = time.perf_counter()
         ref = O.rrrw_rank(w, c, i)
@@ -104,6 +110,103 @@ def bench_rrr(steps: int, warmup: int, cpu: bool = True) -> dict:
         assert np.array_equal(ref, rank_gpu), "GPU rank != oracle rank"
         res["cpu_baseline"] = {"value": nq / dt / 1e6, "unit": "Mq/s", "cores": th, "kind": "port",
                                "sample": f"1M rank queries on the C1 index (oracle, OpenMP {th} threads)"}
+    return res
+
+
+# ------------------------------------------------------------------------------------------------ FM-index (C2)
+def bench_fm(steps: int, warmup: int, cpu: bool = True) -> dict:
+    """16M Zipf tokens, vocab 32000: GPU suffix array + BWT + RRR wavelet build, then count of 1M patterns (900K cut
+    from the text, 100K random) and locate of every occurrence of the cut patterns."""
+    import torch
+    from chromofold_amd import synth
+    from chromofold_amd.search import build_fm
+
+    n, vocab = 1 << 24, 32000
+    tok = synth.zipf_tokens(n, vocab, 1.1, synth.SEED_C2)
+    dtok = torch.from_numpy(tok.view(np.int32)).to("cuda:0")
+    fm, info = build_fm(dtok, 32)
+    flat, pstart, plen = synth.fm_patterns(tok, 900_000, 100_000, vocab, synth.SEED_C2 + 1)
+    dpat, dps, dpl = (torch.from_numpy(a).to("cuda:0") for a in (flat, pstart, plen))
+    cnt = fm.count(dpat, dps, dpl)
+    lo, hi = fm.ranges(dpat, dps, dpl)
+    occ = int((hi - lo).sum().item())
+    # every occurrence row of every pattern, flattened on the device
+    rows = (torch.repeat_interleave(lo, (hi - lo).long()) +
+            torch.arange(occ, device="cuda:0", dtype=torch.int32) -
+            torch.repeat_interleave(torch.cumsum(hi - lo, 0, dtype=torch.int32) - (hi - lo), (hi - lo).long()))
+    rows = rows.to(torch.int32).contiguous()
+    pos = torch.empty_like(rows)
+    fm.locate(rows, pos)
+    torch.cuda.synchronize()
+    # gate (size-independent): cut patterns occur, counts agree with ranges, every located position spells its
+    # pattern in the text
+    c_h = cnt.cpu().numpy()
+    assert (c_h[:900_000] >= 1).all() and np.array_equal(c_h, (hi - lo).cpu().numpy())
+    s = np.concatenate([tok.astype(np.int64) + 1, [0]])
+    rng = np.random.default_rng(5)
+    owner = np.repeat(np.arange(c_h.size), c_h)
+    p_h = pos.cpu().numpy()
+    for k in rng.integers(0, occ, 2000):
+        j = owner[k]
+        a = int(p_h[k])
+        assert np.array_equal(s[a:a + plen[j]], flat[pstart[j]:pstart[j] + plen[j]]), "located position mismatch"
+    _, per_c = _events_time(lambda: fm.count(dpat, dps, dpl), steps, warmup)
+    _, per_l = _events_time(lambda: fm.locate(rows, pos), steps, warmup)
+    t_c = float(np.mean(per_c)) * 1e-3
+    t_l = float(np.mean(per_l)) * 1e-3
+    res = {"count_mpats": pstart.size / t_c / 1e6, "count_ms": t_c * 1e3, "occurrences": occ,
+           "locate_mocc": occ / t_l / 1e6, "locate_ms": t_l * 1e3, "gpu_sa_build_s": info["sa_s"],
+           "gpu_index_build_s": info["build_s"], "index_bytes": fm.w.device_bytes()}
+    if cpu:
+        import oracle as O
+        from chromofold_amd.search import to_u32
+        w = O.RrrwArrays(fm.w.bits, fm.w.cwords, fm.w.nsb, fm.w.na,
+                         *[fm.w.tensors[k].cpu().numpy().view(dt) for k, dt in
+                           (("classes", np.uint32), ("offsets", np.uint32), ("rank_a", np.int32),
+                            ("rank_d", np.uint16), ("off_a", np.int32), ("off_d", np.uint16),
+                            ("offbase", np.int32), ("zeros", np.int32))])
+        f = O.FmArrays(w, fm.tensors["C"].cpu().numpy(), to_u32(fm.tensors["mwords"]), fm.tensors["msb"].cpu().numpy(),
+                       fm.tensors["sval"].cpu().numpy(), fm.sigma, fm.n, fm.sa_sample)
+        k = 100_000
+        th = O.num_threads()
+        t0 = time.perf_counter()
+        ref = O.fm_count(f, flat, pstart[:k], plen[:k])
+        dt = time.perf_counter() - t0
+        assert np.array_equal(ref, c_h[:k]), "GPU count != oracle count"
+        res["cpu_baseline"] = {"value": k / dt / 1e6, "unit": "M patterns/s", "cores": th, "kind": "port",
+                               "sample": f"count of the first {k} patterns on the same index (oracle, OpenMP {th} "
+                                         f"threads)"}
+    return res
+
+
+# ------------------------------------------------------------------------------------------------ matmul (C3)
+def bench_qw(steps: int, warmup: int, batches=(1, 4, 16, 64)) -> dict:
+    """4096 x 4096 int4 weights (N(0,1), per (row, 64-col) absmax), per-band Huffman, bf16 x: y = x W^T."""
+    import torch
+    import oracle as O
+    from chromofold_amd import qw, synth
+
+    M = K = 4096
+    rng = np.random.default_rng(synth.SEED_C3)
+    W = rng.standard_normal((M, K), dtype=np.float32)
+    h = qw.encode_int4(W)
+    mat = qw.QwMatrix(h, "cuda:0")
+    res = {"coded_bytes": h.nbytes, "bits_per_weight": h.nbytes * 8.0 / (M * K)}
+    scales = np.repeat(h.scales, 64, axis=1)
+    for B in batches:
+        x = torch.from_numpy(rng.standard_normal((B, K), dtype=np.float32)).to(torch.bfloat16)
+        dx = x.to("cuda:0")
+        y = torch.empty((B, M), device="cuda:0")
+        mat.matmul_into(dx, y)
+        torch.cuda.synchronize()
+        if B <= 16:  # gate against the fp64 oracle
+            ref = O.qmatmul_f64(x.float().numpy(), h.sym, scales, 8)
+            err = float(np.abs(y.cpu().numpy() - ref).max() / np.abs(ref).max())
+            assert err <= 1e-3, err
+        _, per = _events_time(lambda: mat.matmul_into(dx, y), steps, warmup)
+        t = float(np.mean(per)) * 1e-3
+        byts = h.nbytes + 2 * B * K + 4 * B * M
+        res[f"B{B}"] = {"us": t * 1e6, "gbs": byts / t / 1e9, "tflops": 2.0 * B * M * K / t / 1e12}
     return res
 
 
@@ -214,6 +317,9 @@ def main() -> int:
         secondary["wavelet_access_mqs"] = rrr["access_mqs"]
         secondary["wavelet_rank_roofline_frac"] = rrr["rank_roofline"]["frac"]
         secondary["wavelet_cpu_baseline"] = rrr.get("cpu_baseline")
+        secondary["c1_rrr"] = {k: v for k, v in rrr.items() if k not in ("rank_roofline", "cpu_baseline")}
+        secondary["c2_fm"] = bench_fm(min(args.steps, 20), 2, cpu=not args.no_cpu)
+        secondary["c3_matmul"] = bench_qw(min(args.steps, 50), 3)
         cp = bench_copy(10, 2)
         secondary["stream_copy_gbs"] = cp["stream_copy_gbs"]
         secondary["roofline_frac_of_stream_copy"] = kvr["roofline"]["achieved"] / cp["stream_copy_gbs"]

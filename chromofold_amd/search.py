@@ -7,6 +7,7 @@ carrying the cf_status the C entry point returned.
 """
 from __future__ import annotations
 
+import ctypes as C
 from dataclasses import dataclass
 
 import numpy as np
@@ -160,3 +161,86 @@ def gpu_suffix_array(s: torch.Tensor, stream=None) -> torch.Tensor:
     sa = torch.empty(n, dtype=torch.int32, device=s.device)
     A.check(A.lib().cf_suffix_array(_ptr(s), n, mx, _ptr(sa), _ptr(ws), wsb, stream_ptr(stream)), "cf_suffix_array")
     return sa
+
+
+# ------------------------------------------------------------------------------------------------ on-device builds
+class cf_rrrw_layout(C.Structure):
+    _fields_ = [("n", A.U64), ("bits", A.U32), ("nblocks", A.U32), ("cwords", A.U32), ("nsb", A.U32), ("na", A.U32),
+                ("owords", A.U32), ("rrr_bytes", A.U64), ("level_owords", A.U32 * 32)]
+
+
+class cf_rrrw_arrays(C.Structure):
+    _fields_ = [(k, A.P) for k in ("classes", "offsets", "rank_a", "rank_d", "off_a", "off_d", "offbase", "zeros")]
+
+
+A.declare("cf_rrrw_build_workspace_bytes", A.U64, [A.U64, A.U32])
+A.declare("cf_rrrw_build", A.I32, [A.P, A.U64, A.U32, A.P, A.U64, C.POINTER(cf_rrrw_layout), A.P])
+A.declare("cf_rrrw_build_copy", A.I32, [A.P, C.POINTER(cf_rrrw_layout), C.POINTER(cf_rrrw_arrays), A.P])
+A.declare("cf_fm_build_workspace_bytes", A.U64, [A.I32, A.I32])
+A.declare("cf_fm_build_aux", A.I32, [A.P, A.P, A.I32, A.I32, A.I32, A.P, A.P, A.P, A.P, A.P, C.POINTER(C.c_int32),
+                                     A.P, A.U64, A.P])
+
+
+def build_rrrw(tokens: torch.Tensor, bits: int, stream=None) -> tuple[RrrWaveletIndex, cf_rrrw_layout]:
+    """RRR wavelet matrix of the device token array (int32 holding u32 values < 2^bits), built on the GPU."""
+    n = tokens.numel()
+    dev = tokens.device
+    L = A.lib()
+    wsb = int(L.cf_rrrw_build_workspace_bytes(n, bits))
+    if wsb == 0:
+        raise A.CfError(A.CF_ERR_UNSUPPORTED, "cf_rrrw_build_workspace_bytes")
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    lay = cf_rrrw_layout()
+    s = stream_ptr(stream)
+    A.check(L.cf_rrrw_build(_ptr(tokens), n, bits, _ptr(ws), wsb, C.byref(lay), s), "cf_rrrw_build")
+    i32 = dict(dtype=torch.int32, device=dev)
+    t = {"classes": torch.empty(bits * lay.cwords, **i32), "offsets": torch.empty(lay.owords, **i32),
+         "rank_a": torch.empty(bits * lay.na, **i32), "rank_d": torch.empty(bits * (lay.nsb + 1), dtype=torch.int16,
+                                                                            device=dev),
+         "off_a": torch.empty(bits * lay.na, **i32), "off_d": torch.empty(bits * (lay.nsb + 1), dtype=torch.int16,
+                                                                          device=dev),
+         "offbase": torch.empty(bits, **i32), "zeros": torch.empty(bits, **i32)}
+    arr = cf_rrrw_arrays(*[_ptr(t[k]) for k in ("classes", "offsets", "rank_a", "rank_d", "off_a", "off_d", "offbase",
+                                                 "zeros")])
+    A.check(L.cf_rrrw_build_copy(_ptr(ws), C.byref(lay), C.byref(arr), s), "cf_rrrw_build_copy")
+    binom, width = rrr_tables()
+    t["binom"] = _dev(binom, dev)
+    t["width"] = _dev(width, dev)
+    (stream if stream is not None else torch.cuda.current_stream(dev)).synchronize()  # copies done before ws goes
+    return RrrWaveletIndex(bits, int(lay.cwords), int(lay.nsb), int(lay.na), t), lay
+
+
+def build_fm(tokens: torch.Tensor, sa_sample: int, stream=None) -> tuple[FmIndex, dict]:
+    """Full on-device FM-index build of a token array (int32 device tensor, values >= 0): text s = (tokens + 1) ++
+    [0], GPU suffix array, BWT, RRR wavelet of the BWT, C / mark plane / msb / sampled SA. Returns the index and the
+    intermediate device arrays (s, sa, bwt) and build timings."""
+    import time
+    dev = tokens.device
+    t0 = time.perf_counter()
+    s = torch.empty(tokens.numel() + 1, dtype=torch.int32, device=dev)
+    s[:-1] = tokens + 1
+    s[-1] = 0
+    n = s.numel()
+    sa = gpu_suffix_array(s, stream)
+    torch.cuda.synchronize(dev)
+    t_sa = time.perf_counter() - t0
+    sigma = int(s.max().item()) + 1
+    bits = max(1, (sigma - 1).bit_length())
+    nw = (n + 31) // 32
+    nb = (nw + 7) // 8
+    bwt = torch.empty(n, dtype=torch.int32, device=dev)
+    Ct = torch.empty(sigma, dtype=torch.int32, device=dev)
+    mw = torch.empty(nw, dtype=torch.int32, device=dev)
+    msb = torch.empty(nb + 1, dtype=torch.int32, device=dev)
+    sval = torch.empty(n // sa_sample + 2, dtype=torch.int32, device=dev)
+    cnt = C.c_int32(0)
+    L = A.lib()
+    wsb = int(L.cf_fm_build_workspace_bytes(n, sigma))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    A.check(L.cf_fm_build_aux(_ptr(s), _ptr(sa), n, sigma, sa_sample, _ptr(bwt), _ptr(Ct), _ptr(mw), _ptr(msb),
+                              _ptr(sval), C.byref(cnt), _ptr(ws), wsb, stream_ptr(stream)), "cf_fm_build_aux")
+    w, lay = build_rrrw(bwt, bits, stream)
+    torch.cuda.synchronize(dev)
+    t_all = time.perf_counter() - t0
+    fm = FmIndex(w, sigma, n, sa_sample, {"C": Ct, "mwords": mw, "msb": msb, "sval": sval[:cnt.value].clone()})
+    return fm, {"s": s, "sa": sa, "bwt": bwt, "sa_s": t_sa, "build_s": t_all, "layout": lay}

@@ -31,3 +31,23 @@ def rrr_queries(tokens: np.ndarray, nq: int, vocab: int, seed: int):
     c[half:] = rng.integers(0, vocab, nq - half).astype(np.uint32)
     i = rng.integers(0, n + 1, nq, dtype=np.int64).astype(np.uint32)
     return pos, c, i
+
+
+def fm_patterns(tokens: np.ndarray, n_cut: int, n_rand: int, vocab: int, seed: int, lmin: int = 8, lmax: int = 32):
+    """Patterns for the FM workload, in text symbols (token + 1): n_cut windows of length U[lmin, lmax] cut at
+    uniform text offsets, then n_rand patterns of uniform random tokens (almost never occurring). Returns the
+    flattened symbols, start offsets and lengths (int32)."""
+    rng = np.random.default_rng(seed)
+    n = tokens.size
+    lens = rng.integers(lmin, lmax + 1, n_cut + n_rand).astype(np.int32)
+    starts = np.zeros(lens.size, np.int64)
+    starts[1:] = np.cumsum(lens[:-1])
+    flat = np.empty(int(lens.sum()), np.int32)
+    offs = rng.integers(0, n - lmax, n_cut)
+    idx = starts[:n_cut, None] + np.arange(lmax)[None, :]
+    src = offs[:, None] + np.arange(lmax)[None, :]
+    mask = np.arange(lmax)[None, :] < lens[:n_cut, None]
+    flat[idx[mask]] = tokens[src[mask]].astype(np.int32) + 1
+    r0 = int(starts[n_cut]) if n_rand else flat.size
+    flat[r0:] = rng.integers(0, vocab, flat.size - r0).astype(np.int32) + 1
+    return flat, starts.astype(np.int32), lens

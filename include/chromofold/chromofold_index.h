@@ -27,6 +27,52 @@ uint64_t cf_suffix_array_workspace_bytes(int32_t n, int32_t max_symbol);
 cf_status cf_suffix_array(const int32_t *s, int32_t n, int32_t max_symbol, int32_t *sa_out, void *workspace,
                           uint64_t workspace_bytes, void *stream);
 
+/* ---- on-device RRR wavelet matrix build (the .cfrw arrays of cf_rrrw_view) ----
+ * Layout identical to the reference builder (tools/build_index.cpp:90-218): T = 15-bit blocks, 64 blocks per
+ * superblock, 32 superblocks per anchor, class nibbles LSB-first, offsets LSB-first packed per level with
+ * offbase[level] = bit offset of the level's first offset word. */
+typedef struct cf_rrrw_layout {
+  uint64_t n;
+  uint32_t bits, nblocks, cwords, nsb, na;
+  uint32_t owords;              /* total offset words over all levels */
+  uint64_t rrr_bytes;           /* stored class + offset bits / 8 + sample bytes (the .cfrw header figure) */
+  uint32_t level_owords[32];    /* offset words of each level (2 words of padding included) */
+} cf_rrrw_layout;
+
+typedef struct cf_rrrw_arrays { /* device outputs, sized from the layout */
+  uint32_t *classes;  /* [bits * cwords] */
+  uint32_t *offsets;  /* [owords] */
+  int32_t *rank_a;    /* [bits * na] */
+  uint16_t *rank_d;   /* [bits * (nsb + 1)] */
+  int32_t *off_a;     /* [bits * na] */
+  uint16_t *off_d;    /* [bits * (nsb + 1)] */
+  int32_t *offbase;   /* [bits] */
+  int32_t *zeros;     /* [bits] */
+} cf_rrrw_arrays;
+
+/* Workspace for cf_rrrw_build (0 if n or bits are out of range: n < 2^31, 1 <= bits <= 31). Host only. */
+uint64_t cf_rrrw_build_workspace_bytes(uint64_t n, uint32_t bits);
+
+/* Builds every level of the RRR wavelet matrix of tokens[0..n) (device, values < 2^bits) inside the workspace and
+ * reports the sizes; synchronises `stream` once at the end (the offset-stream lengths are data dependent).
+ * No counterpart in the reference C ABI (its builder is the CPU tool tools/build_index.cpp). */
+cf_status cf_rrrw_build(const uint32_t *tokens, uint64_t n, uint32_t bits, void *workspace, uint64_t workspace_bytes,
+                        cf_rrrw_layout *layout, void *stream);
+
+/* Copies a built matrix from the workspace into caller arrays (asynchronous device-to-device copies). */
+cf_status cf_rrrw_build_copy(const void *workspace, const cf_rrrw_layout *layout, const cf_rrrw_arrays *out,
+                             void *stream);
+
+/* ---- on-device FM-index side arrays (reference tools/build_index.cpp:368-371, 455-469) ----
+ * From the text s[0..n) (device, ending in the unique sentinel 0, symbols < sigma) and its suffix array: bwt[i] =
+ * s[sa[i] - 1] (cyclic), C[c] = #symbols < c, mark plane mwords[(n + 31) / 32] (bit i set when sa[i] % sa_sample == 0)
+ * with its directory msb[nb + 1] (cumulative marks every 8 words, nb = ((n + 31) / 32 + 7) / 8), and sval (sa of the
+ * marked rows in row order; *sval_count receives their number after the one synchronisation). */
+uint64_t cf_fm_build_workspace_bytes(int32_t n, int32_t sigma);
+cf_status cf_fm_build_aux(const int32_t *s, const int32_t *sa, int32_t n, int32_t sigma, int32_t sa_sample,
+                          uint32_t *bwt, int32_t *C, uint32_t *mwords, int32_t *msb, int32_t *sval, int32_t *sval_count,
+                          void *workspace, uint64_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 
