@@ -89,7 +89,6 @@ def _declare(L):
         "or_kv_window_attention_f64": (None, [P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, P]),
         "or_kv_decode_group": (C.c_int, [P, P, U32, P, P, P, P, P]),
         "or_kv_quantize_page_absmax": (None, [P, U32, P, P]),
-        "or_softmax_merge": (None, [P, P, P, C.c_double, C.c_double, P, U32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name, None)

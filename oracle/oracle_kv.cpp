@@ -5,12 +5,21 @@
 //   paged attention, fp64 online softmax      reference src/runtime/kv_reference.cpp:50-67,164-243 and the GPU
 //                                             seam semantics of src/cuda/paged_kv_attention.cu:41-176 (window,
 //                                             GQA h / gqa_group_size, active tail, no visible token -> zeros)
-//   online-softmax state merge                reference src/runtime/kv_runtime.cpp:179-254
 //   canonical Huffman LUT decode              reference include/chromofold/detail/block_huffman_device.cuh:12-19
 //   block rANS decode                         reference src/cuda/rans.cu:16-26
 //   RANS_HYBRID / INT8 page decode            the byte format written out in include/chromofold/kv_codec_ext.h
 //                                             (this project's codec; restated here from the format text, not
 //                                             from the product encoder, so a format slip shows as a mismatch)
+//   windowed attention (fp64)                 reference src/cuda/fused_kv_attention.cu:27-65
+//
+// Parity pins (tests/test_oracle_vs_reference.py, tests/test_oracle_codecs.py, tests/test_kv_codec.py):
+//   quantiser + packing      bit-identical to the reference's own encode_int{4,8}_page, compiled from its sources
+//   paged attention          within 1e-6 of the reference's own paged_attention (GQA, windows, tail, page order)
+//   dense / window attention reduce to the pinned paged attention on one page (closed-form special case)
+//   Huffman LUT decode       inverts two independent packers (per-symbol and vectorised) from any block offset
+//   block rANS decode        inverts an independent encoder (ryg-style byte renormalisation), incl. the
+//                            single-symbol distribution and 1-symbol blocks; a corrupted byte changes the output
+//   group decode             inverts the product encoder and reproduces the quantiser's symbols exactly
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
@@ -263,23 +272,6 @@ void or_kv_quantize_page_absmax(const float *x, uint32_t n, uint8_t *sym, float 
   for (uint32_t i = 0; i < n; ++i) m = std::max(m, std::fabs(x[i]));
   *scale = m == 0.0f ? 1.0f : m / 127.0f;
   for (uint32_t i = 0; i < n; ++i) sym[i] = (uint8_t)(std::clamp(std::lrint(x[i] / *scale), -128L, 127L) + 128);
-}
-
-// ---------------------------------------------------------------------------------------- online softmax
-// (m, l, acc[D]) merge as reference kv_runtime.cpp:219-243 (returns merged state in dst)
-void or_softmax_merge(double *dst_m, double *dst_l, double *dst_acc, double src_m, double src_l,
-                      const double *src_acc, uint32_t D) {
-  if (src_l == 0.0) return;
-  if (*dst_l == 0.0) {
-    *dst_m = src_m;
-    *dst_l = src_l;
-    std::memcpy(dst_acc, src_acc, sizeof(double) * D);
-    return;
-  }
-  const double nm = std::max(*dst_m, src_m), a = std::exp(*dst_m - nm), b = std::exp(src_m - nm);
-  *dst_l = *dst_l * a + src_l * b;
-  for (uint32_t d = 0; d < D; ++d) dst_acc[d] = dst_acc[d] * a + src_acc[d] * b;
-  *dst_m = nm;
 }
 
 }  // extern "C"

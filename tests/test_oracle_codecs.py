@@ -64,3 +64,37 @@ def test_huffman_packers_agree_and_decode(maxlen):
     w3 = w2.copy()
     w3[3] ^= 1 << 17
     assert not np.array_equal(O.huffman_decode(w3, l2, maxlen, 0, sym.size), sym)
+
+
+def test_dense_and_window_attention_reduce_to_paged():
+    """or_dense_attention_f64 (and the windowed attention built on it) equals the reference-pinned paged oracle:
+    one page holding all rows, query at the last token, causal window w <-> the last w rows."""
+    rng = np.random.default_rng(12)
+    T, D = 40, 32
+    K = rng.standard_normal((T, D)).astype(np.float32)
+    V = rng.standard_normal((T, D)).astype(np.float32)
+    Q = rng.standard_normal((T, D)).astype(np.float32)
+    for i, w in ((T - 1, 1000), (T - 1, 7), (10, 3), (0, 5)):
+        paged, empty = O.paged_attention_f64(Q[i][None], 1, 1, D, 1, i, w if w < 1000 else 0, 0.3, [(0, 0, K, V)])
+        assert empty == 0
+        lo = max(0, i - w + 1)
+        dense = O.dense_attention_f64(Q[i], K[lo:i + 1], V[lo:i + 1], 0.3)
+        np.testing.assert_allclose(dense, paged[0], rtol=1e-6, atol=1e-7)
+        win = O.kv_window_attention_f64(K, V, Q, i + 1, min(w, 512), 0.3)[i]
+        np.testing.assert_allclose(win, paged[0], rtol=1e-6, atol=1e-7)
+
+
+def test_qmatmul_oracle_special_cases():
+    """y = x (q - zero)^T scale: a one-hot weight row selects one activation column; zero symbols give zero; a
+    per-element scale array multiplies elementwise (a transposed operand or a dropped zero point fails these)."""
+    rng = np.random.default_rng(3)
+    B, M, K = 3, 5, 7
+    x = rng.standard_normal((B, K))
+    sym = np.full((M, K), 8)
+    cols = rng.integers(0, K, M)
+    sym[np.arange(M), cols] = 9  # (q - 8) = one-hot
+    y = O.qmatmul_f64(x, sym, 2.0, 8)
+    np.testing.assert_array_equal(y, 2.0 * x[:, cols])
+    sc = rng.random((M, K)) + 0.5
+    y2 = O.qmatmul_f64(x, sym, sc, 8)
+    np.testing.assert_allclose(y2, x[:, cols] * sc[np.arange(M), cols][None, :])
