@@ -12,8 +12,9 @@
 //            (A = probabilities of those 4 tokens for the 4 heads, B = the 4 decoded values) accumulating the
 //            lane's 4 heads x 8 dims output.
 // Codec decode per quad: one rANS step (LDS slot table, 64-bit entry = freq/offset + the four 2-bit high parts
-// already spread to their bytes), three bit-sliced low-part words per 4 quads, and two v_perm to build the f16
-// operand (1024 + symbol; the constant 1024+128 offset is folded out with the sum of the other operand).
+// already spread to their bytes; SDWA reads the 16-bit freq/offset halves in place), three bit-sliced low-part
+// words per 4 quads merged with two bit-field inserts, and two v_perm to build the f16 operand (1024 + symbol; the
+// constant 1024+128 offset is folded out with the sum of the other operand).
 // Split-context partial states (m, l, acc) are merged by a second small kernel (online-softmax merge,
 // reference src/runtime/kv_runtime.cpp:219-243 semantics).
 #include <hip/hip_fp16.h>
@@ -55,14 +56,20 @@ __device__ __forceinline__ float4_t mfma4(half4_t a, half4_t b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 0, 0, 0);
 }
 
+// (a & mask) | (b & ~mask) in one v_bfi_b32
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(b));
+  return r;
+}
+
 // Symbol bytes of quad qd (0..3) of a 16-value low-part group: nibbles from n0/n1, bits 4-5 from the crumb word
-// c, bits 6-7 from the spread high parts (two bit-field inserts).
+// c, bits 6-7 from the spread high parts — two bit-field inserts per quad.
 template <int QD>
 __device__ __forceinline__ uint32_t quad_bytes(uint32_t n0, uint32_t n1, uint32_t c, uint32_t spread) {
   const uint32_t nsrc = QD == 0 ? n0 : QD == 1 ? (n0 >> 4) : QD == 2 ? n1 : (n1 >> 4);
   const uint32_t cs = QD == 0 ? (c << 4) : QD == 1 ? (c << 2) : QD == 2 ? c : (c >> 2);
-  const uint32_t r = (nsrc & 0x0F0F0F0Fu) | (cs & 0xF0F0F0F0u);
-  return (spread & 0xC0C0C0C0u) | (r & 0x3F3F3F3Fu);
+  return bfi(0x3F3F3F3Fu, bfi(0x0F0F0F0Fu, nsrc, cs), spread);
 }
 
 // One interleaved-rANS step of the 64-lane stream. x = lane state; wbase = wave-uniform address of the current
@@ -71,7 +78,13 @@ __device__ __forceinline__ uint32_t quad_bytes(uint32_t n0, uint32_t n1, uint32_
 template <typename WordPtr>
 __device__ __forceinline__ uint32_t rans_step(const uint2 *__restrict__ tab, uint32_t &x, WordPtr &wbase) {
   const uint2 e = tab[x & (kSlots - 1)];
-  x = __umul24(e.x & 0xFFFFu, x >> CF_KV_RANS_PROB_BITS) + (e.x >> 16);
+  // x = f * (x >> 11) + c with f, c the two 16-bit halves of e.x, read in place by SDWA operand selects
+  const uint32_t xs = x >> CF_KV_RANS_PROB_BITS;
+  uint32_t fx;
+  asm("v_mul_u32_u24_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD"
+      : "=v"(fx) : "v"(e.x), "v"(xs));
+  asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:DWORD"
+      : "=v"(x) : "v"(e.x), "v"(fx));
   const bool need = x < 65536u;
   const uint64_t m = __builtin_amdgcn_ballot_w64(need);
   const uint32_t idx = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
@@ -389,11 +402,30 @@ __global__ __launch_bounds__(kGqa * D) void kv_merge_kernel(cf_kv_batched_desc d
   d.output[(static_cast<size_t>(seq) * d.query_head_count + head * gqa + h) * D + dd] = l > 0.0f ? o / l : 0.0f;
 }
 
+// Workgroups resident at once: 3 per CU (the LDS and VGPR budget of kv_batched_kernel).
+uint32_t resident_workgroups() {
+  static thread_local int cached_dev = -1;
+  static thread_local uint32_t cached = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 768;
+  if (dev != cached_dev) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached = 3u * static_cast<uint32_t>(cus);
+    cached_dev = dev;
+  }
+  return cached;
+}
+
+// Context splits per (sequence, KV head): enough workgroups to fill the chip in exactly one round when the
+// (sequence, head) units alone do not (a partial second round leaves most CUs idle at the tail), while keeping at
+// least one page group per wavefront.
 uint32_t choose_splits(const cf_kv_batched_desc *d) {
   if (d->splits) return d->splits;
   const uint32_t units = d->seq_count * d->kv_head_count;
-  uint32_t s = (2048 + units - 1) / units;           // aim at ~2048 workgroups (8 per CU)
-  s = std::min<uint32_t>(s, std::max<uint32_t>(1, d->max_groups / kWaves));  // keep >= one group per wavefront
+  const uint32_t resident = resident_workgroups();
+  uint32_t s = units >= resident ? 1u : resident / units;
+  s = std::min<uint32_t>(s, std::max<uint32_t>(1, d->max_groups / kWaves));
   return std::max<uint32_t>(1, std::min<uint32_t>(s, 64));
 }
 
