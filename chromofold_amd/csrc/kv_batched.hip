@@ -15,6 +15,9 @@
 // already spread to their bytes; SDWA reads the 16-bit freq/offset halves in place), three bit-sliced low-part
 // words per 4 quads merged with two bit-field inserts, and two v_perm to build the f16 operand (1024 + symbol; the
 // constant 1024+128 offset is folded out with the sum of the other operand).
+// Memory: a wavefront's next group is in flight while it works on the current one (header in registers, word
+// streams copied straight into LDS by global_load_lds after the current decode loop, first low-part words in
+// registers), so a group starts without a memory round trip.
 // Split-context partial states (m, l, acc) are merged by a second small kernel (online-softmax merge,
 // reference src/runtime/kv_runtime.cpp:219-243 semantics).
 #include <hip/hip_fp16.h>
@@ -111,10 +114,12 @@ struct GroupCtx {
   static constexpr int NQ = D / 4, NG = D / 16, LOWS = 3 * NG * 64;
 };
 
-// Decode one page group (K scores, softmax, V accumulation) with the word streams read through `words`
-// (LDS staging buffer or the blob in HBM).
-template <int D, int CODEC, typename WordPtr>
-__device__ __forceinline__ void group_body(const uint8_t *__restrict__ blob, WordPtr wk, uint32_t kw,
+// Decode one page group (K scores, softmax, V accumulation) with the word streams read through `wk` (the wave's
+// LDS staging buffer). `pre` holds the group's first low-part words (prefetched); `after_decode` runs as soon as
+// the decode loop no longer needs the word buffer (the caller stages the next group there).
+template <int D, int CODEC, typename WordPtr, typename Hook>
+__device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&pre)[6],
+                                           const uint8_t *__restrict__ blob, WordPtr wk, uint32_t kw,
                                            const uint2 (*__restrict__ s_tab)[kSlots], const half4_t *qhi,
                                            const half4_t *qlo, const float *qsum, _Float16 (*s_pw)[kGqa][16],
                                            int lane, bool tok_ok, float ks, float vs, float *m_run, float *l_run,
@@ -140,8 +145,13 @@ __device__ __forceinline__ void group_body(const uint8_t *__restrict__ blob, Wor
               if constexpr (qd == 0) {
 #pragma unroll
                 for (int w = 0; w < 3; ++w) {
-                  kl[w] = lowk[(g * 3 + w) * 64 + lane];
-                  vl[w] = lowk[LOWS + (g * 3 + w) * 64 + lane];
+                  if constexpr (g == 0) {  // first low-part words arrive prefetched by the previous group
+                    kl[w] = pre[w];
+                    vl[w] = pre[3 + w];
+                  } else {
+                    kl[w] = lowk[(g * 3 + w) * 64 + lane];
+                    vl[w] = lowk[LOWS + (g * 3 + w) * 64 + lane];
+                  }
                 }
               }
               const uint32_t hk = rans_step(s_tab[0], xk, wk);
@@ -160,6 +170,7 @@ __device__ __forceinline__ void group_body(const uint8_t *__restrict__ blob, Wor
           ...);
     }(std::make_integer_sequence<int, NQ>{});
   }
+  after_decode();  // the word buffer is free from here on
 
   // ---- online softmax over the wavefront's 64 tokens (one running max per head for all four pages)
   float s[kGqa], mx[kGqa];
@@ -294,28 +305,97 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
   for (int i = 0; i < D / 16; ++i) acc_v[i] = float4_t{0, 0, 0, 0};
 
   uint32_t *buf = s_buf[wave];
+  // Memory pipeline of a wavefront over its groups gi = ga + wave, +4, ...:
+  //   blob offset   loaded two groups ahead;
+  //   header        loaded at the start of the previous group (fields kept in registers);
+  //   word streams  copied into this wave's LDS buffer by global_load_lds (16 bytes per lane, 1 KiB per wave
+  //                 instruction, whole 16-byte chunks: blobs are padded to 16 bytes) during the previous group's
+  //                 softmax / V phase — the buffer is free once that group's decode loop has ended;
+  //   low parts     the first 6 words per lane prefetched together with the word streams.
+  // The next group's copies are awaited with s_waitcnt vmcnt(0) at the top of the loop.
+  auto blob_at = [&](uint32_t g) { return d.pool + static_cast<size_t>(grow[g]) * 16; };
+  uint32_t off_next = (ga + wave + kWaves < gb) ? grow[ga + wave + kWaves] : 0u;
+  const uint8_t *blob = (ga + wave < gb) ? blob_at(ga + wave) : d.pool;
+  uint32_t h_cnt = 0, h_tc = 0, h_codec = 0;
+  float h_ks = 0.f, h_vs = 0.f;
+  if (ga + wave < gb) {
+    h_cnt = *reinterpret_cast<const uint32_t *>(blob + 4);
+    h_tc = reinterpret_cast<const uint16_t *>(blob + 8)[G];
+    h_ks = reinterpret_cast<const float *>(blob + 32)[G];
+    h_vs = reinterpret_cast<const float *>(blob + 48)[G];
+    h_codec = *reinterpret_cast<const uint32_t *>(blob);
+  }
+  constexpr int kStage16 = ((kCapWords * 2) + 1023) / 1024;  // 1 KiB copies per group
+  uint32_t pre[6] = {0, 0, 0, 0, 0, 0};
+  if (RANS && ga + wave < gb && h_codec == CF_KV_CODEC_RANS_HYBRID) {
+    {
+      const uint32_t *lw = reinterpret_cast<const uint32_t *>(blob + kHdr + 512);
+#pragma unroll
+      for (int w = 0; w < 3; ++w) {
+        pre[w] = lw[w * 64 + lane];
+        pre[3 + w] = lw[LOWS + w * 64 + lane];
+      }
+    }
+    const uint32_t nbytes = ((min((h_cnt & 0xFFFFu) + (h_cnt >> 16), kCapWords) * 2u) + 15u) & ~15u;
+    const uint8_t *src = blob + kHdr + 512 + 2 * LOWS * 4;
+#pragma unroll
+    for (int k = 0; k < kStage16; ++k) {
+      const uint32_t at = 1024u * k + 16u * lane;
+      if (at < nbytes)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t *>(src + at),
+                                         (__attribute__((address_space(3))) void *)(buf + 256 * k), 16,
+                                         0, 0);
+    }
+  }
   for (uint32_t gi = ga + wave; gi < gb; gi += kWaves) {
-    const uint8_t *blob = d.pool + static_cast<size_t>(grow[gi]) * 16;
-    const uint32_t cnt = *reinterpret_cast<const uint32_t *>(blob + 4);
-    const uint32_t kw = cnt & 0xFFFFu, vw = cnt >> 16;
-    const uint32_t tcG = reinterpret_cast<const uint16_t *>(blob + 8)[G];
-    const float ks = reinterpret_cast<const float *>(blob + 32)[G];
-    const float vs = reinterpret_cast<const float *>(blob + 48)[G];
+    const uint32_t cnt = h_cnt, tcG = h_tc, gcodec = h_codec;  // gcodec is wave-uniform
+    const float ks = h_ks, vs = h_vs;
+    const uint8_t *cur = blob;
+    const uint32_t kw = cnt & 0xFFFFu;
     const bool tok_ok = static_cast<uint32_t>(t) < tcG && 64 * gi + 16 * G + t < visible;
-    const uint32_t gcodec = *reinterpret_cast<const uint32_t *>(blob);  // wave-uniform
-    if (RANS && gcodec == CF_KV_CODEC_RANS_HYBRID) {
-      // stage both word streams in LDS (coalesced u32 copy); the encoder guarantees kw + vw <= kCapWords
-      const uint32_t *src = reinterpret_cast<const uint32_t *>(blob + kHdr + 512 + 2 * LOWS * 4);
-      const uint32_t n32 = (min(kw + vw, kCapWords) + 1) / 2;
-      for (uint32_t i = lane; i < n32; i += 64) buf[i] = src[i];
+    if constexpr (RANS) {  // this group's copies (started during the previous group) have landed
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      group_body<D, CF_KV_CODEC_RANS_HYBRID>(blob, reinterpret_cast<const uint16_t *>(buf), kw, s_tab, qhi, qlo,
-                                             qsum, s_p[wave], lane, tok_ok, ks, vs, m_run, l_run, corr, acc_v);
+    }
+    if (gi + kWaves < gb) {  // next group's header (its offset was loaded one group earlier)
+      blob = d.pool + static_cast<size_t>(off_next) * 16;
+      h_cnt = *reinterpret_cast<const uint32_t *>(blob + 4);
+      h_tc = reinterpret_cast<const uint16_t *>(blob + 8)[G];
+      h_ks = reinterpret_cast<const float *>(blob + 32)[G];
+      h_vs = reinterpret_cast<const float *>(blob + 48)[G];
+      h_codec = *reinterpret_cast<const uint32_t *>(blob);
+      off_next = (gi + 2 * kWaves < gb) ? grow[gi + 2 * kWaves] : 0u;
+    }
+    const bool next_rans = RANS && gi + kWaves < gb && h_codec == CF_KV_CODEC_RANS_HYBRID;
+    auto stage_next = [&]() {  // next group's first low words + word streams (no VGPRs for the streams)
+      if (!next_rans) return;
+      {
+        const uint32_t *lw = reinterpret_cast<const uint32_t *>(blob + kHdr + 512);
+#pragma unroll
+        for (int w = 0; w < 3; ++w) {
+          pre[w] = lw[w * 64 + lane];
+          pre[3 + w] = lw[LOWS + w * 64 + lane];
+        }
+      }
+      const uint32_t nbytes = ((min((h_cnt & 0xFFFFu) + (h_cnt >> 16), kCapWords) * 2u) + 15u) & ~15u;
+      const uint8_t *src = blob + kHdr + 512 + 2 * LOWS * 4;
+#pragma unroll
+      for (int k = 0; k < kStage16; ++k) {
+        const uint32_t at = 1024u * k + 16u * lane;
+        if (at < nbytes)
+          __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t *>(src + at),
+                                           (__attribute__((address_space(3))) void *)(buf + 256 * k),
+                                           16, 0, 0);
+      }
+    };
+    if (RANS && gcodec == CF_KV_CODEC_RANS_HYBRID) {
+      group_body<D, CF_KV_CODEC_RANS_HYBRID>(stage_next, pre, cur, reinterpret_cast<const uint16_t *>(buf), kw, s_tab, qhi,
+                                             qlo, qsum, s_p[wave], lane, tok_ok, ks, vs, m_run, l_run, corr, acc_v);
     } else {  // raw int8 group (the INT8 codec, or the raw fallback of a high-entropy group)
-      group_body<D, CF_KV_CODEC_INT8>(blob, static_cast<const uint16_t *>(nullptr), 0, s_tab, qhi, qlo, qsum,
-                                      s_p[wave], lane, tok_ok, ks, vs, m_run, l_run, corr, acc_v);
+      group_body<D, CF_KV_CODEC_INT8>(stage_next, pre, cur, static_cast<const uint16_t *>(nullptr), 0, s_tab, qhi, qlo,
+                                      qsum, s_p[wave], lane, tok_ok, ks, vs, m_run, l_run, corr, acc_v);
     }
   }
 
