@@ -164,6 +164,16 @@ cf_status cf_kv_encode_groups(uint32_t codec, const float *keys, const float *va
                               uint64_t pool_capacity, uint64_t pool_at, uint32_t *offsets_out, uint64_t *pool_end,
                               uint32_t threads);
 
+/* Host encoder of the reference's fixed-width page format (the format cf_kv_paged_attention_async decodes with
+ * fixed_code_length = bits): K per-channel and V per-token scales max|x| / (2^(bits-1) - 1) (1.0 when all zero),
+ * sym = clamp(lrint(x / s), -2^(bits-1), 2^(bits-1) - 1) + 2^(bits-1), codes packed MSB-first, one block offset
+ * (bit position) every `block` symbols. bits is 4 or 8. Outputs: k_words/v_words [(T*D*bits + 31) / 32],
+ * k_scales [D], v_scales [T], block_offsets [ceil(T*D / block)] (identical for K and V). Same results as reference
+ * src/runtime/kv_gpu_fixture.cpp:12-95; returns CF_ERR_INVALID_ARGUMENT for bad shapes or non-finite input. */
+cf_status cf_kv_encode_fixed_page(uint32_t bits, const float *keys, const float *values, uint32_t token_count,
+                                  uint32_t head_dim, uint32_t block, uint32_t *k_words, uint32_t *v_words,
+                                  float *k_scales, float *v_scales, int32_t *block_offsets);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

@@ -8,6 +8,7 @@
 #include "chromofold/chromofold.h"
 #include "chromofold/chromofold_extra.h"
 #include "chromofold/chromofold_index.h"
+#include "chromofold/chromofold_kv_adapter.h"
 #include "chromofold/chromofold_qw.h"
 #include "chromofold/chromofold_search.h"
 #include "chromofold/kv_codec_ext.h"
@@ -88,6 +89,15 @@ int main(void) {
   expect("cf_online_softmax_accumulate", cf_online_softmax_accumulate(NULL, 0.0, NULL), INV);
   expect("cf_online_softmax_merge", cf_online_softmax_merge(NULL, NULL), INV);
   expect("cf_online_softmax_finalize", cf_online_softmax_finalize(NULL, NULL), INV);
+  /* chromofold_kv_adapter.h: int 0 / -1 convention, NULL create for bad options */
+  expect("cf_llama_kv_options_validate", cf_llama_kv_options_validate(NULL), -1);
+  expect("cf_llama_kv_create", cf_llama_kv_create(NULL) == NULL, 1);
+  expect("cf_llama_kv_append", cf_llama_kv_append(NULL, 0, 0, 0, NULL, NULL, 1, NULL), -1);
+  expect("cf_llama_kv_attention", cf_llama_kv_attention(NULL, 0, NULL, NULL, 1, 1, 1, 0, 1.0f, 0, NULL), -1);
+  expect("cf_llama_kv_flush", cf_llama_kv_flush(NULL, NULL), -1);
+  expect("cf_llama_kv_get_stats", cf_llama_kv_get_stats(NULL, NULL), -1);
+  expect("cf_llama_kv_last_error", cf_llama_kv_last_error(NULL) != NULL, 1);
+  expect("cf_kv_encode_fixed_page", cf_kv_encode_fixed_page(4, NULL, NULL, 1, 1, 64, NULL, NULL, NULL, NULL, NULL), INV);
   printf("%s (%d failure%s)\n", failures ? "FAIL" : "PASS", failures, failures == 1 ? "" : "s");
   return failures ? 1 : 0;
 }

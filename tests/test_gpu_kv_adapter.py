@@ -1,0 +1,138 @@
+"""llama.cpp adapter end to end on the GPU (cf_llama_kv_create -> append -> attention), mirroring reference
+tests/adapter_attention_test.cu (head_dim {32,64,96,128} x {int4,int8}, 2 kv heads, 14 query heads, GQA 7, page 32,
+70 tokens appended one by one: 2 sealed pages + 6 active) and tests/cache_roundtrip_attention.cu (1 head, hd 64).
+Expected values: the fp64 oracle over exactly what the cache stores (the pinned fixture quantiser's dequantised
+values for sealed tokens, raw fp32 for the active tail). Bar: max abs error <= 2e-4 (the reference test's bar).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+def _expected(K, V, Q, kvh, gqa, hd, page, N, bits, query_token, window=0, sealed_upto=None):
+    sealed = (N // page) * page if sealed_upto is None else sealed_upto
+    pages = []
+    for h in range(kvh):
+        for tb in range(0, sealed, page):
+            n = min(page, sealed - tb)
+            _, _, _, _, kd, vd = O.kv_fixture_quantize(K[h][tb:tb + n], V[h][tb:tb + n], bits)
+            pages.append((h, tb, kd, vd))
+    tail = None
+    if sealed < N:
+        tail = (sealed, np.stack([K[h][sealed:N] for h in range(kvh)], 1), np.stack([V[h][sealed:N] for h in range(kvh)], 1))
+    out, empty = O.paged_attention_f64(Q, kvh * gqa, kvh, hd, gqa, query_token, window, 1.0 / np.sqrt(hd), pages, tail)
+    assert empty == 0
+    return out
+
+
+def _adapter(kvh, qh, hd, page, gqa, bits, layers=1):
+    from chromofold_amd import llama as Lm
+    return Lm.KvAdapter(Lm.options(layers, kvh, qh, hd, page, gqa, bits))
+
+
+@pytest.mark.parametrize("hd", [32, 64, 96, 128])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_adapter_attention_matrix(dev, hd, bits):
+    import torch
+    page, N, kvh, qh, gqa = 32, 70, 2, 14, 7
+    rng = np.random.default_rng(9001 + hd + bits)
+    K = [rng.standard_normal((N, hd)).astype(np.float32) for _ in range(kvh)]
+    V = [rng.standard_normal((N, hd)).astype(np.float32) for _ in range(kvh)]
+    Q = rng.standard_normal((qh, hd)).astype(np.float32)
+    a = _adapter(kvh, qh, hd, page, gqa, bits)
+    for h in range(kvh):
+        for t in range(N):
+            a.append(0, h, t, K[h][t:t + 1], V[h][t:t + 1])
+    st = a.stats()
+    assert st.appended_tokens == kvh * N and st.sealed_pages == kvh * (N // page)
+    assert st.active_tokens == kvh * (N % page) and st.sealed_tokens == kvh * (N // page) * page
+    dq = torch.from_numpy(Q).to(dev)
+    out = torch.full_like(dq, float("nan"))
+    a.attention(0, dq.data_ptr(), out.data_ptr(), 1, qh, gqa, N - 1, 1.0 / np.sqrt(hd))
+    torch.cuda.synchronize()
+    exp = _expected(K, V, Q, kvh, gqa, hd, page, N, bits, N - 1)
+    assert np.abs(out.cpu().numpy() - exp).max() <= 2e-4
+    # the host-memory twin gives the same answer
+    host = a.attention_host(0, Q[None], qh, gqa, N - 1, 1.0 / np.sqrt(hd))[0]
+    assert np.array_equal(host, out.cpu().numpy())
+
+
+def test_cache_roundtrip_flush_window_and_clear(dev):
+    """1 head, hd 64: attention with the active tail, after flush (partial page sealed: own block offsets), with a
+    causal window, then clear() and reuse of the same arenas."""
+    import torch
+    hd, page, N = 64, 32, 70
+    rng = np.random.default_rng(12345)
+    K = [rng.standard_normal((N, hd)).astype(np.float32)]
+    V = [rng.standard_normal((N, hd)).astype(np.float32)]
+    Q = rng.standard_normal((1, hd)).astype(np.float32)
+    a = _adapter(1, 1, hd, page, 1, 4)
+    for t in range(N):
+        a.append(0, 0, t, K[0][t:t + 1], V[0][t:t + 1])
+    dq = torch.from_numpy(Q).to(dev)
+    out = torch.empty_like(dq)
+    sc = 1.0 / np.sqrt(hd)
+    a.attention(0, dq.data_ptr(), out.data_ptr(), 1, 1, 1, N - 1, sc)
+    torch.cuda.synchronize()
+    assert np.abs(out.cpu().numpy() - _expected(K, V, Q, 1, 1, hd, page, N, 4, N - 1)).max() <= 2e-4
+    a.flush()
+    assert a.stats().active_tokens == 0 and a.stats().sealed_pages == 3
+    for window in (0, 20):
+        a.attention(0, dq.data_ptr(), out.data_ptr(), 1, 1, 1, N - 1, sc, window)
+        torch.cuda.synchronize()
+        # after flush the 6-token tail is its own int4 page (quantised like any page of that size)
+        pages = []
+        for tb, n in ((0, 32), (32, 32), (64, 6)):
+            _, _, _, _, kd, vd = O.kv_fixture_quantize(K[0][tb:tb + n], V[0][tb:tb + n], 4)
+            pages.append((0, tb, kd, vd))
+        exp, _ = O.paged_attention_f64(Q, 1, 1, hd, 1, N - 1, window, sc, pages)
+        assert np.abs(out.cpu().numpy() - exp).max() <= 2e-4, window
+    a._ok(a.L.cf_llama_kv_clear(a.h), "clear")
+    assert a.stats().sealed_pages == 0
+    for t in range(40):  # reuse after clear: one sealed page + 8 active
+        a.append(0, 0, 100 + t, K[0][t:t + 1], V[0][t:t + 1])
+    a.attention(0, dq.data_ptr(), out.data_ptr(), 1, 1, 1, 139, sc)
+    torch.cuda.synchronize()
+    K2, V2 = [K[0][:40]], [V[0][:40]]
+    pages = []
+    _, _, _, _, kd, vd = O.kv_fixture_quantize(K2[0][:32], V2[0][:32], 4)
+    exp, _ = O.paged_attention_f64(Q, 1, 1, hd, 1, 139, 0, sc, [(0, 100, kd, vd)],
+                                   (132, K2[0][32:40][:, None], V2[0][32:40][:, None]))
+    assert np.abs(out.cpu().numpy() - exp).max() <= 2e-4
+
+
+def test_many_pages_arena_growth_and_misaligned_tails(dev):
+    """Enough pages to grow the arena several times (descriptors rebuilt after each move), two layers; then a tail
+    misalignment across heads is reported as an error, not served."""
+    import torch
+    from chromofold_amd import llama as Lm
+    hd, page, N, kvh, gqa = 128, 16, 16 * 300 + 5, 2, 4
+    rng = np.random.default_rng(7)
+    K = [rng.standard_normal((N, hd)).astype(np.float32) for _ in range(kvh)]
+    V = [rng.standard_normal((N, hd)).astype(np.float32) for _ in range(kvh)]
+    Q = rng.standard_normal((kvh * gqa, hd)).astype(np.float32)
+    a = _adapter(kvh, kvh * gqa, hd, page, gqa, 8, layers=2)
+    for h in range(kvh):
+        for t0 in range(0, N, 700):
+            a.append(1, h, t0, K[h][t0:t0 + 700], V[h][t0:t0 + 700])
+    dq = torch.from_numpy(Q).to(dev)
+    out = torch.empty_like(dq)
+    a.attention(1, dq.data_ptr(), out.data_ptr(), 1, kvh * gqa, gqa, N - 1, 1.0 / np.sqrt(hd))
+    torch.cuda.synchronize()
+    assert np.abs(out.cpu().numpy() - _expected(K, V, Q, kvh, gqa, hd, page, N, 8, N - 1)).max() <= 2e-4
+    a.append(1, 0, N, K[0][:1], V[0][:1])  # head 0 one token ahead of head 1
+    with pytest.raises(Lm.CfAdapterError, match="aligned"):
+        a.attention(1, dq.data_ptr(), out.data_ptr(), 1, kvh * gqa, gqa, N, 1.0 / np.sqrt(hd))
+    with pytest.raises(Lm.CfAdapterError, match="invalid ChromoFold attention request"):
+        a.attention(1, dq.data_ptr(), out.data_ptr(), 1, 7, 2, N, 1.0)
