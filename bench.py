@@ -287,12 +287,104 @@ def bench_kv(steps: int, warmup: int, context: int = 32768, batch: int = 32, cod
     return res
 
 
+# ------------------------------------------------------------------------------------------------ long context (C5)
+def bench_c5(steps: int, warmup: int) -> dict:
+    """C4 shapes (8 KV / 32 q heads, hd 128, rANS-hybrid pages). (a) 256 sequences sharing one 8192-token prefix
+    (stored once, referenced by every sequence's page table) plus 512 unique tokens each; (b) 4 sequences x 131072
+    tokens. One decode token per sequence per step. Gate: the fp64 oracle on one sequence of (a) and on KV head 0
+    of one sequence of (b)."""
+    import torch
+    import oracle as O
+    from chromofold_amd import kv, synth
+
+    H, QH, D = 8, 32, 128
+    gqa = QH // H
+    sc = 1.0 / np.sqrt(D)
+    res = {}
+    rng = np.random.default_rng(synth.SEED_C5)
+    K0 = rng.standard_normal((H, 1024, D), dtype=np.float32)
+    V0 = rng.standard_normal((H, 1024, D), dtype=np.float32)
+    tables = np.concatenate([t for h in range(H) for t in (kv.build_table(K0[h].reshape(-1, 16, D)),
+                                                           kv.build_table(V0[h].reshape(-1, 16, D)))])
+
+    def run(kvb, S, T, qp):
+        q = torch.from_numpy(rng.standard_normal((S, QH, D), dtype=np.float32)).to("cuda:0")
+        dqp = torch.from_numpy(qp.view(np.int32)).to("cuda:0")
+        out = torch.empty_like(q)
+        desc = kvb.desc(q, out, dqp, sc)
+        kvb.attention(q, out, dqp, sc, desc=desc)
+        torch.cuda.synchronize()
+        _, per = _events_time(lambda: kvb.attention(q, out, dqp, sc, desc=desc), steps, warmup)
+        return q.cpu().numpy(), out.cpu().numpy(), float(np.mean(per)) * 1e-3
+
+    # (a) shared prefix
+    S, P, U = 256, 8192, 512
+    T = P + U
+    seeds = rng.integers(0, 2 ** 63, size=S)
+    prefix = (rng.standard_normal((H, P, D), dtype=np.float32), rng.standard_normal((H, P, D), dtype=np.float32))
+
+    def src_a(s):
+        g = np.random.default_rng(int(seeds[s]))
+        Ks = np.empty((H, T, D), np.float32)
+        Vs = np.empty((H, T, D), np.float32)
+        if s == 0:
+            Ks[:, :P], Vs[:, :P] = prefix
+        else:  # the prefix groups of s > 0 come from sequence 0's blobs and are never encoded from here
+            Ks[:, :P] = 0.0
+            Vs[:, :P] = 0.0
+        Ks[:, P:] = g.standard_normal((H, U, D), dtype=np.float32)
+        Vs[:, P:] = g.standard_normal((H, U, D), dtype=np.float32)
+        return Ks, Vs
+
+    kvb = kv.build_batched(kv.CODEC_RANS_HYBRID, src_a, S, H, np.full(S, T, np.uint32), D, tables, "cuda:0",
+                           keep_host=True, shared={s: (0, P // 64) for s in range(1, S)})
+    qp = np.full(S, T - 1, np.uint32)
+    q, out, t = run(kvb, S, T, qp)
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from kv_helpers import decoded_pages, normwise_err
+    s_chk = 7
+    pages = []
+    for h in range(H):
+        pages += [(h, t0, k, v) for t0, k, v in decoded_pages(kvb, s_chk, h, T)]
+    ref, _ = O.paged_attention_f64(q[s_chk], QH, H, D, gqa, T - 1, 0, sc, pages)
+    err_a = normwise_err(out[s_chk], ref)
+    assert err_a <= 1e-3, err_a
+    logical = 2.0 * S * H * T * D * 2  # bf16 bytes of every sequence's full KV
+    res["shared_prefix"] = {"workload": "256 seqs x (8192 shared + 512 unique) tokens", "tokens_per_s": S / t,
+                            "ms_per_step": t * 1e3, "unique_pool_bytes": kvb.pool_bytes,
+                            "ratio_vs_bf16_logical": logical / kvb.pool_bytes,
+                            "unique_gbs": kvb.pool_bytes / t / 1e9, "max_normwise_err": err_a}
+    del kvb
+
+    # (b) 4 x 131072
+    S, T = 4, 131072
+    seeds = rng.integers(0, 2 ** 63, size=S)
+
+    def src_b(s):
+        g = np.random.default_rng(int(seeds[s]))
+        return g.standard_normal((H, T, D), dtype=np.float32), g.standard_normal((H, T, D), dtype=np.float32)
+
+    kvb = kv.build_batched(kv.CODEC_RANS_HYBRID, src_b, S, H, np.full(S, T, np.uint32), D, tables, "cuda:0",
+                           keep_host=True)
+    qp = np.full(S, T - 1, np.uint32)
+    q, out, t = run(kvb, S, T, qp)
+    pages = [(0, t0, k, v) for t0, k, v in decoded_pages(kvb, 1, 0, T)]
+    ref, _ = O.paged_attention_f64(q[1][:gqa], gqa, 1, D, gqa, T - 1, 0, sc, pages)
+    err_b = normwise_err(out[1][:gqa], ref)
+    assert err_b <= 1e-3, err_b
+    step_bytes = kvb.pool_bytes + tables.size + S * H * (T // 64) * 4 + 2 * q.nbytes
+    res["long_131k"] = {"workload": "4 seqs x 131072 tokens", "tokens_per_s": S / t, "ms_per_step": t * 1e3,
+                        "pool_bytes": kvb.pool_bytes, "hbm_gbs": step_bytes / t / 1e9,
+                        "roofline_frac": step_bytes / t / 1e9 / HBM_PEAK_GBS, "max_normwise_err_head0": err_b}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="auto", choices=["auto", "kv", "rrr", "copy"])
+    ap.add_argument("--workload", default="auto", choices=["auto", "kv", "rrr", "copy", "c5"])
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -309,6 +401,9 @@ def main() -> int:
                           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
                           "data": "synthetic", "config": {"workload": f"torch copy_ of {cp['copy_bytes']} B"}}))
         return 0
+    if args.workload == "c5":
+        print(json.dumps({"c5": bench_c5(args.steps, args.warmup)}))
+        return 0
     if args.workload in ("auto", "kv"):
         kvr = bench_kv(args.steps, args.warmup, cpu=not args.no_cpu, check_seqs=0 if args.no_cpu else 2)
         rrr = bench_rrr(args.steps, args.warmup, cpu=not args.no_cpu)
@@ -320,6 +415,7 @@ def main() -> int:
         secondary["c1_rrr"] = {k: v for k, v in rrr.items() if k not in ("rank_roofline", "cpu_baseline")}
         secondary["c2_fm"] = bench_fm(min(args.steps, 20), 2, cpu=not args.no_cpu)
         secondary["c3_matmul"] = bench_qw(min(args.steps, 50), 3)
+        secondary["c5_long_context"] = bench_c5(min(args.steps, 20), 2)
         cp = bench_copy(10, 2)
         secondary["stream_copy_gbs"] = cp["stream_copy_gbs"]
         secondary["roofline_frac_of_stream_copy"] = kvr["roofline"]["achieved"] / cp["stream_copy_gbs"]
