@@ -329,7 +329,8 @@ extern "C" cf_status cf_qw_validate(const cf_qw_matrix *w) {
     return CF_ERR_INVALID_ARGUMENT;
   if (w->codec != CF_QW_CODEC_HUFFMAN) return CF_ERR_UNSUPPORTED;
   if (w->rows == 0 || w->cols == 0 || w->rows > (1u << 30) || w->cols > (1u << 30)) return CF_ERR_INVALID_ARGUMENT;
-  if (!w->words || !w->seg_offsets || !w->code_lengths || !w->scales) return CF_ERR_INVALID_ARGUMENT;
+  if (!w->words || !w->seg_offsets || !w->code_lengths || !w->scales || w->word_count == 0)
+    return CF_ERR_INVALID_ARGUMENT;
   if (w->zero < 0 || w->zero > 15) return CF_ERR_INVALID_ARGUMENT;
   return CF_OK;
 }

@@ -13,12 +13,12 @@ import torch
 
 from . import _abi as A
 
-QW_ABI_VERSION, QW_CODEC_HUFFMAN, QW_BAND_ROWS, QW_SEG_COLS = 1, 1, 16, 64
+QW_ABI_VERSION, QW_CODEC_HUFFMAN, QW_BAND_ROWS, QW_SEG_COLS = 2, 1, 16, 64
 
 
 class cf_qw_matrix(C.Structure):
     _fields_ = [("struct_size", A.U32), ("abi_version", A.U32), ("codec", A.U32), ("rows", A.U32),
-                ("cols", A.U32), ("zero", A.I32), ("words", A.P), ("seg_offsets", A.P), ("code_lengths", A.P),
+                ("cols", A.U32), ("zero", A.I32), ("word_count", A.U64), ("words", A.P), ("seg_offsets", A.P), ("code_lengths", A.P),
                 ("scales", A.P)]
 
 
@@ -92,7 +92,7 @@ class QwMatrix:
         }
         t = self.t
         self.desc = cf_qw_matrix(C.sizeof(cf_qw_matrix), QW_ABI_VERSION, QW_CODEC_HUFFMAN, h.rows, h.cols, 8,
-                                 t["words"].data_ptr(), t["offs"].data_ptr(), t["lens"].data_ptr(),
+                                 h.words.size, t["words"].data_ptr(), t["offs"].data_ptr(), t["lens"].data_ptr(),
                                  t["scales"].data_ptr())
 
     def matmul_into(self, x: torch.Tensor, y: torch.Tensor, stream=None) -> None:

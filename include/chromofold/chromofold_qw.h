@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define CF_QW_ABI_VERSION 1u
+#define CF_QW_ABI_VERSION 2u
 #define CF_QW_BAND_ROWS 16u
 #define CF_QW_SEG_COLS 64u
 #define CF_QW_MAX_CODE_LENGTH 12u
@@ -38,6 +38,7 @@ typedef struct cf_qw_matrix {
   uint32_t rows;        /* M */
   uint32_t cols;        /* K */
   int32_t zero;         /* symbol of value 0 (8 for int4) */
+  uint64_t word_count;  /* 32-bit words of `words` (bounds the decoder's read-ahead) */
   const uint32_t *words;        /* device: code stream */
   const uint32_t *seg_offsets;  /* device: [rows * ceil(cols / 64)] bit offsets */
   const uint8_t *code_lengths;  /* device: [ceil(rows / 16) * 16] */
