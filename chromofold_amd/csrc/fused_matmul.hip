@@ -35,7 +35,11 @@ constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 constexpr int kTM = 16;                // W rows per workgroup (MFMA N)
 constexpr int kKC = 4096;              // columns staged per chunk
-constexpr int kLdB = kKC + 16;         // LDS row stride in bytes: rows land 4 banks apart for the B-fragment reads
+// Symbol tile layout: 64-column segments 68 bytes apart inside a row (the 64 lanes of a wave, one segment each,
+// write word q of their segments to 64 distinct banks: 17 * s + q), rows kLdB bytes apart (kLdB / 4 = 4 mod 64:
+// the B-fragment read of 16 rows x 4 column groups hits 64 distinct banks).
+constexpr int kSegB = 68;
+constexpr int kLdB = (kKC / 64) * kSegB + 16;
 constexpr int kBT = 4;                 // batch tiles of 16 per pass
 constexpr int kLutBits = 12;           // LUTs up to 2^12 entries are staged in LDS
 constexpr int kSmemW = kTM * kLdB;     // u8 symbol tile
@@ -79,30 +83,30 @@ __device__ __forceinline__ short bf16_of_int(int v) {  // |v| <= 256: exact
   return static_cast<short>(__float_as_uint(static_cast<float>(v)) >> 16);
 }
 
-// canonical-Huffman LUT (symbol | length << 8 over maxlen lookahead bits) from 16 code lengths, built in LDS: symbols
-// sorted by (length, value) receive consecutive codes.
-__device__ void build_band_lut(const uint8_t *__restrict__ len16, int maxlen, int32_t *__restrict__ lut) {
-  // every thread derives the canonical codes itself (16 symbols), then fills its share of the table
-  uint32_t code[16];
-  int L[16];
-#pragma unroll
-  for (int s = 0; s < 16; ++s) L[s] = len16[s];
-  uint32_t c = 0;
-  int prev = 0;
-  for (int l = 1; l <= maxlen; ++l) {
-#pragma unroll
-    for (int s = 0; s < 16; ++s)
-      if (L[s] == l) {
-        c <<= (l - prev);
-        prev = l;
-        code[s] = c++;
-      }
+// canonical-Huffman LUT (symbol | length << 8 over maxlen lookahead bits) from 16 code lengths, built in LDS. The
+// canonical code of symbol s is sum over the symbols t before it in (length, symbol) order of 2^(L_s - L_t); lanes
+// 0..15 compute one symbol each, then every thread fills its share of the table from the 16 (code, length) pairs.
+__device__ void build_band_lut(const uint8_t *__restrict__ len16, int maxlen, int32_t *__restrict__ lut,
+                               uint32_t *__restrict__ s_first) {
+  const int t = threadIdx.x;
+  if (t < 16) {
+    const int L = len16[t];
+    uint32_t code = 0;
+    for (int u = 0; u < 16; ++u) {
+      const int Lu = len16[u];
+      if (Lu > 0 && (Lu < L || (Lu == L && u < t))) code += 1u << (L - Lu);
+    }
+    // first table entry of the symbol's range and the range length (0 for an absent symbol)
+    s_first[t] = L > 0 ? (code << (maxlen - L)) : 0u;
+    s_first[16 + t] = L > 0 ? (1u << (maxlen - L)) : 0u;
+    s_first[32 + t] = static_cast<uint32_t>(t | (L << 8));
   }
-  for (int e = threadIdx.x; e < (1 << maxlen); e += kThreads) {
+  __syncthreads();
+  for (int e = t; e < (1 << maxlen); e += kThreads) {
     int v = 0;
 #pragma unroll
-    for (int s = 0; s < 16; ++s)
-      if (L[s] > 0 && (static_cast<uint32_t>(e) >> (maxlen - L[s])) == code[s]) v = s | (L[s] << 8);
+    for (int u = 0; u < 16; ++u)
+      if (static_cast<uint32_t>(e) - s_first[u] < s_first[16 + u]) v = static_cast<int>(s_first[32 + u]);
     lut[e] = v;
   }
 }
@@ -111,6 +115,7 @@ template <bool kQw, XKind kX>
 __global__ void __launch_bounds__(kThreads) fused_matmul_kernel(Args a) {
   __shared__ __attribute__((aligned(16))) uint8_t s_tile[kSmemTile];
   __shared__ int32_t s_lut[1 << kLutBits];
+  __shared__ uint32_t s_first[48];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int m0 = blockIdx.x * kTM;
   const int B = a.B, M = a.M, K = a.K;
@@ -121,7 +126,7 @@ __global__ void __launch_bounds__(kThreads) fused_matmul_kernel(Args a) {
   int maxlen = a.maxlen;
   if constexpr (kQw) {
     maxlen = CF_QW_MAX_CODE_LENGTH;
-    build_band_lut(a.code_len + (m0 / CF_QW_BAND_ROWS) * 16, maxlen, s_lut);
+    build_band_lut(a.code_len + (m0 / CF_QW_BAND_ROWS) * 16, maxlen, s_lut, s_first);
     lut = s_lut;
   } else if (a.maxlen <= kLutBits) {
     for (int e = t; e < (1 << a.maxlen); e += kThreads) s_lut[e] = a.lut[e];
@@ -137,25 +142,35 @@ __global__ void __launch_bounds__(kThreads) fused_matmul_kernel(Args a) {
     for (int kc0 = 0; kc0 < K; kc0 += kKC) {
       const int kc1 = min(K, kc0 + kKC);
       __syncthreads();  // previous chunk (or the LUT build) done
-      {  // decode: lane -> (row r, 64-column segment s) of the chunk
+      {  // decode: lane -> (row r, 64-column segment s) of the chunk; 4 symbols per LDS word write
         const int r = t >> 6, s = t & 63;
         const int m = m0 + r, k0 = kc0 + 64 * s;
-        uint8_t *dst = s_tile + r * kLdB + 64 * s;
+        uint32_t *dst = reinterpret_cast<uint32_t *>(s_tile + r * kLdB + kSegB * s);
         const int n = (m < M && k0 < kc1) ? min(64, kc1 - k0) : 0;
-        if constexpr (kQw) {
-          if (n > 0) {
-            cfh::BitReader br(a.words, static_cast<int64_t>(a.seg_off[static_cast<int64_t>(m) * nseg + k0 / 64]));
-            for (int j = 0; j < n; ++j) dst[j] = static_cast<uint8_t>(br.decode(lut, maxlen) & 0xff);
+        const uint32_t pad = static_cast<uint32_t>(zc) * 0x01010101u;  // padding contributes q - zc = 0
+        auto emit = [&](auto &br) {
+#pragma unroll 4
+          for (int q = 0; q < 16; ++q) {
+            uint32_t w = pad;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (4 * q + e < n) w = (w & ~(0xFFu << (8 * e))) | ((br.decode(lut, maxlen) & 0xFFu) << (8 * e));
+            dst[q] = w;
           }
-        } else if (n > 0) {
+        };
+        if constexpr (kQw) {
+          cfh::BitReader br(a.words, n > 0 ? static_cast<int64_t>(a.seg_off[static_cast<int64_t>(m) * nseg + k0 / 64])
+                                           : 0);
+          emit(br);
+        } else {
           // reference stream: skip-decode from the start of the code block holding W[m, k0]
           const int64_t f = static_cast<int64_t>(m) * K + k0;
-          const int64_t bs = f / a.block;
+          const int64_t bs = n > 0 ? f / a.block : 0;
           cfh::BitReader br(a.words, static_cast<int64_t>(a.block_off[bs]));
-          for (int64_t i = bs * a.block; i < f; ++i) br.decode(lut, maxlen);
-          for (int j = 0; j < n; ++j) dst[j] = static_cast<uint8_t>(br.decode(lut, maxlen) & 0xff);
+          if (n > 0)
+            for (int64_t i = bs * a.block; i < f; ++i) br.decode(lut, maxlen);
+          emit(br);
         }
-        for (int j = n; j < 64; ++j) dst[j] = static_cast<uint8_t>(zc);  // padding contributes q - zc = 0
       }
       __syncthreads();
       // MFMA: wave takes k-steps wave, wave + 16, ...; lane's B fragment = rows (lane & 15), k = 4 * (lane >> 4)
@@ -163,7 +178,7 @@ __global__ void __launch_bounds__(kThreads) fused_matmul_kernel(Args a) {
       const int bn = lane & 15, bk = 4 * (lane >> 4);
       for (int st = wave; st < nsteps; st += kWaves) {
         const int kk = st * 16 + bk;  // column within the chunk
-        const uint32_t q4 = *reinterpret_cast<const uint32_t *>(s_tile + bn * kLdB + kk);
+        const uint32_t q4 = *reinterpret_cast<const uint32_t *>(s_tile + bn * kLdB + (kk >> 6) * kSegB + (kk & 63));
         bf16x4_t bfrag;
         bfrag[0] = bf16_of_int(static_cast<int>(q4 & 0xff) - zc);
         bfrag[1] = bf16_of_int(static_cast<int>((q4 >> 8) & 0xff) - zc);

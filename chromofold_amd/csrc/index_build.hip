@@ -241,11 +241,18 @@ __global__ void msb_kernel(const uint32_t *__restrict__ wbase, int32_t nw, int32
   msb[j] = static_cast<int32_t>(wbase[min(j * 8, nw)]);
 }
 
-__global__ void count_kernel(const int32_t *__restrict__ s, int32_t n, int32_t sigma, uint32_t *__restrict__ cnt) {
+// C[c] = number of text symbols < c = the first suffix-array row whose suffix starts with a symbol >= c (rows are
+// sorted by first symbol). Row i writes C[c] for every c in (first[i-1], first[i]]; the last row also fills up to
+// sigma - 1. No histogram, no atomics (a Zipf text makes per-symbol atomic counters contend heavily).
+__global__ void c_table_kernel(const int32_t *__restrict__ s, const int32_t *__restrict__ sa, int32_t n, int32_t sigma,
+                               int32_t *__restrict__ C) {
   const int i = blockIdx.x * kThreads + threadIdx.x;
   if (i >= n) return;
-  const int c = s[i];
-  if (c >= 0 && c < sigma) atomicAdd(cnt + c, 1u);
+  const int f = s[sa[i]];
+  const int prev = i == 0 ? -1 : s[sa[i - 1]];
+  for (int c = prev + 1; c <= f && c < sigma; ++c) C[c] = i;
+  if (i == n - 1)
+    for (int c = f + 1; c < sigma; ++c) C[c] = n;
 }
 
 }  // namespace
@@ -386,17 +393,11 @@ extern "C" cf_status cf_fm_build_aux(const int32_t *s, const int32_t *sa, int32_
   uint8_t *w = static_cast<uint8_t *>(ws);
   uint32_t *wcount = reinterpret_cast<uint32_t *>(w);
   uint32_t *wbase = reinterpret_cast<uint32_t *>(w + align256(4 * (static_cast<size_t>(nw) + 1)));
-  uint32_t *cnt = reinterpret_cast<uint32_t *>(w + 2 * align256(4 * (static_cast<size_t>(nw) + 1)));
   uint8_t *tmp = w + 2 * align256(4 * (static_cast<size_t>(nw) + 1)) + align256(4ull * sigma);
   const unsigned gn = cfd::grid_for(n, kThreads);
   bwt_kernel<<<gn, kThreads, 0, st>>>(s, sa, n, bwt);
-  // C[c] = number of text symbols < c (the BWT is a permutation of the text)
-  fill_u32<<<cfd::grid_for(sigma, kThreads), kThreads, 0, st>>>(cnt, sigma, 0u);
-  count_kernel<<<gn, kThreads, 0, st>>>(s, n, sigma, cnt);
+  c_table_kernel<<<gn, kThreads, 0, st>>>(s, sa, n, sigma, C);
   size_t tb = 0;
-  hipcub::DeviceScan::ExclusiveSum(nullptr, tb, cnt, reinterpret_cast<uint32_t *>(C), sigma, st);
-  if (hipcub::DeviceScan::ExclusiveSum(tmp, tb, cnt, reinterpret_cast<uint32_t *>(C), sigma, st) != hipSuccess)
-    return CF_ERR_CUDA;
   marks_kernel<<<cfd::grid_for(nw, kThreads), kThreads, 0, st>>>(sa, n, sa_sample, mwords, wcount);
   fill_u32<<<1, 1, 0, st>>>(wcount + nw, 1, 0u);
   hipcub::DeviceScan::ExclusiveSum(nullptr, tb, wcount, wbase, nw + 1, st);
