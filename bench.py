@@ -29,7 +29,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the dominant kernel, from rocprofv3 FETCH_SIZE + WRITE_SIZE runs calibrated on a copy of
 # known size (profiles/kv_batched_c4_32k.md): only quoted for the workload shape it was measured on.
-MEASURED_TRAFFIC = {("kv", 32768, 32): 2.139e9}
+MEASURED_TRAFFIC = {("kv", 32768, 32): 2.092e9}
 METRIC = "compressed-KV attn decode tokens/s + HBM GB/s fraction; wavelet rank Mq/s"
 
 
@@ -287,6 +287,71 @@ def bench_kv(steps: int, warmup: int, context: int = 32768, batch: int = 32, cod
     return res
 
 
+# ------------------------------------------------------------------------------------------------ device sealing
+def bench_seal(steps: int, warmup: int, cpu: bool = True, seqs: int = 32, tokens: int = 4096) -> dict:
+    """Sealing on the device (cf_kv_encode_groups_async): the C4 shape's prompt KV (32 sequences x 4096 tokens x 8
+    KV heads, hd 128, fp32, already in HBM) quantised and rANS-coded into one pool per call. Gate: the first 64
+    groups' bytes and offsets equal the host encoder's on the same pages. CPU baseline: the host encoder
+    (cf_kv_encode_groups, all host threads) on a 2048-group sample."""
+    import torch
+    from chromofold_amd import _abi as A
+    from chromofold_amd import kv, synth
+
+    H, D = 8, 128
+    pages = seqs * H * tokens // 16
+    ngroups = pages // 4
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(synth.SEED_C4 + 7)
+    K = torch.randn((pages, 16, D), generator=gen, device="cuda:0", dtype=torch.float32)
+    V = torch.randn((pages, 16, D), generator=gen, device="cuda:0", dtype=torch.float32)
+    Ks = K[:256].cpu().numpy()
+    Vs = V[:256].cpu().numpy()
+    tables = np.concatenate([t for h in range(H) for t in (kv.build_table(Ks[32 * h:32 * h + 32]),
+                                                           kv.build_table(Vs[32 * h:32 * h + 32]))])
+    first = np.arange(ngroups, dtype=np.int64) * 4
+    heads = ((np.arange(ngroups) // (tokens // 64)) % H).astype(np.int32)
+    d_first = torch.from_numpy(first).to("cuda:0")
+    d_counts = torch.full((ngroups,), 4, dtype=torch.int32, device="cuda:0")
+    d_heads = torch.from_numpy(heads).to("cuda:0")
+    d_tab = torch.from_numpy(tables).to("cuda:0")
+    cap = ngroups * int(A.lib().cf_kv_group_blob_max_bytes(kv.CODEC_RANS_HYBRID, D))
+    pool = torch.empty(cap, dtype=torch.uint8, device="cuda:0")
+    ws = torch.empty(int(A.lib().cf_kv_encode_groups_workspace_bytes(kv.CODEC_RANS_HYBRID, D, ngroups, 2 * H)),
+                     dtype=torch.uint8, device="cuda:0")
+
+    def seal():
+        return kv.encode_groups_device(kv.CODEC_RANS_HYBRID, K, V, D, d_tab, d_first, d_counts, pool, 0, d_heads,
+                                       None, ws)
+
+    r = seal()
+    torch.cuda.synchronize()
+    assert int(r.status.item()) == 0
+    end = int(r.pool_end.item())
+    n_chk = 64
+    host, hoff = kv.encode_groups(kv.CODEC_RANS_HYBRID, Ks, Vs, D, tables, first[:n_chk], np.full(n_chk, 4),
+                                  heads[:n_chk].astype(np.uint32))
+    assert np.array_equal(r.offsets[:n_chk].cpu().numpy().view(np.uint32), hoff), "device offsets != host"
+    assert np.array_equal(pool[:host.size].cpu().numpy(), host), "device-sealed bytes != host encoder bytes"
+    wall, per = _events_time(seal, steps, warmup)
+    t = float(np.mean(per)) * 1e-3
+    in_bytes = 2 * K.numel() * 4
+    res = {"workload": f"{seqs} seqs x {tokens} tokens x {H} KV heads, hd {D}: {ngroups} groups per call",
+           "ms_per_call": t * 1e3, "groups_per_s": ngroups / t, "tokens_per_s": seqs * tokens / t,
+           "fp32_in_gbs": in_bytes / t / 1e9, "pool_bytes": end,
+           "hbm_frac": (in_bytes + end) / t / 1e9 / HBM_PEAK_GBS}
+    if cpu:
+        n = 2048
+        Kh, Vh = K[:4 * n].cpu().numpy(), V[:4 * n].cpu().numpy()
+        th = min(16, os.cpu_count() or 1)  # the box's CPU share for one GPU
+        t0 = time.perf_counter()
+        kv.encode_groups(kv.CODEC_RANS_HYBRID, Kh, Vh, D, tables, first[:n], np.full(n, 4),
+                         heads[:n].astype(np.uint32), threads=th)
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": n / dt, "unit": "groups/s", "cores": th, "kind": "port",
+                               "sample": f"{n} groups with the library's host encoder on {th} threads"}
+    return res
+
+
 # ------------------------------------------------------------------------------------------------ long context (C5)
 def bench_c5(steps: int, warmup: int) -> dict:
     """C4 shapes (8 KV / 32 q heads, hd 128, rANS-hybrid pages). (a) 256 sequences sharing one 8192-token prefix
@@ -384,7 +449,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="auto", choices=["auto", "kv", "rrr", "copy", "c5"])
+    ap.add_argument("--workload", default="auto", choices=["auto", "kv", "rrr", "copy", "c5", "seal"])
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -401,6 +466,9 @@ def main() -> int:
                           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
                           "data": "synthetic", "config": {"workload": f"torch copy_ of {cp['copy_bytes']} B"}}))
         return 0
+    if args.workload == "seal":
+        print(json.dumps({"device_seal": bench_seal(args.steps, args.warmup, cpu=not args.no_cpu)}))
+        return 0
     if args.workload == "c5":
         print(json.dumps({"c5": bench_c5(args.steps, args.warmup)}))
         return 0
@@ -416,6 +484,7 @@ def main() -> int:
         secondary["c2_fm"] = bench_fm(min(args.steps, 20), 2, cpu=not args.no_cpu)
         secondary["c3_matmul"] = bench_qw(min(args.steps, 50), 3)
         secondary["c5_long_context"] = bench_c5(min(args.steps, 20), 2)
+        secondary["device_seal"] = bench_seal(min(args.steps, 20), 2, cpu=not args.no_cpu)
         cp = bench_copy(10, 2)
         secondary["stream_copy_gbs"] = cp["stream_copy_gbs"]
         secondary["roofline_frac_of_stream_copy"] = kvr["roofline"]["achieved"] / cp["stream_copy_gbs"]

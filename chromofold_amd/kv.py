@@ -5,8 +5,9 @@ Two entry points are mirrored:
     device pool, per-(sequence, head) page tables, split-context workspace) — the benchmark path;
   * the legacy single-sequence seam cf_kv_paged_attention_async of include/chromofold/kv_cuda.h (see legacy.py).
 
-Encoding happens on the host through the library's C encoder (cf_kv_encode_groups); pools, page tables, queries
-and outputs live in HBM as torch tensors. Every launch goes through libchromofold.so.
+Encoding happens either on the host through the library's C encoder (cf_kv_encode_groups) or on the device
+(cf_kv_encode_groups_async, the same bytes); pools, page tables, queries and outputs live in HBM as torch tensors.
+Every launch goes through libchromofold.so.
 """
 from __future__ import annotations
 
@@ -43,6 +44,9 @@ A.declare("cf_kv_group_blob_max_bytes", A.U64, [A.U32, A.U32])
 A.declare("cf_kv_batched_workspace_bytes", A.U64, [A.P])
 A.declare("cf_kv_validate_batched_desc", A.I32, [A.P])
 A.declare("cf_kv_paged_attention_batched_async", A.I32, [A.P, A.P])
+A.declare("cf_kv_encode_groups_workspace_bytes", A.U64, [A.U32, A.U32, A.U64, A.U32])
+A.declare("cf_kv_encode_groups_async", A.I32, [A.U32, A.P, A.P, A.U64, A.P, A.P, A.P, A.U32, A.P, A.U32, A.P, A.P,
+                                               A.U64, A.U64, A.P, A.P, A.P, A.P, A.U64, A.P])
 
 
 def _np_ptr(a: np.ndarray | None):
@@ -82,6 +86,46 @@ def encode_groups(codec: int, keys: np.ndarray, values: np.ndarray, head_dim: in
                                _np_ptr(offs), C.byref(end), threads)
     A.check(st, "cf_kv_encode_groups")
     return pool[:end.value], offs
+
+
+def _dptr(t):
+    return None if t is None else t.data_ptr()
+
+
+@dataclass
+class DeviceEncodeResult:
+    offsets: torch.Tensor    # [ngroups] int32 view of the u32 pool offsets / 16
+    pool_end: torch.Tensor   # [1] int64 (u64 first free byte)
+    status: torch.Tensor     # [1] int32 (cf_status of the device-side outcome)
+
+
+def encode_groups_device(codec: int, keys: torch.Tensor, values: torch.Tensor, head_dim: int,
+                         tables: torch.Tensor | None, first_page: torch.Tensor, page_counts: torch.Tensor,
+                         pool: torch.Tensor, pool_at: int = 0, heads: torch.Tensor | None = None,
+                         token_counts: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                         stream=None) -> DeviceEncodeResult:
+    """cf_kv_encode_groups_async on device tensors: keys/values fp32 [n_pages, 16, D], first_page int64,
+    page_counts/heads/token_counts int32 (u32 bit patterns), tables uint8 (table blobs), pool uint8. Asynchronous:
+    read `status` after the stream has run. The workspace is allocated here when not given (the C entry point
+    itself allocates nothing)."""
+    L = A.lib()
+    n = first_page.numel()
+    tcount = 0 if tables is None else tables.numel() // TABLE_BYTES
+    ws_bytes = int(L.cf_kv_encode_groups_workspace_bytes(codec, head_dim, n, tcount))
+    if ws_bytes == 0:
+        raise A.CfError(A.CF_ERR_INVALID_ARGUMENT, "cf_kv_encode_groups_workspace_bytes")
+    if workspace is None or workspace.numel() < ws_bytes:
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=pool.device)
+    offs = torch.empty(n, dtype=torch.int32, device=pool.device)
+    end = torch.zeros(1, dtype=torch.int64, device=pool.device)
+    status = torch.full((1,), -1, dtype=torch.int32, device=pool.device)
+    s = (stream if stream is not None else torch.cuda.current_stream()).cuda_stream
+    st = L.cf_kv_encode_groups_async(codec, keys.data_ptr(), values.data_ptr(), n, first_page.data_ptr(),
+                                     page_counts.data_ptr(), _dptr(token_counts), head_dim, _dptr(tables), tcount,
+                                     _dptr(heads), pool.data_ptr(), pool.numel(), pool_at, offs.data_ptr(),
+                                     end.data_ptr(), status.data_ptr(), workspace.data_ptr(), workspace.numel(), s)
+    A.check(st, "cf_kv_encode_groups_async")
+    return DeviceEncodeResult(offs, end, status)
 
 
 @dataclass
@@ -141,16 +185,50 @@ class BatchedKv:
         A.check(A.lib().cf_kv_paged_attention_batched_async(C.byref(d), s), "cf_kv_paged_attention_batched_async")
 
 
+def seal_device(codec: int, keys: torch.Tensor, values: torch.Tensor, tables: torch.Tensor | None,
+                stream=None) -> BatchedKv:
+    """Seal dense device K/V [seq_count, kv_heads, T, D] fp32 (T a multiple of 16, every sequence T tokens long)
+    into a device pool with cf_kv_encode_groups_async, without a host round trip of the values. Group g of
+    (sequence s, head h) holds pages 4g..4g+3 of that (s, h). Synchronises once to read the pool end and status."""
+    S, H, T, D = keys.shape
+    assert values.shape == keys.shape and T % PAGE_TOKENS == 0 and keys.is_contiguous() and values.is_contiguous()
+    dev = keys.device
+    npg = T // PAGE_TOKENS
+    ngr = (npg + GROUP_PAGES - 1) // GROUP_PAGES
+    g = torch.arange(S * H * ngr, device=dev, dtype=torch.int64)
+    gl = g % ngr
+    first = (g // ngr) * npg + gl * GROUP_PAGES
+    counts = torch.clamp(npg - gl * GROUP_PAGES, max=GROUP_PAGES).to(torch.int32)
+    heads = ((g // ngr) % H).to(torch.int32)
+    cap = int(A.lib().cf_kv_group_blob_max_bytes(codec, D)) * S * H * ngr
+    pool = torch.empty(cap, dtype=torch.uint8, device=dev)
+    r = encode_groups_device(codec, keys.view(-1, PAGE_TOKENS, D), values.view(-1, PAGE_TOKENS, D), D, tables, first,
+                             counts, pool, 0, heads, None, None, stream)
+    st, end = int(r.status.item()), int(r.pool_end.item())
+    if st != 0:
+        raise A.CfError(st, "cf_kv_encode_groups_async (device status)")
+    t_tok = torch.full((S,), T, dtype=torch.int32, device=dev)
+    return BatchedKv(codec, S, H, D, ngr, pool[:end], r.offsets.view(S, H, ngr), t_tok, tables)
+
+
 def build_batched(codec: int, kv_source, seq_count: int, kv_heads: int, seq_tokens: np.ndarray, head_dim: int,
                   tables: np.ndarray | None, device="cuda", keep_host: bool = False,
-                  shared: dict | None = None) -> BatchedKv:
+                  shared: dict | None = None, encoder: str = "host") -> BatchedKv:
     """Encode and upload page groups. kv_source(s) -> (K, V) fp32 arrays [kv_heads, T_s, D] for sequence s.
     `shared` optionally maps sequence s -> (donor sequence, prefix groups): the first `prefix groups` groups of s are
-    the donor's blobs (no copy), modelling refcounted shared-prefix pages."""
+    the donor's blobs (no copy), modelling refcounted shared-prefix pages. encoder="device" uploads the fp32 pages
+    and seals them with cf_kv_encode_groups_async straight into the device pool (same bytes as the host encoder)."""
     seq_tokens = np.asarray(seq_tokens, np.uint32)
     max_groups = int((seq_tokens.max() + GROUP_TOKENS - 1) // GROUP_TOKENS)
     offsets = np.zeros((seq_count, kv_heads, max_groups), np.uint32)
     blobs, at = [], 0
+    on_device = encoder == "device"
+    if on_device:
+        L = A.lib()
+        cap = int(L.cf_kv_group_blob_max_bytes(codec, head_dim))
+        groups = int(sum(kv_heads * ((int(t) + GROUP_TOKENS - 1) // GROUP_TOKENS) for t in seq_tokens))
+        dpool = torch.empty(groups * cap + 16, dtype=torch.uint8, device=device)
+        d_tab = None if tables is None else torch.from_numpy(np.ascontiguousarray(tables).ravel()).to(device)
     for s in range(seq_count):
         T = int(seq_tokens[s])
         npg = (T + PAGE_TOKENS - 1) // PAGE_TOKENS
@@ -178,13 +256,28 @@ def build_batched(codec: int, kv_source, seq_count: int, kv_heads: int, seq_toke
         page_counts = np.broadcast_to(np.minimum(GROUP_PAGES, npg - gl * GROUP_PAGES)[None, :],
                                       (kv_heads, gl.size)).ravel()
         heads = np.repeat(np.arange(kv_heads, dtype=np.uint32), gl.size)
+        if on_device:
+            r = encode_groups_device(codec, torch.from_numpy(Kp).to(device), torch.from_numpy(Vp).to(device),
+                                     head_dim, d_tab, torch.from_numpy(first_page.astype(np.int64)).to(device),
+                                     torch.from_numpy(page_counts.astype(np.int32)).to(device), dpool, at,
+                                     torch.from_numpy(heads.view(np.int32)).to(device),
+                                     torch.from_numpy(tc.ravel().view(np.int32)).to(device))
+            if int(r.status.item()) != 0:
+                raise A.CfError(int(r.status.item()), "cf_kv_encode_groups_async (device status)")
+            offsets[s, :, first:ngr] = r.offsets.cpu().numpy().view(np.uint32).reshape(kv_heads, gl.size)
+            at = int(r.pool_end.item())
+            continue
         blob, offs = encode_groups(codec, Kp, Vp, head_dim, tables, first_page, page_counts, heads, tc.ravel())
         offsets[s, :, first:ngr] = (offs + at // 16).reshape(kv_heads, gl.size)
         blobs.append(blob)
         at += blob.size
-    host_pool = np.concatenate(blobs) if blobs else np.zeros(16, np.uint8)
     assert at // 16 < 2 ** 32
-    pool = torch.from_numpy(host_pool).to(device)
+    if on_device:
+        pool = dpool[:max(at, 16)]
+        host_pool = pool.cpu().numpy() if keep_host else None
+    else:
+        host_pool = np.concatenate(blobs) if blobs else np.zeros(16, np.uint8)
+        pool = torch.from_numpy(host_pool).to(device)
     t_off = torch.from_numpy(offsets.view(np.int32)).to(device)
     t_tok = torch.from_numpy(seq_tokens.view(np.int32)).to(device)
     t_tab = None if tables is None else torch.from_numpy(np.ascontiguousarray(tables).ravel()).to(device)

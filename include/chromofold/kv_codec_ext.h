@@ -164,6 +164,28 @@ cf_status cf_kv_encode_groups(uint32_t codec, const float *keys, const float *va
                               uint64_t pool_capacity, uint64_t pool_at, uint32_t *offsets_out, uint64_t *pool_end,
                               uint32_t threads);
 
+/* ---- device-side page encoder (sealing on the GPU) --------------------------------------------------------- */
+
+/* Device twin of cf_kv_encode_groups: the same groups quantised and encoded on the GPU, producing the same blobs
+ * at the same pool offsets, byte for byte (no counterpart in the reference, whose pages are always sealed on the
+ * host: src/runtime/compressed_kv_cache.cu:89-109). Every array argument is DEVICE memory: keys/values (page-major
+ * [*][16][head_dim] fp32, 16-byte aligned), first_page/page_counts/heads [ngroups], token_counts per page (NULL:
+ * all 16), tables = table_count table blobs (RANS_HYBRID), pool (16-byte aligned), offsets_out [ngroups],
+ * *pool_end, *status, workspace. Asynchronous on `stream`; allocates nothing and never synchronises.
+ * Synchronous return: argument errors only. Device-side outcome in *status once the stream has run: CF_OK, or
+ * CF_ERR_INVALID_ARGUMENT when a group has a bad page/token count or table pair (heads[i] must satisfy
+ * 2 * heads[i] + 1 < table_count and both tables must be valid) or the blobs do not fit pool_capacity — in those
+ * cases nothing is written to pool, offsets_out or *pool_end. */
+uint64_t cf_kv_encode_groups_workspace_bytes(uint32_t codec, uint32_t head_dim, uint64_t ngroups,
+                                             uint32_t table_count);
+cf_status cf_kv_encode_groups_async(uint32_t codec, const float *keys, const float *values, uint64_t ngroups,
+                                    const uint64_t *first_page, const uint32_t *page_counts,
+                                    const uint32_t *token_counts, uint32_t head_dim, const uint8_t *tables,
+                                    uint32_t table_count, const uint32_t *heads, uint8_t *pool,
+                                    uint64_t pool_capacity, uint64_t pool_at, uint32_t *offsets_out,
+                                    uint64_t *pool_end, uint32_t *status, void *workspace, uint64_t workspace_bytes,
+                                    void *stream);
+
 /* Host encoder of the reference's fixed-width page format (the format cf_kv_paged_attention_async decodes with
  * fixed_code_length = bits): K per-channel and V per-token scales max|x| / (2^(bits-1) - 1) (1.0 when all zero),
  * sym = clamp(lrint(x / s), -2^(bits-1), 2^(bits-1) - 1) + 2^(bits-1), codes packed MSB-first, one block offset

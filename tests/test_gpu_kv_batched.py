@@ -105,3 +105,48 @@ def test_batched_rejects_bad_desc(dev):
         bad = kv.cf_kv_batched_desc.from_buffer_copy(d)
         setattr(bad, field, val)
         assert L.cf_kv_paged_attention_batched_async(C.byref(bad), None) == st, field
+
+
+def test_batched_full_c4_32k_every_sequence_torch_reference(dev):
+    """BASELINE's full C4 shape — 32 sequences x 32768 tokens, 8 KV / 32 q heads, hd 128 — sealed on the device,
+    then EVERY output row against an independent float64 torch reference over the dequantised values (quantised
+    here with torch: per-page absmax / 127, IEEE division, round half to even). Covers every group of every
+    (sequence, head) at the benchmark's real size. Bar: max abs error <= 1e-3 x max |ref| per sequence."""
+    import torch
+    from chromofold_amd import kv
+    S, T, H, QH, D = 32, 32768, 8, 32, 128
+    gqa = QH // H
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0xC4)
+    K = torch.randn((S, H, T, D), generator=gen, device=dev)
+    V = torch.randn((S, H, T, D), generator=gen, device=dev)
+    Kh = K[0, 0, :512].cpu().numpy().reshape(-1, 16, D)
+    Vh = V[0, 0, :512].cpu().numpy().reshape(-1, 16, D)
+    tables = torch.from_numpy(np.concatenate([t for _ in range(H) for t in (kv.build_table(Kh), kv.build_table(Vh))]))
+    kvb = kv.seal_device(kv.CODEC_RANS_HYBRID, K, V, tables.to(dev))
+    q = torch.randn((S, QH, D), generator=gen, device=dev)
+    qp = torch.full((S,), T - 1, dtype=torch.int32, device=dev)
+    out = torch.full_like(q, float("nan"))
+    sc = 1.0 / np.sqrt(D)
+    kvb.attention(q, out, qp, sc)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+
+    def deq(x):  # [T, D] -> dequantised float64
+        p = x.view(-1, 16, D)
+        m = p.abs().amax(dim=(1, 2), keepdim=True)
+        s = torch.where(m == 0, torch.ones_like(m), m / 127.0)
+        return (torch.clamp(torch.round(p / s), -128, 127) * s).view(T, D).double()
+
+    worst = 0.0
+    for s in range(S):
+        ref = torch.empty((QH, D), dtype=torch.float64, device=dev)
+        for h in range(H):
+            kd, vd = deq(K[s, h]), deq(V[s, h])
+            qs = q[s, h * gqa:(h + 1) * gqa].double()
+            p = torch.softmax((qs @ kd.T) * sc, dim=-1)
+            ref[h * gqa:(h + 1) * gqa] = p @ vd
+        err = float((out[s].double() - ref).abs().max() / ref.abs().max())
+        worst = max(worst, err)
+        assert err <= 1e-3, (s, err)
+    print(f"full C4 32k: worst normwise error over 32 sequences {worst:.3e}")

@@ -113,3 +113,24 @@ def test_table_every_symbol_codable(kv):
     ks, vs, *_ = O.kv_decode_group(blob, tt, 0, 64)
     assert np.array_equal(ks[0], O.kv_quantize_absmax(K[0])[0])
     assert np.array_equal(ks[1], O.kv_quantize_absmax(K[1])[0])
+
+
+def test_device_encoder_rejects_bad_arguments_before_any_device_call(kv):
+    """cf_kv_encode_groups_async checks its arguments on the host (no device is touched, so this runs without a
+    GPU): NULLs, misaligned K/V or pool pointers, a misaligned pool_at, a bad head_dim or codec, a RANS call without
+    tables, and a workspace smaller than cf_kv_encode_groups_workspace_bytes."""
+    L = kv.A.lib()
+    f = L.cf_kv_encode_groups_async
+    ws = int(L.cf_kv_encode_groups_workspace_bytes(2, 128, 4, 2))
+    assert ws > 4 * int(L.cf_kv_group_blob_max_bytes(2, 128))
+    assert L.cf_kv_encode_groups_workspace_bytes(2, 20, 4, 2) == 0
+    assert L.cf_kv_encode_groups_workspace_bytes(3, 128, 4, 2) == 0
+    A = 1 << 20  # a fake, aligned address: never dereferenced because every call below fails validation
+
+    def call(codec=2, keys=A, values=A, n=4, D=128, tables=A, tcount=2, pool=A, pool_at=0, ws_bytes=ws):
+        return f(codec, keys, values, n, A, A, None, D, tables, tcount, None, pool, 1 << 30, pool_at, A, A, A, A,
+                 ws_bytes, None)
+
+    assert call(keys=None) == 1 and call(values=A + 8) == 1 and call(pool=A + 4) == 1 and call(pool_at=8) == 1
+    assert call(n=0) == 1 and call(tables=None) == 1 and call(tcount=1) == 1 and call(ws_bytes=ws - 1) == 1
+    assert call(D=20) == 2 and call(D=256) == 2 and call(codec=7) == 2
