@@ -98,9 +98,40 @@ __device__ __forceinline__ uint32_t rans_step(const uint2 *__restrict__ tab, uin
   return e.y;
 }
 
+// The same step split in three so that the four chains of a lane overlap their LDS round trips: the slot entry
+// lookups of all chains are issued first, then the state updates with their renormalisation-word fetches, then
+// the word merges.
+__device__ __forceinline__ uint2 rans_lookup(const uint2 *__restrict__ tab, uint32_t x) {
+  return tab[x & (kSlots - 1)];
+}
+
+template <typename WordPtr>
+__device__ __forceinline__ uint32_t rans_advance(uint32_t ex, uint32_t &x, WordPtr &wbase, uint32_t &sel) {
+  const uint32_t xs = x >> CF_KV_RANS_PROB_BITS;
+  uint32_t fx;
+  asm("v_mul_u32_u24_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD"
+      : "=v"(fx) : "v"(ex), "v"(xs));
+  asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:DWORD"
+      : "=v"(x) : "v"(ex), "v"(fx));
+  const bool need = x < 65536u;
+  const uint64_t m = __builtin_amdgcn_ballot_w64(need);
+  const uint32_t idx = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+  const uint32_t w = wbase[idx];  // lanes that do not renormalise read a harmless in-bounds word
+  wbase += __builtin_popcountll(m);
+  sel = need ? 0x05040100u : 0x07060504u;  // (x << 16) | w  or  x
+  return w;
+}
+
 constexpr int kHdr = 64;                 // group header bytes
+constexpr int kStateBytes = 4 * 64 * 4;  // K A, K B, V A, V B lane states
 constexpr uint32_t kCapWords = CF_KV_RANS_MAX_GROUP_WORDS;  // K+V words staged in LDS per wavefront
 constexpr uint32_t kSlackWords = 64;     // reads past the last word by non-renormalising lanes stay in the buffer
+
+// rANS words of a group: the sum of its four chains' counts (header word_count[0..3] as two u32)
+__device__ __forceinline__ uint32_t word_total(uint32_t c01, uint32_t c23) {
+  return (c01 & 0xFFFFu) + (c01 >> 16) + (c23 & 0xFFFFu) + (c23 >> 16);
+}
 
 template <int D>
 constexpr int buf_u32() {
@@ -115,11 +146,15 @@ struct GroupCtx {
 };
 
 // Decode one page group (K scores, softmax, V accumulation) with the word streams read through `wk` (the wave's
-// LDS staging buffer). `pre` holds the group's first low-part words (prefetched); `after_decode` runs as soon as
-// the decode loop no longer needs the word buffer (the caller stages the next group there).
+// LDS staging buffer). `pre` always holds the NEXT low-part group's 6 words (3 K + 3 V): on entry the group's
+// first, and while low group g is decoded, group g + 1's (or, during the last one, the first low group of the next
+// RANS group at `nlw`, NULL if none) are in flight, a quarter of the group ahead of their use. `after_decode` runs as
+// soon as the decode loop no longer needs the word buffer (the caller stages the next group there).
 template <int D, int CODEC, typename WordPtr, typename Hook>
-__device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&pre)[6],
-                                           const uint8_t *__restrict__ blob, WordPtr wk, uint32_t kw,
+__device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&pre)[6], const uint32_t *nlw,
+                                           const uint32_t (&st4)[4],
+                                           const uint8_t *__restrict__ blob, WordPtr wk, uint32_t cnt01,
+                                           uint32_t cnt23,
                                            const uint2 (*__restrict__ s_tab)[kSlots], const half4_t *qhi,
                                            const half4_t *qlo, const float *qsum, _Float16 (*s_pw)[kGqa][16],
                                            int lane, bool tok_ok, float ks, float vs, float *m_run, float *l_run,
@@ -130,45 +165,79 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
   float4_t sa = {0, 0, 0, 0}, sb = {0, 0, 0, 0};
   uint32_t vb[NQ];
   {
-    const uint32_t *st = reinterpret_cast<const uint32_t *>(blob + kHdr);
-    const uint32_t *lowk = reinterpret_cast<const uint32_t *>(blob + kHdr + 512);
+    const uint32_t *lowk = reinterpret_cast<const uint32_t *>(blob + kHdr + kStateBytes);
     const uint32_t *raw = reinterpret_cast<const uint32_t *>(blob + kHdr);
-    uint32_t xk = RANS ? st[lane] : 0u, xv = RANS ? st[64 + lane] : 0u;
-    WordPtr wv = wk + kw;
+    // chain A = even quads, chain B = odd quads of each stream: four independent states per lane
+    // (loaded with the group's header, one group ahead)
+    uint32_t xk0 = st4[0], xk1 = st4[1], xv0 = st4[2], xv1 = st4[3];
+    // word cursors of the four chains (wave-uniform: scalar registers; their advance is scalar work)
+    const uint32_t c01 = __builtin_amdgcn_readfirstlane(cnt01), c23 = __builtin_amdgcn_readfirstlane(cnt23);
+    WordPtr wk0 = wk, wk1 = wk + (c01 & 0xFFFFu), wv0 = wk1 + (c01 >> 16), wv1 = wv0 + (c23 & 0xFFFFu);
     uint32_t kl[3] = {0, 0, 0}, vl[3] = {0, 0, 0};
-    [&]<int... Q>(std::integer_sequence<int, Q...>) {
-      (
-          [&] {
-            constexpr int q = Q, g = q / 4, qd = q % 4;
-            uint32_t kbytes, vbytes;
-            if constexpr (RANS) {
-              if constexpr (qd == 0) {
+    // K scores of quad q: the decoded symbol bytes go straight into the MFMA (B operand); V bytes wait in vb
+    auto consume = [&](auto qc, uint32_t kbytes, uint32_t vbytes) {
+      constexpr int q = decltype(qc)::value;
+      vb[q] = vbytes;
+      const half4_t bk = bytes_to_half4(kbytes);
+      sa = __builtin_amdgcn_mfma_f32_4x4x4f16(qhi[q / 16], bk, sa, 4, q % 16, 0);
+      sb = __builtin_amdgcn_mfma_f32_4x4x4f16(qlo[q / 16], bk, sb, 4, q % 16, 0);
+    };
+    if constexpr (RANS) {
+      // pair P = quads 2P (chain A) and 2P + 1 (chain B) of K and of V: four independent rANS steps
+      [&]<int... P>(std::integer_sequence<int, P...>) {
+        (
+            [&] {
+              constexpr int q0 = 2 * P, g = q0 / 4, qd0 = q0 % 4;
+              if constexpr (qd0 == 0) {  // low group g: take the prefetched words, start the next group's
 #pragma unroll
                 for (int w = 0; w < 3; ++w) {
-                  if constexpr (g == 0) {  // first low-part words arrive prefetched by the previous group
-                    kl[w] = pre[w];
-                    vl[w] = pre[3 + w];
-                  } else {
-                    kl[w] = lowk[(g * 3 + w) * 64 + lane];
-                    vl[w] = lowk[LOWS + (g * 3 + w) * 64 + lane];
+                  kl[w] = pre[w];
+                  vl[w] = pre[3 + w];
+                }
+                if constexpr (g + 1 < D / 16) {
+#pragma unroll
+                  for (int w = 0; w < 3; ++w) {
+                    pre[w] = lowk[((g + 1) * 3 + w) * 64 + lane];
+                    pre[3 + w] = lowk[LOWS + ((g + 1) * 3 + w) * 64 + lane];
+                  }
+                } else if (nlw) {
+#pragma unroll
+                  for (int w = 0; w < 3; ++w) {
+                    pre[w] = nlw[w * 64 + lane];
+                    pre[3 + w] = nlw[LOWS + w * 64 + lane];
                   }
                 }
               }
-              const uint32_t hk = rans_step(s_tab[0], xk, wk);
-              const uint32_t hv = rans_step(s_tab[1], xv, wv);
-              kbytes = quad_bytes<qd>(kl[0], kl[1], kl[2], hk);
-              vbytes = quad_bytes<qd>(vl[0], vl[1], vl[2], hv);
-            } else {
-              kbytes = raw[q * 64 + lane];
-              vbytes = raw[NQ * 64 + q * 64 + lane];
-            }
-            vb[q] = vbytes;
-            const half4_t bk = bytes_to_half4(kbytes);
-            sa = __builtin_amdgcn_mfma_f32_4x4x4f16(qhi[q / 16], bk, sa, 4, q % 16, 0);
-            sb = __builtin_amdgcn_mfma_f32_4x4x4f16(qlo[q / 16], bk, sb, 4, q % 16, 0);
-          }(),
-          ...);
-    }(std::make_integer_sequence<int, NQ>{});
+              const uint2 ek0 = rans_lookup(s_tab[0], xk0), ek1 = rans_lookup(s_tab[0], xk1);
+              const uint2 ev0 = rans_lookup(s_tab[1], xv0), ev1 = rans_lookup(s_tab[1], xv1);
+              uint32_t sk0, sk1, sv0, sv1;
+              const uint32_t wdk0 = rans_advance(ek0.x, xk0, wk0, sk0);
+              const uint32_t wdk1 = rans_advance(ek1.x, xk1, wk1, sk1);
+              const uint32_t wdv0 = rans_advance(ev0.x, xv0, wv0, sv0);
+              const uint32_t wdv1 = rans_advance(ev1.x, xv1, wv1, sv1);
+              xk0 = __builtin_amdgcn_perm(xk0, wdk0, sk0);
+              xk1 = __builtin_amdgcn_perm(xk1, wdk1, sk1);
+              xv0 = __builtin_amdgcn_perm(xv0, wdv0, sv0);
+              xv1 = __builtin_amdgcn_perm(xv1, wdv1, sv1);
+              consume(std::integral_constant<int, q0>{}, quad_bytes<qd0>(kl[0], kl[1], kl[2], ek0.y),
+                      quad_bytes<qd0>(vl[0], vl[1], vl[2], ev0.y));
+              consume(std::integral_constant<int, q0 + 1>{}, quad_bytes<qd0 + 1>(kl[0], kl[1], kl[2], ek1.y),
+                      quad_bytes<qd0 + 1>(vl[0], vl[1], vl[2], ev1.y));
+            }(),
+            ...);
+      }(std::make_integer_sequence<int, NQ / 2>{});
+    } else {
+      if (nlw) {  // a raw group: start the next RANS group's first low-part words now
+#pragma unroll
+        for (int w = 0; w < 3; ++w) {
+          pre[w] = nlw[w * 64 + lane];
+          pre[3 + w] = nlw[LOWS + w * 64 + lane];
+        }
+      }
+      [&]<int... Q>(std::integer_sequence<int, Q...>) {
+        (consume(std::integral_constant<int, Q>{}, raw[Q * 64 + lane], raw[NQ * 64 + Q * 64 + lane]), ...);
+      }(std::make_integer_sequence<int, NQ>{});
+    }
   }
   after_decode();  // the word buffer is free from here on
 
@@ -232,7 +301,8 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
   __shared__ _Float16 s_p[kWaves][4][kGqa][16];     // per wave: [page][head][token] probability * v_scale
   __shared__ uint32_t s_buf[kWaves][BUF];           // per wave: staged words; query staging and partials alias it
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int G = lane >> 4, t = lane & 15;
   const uint32_t split = blockIdx.x, head = blockIdx.y, seq = blockIdx.z;
   const uint32_t gqa = d.query_head_count / d.kv_head_count;
@@ -307,20 +377,25 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
   uint32_t *buf = s_buf[wave];
   // Memory pipeline of a wavefront over its groups gi = ga + wave, +4, ...:
   //   blob offset   loaded two groups ahead;
-  //   header        loaded at the start of the previous group (fields kept in registers);
+  //   header        loaded at the start of the previous group (fields and lane states kept in registers);
   //   word streams  copied into this wave's LDS buffer by global_load_lds (16 bytes per lane, 1 KiB per wave
   //                 instruction, whole 16-byte chunks: blobs are padded to 16 bytes) during the previous group's
   //                 softmax / V phase — the buffer is free once that group's decode loop has ended;
-  //   low parts     the first 6 words per lane prefetched together with the word streams.
+  //   low parts     rolling prefetch: the next low-part group's 6 words per lane are always in flight (issued
+  //                 when the previous low group starts; across the group boundary for the last one).
   // The next group's copies are awaited with s_waitcnt vmcnt(0) at the top of the loop.
   auto blob_at = [&](uint32_t g) { return d.pool + static_cast<size_t>(grow[g]) * 16; };
   uint32_t off_next = (ga + wave + kWaves < gb) ? grow[ga + wave + kWaves] : 0u;
   const uint8_t *blob = (ga + wave < gb) ? blob_at(ga + wave) : d.pool;
-  uint32_t h_cnt = 0, h_tc = 0, h_codec = 0;
+  uint32_t h_cnt01 = 0, h_cnt23 = 0, h_tc = 0, h_codec = 0;
+  uint32_t h_st[4] = {0, 0, 0, 0};  // the group's four lane states (read for raw groups too: harmless, unused)
   float h_ks = 0.f, h_vs = 0.f;
   if (ga + wave < gb) {
-    h_cnt = *reinterpret_cast<const uint32_t *>(blob + 4);
-    h_tc = reinterpret_cast<const uint16_t *>(blob + 8)[G];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) h_st[c] = reinterpret_cast<const uint32_t *>(blob + kHdr)[64 * c + lane];
+    h_cnt01 = *reinterpret_cast<const uint32_t *>(blob + 4);
+    h_cnt23 = *reinterpret_cast<const uint32_t *>(blob + 8);
+    h_tc = reinterpret_cast<const uint16_t *>(blob + 12)[G];
     h_ks = reinterpret_cast<const float *>(blob + 32)[G];
     h_vs = reinterpret_cast<const float *>(blob + 48)[G];
     h_codec = *reinterpret_cast<const uint32_t *>(blob);
@@ -329,29 +404,26 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
   uint32_t pre[6] = {0, 0, 0, 0, 0, 0};
   if (RANS && ga + wave < gb && h_codec == CF_KV_CODEC_RANS_HYBRID) {
     {
-      const uint32_t *lw = reinterpret_cast<const uint32_t *>(blob + kHdr + 512);
+      const uint32_t *lw = reinterpret_cast<const uint32_t *>(blob + kHdr + kStateBytes);
 #pragma unroll
       for (int w = 0; w < 3; ++w) {
         pre[w] = lw[w * 64 + lane];
         pre[3 + w] = lw[LOWS + w * 64 + lane];
       }
     }
-    const uint32_t nbytes = ((min((h_cnt & 0xFFFFu) + (h_cnt >> 16), kCapWords) * 2u) + 15u) & ~15u;
-    const uint8_t *src = blob + kHdr + 512 + 2 * LOWS * 4;
+    const uint32_t nbytes = ((min(word_total(h_cnt01, h_cnt23), kCapWords) * 2u) + 15u) & ~15u;
+    const uint8_t *src = blob + kHdr + kStateBytes + 2 * LOWS * 4 + 16u * lane;  // this lane's 16-byte chunk
 #pragma unroll
-    for (int k = 0; k < kStage16; ++k) {
-      const uint32_t at = 1024u * k + 16u * lane;
-      if (at < nbytes)
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t *>(src + at),
+    for (int k = 0; k < kStage16; ++k)
+      if (1024u * k + 16u * lane < nbytes)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t *>(src + 1024 * k),
                                          (__attribute__((address_space(3))) void *)(buf + 256 * k), 16,
                                          0, 0);
-    }
   }
   for (uint32_t gi = ga + wave; gi < gb; gi += kWaves) {
-    const uint32_t cnt = h_cnt, tcG = h_tc, gcodec = h_codec;  // gcodec is wave-uniform
+    const uint32_t cnt01 = h_cnt01, cnt23 = h_cnt23, tcG = h_tc, gcodec = h_codec;  // gcodec is wave-uniform
     const float ks = h_ks, vs = h_vs;
     const uint8_t *cur = blob;
-    const uint32_t kw = cnt & 0xFFFFu;
     const bool tok_ok = static_cast<uint32_t>(t) < tcG && 64 * gi + 16 * G + t < visible;
     if constexpr (RANS) {  // this group's copies (started during the previous group) have landed
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -359,42 +431,37 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    if (gi + kWaves < gb) {  // next group's header (its offset was loaded one group earlier)
+    const uint32_t st4[4] = {h_st[0], h_st[1], h_st[2], h_st[3]};
+    if (gi + kWaves < gb) {  // next group's header and states (its offset was loaded one group earlier)
       blob = d.pool + static_cast<size_t>(off_next) * 16;
-      h_cnt = *reinterpret_cast<const uint32_t *>(blob + 4);
-      h_tc = reinterpret_cast<const uint16_t *>(blob + 8)[G];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) h_st[c] = reinterpret_cast<const uint32_t *>(blob + kHdr)[64 * c + lane];
+      h_cnt01 = *reinterpret_cast<const uint32_t *>(blob + 4);
+      h_cnt23 = *reinterpret_cast<const uint32_t *>(blob + 8);
+      h_tc = reinterpret_cast<const uint16_t *>(blob + 12)[G];
       h_ks = reinterpret_cast<const float *>(blob + 32)[G];
       h_vs = reinterpret_cast<const float *>(blob + 48)[G];
       h_codec = *reinterpret_cast<const uint32_t *>(blob);
       off_next = (gi + 2 * kWaves < gb) ? grow[gi + 2 * kWaves] : 0u;
     }
     const bool next_rans = RANS && gi + kWaves < gb && h_codec == CF_KV_CODEC_RANS_HYBRID;
-    auto stage_next = [&]() {  // next group's first low words + word streams (no VGPRs for the streams)
+    const uint32_t *nlw = next_rans ? reinterpret_cast<const uint32_t *>(blob + kHdr + kStateBytes) : nullptr;
+    auto stage_next = [&]() {  // next group's word streams, straight into LDS (no VGPRs)
       if (!next_rans) return;
-      {
-        const uint32_t *lw = reinterpret_cast<const uint32_t *>(blob + kHdr + 512);
+      const uint32_t nbytes = ((min(word_total(h_cnt01, h_cnt23), kCapWords) * 2u) + 15u) & ~15u;
+      const uint8_t *src = blob + kHdr + kStateBytes + 2 * LOWS * 4 + 16u * lane;
 #pragma unroll
-        for (int w = 0; w < 3; ++w) {
-          pre[w] = lw[w * 64 + lane];
-          pre[3 + w] = lw[LOWS + w * 64 + lane];
-        }
-      }
-      const uint32_t nbytes = ((min((h_cnt & 0xFFFFu) + (h_cnt >> 16), kCapWords) * 2u) + 15u) & ~15u;
-      const uint8_t *src = blob + kHdr + 512 + 2 * LOWS * 4;
-#pragma unroll
-      for (int k = 0; k < kStage16; ++k) {
-        const uint32_t at = 1024u * k + 16u * lane;
-        if (at < nbytes)
-          __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t *>(src + at),
+      for (int k = 0; k < kStage16; ++k)
+        if (1024u * k + 16u * lane < nbytes)
+          __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t *>(src + 1024 * k),
                                            (__attribute__((address_space(3))) void *)(buf + 256 * k),
                                            16, 0, 0);
-      }
     };
     if (RANS && gcodec == CF_KV_CODEC_RANS_HYBRID) {
-      group_body<D, CF_KV_CODEC_RANS_HYBRID>(stage_next, pre, cur, reinterpret_cast<const uint16_t *>(buf), kw, s_tab, qhi,
+      group_body<D, CF_KV_CODEC_RANS_HYBRID>(stage_next, pre, nlw, st4, cur, reinterpret_cast<const uint16_t *>(buf), cnt01, cnt23, s_tab, qhi,
                                              qlo, qsum, s_p[wave], lane, tok_ok, ks, vs, m_run, l_run, corr, acc_v);
     } else {  // raw int8 group (the INT8 codec, or the raw fallback of a high-entropy group)
-      group_body<D, CF_KV_CODEC_INT8>(stage_next, pre, cur, static_cast<const uint16_t *>(nullptr), 0, s_tab, qhi, qlo,
+      group_body<D, CF_KV_CODEC_INT8>(stage_next, pre, nlw, st4, cur, static_cast<const uint16_t *>(nullptr), 0, 0, s_tab, qhi, qlo,
                                       qsum, s_p[wave], lane, tok_ok, ks, vs, m_run, l_run, corr, acc_v);
     }
   }

@@ -4,9 +4,9 @@
 // src/runtime/kv_gpu_fixture.cpp:12-16: symmetric, qmax = 127, zero point 128, lrint of the IEEE fp32 quotient,
 // clamp to [-(qmax+1), qmax]); the scale granularity is one absmax scale per page and head for K and for V (the
 // benchmark configuration's "per-page-per-head absmax"). The entropy coder is this project's own design (the
-// reference has no rANS KV codec): joint 2-bit high parts coded with 64-lane interleaved rANS (M = 2^11,
-// 16-bit renormalisation), 6-bit low parts stored raw and bit-sliced. The byte format is specified in
-// include/chromofold/kv_codec_ext.h.
+// reference has no rANS KV codec): joint 2-bit high parts coded with interleaved rANS (M = 2^11, 16-bit
+// renormalisation; two chains of 64 lane states per stream), 6-bit low parts stored raw and bit-sliced. The byte
+// format is specified in include/chromofold/kv_codec_ext.h.
 #include <algorithm>
 #include <atomic>
 #include <cmath>
@@ -83,15 +83,16 @@ uint32_t spread_highs(uint32_t j) {
   return v;
 }
 
-// Interleaved rANS encode of one stream: joint[L][q] for 64 lanes x nq quads. Writes states and the shared word
-// stream in decode order (decoder: quad q = 0..nq-1, all lanes decode, renorm reads in ascending lane order).
-void rans_encode(const Table &tb, const std::vector<uint8_t> &joint, uint32_t nq, uint32_t *states,
+// Interleaved rANS encode of one chain: the quads q = chain, chain + 2, ... of joint[L][q] (64 lanes x nq quads).
+// Writes the 64 states and the chain's word stream in decode order (decoder: the chain's quads ascending, all lanes
+// decode, renorm reads in ascending lane order).
+void rans_encode(const Table &tb, const std::vector<uint8_t> &joint, uint32_t nq, uint32_t chain, uint32_t *states,
                  std::vector<uint16_t> *words) {
   uint32_t x[kLanes];
   for (uint32_t t = 0; t < kLanes; ++t) x[t] = kL;
   std::vector<uint16_t> emitted;
-  emitted.reserve(static_cast<size_t>(nq) * kLanes);
-  for (int64_t q = static_cast<int64_t>(nq) - 1; q >= 0; --q) {
+  emitted.reserve(static_cast<size_t>(nq) * kLanes / 2);
+  for (int64_t q = static_cast<int64_t>(nq) - 2 + chain; q >= 0; q -= 2) {
     for (int t = static_cast<int>(kLanes) - 1; t >= 0; --t) {
       const uint32_t s = joint[static_cast<size_t>(t) * nq + q];
       const uint32_t f = tb.freq[s];
@@ -135,9 +136,10 @@ extern "C" uint64_t cf_kv_group_blob_max_bytes(uint32_t codec, uint32_t head_dim
   if (!dim_ok(head_dim)) return 0;
   if (codec == CF_KV_CODEC_INT8) return kHeader + 2ull * CF_KV_GROUP_PAGES * kPageTok * head_dim;
   if (codec != CF_KV_CODEC_RANS_HYBRID) return 0;
+  // header, 4 x 64 states, K and V low parts, at most CF_KV_RANS_MAX_GROUP_WORDS words (above that the group is
+  // stored raw, which is smaller than this bound)
   const uint64_t lows = 3ull * (head_dim / 16) * kLanes * 4;
-  const uint64_t max_words = (static_cast<uint64_t>(head_dim / 4) * kLanes * kProbBits + 15) / 16 + kLanes;
-  return align16(kHeader + 2 * kLanes * 4 + 2 * lows + 2 * 2 * max_words);
+  return align16(kHeader + 4 * kLanes * 4 + 2 * lows + 2ull * CF_KV_RANS_MAX_GROUP_WORDS);
 }
 
 extern "C" cf_status cf_kv_rans_page_histogram(const float *values, uint32_t token_count, uint32_t head_dim,
@@ -243,8 +245,8 @@ extern "C" cf_status cf_kv_encode_group(uint32_t codec, const float *keys, const
 
   Table tk, tv;
   if (!load_table(k_table, &tk) || !load_table(v_table, &tv)) return CF_ERR_INVALID_ARGUMENT;
-  uint32_t states[2][kLanes];
-  std::vector<uint16_t> words[2];
+  uint32_t states[4][kLanes];  // K A, K B, V A, V B
+  std::vector<uint16_t> words[4];
   const uint32_t nlow = 3 * (head_dim / 16) * kLanes;
   std::vector<uint32_t> lows(2 * static_cast<size_t>(nlow), 0u);
   for (int s = 0; s < 2; ++s) {
@@ -259,13 +261,15 @@ extern "C" cf_status cf_kv_encode_group(uint32_t codec, const float *keys, const
       }
       pack_lows(sym, head_dim, s == 1, L, lows.data() + s * nlow);
     }
-    rans_encode(s ? tv : tk, joint, nq, states[s], &words[s]);
+    for (uint32_t chain = 0; chain < 2; ++chain)
+      rans_encode(s ? tv : tk, joint, nq, chain, states[2 * s + chain], &words[2 * s + chain]);
   }
-  if (words[0].size() + words[1].size() > CF_KV_RANS_MAX_GROUP_WORDS)  // raw fallback (see kv_codec_ext.h)
+  size_t total_words = 0;
+  for (const auto &w : words) total_words += w.size();
+  if (total_words > CF_KV_RANS_MAX_GROUP_WORDS)  // raw fallback (see kv_codec_ext.h)
     return cf_kv_encode_group(CF_KV_CODEC_INT8, keys, values, page_count, token_counts, head_dim, nullptr, nullptr,
                               k_table_index, v_table_index, blob, capacity, blob_bytes);
-  h.k_word_count = static_cast<uint16_t>(words[0].size());
-  h.v_word_count = static_cast<uint16_t>(words[1].size());
+  for (int c = 0; c < 4; ++c) h.word_count[c] = static_cast<uint16_t>(words[c].size());
   uint64_t at = 0;
   std::memcpy(blob + at, &h, sizeof h);
   at += kHeader;
@@ -273,9 +277,9 @@ extern "C" cf_status cf_kv_encode_group(uint32_t codec, const float *keys, const
   at += sizeof states;
   std::memcpy(blob + at, lows.data(), lows.size() * 4);
   at += lows.size() * 4;
-  for (int s = 0; s < 2; ++s) {
-    std::memcpy(blob + at, words[s].data(), words[s].size() * 2);
-    at += words[s].size() * 2;
+  for (int c = 0; c < 4; ++c) {
+    std::memcpy(blob + at, words[c].data(), words[c].size() * 2);
+    at += words[c].size() * 2;
   }
   const uint64_t end = align16(at);
   std::memset(blob + at, 0, end - at);

@@ -9,12 +9,12 @@
 //      workgroup 0 also clears the status word.
 //   2. encode_kernel: one 4-wavefront workgroup per group. Phase 1: wavefront G quantises page G (absmax over the
 //      page's present tokens, IEEE division, round half to even) into LDS symbol tiles laid out for phase 2's
-//      reads (K token-major, V dim-major, both padded to odd word strides). Phase 2: wavefront 0 rANS-codes the K
-//      stream and wavefront 1 the V stream, 64 interleaved states each; the renormalisation words of one step are
-//      placed with a ballot prefix count, written from the top of an LDS buffer down so that the reversed stream
-//      needs no second pass; wavefronts 2 and 3 bit-slice the low parts. Phase 3 writes the blob (or the INT8
-//      fallback when K + V words exceed CF_KV_RANS_MAX_GROUP_WORDS) into a fixed-capacity staging slot and its
-//      size in 16-byte units.
+//      reads (K token-major, V dim-major, both padded to odd word strides). Phase 2: each wavefront rANS-codes one
+//      of the four chains (K A, K B, V A, V B; 64 interleaved states each); the renormalisation words of one step
+//      are placed with a ballot prefix count, written from the top of an LDS buffer down so that the reversed
+//      stream needs no second pass. Phase 3 bit-slices the low parts and writes the blob (or the INT8 fallback when
+//      the words exceed CF_KV_RANS_MAX_GROUP_WORDS) into a fixed-capacity staging slot, and its size in 16-byte
+//      units.
 //   3. an exclusive scan of the sizes (hipcub), then pack_kernel copies every blob to pool[pool_at + offset],
 //      writes offsets_out and *pool_end — or nothing at all when any group or the pool capacity failed, in which
 //      case the status word holds CF_ERR_INVALID_ARGUMENT.
@@ -30,7 +30,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr uint32_t kHeader = 64;
 constexpr uint32_t kMaxDim = CF_KV_MAX_HEAD_DIM;
-constexpr uint32_t kCap = CF_KV_RANS_MAX_GROUP_WORDS;  // per stream: D/4 quads x 64 lanes <= 2048 words
+constexpr uint32_t kChainCap = CF_KV_RANS_MAX_GROUP_WORDS / 2;  // per chain: D/8 quads x 64 lanes <= 1024 words
 constexpr int kKStride = kMaxDim / 4 + 1;              // words per K token row (odd: conflict-free lane reads)
 constexpr int kVStride = 5;                            // words per V dim row (4 token quads + 1)
 constexpr uint32_t kTableBytes = CF_KV_RANS_TABLE_BYTES;
@@ -116,10 +116,10 @@ __device__ __forceinline__ uint32_t joint_of(uint32_t w) {
 __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
   __shared__ uint32_t kS[4 * 16 * kKStride];
   __shared__ uint32_t vT[4 * kMaxDim * kVStride];
-  __shared__ uint16_t s_words[2][kCap];
+  __shared__ uint16_t s_words[4][kChainCap];
   __shared__ uint32_t s_tab[2][256];
   __shared__ float s_scale[2][4];
-  __shared__ uint32_t s_tc[4], s_count[2], s_bad;
+  __shared__ uint32_t s_tc[4], s_count[4], s_bad;
 
   const uint64_t g = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -228,13 +228,13 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
 
   uint8_t *blob = a.stage + g * a.cap;
   const int G = lane >> 4, t = lane & 15;
-  // ---- phase 2: rANS (waves 0, 1) and low parts (waves 2, 3, kept in registers until the codec is decided)
-  uint32_t lows[3 * (kMaxDim / 16)];
-  if (rans && wave < 2) {
-    const int s = wave;
+  // ---- phase 2: rANS, one chain per wavefront: wave w codes stream w / 2 (K, V), chain w % 2 (its quads
+  // q = chain, chain + 2, ..., encoded in reverse)
+  if (rans) {
+    const int s = wave >> 1, ch = wave & 1;
     uint32_t x = 1u << 16;
     uint32_t base = 0;
-    for (int q = static_cast<int>(nq) - 1; q >= 0; --q) {
+    for (int q = static_cast<int>(nq) - 2 + ch; q >= 0; q -= 2) {
       const uint32_t w = s == 0 ? k_word(kS, G, t, q) : v_word(vT, G, t, q, ng);
       const uint32_t e = s_tab[s][joint_of(w)];
       const uint32_t f = e & 0xFFFFu, cum = e >> 16;
@@ -242,42 +242,27 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
       const uint64_t mask = __ballot(emit);
       if (emit) {
         const uint32_t above = __popcll(mask & ~((2ull << lane) - 1ull));  // emitters at higher lanes go first
-        s_words[s][kCap - 1 - (base + above)] = static_cast<uint16_t>(x & 0xFFFFu);
+        s_words[wave][kChainCap - 1 - (base + above)] = static_cast<uint16_t>(x & 0xFFFFu);
         x >>= 16;
       }
       base += __popcll(mask);
       x = ((x / f) << CF_KV_RANS_PROB_BITS) + (x % f) + cum;
     }
-    *reinterpret_cast<uint32_t *>(blob + kHeader + 4 * (s * 64 + lane)) = x;
-    if (lane == 0) s_count[s] = base;
-  } else if (rans) {
-    const int s = wave - 2;
-#pragma unroll
-    for (uint32_t gi = 0; gi < kMaxDim / 16; ++gi) {
-      if (gi >= ng) break;
-      uint32_t n0 = 0, n1 = 0, c = 0;
-#pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const int q = 4 * gi + qd;
-        const uint32_t w = s == 0 ? k_word(kS, G, t, q) : v_word(vT, G, t, q, ng);
-        const uint32_t nib = (w & 0x0F0F0F0Fu) << (4 * (qd & 1));
-        if (qd < 2) n0 |= nib; else n1 |= nib;
-        c |= ((w >> 4) & 0x03030303u) << (2 * qd);
-      }
-      lows[3 * gi] = n0;
-      lows[3 * gi + 1] = n1;
-      lows[3 * gi + 2] = c;
-    }
+    *reinterpret_cast<uint32_t *>(blob + kHeader + 4 * (wave * 64 + lane)) = x;
+    if (lane == 0) s_count[wave] = base;
   }
   __syncthreads();
 
   // ---- phase 3: the blob
-  const uint32_t kw = rans ? s_count[0] : 0u, vw = rans ? s_count[1] : 0u;
+  uint32_t wc[4] = {0, 0, 0, 0};
+  if (rans)
+    for (int c = 0; c < 4; ++c) wc[c] = s_count[c];
+  const uint32_t total = wc[0] + wc[1] + wc[2] + wc[3];
   const uint32_t nlow = 3 * ng * 64;
-  const uint64_t wat = kHeader + 2 * 64 * 4 + 2ull * nlow * 4;  // first rANS word of the blob
-  // (the second bound never binds: a stream emits at most 11 bits per quad plus one word per lane, which the
-  // capacity covers; it keeps the staging slot safe by construction)
-  const bool raw = !rans || kw + vw > CF_KV_RANS_MAX_GROUP_WORDS || wat + 2ull * (kw + vw) > a.cap;
+  const uint64_t wat = kHeader + 4 * 64 * 4 + 2ull * nlow * 4;  // first rANS word of the blob
+  // (the second bound never binds: the first one caps the words and the capacity covers it; it keeps the staging
+  // slot safe by construction)
+  const bool raw = !rans || total > CF_KV_RANS_MAX_GROUP_WORDS || wat + 2ull * total > a.cap;
   uint64_t size;
   if (raw) {
     // INT8: word (q * 64 + L) of stream s = the 4 symbols of quad q of lane L
@@ -288,24 +273,39 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
     }
     size = kHeader + 2ull * nq * 64 * 4;
   } else {
-    if (wave >= 2) {
-      uint32_t *lo = reinterpret_cast<uint32_t *>(blob + kHeader + 2 * 64 * 4) + (wave - 2) * nlow;
-      for (uint32_t gi = 0; gi < ng; ++gi)
+    if (wave < 2) {  // bit-sliced low parts of stream `wave`
+      const int s = wave;
+      uint32_t *lo = reinterpret_cast<uint32_t *>(blob + kHeader + 4 * 64 * 4) + s * nlow;
+      for (uint32_t gi = 0; gi < ng; ++gi) {
+        uint32_t n0 = 0, n1 = 0, c = 0;
 #pragma unroll
-        for (int w = 0; w < 3; ++w) lo[(gi * 3 + w) * 64 + lane] = lows[3 * gi + w];
+        for (int qd = 0; qd < 4; ++qd) {
+          const int q = 4 * gi + qd;
+          const uint32_t w = s == 0 ? k_word(kS, G, t, q) : v_word(vT, G, t, q, ng);
+          const uint32_t nib = (w & 0x0F0F0F0Fu) << (4 * (qd & 1));
+          if (qd < 2) n0 |= nib; else n1 |= nib;
+          c |= ((w >> 4) & 0x03030303u) << (2 * qd);
+        }
+        lo[(gi * 3 + 0) * 64 + lane] = n0;
+        lo[(gi * 3 + 1) * 64 + lane] = n1;
+        lo[(gi * 3 + 2) * 64 + lane] = c;
+      }
     }
-    uint16_t *wo = reinterpret_cast<uint16_t *>(blob + wat);
-    for (uint32_t i = tid; i < kw + vw; i += kThreads)
-      wo[i] = i < kw ? s_words[0][kCap - kw + i] : s_words[1][kCap - vw + (i - kw)];
-    const uint64_t end = wat + 2ull * (kw + vw);
+    uint16_t *wo = reinterpret_cast<uint16_t *>(blob + wat);  // streams K A, K B, V A, V B back to back
+    const uint32_t o1 = wc[0], o2 = o1 + wc[1], o3 = o2 + wc[2];
+    for (uint32_t i = tid; i < total; i += kThreads) {
+      const uint32_t c = i < o1 ? 0u : i < o2 ? 1u : i < o3 ? 2u : 3u;
+      const uint32_t at = i - (c == 0 ? 0u : c == 1 ? o1 : c == 2 ? o2 : o3);
+      wo[i] = s_words[c][kChainCap - wc[c] + at];
+    }
+    const uint64_t end = wat + 2ull * total;
     size = align16(end);
     for (uint64_t b = end + tid; b < size; b += kThreads) blob[b] = 0;
   }
   if (tid == 0) {
     cf_kv_group_header h{};
     h.codec = raw ? CF_KV_CODEC_INT8 : CF_KV_CODEC_RANS_HYBRID;
-    h.k_word_count = static_cast<uint16_t>(raw ? 0 : kw);
-    h.v_word_count = static_cast<uint16_t>(raw ? 0 : vw);
+    for (int c = 0; c < 4; ++c) h.word_count[c] = static_cast<uint16_t>(raw ? 0 : wc[c]);
     for (int i = 0; i < 4; ++i) {
       h.token_count[i] = static_cast<uint16_t>(s_tc[i]);
       h.k_scale[i] = s_scale[0][i];

@@ -22,7 +22,7 @@ from . import _abi as A
 CODEC_INT8, CODEC_RANS_HYBRID = 1, 2
 PAGE_TOKENS = 16
 TABLE_BYTES = 16384
-EXT_ABI_VERSION = 2
+EXT_ABI_VERSION = 3
 GROUP_PAGES = 4
 GROUP_TOKENS = PAGE_TOKENS * GROUP_PAGES
 

@@ -10,8 +10,8 @@
  *
  * ------------------------------------------------------------------------------------------------------------
  * Storage unit: a "page group" = up to 4 consecutive 16-token pages of one (sequence, KV head) coded together, so
- * that one 64-lane wavefront decodes it with 64 interleaved rANS states and ONE shared word stream (wave-uniform
- * cursor, lane offset by mbcnt). Pages stay the logical unit: each page has its own token count and scales.
+ * that one 64-lane wavefront decodes it with interleaved rANS states, 64 per word stream (wave-uniform cursor, lane
+ * offset by mbcnt). Pages stay the logical unit: each page has its own token count and scales.
  * Lane L = 16 G + t belongs to page G of the group.
  *
  * Quantisation (per page and head; K and V separately): s = max|x| / 127 (1.0 if all zero),
@@ -28,11 +28,14 @@
  *   V stream: lane L owns dims {t + 16 i : i < D/16} of page G; quads in the order (tq = 0..3, i = 0..D/16-1),
  *             quad = tokens 4tq..4tq+3 at dim t + 16 i.
  *
- * rANS: M = 2^11, state in [2^16, 2^32), 16-bit renormalisation words. Decode step (all 64 lanes, quad q):
+ * rANS: M = 2^11, state in [2^16, 2^32), 16-bit renormalisation words. Each stream (K, V) is coded as TWO
+ * interleaved chains of 64 lane states: chain A holds the even quads (q = 0, 2, 4, ...) and chain B the odd quads,
+ * each with its own word stream, so a lane advances four independent states (K A/B, V A/B) at once. Decode step of
+ * a chain (all 64 lanes, its next quad q):
  *   slot = x & 2047; (f, c, j) = table[slot]; x = f * (x >> 11) + c; then the lanes with x < 2^16 read, in
- *   ascending lane order, the next words of the stream: x = (x << 16) | word.  (c = slot - cum[j].)
- * The encoder runs the exact reverse (quads descending, lanes descending) starting every state at 2^16, so a
- * correct decode ends with all 64 states at 2^16 and the cursor at the word count.
+ *   ascending lane order, the next words of the chain's stream: x = (x << 16) | word.  (c = slot - cum[j].)
+ * The encoder runs the exact reverse per chain (its quads descending, lanes descending) starting every state at
+ * 2^16, so a correct decode ends with all states at 2^16 and every cursor at its stream's word count.
  *
  * Low parts, bit-sliced per lane in groups of 16 values (4 quads qd = 0..3, position i = 0..3 inside a quad):
  *   N0 = sum_i (l(0,i) & 15) << 8i | (l(1,i) & 15) << (8i + 4)      (quads 0,1)
@@ -44,8 +47,10 @@
  *
  * Group blob (16-byte aligned, little-endian):
  *   [0]    cf_kv_group_header (64 B)
- *   RANS_HYBRID: [64] k_states[64] u32, v_states[64] u32; [576] k_lows[3*(D/16)*64] u32, v_lows[same];
- *                then k_words[k_word_count] u16, v_words[v_word_count] u16, zero padding to 16 bytes.
+ *   RANS_HYBRID: [64] states u32: K chain A [64], K chain B [64], V chain A [64], V chain B [64];
+ *                [1088] k_lows[3*(D/16)*64] u32, v_lows[same];
+ *                then the word streams u16 of K A, K B, V A, V B (word_count[0..3] words each), zero padding to 16
+ *                bytes.
  *   INT8:        [64] K symbol bytes, word (q*64 + L) = the 4 bytes of quad q of lane L; then V the same way.
  *
  * Table blob (CF_KV_RANS_TABLE_BYTES = 16 KiB): 2048 slot entries of two u32:
@@ -53,9 +58,9 @@
  *   hi = spread(j) = sum_i ((j >> 2i) & 3) << (8i + 6)
  * The batched launch uses table 2h for the K streams and 2h+1 for the V streams of KV head h.
  *
- * Raw fallback: a group whose K + V rANS words would exceed CF_KV_RANS_MAX_GROUP_WORDS (data the tables do not
- * fit, e.g. near-uniform high parts) is stored as an INT8 group instead (its header says so); a RANS_HYBRID pool
- * may therefore hold both kinds and the decoder dispatches per group.
+ * Raw fallback: a group whose rANS words (all four streams together) would exceed CF_KV_RANS_MAX_GROUP_WORDS
+ * (data the tables do not fit, e.g. near-uniform high parts) is stored as an INT8 group instead (its header says
+ * so); a RANS_HYBRID pool may therefore hold both kinds and the decoder dispatches per group.
  * ------------------------------------------------------------------------------------------------------------ */
 #ifndef CHROMOFOLD_KV_CODEC_EXT_H
 #define CHROMOFOLD_KV_CODEC_EXT_H
@@ -69,7 +74,7 @@
 extern "C" {
 #endif
 
-#define CF_KV_EXT_ABI_VERSION 2u
+#define CF_KV_EXT_ABI_VERSION 3u
 #define CF_KV_GROUP_PAGES 4u
 #define CF_KV_CODEC_INT8 1u
 #define CF_KV_CODEC_RANS_HYBRID 2u
@@ -81,14 +86,12 @@ extern "C" {
 
 typedef struct cf_kv_group_header {
     uint32_t codec;            /* CF_KV_CODEC_* */
-    uint16_t k_word_count;     /* 16-bit rANS words of the K stream (0 for INT8) */
-    uint16_t v_word_count;
+    uint16_t word_count[4];    /* 16-bit rANS words of the K A, K B, V A, V B streams (0 for INT8) */
     uint16_t token_count[4];   /* tokens of each page, 0 = page absent */
     uint16_t head_dim;
     uint16_t page_count;       /* 1..4 */
     uint32_t k_table;          /* table index of the K stream (informational) */
     uint32_t v_table;
-    uint32_t reserved;
     float k_scale[4];
     float v_scale[4];
 } cf_kv_group_header;

@@ -192,13 +192,12 @@ void or_kv_window_attention_f64(const float *K, const float *V, const float *Q, 
 int or_kv_decode_group(const uint8_t *blob, const uint8_t *tables, uint32_t head, uint8_t *k_sym, uint8_t *v_sym,
                        float *k_scale, float *v_scale, uint32_t *token_count) {
   uint32_t codec;
-  uint16_t kw, vw, tc[4], D, npg;
+  uint16_t wc[4], tc[4], D, npg;
   std::memcpy(&codec, blob, 4);
-  std::memcpy(&kw, blob + 4, 2);
-  std::memcpy(&vw, blob + 6, 2);
-  std::memcpy(tc, blob + 8, 8);
-  std::memcpy(&D, blob + 16, 2);
-  std::memcpy(&npg, blob + 18, 2);
+  std::memcpy(wc, blob + 4, 8);  // words of the K A, K B, V A, V B chains
+  std::memcpy(tc, blob + 12, 8);
+  std::memcpy(&D, blob + 20, 2);
+  std::memcpy(&npg, blob + 22, 2);
   std::memcpy(k_scale, blob + 32, 16);
   std::memcpy(v_scale, blob + 48, 16);
   for (int g = 0; g < 4; ++g) token_count[g] = tc[g];
@@ -222,31 +221,34 @@ int or_kv_decode_group(const uint8_t *blob, const uint8_t *tables, uint32_t head
   }
   if (codec != 2) return -1;
   const uint32_t nlow = 3 * (D / 16) * 64;
-  const uint32_t *states = reinterpret_cast<const uint32_t *>(blob + 64);
-  const uint32_t *lows = reinterpret_cast<const uint32_t *>(blob + 576);
-  const uint16_t *words = reinterpret_cast<const uint16_t *>(blob + 576 + 2 * (size_t)nlow * 4);
+  const uint32_t *states = reinterpret_cast<const uint32_t *>(blob + 64);  // K A, K B, V A, V B x 64 lanes
+  const uint32_t *lows = reinterpret_cast<const uint32_t *>(blob + 64 + 4 * 64 * 4);
+  const uint16_t *words = reinterpret_cast<const uint16_t *>(blob + 64 + 4 * 64 * 4 + 2 * (size_t)nlow * 4);
+  const uint16_t *cw[4];  // each chain's word stream, in the order K A, K B, V A, V B
+  cw[0] = words;
+  for (int c = 1; c < 4; ++c) cw[c] = cw[c - 1] + wc[c - 1];
   for (int s = 0; s < 2; ++s) {
     const uint8_t *tab = tables + (size_t)(2 * head + s) * 16384;
-    const uint16_t *w = words + (s ? kw : 0);
-    const uint32_t nw = s ? vw : kw;
-    uint32_t x[64];
-    for (int L = 0; L < 64; ++L) x[L] = states[s * 64 + L];
-    uint32_t cur = 0;
+    uint32_t x[2][64], cur[2] = {0, 0};
+    for (int ch = 0; ch < 2; ++ch)
+      for (int L = 0; L < 64; ++L) x[ch][L] = states[(2 * s + ch) * 64 + L];
     uint8_t *out = s ? v_sym : k_sym;
     const uint32_t *lw = lows + (size_t)s * nlow;
-    for (uint32_t q = 0; q < nq; ++q) {
+    for (uint32_t q = 0; q < nq; ++q) {  // quad q belongs to chain q % 2; chains are independent
+      const uint32_t ch = q % 2, nw = wc[2 * s + ch];
+      const uint16_t *w = cw[2 * s + ch];
       uint32_t j[64];
       for (uint32_t L = 0; L < 64; ++L) {  // all lanes decode quad q
         uint32_t lo;
-        std::memcpy(&lo, tab + 8 * (x[L] & 2047u), 4);
+        std::memcpy(&lo, tab + 8 * (x[ch][L] & 2047u), 4);
         const uint32_t f = lo & 2047u, c = (lo >> 11) & 2047u;
         j[L] = (lo >> 22) & 255u;
-        x[L] = f * (x[L] >> 11) + c;
+        x[ch][L] = f * (x[ch][L] >> 11) + c;
       }
       for (uint32_t L = 0; L < 64; ++L)  // renormalisation reads in ascending lane order
-        if (x[L] < 65536u) {
-          if (cur >= nw) return -1;
-          x[L] = (x[L] << 16) | w[cur++];
+        if (x[ch][L] < 65536u) {
+          if (cur[ch] >= nw) return -1;
+          x[ch][L] = (x[ch][L] << 16) | w[cur[ch]++];
         }
       const uint32_t g = q / 4, qd = q % 4;
       for (uint32_t L = 0; L < 64; ++L) {
@@ -258,9 +260,11 @@ int or_kv_decode_group(const uint8_t *blob, const uint8_t *tables, uint32_t head
         }
       }
     }
-    if (cur != nw) return -1;
-    for (int L = 0; L < 64; ++L)
-      if (x[L] != 65536u) return -1;
+    for (int ch = 0; ch < 2; ++ch) {
+      if (cur[ch] != wc[2 * s + ch]) return -1;
+      for (int L = 0; L < 64; ++L)
+        if (x[ch][L] != 65536u) return -1;
+    }
   }
   return 0;
 }
