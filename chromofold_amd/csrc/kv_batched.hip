@@ -374,7 +374,7 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) acc_v[i] = float4_t{0, 0, 0, 0};
 
-  uint32_t *buf = s_buf[wave];
+  uint32_t *buf = s_buf[__builtin_amdgcn_readfirstlane(wave)];  // uniform base: cursor arithmetic stays scalar
   // Memory pipeline of a wavefront over its groups gi = ga + wave, +4, ...:
   //   blob offset   loaded two groups ahead;
   //   header        loaded at the start of the previous group (fields and lane states kept in registers);
