@@ -244,3 +244,158 @@ def build_fm(tokens: torch.Tensor, sa_sample: int, stream=None) -> tuple[FmIndex
     t_all = time.perf_counter() - t0
     fm = FmIndex(w, sigma, n, sa_sample, {"C": Ct, "mwords": mw, "msb": msb, "sval": sval[:cnt.value].clone()})
     return fm, {"s": s, "sa": sa, "bwt": bwt, "sa_s": t_sa, "build_s": t_all, "layout": lay}
+
+
+# ------------------------------------------------------------------------------------------------ on-disk formats
+class cf_rrrw_file_header(C.Structure):
+    _fields_ = [("n", A.U64), ("rrr_bytes", A.U64), ("packed_bytes", A.U64), ("bits", A.U32), ("vocab", A.U32),
+                ("nblocks", A.U32), ("nsb", A.U32), ("cwords", A.U32), ("na", A.U32), ("owords", A.U32),
+                ("nq", A.U32), ("nr", A.U32), ("h0", A.F32)]
+
+
+class cf_rrrw_file_queries(C.Structure):
+    _fields_ = [("pos", A.P), ("access_golden", A.P), ("rank_c", A.P), ("rank_i", A.P), ("rank_golden", A.P)]
+
+
+class cf_fm_file_header(C.Structure):
+    _fields_ = [("n", A.U64), ("rrr_bytes", A.U64)] + [(k, A.U32) for k in (
+        "bits", "vocab", "sigma", "nblocks", "nsb", "cwords", "na", "owords", "sa_sample", "mwords", "msb", "nsval",
+        "npat", "patflat", "nloc", "reserved")]
+
+
+class cf_fm_file_arrays(C.Structure):
+    _fields_ = [(k, A.P) for k in ("C", "mwords", "msb", "sval", "pat", "pstart", "plen", "count_golden", "locoff",
+                                   "locpos")]
+
+
+for _name, _args in (("cf_rrrw_file_read_header", [C.c_char_p, A.P]), ("cf_rrrw_file_read", [C.c_char_p, A.P, A.P, A.P]),
+                     ("cf_rrrw_file_write", [C.c_char_p, A.P, A.P, A.P]),
+                     ("cf_fm_file_read_header", [C.c_char_p, A.P]), ("cf_fm_file_read", [C.c_char_p, A.P, A.P, A.P]),
+                     ("cf_fm_file_write", [C.c_char_p, A.P, A.P, A.P])):
+    A.declare(_name, A.I32, _args)
+
+_WAVELET = (("classes", np.uint32, lambda h: h.bits * h.cwords), ("offsets", np.uint32, lambda h: h.owords),
+            ("rank_a", np.int32, lambda h: h.bits * h.na), ("rank_d", np.uint16, lambda h: h.bits * (h.nsb + 1)),
+            ("off_a", np.int32, lambda h: h.bits * h.na), ("off_d", np.uint16, lambda h: h.bits * (h.nsb + 1)),
+            ("offbase", np.int32, lambda h: h.bits), ("zeros", np.int32, lambda h: h.bits))
+_RRRW_QUERIES = (("pos", lambda h: h.nq), ("access_golden", lambda h: h.nq), ("rank_c", lambda h: h.nr),
+                 ("rank_i", lambda h: h.nr), ("rank_golden", lambda h: h.nr))
+_FM = (("C", np.int32, lambda h: h.sigma), ("mwords", np.uint32, lambda h: h.mwords), ("msb", np.int32, lambda h: h.msb),
+       ("sval", np.int32, lambda h: h.nsval), ("pat", np.int32, lambda h: h.patflat),
+       ("pstart", np.int32, lambda h: h.npat), ("plen", np.int32, lambda h: h.npat),
+       ("count_golden", np.uint32, lambda h: h.npat), ("locoff", np.int32, lambda h: h.npat + 1),
+       ("locpos", np.int32, lambda h: h.nloc))
+
+
+def _host_ptr(a: np.ndarray | None):
+    return None if a is None or a.size == 0 else a.ctypes.data_as(C.c_void_p)
+
+
+def _wavelet_struct(d: dict) -> cf_rrrw_arrays:
+    return cf_rrrw_arrays(*[_host_ptr(d[k]) for k, _, _ in _WAVELET])
+
+
+def read_cfrw(path: str) -> dict:
+    """Read a .cfrw v1 file with the library's reader (cf_rrrw_file_read): header fields + index arrays + query
+    sections as host numpy arrays."""
+    L = A.lib()
+    h = cf_rrrw_file_header()
+    A.check(L.cf_rrrw_file_read_header(path.encode(), C.byref(h)), "cf_rrrw_file_read_header")
+    d = {k: getattr(h, k) for k, _ in h._fields_}
+    for k, dt, cnt in _WAVELET:
+        d[k] = np.zeros(cnt(h), dt)
+    for k, cnt in _RRRW_QUERIES:
+        d[k] = np.zeros(cnt(h), np.uint32)
+    q = cf_rrrw_file_queries(*[_host_ptr(d[k]) for k, _ in _RRRW_QUERIES])
+    A.check(L.cf_rrrw_file_read(path.encode(), C.byref(h), C.byref(_wavelet_struct(d)), C.byref(q)),
+            "cf_rrrw_file_read")
+    return d
+
+
+def write_cfrw(path: str, d: dict) -> None:
+    """Write a .cfrw v1 file (cf_rrrw_file_write) from the fields/arrays `read_cfrw` returns; the query sections
+    may be absent (written empty)."""
+    h = cf_rrrw_file_header()
+    arrays = {k: np.ascontiguousarray(d[k], dt) for k, dt, _ in _WAVELET}
+    queries = {k: np.ascontiguousarray(d.get(k, np.zeros(0)), np.uint32) for k, _ in _RRRW_QUERIES}
+    for k, _ in h._fields_:
+        if k in ("nq", "nr"):
+            continue
+        setattr(h, k, d[k])
+    h.nq, h.nr = queries["pos"].size, queries["rank_c"].size
+    q = cf_rrrw_file_queries(*[_host_ptr(queries[k]) for k, _ in _RRRW_QUERIES])
+    A.check(A.lib().cf_rrrw_file_write(path.encode(), C.byref(h), C.byref(_wavelet_struct(arrays)), C.byref(q)),
+            "cf_rrrw_file_write")
+
+
+def read_cffm(path: str) -> dict:
+    """Read a .cffm v1 file with the library's reader (cf_fm_file_read)."""
+    L = A.lib()
+    h = cf_fm_file_header()
+    A.check(L.cf_fm_file_read_header(path.encode(), C.byref(h)), "cf_fm_file_read_header")
+    d = {k: getattr(h, k) for k, _ in h._fields_}
+    for k, dt, cnt in _WAVELET + _FM:
+        d[k] = np.zeros(cnt(h), dt)
+    fm = cf_fm_file_arrays(*[_host_ptr(d[k]) for k, _, _ in _FM])
+    A.check(L.cf_fm_file_read(path.encode(), C.byref(h), C.byref(_wavelet_struct(d)), C.byref(fm)),
+            "cf_fm_file_read")
+    return d
+
+
+def write_cffm(path: str, d: dict) -> None:
+    """Write a .cffm v1 file (cf_fm_file_write); the pattern section may be absent (written empty)."""
+    h = cf_fm_file_header()
+    arrays = {k: np.ascontiguousarray(d[k], dt) for k, dt, _ in _WAVELET}
+    extra = {k: np.ascontiguousarray(d.get(k, np.zeros(0)), dt) for k, dt, _ in _FM}
+    if extra["locoff"].size == 0:
+        extra["locoff"] = np.zeros(1, np.int32)
+    for k, _ in h._fields_:
+        if k in ("mwords", "msb", "nsval", "npat", "patflat", "nloc", "reserved"):
+            continue
+        setattr(h, k, d[k])
+    h.mwords, h.msb, h.nsval = extra["mwords"].size, extra["msb"].size, extra["sval"].size
+    h.npat, h.patflat, h.nloc = extra["pstart"].size, extra["pat"].size, extra["locpos"].size
+    fm = cf_fm_file_arrays(*[_host_ptr(extra[k]) for k, _, _ in _FM])
+    A.check(A.lib().cf_fm_file_write(path.encode(), C.byref(h), C.byref(_wavelet_struct(arrays)), C.byref(fm)),
+            "cf_fm_file_write")
+
+
+def _wavelet_file_fields(w: RrrWaveletIndex, lay: cf_rrrw_layout) -> dict:
+    dt = {"classes": np.uint32, "offsets": np.uint32, "rank_a": np.int32, "rank_d": np.uint16, "off_a": np.int32,
+          "off_d": np.uint16, "offbase": np.int32, "zeros": np.int32}
+    d = {k: w.tensors[k].cpu().numpy().view(dt[k]) for k in dt}
+    d.update(n=int(lay.n), bits=w.bits, nblocks=int(lay.nblocks), nsb=w.nsb, cwords=w.cwords, na=w.na,
+             owords=int(lay.owords), rrr_bytes=int(lay.rrr_bytes))
+    return d
+
+
+def save_cfrw(path: str, w: RrrWaveletIndex, lay: cf_rrrw_layout, vocab: int, symbols: torch.Tensor,
+              queries: dict | None = None) -> None:
+    """Write a GPU-built RRR wavelet matrix as .cfrw v1, with the header figures the reference builder writes
+    (tools/build_index.cpp:403-424): packed_bytes = the packed bit-plane wavelet's footprint, h0 = the empirical
+    entropy of `symbols` (the sequence the matrix was built from) in bits per symbol. `queries` optionally carries
+    pos / access_golden / rank_c / rank_i / rank_golden."""
+    d = _wavelet_file_fields(w, lay)
+    n, bits = d["n"], d["bits"]
+    nwords = (n + 31) // 32
+    d["packed_bytes"] = bits * nwords * 4 + bits * ((nwords + 7) // 8 + 1) * 4
+    cnt = torch.bincount(symbols.reshape(-1).long()).cpu().numpy()
+    h0 = 0.0
+    for c in cnt:
+        if c:
+            p = float(c) / n
+            h0 -= p * float(np.log2(p))
+    d["h0"], d["vocab"] = h0, vocab
+    d.update(queries or {})
+    write_cfrw(path, d)
+
+
+def save_cffm(path: str, fm: FmIndex, lay: cf_rrrw_layout, vocab: int, patterns: dict | None = None) -> None:
+    """Write a GPU-built FM-index (build_fm's index and layout) as .cffm v1 (reference tools/build_index.cpp:496-526).
+    `patterns` optionally carries pat / pstart / plen / count_golden / locoff / locpos."""
+    d = _wavelet_file_fields(fm.w, lay)
+    d.update(vocab=vocab, sigma=fm.sigma, sa_sample=fm.sa_sample)
+    for k, dt in (("C", np.int32), ("mwords", np.uint32), ("msb", np.int32), ("sval", np.int32)):
+        d[k] = fm.tensors[k].cpu().numpy().view(dt)
+    d.update(patterns or {})
+    write_cffm(path, d)

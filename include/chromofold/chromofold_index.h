@@ -73,6 +73,56 @@ cf_status cf_fm_build_aux(const int32_t *s, const int32_t *sa, int32_t n, int32_
                           uint32_t *bwt, int32_t *C, uint32_t *mwords, int32_t *msb, int32_t *sval, int32_t *sval_count,
                           void *workspace, uint64_t workspace_bytes, void *stream);
 
+/* ---- on-disk formats: .cfrw v1 and .cffm v1 (host files; host arrays) ----
+ * Byte-compatible with the reference writer (tools/build_index.cpp:413-438 and 496-526; exporter docstrings
+ * tools/export_rrr_wavelet.py:11-19, tools/export_fm_index.py:19-29): magic, version 1, little-endian header
+ * scalars without padding, then the arrays back to back. The files also carry the benchmark's query and golden
+ * sections (counts may be 0). No counterpart in the reference C ABI (its reader/writers are its tools and test
+ * drivers). Readers validate magic, version and the exact file size implied by the header; read into caller-owned
+ * host arrays sized from the header (cf_rrrw_arrays then holds HOST pointers). */
+typedef struct cf_rrrw_file_header {
+  uint64_t n, rrr_bytes, packed_bytes;
+  uint32_t bits, vocab, nblocks, nsb, cwords, na, owords;
+  uint32_t nq, nr; /* access queries (pos, golden) and rank queries (c, i, golden) in the file */
+  float h0;
+} cf_rrrw_file_header;
+
+typedef struct cf_rrrw_file_queries { /* host arrays: [nq] / [nr]; may be NULL when the count is 0 */
+  uint32_t *pos, *access_golden, *rank_c, *rank_i, *rank_golden;
+} cf_rrrw_file_queries;
+
+cf_status cf_rrrw_file_read_header(const char *path, cf_rrrw_file_header *header);
+cf_status cf_rrrw_file_read(const char *path, const cf_rrrw_file_header *header, const cf_rrrw_arrays *host_arrays,
+                            const cf_rrrw_file_queries *queries);
+cf_status cf_rrrw_file_write(const char *path, const cf_rrrw_file_header *header, const cf_rrrw_arrays *host_arrays,
+                             const cf_rrrw_file_queries *queries);
+
+typedef struct cf_fm_file_header {
+  uint64_t n, rrr_bytes;
+  uint32_t bits, vocab, sigma, nblocks, nsb, cwords, na, owords, sa_sample;
+  uint32_t mwords, msb, nsval;    /* mark plane words, mark directory entries, sampled SA values */
+  uint32_t npat, patflat, nloc;   /* pattern section: patterns, flattened symbols, located occurrences */
+  uint32_t reserved;              /* 0 (not in the file) */
+} cf_fm_file_header;
+
+typedef struct cf_fm_file_arrays { /* host arrays sized from the header */
+  int32_t *C;              /* [sigma] */
+  uint32_t *mwords;        /* [mwords] */
+  int32_t *msb;            /* [msb] */
+  int32_t *sval;           /* [nsval] */
+  int32_t *pat;            /* [patflat] symbols + 1, as the reference writes them */
+  int32_t *pstart, *plen;  /* [npat] */
+  uint32_t *count_golden;  /* [npat] */
+  int32_t *locoff;         /* [npat + 1] */
+  int32_t *locpos;         /* [nloc] */
+} cf_fm_file_arrays;
+
+cf_status cf_fm_file_read_header(const char *path, cf_fm_file_header *header);
+cf_status cf_fm_file_read(const char *path, const cf_fm_file_header *header, const cf_rrrw_arrays *host_wavelet,
+                          const cf_fm_file_arrays *host_arrays);
+cf_status cf_fm_file_write(const char *path, const cf_fm_file_header *header, const cf_rrrw_arrays *host_wavelet,
+                           const cf_fm_file_arrays *host_arrays);
+
 #ifdef __cplusplus
 } /* extern "C" */
 

@@ -102,6 +102,21 @@ int main(void) {
          cf_kv_encode_groups_async(2, NULL, NULL, 1, NULL, NULL, NULL, 64, NULL, 2, NULL, NULL, 0, 0, NULL, NULL,
                                    NULL, NULL, 0, NULL), INV);
   expect("cf_kv_encode_groups_workspace_bytes", cf_kv_encode_groups_workspace_bytes(2, 20, 1, 2) == 0, 1);
+  {
+    cf_rrrw_file_header rh;
+    cf_fm_file_header fh;
+    memset(&rh, 0, sizeof rh);
+    memset(&fh, 0, sizeof fh);
+    printf("sizeof cf_rrrw_file_header %zu\n", sizeof(cf_rrrw_file_header));
+    printf("sizeof cf_fm_file_header %zu\n", sizeof(cf_fm_file_header));
+    printf("sizeof cf_fm_file_arrays %zu\n", sizeof(cf_fm_file_arrays));
+    expect("cf_rrrw_file_read_header", cf_rrrw_file_read_header(NULL, &rh), INV);
+    expect("cf_rrrw_file_read", cf_rrrw_file_read("x", NULL, NULL, NULL), INV);
+    expect("cf_rrrw_file_write", cf_rrrw_file_write("x", &rh, NULL, NULL), INV);
+    expect("cf_fm_file_read_header", cf_fm_file_read_header(NULL, &fh), INV);
+    expect("cf_fm_file_read", cf_fm_file_read("x", &fh, NULL, NULL), INV);
+    expect("cf_fm_file_write", cf_fm_file_write(NULL, &fh, NULL, NULL), INV);
+  }
   printf("%s (%d failure%s)\n", failures ? "FAIL" : "PASS", failures, failures == 1 ? "" : "s");
   return failures ? 1 : 0;
 }

@@ -68,10 +68,12 @@ def test_c_headers_link_and_null_contract(tmp_path):
     assert r.returncode == 0, r.stdout + r.stderr
     assert "PASS" in r.stdout
     from chromofold_amd import _abi as A
-    from chromofold_amd import kv, qw
+    from chromofold_amd import kv, qw, search
     mirrors = {"cf_wavelet_view": A.cf_wavelet_view, "cf_rrrw_view": A.cf_rrrw_view, "cf_fm_view": A.cf_fm_view,
                "cf_kv_device_page": A.cf_kv_device_page, "cf_kv_paged_attention_desc": A.cf_kv_paged_attention_desc,
-               "cf_kv_batched_desc": kv.cf_kv_batched_desc, "cf_qw_matrix": qw.cf_qw_matrix}
+               "cf_kv_batched_desc": kv.cf_kv_batched_desc, "cf_qw_matrix": qw.cf_qw_matrix,
+               "cf_rrrw_file_header": search.cf_rrrw_file_header, "cf_fm_file_header": search.cf_fm_file_header,
+               "cf_fm_file_arrays": search.cf_fm_file_arrays}
     sizes = dict(re.findall(r"^sizeof (\w+) (\d+)$", r.stdout, flags=re.M))
     assert set(sizes) == set(mirrors)
     for name, cls in mirrors.items():
