@@ -89,6 +89,9 @@ def _declare(L):
         "or_kv_window_attention_f64": (None, [P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, P]),
         "or_kv_decode_group": (C.c_int, [P, P, U32, P, P, P, P, P]),
         "or_kv_quantize_page_absmax": (None, [P, U32, P, P]),
+        "or_nib_seal": (C.c_int, [P, U32, U32, P, P, P, P, P]),
+        "or_nib_attention": (None, [U32, P, P, P, P, P, P, U32, P, P, U32, U32, P, U32, U32, U32, U32, U32,
+                                    C.c_float, U32, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name, None)
@@ -438,6 +441,69 @@ def qmatmul_f64(x: np.ndarray, sym: np.ndarray, scale, zero) -> np.ndarray:
 # ------------------------------------------------------------------ the reference's own CPU code (oracle/_ref)
 # Built by `make -C oracle ref` from the reference sources where /root/reference is mounted; absent elsewhere.
 _ref = None
+
+
+@dataclass
+class NibPage:
+    """One sealed int4 nibble page (host arrays), the cf_device_page_descriptor payload."""
+    k_payload: np.ndarray
+    v_payload: np.ndarray
+    k_scales: np.ndarray
+    v_scales: np.ndarray
+    token_begin: int
+    token_count: int
+
+
+def nib_seal(x: np.ndarray, block_size: int):
+    """Seal one fp32 stream (reference src/cuda/device_kv_seal_attention.cu:72-113). Returns (payload u8, scales
+    f32, saturated) or raises ValueError naming the NaN/Inf counts."""
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    nb = (x.size + block_size - 1) // block_size
+    payload = np.zeros((x.size + 1) // 2, np.uint8)
+    scales = np.zeros(nb, np.float32)
+    sat, nan, inf = (np.zeros(1, np.uint64) for _ in range(3))
+    rc = lib().or_nib_seal(_ptr(x), x.size, block_size, _ptr(payload), _ptr(scales), _ptr(sat), _ptr(nan), _ptr(inf))
+    if rc != 0:
+        raise ValueError(f"page rejected: {int(nan[0])} NaN, {int(inf[0])} Inf")
+    return payload, scales, int(sat[0])
+
+
+def nib_seal_page(k: np.ndarray, v: np.ndarray, token_begin: int, block_size: int) -> NibPage:
+    """Seal K and V [tokens, kv_heads, head_dim] fp32 into one page."""
+    kp, ks, _ = nib_seal(k, block_size)
+    vp, vs, _ = nib_seal(v, block_size)
+    return NibPage(kp, vp, ks, vs, token_begin, int(k.shape[0]))
+
+
+def nib_dequant(payload: np.ndarray, scales: np.ndarray, values: int, block_size: int) -> np.ndarray:
+    """(symbol - 8) * scale[i // block] for i < values (float64)."""
+    sym = np.empty(values, np.int64)
+    sym[0::2] = payload[: (values + 1) // 2] & 0x0F
+    sym[1::2] = payload[: values // 2] >> 4
+    return (sym - 8).astype(np.float64) * scales[np.arange(values) // block_size].astype(np.float64)
+
+
+def nib_attention(pages: list, block_size: int, q: np.ndarray, query_begin: int, kv_heads: int, gqa: int,
+                  scale: float, window: int = 0, active_k=None, active_v=None, active_begin: int = 0) -> np.ndarray:
+    """Attention of q [q_tokens, kv_heads * gqa, head_dim] over sealed pages then the fp32 active page
+    (reference device_kv_seal_attention.cu:116-187), float64 accumulation; returns float32."""
+    q = np.ascontiguousarray(q, np.float32)
+    qt, _, D = q.shape
+    out = np.zeros_like(q)
+    arr = lambda xs, t: (t * len(xs))(*[x.ctypes.data for x in xs]) if xs else None
+    keep = [p.k_payload for p in pages] + [p.v_payload for p in pages]
+    tb = np.array([p.token_begin for p in pages] or [0], np.uint32)
+    tc = np.array([p.token_count for p in pages] or [0], np.uint32)
+    ak = None if active_k is None else np.ascontiguousarray(active_k, np.float32)
+    av = None if active_v is None else np.ascontiguousarray(active_v, np.float32)
+    acount = 0 if ak is None else int(ak.shape[0])
+    lib().or_nib_attention(len(pages), arr([p.k_payload for p in pages], C.c_void_p),
+                           arr([p.v_payload for p in pages], C.c_void_p), arr([p.k_scales for p in pages], C.c_void_p),
+                           arr([p.v_scales for p in pages], C.c_void_p), _ptr(tb), _ptr(tc), block_size, _ptr(ak),
+                           _ptr(av), active_begin, acount, _ptr(q), qt, query_begin, kv_heads, gqa, D, scale, window,
+                           _ptr(out))
+    del keep
+    return out
 
 
 def ref_lib() -> C.CDLL | None:

@@ -11,6 +11,9 @@
 #include "chromofold/chromofold_kv_adapter.h"
 #include "chromofold/chromofold_qw.h"
 #include "chromofold/chromofold_search.h"
+#include "chromofold/device_kv_dataplane.h"
+#include "chromofold/device_kv_seal_attention.h"
+#include "chromofold/multisequence_cuda_resolver.h"
 #include "chromofold/kv_codec_ext.h"
 #include "chromofold/kv_cuda.h"
 #include "chromofold/kv_runtime.h"
@@ -116,6 +119,31 @@ int main(void) {
     expect("cf_fm_file_read_header", cf_fm_file_read_header(NULL, &fh), INV);
     expect("cf_fm_file_read", cf_fm_file_read("x", &fh, NULL, NULL), INV);
     expect("cf_fm_file_write", cf_fm_file_write(NULL, &fh, NULL, NULL), INV);
+  }
+  {
+    printf("sizeof cf_device_tensor_view %zu\n", sizeof(cf_device_tensor_view));
+    printf("sizeof cf_device_page_descriptor %zu\n", sizeof(cf_device_page_descriptor));
+    printf("sizeof cf_device_seal_counters %zu\n", sizeof(cf_device_seal_counters));
+    printf("sizeof cf_device_kv_counters %zu\n", sizeof(cf_device_kv_counters));
+    printf("sizeof cf_ms_page_publication %zu\n", sizeof(cf_ms_page_publication));
+    printf("sizeof cf_ms_batch_item %zu\n", sizeof(cf_ms_batch_item));
+    printf("sizeof cf_ms_cuda_counters %zu\n", sizeof(cf_ms_cuda_counters));
+    cf_device_tensor_view tv;
+    memset(&tv, 0, sizeof tv);
+    expect("cf_device_tensor_validate", cf_device_tensor_validate(&tv), -1);
+    expect("cf_device_seal_create", cf_device_seal_create(NULL) == NULL, 1);
+    expect("cf_device_seal_full_page_async", cf_device_seal_full_page_async(NULL, 0, NULL), -1);
+    expect("cf_device_seal_attention_async",
+           cf_device_seal_attention_async(NULL, 0, NULL, NULL, 3, 0, 0, 0, 0, 1.0f, 0, NULL), -1);
+    expect("cf_device_seal_set_fault", cf_device_seal_set_fault(NULL, 0), -1);
+    expect("cf_device_seal_get_pages", cf_device_seal_get_pages(NULL, 0, NULL, 0, NULL), -1);
+    expect("cf_device_kv_create", cf_device_kv_create(NULL) == NULL, 1);
+    expect("cf_device_kv_append_async", cf_device_kv_append_async(NULL, 0, 0, NULL, NULL, NULL), -1);
+    expect("cf_device_kv_attention_async", cf_device_kv_attention_async(NULL, 0, NULL, NULL, 1, 0, 1.0f, 0, NULL), -1);
+    expect("cf_ms_cuda_create", cf_ms_cuda_create(NULL) == NULL, 1);
+    expect("cf_ms_cuda_execute_batch_async", cf_ms_cuda_execute_batch_async(NULL, NULL, 0, NULL), -1);
+    expect("cf_ms_cuda_audit", cf_ms_cuda_audit(NULL), -1);
+    expect("cf_ms_cuda_last_error", cf_ms_cuda_last_error(NULL) != NULL, 1);
   }
   printf("%s (%d failure%s)\n", failures ? "FAIL" : "PASS", failures, failures == 1 ? "" : "s");
   return failures ? 1 : 0;

@@ -68,12 +68,18 @@ def test_c_headers_link_and_null_contract(tmp_path):
     assert r.returncode == 0, r.stdout + r.stderr
     assert "PASS" in r.stdout
     from chromofold_amd import _abi as A
-    from chromofold_amd import kv, qw, search
+    from chromofold_amd import kv, qw, search, sealkv
     mirrors = {"cf_wavelet_view": A.cf_wavelet_view, "cf_rrrw_view": A.cf_rrrw_view, "cf_fm_view": A.cf_fm_view,
                "cf_kv_device_page": A.cf_kv_device_page, "cf_kv_paged_attention_desc": A.cf_kv_paged_attention_desc,
                "cf_kv_batched_desc": kv.cf_kv_batched_desc, "cf_qw_matrix": qw.cf_qw_matrix,
                "cf_rrrw_file_header": search.cf_rrrw_file_header, "cf_fm_file_header": search.cf_fm_file_header,
-               "cf_fm_file_arrays": search.cf_fm_file_arrays}
+               "cf_fm_file_arrays": search.cf_fm_file_arrays,
+               "cf_device_tensor_view": sealkv.cf_device_tensor_view,
+               "cf_device_page_descriptor": sealkv.cf_device_page_descriptor,
+               "cf_device_seal_counters": sealkv.cf_device_seal_counters,
+               "cf_device_kv_counters": sealkv.cf_device_kv_counters,
+               "cf_ms_page_publication": sealkv.cf_ms_page_publication,
+               "cf_ms_batch_item": sealkv.cf_ms_batch_item, "cf_ms_cuda_counters": sealkv.cf_ms_cuda_counters}
     sizes = dict(re.findall(r"^sizeof (\w+) (\d+)$", r.stdout, flags=re.M))
     assert set(sizes) == set(mirrors)
     for name, cls in mirrors.items():
