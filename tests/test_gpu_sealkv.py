@@ -235,7 +235,8 @@ def test_dataplane_append_seal_attend(dev):
     np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-3, atol=1e-4)
     c = dp.counters()
     assert c["seal_successes"] == 2 and c["device_append_calls"] == 4
-    assert c["bf16_values_converted"] == 11 * kvh * D and c["fp16_values_converted"] == 10 * kvh * D
+    # K and V are counted separately, as in reference src/cuda/device_kv_dataplane.cu:163-180
+    assert c["bf16_values_converted"] == 2 * 11 * kvh * D and c["fp16_values_converted"] == 2 * 10 * kvh * D
     dp.clear()
     dp.close()
 
