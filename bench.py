@@ -352,6 +352,116 @@ def bench_seal(steps: int, warmup: int, cpu: bool = True, seqs: int = 32, tokens
     return res
 
 
+# ------------------------------------------------------------------------------------------------ int4 nibble pages
+def _d2h(ptr: int, nbytes: int) -> np.ndarray:
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    out = np.empty(nbytes, np.uint8)
+    assert hip.hipMemcpy(out.ctypes.data, ptr, nbytes, 2) == 0  # device to host
+    return out
+
+
+def _nib_dequant(payload: np.ndarray, scales: np.ndarray, bs: int) -> np.ndarray:
+    sym = np.empty(payload.size * 2, np.int64)
+    sym[0::2] = payload & 0x0F
+    sym[1::2] = payload >> 4
+    return (sym - 8) * scales.astype(np.float64)[np.arange(sym.size) // bs]
+
+
+def bench_nibble(steps: int, warmup: int, cpu: bool = True, seqs: int = 32, tokens: int = 32768, page: int = 64,
+                 bs: int = 32) -> dict:
+    """Batched decode over int4 nibble pages through the multi-sequence resolver (cf_ms_cuda_execute_batch_async):
+    C4 shape (32 sequences x 32768 tokens, 8 KV / 32 q heads, hd 128), pages of 64 tokens sealed on the device by
+    the seal engine (block 32), published to 32 resolver sequences; one step = one batch of 32 decode items (one
+    attention launch + one merge launch). Gate: sequence 0 against a float64 numpy softmax over its pages'
+    dequantised bytes (read back from HBM). CPU baseline: the oracle's attention on a 4096-token sample."""
+    import ctypes as C
+    import torch
+    from chromofold_amd import _abi as A
+    from chromofold_amd import sealkv as SK
+
+    H, QH, D = 8, 32, 128
+    gqa = QH // H
+    sc = 1.0 / np.sqrt(D)
+    npg = tokens // page
+    eng = SK.SealEngine(seqs, H, QH, D, page, bs)
+    res_ = SK.MsResolver(1, H, QH, D, page)
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(0x5EA1)
+    t0 = time.perf_counter()
+    for s in range(seqs):
+        res_.create(s)
+        for p in range(npg):
+            kv_ = torch.randn((2, page, H, D), generator=gen, device="cuda:0")
+            eng.stage(s, p * page, kv_[0], kv_[1])
+            eng.seal(s)
+        for d in eng.pages(s):
+            res_.publish(s, 0, d)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
+    q = torch.randn((seqs, 1, QH, D), generator=gen, device="cuda:0")
+    out = torch.empty_like(q)
+    arr = (SK.cf_ms_batch_item * seqs)()
+    for s in range(seqs):
+        op, ot, ots, ohs, oes = SK._out_args(out[s])
+        arr[s] = SK.cf_ms_batch_item(s, 0, SK.tensor_view(q[s]), op, ot, ots, ohs, oes, tokens - 1, sc, 0)
+    L = A.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        if L.cf_ms_cuda_execute_batch_async(res_.h, arr, seqs, stream) != 0:
+            raise RuntimeError(L.cf_ms_cuda_last_error(res_.h).decode())
+
+    step()
+    torch.cuda.synchronize()
+    # gate: sequence 0 in float64 from the sealed bytes
+    descs = eng.pages(0)
+    vals = page * H * D
+    Kd = np.concatenate([_nib_dequant(_d2h(d.key_payload, vals // 2), _d2h(d.key_scales, vals // bs * 4).view(
+        np.float32), bs) for d in descs]).reshape(tokens, H, D)
+    Vd = np.concatenate([_nib_dequant(_d2h(d.value_payload, vals // 2), _d2h(d.value_scales, vals // bs * 4).view(
+        np.float32), bs) for d in descs]).reshape(tokens, H, D)
+    qh = q[0, 0].double().cpu().numpy()
+    ref = np.empty((QH, D))
+    for h in range(QH):
+        sco = Kd[:, h // gqa] @ qh[h] * sc
+        w = np.exp(sco - sco.max())
+        ref[h] = w @ Vd[:, h // gqa] / w.sum()
+    got = out[0, 0].double().cpu().numpy()
+    err = float(np.linalg.norm(got - ref) / np.linalg.norm(ref))
+    assert err <= 1e-3, err
+    wall, per = _events_time(step, steps, warmup)
+    torch.cuda.synchronize()
+    res_.reclaim()
+    t = float(np.mean(per)) * 1e-3
+    page_bytes = sum(d.resident_bytes for s in range(seqs) for d in eng.pages(s))
+    step_bytes = page_bytes + seqs * npg * C.sizeof(SK.cf_device_page_descriptor) + q.numel() * 4 * 2
+    r = {"workload": f"{seqs} seqs x {tokens} tokens, int4 nibble pages of {page} tokens (block {bs}), 32 q / 8 kv "
+                     f"heads, hd {D}, one batch of {seqs} decode items per step",
+         "tokens_per_s": seqs / t, "ms_per_step": t * 1e3, "page_bytes": page_bytes,
+         "bits_per_value": page_bytes * 8 / (2 * seqs * tokens * H * D), "hbm_gbs": step_bytes / t / 1e9,
+         "roofline_frac": step_bytes / t / 1e9 / HBM_PEAK_GBS, "seq0_normwise_err": err, "build_s": build_s}
+    if cpu:
+        import oracle as O
+        ns = 4096
+        pages = []
+        for i, d in enumerate(descs[: ns // page]):
+            pages.append(O.NibPage(_d2h(d.key_payload, vals // 2), _d2h(d.value_payload, vals // 2),
+                                   _d2h(d.key_scales, vals // bs * 4).view(np.float32),
+                                   _d2h(d.value_scales, vals // bs * 4).view(np.float32), i * page, page))
+        qn = q[0].cpu().numpy()
+        t1 = time.perf_counter()
+        O.nib_attention(pages, bs, qn, ns - 1, H, gqa, sc)
+        dt = (time.perf_counter() - t1) * tokens / ns
+        r["cpu_baseline"] = {"value": 1.0 / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+                             "sample": f"oracle attention (float64) of one decode token over {ns} tokens, scaled "
+                                       f"to {tokens}"}
+    res_.close()
+    eng.close()
+    return r
+
+
 # ------------------------------------------------------------------------------------------------ long context (C5)
 def bench_c5(steps: int, warmup: int) -> dict:
     """C4 shapes (8 KV / 32 q heads, hd 128, rANS-hybrid pages). (a) 256 sequences sharing one 8192-token prefix
@@ -449,7 +559,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="auto", choices=["auto", "kv", "rrr", "copy", "c5", "seal"])
+    ap.add_argument("--workload", default="auto", choices=["auto", "kv", "rrr", "copy", "c5", "seal", "nibble"])
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -472,6 +582,9 @@ def main() -> int:
     if args.workload == "c5":
         print(json.dumps({"c5": bench_c5(args.steps, args.warmup)}))
         return 0
+    if args.workload == "nibble":
+        print(json.dumps({"nibble_pages": bench_nibble(args.steps, args.warmup, cpu=not args.no_cpu)}))
+        return 0
     if args.workload in ("auto", "kv"):
         kvr = bench_kv(args.steps, args.warmup, cpu=not args.no_cpu, check_seqs=0 if args.no_cpu else 2)
         rrr = bench_rrr(args.steps, args.warmup, cpu=not args.no_cpu)
@@ -485,6 +598,7 @@ def main() -> int:
         secondary["c3_matmul"] = bench_qw(min(args.steps, 50), 3)
         secondary["c5_long_context"] = bench_c5(min(args.steps, 20), 2)
         secondary["device_seal"] = bench_seal(min(args.steps, 20), 2, cpu=not args.no_cpu)
+        secondary["nibble_pages"] = bench_nibble(min(args.steps, 20), 2, cpu=not args.no_cpu)
         cp = bench_copy(10, 2)
         secondary["stream_copy_gbs"] = cp["stream_copy_gbs"]
         secondary["roofline_frac_of_stream_copy"] = kvr["roofline"]["achieved"] / cp["stream_copy_gbs"]
