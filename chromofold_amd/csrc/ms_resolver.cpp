@@ -62,6 +62,8 @@ struct LayerState {
   DeviceBuffer active_k, active_v;
   uint32_t active_begin = 0, active_count = 0;
   uint64_t active_generation = 0;
+  uint32_t block_size = 0;  // the block size of every page of the layer
+  bool vector_only = false;  // mixed block sizes, or payloads not 16-byte aligned: the VALU attention kernel
 };
 
 struct SequenceState {
@@ -77,6 +79,7 @@ struct PendingBatch {
 };
 
 bool aligned4(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
 
@@ -214,11 +217,18 @@ extern "C" int cf_ms_cuda_publish_page_async(cf_ms_cuda_resolver *r, const cf_ms
     page.logical_refs = 1;
     r->pages.emplace(page.id, page);
     LayerState &layer = seq->second.layers[pub->layer];
+    const uint32_t bs_before = layer.block_size;
+    const bool vector_before = layer.vector_only;
+    if (layer.pages.empty()) layer.block_size = d.block_size;
+    else if (layer.block_size != d.block_size) layer.vector_only = true;
+    if (!aligned16(d.key_payload) || !aligned16(d.value_payload)) layer.vector_only = true;
     layer.pages.push_back({page.id, int64_t(d.token_begin)});
     try {
       r->refresh_table(layer, static_cast<hipStream_t>(stream));
     } catch (...) {
       layer.pages.pop_back();
+      layer.block_size = bs_before;
+      layer.vector_only = vector_before;
       r->pages.erase(page.id);
       throw;
     }
@@ -277,6 +287,8 @@ extern "C" int cf_ms_cuda_copy_sequence_async(cf_ms_cuda_resolver *r, int64_t so
       const LayerState &from = src->second.layers[li];
       LayerState &to = cand.layers[li];
       to.pages = from.pages;
+      to.block_size = from.block_size;
+      to.vector_only = from.vector_only;
       for (const auto &ref : to.pages) {
         ++r->pages.at(ref.page_id).logical_refs;
         acquired.push_back(ref.page_id);
@@ -398,11 +410,12 @@ extern "C" int cf_ms_cuda_execute_batch_async(cf_ms_cuda_resolver *r, const cf_m
       q.query_begin = it.query_token_begin;
       q.window = it.causal_window;
       q.softmax_scale = it.softmax_scale;
+      q.block_size = layer.vector_only ? 0u : layer.block_size;
     }
     ++r->counters.server_batches_received;
     r->counters.tokens_per_batch_peak = std::max<uint64_t>(r->counters.tokens_per_batch_peak, item_count);
     const cfnib::AttnShape sh{r->config.kv_head_count, r->config.query_head_count, r->config.gqa_group_size,
-                              r->config.head_dim};
+                              r->config.head_dim, r->config.page_size};
     std::string err;
     const hipError_t st = r->runner.run(reqs, sh, s, err);
     if (st != hipSuccess)

@@ -285,12 +285,13 @@ __global__ __launch_bounds__(256) void nib_attn_kernel(const AttnItem *__restric
     for (int e = 0; e < 8; ++e) st.acc[j][e] = 0.0f;
   }
 
-  const uint32_t page_splits = (it.page_count + it.pages_per_split - 1u) / it.pages_per_split;
+  const uint32_t page_splits = it.page_splits;
+  if (it.mfma_nb && split < page_splits) return;  // the MFMA kernel reads these pages
   const uint32_t words_per_token = kvh * (D / 8u);
   const uint32_t lane_word = h * (D / 8u) + c;
   if (split < page_splits) {
-    const uint32_t p_end = min(it.page_count, (split + 1u) * it.pages_per_split);
-    for (uint32_t p = split * it.pages_per_split; p < p_end; ++p) {
+    const uint32_t p_end = min(it.page_count, (split + 1u) * it.units_per_split);
+    for (uint32_t p = split * it.units_per_split; p < p_end; ++p) {
       const cf_device_page_descriptor &pg = it.pages[p];
       const uint32_t tcount = pg.token_count, tbegin = pg.token_begin, bs = pg.block_size;
       const uint32_t *kw = reinterpret_cast<const uint32_t *>(pg.key_payload);
@@ -486,15 +487,25 @@ hipError_t AttnRunner::run(const std::vector<AttnRequest> &reqs, const AttnShape
   const uint32_t hw = std::min(sh.kv_heads, 256u / lg);
   const uint32_t hgroups = (sh.kv_heads + hw - 1u) / hw;
 
-  // pages per split: aim at about 2048 workgroups over the whole batch, at most 64 pages per split
-  uint64_t page_work = 0;
-  for (const auto &r : reqs) page_work += uint64_t(r.page_count) * r.query.token_count;
-  page_work *= uint64_t(hgroups) * qchunks;
+  // context splits: aim at about 2048 workgroups over the whole batch
+  uint64_t page_work = 0, tile_work = 0;
+  const uint32_t cpp = (sh.page_size + 15u) / 16u;  // 16-token chunks per page (MFMA kernel)
+  std::vector<uint32_t> nb(reqs.size());
+  for (size_t i = 0; i < reqs.size(); ++i) {
+    const auto &r = reqs[i];
+    nb[i] = mfma_sets(D, r.block_size);
+    if (nb[i]) tile_work += uint64_t((r.page_count * cpp + 3u) / 4u) * r.query.token_count * ((sh.gqa + 3u) / 4u);
+    else page_work += uint64_t(r.page_count) * r.query.token_count * hgroups * qchunks;
+  }
   const uint32_t pps = static_cast<uint32_t>(std::clamp<uint64_t>((page_work + 2047u) / 2048u, 1u, 64u));
+  // the MFMA kernel's workgroups take four 64-slot tiles per round (one per wave), KV head by KV head
+  const uint32_t tps = static_cast<uint32_t>(
+      std::clamp<uint64_t>((tile_work * sh.kv_heads + 2047u) / 2048u, 4u, 256u));
 
   std::vector<AttnItem> items(reqs.size());
   uint64_t floats = 0;
-  uint32_t max_split = 1, max_qtok = 1;
+  uint32_t max_split = 1, max_qtok = 1, max_mfma_split = 0;
+  bool any_nb[5] = {false, false, false, false, false};
   for (size_t i = 0; i < reqs.size(); ++i) {
     const AttnRequest &r = reqs[i];
     AttnItem &it = items[i];
@@ -511,7 +522,17 @@ hipError_t AttnRunner::run(const std::vector<AttnRequest> &reqs, const AttnShape
     it.o_type = r.output_type;
     it.pages = r.pages;
     it.page_count = r.page_count;
-    it.pages_per_split = pps;
+    it.mfma_nb = nb[i];
+    if (nb[i]) {
+      const uint32_t tiles = (r.page_count * cpp + 3u) / 4u;
+      it.units_per_split = tps;
+      it.page_splits = (tiles + tps - 1u) / tps;
+      max_mfma_split = std::max(max_mfma_split, it.page_splits);
+      any_nb[nb[i]] = true;
+    } else {
+      it.units_per_split = pps;
+      it.page_splits = (r.page_count + pps - 1u) / pps;
+    }
     it.active_k = r.active_k;
     it.active_v = r.active_v;
     it.active_begin = r.active_begin;
@@ -520,7 +541,7 @@ hipError_t AttnRunner::run(const std::vector<AttnRequest> &reqs, const AttnShape
     it.window = r.window;
     it.scale_log2 = r.softmax_scale * 1.4426950408889634f;
     it.pad = 0;
-    it.nsplit = (r.page_count + pps - 1u) / pps + (it.active_count > 0u ? 1u : 0u);
+    it.nsplit = it.page_splits + (it.active_count > 0u ? 1u : 0u);
     if (it.nsplit == 0u) it.nsplit = 1u;  // nothing visible: one empty split, the row comes out 0
     it.ws_offset = floats;
     floats += uint64_t(it.nsplit) * it.q_tokens * sh.q_heads * (D + 4u);
@@ -564,6 +585,12 @@ hipError_t AttnRunner::run(const std::vector<AttnRequest> &reqs, const AttnShape
     default: e = launch_attn_lg<32>(G, grid, block, stream, d_items, sh, hw, hgroups, qchunks, partials); break;
   }
   if (e != hipSuccess) return e;
+  for (uint32_t n : {1u, 2u, 4u}) {
+    if (!any_nb[n]) continue;
+    e = launch_nib_mfma(n, d_items, static_cast<uint32_t>(items.size()), max_mfma_split, max_qtok, sh, partials,
+                        stream);
+    if (e != hipSuccess) return e;
+  }
   nib_merge_kernel<<<dim3(sh.q_heads, max_qtok, static_cast<uint32_t>(items.size())), 64, 0, stream>>>(d_items, sh,
                                                                                                      partials);
   e = hipPeekAtLastError();

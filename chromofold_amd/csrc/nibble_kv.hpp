@@ -47,7 +47,10 @@ struct AttnItem {
   uint64_t o_token_stride, o_head_stride, o_elem_stride;
   uint32_t o_type, nsplit;
   const cf_device_page_descriptor *pages;
-  uint32_t page_count, pages_per_split;
+  uint32_t page_count;
+  uint32_t units_per_split;  // pages (VALU kernel) or 64-token tiles (MFMA kernel) per context split
+  uint32_t page_splits;      // splits over the sealed pages; split page_splits is the active page (when present)
+  uint32_t mfma_nb;          // 0: the VALU kernel reads the pages; 1/2/4: the MFMA kernel, scale blocks per row
   const float *active_k;
   const float *active_v;
   uint32_t active_begin, active_count;
@@ -59,7 +62,20 @@ struct AttnItem {
 
 struct AttnShape {
   uint32_t kv_heads, q_heads, gqa, head_dim;
+  uint32_t page_size;  // tokens per page (pages may hold fewer)
 };
+
+// Scale blocks per 128-dim row for the MFMA path (0 = not eligible): block_size 32 / 64 / any multiple of 128.
+inline uint32_t mfma_sets(uint32_t head_dim, uint32_t block_size) {
+  if (head_dim != 128 || block_size == 0) return 0;
+  if (block_size == 32) return 4;
+  if (block_size == 64) return 2;
+  return block_size % 128 == 0 ? 1 : 0;
+}
+
+// Launch of the MFMA kernel over the items whose mfma_nb == nb (nibble_mfma.hip).
+hipError_t launch_nib_mfma(uint32_t nb, const AttnItem *items, uint32_t nitems, uint32_t max_page_splits,
+                           uint32_t max_qtok, const AttnShape &sh, float *ws, hipStream_t stream);
 
 // Host description of one request before splitting.
 struct AttnRequest {
@@ -73,6 +89,7 @@ struct AttnRequest {
   uint32_t active_begin, active_count;
   uint32_t query_begin, window;
   float softmax_scale;
+  uint32_t block_size;  // the block size of every page of the request, 0 when mixed or unknown
 };
 
 // Runs a batch of requests: one split-context attention launch over every item, then one merge launch.

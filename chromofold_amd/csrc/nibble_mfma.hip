@@ -1,0 +1,366 @@
+// nibble_mfma.hip — attention over sealed int4 nibble pages on the matrix cores (head_dim 128).
+//
+// Same contract as nib_attn_kernel (nibble_kv.hip) for the sealed pages of an item: key position p counts for query
+// position P when p <= P and, with a window w > 0, p + w > P; softmax with a running maximum in log2 units; the
+// split partials (m, l, unnormalised acc) go to the same workspace rows, and the same merge kernel finishes them.
+// The item's active fp32 page stays with the VALU kernel.
+//
+// Layout. A workgroup = 4 wavefronts serves one (item, query token, KV head, group of 4 query heads, context
+// split); each wavefront walks 64-slot tiles = four 16-token chunks of pages (chunk G of a tile on lanes
+// 16G..16G+15, a page of N tokens giving ceil(N/16) chunks).
+//   staging:  global_load_lds copies a chunk's 16 K rows and 16 V rows of this KV head (64 B each) into LDS, the
+//             four 16-byte pieces of row r stored in the order piece ^ (r & 3) so that the lanes' row reads below
+//             hit different banks; the next tile's copies and its lanes' scales are in flight while the current
+//             tile is computed.
+//   K phase:  lane = token. Each 4-dim quad of the lane's row becomes the f16 B operand of v_mfma_f32_4x4x4f16
+//             (nibble - 8, exact: 0x6400 | nibble is 1024 + nibble in f16, then one packed f16 subtract of 1032 per
+//             two values), with the 4 query heads (split into f16 hi + lo for fp32-grade scores) broadcast as the A
+//             operand, accumulating one score per head in the lane. One accumulator pair per scale block of the row
+//             (the page's block size is 32, 64 or a multiple of 128): score = sum over blocks of k_scale * acc.
+//   softmax:  one running maximum per head for the wavefront; p goes to LDS with the tokens' V scales.
+//   V phase:  lane (G, t) owns dims 8t..8t+7 of chunk G's tokens: it reads word t of four rows, transposes the
+//             4 x 8 nibbles with v_perm into eight f16 B operands (4 tokens x 1 dim), and the A operand is p times
+//             the V scale of its 32-dim block for those 4 tokens, as f16 hi + lo.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <utility>
+
+#include "nibble_kv.hpp"
+
+namespace cfnib {
+namespace {
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kD = 128;
+constexpr int kWaves = 4;
+constexpr uint32_t kRowBytes = kD / 2;                    // nibbles of one token's row of one KV head
+constexpr uint32_t kChunkStride = 16 * kRowBytes + 64;   // staged 16-row chunk + a bank offset between chunks
+constexpr uint32_t kTileBytes = 4 * kChunkStride;
+constexpr float kOff = 1032.0f;                           // operand 1024 + nibble, value nibble - 8
+constexpr float kNegInf = -__builtin_huge_valf();
+
+__device__ inline half4_t as_half4(uint32_t lo, uint32_t hi) {
+  half4_t h;
+  uint32_t *w = reinterpret_cast<uint32_t *>(&h);
+  w[0] = lo;
+  w[1] = hi;
+  return h;
+}
+
+// Two f16 lanes holding 1024 + n (the 0x6400 | n bit trick) -> n - 8, exact, in one packed f16 add.
+__device__ inline uint32_t minus_1032(uint32_t x) {
+  half2_t h = __builtin_bit_cast(half2_t, x);
+  h = h - half2_t{static_cast<_Float16>(kOff), static_cast<_Float16>(kOff)};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+// x = four nibbles n0 | n1 << 4 | n2 << 8 | n3 << 12 (x < 65536)  ->  (n0 - 8, ..., n3 - 8) as f16
+__device__ inline half4_t nib_quad(uint32_t x) {
+  const uint32_t lo = (((x << 12) | x) & 0x000F000Fu) | 0x64006400u;
+  const uint32_t hi = (((x << 4) | (x >> 8)) & 0x000F000Fu) | 0x64006400u;
+  return as_half4(minus_1032(lo), minus_1032(hi));
+}
+
+__device__ inline float load_q(const void *base, uint32_t type, uint64_t off) {
+  const char *p = static_cast<const char *>(base) + off;
+  if (type == CF_DEVICE_F16) return static_cast<float>(*reinterpret_cast<const _Float16 *>(p));
+  if (type == CF_DEVICE_BF16) return __uint_as_float(uint32_t(*reinterpret_cast<const uint16_t *>(p)) << 16);
+  return *reinterpret_cast<const float *>(p);
+}
+
+__device__ inline void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int NB>
+__global__ __launch_bounds__(256) void nib_mfma_kernel(const AttnItem *__restrict__ items, AttnShape sh,
+                                                       uint32_t qchunks, float *__restrict__ ws) {
+  __shared__ __attribute__((aligned(16))) uint8_t s_kv[kWaves][2][2][kTileBytes];  // [wave][buffer][K, V]
+  __shared__ __attribute__((aligned(16))) float s_p[kWaves][4][64];                // p per [head][slot]
+  __shared__ float s_vs[kWaves][64][NB];                                           // V scales per slot
+  const AttnItem &it = items[blockIdx.z];
+  if (it.mfma_nb != static_cast<uint32_t>(NB)) return;
+  const uint32_t split = blockIdx.x;
+  if (split >= it.page_splits) return;
+  const uint32_t kvh = sh.kv_heads, gqa = sh.gqa;
+  const uint32_t per_tok = qchunks * kvh;
+  const uint32_t qt = blockIdx.y / per_tok;
+  if (qt >= it.q_tokens) return;
+  const uint32_t rest = blockIdx.y - qt * per_tok;
+  const uint32_t h = rest / qchunks, qc = rest - h * qchunks;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int G = lane >> 4, t = lane & 15;
+  const uint32_t qpos = it.q_begin + qt;
+  const uint32_t window = it.window;
+
+  // ---- queries (scaled to log2 units) as f16 hi + lo in LDS, then in registers
+  _Float16(*s_q)[4][kD] = reinterpret_cast<_Float16(*)[4][kD]>(&s_kv[0][0][0][0]);
+  for (int i = threadIdx.x; i < 4 * kD; i += 256) {
+    const int j = i / kD, dd = i % kD;
+    float q = 0.0f;
+    if (qc * 4 + j < gqa)
+      q = load_q(it.q, it.q_type, uint64_t(qt) * it.q_token_stride + uint64_t(h * gqa + qc * 4 + j) * it.q_head_stride +
+                                       uint64_t(dd) * it.q_elem_stride) *
+          it.scale_log2;
+    const _Float16 hi = static_cast<_Float16>(q);
+    s_q[0][j][dd] = hi;
+    s_q[1][j][dd] = static_cast<_Float16>(q - static_cast<float>(hi));
+  }
+  __syncthreads();
+  half4_t qhi[2], qlo[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int qd = 16 * c + (lane >> 2);
+    qhi[c] = *reinterpret_cast<const half4_t *>(&s_q[0][lane & 3][4 * qd]);
+    qlo[c] = *reinterpret_cast<const half4_t *>(&s_q[1][lane & 3][4 * qd]);
+  }
+  __syncthreads();  // the query staging aliases wave 0's tile buffers
+
+  const uint32_t cpp = (sh.page_size + 15u) / 16u;
+  const uint32_t nchunks = it.page_count * cpp;
+  const uint32_t ntiles = (nchunks + 3u) / 4u;
+  const uint32_t tb = split * it.units_per_split;
+  const uint32_t te = min(ntiles, tb + it.units_per_split);
+  const cf_device_page_descriptor *pages = it.pages;
+
+  float m_run[4], l_run[4];
+  float4_t acc[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    m_run[j] = kNegInf;
+    l_run[j] = 0.0f;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = float4_t{0, 0, 0, 0};
+
+  // per-lane metadata of the tile in flight: this lane's token (row of chunk G), its visibility and scales
+  bool n_ok = false;
+  float n_ks[NB], n_vs[NB];
+#pragma unroll
+  for (int s = 0; s < NB; ++s) n_ks[s] = n_vs[s] = 0.0f;
+
+  // copies of tile `tile` into buffer `buf` + this lane's metadata for it
+  auto stage = [&](uint32_t tile, int buf) {
+    n_ok = false;
+#pragma unroll
+    for (int C = 0; C < 4; ++C) {
+      const uint32_t ch = 4u * tile + C;
+      if (ch >= nchunks) break;  // wave-uniform
+      const uint32_t p = ch / cpp, off = (ch - p * cpp) * 16u;
+      const cf_device_page_descriptor &pg = pages[p];
+      const uint32_t tc = pg.token_count;
+      if (off >= tc) continue;  // a partial page's empty chunk: its slots stay masked
+      const uint32_t r = static_cast<uint32_t>(lane) >> 2, piece = (lane & 3) ^ (r & 3);
+      const uint32_t row = min(off + r, tc - 1u);  // slots past the page's tokens re-read its last row
+      const uint64_t goff = (uint64_t(row) * kvh + h) * kRowBytes + 16u * piece;
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t *>(pg.key_payload + goff),
+                                       (__attribute__((address_space(3))) void *)(&s_kv[wave][buf][0][C * kChunkStride]),
+                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t *>(pg.value_payload + goff),
+                                       (__attribute__((address_space(3))) void *)(&s_kv[wave][buf][1][C * kChunkStride]),
+                                       16, 0, 0);
+      if (G == C) {
+        const uint32_t tok = off + static_cast<uint32_t>(t);
+        const uint32_t pos = pg.token_begin + tok;
+        n_ok = tok < tc && pos <= qpos && (window == 0u || uint64_t(pos) + window > qpos);
+        const uint32_t srow = min(tok, tc - 1u);
+        const uint64_t base = (uint64_t(srow) * kvh + h) * kD;
+        const uint32_t bs = pg.block_size;
+#pragma unroll
+        for (int s = 0; s < NB; ++s) {
+          const uint64_t bi = (base + uint64_t(s) * (kD / NB)) / bs;
+          n_ks[s] = pg.key_scales[bi];
+          n_vs[s] = pg.value_scales[bi];
+        }
+      }
+    }
+  };
+
+  int cur = 0;
+  uint32_t tile = tb + wave;
+  if (tile < te) stage(tile, 0);
+  for (; tile < te; tile += kWaves) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this tile's rows and the lane's scales have landed
+    wave_sync_lds();
+    const bool tok_ok = n_ok;
+    float ks[NB], vs[NB];
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+      ks[s] = n_ks[s];
+      vs[s] = n_vs[s];
+    }
+    if (tile + kWaves < te) stage(tile + kWaves, cur ^ 1);
+
+    // ---- K: one score per head for this lane's token
+    float4_t sa[NB], sb[NB];
+#pragma unroll
+    for (int s = 0; s < NB; ++s) sa[s] = sb[s] = float4_t{0, 0, 0, 0};
+    {
+      const uint8_t *kb = &s_kv[wave][cur][0][G * kChunkStride + t * kRowBytes];
+      uint4 pc[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) pc[k] = *reinterpret_cast<const uint4 *>(kb + 16 * (k ^ (t & 3)));
+      const uint32_t w16[16] = {pc[0].x, pc[0].y, pc[0].z, pc[0].w, pc[1].x, pc[1].y, pc[1].z, pc[1].w,
+                                pc[2].x, pc[2].y, pc[2].z, pc[2].w, pc[3].x, pc[3].y, pc[3].z, pc[3].w};
+      constexpr int QPS = 32 / NB;  // quads per scale block
+      [&]<int... Q>(std::integer_sequence<int, Q...>) {
+        (
+            [&] {
+              constexpr int q = Q;  // quad = dims 4q..4q+3
+              const uint32_t w = w16[q / 2];
+              const half4_t b = nib_quad((q & 1) ? (w >> 16) : (w & 0xFFFFu));
+              sa[q / QPS] = __builtin_amdgcn_mfma_f32_4x4x4f16(qhi[q / 16], b, sa[q / QPS], 4, q % 16, 0);
+              sb[q / QPS] = __builtin_amdgcn_mfma_f32_4x4x4f16(qlo[q / 16], b, sb[q / QPS], 4, q % 16, 0);
+            }(),
+            ...);
+      }(std::make_integer_sequence<int, 32>{});
+    }
+    float sc[4], mx[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v = 0.0f;
+#pragma unroll
+      for (int s = 0; s < NB; ++s) v = fmaf(ks[s], sa[s][j] + sb[s][j], v);
+      sc[j] = tok_ok ? v : kNegInf;
+      mx[j] = sc[j];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) mx[j] = fmaxf(mx[j], __shfl_xor(mx[j], o));
+    float alpha[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float mn = fmaxf(m_run[j], mx[j]);
+      alpha[j] = (m_run[j] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(m_run[j] - mn);
+      const float p = tok_ok ? __builtin_amdgcn_exp2f(sc[j] - mn) : 0.0f;
+      l_run[j] = fmaf(l_run[j], alpha[j], p);
+      m_run[j] = mn;
+      s_p[wave][j][lane] = p;
+    }
+#pragma unroll
+    for (int s = 0; s < NB; ++s) s_vs[wave][lane][s] = vs[s];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[e][j] *= alpha[j];
+    wave_sync_lds();
+
+    // ---- V: out[head][8t + e] += sum over 4 tokens of p * v_scale * (nibble - 8)
+    {
+      const uint8_t *vb = &s_kv[wave][cur][1][G * kChunkStride];
+      const int vset = NB == 4 ? (t >> 2) : NB == 2 ? (t >> 3) : 0;
+#pragma unroll
+      for (int tq = 0; tq < 4; ++tq) {
+        const int slot = 16 * G + 4 * tq;
+        const float4 pp = *reinterpret_cast<const float4 *>(&s_p[wave][lane & 3][slot]);
+        const float pv[4] = {pp.x * s_vs[wave][slot][vset], pp.y * s_vs[wave][slot + 1][vset],
+                             pp.z * s_vs[wave][slot + 2][vset], pp.w * s_vs[wave][slot + 3][vset]};
+        half4_t a, al;  // p * v_scale as f16 hi + lo (fp32-grade weights, like the query operand)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          a[k] = static_cast<_Float16>(pv[k]);
+          al[k] = static_cast<_Float16>(pv[k] - static_cast<float>(a[k]));
+        }
+        uint32_t wk[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          wk[k] = *reinterpret_cast<const uint32_t *>(vb + (4 * tq + k) * kRowBytes + 16 * ((t >> 2) ^ k) + 4 * (t & 3));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {  // byte j of the four words: dims 8t + 2j (low nibbles), 8t + 2j + 1 (high)
+          const uint32_t sel = uint32_t(j) | 0x0c00u | (uint32_t(4 + j) << 16) | 0x0c000000u;
+          const uint32_t x01 = __builtin_amdgcn_perm(wk[1], wk[0], sel);  // [w0.bj, 0, w1.bj, 0]
+          const uint32_t x23 = __builtin_amdgcn_perm(wk[3], wk[2], sel);
+          const half4_t b0 = as_half4(minus_1032((x01 & 0x000F000Fu) | 0x64006400u),
+                                      minus_1032((x23 & 0x000F000Fu) | 0x64006400u));
+          const half4_t b1 = as_half4(minus_1032(((x01 >> 4) & 0x000F000Fu) | 0x64006400u),
+                                      minus_1032(((x23 >> 4) & 0x000F000Fu) | 0x64006400u));
+          acc[2 * j] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, b0, acc[2 * j], 0, 0, 0);
+          acc[2 * j] = __builtin_amdgcn_mfma_f32_4x4x4f16(al, b0, acc[2 * j], 0, 0, 0);
+          acc[2 * j + 1] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, b1, acc[2 * j + 1], 0, 0, 0);
+          acc[2 * j + 1] = __builtin_amdgcn_mfma_f32_4x4x4f16(al, b1, acc[2 * j + 1], 0, 0, 0);
+        }
+      }
+    }
+    wave_sync_lds();
+    cur ^= 1;
+  }
+
+  // ---- wavefront partial: sum the four chunk groups, l over all lanes
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v = acc[e][j];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      acc[e][j] = v;
+    }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) l_run[j] += __shfl_xor(l_run[j], o);
+  __syncthreads();  // every wave is done with its tile buffers: reuse them for the partials
+  float(*red)[4][kD + 2] = reinterpret_cast<float(*)[4][kD + 2]>(&s_kv[0][0][0][0]);
+  if (lane < 16) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) red[wave][j][8 * t + e] = acc[e][j];
+  }
+  if (lane < 4) {
+    red[wave][lane][kD] = m_run[lane];
+    red[wave][lane][kD + 1] = l_run[lane];
+  }
+  __syncthreads();
+  const uint32_t stride = kD + 4u;
+  float *base = ws + it.ws_offset + (uint64_t(split) * it.q_tokens + qt) * sh.q_heads * stride;
+  for (int i = threadIdx.x; i < 4 * kD; i += 256) {
+    const int j = i / kD, dd = i % kD;
+    if (qc * 4 + j >= gqa) continue;
+    float m = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) m = fmaxf(m, red[w][j][kD]);
+    float l = 0.0f, o = 0.0f;
+    if (m != kNegInf)
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float mw = red[w][j][kD];
+        if (mw == kNegInf) continue;
+        const float f = __builtin_amdgcn_exp2f(mw - m);
+        l = fmaf(red[w][j][kD + 1], f, l);
+        o = fmaf(red[w][j][dd], f, o);
+      }
+    float *row = base + uint64_t(h * gqa + qc * 4 + j) * stride;
+    row[dd] = o;
+    if (dd == 0) {
+      row[kD] = m;
+      row[kD + 1] = l;
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_nib_mfma(uint32_t nb, const AttnItem *items, uint32_t nitems, uint32_t max_page_splits,
+                           uint32_t max_qtok, const AttnShape &sh, float *ws, hipStream_t stream) {
+  if (sh.head_dim != kD || max_page_splits == 0) return hipSuccess;
+  const uint32_t qchunks = (sh.gqa + 3u) / 4u;
+  const uint64_t ydim = uint64_t(max_qtok) * qchunks * sh.kv_heads;
+  if (ydim > 65535u) return hipErrorInvalidValue;
+  const dim3 grid(max_page_splits, static_cast<uint32_t>(ydim), nitems);
+  switch (nb) {
+    case 1: nib_mfma_kernel<1><<<grid, 256, 0, stream>>>(items, sh, qchunks, ws); break;
+    case 2: nib_mfma_kernel<2><<<grid, 256, 0, stream>>>(items, sh, qchunks, ws); break;
+    default: nib_mfma_kernel<4><<<grid, 256, 0, stream>>>(items, sh, qchunks, ws); break;
+  }
+  return hipPeekAtLastError();
+}
+
+}  // namespace cfnib

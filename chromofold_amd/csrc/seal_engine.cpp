@@ -259,8 +259,9 @@ int engine_attention(cf_device_seal_engine *e, uint32_t layer_index, const cf_de
     r.query_begin = query_begin;
     r.window = window;
     r.softmax_scale = softmax_scale;
+    r.block_size = e->config.block_size;
     const cfnib::AttnShape sh{e->config.kv_head_count, e->config.query_head_count, e->config.gqa_group_size,
-                              e->config.head_dim};
+                              e->config.head_dim, e->config.page_size};
     std::string err;
     const hipError_t st = e->runner.run({r}, sh, stream, err);
     if (st != hipSuccess) throw HipError(err.empty() ? std::string("compressed attention launch: ") + hipGetErrorString(st) : err);

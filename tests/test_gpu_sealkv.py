@@ -98,7 +98,12 @@ def _run_engine_case(dev, kvh, gqa, D, page, bs, seed):
 
 @pytest.mark.parametrize("kvh,gqa,D,page,bs", [(4, 2, 64, 64, 32), (2, 7, 128, 16, 128), (1, 1, 32, 8, 12),
                                                (8, 4, 128, 32, 64), (2, 8, 256, 16, 32), (3, 3, 96, 8, 24),
-                                               (2, 4, 16, 32, 5), (1, 16, 64, 16, 64)])
+                                               (2, 4, 16, 32, 5), (1, 16, 64, 16, 64),
+                                               # head_dim 128 with block 32 / 64 / 128k: the MFMA kernel reads the
+                                               # pages (partial 16-token chunks, pages across tiles, several tiles
+                                               # per page, a block spanning two rows)
+                                               (4, 4, 128, 8, 32), (2, 4, 128, 48, 64), (1, 2, 128, 128, 256),
+                                               (8, 1, 128, 64, 128), (2, 3, 128, 16, 32)])
 def test_seal_engine_bytes_and_attention(dev, kvh, gqa, D, page, bs):
     import torch
     print(f"case kvh={kvh} gqa={gqa} D={D} page={page} bs={bs}", flush=True)
@@ -120,6 +125,32 @@ def test_seal_engine_bytes_and_attention(dev, kvh, gqa, D, page, bs):
     c = e.counters()
     assert c["seal_successes"] == 3 and c["compressed_attention_launches"] == len(cases)
     assert c["finite_validation_launches"] == 3 and c["quantization_launches"] == 3
+    e.close()
+
+
+@pytest.mark.parametrize("bs,gqa", [(32, 4), (128, 8)])
+def test_seal_engine_long_context_many_splits(dev, bs, gqa):
+    """96 pages x 64 tokens: many tiles per wavefront, several context splits, decode and a short prefill."""
+    import torch
+    from chromofold_amd.sealkv import SealEngine
+    kvh, D, page = 2, 128, 64
+    rng = np.random.default_rng(bs + gqa)
+    e = SealEngine(1, kvh, kvh * gqa, D, page, bs)
+    pages = []
+    for p in range(96):
+        k = rng.standard_normal((page, kvh, D)).astype(np.float32)
+        v = rng.standard_normal((page, kvh, D)).astype(np.float32)
+        e.stage(0, p * page, _t(k, dev), _t(v, dev))
+        e.seal(0)
+        pages.append(O.nib_seal_page(k, v, p * page, bs))
+    total = 96 * page
+    for qt, qbegin, window in [(1, total - 1, 0), (3, total - 3, 0), (1, total - 1, 1000), (2, 4000, 0)]:
+        q = rng.standard_normal((qt, kvh * gqa, D)).astype(np.float32)
+        out = torch.full((qt, kvh * gqa, D), float("nan"), device=dev)
+        e.attention(0, _t(q, dev), out, qbegin, 1 / np.sqrt(D), window)
+        torch.cuda.synchronize()
+        ref = O.nib_attention(pages, bs, q, qbegin, kvh, gqa, 1 / np.sqrt(D), window)
+        np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-3, atol=1e-4, err_msg=f"{qt} {qbegin} {window}")
     e.close()
 
 
