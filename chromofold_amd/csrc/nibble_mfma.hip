@@ -17,7 +17,8 @@
 //             two values), with the 4 query heads (split into f16 hi + lo for fp32-grade scores) broadcast as the A
 //             operand, accumulating one score per head in the lane. One accumulator pair per scale block of the row
 //             (the page's block size is 32, 64 or a multiple of 128): score = sum over blocks of k_scale * acc.
-//   softmax:  one running maximum per head for the wavefront; p goes to LDS with the tokens' V scales.
+//   softmax:  one running maximum per head for each chunk group (a 16-lane DPP row, so the maximum is four DPP
+//             steps), merged across the groups once after the loop; p goes to LDS with the tokens' V scales.
 //   V phase:  lane (G, t) owns dims 8t..8t+7 of chunk G's tokens: it reads word t of four rows, transposes the
 //             4 x 8 nibbles with v_perm into eight f16 B operands (4 tokens x 1 dim), and the A operand is p times
 //             the V scale of its 32-dim block for those 4 tokens, as f16 hi + lo.
@@ -65,11 +66,38 @@ __device__ inline half4_t nib_quad(uint32_t x) {
   return as_half4(minus_1032(lo), minus_1032(hi));
 }
 
+// Pointers read from the item table are generic; these casts make their loads global (vector) or constant
+// (scalar) accesses, which the compiler does not have to order against the LDS DMA the way it orders FLAT loads.
+#define CF_GLOBAL __attribute__((address_space(1)))
+#define CF_CONST __attribute__((address_space(4)))
+template <typename T>
+__device__ inline const CF_GLOBAL T *gptr(const T *p) {
+  return (const CF_GLOBAL T *)p;  // an address-space conversion (C-style cast)
+}
+template <typename T>
+__device__ inline const CF_CONST T *cptr(const T *p) {
+  return (const CF_CONST T *)p;
+}
+
 __device__ inline float load_q(const void *base, uint32_t type, uint64_t off) {
-  const char *p = static_cast<const char *>(base) + off;
-  if (type == CF_DEVICE_F16) return static_cast<float>(*reinterpret_cast<const _Float16 *>(p));
-  if (type == CF_DEVICE_BF16) return __uint_as_float(uint32_t(*reinterpret_cast<const uint16_t *>(p)) << 16);
-  return *reinterpret_cast<const float *>(p);
+  const CF_GLOBAL char *p = gptr(static_cast<const char *>(base)) + off;
+  if (type == CF_DEVICE_F16) return static_cast<float>(*reinterpret_cast<const CF_GLOBAL _Float16 *>(p));
+  if (type == CF_DEVICE_BF16) return __uint_as_float(uint32_t(*reinterpret_cast<const CF_GLOBAL uint16_t *>(p)) << 16);
+  return *reinterpret_cast<const CF_GLOBAL float *>(p);
+}
+
+template <int CTRL>
+__device__ inline float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+// Maximum over the 16 lanes of a DPP row; every lane of the row receives it.
+__device__ inline float row_max(float x) {
+  x = fmaxf(x, dpp_mov<0xb1>(x));   // quad_perm [1,0,3,2]
+  x = fmaxf(x, dpp_mov<0x4e>(x));   // quad_perm [2,3,0,1]
+  x = fmaxf(x, dpp_mov<0x141>(x));  // row_half_mirror
+  x = fmaxf(x, dpp_mov<0x140>(x));  // row_mirror
+  return x;
 }
 
 __device__ inline void wave_sync_lds() {
@@ -145,48 +173,84 @@ __global__ __launch_bounds__(256) void nib_mfma_kernel(const AttnItem *__restric
 #pragma unroll
   for (int s = 0; s < NB; ++s) n_ks[s] = n_vs[s] = 0.0f;
 
-  // copies of tile `tile` into buffer `buf` + this lane's metadata for it
-  auto stage = [&](uint32_t tile, int buf) {
-    n_ok = false;
+  // Descriptor fields of a tile's four chunks, fetched one tile ahead of its copies with vector loads (they land
+  // under the same vmcnt wait as the copies, and unlike scalar loads they do not hold up the LDS reads).
+  struct TileDesc {
+    const uint8_t *kp[4], *vp[4];
+    uint32_t tc[4];
+    const float *ks, *vs;  // this lane's chunk (G)
+    uint32_t tb, bs;
+  };
+  auto fetch = [&](uint32_t tile, TileDesc &d) {
+    const CF_GLOBAL cf_device_page_descriptor *gp = gptr(pages);
 #pragma unroll
     for (int C = 0; C < 4; ++C) {
       const uint32_t ch = 4u * tile + C;
-      if (ch >= nchunks) break;  // wave-uniform
-      const uint32_t p = ch / cpp, off = (ch - p * cpp) * 16u;
-      const cf_device_page_descriptor &pg = pages[p];
-      const uint32_t tc = pg.token_count;
-      if (off >= tc) continue;  // a partial page's empty chunk: its slots stay masked
+      d.tc[C] = 0u;
+      if (ch < nchunks) {
+        const uint32_t p = ch / cpp;
+        d.kp[C] = gp[p].key_payload;
+        d.vp[C] = gp[p].value_payload;
+        d.tc[C] = gp[p].token_count;
+      }
+    }
+    const uint32_t mine = 4u * tile + G;
+    if (mine < nchunks) {
+      const uint32_t p = mine / cpp;
+      d.ks = gp[p].key_scales;
+      d.vs = gp[p].value_scales;
+      d.tb = gp[p].token_begin;
+      d.bs = gp[p].block_size;
+    }
+  };
+  // copies of tile `tile` into buffer `buf`, and this lane's scales for it (the descriptors have landed)
+  auto stage = [&](uint32_t tile, const TileDesc &d, int buf) {
+#pragma unroll
+    for (int C = 0; C < 4; ++C) {
+      const uint32_t ch = 4u * tile + C;
+      const uint32_t off = (ch % cpp) * 16u;
+      const uint32_t tc = __builtin_amdgcn_readfirstlane(d.tc[C]);
+      if (ch >= nchunks || off >= tc) continue;  // past the split / a partial page's empty chunk: masked slots
       const uint32_t r = static_cast<uint32_t>(lane) >> 2, piece = (lane & 3) ^ (r & 3);
       const uint32_t row = min(off + r, tc - 1u);  // slots past the page's tokens re-read its last row
       const uint64_t goff = (uint64_t(row) * kvh + h) * kRowBytes + 16u * piece;
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t *>(pg.key_payload + goff),
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const CF_GLOBAL uint32_t *>(gptr(d.kp[C]) + goff),
                                        (__attribute__((address_space(3))) void *)(&s_kv[wave][buf][0][C * kChunkStride]),
                                        16, 0, 0);
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t *>(pg.value_payload + goff),
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const CF_GLOBAL uint32_t *>(gptr(d.vp[C]) + goff),
                                        (__attribute__((address_space(3))) void *)(&s_kv[wave][buf][1][C * kChunkStride]),
                                        16, 0, 0);
-      if (G == C) {
-        const uint32_t tok = off + static_cast<uint32_t>(t);
-        const uint32_t pos = pg.token_begin + tok;
-        n_ok = tok < tc && pos <= qpos && (window == 0u || uint64_t(pos) + window > qpos);
-        const uint32_t srow = min(tok, tc - 1u);
-        const uint64_t base = (uint64_t(srow) * kvh + h) * kD;
-        const uint32_t bs = pg.block_size;
+    }
+    n_ok = false;
+    const uint32_t mine = 4u * tile + G;
+    const uint32_t my_tc = G == 0 ? d.tc[0] : G == 1 ? d.tc[1] : G == 2 ? d.tc[2] : d.tc[3];
+    const uint32_t off = (mine % cpp) * 16u;
+    if (mine < nchunks && off < my_tc) {
+      const uint32_t tok = off + static_cast<uint32_t>(t);
+      const uint32_t pos = d.tb + tok;
+      n_ok = tok < my_tc && pos <= qpos && (window == 0u || uint64_t(pos) + window > qpos);
+      const uint32_t row = min(tok, my_tc - 1u) * kvh + h;  // token-head row of the page
+      // first scale of the row: block = row * 128 / block_size (block_size 32 / 64 / a multiple of 128)
+      const uint32_t bi = NB == 4 ? row * 4u : NB == 2 ? row * 2u : row / (d.bs / 128u);
 #pragma unroll
-        for (int s = 0; s < NB; ++s) {
-          const uint64_t bi = (base + uint64_t(s) * (kD / NB)) / bs;
-          n_ks[s] = pg.key_scales[bi];
-          n_vs[s] = pg.value_scales[bi];
-        }
+      for (int s = 0; s < NB; ++s) {
+        n_ks[s] = gptr(d.ks)[bi + s];
+        n_vs[s] = gptr(d.vs)[bi + s];
       }
     }
   };
 
   int cur = 0;
   uint32_t tile = tb + wave;
-  if (tile < te) stage(tile, 0);
+  TileDesc dnext;
+  if (tile < te) {
+    fetch(tile, dnext);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    stage(tile, dnext, 0);
+    if (tile + kWaves < te) fetch(tile + kWaves, dnext);
+  }
   for (; tile < te; tile += kWaves) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this tile's rows and the lane's scales have landed
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this tile's rows and scales, the next tile's descriptors
     wave_sync_lds();
     const bool tok_ok = n_ok;
     float ks[NB], vs[NB];
@@ -195,12 +259,18 @@ __global__ __launch_bounds__(256) void nib_mfma_kernel(const AttnItem *__restric
       ks[s] = n_ks[s];
       vs[s] = n_vs[s];
     }
-    if (tile + kWaves < te) stage(tile + kWaves, cur ^ 1);
+    if (tile + kWaves < te) {
+      stage(tile + kWaves, dnext, cur ^ 1);
+      if (tile + 2 * kWaves < te) fetch(tile + 2 * kWaves, dnext);
+    }
 
     // ---- K: one score per head for this lane's token
-    float4_t sa[NB], sb[NB];
+    // four independent accumulator chains (x hi / lo): chain c holds quads of scale block c / (4 / NB), and the
+    // quad order below makes consecutive MFMAs hit different chains
+    constexpr int CPS = 4 / NB;  // chains per scale block
+    float4_t sa[4], sb[4];
 #pragma unroll
-    for (int s = 0; s < NB; ++s) sa[s] = sb[s] = float4_t{0, 0, 0, 0};
+    for (int c = 0; c < 4; ++c) sa[c] = sb[c] = float4_t{0, 0, 0, 0};
     {
       const uint8_t *kb = &s_kv[wave][cur][0][G * kChunkStride + t * kRowBytes];
       uint4 pc[4];
@@ -208,48 +278,53 @@ __global__ __launch_bounds__(256) void nib_mfma_kernel(const AttnItem *__restric
       for (int k = 0; k < 4; ++k) pc[k] = *reinterpret_cast<const uint4 *>(kb + 16 * (k ^ (t & 3)));
       const uint32_t w16[16] = {pc[0].x, pc[0].y, pc[0].z, pc[0].w, pc[1].x, pc[1].y, pc[1].z, pc[1].w,
                                 pc[2].x, pc[2].y, pc[2].z, pc[2].w, pc[3].x, pc[3].y, pc[3].z, pc[3].w};
-      constexpr int QPS = 32 / NB;  // quads per scale block
-      [&]<int... Q>(std::integer_sequence<int, Q...>) {
+      [&]<int... I>(std::integer_sequence<int, I...>) {
         (
             [&] {
-              constexpr int q = Q;  // quad = dims 4q..4q+3
+              constexpr int c = I % 4;                         // chain
+              constexpr int blk = c / CPS, sub = c % CPS;      // scale block, position among its chains
+              constexpr int q = blk * (32 / NB) + CPS * (I / 4) + sub;  // quad = dims 4q..4q+3
               const uint32_t w = w16[q / 2];
               const half4_t b = nib_quad((q & 1) ? (w >> 16) : (w & 0xFFFFu));
-              sa[q / QPS] = __builtin_amdgcn_mfma_f32_4x4x4f16(qhi[q / 16], b, sa[q / QPS], 4, q % 16, 0);
-              sb[q / QPS] = __builtin_amdgcn_mfma_f32_4x4x4f16(qlo[q / 16], b, sb[q / QPS], 4, q % 16, 0);
+              sa[c] = __builtin_amdgcn_mfma_f32_4x4x4f16(qhi[q / 16], b, sa[c], 4, q % 16, 0);
+              sb[c] = __builtin_amdgcn_mfma_f32_4x4x4f16(qlo[q / 16], b, sb[c], 4, q % 16, 0);
             }(),
             ...);
       }(std::make_integer_sequence<int, 32>{});
     }
+    // softmax: one running maximum per head for each 16-lane chunk group (a DPP row), merged after the loop
     float sc[4], mx[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       float v = 0.0f;
 #pragma unroll
-      for (int s = 0; s < NB; ++s) v = fmaf(ks[s], sa[s][j] + sb[s][j], v);
+      for (int c = 0; c < 4; ++c) v = fmaf(ks[c / CPS], sa[c][j] + sb[c][j], v);
       sc[j] = tok_ok ? v : kNegInf;
-      mx[j] = sc[j];
+      mx[j] = row_max(sc[j]);
+    }
+    // raise the running maxima (and rescale the accumulators) only when some lane's maximum grew
+    bool grow = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) grow |= mx[j] > m_run[j];
+    if (__ballot(grow) != 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float mn = fmaxf(m_run[j], mx[j]);
+        const float alpha = (m_run[j] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(m_run[j] - mn);
+        l_run[j] *= alpha;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e][j] *= alpha;
+        m_run[j] = mn;
+      }
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) mx[j] = fmaxf(mx[j], __shfl_xor(mx[j], o));
-    float alpha[4];
-#pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float mn = fmaxf(m_run[j], mx[j]);
-      alpha[j] = (m_run[j] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(m_run[j] - mn);
-      const float p = tok_ok ? __builtin_amdgcn_exp2f(sc[j] - mn) : 0.0f;
-      l_run[j] = fmaf(l_run[j], alpha[j], p);
-      m_run[j] = mn;
+      const float p = tok_ok ? __builtin_amdgcn_exp2f(sc[j] - m_run[j]) : 0.0f;
+      l_run[j] += p;
       s_p[wave][j][lane] = p;
     }
 #pragma unroll
     for (int s = 0; s < NB; ++s) s_vs[wave][lane][s] = vs[s];
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[e][j] *= alpha[j];
     wave_sync_lds();
 
     // ---- V: out[head][8t + e] += sum over 4 tokens of p * v_scale * (nibble - 8)
@@ -272,27 +347,38 @@ __global__ __launch_bounds__(256) void nib_mfma_kernel(const AttnItem *__restric
 #pragma unroll
         for (int k = 0; k < 4; ++k)
           wk[k] = *reinterpret_cast<const uint32_t *>(vb + (4 * tq + k) * kRowBytes + 16 * ((t >> 2) ^ k) + 4 * (t & 3));
+        half4_t bv[8];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {  // byte j of the four words: dims 8t + 2j (low nibbles), 8t + 2j + 1 (high)
           const uint32_t sel = uint32_t(j) | 0x0c00u | (uint32_t(4 + j) << 16) | 0x0c000000u;
           const uint32_t x01 = __builtin_amdgcn_perm(wk[1], wk[0], sel);  // [w0.bj, 0, w1.bj, 0]
           const uint32_t x23 = __builtin_amdgcn_perm(wk[3], wk[2], sel);
-          const half4_t b0 = as_half4(minus_1032((x01 & 0x000F000Fu) | 0x64006400u),
-                                      minus_1032((x23 & 0x000F000Fu) | 0x64006400u));
-          const half4_t b1 = as_half4(minus_1032(((x01 >> 4) & 0x000F000Fu) | 0x64006400u),
-                                      minus_1032(((x23 >> 4) & 0x000F000Fu) | 0x64006400u));
-          acc[2 * j] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, b0, acc[2 * j], 0, 0, 0);
-          acc[2 * j] = __builtin_amdgcn_mfma_f32_4x4x4f16(al, b0, acc[2 * j], 0, 0, 0);
-          acc[2 * j + 1] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, b1, acc[2 * j + 1], 0, 0, 0);
-          acc[2 * j + 1] = __builtin_amdgcn_mfma_f32_4x4x4f16(al, b1, acc[2 * j + 1], 0, 0, 0);
+          bv[2 * j] = as_half4(minus_1032((x01 & 0x000F000Fu) | 0x64006400u),
+                               minus_1032((x23 & 0x000F000Fu) | 0x64006400u));
+          bv[2 * j + 1] = as_half4(minus_1032(((x01 >> 4) & 0x000F000Fu) | 0x64006400u),
+                                   minus_1032(((x23 >> 4) & 0x000F000Fu) | 0x64006400u));
         }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, bv[e], acc[e], 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = __builtin_amdgcn_mfma_f32_4x4x4f16(al, bv[e], acc[e], 0, 0, 0);
       }
     }
     wave_sync_lds();
     cur ^= 1;
   }
 
-  // ---- wavefront partial: sum the four chunk groups, l over all lanes
+  // ---- wavefront partial: bring the four chunk groups to a common maximum, then sum them (l over all lanes)
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float mw = fmaxf(m_run[j], __shfl_xor(m_run[j], 16));
+    mw = fmaxf(mw, __shfl_xor(mw, 32));
+    const float f = (m_run[j] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(m_run[j] - mw);
+    l_run[j] *= f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e][j] *= f;
+    m_run[j] = mw;
+  }
 #pragma unroll
   for (int e = 0; e < 8; ++e)
 #pragma unroll
