@@ -578,7 +578,10 @@ hipError_t AttnRunner::run(const std::vector<AttnRequest> &reqs, const AttnShape
   float *partials = reinterpret_cast<float *>(static_cast<char *>(ws_) + table_bytes);
   const dim3 grid(max_split, static_cast<uint32_t>(ydim), static_cast<uint32_t>(items.size()));
   const dim3 block(hw * lg);
-  switch (lg) {
+  // the VALU kernel serves items without the MFMA path, every active page and every item with nothing visible
+  bool valu_work = false;
+  for (const AttnItem &it : items) valu_work = valu_work || !it.mfma_nb || it.nsplit > it.page_splits;
+  if (valu_work) switch (lg) {
     case 4: e = launch_attn_lg<4>(G, grid, block, stream, d_items, sh, hw, hgroups, qchunks, partials); break;
     case 8: e = launch_attn_lg<8>(G, grid, block, stream, d_items, sh, hw, hgroups, qchunks, partials); break;
     case 16: e = launch_attn_lg<16>(G, grid, block, stream, d_items, sh, hw, hgroups, qchunks, partials); break;
