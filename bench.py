@@ -352,6 +352,65 @@ def bench_seal(steps: int, warmup: int, cpu: bool = True, seqs: int = 32, tokens
     return res
 
 
+# ------------------------------------------------------------------------------------------------ gathers (§8f.4)
+def bench_gather(steps: int, warmup: int, dim: int = 128, nq: int = 1 << 20) -> dict:
+    """Embedding-row gathers through the C1 index (1M Zipf tokens, vocab 32000, GPU-built RRR wavelet): for 1M
+    random positions, out[q] = emb[token[pos[q]]] with emb [32000, 128] fp32. Fused (cf_sparse_gather_fused_async:
+    access + row copy in one kernel) against decode-all + gather (cf_sparse_decode_all_async once, then
+    cf_sparse_gather_async per step). Gate: the closed form emb[tok[pos]]. Algorithmic HBM bytes per call: the
+    positions and the output rows (the 16 MB table and the index stay in L2/MALL)."""
+    import ctypes as C
+    import torch
+    from chromofold_amd import _abi as A
+    from chromofold_amd import synth
+    from chromofold_amd.search import build_rrrw, u32_dev
+
+    n, vocab = 1 << 20, 32000
+    tok = synth.zipf_tokens(n, vocab, 1.1, synth.SEED_C1)
+    idx, _ = build_rrrw(torch.from_numpy(tok.view(np.int32)).to("cuda:0"), 15)
+    rng = np.random.default_rng(synth.SEED_C1 + 9)
+    pos = rng.integers(0, n, nq).astype(np.uint32)
+    emb = torch.randn((vocab, dim), device="cuda:0", generator=torch.Generator(device="cuda:0").manual_seed(3))
+    dpos = u32_dev(pos)
+    out = torch.empty((nq, dim), device="cuda:0")
+    ids = torch.empty(n, dtype=torch.int32, device="cuda:0")
+    L = A.lib()
+    v = idx.view()
+    for name, args in (("cf_sparse_gather_fused_async", [A.cf_rrrw_view, A.P, C.c_int, A.P, A.P, C.c_size_t, A.P]),
+                       ("cf_sparse_decode_all_async", [A.cf_rrrw_view, A.P, C.c_size_t, A.P]),
+                       ("cf_sparse_gather_async", [A.P, A.P, C.c_int, A.P, A.P, C.c_size_t, A.P])):
+        A.declare(name, A.I32, args)
+    s = torch.cuda.current_stream().cuda_stream
+
+    def fused():
+        A.check(L.cf_sparse_gather_fused_async(v, emb.data_ptr(), dim, dpos.data_ptr(), out.data_ptr(), nq, s),
+                "cf_sparse_gather_fused_async")
+
+    def via_ids():
+        A.check(L.cf_sparse_gather_async(ids.data_ptr(), emb.data_ptr(), dim, dpos.data_ptr(), out.data_ptr(), nq, s),
+                "cf_sparse_gather_async")
+
+    fused()
+    torch.cuda.synchronize()
+    chk = rng.integers(0, nq, 4096)
+    ref = emb[torch.from_numpy(tok[pos[chk]].astype(np.int64)).to("cuda:0")]
+    assert torch.equal(out[torch.from_numpy(chk).to("cuda:0")], ref), "fused gather != emb[tok[pos]]"
+    _, per_f = _events_time(fused, steps, warmup)
+    A.check(L.cf_sparse_decode_all_async(v, ids.data_ptr(), n, s), "cf_sparse_decode_all_async")
+    _, per_d = _events_time(lambda: A.check(L.cf_sparse_decode_all_async(v, ids.data_ptr(), n, s), "decode_all"),
+                            steps, warmup)
+    _, per_g = _events_time(via_ids, steps, warmup)
+    torch.cuda.synchronize()
+    assert torch.equal(out[torch.from_numpy(chk).to("cuda:0")], ref), "gather via ids != emb[tok[pos]]"
+    tf, td, tg = (float(np.mean(p)) * 1e-3 for p in (per_f, per_d, per_g))
+    step_bytes = nq * 4 + nq * dim * 4
+    return {"workload": f"{nq} positions into the C1 index, rows of {dim} fp32 from a {vocab}-row table",
+            "fused_ms": tf * 1e3, "fused_mqs": nq / tf / 1e6, "fused_gbs": step_bytes / tf / 1e9,
+            "fused_roofline_frac": step_bytes / tf / 1e9 / HBM_PEAK_GBS,
+            "decode_all_ms": td * 1e3, "gather_via_ids_ms": tg * 1e3,
+            "decode_all_plus_gather_ms": (td + tg) * 1e3}
+
+
 # ------------------------------------------------------------------------------------------------ int4 nibble pages
 def _d2h(ptr: int, nbytes: int) -> np.ndarray:
     import ctypes as C
@@ -559,7 +618,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="auto", choices=["auto", "kv", "rrr", "copy", "c5", "seal", "nibble"])
+    ap.add_argument("--workload", default="auto", choices=["auto", "kv", "rrr", "copy", "c5", "seal", "nibble",
+                                                                  "gather"])
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -582,6 +642,9 @@ def main() -> int:
     if args.workload == "c5":
         print(json.dumps({"c5": bench_c5(args.steps, args.warmup)}))
         return 0
+    if args.workload == "gather":
+        print(json.dumps({"gather": bench_gather(args.steps, args.warmup)}))
+        return 0
     if args.workload == "nibble":
         print(json.dumps({"nibble_pages": bench_nibble(args.steps, args.warmup, cpu=not args.no_cpu)}))
         return 0
@@ -599,6 +662,7 @@ def main() -> int:
         secondary["c5_long_context"] = bench_c5(min(args.steps, 20), 2)
         secondary["device_seal"] = bench_seal(min(args.steps, 20), 2, cpu=not args.no_cpu)
         secondary["nibble_pages"] = bench_nibble(min(args.steps, 20), 2, cpu=not args.no_cpu)
+        secondary["gathers"] = bench_gather(min(args.steps, 20), 2)
         cp = bench_copy(10, 2)
         secondary["stream_copy_gbs"] = cp["stream_copy_gbs"]
         secondary["roofline_frac_of_stream_copy"] = kvr["roofline"]["achieved"] / cp["stream_copy_gbs"]
