@@ -570,25 +570,29 @@ def bench_c5(steps: int, warmup: int) -> dict:
         Vs[:, P:] = g.standard_normal((H, U, D), dtype=np.float32)
         return Ks, Vs
 
-    kvb = kv.build_batched(kv.CODEC_RANS_HYBRID, src_a, S, H, np.full(S, T, np.uint32), D, tables, "cuda:0",
-                           keep_host=True, shared={s: (0, P // 64) for s in range(1, S)})
-    qp = np.full(S, T - 1, np.uint32)
-    q, out, t = run(kvb, S, T, qp)
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from kv_helpers import decoded_pages, normwise_err
-    s_chk = 7
-    pages = []
-    for h in range(H):
-        pages += [(h, t0, k, v) for t0, k, v in decoded_pages(kvb, s_chk, h, T)]
-    ref, _ = O.paged_attention_f64(q[s_chk], QH, H, D, gqa, T - 1, 0, sc, pages)
-    err_a = normwise_err(out[s_chk], ref)
-    assert err_a <= 1e-3, err_a
     logical = 2.0 * S * H * T * D * 2  # bf16 bytes of every sequence's full KV
-    res["shared_prefix"] = {"workload": "256 seqs x (8192 shared + 512 unique) tokens", "tokens_per_s": S / t,
-                            "ms_per_step": t * 1e3, "unique_pool_bytes": kvb.pool_bytes,
-                            "ratio_vs_bf16_logical": logical / kvb.pool_bytes,
-                            "unique_gbs": kvb.pool_bytes / t / 1e9, "max_normwise_err": err_a}
-    del kvb
+    # the prefix rANS-coded like the rest, then (the serving policy for a prefix every sequence reads each step)
+    # stored as INT8 groups inside the same pool: no per-sequence entropy decode of the shared pages
+    for name, raw in (("shared_prefix_rans", None), ("shared_prefix", {0: P // 64})):
+        kvb = kv.build_batched(kv.CODEC_RANS_HYBRID, src_a, S, H, np.full(S, T, np.uint32), D, tables, "cuda:0",
+                               keep_host=True, shared={s: (0, P // 64) for s in range(1, S)}, raw_groups=raw)
+        qp = np.full(S, T - 1, np.uint32)
+        q, out, t = run(kvb, S, T, qp)
+        s_chk = 7
+        pages = []
+        for h in range(H):
+            pages += [(h, t0, k, v) for t0, k, v in decoded_pages(kvb, s_chk, h, T)]
+        ref, _ = O.paged_attention_f64(q[s_chk], QH, H, D, gqa, T - 1, 0, sc, pages)
+        err_a = normwise_err(out[s_chk], ref)
+        assert err_a <= 1e-3, err_a
+        res[name] = {"workload": "256 seqs x (8192 shared + 512 unique) tokens",
+                     "prefix_codec": "int8" if raw else "rans_hybrid", "tokens_per_s": S / t,
+                     "ms_per_step": t * 1e3, "unique_pool_bytes": kvb.pool_bytes,
+                     "ratio_vs_bf16_logical": logical / kvb.pool_bytes,
+                     "unique_gbs": kvb.pool_bytes / t / 1e9, "max_normwise_err": err_a}
+        del kvb
 
     # (b) 4 x 131072
     S, T = 4, 131072

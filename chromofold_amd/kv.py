@@ -213,11 +213,14 @@ def seal_device(codec: int, keys: torch.Tensor, values: torch.Tensor, tables: to
 
 def build_batched(codec: int, kv_source, seq_count: int, kv_heads: int, seq_tokens: np.ndarray, head_dim: int,
                   tables: np.ndarray | None, device="cuda", keep_host: bool = False,
-                  shared: dict | None = None, encoder: str = "host") -> BatchedKv:
+                  shared: dict | None = None, encoder: str = "host", raw_groups: dict | None = None) -> BatchedKv:
     """Encode and upload page groups. kv_source(s) -> (K, V) fp32 arrays [kv_heads, T_s, D] for sequence s.
     `shared` optionally maps sequence s -> (donor sequence, prefix groups): the first `prefix groups` groups of s are
-    the donor's blobs (no copy), modelling refcounted shared-prefix pages. encoder="device" uploads the fp32 pages
-    and seals them with cf_kv_encode_groups_async straight into the device pool (same bytes as the host encoder)."""
+    the donor's blobs (no copy), modelling refcounted shared-prefix pages. `raw_groups` optionally maps sequence s
+    -> n: its first n groups are stored with the INT8 codec (raw symbols, decode-free) inside the pool whatever
+    `codec` is; meant for pages many sequences read every step, such as a shared prefix (host encoder only).
+    encoder="device" uploads the fp32 pages and seals them with cf_kv_encode_groups_async straight into the device
+    pool (same bytes as the host encoder)."""
     seq_tokens = np.asarray(seq_tokens, np.uint32)
     max_groups = int((seq_tokens.max() + GROUP_TOKENS - 1) // GROUP_TOKENS)
     offsets = np.zeros((seq_count, kv_heads, max_groups), np.uint32)
@@ -257,6 +260,8 @@ def build_batched(codec: int, kv_source, seq_count: int, kv_heads: int, seq_toke
                                       (kv_heads, gl.size)).ravel()
         heads = np.repeat(np.arange(kv_heads, dtype=np.uint32), gl.size)
         if on_device:
+            if (raw_groups or {}).get(s):
+                raise ValueError("raw_groups needs the host encoder")
             r = encode_groups_device(codec, torch.from_numpy(Kp).to(device), torch.from_numpy(Vp).to(device),
                                      head_dim, d_tab, torch.from_numpy(first_page.astype(np.int64)).to(device),
                                      torch.from_numpy(page_counts.astype(np.int32)).to(device), dpool, at,
@@ -267,10 +272,17 @@ def build_batched(codec: int, kv_source, seq_count: int, kv_heads: int, seq_toke
             offsets[s, :, first:ngr] = r.offsets.cpu().numpy().view(np.uint32).reshape(kv_heads, gl.size)
             at = int(r.pool_end.item())
             continue
-        blob, offs = encode_groups(codec, Kp, Vp, head_dim, tables, first_page, page_counts, heads, tc.ravel())
-        offsets[s, :, first:ngr] = (offs + at // 16).reshape(kv_heads, gl.size)
-        blobs.append(blob)
-        at += blob.size
+        nraw = min(max(int((raw_groups or {}).get(s, 0)) - first, 0), gl.size)
+        per_head = [np.arange(h * gl.size, (h + 1) * gl.size) for h in range(kv_heads)]
+        for lo, hi, cdc in ((0, nraw, CODEC_INT8), (nraw, gl.size, codec)):
+            if hi <= lo:
+                continue
+            sel = np.concatenate([ph[lo:hi] for ph in per_head])
+            blob, offs = encode_groups(cdc, Kp, Vp, head_dim, tables if cdc != CODEC_INT8 else None,
+                                       first_page[sel], page_counts[sel], heads[sel], tc.ravel())
+            offsets[s, :, first + lo:first + hi] = (offs + at // 16).reshape(kv_heads, hi - lo)
+            blobs.append(blob)
+            at += blob.size
     assert at // 16 < 2 ** 32
     if on_device:
         pool = dpool[:max(at, 16)]

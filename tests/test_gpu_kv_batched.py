@@ -19,7 +19,7 @@ def dev():
 
 
 def _run(dev, codec, seq_tokens, kv_heads, gqa, D, seed, query_pos=None, splits=(0,), shared=None,
-         scale_spread=False):
+         scale_spread=False, raw_groups=None):
     import torch
     from chromofold_amd import kv
     data = make_seqs(seq_tokens, kv_heads, D, seed, scale_spread)
@@ -38,7 +38,7 @@ def _run(dev, codec, seq_tokens, kv_heads, gqa, D, seed, query_pos=None, splits=
             data[s][1][:, :n] = data[donor][1][:, :n]
     S = len(seq_tokens)
     kvb = kv.build_batched(codec, lambda s: data[s], S, kv_heads, np.array(seq_tokens), D, tables, dev,
-                           keep_host=True, shared=shared)
+                           keep_host=True, shared=shared, raw_groups=raw_groups)
     rng = np.random.default_rng(seed + 1)
     q = rng.standard_normal((S, kv_heads * gqa, D)).astype(np.float32)
     qp = np.array([t - 1 for t in seq_tokens] if query_pos is None else query_pos, np.uint32)
@@ -77,6 +77,14 @@ def test_batched_gqa(dev, gqa):
 def test_batched_shared_prefix(dev):
     # sequences 1..3 reuse sequence 0's first 2 page groups = 128 tokens (refcounted prefix blobs)
     _run(dev, 2, [256, 200, 300, 129], 2, 4, 128, seed=21, shared={1: (0, 2), 2: (0, 2), 3: (0, 2)})
+
+
+@pytest.mark.parametrize("D", [128, 64])
+def test_batched_shared_prefix_stored_raw(dev, D):
+    # the shared prefix kept as INT8 groups inside the rANS pool (one sequence also has a raw group of its own);
+    # the kernel takes each group by its header's codec
+    _run(dev, 2, [256, 200, 300, 129], 2, 4, D, seed=23, splits=(0, 2), shared={1: (0, 2), 2: (0, 2), 3: (0, 2)},
+         raw_groups={0: 2, 2: 3})
 
 
 def test_batched_value_spread(dev):

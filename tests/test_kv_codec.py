@@ -134,3 +134,42 @@ def test_device_encoder_rejects_bad_arguments_before_any_device_call(kv):
     assert call(keys=None) == 1 and call(values=A + 8) == 1 and call(pool=A + 4) == 1 and call(pool_at=8) == 1
     assert call(n=0) == 1 and call(tables=None) == 1 and call(tcount=1) == 1 and call(ws_bytes=ws - 1) == 1
     assert call(D=20) == 2 and call(D=256) == 2 and call(codec=7) == 2
+
+
+def test_mixed_pool_raw_prefix(kv):
+    """build_batched(raw_groups=...) on the host: a sequence's leading groups are INT8 blobs inside a RANS_HYBRID
+    pool. Every group decodes (oracle decoder) to the same symbols and scales as in an all-INT8 and an all-rANS pool,
+    the leading groups carry the INT8 codec byte and the rest the RANS_HYBRID one, and sharing the raw prefix with
+    other sequences reuses the donor's blobs."""
+    rng = np.random.default_rng(77)
+    H, D, T = 2, 128, [300, 300, 200]
+    data = [(rng.standard_normal((H, t, D)).astype(np.float32), rng.standard_normal((H, t, D)).astype(np.float32))
+            for t in T]
+    for s in (1, 2):  # the first 128 tokens (2 groups) of sequences 1 and 2 are sequence 0's
+        data[s][0][:, :128] = data[0][0][:, :128]
+        data[s][1][:, :128] = data[0][1][:, :128]
+    tables = np.concatenate([kv.build_table(data[0][i][h][:256].reshape(-1, 16, D)) for h in range(H) for i in (0, 1)])
+    shared = {1: (0, 2), 2: (0, 2)}
+    args = (lambda s: data[s], 3, H, np.array(T), D)
+    mixed = kv.build_batched(kv.CODEC_RANS_HYBRID, *args, tables, "cpu", keep_host=True, shared=shared,
+                             raw_groups={0: 2, 1: 3})
+    rans = kv.build_batched(kv.CODEC_RANS_HYBRID, *args, tables, "cpu", keep_host=True, shared=shared)
+    raw = kv.build_batched(kv.CODEC_INT8, *args, None, "cpu", keep_host=True, shared=shared)
+    assert mixed.pool_bytes < rans.pool_bytes + 2 * raw.pool_bytes  # sanity: nothing duplicated wholesale
+    for s in range(3):
+        for h in range(H):
+            for g in range((T[s] + 63) // 64):
+                is_raw = g < (2 if s != 1 else 3)
+                ref = raw if is_raw else rans
+                off_m = int(mixed.host_offsets[s, h, g]) * 16
+                off_r = int(ref.host_offsets[s, h, g]) * 16
+                got = O.kv_decode_group(mixed.host_pool[off_m:off_m + 65536], tables, h, D)
+                exp = O.kv_decode_group(ref.host_pool[off_r:off_r + 65536], tables, h, D)
+                for a, b in zip(got, exp):
+                    assert np.array_equal(a, b), (s, h, g)
+                codec = int(mixed.host_pool[off_m:off_m + 4].view(np.uint32)[0])  # cf_kv_group_header.codec
+                assert codec == (kv.CODEC_INT8 if is_raw else kv.CODEC_RANS_HYBRID), (s, h, g)
+            if s:
+                assert np.array_equal(mixed.host_offsets[s, h, :2], mixed.host_offsets[0, h, :2])
+    with pytest.raises(ValueError):
+        kv.build_batched(kv.CODEC_RANS_HYBRID, *args, tables, "cpu", encoder="device", raw_groups={0: 1})
