@@ -4,18 +4,16 @@
 //   cf_fused_matmul_async  reference src/cuda/fused_matmul.cu:17-38, 67-80: one block-Huffman stream over row-major
 //                          W (block_off every `block` symbols, one LUT), W = (q - zero) * scale per tensor, fp32 x;
 //   cf_dense_matmul_async  reference src/cuda/fused_matmul.cu:41-65, 83-96: decode W to dense fp32 (the reference's
-//                          exact values), then the reference's k-outer / b-inner fp32 GEMM order per output;
-//   cf_qw_matmul_async     the MI355X-side format (include/chromofold/chromofold_qw.h): int4 symbols coded per
-//                          (row, 64-column segment) with one canonical-Huffman table per 16-row band, a scale per
-//                          (row, 64-column segment), bf16 activations.
+//                          exact values), then the reference's k-outer / b-inner fp32 GEMM order per output.
+// (The band-table int4 format of chromofold_qw.h has its own kernel in qw_matmul.hip.)
 //
-// One kernel design serves both fused entry points. A 1024-thread workgroup (16 waves) owns 16 rows of W:
+// A 1024-thread workgroup (16 waves) owns 16 rows of W:
 //   decode   lanes decode the code blocks / segments covering the tile's 16 rows x a 4096-column chunk straight
 //            into LDS as u8 symbols (register bit window, LUT staged in LDS);
 //   MFMA     v_mfma_f32_16x16x16_bf16 with A = x (batch x k, 16 batch rows per tile) and B = the decoded symbols
 //            (k x 16 rows). Symbols are small integers, exact in bf16. fp32 activations are split exactly into three
 //            bf16 terms (x = h + m + l, 8 mantissa bits each), so every product is exact and only the fp32
-//            accumulation rounds; bf16 activations need one term. The 16 waves split the k-steps; per-wave partial
+//            accumulation rounds. The 16 waves split the k-steps; per-wave partial
 //            tiles are reduced through LDS in a fixed order (deterministic), scaled, and written once — y needs no
 //            prior zeroing and is never read-modify-written.
 // Batches are padded to tiles of 16 (MFMA rows); 4 batch tiles (B <= 64) are served per pass over W.
@@ -23,7 +21,6 @@
 
 #include "cf_device.hpp"
 #include "chromofold/chromofold_extra.h"
-#include "chromofold/chromofold_qw.h"
 #include "huffman_core.hpp"
 
 namespace {
@@ -48,20 +45,12 @@ constexpr int kSmemTile = kSmemW > kSmemRed ? kSmemW : kSmemRed;
 
 static_assert(kTM * (kKC / 64) == kThreads, "one 64-column segment per lane per chunk");
 
-enum XKind { kXf32 = 0, kXbf16 = 1 };
-
 struct Args {
-  // reference stream (cf_fused_matmul_async)
   const uint32_t *words;
   const int32_t *block_off;
   const int32_t *lut;
   int maxlen, block;
-  // qw format (cf_qw_matmul_async)
-  const uint32_t *seg_off;
-  const uint8_t *code_len;
-  const float *seg_scale;
-  // operands
-  const void *x;
+  const float *x;
   float *y;
   int B, M, K;
   float scale;
@@ -83,56 +72,21 @@ __device__ __forceinline__ short bf16_of_int(int v) {  // |v| <= 256: exact
   return static_cast<short>(__float_as_uint(static_cast<float>(v)) >> 16);
 }
 
-// canonical-Huffman LUT (symbol | length << 8 over maxlen lookahead bits) from 16 code lengths, built in LDS. The
-// canonical code of symbol s is sum over the symbols t before it in (length, symbol) order of 2^(L_s - L_t); lanes
-// 0..15 compute one symbol each, then every thread fills its share of the table from the 16 (code, length) pairs.
-__device__ void build_band_lut(const uint8_t *__restrict__ len16, int maxlen, int32_t *__restrict__ lut,
-                               uint32_t *__restrict__ s_first) {
-  const int t = threadIdx.x;
-  if (t < 16) {
-    const int L = len16[t];
-    uint32_t code = 0;
-    for (int u = 0; u < 16; ++u) {
-      const int Lu = len16[u];
-      if (Lu > 0 && (Lu < L || (Lu == L && u < t))) code += 1u << (L - Lu);
-    }
-    // first table entry of the symbol's range and the range length (0 for an absent symbol)
-    s_first[t] = L > 0 ? (code << (maxlen - L)) : 0u;
-    s_first[16 + t] = L > 0 ? (1u << (maxlen - L)) : 0u;
-    s_first[32 + t] = static_cast<uint32_t>(t | (L << 8));
-  }
-  __syncthreads();
-  for (int e = t; e < (1 << maxlen); e += kThreads) {
-    int v = 0;
-#pragma unroll
-    for (int u = 0; u < 16; ++u)
-      if (static_cast<uint32_t>(e) - s_first[u] < s_first[16 + u]) v = static_cast<int>(s_first[32 + u]);
-    lut[e] = v;
-  }
-}
-
-template <bool kQw, XKind kX>
 __global__ void __launch_bounds__(kThreads) fused_matmul_kernel(Args a) {
   __shared__ __attribute__((aligned(16))) uint8_t s_tile[kSmemTile];
   __shared__ int32_t s_lut[1 << kLutBits];
-  __shared__ uint32_t s_first[48];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int m0 = blockIdx.x * kTM;
   const int B = a.B, M = a.M, K = a.K;
-  const int zc = kQw ? a.zero : min(255, max(0, a.zero));  // symbols are u8: q - zc stays within +-255
+  const int zc = min(255, max(0, a.zero));  // symbols are u8: q - zc stays within +-255
 
-  // code table for this workgroup
+  // the code table, staged in LDS when it fits
   const int32_t *lut = a.lut;
-  int maxlen = a.maxlen;
-  if constexpr (kQw) {
-    maxlen = CF_QW_MAX_CODE_LENGTH;
-    build_band_lut(a.code_len + (m0 / CF_QW_BAND_ROWS) * 16, maxlen, s_lut, s_first);
-    lut = s_lut;
-  } else if (a.maxlen <= kLutBits) {
+  const int maxlen = a.maxlen;
+  if (a.maxlen <= kLutBits) {
     for (int e = t; e < (1 << a.maxlen); e += kThreads) s_lut[e] = a.lut[e];
     lut = s_lut;
   }
-  const int nseg = (K + 63) / 64;
 
   for (int bt0 = 0; bt0 < (B + 15) / 16; bt0 += kBT) {
     f32x4_t acc[kBT];
@@ -141,35 +95,26 @@ __global__ void __launch_bounds__(kThreads) fused_matmul_kernel(Args a) {
 
     for (int kc0 = 0; kc0 < K; kc0 += kKC) {
       const int kc1 = min(K, kc0 + kKC);
-      __syncthreads();  // previous chunk (or the LUT build) done
+      __syncthreads();  // previous chunk (or the table staging) done
       {  // decode: lane -> (row r, 64-column segment s) of the chunk; 4 symbols per LDS word write
         const int r = t >> 6, s = t & 63;
         const int m = m0 + r, k0 = kc0 + 64 * s;
         uint32_t *dst = reinterpret_cast<uint32_t *>(s_tile + r * kLdB + kSegB * s);
         const int n = (m < M && k0 < kc1) ? min(64, kc1 - k0) : 0;
         const uint32_t pad = static_cast<uint32_t>(zc) * 0x01010101u;  // padding contributes q - zc = 0
-        auto emit = [&](auto &br) {
+        // skip-decode from the start of the code block holding W[m, k0]
+        const int64_t f = static_cast<int64_t>(m) * K + k0;
+        const int64_t bs = n > 0 ? f / a.block : 0;
+        cfh::BitReader br(a.words, static_cast<int64_t>(a.block_off[bs]));
+        if (n > 0)
+          for (int64_t i = bs * a.block; i < f; ++i) br.decode(lut, maxlen);
 #pragma unroll 4
-          for (int q = 0; q < 16; ++q) {
-            uint32_t w = pad;
+        for (int q = 0; q < 16; ++q) {
+          uint32_t w = pad;
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (4 * q + e < n) w = (w & ~(0xFFu << (8 * e))) | ((br.decode(lut, maxlen) & 0xFFu) << (8 * e));
-            dst[q] = w;
-          }
-        };
-        if constexpr (kQw) {
-          cfh::BitReader br(a.words, n > 0 ? static_cast<int64_t>(a.seg_off[static_cast<int64_t>(m) * nseg + k0 / 64])
-                                           : 0);
-          emit(br);
-        } else {
-          // reference stream: skip-decode from the start of the code block holding W[m, k0]
-          const int64_t f = static_cast<int64_t>(m) * K + k0;
-          const int64_t bs = n > 0 ? f / a.block : 0;
-          cfh::BitReader br(a.words, static_cast<int64_t>(a.block_off[bs]));
-          if (n > 0)
-            for (int64_t i = bs * a.block; i < f; ++i) br.decode(lut, maxlen);
-          emit(br);
+          for (int e = 0; e < 4; ++e)
+            if (4 * q + e < n) w = (w & ~(0xFFu << (8 * e))) | ((br.decode(lut, maxlen) & 0xFFu) << (8 * e));
+          dst[q] = w;
         }
       }
       __syncthreads();
@@ -184,45 +129,25 @@ __global__ void __launch_bounds__(kThreads) fused_matmul_kernel(Args a) {
         bfrag[1] = bf16_of_int(static_cast<int>((q4 >> 8) & 0xff) - zc);
         bfrag[2] = bf16_of_int(static_cast<int>((q4 >> 16) & 0xff) - zc);
         bfrag[3] = bf16_of_int(static_cast<int>(q4 >> 24) - zc);
-        float sc = 1.f;
-        if constexpr (kQw) {
-          const int m = min(m0 + bn, M - 1);
-          sc = a.seg_scale[static_cast<int64_t>(m) * nseg + (kc0 + st * 16) / 64];
-        }
         const int k = kc0 + kk;
 #pragma unroll
         for (int i = 0; i < kBT; ++i) {
           const int b = (bt0 + i) * 16 + (lane & 15);
           if ((bt0 + i) * 16 >= B) break;  // wave-uniform
-          f32x4_t part = kQw ? f32x4_t{0.f, 0.f, 0.f, 0.f} : acc[i];
-          if constexpr (kX == kXbf16) {
-            const uint16_t *xr = static_cast<const uint16_t *>(a.x) + static_cast<int64_t>(b) * K;
-            bf16x4_t afrag;
+          const float *xr = a.x + static_cast<int64_t>(b) * K;
+          bf16x4_t ah, am, al;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) afrag[e] = (b < B && k + e < K) ? static_cast<short>(xr[k + e]) : short(0);
-            part = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(afrag, bfrag, part, 0, 0, 0);
-          } else {
-            const float *xr = static_cast<const float *>(a.x) + static_cast<int64_t>(b) * K;
-            bf16x4_t ah, am, al;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float xv = (b < B && k + e < K) ? xr[k + e] : 0.f;
-              short h, mm, l;
-              split3(xv, h, mm, l);
-              ah[e] = h;
-              am[e] = mm;
-              al[e] = l;
-            }
-            part = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bfrag, part, 0, 0, 0);
-            part = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(am, bfrag, part, 0, 0, 0);
-            part = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bfrag, part, 0, 0, 0);
+          for (int e = 0; e < 4; ++e) {
+            const float xv = (b < B && k + e < K) ? xr[k + e] : 0.f;
+            short h, mm, l;
+            split3(xv, h, mm, l);
+            ah[e] = h;
+            am[e] = mm;
+            al[e] = l;
           }
-          if constexpr (kQw) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[i][e] += sc * part[e];  // lane's column is row bn: one scale
-          } else {
-            acc[i] = part;
-          }
+          acc[i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bfrag, acc[i], 0, 0, 0);
+          acc[i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(am, bfrag, acc[i], 0, 0, 0);
+          acc[i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(al, bfrag, acc[i], 0, 0, 0);
         }
       }
     }
@@ -241,20 +166,14 @@ __global__ void __launch_bounds__(kThreads) fused_matmul_kernel(Args a) {
       float s = 0.f;
       for (int w = 0; w < kWaves; ++w) s += red[(w * kBT + i) * 256 + idx];
       if (b < B && m < M) {
-        float v;
-        if constexpr (kQw) {
-          v = s;
-        } else {
-          // out-of-range zero points: the u8 symbols were offset by zc, the rest is -(zero - zc) * sum_k x[b, k]
-          float corr = 0.f;
-          if (a.zero != zc) {
-            const float *xr = static_cast<const float *>(a.x) + static_cast<int64_t>(b) * K;
-            for (int k = 0; k < K; ++k) corr += xr[k];
-            corr *= static_cast<float>(a.zero - zc);
-          }
-          v = (s - corr) * a.scale;
+        // out-of-range zero points: the u8 symbols were offset by zc, the rest is -(zero - zc) * sum_k x[b, k]
+        float corr = 0.f;
+        if (a.zero != zc) {
+          const float *xr = a.x + static_cast<int64_t>(b) * K;
+          for (int k = 0; k < K; ++k) corr += xr[k];
+          corr *= static_cast<float>(a.zero - zc);
         }
-        a.y[static_cast<int64_t>(b) * M + m] = v;
+        a.y[static_cast<int64_t>(b) * M + m] = (s - corr) * a.scale;
       }
     }
     __syncthreads();
@@ -319,7 +238,7 @@ extern "C" cf_status cf_fused_matmul_async(const uint32_t *words, const int32_t 
   a.K = K;
   a.scale = scale;
   a.zero = zero;
-  fused_matmul_kernel<false, kXf32><<<cfd::grid_for(M, kTM), kThreads, 0, cfd::as_stream(stream)>>>(a);
+  fused_matmul_kernel<<<cfd::grid_for(M, kTM), kThreads, 0, cfd::as_stream(stream)>>>(a);
   return cfd::launch_status();
 }
 
@@ -336,38 +255,5 @@ extern "C" cf_status cf_dense_matmul_async(const uint32_t *words, const int32_t 
     decode_dense_kernel<<<cfd::grid_for(static_cast<size_t>((n + block - 1) / block), 256), 256, 0, s>>>(
         words, block_off, lut, maxlen, block, n, scale, zero, W);
   if (B > 0) dense_gemm_kernel<16><<<cfd::grid_for(M, 256), 256, 0, s>>>(W, x, y, B, M, K);
-  return cfd::launch_status();
-}
-
-extern "C" cf_status cf_qw_validate(const cf_qw_matrix *w) {
-  if (!w || w->struct_size != sizeof(cf_qw_matrix) || w->abi_version != CF_QW_ABI_VERSION)
-    return CF_ERR_INVALID_ARGUMENT;
-  if (w->codec != CF_QW_CODEC_HUFFMAN) return CF_ERR_UNSUPPORTED;
-  if (w->rows == 0 || w->cols == 0 || w->rows > (1u << 30) || w->cols > (1u << 30)) return CF_ERR_INVALID_ARGUMENT;
-  if (!w->words || !w->seg_offsets || !w->code_lengths || !w->scales || w->word_count == 0)
-    return CF_ERR_INVALID_ARGUMENT;
-  if (w->zero < 0 || w->zero > 15) return CF_ERR_INVALID_ARGUMENT;
-  return CF_OK;
-}
-
-extern "C" cf_status cf_qw_matmul_async(const cf_qw_matrix *w, const uint16_t *x, float *y, uint32_t batch,
-                                        void *stream) {
-  const cf_status st = cf_qw_validate(w);
-  if (st != CF_OK) return st;
-  if (!x || !y) return CF_ERR_INVALID_ARGUMENT;
-  if (batch == 0) return CF_OK;
-  if (batch > (1u << 20)) return CF_ERR_UNSUPPORTED;
-  Args a{};
-  a.words = w->words;
-  a.seg_off = w->seg_offsets;
-  a.code_len = w->code_lengths;
-  a.seg_scale = w->scales;
-  a.x = x;
-  a.y = y;
-  a.B = static_cast<int>(batch);
-  a.M = static_cast<int>(w->rows);
-  a.K = static_cast<int>(w->cols);
-  a.zero = w->zero;
-  fused_matmul_kernel<true, kXbf16><<<cfd::grid_for(a.M, kTM), kThreads, 0, cfd::as_stream(stream)>>>(a);
   return cfd::launch_status();
 }

@@ -41,7 +41,7 @@ typedef struct cf_qw_matrix {
   uint64_t word_count;  /* 32-bit words of `words` (bounds the decoder's read-ahead) */
   const uint32_t *words;        /* device: code stream */
   const uint32_t *seg_offsets;  /* device: [rows * ceil(cols / 64)] bit offsets */
-  const uint8_t *code_lengths;  /* device: [ceil(rows / 16) * 16] */
+  const uint8_t *code_lengths;  /* device: [ceil(rows / 16) * 16], 16-byte aligned */
   const float *scales;          /* device: [rows * ceil(cols / 64)] */
 } cf_qw_matrix;
 

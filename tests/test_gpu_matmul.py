@@ -80,12 +80,10 @@ def test_reference_stream_contract(dev):
     assert L.cf_dense_matmul_async(p, p, p, 8, 64, p, None, p, 1, 1, 1, 1.0, 8, None) == _abi.CF_ERR_INVALID_ARGUMENT
 
 
-@pytest.mark.parametrize("M,K,batches", [(4096, 4096, (1, 4, 16, 64)), (40, 1000, (3, 17)), (24, 8200, (64,))])
-def test_qw_matmul(dev, M, K, batches):
+def _qw_check(dev, W, batches):
     import torch
     from chromofold_amd import qw
-    rng = np.random.default_rng(M * 3 + K)
-    W = rng.standard_normal((M, K)).astype(np.float32)
+    M, K = W.shape
     h = qw.encode_int4(W)
     mat = qw.QwMatrix(h, dev)
     scales = np.repeat(h.scales, 64, axis=1)[:, :K]
@@ -98,3 +96,57 @@ def test_qw_matmul(dev, M, K, batches):
         ref = O.qmatmul_f64(xf.float().numpy(), h.sym, scales, 8)
         e = _err(y.cpu().numpy(), ref)
         assert e <= 1e-3, (B, e)
+    return h
+
+
+@pytest.mark.parametrize("M,K,batches", [(4096, 4096, (1, 4, 16, 64)), (40, 1000, (3, 17)), (24, 8200, (64,)),
+                                         (33, 1001, (70, 1))])
+def test_qw_matmul(dev, M, K, batches):
+    # ragged rows (not a band multiple), K not a multiple of 64 (or of 4: scalar x loads), K over one 4096-column
+    # chunk, and 70 batch rows (two launches: 4 tiles + 1)
+    rng = np.random.default_rng(M * 3 + K)
+    _qw_check(dev, rng.standard_normal((M, K)).astype(np.float32), batches)
+
+
+def test_qw_matmul_skewed_band(dev):
+    """A band whose rows differ wildly: 14 zero rows, one two-valued row and one uniform row. The uniform row's
+    codes average ~7 bits, more than the kernel stages in LDS per row (640 words per 4096-column chunk), so its
+    lanes decode straight from global memory; the other bands take the staged path."""
+    rng = np.random.default_rng(99)
+    M, K = 48, 4096
+    W = np.zeros((M, K), np.float32)
+    W[14] = np.where(rng.random(K) < 0.5, -1.0, 1.0)
+    W[15] = rng.uniform(-1, 1, K)
+    W[16:] = rng.standard_normal((32, K))
+    h = _qw_check(dev, W, (1, 16))
+    offs = h.seg_offsets.astype(np.int64).ravel()
+    ends = np.append(offs[1:], h.words.size * 32).reshape(M, -1)
+    first = offs.reshape(M, -1)[:, 0]
+    need = (ends[:, -1] >> 5) + 6 - ((first >> 5) & ~3)
+    assert need[15] > 640 and need[16:].max() <= 640, need
+
+
+def test_qw_matmul_graph_replays(dev):
+    """cf_qw_matmul_async captured in a HIP graph: every replay (with eager work changing x in between) equals the
+    eager call on the same x bit for bit."""
+    import torch
+    from chromofold_amd import qw
+    rng = np.random.default_rng(7)
+    M, K, B = 64, 4096, 16
+    mat = qw.QwMatrix(qw.encode_int4(rng.standard_normal((M, K)).astype(np.float32)), dev)
+    x = torch.zeros((B, K), dtype=torch.bfloat16, device=dev)
+    y = torch.zeros((B, M), device=dev)
+    mat.matmul_into(x, y)  # warm up outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        mat.matmul_into(x, y)
+    for r in range(3):
+        xr = torch.from_numpy(rng.standard_normal((B, K)).astype(np.float32)).to(torch.bfloat16).to(dev)
+        x.copy_(xr)
+        g.replay()
+        torch.cuda.synchronize()
+        got = y.clone()
+        want = mat.matmul(xr)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), r
