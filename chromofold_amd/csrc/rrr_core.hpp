@@ -25,10 +25,47 @@ __device__ __forceinline__ uint32_t read_bits(const uint32_t *__restrict__ s, in
   return static_cast<uint32_t>(both >> b) & ((1u << w) - 1u);
 }
 
+// Where rank1 reads the per-superblock samples and the unrank table: straight from the view (global memory, L2)
+// or from copies staged in LDS by a persistent kernel (LdsTables, see rrr_wavelet.hip).
+struct GlobalTables {
+  const cf_rrrw_view &v;
+  __device__ int rank(size_t arow_a, size_t srow_sb) const { return v.rank_a[arow_a] + v.rank_d[srow_sb]; }
+  __device__ int off(size_t arow_a, size_t srow_sb) const { return v.off_a[arow_a] + v.off_d[srow_sb]; }
+  __device__ int base(int k) const { return kTab.base[k]; }
+  __device__ uint32_t unrank(int i) const { return kTab.unrank[i]; }
+};
+struct LdsTables {
+  const int32_t *rank_a, *off_a;   // [bits * na]
+  const uint16_t *rank_d, *off_d;  // [bits * (nsb + 1)]
+  const uint16_t *unrank_tab;      // the 64 KiB unrank table
+  const int32_t *base_tab;         // the unrank table's class starts (17 entries)
+  __device__ int rank(size_t arow_a, size_t srow_sb) const { return rank_a[arow_a] + rank_d[srow_sb]; }
+  __device__ int off(size_t arow_a, size_t srow_sb) const { return off_a[arow_a] + off_d[srow_sb]; }
+  __device__ int base(int k) const { return base_tab[k]; }
+  __device__ uint32_t unrank(int i) const { return unrank_tab[i]; }
+};
+
+// The 8 class words of superblock sbi: two 16-byte loads (4-byte aligned) when all 8 lie inside the level's
+// `cwords`, otherwise word by word (only the level's last superblock can be short).
+__device__ __forceinline__ void class_words(const uint32_t *__restrict__ cls, int sbi, int cwords, int full,
+                                            uint32_t (&x)[8]) {
+  const uint32_t *__restrict__ cw = cls + (static_cast<size_t>(sbi) << 3);
+  if ((sbi << 3) + 8 <= cwords) {
+    uint4 a, b;
+    __builtin_memcpy(&a, cw, 16);
+    __builtin_memcpy(&b, cw + 4, 16);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+  } else {
+#pragma unroll
+    for (int w = 0; w < 8; ++w) x[w] = w <= full ? cw[w] : 0u;
+  }
+}
+
 // rank1 of level `lvl` over [0, pos); with kBit also the plane bit at pos (the access primitive, one block decode
 // serving both). reference rrr_wavelet_device.cuh:56-113.
-template <bool kBit>
-__device__ __forceinline__ int rank1_lvl(const cf_rrrw_view &v, int lvl, int pos, int *bit) {
+template <bool kBit, class Tables, bool kVecClasses = false>
+__device__ __forceinline__ int rank1_lvl_t(const cf_rrrw_view &v, const Tables &tb, int lvl, int pos, int *bit) {
   const uint32_t *__restrict__ cls = v.classes + static_cast<size_t>(lvl) * v.cwords;
   const size_t srow = static_cast<size_t>(lvl) * (v.nsb + 1);
   const size_t arow = static_cast<size_t>(lvl) * v.na;
@@ -36,19 +73,26 @@ __device__ __forceinline__ int rank1_lvl(const cf_rrrw_view &v, int lvl, int pos
   const int b = pos - blk * cfd::kRrrT;
   const int sbi = blk >> 6;  // / kRrrS
   const int a = sbi >> 5;    // / kRrrK
-  int r = v.rank_a[arow + a] + static_cast<int>(v.rank_d[srow + sbi]);
-  int obit = v.off_a[arow + a] + static_cast<int>(v.off_d[srow + sbi]);
+  int r = tb.rank(arow + a, srow + sbi);
+  const int obit = tb.off(arow + a, srow + sbi);
 
   // class words of superblock sbi: blocks [sbi*64 + 8w, +8) live in word sbi*8 + w
-  const uint32_t *__restrict__ cw = cls + (static_cast<size_t>(sbi) << 3);
   const int nblk = blk - (sbi << 6);  // blocks to sum before the target block, 0..63
   const int full = nblk >> 3, rem = nblk & 7;
+  uint32_t xs[8];
+  if constexpr (kVecClasses) {
+    class_words(cls, sbi, v.cwords, full, xs);
+  } else {
+    const uint32_t *__restrict__ cw = cls + (static_cast<size_t>(sbi) << 3);
+#pragma unroll
+    for (int w = 0; w < 8; ++w) xs[w] = w <= full ? cw[w] : 0u;
+  }
   int csum = 0, wsum = 0;
   uint32_t target_word = 0;
 #pragma unroll
   for (int w = 0; w < 8; ++w) {
     if (w <= full) {
-      uint32_t x = cw[w];
+      uint32_t x = xs[w];
       if (w == full) {
         target_word = x;
         x &= rem ? ((1u << (4 * rem)) - 1u) : 0u;
@@ -62,21 +106,26 @@ __device__ __forceinline__ int rank1_lvl(const cf_rrrw_view &v, int lvl, int pos
     const int k = static_cast<int>((target_word >> (4 * rem)) & 15u);
     const int w = cfd::width_of(k);
     const uint32_t off = w ? read_bits(v.offsets, static_cast<int64_t>(v.offbase[lvl]) + obit + wsum, w) : 0u;
-    const uint32_t word = kTab.unrank[kTab.base[k] + off];
+    const uint32_t word = tb.unrank(tb.base(k) + static_cast<int>(off));
     r += __popc(word & ((1u << b) - 1u));
     if (kBit) *bit = static_cast<int>((word >> b) & 1u);
   }
   return r;
 }
 
+template <bool kBit>
+__device__ __forceinline__ int rank1_lvl(const cf_rrrw_view &v, int lvl, int pos, int *bit) {
+  return rank1_lvl_t<kBit>(v, GlobalTables{v}, lvl, pos, bit);
+}
+
 // token at position i: one block decode per level (reference rrr_wavelet_device.cuh:117-134)
-template <int LEVELS>
-__device__ __forceinline__ uint32_t access_one(const cf_rrrw_view &v, int i) {
+template <int LEVELS, class Tables, bool kVec>
+__device__ __forceinline__ uint32_t access_one_t(const cf_rrrw_view &v, const Tables &tb, int i) {
   const int L = LEVELS > 0 ? LEVELS : v.bits;
   uint32_t val = 0;
   for (int lvl = 0; lvl < L; ++lvl) {
     int bit = 0;
-    const int r = rank1_lvl<true>(v, lvl, i, &bit);
+    const int r = rank1_lvl_t<true, Tables, kVec>(v, tb, lvl, i, &bit);
     val = (val << 1) | static_cast<uint32_t>(bit);
     i = bit ? v.zeros[lvl] + r : i - r;
   }
@@ -85,14 +134,14 @@ __device__ __forceinline__ uint32_t access_one(const cf_rrrw_view &v, int i) {
 
 // occurrences of c in [0, i): two rank1 per level narrowing [p, q) (reference rrr_wavelet_device.cuh:137-149).
 // Once the interval is empty every later level keeps it empty, so the walk stops early with the same answer.
-template <int LEVELS>
-__device__ __forceinline__ uint32_t rank_one(const cf_rrrw_view &v, int c, int i) {
+template <int LEVELS, class Tables, bool kVec>
+__device__ __forceinline__ uint32_t rank_one_t(const cf_rrrw_view &v, const Tables &tb, int c, int i) {
   const int L = LEVELS > 0 ? LEVELS : v.bits;
   int p = 0, q = i;
   for (int lvl = 0; lvl < L; ++lvl) {
     if (p >= q) break;
-    const int rp = rank1_lvl<false>(v, lvl, p, nullptr);
-    const int rq = rank1_lvl<false>(v, lvl, q, nullptr);
+    const int rp = rank1_lvl_t<false, Tables, kVec>(v, tb, lvl, p, nullptr);
+    const int rq = rank1_lvl_t<false, Tables, kVec>(v, tb, lvl, q, nullptr);
     if ((c >> (L - 1 - lvl)) & 1) {
       p = v.zeros[lvl] + rp;
       q = v.zeros[lvl] + rq;
@@ -102,6 +151,16 @@ __device__ __forceinline__ uint32_t rank_one(const cf_rrrw_view &v, int c, int i
     }
   }
   return static_cast<uint32_t>(q - p);
+}
+
+template <int LEVELS>
+__device__ __forceinline__ uint32_t access_one(const cf_rrrw_view &v, int i) {
+  return access_one_t<LEVELS, GlobalTables, false>(v, GlobalTables{v}, i);
+}
+
+template <int LEVELS>
+__device__ __forceinline__ uint32_t rank_one(const cf_rrrw_view &v, int c, int i) {
+  return rank_one_t<LEVELS, GlobalTables, false>(v, GlobalTables{v}, c, i);
 }
 
 // rank(c, lo) and rank(c, hi) together: both walks share the start-of-c chain p (its rank1 is computed once),
