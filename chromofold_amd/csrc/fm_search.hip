@@ -17,9 +17,9 @@ namespace {
 constexpr unsigned kThreads = 256;
 
 // reference fm_search_device.cuh:31-48
-template <int LEVELS>
+template <int LEVELS, class Tables = cfr::GlobalTables, bool kVec = false>
 __device__ __forceinline__ void backward(const cf_fm_view &v, const int32_t *__restrict__ pat, int st, int len,
-                                         int &lo, int &hi) {
+                                         int &lo, int &hi, const Tables &tb) {
   lo = 0;
   hi = v.n;
   for (int k = len - 1; k >= 0; --k) {
@@ -30,7 +30,7 @@ __device__ __forceinline__ void backward(const cf_fm_view &v, const int32_t *__r
     }
     if (lo < hi) {
       int rl, rh;
-      cfr::rank_pair<LEVELS>(v.w, c, lo, hi, rl, rh);
+      cfr::rank_pair<LEVELS, Tables, kVec>(v.w, c, lo, hi, rl, rh, tb);
       lo = v.C[c] + rl;
       hi = v.C[c] + rh;
     }
@@ -45,7 +45,7 @@ __global__ __launch_bounds__(kThreads) void fm_count_kernel(cf_fm_view v, const 
   const size_t t = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
   if (t >= npat) return;
   int lo, hi;
-  backward<LEVELS>(v, pat, pstart[t], plen[t], lo, hi);
+  backward<LEVELS>(v, pat, pstart[t], plen[t], lo, hi, cfr::GlobalTables{v.w});
   out[t] = static_cast<uint32_t>(hi - lo);
 }
 
@@ -58,18 +58,18 @@ __global__ __launch_bounds__(kThreads) void fm_ranges_kernel(cf_fm_view v, const
   const size_t t = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
   if (t >= npat) return;
   int lo, hi;
-  backward<LEVELS>(v, pat, pstart[t], plen[t], lo, hi);
+  backward<LEVELS>(v, pat, pstart[t], plen[t], lo, hi, cfr::GlobalTables{v.w});
   lo_out[t] = lo;
   hi_out[t] = hi;
 }
 
 // reference fm_search_device.cuh:52-62
-template <int LEVELS>
-__device__ __forceinline__ int32_t locate_one(const cf_fm_view &v, int p) {
+template <int LEVELS, class Tables = cfr::GlobalTables, bool kVec = false>
+__device__ __forceinline__ int32_t locate_one(const cf_fm_view &v, int p, const Tables &tb) {
   int steps = 0;
   while (!((v.mwords[p >> 5] >> (p & 31)) & 1u)) {
     int c;
-    const int r = cfr::access_rank<LEVELS>(v.w, p, c);
+    const int r = cfr::access_rank<LEVELS, Tables, kVec>(v.w, p, c, tb);
     p = v.C[c] + r;
     ++steps;
   }
@@ -82,8 +82,71 @@ __global__ __launch_bounds__(kThreads) void fm_locate_kernel(cf_fm_view v, const
                                                              int32_t *__restrict__ out, size_t nocc) {
   const size_t t = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x;
   if (t >= nocc) return;
-  out[t] = locate_one<LEVELS>(v, rows[t]);
+  out[t] = locate_one<LEVELS>(v, rows[t], cfr::GlobalTables{v.w});
 }
+
+// ---- persistent variants: one 1024-thread workgroup per CU stages the wavelet's anchors, the unrank table and
+// its class starts (and, for small indexes, the per-superblock deltas) in LDS, then strides over the items.
+constexpr unsigned kStagedThreads = 1024;
+
+template <int LEVELS, bool kDeltas>
+__global__ __launch_bounds__(kStagedThreads) void fm_count_staged_kernel(cf_fm_view v, const int32_t *__restrict__ pat,
+                                                                         const int32_t *__restrict__ pstart,
+                                                                         const int32_t *__restrict__ plen,
+                                                                         uint32_t *__restrict__ out, size_t npat) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const auto tb = cfr::stage_tables<kDeltas>(v.w, smem, kStagedThreads);
+  for (size_t t = blockIdx.x * static_cast<size_t>(kStagedThreads) + threadIdx.x; t < npat;
+       t += static_cast<size_t>(gridDim.x) * kStagedThreads) {
+    int lo, hi;
+    backward<LEVELS, cfr::StagedTables<kDeltas>, true>(v, pat, pstart[t], plen[t], lo, hi, tb);
+    out[t] = static_cast<uint32_t>(hi - lo);
+  }
+}
+
+template <int LEVELS, bool kDeltas>
+__global__ __launch_bounds__(kStagedThreads) void fm_ranges_staged_kernel(
+    cf_fm_view v, const int32_t *__restrict__ pat, const int32_t *__restrict__ pstart,
+    const int32_t *__restrict__ plen, int32_t *__restrict__ lo_out, int32_t *__restrict__ hi_out, size_t npat) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const auto tb = cfr::stage_tables<kDeltas>(v.w, smem, kStagedThreads);
+  for (size_t t = blockIdx.x * static_cast<size_t>(kStagedThreads) + threadIdx.x; t < npat;
+       t += static_cast<size_t>(gridDim.x) * kStagedThreads) {
+    int lo, hi;
+    backward<LEVELS, cfr::StagedTables<kDeltas>, true>(v, pat, pstart[t], plen[t], lo, hi, tb);
+    lo_out[t] = lo;
+    hi_out[t] = hi;
+  }
+}
+
+template <int LEVELS, bool kDeltas>
+__global__ __launch_bounds__(kStagedThreads) void fm_locate_staged_kernel(cf_fm_view v,
+                                                                          const int32_t *__restrict__ rows,
+                                                                          int32_t *__restrict__ out, size_t nocc) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const auto tb = cfr::stage_tables<kDeltas>(v.w, smem, kStagedThreads);
+  for (size_t t = blockIdx.x * static_cast<size_t>(kStagedThreads) + threadIdx.x; t < nocc;
+       t += static_cast<size_t>(gridDim.x) * kStagedThreads)
+    out[t] = locate_one<LEVELS, cfr::StagedTables<kDeltas>, true>(v, rows[t], tb);
+}
+
+// Launches the staged variant when one applies (levels 15 and 16 get fixed-depth instances); false otherwise.
+#define CF_FM_STAGED(KERNEL, COUNT, ...)                                                                         \
+  do {                                                                                                        \
+    unsigned g = 0;                                                                                           \
+    const int mode = cfr::staged_mode(v.w, (COUNT), kStagedThreads, g);                                      \
+    if (mode != 0) {                                                                                          \
+      const size_t lb = cfr::stage_layout(v.w, mode == 2).bytes;                                              \
+      if (mode == 2) {                                                                                        \
+        if (v.w.bits == 15) return cfr::launch_staged(kStagedThreads, KERNEL<15, true>, g, lb, s, __VA_ARGS__); \
+        if (v.w.bits == 16) return cfr::launch_staged(kStagedThreads, KERNEL<16, true>, g, lb, s, __VA_ARGS__); \
+        return cfr::launch_staged(kStagedThreads, KERNEL<0, true>, g, lb, s, __VA_ARGS__);                    \
+      }                                                                                                       \
+      if (v.w.bits == 15) return cfr::launch_staged(kStagedThreads, KERNEL<15, false>, g, lb, s, __VA_ARGS__); \
+      if (v.w.bits == 16) return cfr::launch_staged(kStagedThreads, KERNEL<16, false>, g, lb, s, __VA_ARGS__); \
+      return cfr::launch_staged(kStagedThreads, KERNEL<0, false>, g, lb, s, __VA_ARGS__);                     \
+    }                                                                                                         \
+  } while (0)
 
 #define CF_FM_DISPATCH(LAUNCH) \
   switch (v.w.bits) {         \
@@ -102,6 +165,7 @@ extern "C" cf_status cf_fm_count_async(cf_fm_view v, const int32_t *pat, const i
   if (npat == 0) return CF_OK;
   if (v.w.bits <= 0 || v.w.bits > 31 || v.n <= 0) return CF_ERR_INVALID_ARGUMENT;
   const hipStream_t s = cfd::as_stream(stream);
+  CF_FM_STAGED(fm_count_staged_kernel, npat, v, pat, pstart, plen, out, npat);
   const unsigned blocks = cfd::grid_for(npat, kThreads);
 #define CF_LAUNCH(L) fm_count_kernel<L><<<blocks, kThreads, 0, s>>>(v, pat, pstart, plen, out, npat)
   CF_FM_DISPATCH(CF_LAUNCH)
@@ -117,6 +181,7 @@ extern "C" cf_status cf_fm_ranges_async(cf_fm_view v, const int32_t *pat, const 
   if (npat == 0) return CF_OK;
   if (v.w.bits <= 0 || v.w.bits > 31 || v.n <= 0) return CF_ERR_INVALID_ARGUMENT;
   const hipStream_t s = cfd::as_stream(stream);
+  CF_FM_STAGED(fm_ranges_staged_kernel, npat, v, pat, pstart, plen, lo_out, hi_out, npat);
   const unsigned blocks = cfd::grid_for(npat, kThreads);
 #define CF_LAUNCH(L) fm_ranges_kernel<L><<<blocks, kThreads, 0, s>>>(v, pat, pstart, plen, lo_out, hi_out, npat)
   CF_FM_DISPATCH(CF_LAUNCH)
@@ -132,6 +197,7 @@ extern "C" cf_status cf_fm_locate_async(cf_fm_view v, const int32_t *r_in, int32
   if (v.w.bits <= 0 || v.w.bits > 31 || v.n <= 0 || !v.mwords || !v.msb || !v.sval || !v.C)
     return CF_ERR_INVALID_ARGUMENT;
   const hipStream_t s = cfd::as_stream(stream);
+  CF_FM_STAGED(fm_locate_staged_kernel, nocc, v, r_in, out, nocc);
   const unsigned blocks = cfd::grid_for(nocc, kThreads);
 #define CF_LAUNCH(L) fm_locate_kernel<L><<<blocks, kThreads, 0, s>>>(v, r_in, out, nocc)
   CF_FM_DISPATCH(CF_LAUNCH)

@@ -34,16 +34,102 @@ struct GlobalTables {
   __device__ int base(int k) const { return kTab.base[k]; }
   __device__ uint32_t unrank(int i) const { return kTab.unrank[i]; }
 };
-struct LdsTables {
-  const int32_t *rank_a, *off_a;   // [bits * na]
-  const uint16_t *rank_d, *off_d;  // [bits * (nsb + 1)]
-  const uint16_t *unrank_tab;      // the 64 KiB unrank table
-  const int32_t *base_tab;         // the unrank table's class starts (17 entries)
+// Tables staged in LDS by a persistent kernel: the anchors, the unrank table and its class starts always; the
+// per-superblock deltas too when kDeltas (small indexes), else those stay in global memory.
+template <bool kDeltas>
+struct StagedTables {
+  const int32_t *rank_a, *off_a;   // LDS [bits * na]
+  const uint16_t *rank_d, *off_d;  // LDS or global [bits * (nsb + 1)]
+  const uint16_t *unrank_tab;      // LDS, the 64 KiB unrank table
+  const int32_t *base_tab;         // LDS, the unrank table's class starts (17 entries)
   __device__ int rank(size_t arow_a, size_t srow_sb) const { return rank_a[arow_a] + rank_d[srow_sb]; }
   __device__ int off(size_t arow_a, size_t srow_sb) const { return off_a[arow_a] + off_d[srow_sb]; }
   __device__ int base(int k) const { return base_tab[k]; }
   __device__ uint32_t unrank(int i) const { return unrank_tab[i]; }
 };
+
+// LDS layout of the staged tables (16-byte aligned parts); `bytes` = the workgroup's dynamic LDS.
+struct StageLayout {
+  size_t unrank, base, rank_a, off_a, rank_d, off_d, bytes;
+};
+
+__host__ __device__ inline size_t align16(size_t x) { return (x + 15) & ~static_cast<size_t>(15); }
+
+__host__ __device__ inline StageLayout stage_layout(const cf_rrrw_view &v, bool deltas) {
+  StageLayout l{};
+  const size_t nd = static_cast<size_t>(v.bits) * (v.nsb + 1), na = static_cast<size_t>(v.bits) * v.na;
+  l.unrank = 0;
+  l.base = align16(sizeof(cfd::RrrTables::unrank));
+  l.rank_a = l.base + align16(sizeof(cfd::RrrTables::base));
+  l.off_a = l.rank_a + align16(na * 4);
+  l.rank_d = l.off_a + align16(na * 4);
+  l.off_d = l.rank_d + (deltas ? align16(nd * 2) : 0);
+  l.bytes = l.off_d + (deltas ? align16(nd * 2) : 0);
+  return l;
+}
+
+// Cooperative copy by all `nthreads` threads of the workgroup, ending with a barrier.
+template <bool kDeltas>
+__device__ StagedTables<kDeltas> stage_tables(const cf_rrrw_view &v, uint8_t *smem, unsigned nthreads) {
+  const StageLayout l = stage_layout(v, kDeltas);
+  const unsigned t = threadIdx.x;
+  {
+    const uint4 *src = reinterpret_cast<const uint4 *>(kTab.unrank);
+    uint4 *dst = reinterpret_cast<uint4 *>(smem + l.unrank);
+    for (size_t i = t; i < sizeof(cfd::RrrTables::unrank) / 16; i += nthreads) dst[i] = src[i];
+  }
+  int32_t *bs = reinterpret_cast<int32_t *>(smem + l.base);
+  if (t < 17) bs[t] = kTab.base[t];
+  const size_t na = static_cast<size_t>(v.bits) * v.na;
+  int32_t *ra = reinterpret_cast<int32_t *>(smem + l.rank_a), *oa = reinterpret_cast<int32_t *>(smem + l.off_a);
+  for (size_t i = t; i < na; i += nthreads) {
+    ra[i] = v.rank_a[i];
+    oa[i] = v.off_a[i];
+  }
+  StagedTables<kDeltas> tb{ra, oa, v.rank_d, v.off_d, reinterpret_cast<const uint16_t *>(smem + l.unrank), bs};
+  if constexpr (kDeltas) {
+    const size_t nd = static_cast<size_t>(v.bits) * (v.nsb + 1);
+    uint16_t *rd = reinterpret_cast<uint16_t *>(smem + l.rank_d), *od = reinterpret_cast<uint16_t *>(smem + l.off_d);
+    for (size_t i = t; i < nd; i += nthreads) {
+      rd[i] = v.rank_d[i];
+      od[i] = v.off_d[i];
+    }
+    tb.rank_d = rd;
+    tb.off_d = od;
+  }
+  __syncthreads();
+  return tb;
+}
+
+// Launch of a persistent staged kernel with `bytes` of dynamic LDS (above the default 64 KiB limit).
+template <class K, class... Args>
+inline cf_status launch_staged(unsigned threads, K kernel, unsigned grid, size_t bytes, hipStream_t s,
+                               const Args &...args) {
+  if (hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          static_cast<int>(bytes)) != hipSuccess)
+    return CF_ERR_CUDA;
+  kernel<<<grid, threads, bytes, s>>>(args...);
+  return cfd::launch_status();
+}
+
+// Which staged variant a persistent launch of `threads`-thread workgroups over `count` items can use: 2 = every
+// table in LDS, 1 = all but the per-superblock deltas, 0 = none (the index is too large, or the batch too small to
+// give each lane of one workgroup per CU an item). `cus` receives the CU count.
+inline int staged_mode(const cf_rrrw_view &v, size_t count, unsigned threads, unsigned &cus) {
+  static int n_cu = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    return n;
+  }();
+  constexpr size_t kLimit = 160 * 1024;
+  cus = n_cu > 0 ? static_cast<unsigned>(n_cu) : 0u;
+  if (cus == 0 || v.bits <= 0 || v.nsb < 0 || v.na < 0 || count < static_cast<size_t>(cus) * threads) return 0;
+  if (stage_layout(v, true).bytes <= kLimit) return 2;
+  if (stage_layout(v, false).bytes <= kLimit) return 1;
+  return 0;
+}
 
 // The 8 class words of superblock sbi: two 16-byte loads (4-byte aligned) when all 8 lie inside the level's
 // `cwords`, otherwise word by word (only the level's last superblock can be short).
@@ -165,14 +251,15 @@ __device__ __forceinline__ uint32_t rank_one(const cf_rrrw_view &v, int c, int i
 
 // rank(c, lo) and rank(c, hi) together: both walks share the start-of-c chain p (its rank1 is computed once),
 // so a backward-search step costs 3 rank1 per level instead of 4. Identical results to two rank_one calls.
-template <int LEVELS>
-__device__ __forceinline__ void rank_pair(const cf_rrrw_view &v, int c, int lo, int hi, int &rlo, int &rhi) {
+template <int LEVELS, class Tables = GlobalTables, bool kVec = false>
+__device__ __forceinline__ void rank_pair(const cf_rrrw_view &v, int c, int lo, int hi, int &rlo, int &rhi,
+                                          const Tables &tb) {
   const int L = LEVELS > 0 ? LEVELS : v.bits;
   int p = 0, a = lo, b = hi;
   for (int lvl = 0; lvl < L; ++lvl) {
-    const int rp = rank1_lvl<false>(v, lvl, p, nullptr);
-    const int ra = rank1_lvl<false>(v, lvl, a, nullptr);
-    const int rb = rank1_lvl<false>(v, lvl, b, nullptr);
+    const int rp = rank1_lvl_t<false, Tables, kVec>(v, tb, lvl, p, nullptr);
+    const int ra = rank1_lvl_t<false, Tables, kVec>(v, tb, lvl, a, nullptr);
+    const int rb = rank1_lvl_t<false, Tables, kVec>(v, tb, lvl, b, nullptr);
     if ((c >> (L - 1 - lvl)) & 1) {
       p = v.zeros[lvl] + rp;
       a = v.zeros[lvl] + ra;
@@ -190,14 +277,14 @@ __device__ __forceinline__ void rank_pair(const cf_rrrw_view &v, int c, int lo, 
 // One LF-mapping step: c = BWT[i] and rank(c, i) in a single walk. The access walk of i follows exactly the bits
 // of c, so it IS the rank walk of position i for symbol c; only the start-of-c chain p needs its own rank1.
 // Returns rank(c, i) (so LF(i) = C[c] + rank) and writes c. Two rank1 per level instead of three.
-template <int LEVELS>
-__device__ __forceinline__ int access_rank(const cf_rrrw_view &v, int i, int &c_out) {
+template <int LEVELS, class Tables = GlobalTables, bool kVec = false>
+__device__ __forceinline__ int access_rank(const cf_rrrw_view &v, int i, int &c_out, const Tables &tb) {
   const int L = LEVELS > 0 ? LEVELS : v.bits;
   int p = 0, c = 0;
   for (int lvl = 0; lvl < L; ++lvl) {
     int bit = 0;
-    const int ri = rank1_lvl<true>(v, lvl, i, &bit);
-    const int rp = rank1_lvl<false>(v, lvl, p, nullptr);
+    const int ri = rank1_lvl_t<true, Tables, kVec>(v, tb, lvl, i, &bit);
+    const int rp = rank1_lvl_t<false, Tables, kVec>(v, tb, lvl, p, nullptr);
     c = (c << 1) | bit;
     if (bit) {
       i = v.zeros[lvl] + ri;
