@@ -124,3 +124,43 @@ def test_gpu_suffix_array_shapes(dev, n, vocab):
     tok = rng.integers(0, vocab, n).astype(np.uint32)
     s = O.fm_text(tok)
     assert np.array_equal(gpu_suffix_array(_i32(s, dev)).cpu().numpy(), O.suffix_array(s))
+
+
+def _fm_oracle_view(fm):
+    from chromofold_amd.search import to_u32
+    w = O.RrrwArrays(fm.w.bits, fm.w.cwords, fm.w.nsb, fm.w.na,
+                     *[fm.w.tensors[k].cpu().numpy().view(dt) for k, dt in
+                       (("classes", np.uint32), ("offsets", np.uint32), ("rank_a", np.int32),
+                        ("rank_d", np.uint16), ("off_a", np.int32), ("off_d", np.uint16),
+                        ("offbase", np.int32), ("zeros", np.int32))])
+    return O.FmArrays(w, fm.tensors["C"].cpu().numpy(), to_u32(fm.tensors["mwords"]), fm.tensors["msb"].cpu().numpy(),
+                      fm.tensors["sval"].cpu().numpy(), fm.sigma, fm.n, fm.sa_sample)
+
+
+@pytest.mark.parametrize("n", [200_000, 2_000_000])
+def test_staged_kernels_vs_oracle(dev, n):
+    """Batches of >= 256 x 1024 items take the persistent kernels that stage the wavelet's tables in LDS: all of them
+    for the 200K-token index, the anchors and the unrank table only for the 2M-token one (its per-superblock deltas
+    exceed the LDS budget). Count, ranges and locate against the oracle, bit for bit."""
+    import torch
+    from chromofold_amd import synth
+    from chromofold_amd.search import build_fm
+    vocab = 32000
+    tok = synth.zipf_tokens(n, vocab, 1.1, 40 + n % 7)
+    fm, _ = build_fm(torch.from_numpy(tok.view(np.int32)).to(dev), 32)
+    w = fm.w
+    deltas = 2 * 2 * w.bits * (w.nsb + 1)
+    assert (deltas < 90_000) == (n < 1_000_000)  # which staged variant each case exercises
+    flat, pstart, plen = synth.fm_patterns(tok, 270_000, 30_000, vocab, 41, 4, 12)
+    dpat, dps, dpl = (_i32(a, dev) for a in (flat, pstart, plen))
+    cnt = fm.count(dpat, dps, dpl).cpu().numpy().view(np.uint32)
+    lo, hi = (x.cpu().numpy() for x in fm.ranges(dpat, dps, dpl))
+    f = _fm_oracle_view(fm)
+    assert np.array_equal(cnt, O.fm_count(f, flat, pstart, plen))
+    rlo, rhi = O.fm_ranges(f, flat, pstart, plen)
+    assert np.array_equal(lo, rlo) and np.array_equal(hi, rhi)
+    rows = np.concatenate([np.arange(a, b, dtype=np.int32) for a, b in zip(lo, hi) if b > a])[:270_000]
+    assert rows.size >= 256 * 1024
+    pos = torch.empty(rows.size, dtype=torch.int32, device=dev)
+    fm.locate(_i32(rows, dev), pos)
+    assert np.array_equal(pos.cpu().numpy(), O.fm_locate(f, rows))
