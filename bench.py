@@ -552,14 +552,15 @@ def bench_c5(steps: int, warmup: int) -> dict:
     tables = np.concatenate([t for h in range(H) for t in (kv.build_table(K0[h].reshape(-1, 16, D)),
                                                            kv.build_table(V0[h].reshape(-1, 16, D)))])
 
-    def run(kvb, S, T, qp):
+    def run(kvb, S, T, qp, shared_groups=0):
         q = torch.from_numpy(rng.standard_normal((S, QH, D), dtype=np.float32)).to("cuda:0")
         dqp = torch.from_numpy(qp.view(np.int32)).to("cuda:0")
         out = torch.empty_like(q)
-        desc = kvb.desc(q, out, dqp, sc)
-        kvb.attention(q, out, dqp, sc, desc=desc)
+        desc = kvb.desc(q, out, dqp, sc, shared_groups=shared_groups)
+        kvb.attention(q, out, dqp, sc, desc=desc, shared_groups=shared_groups)
         torch.cuda.synchronize()
-        _, per = _events_time(lambda: kvb.attention(q, out, dqp, sc, desc=desc), steps, warmup)
+        _, per = _events_time(lambda: kvb.attention(q, out, dqp, sc, desc=desc, shared_groups=shared_groups), steps,
+                              warmup)
         return q.cpu().numpy(), out.cpu().numpy(), float(np.mean(per)) * 1e-3
 
     # (a) shared prefix
@@ -584,13 +585,21 @@ def bench_c5(steps: int, warmup: int) -> dict:
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from kv_helpers import decoded_pages, normwise_err
     logical = 2.0 * S * H * T * D * 2  # bf16 bytes of every sequence's full KV
-    # the prefix rANS-coded like the rest, then (the serving policy for a prefix every sequence reads each step)
-    # stored as INT8 groups inside the same pool: no per-sequence entropy decode of the shared pages
-    for name, raw in (("shared_prefix_rans", None), ("shared_prefix", {0: P // 64})):
-        kvb = kv.build_batched(kv.CODEC_RANS_HYBRID, src_a, S, H, np.full(S, T, np.uint32), D, tables, "cuda:0",
-                               keep_host=True, shared={s: (0, P // 64) for s in range(1, S)}, raw_groups=raw)
+    # The prefix rANS-coded like the rest and decoded by every sequence; then (the serving policy for a prefix every
+    # sequence reads each step) stored as INT8 groups inside the same pool, decoded per sequence by the batched
+    # kernel and, the headline of this config, by the cascade entry point that streams it once per KV head for all
+    # 256 query sets.
+    runs = (("shared_prefix_rans", None, 0), ("shared_prefix_batched", {0: P // 64}, 0),
+            ("shared_prefix", {0: P // 64}, P // 64))
+    kvb, built_raw = None, None
+    for name, raw, cascade in runs:
+        if kvb is None or built_raw != raw:
+            kvb = None
+            kvb = kv.build_batched(kv.CODEC_RANS_HYBRID, src_a, S, H, np.full(S, T, np.uint32), D, tables, "cuda:0",
+                                   keep_host=True, shared={s: (0, P // 64) for s in range(1, S)}, raw_groups=raw)
+            built_raw = raw
         qp = np.full(S, T - 1, np.uint32)
-        q, out, t = run(kvb, S, T, qp)
+        q, out, t = run(kvb, S, T, qp, cascade)
         s_chk = 7
         pages = []
         for h in range(H):
@@ -599,11 +608,13 @@ def bench_c5(steps: int, warmup: int) -> dict:
         err_a = normwise_err(out[s_chk], ref)
         assert err_a <= 1e-3, err_a
         res[name] = {"workload": "256 seqs x (8192 shared + 512 unique) tokens",
-                     "prefix_codec": "int8" if raw else "rans_hybrid", "tokens_per_s": S / t,
-                     "ms_per_step": t * 1e3, "unique_pool_bytes": kvb.pool_bytes,
+                     "prefix_codec": "int8" if raw else "rans_hybrid",
+                     "entry": "cf_kv_paged_attention_cascade_async" if cascade else
+                              "cf_kv_paged_attention_batched_async",
+                     "tokens_per_s": S / t, "ms_per_step": t * 1e3, "unique_pool_bytes": kvb.pool_bytes,
                      "ratio_vs_bf16_logical": logical / kvb.pool_bytes,
                      "unique_gbs": kvb.pool_bytes / t / 1e9, "max_normwise_err": err_a}
-        del kvb
+    del kvb
 
     # (b) 4 x 131072
     S, T = 4, 131072

@@ -290,9 +290,16 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
 #define CF_KV_OCC
 #endif
 
+// Partial-state slots of one (sequence, KV head) in the split workspace: this launch's splits write slots
+// [slot0, slot0 + splits) of `slots`; with slots == 1 the kernel writes the output directly. The launch covers the
+// sequence's groups from g0 on (a cascade launch leaves the shared prefix groups [0, g0) to the prefix kernel).
+struct SplitSlots {
+  uint32_t g0, slot0, slots;
+};
+
 template <int D, int CODEC>
 __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_batched_desc d, uint32_t splits,
-                                                                         float *__restrict__ partial) {
+                                                                         float *__restrict__ partial, SplitSlots ss) {
   constexpr int NQ = D / 4;
   constexpr int LOWS = 3 * (D / 16) * 64;  // u32 words of one stream's low parts
   constexpr bool RANS = CODEC == CF_KV_CODEC_RANS_HYBRID;
@@ -359,8 +366,9 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
   const uint32_t qpos = d.query_pos[seq];
   const uint32_t visible = min(ntok_seq, qpos + 1);  // tokens [0, visible) are attended
   const uint32_t ngroups = min((visible + 63) / 64, d.max_groups);
-  const uint32_t per = (ngroups + splits - 1) / splits;
-  const uint32_t ga = min(ngroups, split * per), gb = min(ngroups, ga + per);
+  const uint32_t g0 = min(ss.g0, ngroups);
+  const uint32_t per = (ngroups - g0 + splits - 1) / splits;
+  const uint32_t ga = min(ngroups, g0 + split * per), gb = min(ngroups, ga + per);
   const uint32_t *grow = d.group_offsets + (static_cast<size_t>(seq) * d.kv_head_count + head) * d.max_groups;
 
   float m_run[kGqa], l_run[kGqa], corr[kGqa];
@@ -512,16 +520,208 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
         l += rw[h * (D + 2) + D + 1] * sc;
         o += rw[h * (D + 2) + dd] * sc;
       }
-    if (splits == 1) {
+    if (ss.slots == 1) {
       if (static_cast<uint32_t>(h) < gqa)
         d.output[(static_cast<size_t>(seq) * d.query_head_count + head * gqa + h) * D + dd] = l > 0.0f ? o / l : 0.0f;
     } else {
-      float *pp = partial + ((static_cast<size_t>(seq) * d.kv_head_count + head) * splits + split) * (kGqa * (D + 2));
+      float *pp = partial + ((static_cast<size_t>(seq) * d.kv_head_count + head) * ss.slots + ss.slot0 + split) *
+                                (kGqa * (D + 2));
       pp[h * (D + 2) + dd] = o;
       if (dd == 0) {
         pp[h * (D + 2) + D] = m;
         pp[h * (D + 2) + D + 1] = l;
       }
+    }
+  }
+}
+
+// ---- shared-prefix pass of the cascade entry point (head_dim 128, INT8 prefix groups)
+// Every sequence's first `shared` groups are the same blobs (sequence 0's table gives them). One wave takes 16 query
+// rows = 4 sequences x 4 query heads of one KV head and streams the prefix groups of its split once for all of
+// them, on v_mfma_f32_16x16x32_f16:
+//   scores   S^T = K Q^T per 16-token page: A = K[token][8 dims] (two raw u32 quads, converted exactly to f16 as
+//            (1024 + sym) - 1152), B = Q^T (hi and lo f16 parts held in registers), scaled by the page's K scale;
+//            the lane's accumulator registers hold S^T[tokens 4kg + r][row lane & 15];
+//   softmax  online per row (its values live in the 4 lanes sharing lane & 15);
+//   P V      those same registers ARE the A operand of the P V product when the k index of a 32-token step is
+//            ordered {4kg + r of page 2s, 4kg + r of page 2s + 1}: no transpose. B = V[those tokens][dim] is two raw
+//            u32 V quads of the INT8 layout as they are; P is pre-multiplied by each page's V scale.
+// A non-INT8 group in the prefix makes the prefix partials NaN, so every output is NaN (the prefix must be raw).
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ half8_t sym8_to_f16(uint32_t w0, uint32_t w1) {
+  const half2_t off = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+  uint32_t u[4] = {__builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u), __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u),
+                   __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u), __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u)};
+  half8_t r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    half2_t h;
+    __builtin_memcpy(&h, &u[i], 4);
+    h = h + off;  // exact: (1024 + sym) - 1152 = sym - 128
+    r[2 * i] = h[0];
+    r[2 * i + 1] = h[1];
+  }
+  return r;
+}
+
+constexpr int kPfxThreads = 256;  // 4 waves x 16 rows = 16 sequences per workgroup
+
+__global__ __launch_bounds__(kPfxThreads) void kv_prefix_kernel(cf_kv_batched_desc d, uint32_t shared,
+                                                                 uint32_t psplits, float *__restrict__ partial,
+                                                                 SplitSlots ss) {
+  constexpr int D = 128, NQ = D / 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = lane & 15, kg = lane >> 4;
+  const uint32_t head = blockIdx.y, psplit = blockIdx.z;
+  const uint32_t gqa = d.query_head_count / d.kv_head_count;
+  const uint32_t rseq = blockIdx.x * 16 + wave * 4 + j / 4, rh = j % 4;  // the lane's row j
+  const bool row_ok = rseq < d.seq_count && rh < gqa;
+
+  // Q^T operand: B[dims 32ks + 8kg .. +7][row j], split into f16 hi + lo parts (fp32-grade scores)
+  half8_t qh[4], ql[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float q = row_ok ? d.queries[(static_cast<size_t>(rseq) * d.query_head_count + head * gqa + rh) * D +
+                                         32 * ks + 8 * kg + e] * d.softmax_scale
+                             : 0.0f;
+      qh[ks][e] = static_cast<_Float16>(q);
+      ql[ks][e] = static_cast<_Float16>(q - static_cast<float>(qh[ks][e]));
+    }
+  const uint32_t vis = row_ok ? min(d.seq_tokens[rseq], d.query_pos[rseq] + 1) : 0u;
+  // wave-wide: the fewest visible tokens over the valid rows (invalid rows are never written)
+  uint32_t vmin = row_ok ? vis : 0xFFFFFFFFu;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) vmin = min(vmin, static_cast<uint32_t>(__shfl_xor(static_cast<int>(vmin), o)));
+
+  const uint32_t per = (shared + psplits - 1) / psplits;
+  const uint32_t ga = min(shared, psplit * per), gb = min(shared, ga + per);
+  const uint32_t *grow = d.group_offsets + static_cast<size_t>(head) * d.max_groups;  // sequence 0's table
+
+  float m = -INFINITY, l = 0.0f;  // row j's running max / sum (same in the 4 lanes of the row)
+  bool coded = false;              // a prefix group that is not INT8 was met
+  float4_t acc[D / 16];            // O[rows 4kg + r][dims 16 dt + j]
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) acc[dt] = float4_t{0, 0, 0, 0};
+
+  // Loads run half a group ahead: the group's V words are issued before its score MFMAs, the next group's K words
+  // right after them (the K registers are free again), so every load has an MFMA phase to land in.
+  uint32_t kw[4][4][2], vw[2][D / 16][2];
+  auto load_k = [&](const uint32_t *raw) {
+#pragma unroll
+    for (int G = 0; G < 4; ++G)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        kw[G][ks][0] = raw[(8 * ks + 2 * kg) * 64 + 16 * G + j];
+        kw[G][ks][1] = raw[(8 * ks + 2 * kg + 1) * 64 + 16 * G + j];
+      }
+  };
+  auto blob_of = [&](uint32_t g) { return d.pool + static_cast<size_t>(grow[g]) * 16; };
+  if (ga < gb) load_k(reinterpret_cast<const uint32_t *>(blob_of(ga) + kHdr));
+  for (uint32_t g = ga; g < gb; ++g) {
+    const uint8_t *blob = blob_of(g);
+    const uint32_t *raw = reinterpret_cast<const uint32_t *>(blob + kHdr);
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) {
+        vw[s2][dt][0] = raw[NQ * 64 + (kg * (D / 16) + dt) * 64 + 16 * (2 * s2) + j];
+        vw[s2][dt][1] = raw[NQ * 64 + (kg * (D / 16) + dt) * 64 + 16 * (2 * s2 + 1) + j];
+      }
+    const uint32_t codec = *reinterpret_cast<const uint32_t *>(blob);
+    const uint32_t tc01 = *reinterpret_cast<const uint32_t *>(blob + 12), tc23 = *reinterpret_cast<const uint32_t *>(blob + 16);
+    const float *kscale = reinterpret_cast<const float *>(blob + 32), *vscale = reinterpret_cast<const float *>(blob + 48);
+    const bool full = tc01 == 0x00100010u && tc23 == 0x00100010u;
+    coded |= codec != CF_KV_CODEC_INT8;
+    const bool fast = full && vmin >= 64u * (g + 1);  // every row sees every token of the group
+    float4_t st[4];
+#pragma unroll
+    for (int G = 0; G < 4; ++G) {
+      float4_t acc_s = {0, 0, 0, 0};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const half8_t kf = sym8_to_f16(kw[G][ks][0], kw[G][ks][1]);
+        acc_s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[ks], acc_s, 0, 0, 0);
+        acc_s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[ks], acc_s, 0, 0, 0);
+      }
+      const float ksc = kscale[G];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) st[G][r] = acc_s[r] * ksc;
+      if (!fast) {
+        const uint32_t tcg = (G < 2 ? tc01 : tc23) >> (16 * (G & 1)) & 0xFFFFu;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t t = 4 * kg + r;
+          if (t >= tcg || 64u * g + 16u * G + t >= vis) st[G][r] = -INFINITY;
+        }
+      }
+    }
+    if (g + 1 < gb) load_k(reinterpret_cast<const uint32_t *>(blob_of(g + 1) + kHdr));
+    // online softmax of row j over the group's 64 tokens
+    float mx = -INFINITY;
+#pragma unroll
+    for (int G = 0; G < 4; ++G)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[G][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mn = fmaxf(m, mx);
+    const float alpha = m == -INFINITY ? 0.0f : __expf(m - mn);
+    m = mn;
+    float psum = 0.0f;
+#pragma unroll
+    for (int G = 0; G < 4; ++G)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = st[G][r] == -INFINITY ? 0.0f : __expf(st[G][r] - mn);
+        st[G][r] = p;
+        psum += p;
+      }
+    psum += __shfl_xor(psum, 16);
+    psum += __shfl_xor(psum, 32);
+    l = l * alpha + psum;
+    // rescale O: its rows are 4kg + r, whose alpha lives in lane 4kg + r
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float ar = __shfl(alpha, 4 * kg + r);
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) acc[dt][r] *= ar;
+    }
+    // P V over page pairs (2s, 2s + 1)
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      half8_t pa;
+      const float v0 = vscale[2 * s2], v1 = vscale[2 * s2 + 1];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pa[r] = static_cast<_Float16>(st[2 * s2][r] * v0);
+        pa[4 + r] = static_cast<_Float16>(st[2 * s2 + 1][r] * v1);
+      }
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt)
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, sym8_to_f16(vw[s2][dt][0], vw[s2][dt][1]), acc[dt], 0, 0,
+                                                         0);
+    }
+  }
+
+  // partial state of rows 4kg + r (m and l from lane 4kg + r) into slot psplit
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = 4 * kg + r;
+    // a coded prefix group makes the partial NaN, which the merge carries into the output
+    const float mr = coded ? __builtin_nanf("") : __shfl(m, row), lr = coded ? __builtin_nanf("") : __shfl(l, row);
+    const uint32_t seq = blockIdx.x * 16 + wave * 4 + row / 4, h = row % 4;
+    if (seq >= d.seq_count || h >= gqa) continue;
+    float *pp = partial + ((static_cast<size_t>(seq) * d.kv_head_count + head) * ss.slots + ss.slot0 + psplit) *
+                              (kGqa * (D + 2)) + h * (D + 2);
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) pp[16 * dt + j] = acc[dt][r];
+    if (j == 0) {
+      pp[D] = mr;
+      pp[D + 1] = lr;
     }
   }
 }
@@ -546,7 +746,29 @@ __global__ __launch_bounds__(kGqa * D) void kv_merge_kernel(cf_kv_batched_desc d
       l += q[D + 1] * sc;
       o += q[dd] * sc;
     }
-  d.output[(static_cast<size_t>(seq) * d.query_head_count + head * gqa + h) * D + dd] = l > 0.0f ? o / l : 0.0f;
+  // 0 when no token is visible; a NaN partial (see kv_prefix_kernel) stays NaN
+  d.output[(static_cast<size_t>(seq) * d.query_head_count + head * gqa + h) * D + dd] = l == 0.0f ? 0.0f : o / l;
+}
+
+// Cascade plan: prefix splits (slots [0, ps)) sized so that the prefix pass has about two workgroups per CU, then the
+// suffix splits (slots [ps, ps + ss)) over each sequence's own groups.
+struct CascadePlan {
+  uint32_t psplits, ssplits, slots;
+};
+
+uint32_t resident_workgroups();
+uint32_t choose_splits(const cf_kv_batched_desc *d);
+
+CascadePlan cascade_plan(const cf_kv_batched_desc *d, uint32_t shared) {
+  CascadePlan p{};
+  const uint32_t tiles = ((d->seq_count + 15) / 16) * d->kv_head_count;
+  const uint32_t want = std::max<uint32_t>(1, (2 * resident_workgroups() / 3 + tiles - 1) / tiles);
+  p.psplits = std::min<uint32_t>(want, shared);
+  cf_kv_batched_desc rest = *d;
+  rest.max_groups = std::max<uint32_t>(1, d->max_groups - shared);
+  p.ssplits = choose_splits(&rest);
+  p.slots = p.psplits + p.ssplits;
+  return p;
 }
 
 // Workgroups resident at once: 3 per CU (the LDS and VGPR budget of kv_batched_kernel).
@@ -609,7 +831,8 @@ extern "C" cf_status cf_kv_paged_attention_batched_async(const cf_kv_batched_des
   const hipStream_t s = cfd::as_stream(stream);
   float *ws = static_cast<float *>(d->workspace);
   const dim3 grid(splits, d->kv_head_count, d->seq_count);
-#define CF_LAUNCH(D, C) kv_batched_kernel<D, C><<<grid, kThreads, 0, s>>>(*d, splits, ws)
+  const SplitSlots ss{0, 0, splits};
+#define CF_LAUNCH(D, C) kv_batched_kernel<D, C><<<grid, kThreads, 0, s>>>(*d, splits, ws, ss)
   if (d->head_dim == 128) {
     if (d->codec == CF_KV_CODEC_RANS_HYBRID) CF_LAUNCH(128, CF_KV_CODEC_RANS_HYBRID);
     else CF_LAUNCH(128, CF_KV_CODEC_INT8);
@@ -623,5 +846,36 @@ extern "C" cf_status cf_kv_paged_attention_batched_async(const cf_kv_batched_des
     if (d->head_dim == 128) kv_merge_kernel<128><<<g2, kGqa * 128, 0, s>>>(*d, splits, ws);
     else kv_merge_kernel<64><<<g2, kGqa * 64, 0, s>>>(*d, splits, ws);
   }
+  return cfd::launch_status();
+}
+
+extern "C" uint64_t cf_kv_cascade_workspace_bytes(const cf_kv_batched_desc *d, uint32_t shared_groups) {
+  if (cf_kv_validate_batched_desc(d) != CF_OK || d->head_dim != 128 || shared_groups == 0 ||
+      shared_groups > d->max_groups)
+    return 0;
+  const CascadePlan p = cascade_plan(d, shared_groups);
+  return static_cast<uint64_t>(d->seq_count) * d->kv_head_count * p.slots * kGqa * (d->head_dim + 2) * sizeof(float);
+}
+
+extern "C" cf_status cf_kv_paged_attention_cascade_async(const cf_kv_batched_desc *d, uint32_t shared_groups,
+                                                          void *stream) {
+  const cf_status v = cf_kv_validate_batched_desc(d);
+  if (v != CF_OK) return v;
+  if (d->head_dim != 128) return CF_ERR_UNSUPPORTED;
+  if (shared_groups == 0 || shared_groups > d->max_groups) return CF_ERR_INVALID_ARGUMENT;
+  const CascadePlan p = cascade_plan(d, shared_groups);
+  const uint64_t need = cf_kv_cascade_workspace_bytes(d, shared_groups);
+  if (!d->workspace || d->workspace_bytes < need) return CF_ERR_INVALID_ARGUMENT;
+  const hipStream_t s = cfd::as_stream(stream);
+  float *ws = static_cast<float *>(d->workspace);
+  kv_prefix_kernel<<<dim3((d->seq_count + 15) / 16, d->kv_head_count, p.psplits), kPfxThreads, 0, s>>>(
+      *d, shared_groups, p.psplits, ws, SplitSlots{0, 0, p.slots});
+  const SplitSlots rest{shared_groups, p.psplits, p.slots};
+  const dim3 grid(p.ssplits, d->kv_head_count, d->seq_count);
+  if (d->codec == CF_KV_CODEC_RANS_HYBRID)
+    kv_batched_kernel<128, CF_KV_CODEC_RANS_HYBRID><<<grid, kThreads, 0, s>>>(*d, p.ssplits, ws, rest);
+  else
+    kv_batched_kernel<128, CF_KV_CODEC_INT8><<<grid, kThreads, 0, s>>>(*d, p.ssplits, ws, rest);
+  kv_merge_kernel<128><<<dim3(d->kv_head_count, d->seq_count), kGqa * 128, 0, s>>>(*d, p.slots, ws);
   return cfd::launch_status();
 }

@@ -44,6 +44,8 @@ A.declare("cf_kv_group_blob_max_bytes", A.U64, [A.U32, A.U32])
 A.declare("cf_kv_batched_workspace_bytes", A.U64, [A.P])
 A.declare("cf_kv_validate_batched_desc", A.I32, [A.P])
 A.declare("cf_kv_paged_attention_batched_async", A.I32, [A.P, A.P])
+A.declare("cf_kv_cascade_workspace_bytes", A.U64, [A.P, A.U32])
+A.declare("cf_kv_paged_attention_cascade_async", A.I32, [A.P, A.U32, A.P])
 A.declare("cf_kv_encode_groups_workspace_bytes", A.U64, [A.U32, A.U32, A.U64, A.U32])
 A.declare("cf_kv_encode_groups_async", A.I32, [A.U32, A.P, A.P, A.U64, A.P, A.P, A.P, A.U32, A.P, A.U32, A.P, A.P,
                                                A.U64, A.U64, A.P, A.P, A.P, A.P, A.U64, A.P])
@@ -151,7 +153,9 @@ class BatchedKv:
         return int(self.pool.numel())
 
     def desc(self, queries: torch.Tensor, output: torch.Tensor, query_pos: torch.Tensor, softmax_scale: float,
-             splits: int = 0) -> cf_kv_batched_desc:
+             splits: int = 0, shared_groups: int = 0) -> cf_kv_batched_desc:
+        """Descriptor (with a workspace of this object's) for attention(); shared_groups > 0 sizes the workspace
+        for the cascade entry point."""
         d = cf_kv_batched_desc()
         d.struct_size = C.sizeof(cf_kv_batched_desc)
         d.abi_version = EXT_ABI_VERSION
@@ -170,7 +174,12 @@ class BatchedKv:
         d.output = output.data_ptr()
         d.softmax_scale = softmax_scale
         d.splits = splits
-        need = int(A.lib().cf_kv_batched_workspace_bytes(C.byref(d)))
+        if shared_groups:
+            need = int(A.lib().cf_kv_cascade_workspace_bytes(C.byref(d), shared_groups))
+            if need == 0:
+                raise ValueError("cascade decode needs head_dim 128 and 1 <= shared_groups <= max_groups")
+        else:
+            need = int(A.lib().cf_kv_batched_workspace_bytes(C.byref(d)))
         if need:
             if self.workspace is None or self.workspace.numel() < need:
                 self.workspace = torch.empty(need, dtype=torch.uint8, device=self.pool.device)
@@ -179,10 +188,17 @@ class BatchedKv:
         return d
 
     def attention(self, queries: torch.Tensor, output: torch.Tensor, query_pos: torch.Tensor,
-                  softmax_scale: float, splits: int = 0, stream=None, desc: cf_kv_batched_desc | None = None):
-        d = desc if desc is not None else self.desc(queries, output, query_pos, softmax_scale, splits)
+                  softmax_scale: float, splits: int = 0, stream=None, desc: cf_kv_batched_desc | None = None,
+                  shared_groups: int = 0):
+        """Batched decode; shared_groups > 0 uses the cascade entry point (the first shared_groups groups of every
+        sequence are sequence 0's, stored as INT8 blobs), with a descriptor made by desc(..., shared_groups=)."""
+        d = desc if desc is not None else self.desc(queries, output, query_pos, softmax_scale, splits, shared_groups)
         s = (stream if stream is not None else torch.cuda.current_stream()).cuda_stream
-        A.check(A.lib().cf_kv_paged_attention_batched_async(C.byref(d), s), "cf_kv_paged_attention_batched_async")
+        if shared_groups:
+            A.check(A.lib().cf_kv_paged_attention_cascade_async(C.byref(d), shared_groups, s),
+                    "cf_kv_paged_attention_cascade_async")
+        else:
+            A.check(A.lib().cf_kv_paged_attention_batched_async(C.byref(d), s), "cf_kv_paged_attention_batched_async")
 
 
 def seal_device(codec: int, keys: torch.Tensor, values: torch.Tensor, tables: torch.Tensor | None,

@@ -136,6 +136,18 @@ cf_status cf_kv_validate_batched_desc(const cf_kv_batched_desc *desc);
  * semantics of one (sequence, query head) equal cf_kv_paged_attention_async with one query row and no tail. */
 cf_status cf_kv_paged_attention_batched_async(const cf_kv_batched_desc *desc, void *stream);
 
+/* Cascade decode for a prefix shared by every sequence: the first `shared_groups` groups of each sequence are the
+ * same blobs (sequence 0's group_offsets rows give them; the other sequences' entries for those groups are not
+ * read). The prefix is streamed once per KV head for all sequences' queries (a dense pass on the matrix cores) and
+ * merged with each sequence's own groups, which are decoded as by cf_kv_paged_attention_batched_async (desc->codec,
+ * desc->splits apply to them). Requirements: head_dim 128; the prefix groups are INT8 blobs (a prefix group of
+ * another codec turns the outputs of every sequence into NaN); 1 <= shared_groups <= max_groups. Query positions
+ * and sequence lengths mask the prefix like any other tokens. `workspace` must hold
+ * cf_kv_cascade_workspace_bytes() bytes; nothing is allocated, nothing synchronises. No counterpart in the
+ * reference: the BASELINE C5 shape (256 sequences sharing an 8192-token prefix) is its caller. */
+uint64_t cf_kv_cascade_workspace_bytes(const cf_kv_batched_desc *desc, uint32_t shared_groups);
+cf_status cf_kv_paged_attention_cascade_async(const cf_kv_batched_desc *desc, uint32_t shared_groups, void *stream);
+
 /* ---- host-side page encoder (CPU, used when sealing pages) ---------------------------------------------- */
 
 /* Build a table blob (CF_KV_RANS_TABLE_BYTES) from a histogram of 256 joint high-part symbols. Every symbol gets

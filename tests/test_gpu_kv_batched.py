@@ -158,3 +158,71 @@ def test_batched_full_c4_32k_every_sequence_torch_reference(dev):
         worst = max(worst, err)
         assert err <= 1e-3, (s, err)
     print(f"full C4 32k: worst normwise error over 32 sequences {worst:.3e}")
+
+
+def _cascade_case(dev, gqa, seq_tokens, shared, seed, query_pos=None, raw_prefix=True, D=128, kv_heads=2):
+    import torch
+    from chromofold_amd import kv
+    data = make_seqs(seq_tokens, kv_heads, D, seed)
+    n = shared * 64
+    for s in range(1, len(seq_tokens)):  # every sequence starts with sequence 0's prefix
+        data[s][0][:, :n] = data[0][0][:, :n]
+        data[s][1][:, :n] = data[0][1][:, :n]
+    parts = []
+    for h in range(kv_heads):
+        parts += [kv.build_table(data[0][0][h][:512].reshape(-1, 16, D)), kv.build_table(data[0][1][h][:512].reshape(-1, 16, D))]
+    tables = np.concatenate(parts)
+    S = len(seq_tokens)
+    kvb = kv.build_batched(kv.CODEC_RANS_HYBRID, lambda s: data[s], S, kv_heads, np.array(seq_tokens), D, tables, dev,
+                           keep_host=True, shared={s: (0, shared) for s in range(1, S)},
+                           raw_groups={0: shared} if raw_prefix else None)
+    rng = np.random.default_rng(seed + 1)
+    q = rng.standard_normal((S, kv_heads * gqa, D)).astype(np.float32)
+    qp = np.array([t - 1 for t in seq_tokens] if query_pos is None else query_pos, np.uint32)
+    sc = 1.0 / np.sqrt(D)
+    dq = torch.from_numpy(q).to(dev)
+    dqp = torch.from_numpy(qp.view(np.int32)).to(dev)
+    out = torch.full_like(dq, float("nan"))
+    kvb.attention(dq, out, dqp, sc, shared_groups=shared)
+    return kvb, data, q, qp, sc, out.cpu().numpy()
+
+
+@pytest.mark.parametrize("gqa,seq_tokens,query_pos", [
+    (4, [512, 300, 129, 700, 200] + [260] * 14, None),         # 19 sequences: a partly filled 16-sequence tile
+    (2, [256, 200, 300, 129], [255, 150, 120, 128]),           # GQA 2; one query sees only part of the prefix
+    (1, [1024] * 3 + [640], None),                              # long prefix split over several workgroups
+])
+def test_cascade_shared_prefix_vs_oracle(dev, gqa, seq_tokens, query_pos):
+    """cf_kv_paged_attention_cascade_async: the INT8 prefix shared by every sequence is streamed once per KV head
+    for all of them, each sequence's own rANS groups by the batched kernel, the partials merged. Against the fp64
+    oracle over the oracle-decoded pages (same bar as the batched tests)."""
+    shared = 2 if min(seq_tokens) < 1024 else 10
+    kvb, data, q, qp, sc, got = _cascade_case(dev, gqa, seq_tokens, shared, seed=61 + gqa, query_pos=query_pos)
+    assert np.isfinite(got).all()
+    ref = oracle_batched(kvb, data, q, qp, sc, gqa)
+    assert normwise_err(got, ref) <= TOL
+
+
+def test_cascade_rejects_a_coded_prefix_loudly(dev):
+    # the prefix pass reads INT8 groups only: a rANS-coded prefix turns every output into NaN instead of a wrong value
+    _, _, _, _, _, got = _cascade_case(dev, 4, [256, 300, 200], 2, seed=71, raw_prefix=False)
+    assert np.isnan(got).all()
+
+
+def test_cascade_argument_checks(dev):
+    import ctypes as C
+    import torch
+    from chromofold_amd import _abi as A
+    from chromofold_amd import kv
+    kvb, *_ = _cascade_case(dev, 4, [256, 200], 2, seed=81)
+    q = torch.zeros((2, 8, 128), device=dev)
+    o = torch.zeros_like(q)
+    qp = torch.zeros(2, dtype=torch.int32, device=dev)
+    d = kvb.desc(q, o, qp, 0.1, shared_groups=2)
+    L = A.lib()
+    assert L.cf_kv_paged_attention_cascade_async(C.byref(d), 0, None) == A.CF_ERR_INVALID_ARGUMENT
+    assert L.cf_kv_paged_attention_cascade_async(C.byref(d), kvb.max_groups + 1, None) == A.CF_ERR_INVALID_ARGUMENT
+    small = kv.cf_kv_batched_desc.from_buffer_copy(d)
+    small.workspace_bytes = 16
+    assert L.cf_kv_paged_attention_cascade_async(C.byref(small), 2, None) == A.CF_ERR_INVALID_ARGUMENT
+    assert L.cf_kv_cascade_workspace_bytes(C.byref(d), 0) == 0
