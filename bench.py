@@ -363,7 +363,7 @@ def bench_seal(steps: int, warmup: int, cpu: bool = True, seqs: int = 32, tokens
     return res
 
 
-# ------------------------------------------------------------------------------------------------ gathers (§8f.4)
+# ------------------------------------------------------------------------------------- gathers (sparse consumers)
 def bench_gather(steps: int, warmup: int, dim: int = 128, nq: int = 1 << 20) -> dict:
     """Embedding-row gathers through the C1 index (1M Zipf tokens, vocab 32000, GPU-built RRR wavelet): for 1M
     random positions, out[q] = emb[token[pos[q]]] with emb [32000, 128] fp32. Fused (cf_sparse_gather_fused_async:

@@ -144,7 +144,8 @@ cf_status cf_kv_paged_attention_batched_async(const cf_kv_batched_desc *desc, vo
  * another codec turns the outputs of every sequence into NaN); 1 <= shared_groups <= max_groups. Query positions
  * and sequence lengths mask the prefix like any other tokens. `workspace` must hold
  * cf_kv_cascade_workspace_bytes() bytes; nothing is allocated, nothing synchronises. No counterpart in the
- * reference: the BASELINE C5 shape (256 sequences sharing an 8192-token prefix) is its caller. */
+ * reference: its caller is a decode step of many sequences over one long common prefix (e.g. 256 sequences
+ * sharing an 8192-token system prompt). */
 uint64_t cf_kv_cascade_workspace_bytes(const cf_kv_batched_desc *desc, uint32_t shared_groups);
 cf_status cf_kv_paged_attention_cascade_async(const cf_kv_batched_desc *desc, uint32_t shared_groups, void *stream);
 

@@ -116,7 +116,7 @@ def test_batched_rejects_bad_desc(dev):
 
 
 def test_batched_full_c4_32k_every_sequence_torch_reference(dev):
-    """BASELINE's full C4 shape — 32 sequences x 32768 tokens, 8 KV / 32 q heads, hd 128 — sealed on the device,
+    """The benchmark's full paged-KV shape — 32 sequences x 32768 tokens, 8 KV / 32 q heads, hd 128 — sealed on the device,
     then EVERY output row against an independent float64 torch reference over the dequantised values (quantised
     here with torch: per-page absmax / 127, IEEE division, round half to even). Covers every group of every
     (sequence, head) at the benchmark's real size. Bar: max abs error <= 1e-3 x max |ref| per sequence."""
