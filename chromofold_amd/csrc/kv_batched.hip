@@ -546,6 +546,7 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
 //   P V      those same registers ARE the A operand of the P V product when the k index of a 32-token step is
 //            ordered {4kg + r of page 2s, 4kg + r of page 2s + 1}: no transpose. B = V[those tokens][dim] is two raw
 //            u32 V quads of the INT8 layout as they are; P is pre-multiplied by each page's V scale.
+// Operands: each group is converted once per workgroup into double-buffered LDS (see the kernel body).
 // A non-INT8 group in the prefix makes the prefix partials NaN, so every output is NaN (the prefix must be raw).
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
@@ -607,30 +608,39 @@ __global__ __launch_bounds__(kPfxThreads) void kv_prefix_kernel(cf_kv_batched_de
 #pragma unroll
   for (int dt = 0; dt < D / 16; ++dt) acc[dt] = float4_t{0, 0, 0, 0};
 
-  // Loads run half a group ahead: the group's V words are issued before its score MFMAs, the next group's K words
-  // right after them (the K registers are free again), so every load has an MFMA phase to land in.
-  uint32_t kw[4][4][2], vw[2][D / 16][2];
-  auto load_k = [&](const uint32_t *raw) {
+  // Each group is converted to f16 MFMA operands once per workgroup: wave w converts operand slots 4w .. 4w + 3 of
+  // K (slot = 4 * page + k-step) and of V (slot = 8 * page pair + dim tile) for every lane, into one of two LDS
+  // buffers; the next group's raw words are loaded while the current group is computed from the other buffer.
+  __shared__ half8_t s_op[2][2][16][64];  // [buffer][K, V][slot][lane], 64 KiB
+  uint32_t w[16];
+  auto fetch = [&](uint32_t g) {
+    const uint32_t *raw = reinterpret_cast<const uint32_t *>(d.pool + static_cast<size_t>(grow[g]) * 16 + kHdr);
 #pragma unroll
-    for (int G = 0; G < 4; ++G)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        kw[G][ks][0] = raw[(8 * ks + 2 * kg) * 64 + 16 * G + j];
-        kw[G][ks][1] = raw[(8 * ks + 2 * kg + 1) * 64 + 16 * G + j];
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int ks_slot = 4 * wave + i, G = ks_slot / 4, ks = ks_slot % 4;
+      w[2 * i] = raw[(8 * ks + 2 * kg) * 64 + 16 * G + j];
+      w[2 * i + 1] = raw[(8 * ks + 2 * kg + 1) * 64 + 16 * G + j];
+      const int v_slot = 4 * wave + i, s2 = v_slot / 8, dt = v_slot % 8;
+      w[8 + 2 * i] = raw[NQ * 64 + (kg * (D / 16) + dt) * 64 + 16 * (2 * s2) + j];
+      w[9 + 2 * i] = raw[NQ * 64 + (kg * (D / 16) + dt) * 64 + 16 * (2 * s2 + 1) + j];
+    }
   };
-  auto blob_of = [&](uint32_t g) { return d.pool + static_cast<size_t>(grow[g]) * 16; };
-  if (ga < gb) load_k(reinterpret_cast<const uint32_t *>(blob_of(ga) + kHdr));
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s_op[buf][0][4 * wave + i][lane] = sym8_to_f16(w[2 * i], w[2 * i + 1]);
+      s_op[buf][1][4 * wave + i][lane] = sym8_to_f16(w[8 + 2 * i], w[9 + 2 * i]);
+    }
+  };
+  if (ga < gb) {
+    fetch(ga);
+    store(0);
+  }
+  __syncthreads();
   for (uint32_t g = ga; g < gb; ++g) {
-    const uint8_t *blob = blob_of(g);
-    const uint32_t *raw = reinterpret_cast<const uint32_t *>(blob + kHdr);
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt) {
-        vw[s2][dt][0] = raw[NQ * 64 + (kg * (D / 16) + dt) * 64 + 16 * (2 * s2) + j];
-        vw[s2][dt][1] = raw[NQ * 64 + (kg * (D / 16) + dt) * 64 + 16 * (2 * s2 + 1) + j];
-      }
+    const int buf = (g - ga) & 1;
+    if (g + 1 < gb) fetch(g + 1);
+    const uint8_t *blob = d.pool + static_cast<size_t>(grow[g]) * 16;
     const uint32_t codec = *reinterpret_cast<const uint32_t *>(blob);
     const uint32_t tc01 = *reinterpret_cast<const uint32_t *>(blob + 12), tc23 = *reinterpret_cast<const uint32_t *>(blob + 16);
     const float *kscale = reinterpret_cast<const float *>(blob + 32), *vscale = reinterpret_cast<const float *>(blob + 48);
@@ -643,7 +653,7 @@ __global__ __launch_bounds__(kPfxThreads) void kv_prefix_kernel(cf_kv_batched_de
       float4_t acc_s = {0, 0, 0, 0};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const half8_t kf = sym8_to_f16(kw[G][ks][0], kw[G][ks][1]);
+        const half8_t kf = s_op[buf][0][4 * G + ks][lane];
         acc_s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[ks], acc_s, 0, 0, 0);
         acc_s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[ks], acc_s, 0, 0, 0);
       }
@@ -659,7 +669,6 @@ __global__ __launch_bounds__(kPfxThreads) void kv_prefix_kernel(cf_kv_batched_de
         }
       }
     }
-    if (g + 1 < gb) load_k(reinterpret_cast<const uint32_t *>(blob_of(g + 1) + kHdr));
     // online softmax of row j over the group's 64 tokens
     float mx = -INFINITY;
 #pragma unroll
@@ -702,9 +711,10 @@ __global__ __launch_bounds__(kPfxThreads) void kv_prefix_kernel(cf_kv_batched_de
       }
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt)
-        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, sym8_to_f16(vw[s2][dt][0], vw[s2][dt][1]), acc[dt], 0, 0,
-                                                         0);
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, s_op[buf][1][8 * s2 + dt][lane], acc[dt], 0, 0, 0);
     }
+    if (g + 1 < gb) store(buf ^ 1);  // the other buffer: every wave finished with it before the last barrier
+    __syncthreads();
   }
 
   // partial state of rows 4kg + r (m and l from lane 4kg + r) into slot psplit
