@@ -226,3 +226,18 @@ def test_cascade_argument_checks(dev):
     small.workspace_bytes = 16
     assert L.cf_kv_paged_attention_cascade_async(C.byref(small), 2, None) == A.CF_ERR_INVALID_ARGUMENT
     assert L.cf_kv_cascade_workspace_bytes(C.byref(d), 0) == 0
+
+
+@pytest.mark.parametrize("seed", [5, 6])
+def test_cascade_random_suffixes(dev, seed):
+    """Random sequence count (17..40), random own lengths after a 3-group shared prefix, random query positions
+    (some inside the prefix, some at the end), GQA 4."""
+    rng = np.random.default_rng(seed)
+    S = int(rng.integers(17, 41))
+    shared = 3
+    tokens = [192 + int(rng.integers(0, 700)) for _ in range(S)]
+    qpos = [int(rng.integers(100, t)) if rng.random() < 0.3 else t - 1 for t in tokens]
+    kvb, data, q, qp, sc, got = _cascade_case(dev, 4, tokens, shared, seed=90 + seed, query_pos=qpos)
+    assert np.isfinite(got).all()
+    ref = oracle_batched(kvb, data, q, qp, sc, 4)
+    assert normwise_err(got, ref) <= TOL

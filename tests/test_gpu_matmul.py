@@ -150,3 +150,15 @@ def test_qw_matmul_graph_replays(dev):
         want = mat.matmul(xr)
         torch.cuda.synchronize()
         assert torch.equal(got, want), r
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_qw_matmul_random_shapes(dev, seed):
+    """Random M (not a band multiple), K (ragged last segment, sometimes over one 4096-column chunk) and batch
+    (1 .. 140: up to three launches), weights with a per-row spread of magnitudes."""
+    rng = np.random.default_rng(1000 + seed)
+    M = int(rng.integers(1, 80))
+    K = int(rng.integers(1, 9000))
+    B = int(rng.integers(1, 141))
+    W = (rng.standard_normal((M, K)) * np.exp(rng.uniform(-3, 3, (M, 1)))).astype(np.float32)
+    _qw_check(dev, W, (B,))
