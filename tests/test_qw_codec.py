@@ -66,3 +66,33 @@ def test_skewed_band_is_length_limited():
     for s in range(h.seg_offsets.shape[1]):
         n = min(64, sym.shape[1] - 64 * s)
         assert np.array_equal(O.huffman_decode(h.words, lut, 12, int(h.seg_offsets[0, s]), n), sym[0, 64 * s:64 * s + n])
+
+
+def test_validate_rules_host_only():
+    """cf_qw_validate checks the descriptor on the host (no device access, so it runs without a GPU): version and
+    size, codec, shape, NULL arrays, zero point, and a 16-byte aligned code-length table (the kernel reads a band's
+    16 lengths with one 16-byte load)."""
+    import ctypes as C
+    from chromofold_amd import _abi as A
+    from chromofold_amd import qw
+    L = A.lib()
+    base = 1 << 20  # fake aligned device addresses: never dereferenced
+
+    def desc(**kw):
+        f = dict(struct_size=C.sizeof(qw.cf_qw_matrix), abi_version=qw.QW_ABI_VERSION, codec=qw.QW_CODEC_HUFFMAN,
+                 rows=64, cols=4096, zero=8, word_count=100, words=base, seg_offsets=base, code_lengths=base,
+                 scales=base)
+        f.update(kw)
+        return qw.cf_qw_matrix(**f)
+
+    ok = A.CF_OK
+    bad = A.CF_ERR_INVALID_ARGUMENT
+    assert L.cf_qw_validate(C.byref(desc())) == ok
+    assert L.cf_qw_validate(C.byref(desc(code_lengths=base + 8))) == bad
+    assert L.cf_qw_validate(C.byref(desc(code_lengths=base + 16))) == ok
+    assert L.cf_qw_validate(C.byref(desc(abi_version=99))) == bad
+    assert L.cf_qw_validate(C.byref(desc(codec=5))) == A.CF_ERR_UNSUPPORTED
+    assert L.cf_qw_validate(C.byref(desc(rows=0))) == bad
+    assert L.cf_qw_validate(C.byref(desc(scales=None))) == bad
+    assert L.cf_qw_validate(C.byref(desc(zero=16))) == bad
+    assert L.cf_qw_validate(C.byref(desc(word_count=0))) == bad
