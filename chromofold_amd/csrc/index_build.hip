@@ -68,10 +68,10 @@ struct WsLayout {
 WsLayout ws_layout(const Geo &g) {
   WsLayout L{};
   size_t scan_bytes = 0, scan2 = 0;
-  hipcub::DeviceScan::ExclusiveSum(nullptr, scan_bytes, static_cast<uint32_t *>(nullptr),
-                                   static_cast<uint32_t *>(nullptr), static_cast<int>(g.nblocks + 1));
-  hipcub::DeviceScan::ExclusiveSum(nullptr, scan2, static_cast<uint32_t *>(nullptr), static_cast<uint32_t *>(nullptr),
-                                   static_cast<int>(g.n));
+  // temp-storage size queries: a failure leaves the size 0 and the checked scan that uses it fails
+  uint32_t *const none = nullptr;
+  static_cast<void>(hipcub::DeviceScan::ExclusiveSum(nullptr, scan_bytes, none, none, static_cast<int>(g.nblocks + 1)));
+  static_cast<void>(hipcub::DeviceScan::ExclusiveSum(nullptr, scan2, none, none, static_cast<int>(g.n)));
   scan_bytes = std::max(scan_bytes, scan2);
   size_t at = 0;
   auto take = [&](size_t bytes) {
@@ -293,7 +293,7 @@ extern "C" cf_status cf_rrrw_build(const uint32_t *tokens, uint64_t n, uint32_t 
     fill_u32<<<1, 1, 0, st>>>(width + g.nblocks, 1, 0u);
     fill_u32<<<1, 1, 0, st>>>(ones + g.nblocks, 1, 0u);
     size_t tb = 0;
-    hipcub::DeviceScan::ExclusiveSum(nullptr, tb, width, obit, static_cast<int>(g.nblocks + 1), st);
+    static_cast<void>(hipcub::DeviceScan::ExclusiveSum(nullptr, tb, width, obit, static_cast<int>(g.nblocks + 1), st));
     if (hipcub::DeviceScan::ExclusiveSum(at<uint8_t>(ws, L.scan_tmp), tb, width, obit,
                                          static_cast<int>(g.nblocks + 1), st) != hipSuccess ||
         hipcub::DeviceScan::ExclusiveSum(at<uint8_t>(ws, L.scan_tmp), tb, ones, ccum,
@@ -309,7 +309,7 @@ extern "C" cf_status cf_rrrw_build(const uint32_t *tokens, uint64_t n, uint32_t 
     level_totals<<<1, 1, 0, st>>>(ccum, obit, g.nblocks, n, static_cast<int>(lvl), zeros, level_bits);
     if (lvl + 1 < bits) {
       size_t tz = 0;
-      hipcub::DeviceScan::ExclusiveSum(nullptr, tz, zflag, zpos, static_cast<int>(n), st);
+      static_cast<void>(hipcub::DeviceScan::ExclusiveSum(nullptr, tz, zflag, zpos, static_cast<int>(n), st));
       if (hipcub::DeviceScan::ExclusiveSum(at<uint8_t>(ws, L.scan_tmp), tz, zflag, zpos, static_cast<int>(n), st) !=
           hipSuccess)
         return CF_ERR_CUDA;
@@ -374,10 +374,10 @@ extern "C" uint64_t cf_fm_build_workspace_bytes(int32_t n, int32_t sigma) {
   if (n <= 0 || sigma <= 0) return 0;
   const size_t nw = (static_cast<size_t>(n) + 31) / 32;
   size_t scan_bytes = 0, s2 = 0;
-  hipcub::DeviceScan::ExclusiveSum(nullptr, scan_bytes, static_cast<uint32_t *>(nullptr),
-                                   static_cast<uint32_t *>(nullptr), static_cast<int>(nw + 1));
-  hipcub::DeviceScan::ExclusiveSum(nullptr, s2, static_cast<uint32_t *>(nullptr), static_cast<uint32_t *>(nullptr),
-                                   sigma);
+  // temp-storage size queries: a failure leaves the size 0 and the checked scan that uses it fails
+  uint32_t *const none = nullptr;
+  static_cast<void>(hipcub::DeviceScan::ExclusiveSum(nullptr, scan_bytes, none, none, static_cast<int>(nw + 1)));
+  static_cast<void>(hipcub::DeviceScan::ExclusiveSum(nullptr, s2, none, none, sigma));
   return align256(4 * (nw + 1)) * 2 + align256(4ull * sigma) + align256(std::max(scan_bytes, s2));
 }
 
@@ -400,7 +400,7 @@ extern "C" cf_status cf_fm_build_aux(const int32_t *s, const int32_t *sa, int32_
   size_t tb = 0;
   marks_kernel<<<cfd::grid_for(nw, kThreads), kThreads, 0, st>>>(sa, n, sa_sample, mwords, wcount);
   fill_u32<<<1, 1, 0, st>>>(wcount + nw, 1, 0u);
-  hipcub::DeviceScan::ExclusiveSum(nullptr, tb, wcount, wbase, nw + 1, st);
+  static_cast<void>(hipcub::DeviceScan::ExclusiveSum(nullptr, tb, wcount, wbase, nw + 1, st));
   if (hipcub::DeviceScan::ExclusiveSum(tmp, tb, wcount, wbase, nw + 1, st) != hipSuccess) return CF_ERR_CUDA;
   msb_kernel<<<cfd::grid_for(nb + 1, kThreads), kThreads, 0, st>>>(wbase, nw, nb, msb);
   sval_kernel<<<gn, kThreads, 0, st>>>(sa, n, mwords, wbase, sval);

@@ -63,11 +63,11 @@ size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 Layout layout(int n, int key_bits) {
   Layout L{};
   size_t sort_bytes = 0, scan_bytes = 0;
-  hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, static_cast<uint64_t *>(nullptr),
+  static_cast<void>(hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, static_cast<uint64_t *>(nullptr),
                                      static_cast<uint64_t *>(nullptr), static_cast<int32_t *>(nullptr),
-                                     static_cast<int32_t *>(nullptr), n, 0, key_bits);
-  hipcub::DeviceScan::InclusiveSum(nullptr, scan_bytes, static_cast<int32_t *>(nullptr),
-                                   static_cast<int32_t *>(nullptr), n);
+                                     static_cast<int32_t *>(nullptr), n, 0, key_bits));
+  static_cast<void>(hipcub::DeviceScan::InclusiveSum(nullptr, scan_bytes, static_cast<int32_t *>(nullptr),
+                                   static_cast<int32_t *>(nullptr), n));
   size_t at = 0;
   auto take = [&](size_t bytes) {
     const size_t here = at;
@@ -119,14 +119,14 @@ extern "C" cf_status cf_suffix_array(const int32_t *s, int32_t n, int32_t max_sy
   for (int64_t k = 1;; k <<= 1) {
     sa_keys<<<blocks, kThreads, 0, st>>>(sa, rank, n, static_cast<int>(std::min<int64_t>(k, n)), sh, key);
     size_t sort_bytes = 0;
-    hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, key, key2, sa, sa2, n, 0, kb, st);
+    static_cast<void>(hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, key, key2, sa, sa2, n, 0, kb, st));
     if (hipcub::DeviceRadixSort::SortPairs(ws + L.sort_tmp, sort_bytes, key, key2, sa, sa2, n, 0, kb, st) !=
         hipSuccess)
       return CF_ERR_CUDA;
     std::swap(sa, sa2);
     sa_flags<<<blocks, kThreads, 0, st>>>(key2, n, pos);
     size_t scan_bytes = 0;
-    hipcub::DeviceScan::InclusiveSum(nullptr, scan_bytes, pos, pos, n, st);
+    static_cast<void>(hipcub::DeviceScan::InclusiveSum(nullptr, scan_bytes, pos, pos, n, st));
     if (hipcub::DeviceScan::InclusiveSum(ws + L.scan_tmp, scan_bytes, pos, pos, n, st) != hipSuccess)
       return CF_ERR_CUDA;
     sa_scatter<<<blocks, kThreads, 0, st>>>(sa, pos, n, rank);
@@ -152,8 +152,8 @@ void cf_gpu_suffix_array(const std::vector<int> &s, std::vector<int> &out) {
   void *d_s = nullptr, *d_sa = nullptr, *d_ws = nullptr;
   if (hipMalloc(&d_s, 4ull * n) != hipSuccess || hipMalloc(&d_sa, 4ull * n) != hipSuccess ||
       hipMalloc(&d_ws, wsb) != hipSuccess) {
-    hipFree(d_s);
-    hipFree(d_sa);
+    static_cast<void>(hipFree(d_s));
+    static_cast<void>(hipFree(d_sa));
     out.clear();
     return;
   }
@@ -164,7 +164,7 @@ void cf_gpu_suffix_array(const std::vector<int> &s, std::vector<int> &out) {
   } else {
     out.clear();
   }
-  hipFree(d_s);
-  hipFree(d_sa);
-  hipFree(d_ws);
+  static_cast<void>(hipFree(d_s));
+  static_cast<void>(hipFree(d_sa));
+  static_cast<void>(hipFree(d_ws));
 }
