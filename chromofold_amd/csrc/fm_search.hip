@@ -89,19 +89,81 @@ __global__ __launch_bounds__(kThreads) void fm_locate_kernel(cf_fm_view v, const
 // its class starts (and, for small indexes, the per-superblock deltas) in LDS, then strides over the items.
 constexpr unsigned kStagedThreads = 1024;
 
+// Work distribution of the staged kernels: workgroup b owns items [b * per, (b + 1) * per) and its lanes take the
+// next item from an LDS counter as soon as they finish one (pattern lengths and LF-walk lengths vary widely, so a
+// static assignment would leave most lanes of a wave waiting for its longest item). Each item is computed exactly
+// as by the kernels above.
+struct ItemQueue {
+  size_t begin, end;
+  uint32_t *next;  // LDS
+  __device__ size_t take() const { return begin + atomicAdd(next, 1u); }
+};
+
+__device__ ItemQueue item_queue(size_t count, uint32_t *s_next) {
+  const size_t per = (count + gridDim.x - 1) / gridDim.x;
+  ItemQueue q{min(count, blockIdx.x * per), min(count, (blockIdx.x + 1) * per), s_next};
+  if (threadIdx.x == 0) *s_next = 0;
+  __syncthreads();
+  return q;
+}
+
+// backward search of pattern t, one symbol per call of step(); done() once its symbols are consumed
+template <int LEVELS, bool kDeltas>
+__device__ __forceinline__ void count_or_ranges(const cf_fm_view &v, const int32_t *__restrict__ pat,
+                                                const int32_t *__restrict__ pstart, const int32_t *__restrict__ plen,
+                                                size_t npat, const cfr::StagedTables<kDeltas> &tb, uint32_t *s_next,
+                                                uint32_t *__restrict__ cnt_out, int32_t *__restrict__ lo_out,
+                                                int32_t *__restrict__ hi_out) {
+  const ItemQueue q = item_queue(npat, s_next);
+  size_t t = q.take();
+  bool active = t < q.end;
+  int st = 0, k = 0, lo = 0, hi = 0;
+  if (active) {
+    st = pstart[t];
+    k = plen[t];
+    hi = v.n;
+  }
+  while (__any(active)) {
+    if (active) {
+      if (k > 0) {  // reference fm_search_device.cuh:31-48, one symbol (right to left)
+        --k;
+        const int c = pat[st + k];
+        if (c < 0 || c >= v.sigma) {
+          lo = hi = 0;
+        } else if (lo < hi) {
+          int rl, rh;
+          cfr::rank_pair<LEVELS, cfr::StagedTables<kDeltas>, true>(v.w, c, lo, hi, rl, rh, tb);
+          lo = v.C[c] + rl;
+          hi = v.C[c] + rh;
+        }
+      } else {
+        if (cnt_out) cnt_out[t] = static_cast<uint32_t>(hi - lo);
+        if (lo_out) {
+          lo_out[t] = lo;
+          hi_out[t] = hi;
+        }
+        t = q.take();
+        active = t < q.end;
+        if (active) {
+          st = pstart[t];
+          k = plen[t];
+          lo = 0;
+          hi = v.n;
+        }
+      }
+    }
+  }
+}
+
 template <int LEVELS, bool kDeltas>
 __global__ __launch_bounds__(kStagedThreads) void fm_count_staged_kernel(cf_fm_view v, const int32_t *__restrict__ pat,
                                                                          const int32_t *__restrict__ pstart,
                                                                          const int32_t *__restrict__ plen,
                                                                          uint32_t *__restrict__ out, size_t npat) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ uint32_t s_next;
   const auto tb = cfr::stage_tables<kDeltas>(v.w, smem, kStagedThreads);
-  for (size_t t = blockIdx.x * static_cast<size_t>(kStagedThreads) + threadIdx.x; t < npat;
-       t += static_cast<size_t>(gridDim.x) * kStagedThreads) {
-    int lo, hi;
-    backward<LEVELS, cfr::StagedTables<kDeltas>, true>(v, pat, pstart[t], plen[t], lo, hi, tb);
-    out[t] = static_cast<uint32_t>(hi - lo);
-  }
+  count_or_ranges<LEVELS, kDeltas>(v, pat, pstart, plen, npat, tb, &s_next, out, nullptr, nullptr);
 }
 
 template <int LEVELS, bool kDeltas>
@@ -109,14 +171,9 @@ __global__ __launch_bounds__(kStagedThreads) void fm_ranges_staged_kernel(
     cf_fm_view v, const int32_t *__restrict__ pat, const int32_t *__restrict__ pstart,
     const int32_t *__restrict__ plen, int32_t *__restrict__ lo_out, int32_t *__restrict__ hi_out, size_t npat) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ uint32_t s_next;
   const auto tb = cfr::stage_tables<kDeltas>(v.w, smem, kStagedThreads);
-  for (size_t t = blockIdx.x * static_cast<size_t>(kStagedThreads) + threadIdx.x; t < npat;
-       t += static_cast<size_t>(gridDim.x) * kStagedThreads) {
-    int lo, hi;
-    backward<LEVELS, cfr::StagedTables<kDeltas>, true>(v, pat, pstart[t], plen[t], lo, hi, tb);
-    lo_out[t] = lo;
-    hi_out[t] = hi;
-  }
+  count_or_ranges<LEVELS, kDeltas>(v, pat, pstart, plen, npat, tb, &s_next, nullptr, lo_out, hi_out);
 }
 
 template <int LEVELS, bool kDeltas>
@@ -124,10 +181,31 @@ __global__ __launch_bounds__(kStagedThreads) void fm_locate_staged_kernel(cf_fm_
                                                                           const int32_t *__restrict__ rows,
                                                                           int32_t *__restrict__ out, size_t nocc) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ uint32_t s_next;
   const auto tb = cfr::stage_tables<kDeltas>(v.w, smem, kStagedThreads);
-  for (size_t t = blockIdx.x * static_cast<size_t>(kStagedThreads) + threadIdx.x; t < nocc;
-       t += static_cast<size_t>(gridDim.x) * kStagedThreads)
-    out[t] = locate_one<LEVELS, cfr::StagedTables<kDeltas>, true>(v, rows[t], tb);
+  const ItemQueue q = item_queue(nocc, &s_next);
+  size_t t = q.take();
+  bool active = t < q.end;
+  int p = active ? rows[t] : 0, steps = 0;
+  while (__any(active)) {
+    if (active) {  // reference fm_search_device.cuh:52-62, one LF step per iteration
+      if ((v.mwords[p >> 5] >> (p & 31)) & 1u) {
+        const int idx = cfp::rank1(v.mwords, v.msb, p);
+        out[t] = static_cast<int32_t>((static_cast<int64_t>(v.sval[idx]) + steps) % v.n);
+        t = q.take();
+        active = t < q.end;
+        if (active) {
+          p = rows[t];
+          steps = 0;
+        }
+      } else {
+        int c;
+        const int r = cfr::access_rank<LEVELS, cfr::StagedTables<kDeltas>, true>(v.w, p, c, tb);
+        p = v.C[c] + r;
+        ++steps;
+      }
+    }
+  }
 }
 
 // Launches the staged variant when one applies (levels 15 and 16 get fixed-depth instances); false otherwise.
