@@ -164,3 +164,31 @@ def test_staged_kernels_vs_oracle(dev, n):
     pos = torch.empty(rows.size, dtype=torch.int32, device=dev)
     fm.locate(_i32(rows, dev), pos)
     assert np.array_equal(pos.cpu().numpy(), O.fm_locate(f, rows))
+
+
+def test_staged_kernels_many_items_per_lane(dev):
+    """The staged kernels hand items to lanes from a per-workgroup queue. Here each lane takes several items of very
+    different cost: 1.2M patterns of length 0-40 (the empty pattern matches every row) and up to 1.2M occurrences,
+    whose LF walks take 0-31 steps. Count, ranges and locate against the oracle, bit for bit."""
+    import torch
+    from chromofold_amd import synth
+    from chromofold_amd.search import build_fm
+    vocab = 32000
+    tok = synth.zipf_tokens(200_000, vocab, 1.1, 43)
+    fm, _ = build_fm(torch.from_numpy(tok.view(np.int32)).to(dev), 32)
+    flat, pstart, plen = synth.fm_patterns(tok, 1_000_000, 200_000, vocab, 44, 0, 40)
+    assert (plen == 0).any() and pstart.size >= 4 * 256 * 1024
+    dpat, dps, dpl = (_i32(a, dev) for a in (flat, pstart, plen))
+    cnt = fm.count(dpat, dps, dpl).cpu().numpy().view(np.uint32)
+    lo, hi = (x.cpu().numpy() for x in fm.ranges(dpat, dps, dpl))
+    f = _fm_oracle_view(fm)
+    assert np.array_equal(cnt, O.fm_count(f, flat, pstart, plen))
+    assert (cnt[plen == 0] == fm.n).all()
+    rlo, rhi = O.fm_ranges(f, flat, pstart, plen)
+    assert np.array_equal(lo, rlo) and np.array_equal(hi, rhi)
+    keep = (hi > lo) & (hi - lo < 64)
+    rows = np.concatenate([np.arange(a, b, dtype=np.int32) for a, b in zip(lo[keep], hi[keep])])[:1_200_000]
+    assert rows.size >= 4 * 256 * 1024
+    pos = torch.empty(rows.size, dtype=torch.int32, device=dev)
+    fm.locate(_i32(rows, dev), pos)
+    assert np.array_equal(pos.cpu().numpy(), O.fm_locate(f, rows))
