@@ -86,7 +86,7 @@ __global__ __launch_bounds__(kThreads) void fm_locate_kernel(cf_fm_view v, const
 }
 
 // ---- persistent variants: one 1024-thread workgroup per CU stages the wavelet's anchors, the unrank table and
-// its class starts (and, for small indexes, the per-superblock deltas) in LDS, then strides over the items.
+// its class starts (and, for small indexes, the per-superblock deltas) in LDS, then works through its items.
 constexpr unsigned kStagedThreads = 1024;
 
 // Work distribution of the staged kernels: workgroup b owns items [b * per, (b + 1) * per) and its lanes take the
@@ -107,7 +107,8 @@ __device__ ItemQueue item_queue(size_t count, uint32_t *s_next) {
   return q;
 }
 
-// backward search of pattern t, one symbol per call of step(); done() once its symbols are consumed
+// Backward search of the queue's patterns: each loop iteration consumes one symbol of the lane's current pattern,
+// or stores its result and takes the next pattern once all its symbols are consumed.
 template <int LEVELS, bool kDeltas>
 __device__ __forceinline__ void count_or_ranges(const cf_fm_view &v, const int32_t *__restrict__ pat,
                                                 const int32_t *__restrict__ pstart, const int32_t *__restrict__ plen,
