@@ -7,14 +7,16 @@
 //            GQA group's 4 query heads (split into f16 hi + lo parts for fp32-grade scores) as the A operand, so
 //            the lane ends up holding its token's 4 head scores. Nothing decoded is written anywhere.
 //   softmax: one running max per head for the whole wavefront (so the 4 page groups can be summed at the end),
-//            probabilities pre-scaled by the page's V scale go to a 512-byte LDS tile.
+//            probabilities times the page's V scale (in units of a power of two per lane, so that the f16 value
+//            neither underflows nor overflows) go to a 512-byte LDS tile.
 //   V phase: lane decodes dims {t + 16i} of page G, 4 tokens per quad, again straight into a 4x4x4 MFMA
-//            (A = probabilities of those 4 tokens for the 4 heads, B = the 4 decoded values) accumulating the
-//            lane's 4 heads x 8 dims output.
+//            (A = probabilities of those 4 tokens for the 4 heads, B = the 4 decoded values as exact signed f16)
+//            accumulating the lane's 4 heads x 8 dims output.
 // Codec decode per quad: one rANS step (LDS slot table, 64-bit entry = freq/offset + the four 2-bit high parts
 // already spread to their bytes; SDWA reads the 16-bit freq/offset halves in place), three bit-sliced low-part
-// words per 4 quads merged with two bit-field inserts, and two v_perm to build the f16 operand (1024 + symbol; the
-// constant 1024+128 offset is folded out with the sum of the other operand).
+// words per 4 quads merged with two bit-field inserts, and two v_perm to build the f16 operand (1024 + symbol). For
+// K the constant 1024+128 offset is folded out with the sum of the query operand; for V it is subtracted from the
+// operand (two packed f16 adds), so the P.V accumulator holds no offset term.
 // Memory: a wavefront's next group is in flight while it works on the current one (header in registers, word
 // streams copied straight into LDS by global_load_lds after the current decode loop, first low-part words in
 // registers), so a group starts without a memory round trip.
@@ -53,6 +55,16 @@ __device__ __forceinline__ half4_t bytes_to_half4(uint32_t b) {
   w[0] = lo;
   w[1] = hi;
   return h;
+}
+
+// The same bytes as exact signed values (symbol - 128) in f16: the 1024 + 128 offset removed by a packed f16
+// subtract (exact: integers in [-128, 127]). The V operand uses this form: with the offset left in, a row whose
+// heaviest tokens have V = 0 would carry 1152 x (sum of their weights) in an fp32 accumulator whose true value
+// is many orders of magnitude smaller.
+__device__ __forceinline__ half4_t bytes_to_half4_signed(uint32_t b) {
+  const half4_t off = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f),
+                       static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};
+  return bytes_to_half4(b) + off;
 }
 
 __device__ __forceinline__ float4_t mfma4(half4_t a, half4_t b, float4_t c) {
@@ -157,8 +169,8 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
                                            uint32_t cnt23,
                                            const uint2 (*__restrict__ s_tab)[kSlots], const half4_t *qhi,
                                            const half4_t *qlo, const float *qsum, _Float16 (*s_pw)[kGqa][16],
-                                           int lane, bool tok_ok, float ks, float vs, float *m_run, float *l_run,
-                                           float *corr, float4_t *acc_v) {
+                                           int lane, bool tok_ok, float ks, float vs, int &e_run, float *m_run,
+                                           float *l_run, float4_t *acc_v) {
   constexpr int NQ = D / 4, LOWS = 3 * (D / 16) * 64;
   constexpr bool RANS = CODEC == CF_KV_CODEC_RANS_HYBRID;
   const int G = lane >> 4, t = lane & 15;
@@ -252,16 +264,25 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
   for (int o = 32; o > 0; o >>= 1)
 #pragma unroll
     for (int h = 0; h < kGqa; ++h) mx[h] = fmaxf(mx[h], __shfl_xor(mx[h], o));
+  // The lane's P.V sums (acc_v) only ever hold tokens of its own page slot G, so they are kept in units of
+  // 2^e with e = (exponent of that page's V scale) - 15: the f16 operand p * vs * 2^-e lies in [0, 2^15) whatever
+  // the V magnitude (no overflow for huge V), and weights p down to 2^-29 of the running maximum stay normal f16
+  // numbers (a row whose heaviest tokens have V = 0 is carried by such small weights). Moving to the next page's
+  // units is an exact power-of-two factor folded into the softmax rescale; a drop of more than 2^60 between
+  // consecutive pages is clamped so that the rescale cannot overflow.
+  const int ev = max(__builtin_amdgcn_frexp_expf(vs) - 15, e_run - 60);
+  const int de = e_run - ev;
+  e_run = ev;
+  const float vsn = ldexpf(vs, -ev);
   float alpha[kGqa];
 #pragma unroll
   for (int h = 0; h < kGqa; ++h) {
     const float mn = fmaxf(m_run[h], mx[h]);
-    alpha[h] = (m_run[h] == -INFINITY) ? 0.0f : __expf(m_run[h] - mn);
+    const float a = (m_run[h] == -INFINITY) ? 0.0f : __expf(m_run[h] - mn);
     const float pr = tok_ok ? __expf(s[h] - mn) : 0.0f;
-    l_run[h] = l_run[h] * alpha[h] + pr;
-    const _Float16 pv = static_cast<_Float16>(pr * vs);
-    s_pw[G][h][t] = pv;
-    corr[h] = corr[h] * alpha[h] + kOffset * static_cast<float>(pv);
+    l_run[h] = l_run[h] * a + pr;
+    alpha[h] = ldexpf(a, de);  // ldexp(0, .) = 0 before the first visible token
+    s_pw[G][h][t] = static_cast<_Float16>(pr * vsn);
     m_run[h] = mn;
   }
 #pragma unroll
@@ -277,7 +298,7 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
   for (int tq = 0; tq < 4; ++tq) {
     const half4_t pa = *reinterpret_cast<const half4_t *>(&s_pw[G][lane & 3][4 * tq]);
 #pragma unroll
-    for (int i = 0; i < D / 16; ++i) acc_v[i] = mfma4(pa, bytes_to_half4(vb[tq * (D / 16) + i]), acc_v[i]);
+    for (int i = 0; i < D / 16; ++i) acc_v[i] = mfma4(pa, bytes_to_half4_signed(vb[tq * (D / 16) + i]), acc_v[i]);
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -371,13 +392,13 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
   const uint32_t ga = min(ngroups, g0 + split * per), gb = min(ngroups, ga + per);
   const uint32_t *grow = d.group_offsets + (static_cast<size_t>(seq) * d.kv_head_count + head) * d.max_groups;
 
-  float m_run[kGqa], l_run[kGqa], corr[kGqa];
+  float m_run[kGqa], l_run[kGqa];
+  int e_run = -(1 << 20);  // exponent of the lane's P.V units (set by its first group)
   float4_t acc_v[D / 16];
 #pragma unroll
   for (int h = 0; h < kGqa; ++h) {
     m_run[h] = -INFINITY;
     l_run[h] = 0.0f;
-    corr[h] = 0.0f;
   }
 #pragma unroll
   for (int i = 0; i < D / 16; ++i) acc_v[i] = float4_t{0, 0, 0, 0};
@@ -467,19 +488,20 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
     };
     if (RANS && gcodec == CF_KV_CODEC_RANS_HYBRID) {
       group_body<D, CF_KV_CODEC_RANS_HYBRID>(stage_next, pre, nlw, st4, cur, reinterpret_cast<const uint16_t *>(buf), cnt01, cnt23, s_tab, qhi,
-                                             qlo, qsum, s_p[wave], lane, tok_ok, ks, vs, m_run, l_run, corr, acc_v);
+                                             qlo, qsum, s_p[wave], lane, tok_ok, ks, vs, e_run, m_run, l_run, acc_v);
     } else {  // raw int8 group (the INT8 codec, or the raw fallback of a high-entropy group)
       group_body<D, CF_KV_CODEC_INT8>(stage_next, pre, nlw, st4, cur, static_cast<const uint16_t *>(nullptr), 0, 0, s_tab, qhi, qlo,
-                                      qsum, s_p[wave], lane, tok_ok, ks, vs, m_run, l_run, corr, acc_v);
+                                      qsum, s_p[wave], lane, tok_ok, ks, vs, e_run, m_run, l_run, acc_v);
     }
   }
 
-  // ---- reduce the wavefront: sum the 4 page groups (lanes t, t+16, t+32, t+48), l and corr over all lanes
+  // ---- reduce the wavefront: sum the 4 page groups (lanes t, t+16, t+32, t+48) after taking each lane's P.V sums
+  // back to absolute units, l over all lanes
 #pragma unroll
   for (int i = 0; i < D / 16; ++i)
 #pragma unroll
     for (int h = 0; h < kGqa; ++h) {
-      float v = acc_v[i][h];
+      float v = ldexpf(acc_v[i][h], e_run);
       v += __shfl_xor(v, 16);
       v += __shfl_xor(v, 32);
       acc_v[i][h] = v;
@@ -487,17 +509,14 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
 #pragma unroll
   for (int h = 0; h < kGqa; ++h)
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      l_run[h] += __shfl_xor(l_run[h], o);
-      corr[h] += __shfl_xor(corr[h], o);
-    }
-  // wave partial -> the wave's LDS buffer: [h][D] acc (minus offset correction), then m, l
+    for (int o = 32; o > 0; o >>= 1) l_run[h] += __shfl_xor(l_run[h], o);
+  // wave partial -> the wave's LDS buffer: [h][D] acc, then m, l
   float *red = reinterpret_cast<float *>(buf);
   if (lane < 16) {
 #pragma unroll
     for (int i = 0; i < D / 16; ++i)
 #pragma unroll
-      for (int h = 0; h < kGqa; ++h) red[h * (D + 2) + t + 16 * i] = acc_v[i][h] - corr[h];
+      for (int h = 0; h < kGqa; ++h) red[h * (D + 2) + t + 16 * i] = acc_v[i][h];
   }
   if (lane < kGqa) {
     red[lane * (D + 2) + D] = m_run[lane];
@@ -604,6 +623,7 @@ __global__ __launch_bounds__(kPfxThreads) void kv_prefix_kernel(cf_kv_batched_de
 
   float m = -INFINITY, l = 0.0f;  // row j's running max / sum (same in the 4 lanes of the row)
   bool coded = false;              // a prefix group that is not INT8 was met
+  int e_run = -(1 << 20);          // acc is kept in units of 2^e_run (e_run: V-scale exponent of the current group)
   float4_t acc[D / 16];            // O[rows 4kg + r][dims 16 dt + j]
 #pragma unroll
   for (int dt = 0; dt < D / 16; ++dt) acc[dt] = float4_t{0, 0, 0, 0};
@@ -613,8 +633,16 @@ __global__ __launch_bounds__(kPfxThreads) void kv_prefix_kernel(cf_kv_batched_de
   // buffers; the next group's raw words are loaded while the current group is computed from the other buffer.
   __shared__ half8_t s_op[2][2][16][64];  // [buffer][K, V][slot][lane], 64 KiB
   uint32_t w[16];
-  auto fetch = [&](uint32_t g) {
+  auto codec_at = [&](uint32_t g) { return *reinterpret_cast<const uint32_t *>(d.pool + static_cast<size_t>(grow[g]) * 16); };
+  // raw words of group g; a group that is not INT8 (smaller blob: reading an INT8-sized span could run past the
+  // pool) is not read, its outputs become NaN anyway
+  auto fetch = [&](uint32_t g, bool raw_group) {
     const uint32_t *raw = reinterpret_cast<const uint32_t *>(d.pool + static_cast<size_t>(grow[g]) * 16 + kHdr);
+    if (!raw_group) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) w[i] = 0;
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int ks_slot = 4 * wave + i, G = ks_slot / 4, ks = ks_slot % 4;
@@ -632,14 +660,18 @@ __global__ __launch_bounds__(kPfxThreads) void kv_prefix_kernel(cf_kv_batched_de
       s_op[buf][1][4 * wave + i][lane] = sym8_to_f16(w[8 + 2 * i], w[9 + 2 * i]);
     }
   };
+  // the codec of group g + 1 is loaded one group ahead of its fetch, so the fetch does not wait for it
+  uint32_t codec_next = ga + 1 < gb ? codec_at(ga + 1) : 0u;
   if (ga < gb) {
-    fetch(ga);
+    fetch(ga, codec_at(ga) == CF_KV_CODEC_INT8);
     store(0);
   }
   __syncthreads();
   for (uint32_t g = ga; g < gb; ++g) {
     const int buf = (g - ga) & 1;
-    if (g + 1 < gb) fetch(g + 1);
+    const uint32_t codec1 = codec_next;
+    if (g + 2 < gb) codec_next = codec_at(g + 2);
+    if (g + 1 < gb) fetch(g + 1, codec1 == CF_KV_CODEC_INT8);
     const uint8_t *blob = d.pool + static_cast<size_t>(grow[g]) * 16;
     const uint32_t codec = *reinterpret_cast<const uint32_t *>(blob);
     const uint32_t tc01 = *reinterpret_cast<const uint32_t *>(blob + 12), tc23 = *reinterpret_cast<const uint32_t *>(blob + 16);
@@ -692,10 +724,21 @@ __global__ __launch_bounds__(kPfxThreads) void kv_prefix_kernel(cf_kv_batched_de
     psum += __shfl_xor(psum, 16);
     psum += __shfl_xor(psum, 32);
     l = l * alpha + psum;
+    // P V units: O is kept in units of 2^e with e = (exponent of the group's largest present-page V scale) - 15,
+    // so the f16 operand p * v_scale * 2^-e stays below 2^15 whatever the V magnitude and weights down to 2^-29
+    // of the running maximum stay normal; moving to the group's units is an exact power-of-two factor folded into
+    // the softmax rescale (a drop of more than 2^60 is clamped)
+    float vmax = 0.0f;
+#pragma unroll
+    for (int G = 0; G < 4; ++G)
+      if (((G < 2 ? tc01 : tc23) >> (16 * (G & 1)) & 0xFFFFu) != 0u) vmax = fmaxf(vmax, vscale[G]);
+    const int ev = max(__builtin_amdgcn_frexp_expf(vmax) - 15, e_run - 60);
+    const int de = e_run - ev;
+    e_run = ev;
     // rescale O: its rows are 4kg + r, whose alpha lives in lane 4kg + r
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float ar = __shfl(alpha, 4 * kg + r);
+      const float ar = ldexpf(__shfl(alpha, 4 * kg + r), de);
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt) acc[dt][r] *= ar;
     }
@@ -703,7 +746,7 @@ __global__ __launch_bounds__(kPfxThreads) void kv_prefix_kernel(cf_kv_batched_de
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
       half8_t pa;
-      const float v0 = vscale[2 * s2], v1 = vscale[2 * s2 + 1];
+      const float v0 = ldexpf(vscale[2 * s2], -ev), v1 = ldexpf(vscale[2 * s2 + 1], -ev);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         pa[r] = static_cast<_Float16>(st[2 * s2][r] * v0);
@@ -728,7 +771,7 @@ __global__ __launch_bounds__(kPfxThreads) void kv_prefix_kernel(cf_kv_batched_de
     float *pp = partial + ((static_cast<size_t>(seq) * d.kv_head_count + head) * ss.slots + ss.slot0 + psplit) *
                               (kGqa * (D + 2)) + h * (D + 2);
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) pp[16 * dt + j] = acc[dt][r];
+    for (int dt = 0; dt < D / 16; ++dt) pp[16 * dt + j] = ldexpf(acc[dt][r], e_run);
     if (j == 0) {
       pp[D] = mr;
       pp[D + 1] = lr;
@@ -746,7 +789,12 @@ __global__ __launch_bounds__(kGqa * D) void kv_merge_kernel(cf_kv_batched_desc d
   if (static_cast<uint32_t>(h) >= gqa) return;
   const float *pp = partial + (static_cast<size_t>(seq) * d.kv_head_count + head) * splits * (kGqa * (D + 2));
   float m = -INFINITY;
-  for (uint32_t s = 0; s < splits; ++s) m = fmaxf(m, pp[s * (kGqa * (D + 2)) + h * (D + 2) + D]);
+  bool nan = false;  // a NaN partial (a coded prefix group, see kv_prefix_kernel) makes the row NaN
+  for (uint32_t s = 0; s < splits; ++s) {
+    const float ms = pp[s * (kGqa * (D + 2)) + h * (D + 2) + D];
+    nan |= ms != ms;
+    m = fmaxf(m, ms);  // fmaxf drops a NaN, hence the flag
+  }
   float l = 0.0f, o = 0.0f;
   if (m != -INFINITY)
     for (uint32_t s = 0; s < splits; ++s) {
@@ -756,8 +804,9 @@ __global__ __launch_bounds__(kGqa * D) void kv_merge_kernel(cf_kv_batched_desc d
       l += q[D + 1] * sc;
       o += q[dd] * sc;
     }
-  // 0 when no token is visible; a NaN partial (see kv_prefix_kernel) stays NaN
-  d.output[(static_cast<size_t>(seq) * d.query_head_count + head * gqa + h) * D + dd] = l == 0.0f ? 0.0f : o / l;
+  // 0 when no token is visible
+  d.output[(static_cast<size_t>(seq) * d.query_head_count + head * gqa + h) * D + dd] =
+      nan ? __builtin_nanf("") : l == 0.0f ? 0.0f : o / l;
 }
 
 // Cascade plan: prefix splits (slots [0, ps)) sized so that the prefix pass has about two workgroups per CU, then the

@@ -6,7 +6,10 @@ import numpy as np
 import oracle as O
 
 
-def make_seqs(seq_tokens, kv_heads, D, seed, scale_spread=False):
+def make_seqs(seq_tokens, kv_heads, D, seed, scale_spread=False, v_mult=None):
+    """K, V ~ N(0,1) per sequence [kv_heads, T, D]. v_mult[s][h] (optional) multiplies all of V of sequence s,
+    head h: whole sequences / heads of small or huge V magnitude, so every page scale of that head is small or
+    huge (not only single tokens inside a page, as scale_spread does)."""
     rng = np.random.default_rng(seed)
     data = []
     for s, T in enumerate(seq_tokens):
@@ -15,6 +18,8 @@ def make_seqs(seq_tokens, kv_heads, D, seed, scale_spread=False):
         if scale_spread:  # channels / tokens of very different magnitude (outlier channels, tiny tokens)
             K *= rng.choice([0.01, 1.0, 30.0], size=(1, 1, D)).astype(np.float32)
             V *= rng.choice([1e-3, 1.0, 8.0], size=(1, T, 1)).astype(np.float32)
+        if v_mult is not None:
+            V *= np.asarray(v_mult[s], np.float32).reshape(kv_heads, 1, 1)
         data.append((K, V))
     return data
 
@@ -56,3 +61,17 @@ def oracle_batched(kv, data, queries, query_pos, softmax_scale, gqa):
 
 def normwise_err(got, ref):
     return float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def head_err(got, ref):
+    """Worst normwise relative error over (sequence, query head) rows: max over rows of max_d |err| / max_d |ref|
+    for outputs [S, QH, D]. Unlike normwise_err over the whole batch, a wrong head of small magnitude cannot hide
+    behind a large one. Rows whose reference is all zero (nothing visible) must be exactly zero."""
+    got = np.asarray(got, np.float64).reshape(-1, got.shape[-1])
+    ref = np.asarray(ref, np.float64).reshape(-1, ref.shape[-1])
+    den = np.abs(ref).max(axis=1)
+    err = np.abs(got - ref).max(axis=1)
+    zero = den == 0
+    if zero.any() and err[zero].max() != 0:
+        return float("inf")
+    return float((err[~zero] / den[~zero]).max()) if (~zero).any() else 0.0
