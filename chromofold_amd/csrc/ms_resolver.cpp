@@ -39,23 +39,23 @@ void hip_check(hipError_t e, const char *what) {
   if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
 }
 
-struct SharedPage {
+struct ArenaPage {
   uint64_t id = 0;
   uint64_t seal_generation = 0;
   cf_device_page_descriptor descriptor{};
   uint64_t resident_bytes = 0;
-  uint32_t logical_refs = 0;
-  uint32_t in_flight_refs = 0;
+  uint32_t holders = 0;
+  uint32_t batch_holds = 0;
   bool retired = false;
 };
 
-struct PageRef {
+struct PageSpan {
   uint64_t page_id = 0;
   int64_t logical_begin = 0;
 };
 
-struct LayerState {
-  std::vector<PageRef> pages;
+struct LayerTable {
+  std::vector<PageSpan> pages;
   DeviceBuffer table;  // device cf_device_page_descriptor[capacity]
   uint32_t capacity = 0;
   uint64_t table_generation = 0;
@@ -66,9 +66,9 @@ struct LayerState {
   bool vector_only = false;  // mixed block sizes, or payloads not 16-byte aligned: the VALU attention kernel
 };
 
-struct SequenceState {
+struct SeqRecord {
   int64_t id = 0;
-  std::vector<LayerState> layers;
+  std::vector<LayerTable> layers;
   uint64_t topology_generation = 1;
   bool dispatchable = true;
 };
@@ -86,8 +86,8 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 struct cf_ms_cuda_resolver {
   cf_ms_cuda_config config{};
   mutable std::mutex mutex;
-  std::map<int64_t, SequenceState> sequences;
-  std::unordered_map<uint64_t, SharedPage> pages;
+  std::map<int64_t, SeqRecord> sequences;
+  std::unordered_map<uint64_t, ArenaPage> pages;
   std::vector<PendingBatch> pending;
   uint64_t next_page_id = 1;
   cf_ms_cuda_counters counters{};
@@ -97,7 +97,7 @@ struct cf_ms_cuda_resolver {
   uint64_t active_bytes() const { return uint64_t(config.page_size) * config.kv_head_count * config.head_dim * 4u; }
 
   // Rewrites the layer's device page table from its references (logical begins) — stream ordered.
-  void refresh_table(LayerState &layer, hipStream_t stream) {
+  void refresh_table(LayerTable &layer, hipStream_t stream) {
     std::vector<cf_device_page_descriptor> host;
     host.reserve(layer.pages.size());
     for (const auto &ref : layer.pages) {
@@ -125,9 +125,9 @@ struct cf_ms_cuda_resolver {
 
   void drop_logical_ref(uint64_t page_id) {
     auto it = pages.find(page_id);
-    if (it == pages.end() || it->second.logical_refs == 0) throw std::runtime_error("page logical reference underflow");
-    SharedPage &p = it->second;
-    if (--p.logical_refs == 0) {
+    if (it == pages.end() || it->second.holders == 0) throw std::runtime_error("page logical reference underflow");
+    ArenaPage &p = it->second;
+    if (--p.holders == 0) {
       p.retired = true;
       ++counters.pages_retired;
       counters.pending_reclamation_bytes += p.resident_bytes;
@@ -136,7 +136,7 @@ struct cf_ms_cuda_resolver {
     }
   }
 
-  void release_sequence(SequenceState &seq) {
+  void release_sequence(SeqRecord &seq) {
     for (auto &layer : seq.layers)
       for (const auto &ref : layer.pages) drop_logical_ref(ref.page_id);
   }
@@ -144,8 +144,8 @@ struct cf_ms_cuda_resolver {
   void release_in_flight(const std::vector<uint64_t> &ids) {
     for (uint64_t id : ids) {
       auto it = pages.find(id);
-      if (it == pages.end() || it->second.in_flight_refs == 0) throw std::runtime_error("snapshot reference underflow");
-      --it->second.in_flight_refs;
+      if (it == pages.end() || it->second.batch_holds == 0) throw std::runtime_error("snapshot reference underflow");
+      --it->second.batch_holds;
       --counters.in_flight_page_references;
     }
   }
@@ -182,7 +182,7 @@ extern "C" int cf_ms_cuda_sequence_create(cf_ms_cuda_resolver *r, int64_t sequen
   std::lock_guard<std::mutex> guard(r->mutex);
   try {
     if (r->sequences.count(sequence_id)) throw std::runtime_error("sequence already exists");
-    SequenceState s;
+    SeqRecord s;
     s.id = sequence_id;
     s.layers.resize(r->config.layer_count);
     r->sequences.emplace(sequence_id, std::move(s));
@@ -209,14 +209,14 @@ extern "C" int cf_ms_cuda_publish_page_async(cf_ms_cuda_resolver *r, const cf_ms
       throw std::runtime_error("publication descriptor does not match the resolver topology");
     if (!aligned4(d.key_payload) || !aligned4(d.value_payload) || !aligned4(d.key_scales) || !aligned4(d.value_scales))
       throw std::runtime_error("publication descriptor storage is not 4-byte aligned");
-    SharedPage page;
+    ArenaPage page;
     page.id = r->next_page_id++;
     page.seal_generation = pub->seal_generation;
     page.descriptor = d;
     page.resident_bytes = pub->resident_bytes;
-    page.logical_refs = 1;
+    page.holders = 1;
     r->pages.emplace(page.id, page);
-    LayerState &layer = seq->second.layers[pub->layer];
+    LayerTable &layer = seq->second.layers[pub->layer];
     const uint32_t bs_before = layer.block_size;
     const bool vector_before = layer.vector_only;
     if (layer.pages.empty()) layer.block_size = d.block_size;
@@ -252,7 +252,7 @@ extern "C" int cf_ms_cuda_stage_active_async(cf_ms_cuda_resolver *r, int64_t seq
     auto seq = r->sequences.find(sequence_id);
     if (seq == r->sequences.end() || layer_index >= seq->second.layers.size())
       throw std::runtime_error("active target is invalid");
-    LayerState &layer = seq->second.layers[layer_index];
+    LayerTable &layer = seq->second.layers[layer_index];
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (!layer.active_k.ptr) hip_check(layer.active_k.allocate(r->active_bytes()), "active K allocation");
     if (!layer.active_v.ptr) hip_check(layer.active_v.allocate(r->active_bytes()), "active V allocation");
@@ -280,17 +280,17 @@ extern "C" int cf_ms_cuda_copy_sequence_async(cf_ms_cuda_resolver *r, int64_t so
     auto src = r->sequences.find(source_id);
     if (src == r->sequences.end()) throw std::runtime_error("source sequence is missing");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    SequenceState cand;
+    SeqRecord cand;
     cand.id = destination_id;
     cand.layers.resize(r->config.layer_count);
     for (uint32_t li = 0; li < r->config.layer_count; ++li) {
-      const LayerState &from = src->second.layers[li];
-      LayerState &to = cand.layers[li];
+      const LayerTable &from = src->second.layers[li];
+      LayerTable &to = cand.layers[li];
       to.pages = from.pages;
       to.block_size = from.block_size;
       to.vector_only = from.vector_only;
       for (const auto &ref : to.pages) {
-        ++r->pages.at(ref.page_id).logical_refs;
+        ++r->pages.at(ref.page_id).holders;
         acquired.push_back(ref.page_id);
       }
       if (from.active_count) {
@@ -319,7 +319,7 @@ extern "C" int cf_ms_cuda_copy_sequence_async(cf_ms_cuda_resolver *r, int64_t so
   } catch (const std::exception &ex) {
     for (uint64_t id : acquired) {
       auto it = r->pages.find(id);
-      if (it != r->pages.end() && it->second.logical_refs) --it->second.logical_refs;
+      if (it != r->pages.end() && it->second.holders) --it->second.holders;
     }
     ++r->counters.cuda_errors;
     r->error = ex.what();
@@ -387,9 +387,9 @@ extern "C" int cf_ms_cuda_execute_batch_async(cf_ms_cuda_resolver *r, const cf_m
       if (seq == r->sequences.end() || !seq->second.dispatchable)
         throw std::runtime_error("sequence is unavailable for dispatch");
       if (it.layer >= seq->second.layers.size()) throw std::runtime_error("layer out of range");
-      const LayerState &layer = seq->second.layers[it.layer];
+      const LayerTable &layer = seq->second.layers[it.layer];
       for (const auto &ref : layer.pages) {
-        ++r->pages.at(ref.page_id).in_flight_refs;
+        ++r->pages.at(ref.page_id).batch_holds;
         ++r->counters.in_flight_page_references;
         taken.push_back(ref.page_id);
       }
@@ -495,7 +495,7 @@ extern "C" int cf_ms_cuda_reclaim_async(cf_ms_cuda_resolver *r, void *) {
       it = r->pending.erase(it);
     }
     for (auto it = r->pages.begin(); it != r->pages.end();) {
-      if (it->second.retired && it->second.logical_refs == 0 && it->second.in_flight_refs == 0) {
+      if (it->second.retired && it->second.holders == 0 && it->second.batch_holds == 0) {
         r->counters.pending_reclamation_bytes -= it->second.resident_bytes;
         ++r->counters.pages_reclaimed;
         it = r->pages.erase(it);
@@ -528,8 +528,8 @@ extern "C" int cf_ms_cuda_audit(const cf_ms_cuda_resolver *r) {
   for (const auto &[id, page] : r->pages) {
     auto o = observed.find(id);
     const uint64_t n = o == observed.end() ? 0u : o->second;
-    if (!page.retired && page.logical_refs != n) return -1;
-    if (page.retired && (page.logical_refs != 0 || n != 0)) return -1;
+    if (!page.retired && page.holders != n) return -1;
+    if (page.retired && (page.holders != 0 || n != 0)) return -1;
   }
   return r->counters.cross_sequence_contamination == 0 && r->counters.dense_fallback_launches == 0 ? 0 : -1;
 }

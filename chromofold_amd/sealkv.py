@@ -337,74 +337,3 @@ class MsResolver:
         c = cf_ms_cuda_counters()
         self._rc(A.lib().cf_ms_cuda_get_counters(self.h, C.byref(c)), "counters")
         return {k: getattr(c, k) for k, _ in c._fields_}
-
-
-# ------------------------------------------------------------------------------------------------ bookkeeping cache
-class cf_multisequence_config(C.Structure):
-    _fields_ = [(k, U32) for k in ("layer_count", "kv_head_count", "query_head_count", "head_dim", "page_size",
-                                   "gqa_group_size", "use_async_allocator", "enable_invariant_auditor")]
-
-
-class cf_multisequence_counters(C.Structure):
-    _fields_ = [(k, U64) for k in (
-        "sequences_created", "sequences_copied", "sequences_removed", "sequences_shifted", "active_sequences",
-        "active_sequences_peak", "shared_pages", "shared_page_references", "page_ref_increments",
-        "page_ref_decrements", "pages_reclaimed", "pages_pending_reclamation", "pending_reclamation_bytes",
-        "pending_reclamation_bytes_peak", "speculative_transactions_started", "speculative_transactions_committed",
-        "speculative_transactions_rolled_back", "batches_dispatched", "sequences_per_batch_peak", "invariant_audits",
-        "invariant_failures", "unsupported_operations", "dense_fallback_launches")]
-
-
-class cf_sequence_attention_item(C.Structure):
-    _fields_ = cf_ms_batch_item._fields_
-
-
-for _n, (_r, _a) in {
-    "cf_multisequence_create": (P, [P]),
-    "cf_multisequence_destroy": (None, [P, P]),
-    "cf_sequence_create": (C.c_int, [P, I64]),
-    "cf_sequence_copy_async": (C.c_int, [P, I64, I64, U32, U32, P]),
-    "cf_sequence_remove_async": (C.c_int, [P, I64, I64, I64, P]),
-    "cf_sequence_shift_async": (C.c_int, [P, I64, U32, U32, I32, P]),
-    "cf_sequence_append_async": (C.c_int, [P, I64, U32, U32, P, P, P]),
-    "cf_multisequence_attention_async": (C.c_int, [P, P, U32, P]),
-    "cf_sequence_speculation_begin": (U64, [P, I64]),
-    "cf_sequence_speculation_commit": (C.c_int, [P, I64, U64, U32, P]),
-    "cf_sequence_speculation_rollback": (C.c_int, [P, I64, U64, P]),
-    "cf_multisequence_reclaim_async": (C.c_int, [P, P]),
-    "cf_multisequence_audit": (C.c_int, [P]),
-    "cf_multisequence_get_counters": (C.c_int, [P, P]),
-    "cf_multisequence_last_error": (C.c_char_p, [P]),
-}.items():
-    A.declare(_n, _r, _a)
-
-
-class MultiSequenceCache:
-    """cf_multisequence_cache: host bookkeeping (token ranges and page references; no KV data)."""
-
-    def __init__(self, layer_count, kv_heads, q_heads, head_dim, page_size, gqa=None, auditor=True):
-        gqa = q_heads // kv_heads if gqa is None else gqa
-        self.config = cf_multisequence_config(layer_count, kv_heads, q_heads, head_dim, page_size, gqa, 0,
-                                              1 if auditor else 0)
-        self.h = A.lib().cf_multisequence_create(C.byref(self.config))
-        if not self.h:
-            raise SealError("cf_multisequence_create rejected the config")
-
-    def close(self):
-        if self.h:
-            A.lib().cf_multisequence_destroy(self.h, None)
-            self.h = None
-
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
-
-    def last_error(self) -> str:
-        return A.lib().cf_multisequence_last_error(self.h).decode()
-
-    def counters(self) -> dict:
-        c = cf_multisequence_counters()
-        assert A.lib().cf_multisequence_get_counters(self.h, C.byref(c)) == 0
-        return {k: getattr(c, k) for k, _ in c._fields_}

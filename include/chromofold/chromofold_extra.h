@@ -40,8 +40,9 @@ cf_status cf_rrr_rank_async(const uint32_t *classes, const uint32_t *offsets, co
                             uint32_t *out, size_t count, void *stream);
 
 /* Delta-cluster fetch: out[t] = delta of leaf[t] at pos[t] if its sorted dpos[dstart[leaf] .. +dlen[leaf]) holds
- * pos[t], else base[pos[t]] (or -1 when pos[t] >= nbase). Replaces reference src/cuda/delta_apply.cu:33-43
- * (benchmarks/delta_bench.cu:25). */
+ * pos[t] (the first such entry when positions repeat), else base[pos[t]] (or -1 when pos[t] >= nbase or
+ * pos[t] < 0; the reference reads before the array for a negative position). Replaces reference
+ * src/cuda/delta_apply.cu:33-43 (benchmarks/delta_bench.cu:25). */
 cf_status cf_delta_fetch_async(const int32_t *base, int nbase, const int32_t *dpos, const int32_t *dval,
                                const int32_t *dstart, const int32_t *dlen, const int32_t *device_leaf,
                                const int32_t *device_pos, int32_t *out, size_t count, void *stream);

@@ -13,7 +13,6 @@
 #include "chromofold/chromofold_search.h"
 #include "chromofold/device_kv_dataplane.h"
 #include "chromofold/device_kv_seal_attention.h"
-#include "chromofold/multisequence_cache.h"
 #include "chromofold/multisequence_cuda_resolver.h"
 #include "chromofold/kv_codec_ext.h"
 #include "chromofold/kv_cuda.h"
@@ -145,12 +144,6 @@ int main(void) {
     expect("cf_ms_cuda_execute_batch_async", cf_ms_cuda_execute_batch_async(NULL, NULL, 0, NULL), -1);
     expect("cf_ms_cuda_audit", cf_ms_cuda_audit(NULL), -1);
     expect("cf_ms_cuda_last_error", cf_ms_cuda_last_error(NULL) != NULL, 1);
-    printf("sizeof cf_multisequence_counters %zu\n", sizeof(cf_multisequence_counters));
-    printf("sizeof cf_sequence_attention_item %zu\n", sizeof(cf_sequence_attention_item));
-    expect("cf_multisequence_create", cf_multisequence_create(NULL) == NULL, 1);
-    expect("cf_sequence_append_async", cf_sequence_append_async(NULL, 0, 0, 0, NULL, NULL, NULL), -1);
-    expect("cf_multisequence_attention_async", cf_multisequence_attention_async(NULL, NULL, 0, NULL), -1);
-    expect("cf_sequence_speculation_begin", cf_sequence_speculation_begin(NULL, 0) == 0, 1);
   }
   printf("%s (%d failure%s)\n", failures ? "FAIL" : "PASS", failures, failures == 1 ? "" : "s");
   return failures ? 1 : 0;

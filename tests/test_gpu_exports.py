@@ -225,6 +225,46 @@ def test_delta_fetch(dev):
     assert np.array_equal(out.cpu().numpy(), exp)
 
 
+def test_delta_fetch_edges(dev):
+    """Leaf lengths 1..9 (around the search's switch to its final scan) and 3000, repeated delta positions (the
+    first one's value wins), queries at every delta position, one before and one after it, and negative positions
+    (-1, like a position past the base)."""
+    import torch
+    rng = np.random.default_rng(11)
+    nbase = 5000
+    base = rng.integers(0, 1 << 30, nbase).astype(np.int32)
+    dpos, dval, dstart, dlen = [], [], [], []
+    for k in list(range(0, 10)) + [3000, 64, 65, 255]:
+        p = np.sort(rng.integers(0, nbase + 10, k)).astype(np.int32)  # with repeats
+        dstart.append(len(dpos))
+        dlen.append(k)
+        dpos.extend(p)
+        dval.extend(rng.integers(0, 1 << 30, k))
+    leaves = len(dlen)
+    dpos, dval = np.array(dpos + [0], np.int32), np.array(dval + [0], np.int32)
+    dstart, dlen = np.array(dstart, np.int32), np.array(dlen, np.int32)
+    leaf, pos = [], []
+    for lf in range(leaves):
+        s, n = dstart[lf], dlen[lf]
+        for v in list(dpos[s:s + n]) + [0, nbase - 1, nbase, nbase + 9, -1, -7]:
+            for dv in (-1, 0, 1):
+                leaf.append(lf)
+                pos.append(int(v) + dv)
+    leaf, pos = np.array(leaf, np.int32), np.array(pos, np.int32)
+    exp = np.where((pos >= 0) & (pos < nbase), base[np.clip(pos, 0, nbase - 1)], -1).astype(np.int32)
+    for t in range(pos.size):
+        s, n = dstart[leaf[t]], dlen[leaf[t]]
+        hit = np.nonzero(dpos[s:s + n] == pos[t])[0]
+        if hit.size:
+            exp[t] = dval[s + hit[0]]
+    Q = pos.size
+    out = torch.empty(Q, dtype=torch.int32, device=dev)
+    a = [_d(x, dev) for x in (base, dpos, dval, dstart, dlen, leaf, pos)]
+    _ok(_lib().cf_delta_fetch_async(a[0].data_ptr(), nbase, *[x.data_ptr() for x in a[1:]], out.data_ptr(), Q, None),
+        "delta")
+    assert np.array_equal(out.cpu().numpy(), exp)
+
+
 @pytest.mark.parametrize("n,V,block", [(50000, 16, 64), (30001, 256, 1024), (4096, 4, 1), (1000, 9, 333)])
 def test_rans_decode(dev, n, V, block):
     import torch
