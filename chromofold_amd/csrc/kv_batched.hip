@@ -78,47 +78,17 @@ __device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
   return r;
 }
 
-// Symbol bytes of quad qd (0..3) of a 16-value low-part group: nibbles from n0/n1, bits 4-5 from the crumb word
-// c, bits 6-7 from the spread high parts — two bit-field inserts per quad.
-template <int QD>
-__device__ __forceinline__ uint32_t quad_bytes(uint32_t n0, uint32_t n1, uint32_t c, uint32_t spread) {
-  const uint32_t nsrc = QD == 0 ? n0 : QD == 1 ? (n0 >> 4) : QD == 2 ? n1 : (n1 >> 4);
-  const uint32_t cs = QD == 0 ? (c << 4) : QD == 1 ? (c << 2) : QD == 2 ? c : (c >> 2);
-  return bfi(0x3F3F3F3Fu, bfi(0x0F0F0F0Fu, nsrc, cs), spread);
-}
-
-// One interleaved-rANS step of the 64-lane stream. x = lane state; wbase = wave-uniform address of the current
-// word (cursor) in the stream staged in LDS (or global memory for oversized groups). The slot entry e is
-// {f | c << 16, spread high parts}. Returns the spread high parts of the decoded joint symbol.
-template <typename WordPtr>
-__device__ __forceinline__ uint32_t rans_step(const uint2 *__restrict__ tab, uint32_t &x, WordPtr &wbase) {
-  const uint2 e = tab[x & (kSlots - 1)];
-  // x = f * (x >> 11) + c with f, c the two 16-bit halves of e.x, read in place by SDWA operand selects
-  const uint32_t xs = x >> CF_KV_RANS_PROB_BITS;
-  uint32_t fx;
-  asm("v_mul_u32_u24_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD"
-      : "=v"(fx) : "v"(e.x), "v"(xs));
-  asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:DWORD"
-      : "=v"(x) : "v"(e.x), "v"(fx));
-  const bool need = x < 65536u;
-  const uint64_t m = __builtin_amdgcn_ballot_w64(need);
-  const uint32_t idx = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
-                                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
-  const uint32_t w = wbase[idx];  // lanes that do not renormalise read a harmless in-bounds word
-  x = __builtin_amdgcn_perm(x, w, need ? 0x05040100u : 0x07060504u);  // (x << 16) | w  or  x
-  wbase += __builtin_popcountll(m);
-  return e.y;
-}
-
-// The same step split in three so that the four chains of a lane overlap their LDS round trips: the slot entry
-// lookups of all chains are issued first, then the state updates with their renormalisation-word fetches, then
-// the word merges.
+// rANS decode of one 64-lane stream, split in three so that the two chains of a lane overlap their LDS round
+// trips: the slot entry lookups of both chains are issued first, then the state updates with their
+// renormalisation-word fetches, then the word merges. x = lane state; wbase = wave-uniform address of the current
+// word (cursor) of the stream staged in LDS. The slot entry is {f | c << 16, spread big bits}.
 __device__ __forceinline__ uint2 rans_lookup(const uint2 *__restrict__ tab, uint32_t x) {
   return tab[x & (kSlots - 1)];
 }
 
 template <typename WordPtr>
 __device__ __forceinline__ uint32_t rans_advance(uint32_t ex, uint32_t &x, WordPtr &wbase, uint32_t &sel) {
+  // x = f * (x >> 11) + c with f, c the two 16-bit halves of ex, read in place by SDWA operand selects
   const uint32_t xs = x >> CF_KV_RANS_PROB_BITS;
   uint32_t fx;
   asm("v_mul_u32_u24_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD"
@@ -135,14 +105,45 @@ __device__ __forceinline__ uint32_t rans_advance(uint32_t ex, uint32_t &x, WordP
   return w;
 }
 
+// ---- format-4 value assembly (kv_codec_ext.h): quad k of a sign group sits in frame r = kFrame[k]
+constexpr uint32_t kFrame[8] = {0, 4, 2, 6, 1, 5, 3, 7};
+constexpr uint32_t kNWord[4] = {0, 1, 3, 4};  // raw word with the nibbles of quads 2m, 2m + 1 (N0 N1 C0 N2 N3 C1 S)
+constexpr uint32_t rotl_c(uint32_t v, uint32_t r) { return r ? (v << r) | (v >> (32 - r)) : v; }
+
+template <uint32_t R>
+__device__ __forceinline__ uint32_t rotr(uint32_t v) {
+  if constexpr (R == 0) return v;
+  else return __builtin_amdgcn_alignbit(v, v, R);
+}
+
+// The magnitude bytes |q| (bit 7 clear) of the quad in frame R: nibbles from n, crumbs from c, big bits from the
+// pair's spread word (already in the pair's frames), then rotated back to byte alignment.
+template <uint32_t R>
+__device__ __forceinline__ uint32_t quad_mag(uint32_t n, uint32_t c, uint32_t spread) {
+  return rotr<R>(bfi(rotl_c(0x0F0F0F0Fu, R), n, bfi(rotl_c(0x30303030u, R), c, spread)));
+}
+
+// The sign bytes (0x80 or 0x00) of the quad in frame R.
+template <uint32_t R>
+__device__ __forceinline__ uint32_t quad_signs(uint32_t s) { return rotr<R>(s) & 0x80808080u; }
+
+// Exact f16 operand of four sign-magnitude values: the f16 denormals (sign << 15) | |q| = q * 2^-24.
+__device__ __forceinline__ half4_t sm_to_half4(uint32_t mag, uint32_t signs) {
+  half4_t h;
+  uint32_t *w = reinterpret_cast<uint32_t *>(&h);
+  w[0] = __builtin_amdgcn_perm(signs, mag, 0x05010400u);  // [|q0|, s0, |q1|, s1]
+  w[1] = __builtin_amdgcn_perm(signs, mag, 0x07030602u);
+  return h;
+}
+
 constexpr int kHdr = 64;                 // group header bytes
-constexpr int kStateBytes = 4 * 64 * 4;  // K A, K B, V A, V B lane states
+constexpr int kStateBytes = 2 * 64 * 4;  // K and V lane states of a chain start
 constexpr uint32_t kCapWords = CF_KV_RANS_MAX_GROUP_WORDS;  // K+V words staged in LDS per wavefront
 constexpr uint32_t kSlackWords = 64;     // reads past the last word by non-renormalising lanes stay in the buffer
 
-// rANS words of a group: the sum of its four chains' counts (header word_count[0..3] as two u32)
-__device__ __forceinline__ uint32_t word_total(uint32_t c01, uint32_t c23) {
-  return (c01 & 0xFFFFu) + (c01 >> 16) + (c23 & 0xFFFFu) + (c23 >> 16);
+template <int D>
+constexpr int raw_words() {  // u32 raw words of one stream of a RANS group
+  return 7 * (D / 32) * 64;
 }
 
 template <int D>
@@ -152,128 +153,124 @@ constexpr int buf_u32() {
   return words > red ? words : red;
 }
 
-template <int D, int CODEC>
-struct GroupCtx {
-  static constexpr int NQ = D / 4, NG = D / 16, LOWS = 3 * NG * 64;
-};
-
-// Decode one page group (K scores, softmax, V accumulation) with the word streams read through `wk` (the wave's
-// LDS staging buffer). `pre` always holds the NEXT low-part group's 6 words (3 K + 3 V): on entry the group's
-// first, and while low group g is decoded, group g + 1's (or, during the last one, the first low group of the next
-// RANS group at `nlw`, NULL if none) are in flight, a quarter of the group ahead of their use. `after_decode` runs as
-// soon as the decode loop no longer needs the word buffer (the caller stages the next group there).
+// Decode one page group (K scores, softmax, V accumulation).
+// RANS groups: `st` holds the chain's lane states on entry (K, V) and the states the group ends with on return;
+// the word streams are read through `wk` (the wave's LDS staging buffer, K stream then V); `raw` points at the
+// group's raw words. `pre` always holds the NEXT sign group's 14 raw words (7 K + 7 V): on entry the group's first,
+// and while sign group s is decoded, sign group s + 1's (or, during the last one, the first sign group of the next
+// RANS group at `nlw`, NULL if none) are in flight, a quarter of the group ahead of their use.
+// INT8 groups: `raw` points at the symbol words (offset binary).
+// `after_decode` runs as soon as the decode loop no longer needs the word buffer (the caller stages the next group
+// there).
 template <int D, int CODEC, typename WordPtr, typename Hook>
-__device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&pre)[6], const uint32_t *nlw,
-                                           const uint32_t (&st4)[4],
-                                           const uint8_t *__restrict__ blob, WordPtr wk, uint32_t cnt01,
-                                           uint32_t cnt23,
-                                           const uint2 (*__restrict__ s_tab)[kSlots], const half4_t *qhi,
-                                           const half4_t *qlo, const float *qsum, _Float16 (*s_pw)[kGqa][16],
-                                           int lane, bool tok_ok, float ks, float vs, int &e_run, float *m_run,
-                                           float *l_run, float4_t *acc_v) {
-  constexpr int NQ = D / 4, LOWS = 3 * (D / 16) * 64;
+__device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&pre)[14], const uint32_t *nlw,
+                                           uint32_t (&st)[2], const uint32_t *__restrict__ raw, WordPtr wk,
+                                           uint32_t cnt_kv, const uint2 (*__restrict__ s_tab)[kSlots],
+                                           const half4_t *qhi, const half4_t *qlo, const float *qsum,
+                                           _Float16 (*s_pw)[kGqa][16], int lane, bool tok_ok, float ks, float vs,
+                                           int &e_run, float *m_run, float *l_run, float4_t *acc_v) {
+  constexpr int NQ = D / 4, RAW = raw_words<D>();
   constexpr bool RANS = CODEC == CF_KV_CODEC_RANS_HYBRID;
   const int G = lane >> 4, t = lane & 15;
   float4_t sa = {0, 0, 0, 0}, sb = {0, 0, 0, 0};
-  uint32_t vb[NQ];
-  {
-    const uint32_t *lowk = reinterpret_cast<const uint32_t *>(blob + kHdr + kStateBytes);
-    const uint32_t *raw = reinterpret_cast<const uint32_t *>(blob + kHdr);
-    // chain A = even quads, chain B = odd quads of each stream: four independent states per lane
-    // (loaded with the group's header, one group ahead)
-    uint32_t xk0 = st4[0], xk1 = st4[1], xv0 = st4[2], xv1 = st4[3];
-    // word cursors of the four chains (wave-uniform: scalar registers; their advance is scalar work)
-    const uint32_t c01 = __builtin_amdgcn_readfirstlane(cnt01), c23 = __builtin_amdgcn_readfirstlane(cnt23);
-    WordPtr wk0 = wk, wk1 = wk + (c01 & 0xFFFFu), wv0 = wk1 + (c01 >> 16), wv1 = wv0 + (c23 & 0xFFFFu);
-    uint32_t kl[3] = {0, 0, 0}, vl[3] = {0, 0, 0};
-    // K scores of quad q: the decoded symbol bytes go straight into the MFMA (B operand); V bytes wait in vb
-    auto consume = [&](auto qc, uint32_t kbytes, uint32_t vbytes) {
-      constexpr int q = decltype(qc)::value;
-      vb[q] = vbytes;
-      const half4_t bk = bytes_to_half4(kbytes);
-      sa = __builtin_amdgcn_mfma_f32_4x4x4f16(qhi[q / 16], bk, sa, 4, q % 16, 0);
-      sb = __builtin_amdgcn_mfma_f32_4x4x4f16(qlo[q / 16], bk, sb, 4, q % 16, 0);
-    };
-    if constexpr (RANS) {
-      // pair P = quads 2P (chain A) and 2P + 1 (chain B) of K and of V: four independent rANS steps
-      [&]<int... P>(std::integer_sequence<int, P...>) {
-        (
-            [&] {
-              constexpr int q0 = 2 * P, g = q0 / 4, qd0 = q0 % 4;
-              if constexpr (qd0 == 0) {  // low group g: take the prefetched words, start the next group's
+  uint32_t vb[NQ];                         // V: magnitude bytes (RANS) or offset-binary symbols (INT8) per quad
+  uint32_t vsg[RANS ? D / 32 : 1];         // V sign words per sign group (RANS)
+  // K MFMAs of quad q (A = the 4 query heads broadcast from block q % 16, hi and lo parts)
+  auto k_mfma = [&](auto qc, half4_t bk) {
+    constexpr int q = decltype(qc)::value;
+    sa = __builtin_amdgcn_mfma_f32_4x4x4f16(qhi[q / 16], bk, sa, 4, q % 16, 0);
+    sb = __builtin_amdgcn_mfma_f32_4x4x4f16(qlo[q / 16], bk, sb, 4, q % 16, 0);
+  };
+  if constexpr (RANS) {
+    uint32_t xk = st[0], xv = st[1];
+    // word cursors of the two streams (wave-uniform: scalar registers; their advance is scalar work)
+    const uint32_t ckv = __builtin_amdgcn_readfirstlane(cnt_kv);
+    WordPtr wkk = wk, wvv = wk + (ckv & 0xFFFFu);
+    uint32_t cw[14];  // this sign group's raw words: K N0 N1 C0 N2 N3 C1 S, then V the same
+    // step P decodes quads 2P and 2P + 1 of K and of V: two independent rANS steps
+    [&]<int... P>(std::integer_sequence<int, P...>) {
+      (
+          [&] {
+            constexpr int sg = P / 4, m = P % 4, q0 = 2 * P;
+            constexpr uint32_t rA = kFrame[2 * m], rB = kFrame[2 * m + 1];
+            if constexpr (m == 0) {  // sign group sg: take the prefetched words, start the next group's
 #pragma unroll
-                for (int w = 0; w < 3; ++w) {
-                  kl[w] = pre[w];
-                  vl[w] = pre[3 + w];
+              for (int w = 0; w < 14; ++w) cw[w] = pre[w];
+              vsg[sg] = cw[13];
+              if constexpr (sg + 1 < D / 32) {
+#pragma unroll
+                for (int w = 0; w < 7; ++w) {
+                  pre[w] = raw[(7 * (sg + 1) + w) * 64 + lane];
+                  pre[7 + w] = raw[RAW + (7 * (sg + 1) + w) * 64 + lane];
                 }
-                if constexpr (g + 1 < D / 16) {
+              } else if (nlw) {
 #pragma unroll
-                  for (int w = 0; w < 3; ++w) {
-                    pre[w] = lowk[((g + 1) * 3 + w) * 64 + lane];
-                    pre[3 + w] = lowk[LOWS + ((g + 1) * 3 + w) * 64 + lane];
-                  }
-                } else if (nlw) {
-#pragma unroll
-                  for (int w = 0; w < 3; ++w) {
-                    pre[w] = nlw[w * 64 + lane];
-                    pre[3 + w] = nlw[LOWS + w * 64 + lane];
-                  }
+                for (int w = 0; w < 7; ++w) {
+                  pre[w] = nlw[w * 64 + lane];
+                  pre[7 + w] = nlw[RAW + w * 64 + lane];
                 }
               }
-              const uint2 ek0 = rans_lookup(s_tab[0], xk0), ek1 = rans_lookup(s_tab[0], xk1);
-              const uint2 ev0 = rans_lookup(s_tab[1], xv0), ev1 = rans_lookup(s_tab[1], xv1);
-              uint32_t sk0, sk1, sv0, sv1;
-              const uint32_t wdk0 = rans_advance(ek0.x, xk0, wk0, sk0);
-              const uint32_t wdk1 = rans_advance(ek1.x, xk1, wk1, sk1);
-              const uint32_t wdv0 = rans_advance(ev0.x, xv0, wv0, sv0);
-              const uint32_t wdv1 = rans_advance(ev1.x, xv1, wv1, sv1);
-              xk0 = __builtin_amdgcn_perm(xk0, wdk0, sk0);
-              xk1 = __builtin_amdgcn_perm(xk1, wdk1, sk1);
-              xv0 = __builtin_amdgcn_perm(xv0, wdv0, sv0);
-              xv1 = __builtin_amdgcn_perm(xv1, wdv1, sv1);
-              consume(std::integral_constant<int, q0>{}, quad_bytes<qd0>(kl[0], kl[1], kl[2], ek0.y),
-                      quad_bytes<qd0>(vl[0], vl[1], vl[2], ev0.y));
-              consume(std::integral_constant<int, q0 + 1>{}, quad_bytes<qd0 + 1>(kl[0], kl[1], kl[2], ek1.y),
-                      quad_bytes<qd0 + 1>(vl[0], vl[1], vl[2], ev1.y));
-            }(),
-            ...);
-      }(std::make_integer_sequence<int, NQ / 2>{});
-    } else {
-      if (nlw) {  // a raw group: start the next RANS group's first low-part words now
+            }
+            const uint2 ek = rans_lookup(s_tab[0], xk), ev = rans_lookup(s_tab[1], xv);
+            uint32_t selk, selv;
+            const uint32_t wdk = rans_advance(ek.x, xk, wkk, selk);
+            const uint32_t wdv = rans_advance(ev.x, xv, wvv, selv);
+            xk = __builtin_amdgcn_perm(xk, wdk, selk);
+            xv = __builtin_amdgcn_perm(xv, wdv, selv);
+            // the spread words hold the big bits in the frames (0, 4): rotate them into this pair's frames
+            const uint32_t spk = rA ? __builtin_amdgcn_alignbit(ek.y, ek.y, 32 - rA) : ek.y;
+            const uint32_t spv = rA ? __builtin_amdgcn_alignbit(ev.y, ev.y, 32 - rA) : ev.y;
+            constexpr int nw = kNWord[m], cwi = m < 2 ? 2 : 5;
+            k_mfma(std::integral_constant<int, q0>{},
+                   sm_to_half4(quad_mag<rA>(cw[nw], cw[cwi], spk), quad_signs<rA>(cw[6])));
+            k_mfma(std::integral_constant<int, q0 + 1>{},
+                   sm_to_half4(quad_mag<rB>(cw[nw], cw[cwi], spk), quad_signs<rB>(cw[6])));
+            vb[q0] = quad_mag<rA>(cw[7 + nw], cw[7 + cwi], spv);
+            vb[q0 + 1] = quad_mag<rB>(cw[7 + nw], cw[7 + cwi], spv);
+          }(),
+          ...);
+    }(std::make_integer_sequence<int, D / 8>{});
+    st[0] = xk;
+    st[1] = xv;
+  } else {
+    if (nlw) {  // a raw group: start the next RANS group's first raw words now
 #pragma unroll
-        for (int w = 0; w < 3; ++w) {
-          pre[w] = nlw[w * 64 + lane];
-          pre[3 + w] = nlw[LOWS + w * 64 + lane];
-        }
+      for (int w = 0; w < 7; ++w) {
+        pre[w] = nlw[w * 64 + lane];
+        pre[7 + w] = nlw[RAW + w * 64 + lane];
       }
-      [&]<int... Q>(std::integer_sequence<int, Q...>) {
-        (consume(std::integral_constant<int, Q>{}, raw[Q * 64 + lane], raw[NQ * 64 + Q * 64 + lane]), ...);
-      }(std::make_integer_sequence<int, NQ>{});
     }
+    [&]<int... Q>(std::integer_sequence<int, Q...>) {
+      ((vb[Q] = raw[NQ * 64 + Q * 64 + lane],
+        k_mfma(std::integral_constant<int, Q>{}, bytes_to_half4(raw[Q * 64 + lane]))), ...);
+    }(std::make_integer_sequence<int, NQ>{});
   }
   after_decode();  // the word buffer is free from here on
 
   // ---- online softmax over the wavefront's 64 tokens (one running max per head for all four pages)
+  // K operands: RANS = q * 2^-24 (f16 denormals); INT8 = 1024 + symbol, the 1152 offset folded out with the query sum
+  const float ksc = RANS ? ks * 16777216.0f : ks;
   float s[kGqa], mx[kGqa];
 #pragma unroll
   for (int h = 0; h < kGqa; ++h) {
-    s[h] = tok_ok ? (sa[h] + sb[h] - kOffset * qsum[h]) * ks : -INFINITY;
+    s[h] = tok_ok ? (RANS ? (sa[h] + sb[h]) : (sa[h] + sb[h] - kOffset * qsum[h])) * ksc : -INFINITY;
     mx[h] = s[h];
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1)
 #pragma unroll
     for (int h = 0; h < kGqa; ++h) mx[h] = fmaxf(mx[h], __shfl_xor(mx[h], o));
-  // The lane's P.V sums (acc_v) only ever hold tokens of its own page slot G, so they are kept in units of
-  // 2^e with e = (exponent of that page's V scale) - 15: the f16 operand p * vs * 2^-e lies in [0, 2^15) whatever
-  // the V magnitude (no overflow for huge V), and weights p down to 2^-29 of the running maximum stay normal f16
-  // numbers (a row whose heaviest tokens have V = 0 is carried by such small weights). Moving to the next page's
-  // units is an exact power-of-two factor folded into the softmax rescale; a drop of more than 2^60 between
-  // consecutive pages is clamped so that the rescale cannot overflow.
-  const int ev = max(__builtin_amdgcn_frexp_expf(vs) - 15, e_run - 60);
+  // The lane's P.V sums (acc_v) only ever hold tokens of its own page slot G, so they are kept in units of 2^e with
+  // e = (exponent of that page's V scale) - 15 (+ 24 for RANS groups, whose V operands are q * 2^-24): the f16
+  // operand p * vs * 2^-(e - 0|24) lies in [0, 2^15) whatever the V magnitude (no overflow for huge V), and weights
+  // p down to 2^-29 of the running maximum stay normal f16 numbers (a row whose heaviest tokens have V = 0 is carried
+  // by such small weights). Moving to the next page's units is an exact power-of-two factor folded into the softmax
+  // rescale; a drop of more than 2^60 between consecutive pages is clamped so that the rescale cannot overflow.
+  constexpr int kOpExp = RANS ? 24 : 0;
+  const int ev = max(__builtin_amdgcn_frexp_expf(vs) - 15 + kOpExp, e_run - 60);
   const int de = e_run - ev;
   e_run = ev;
-  const float vsn = ldexpf(vs, -ev);
+  const float vsn = ldexpf(vs, kOpExp - ev);
   float alpha[kGqa];
 #pragma unroll
   for (int h = 0; h < kGqa; ++h) {
@@ -294,12 +291,20 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
   // ---- V MFMAs: out[h][t + 16i] += sum over the quad's 4 tokens of p * v
-#pragma unroll
-  for (int tq = 0; tq < 4; ++tq) {
-    const half4_t pa = *reinterpret_cast<const half4_t *>(&s_pw[G][lane & 3][4 * tq]);
-#pragma unroll
-    for (int i = 0; i < D / 16; ++i) acc_v[i] = mfma4(pa, bytes_to_half4_signed(vb[tq * (D / 16) + i]), acc_v[i]);
-  }
+  [&]<int... Q>(std::integer_sequence<int, Q...>) {
+    (
+        [&] {
+          constexpr int q = Q, tq = q / (D / 16), i = q % (D / 16);  // quad q = tokens 4tq.. at dim t + 16i
+          const half4_t pa = *reinterpret_cast<const half4_t *>(&s_pw[G][lane & 3][4 * tq]);
+          half4_t bv;
+          if constexpr (RANS)  // quad q is quad q % 8 of sign group q / 8
+            bv = sm_to_half4(vb[q], quad_signs<kFrame[q % 8]>(vsg[q / 8]));
+          else
+            bv = bytes_to_half4_signed(vb[q]);
+          acc_v[i] = mfma4(pa, bv, acc_v[i]);
+        }(),
+        ...);
+  }(std::make_integer_sequence<int, NQ>{});
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -318,14 +323,22 @@ struct SplitSlots {
   uint32_t g0, slot0, slots;
 };
 
+// A wave's groups: the pairs (2k, 2k + 1), k = k0 + wave, k0 + wave + 4, ..., clipped to the split's [ga, gb). The
+// groups of a pair are decoded back to back by the same wave (a RANS chain may run across them).
+__device__ __forceinline__ uint32_t next_group(uint32_t g, uint32_t gb) {
+  if ((g & 1u) == 0 && g + 1 < gb) return g + 1;
+  const uint32_t n = ((g >> 1) + kWaves) * 2;
+  return n < gb ? n : gb;
+}
+
 template <int D, int CODEC>
 __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_batched_desc d, uint32_t splits,
                                                                          float *__restrict__ partial, SplitSlots ss) {
   constexpr int NQ = D / 4;
-  constexpr int LOWS = 3 * (D / 16) * 64;  // u32 words of one stream's low parts
+  constexpr int RAW = raw_words<D>();
   constexpr bool RANS = CODEC == CF_KV_CODEC_RANS_HYBRID;
   constexpr int BUF = buf_u32<D>();
-  __shared__ uint2 s_tab[RANS ? 2 : 1][kSlots];     // {f | c << 16, spread high parts} per slot, K and V tables
+  __shared__ uint2 s_tab[RANS ? 2 : 1][kSlots];     // {f | c << 16, spread big bits} per slot, K and V tables
   __shared__ _Float16 s_p[kWaves][4][kGqa][16];     // per wave: [page][head][token] probability * v_scale
   __shared__ uint32_t s_buf[kWaves][BUF];           // per wave: staged words; query staging and partials alias it
 
@@ -366,7 +379,8 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
     qhi[c] = (4 * qd < D) ? *reinterpret_cast<const half4_t *>(&s_q[0][lane & 3][4 * qd]) : half4_t{0, 0, 0, 0};
     qlo[c] = (4 * qd < D) ? *reinterpret_cast<const half4_t *>(&s_q[1][lane & 3][4 * qd]) : half4_t{0, 0, 0, 0};
   }
-  // per-head sum of the query operand as the MFMA sees it, for the 1152 offset fold (lanes 16h.. reduce head h)
+  // per-head sum of the query operand as the MFMA sees it, for the 1152 offset fold of INT8 groups (lanes 16h..
+  // reduce head h)
   float qsum[kGqa];
   {
     float part = 0.0f;
@@ -388,8 +402,11 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
   const uint32_t visible = min(ntok_seq, qpos + 1);  // tokens [0, visible) are attended
   const uint32_t ngroups = min((visible + 63) / 64, d.max_groups);
   const uint32_t g0 = min(ss.g0, ngroups);
-  const uint32_t per = (ngroups - g0 + splits - 1) / splits;
-  const uint32_t ga = min(ngroups, g0 + split * per), gb = min(ngroups, ga + per);
+  // splits cover whole group pairs: pairs [p0, p1) over groups [g0, ngroups)
+  const uint32_t p0 = g0 >> 1, p1 = (ngroups + 1) >> 1;
+  const uint32_t per = (p1 - p0 + splits - 1) / splits;
+  const uint32_t pa = min(p1, p0 + split * per), pb = min(p1, pa + per);
+  const uint32_t ga = max(g0, 2 * pa), gb = min(ngroups, 2 * pb);
   const uint32_t *grow = d.group_offsets + (static_cast<size_t>(seq) * d.kv_head_count + head) * d.max_groups;
 
   float m_run[kGqa], l_run[kGqa];
@@ -404,53 +421,67 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
   for (int i = 0; i < D / 16; ++i) acc_v[i] = float4_t{0, 0, 0, 0};
 
   uint32_t *buf = s_buf[__builtin_amdgcn_readfirstlane(wave)];  // uniform base: cursor arithmetic stays scalar
-  // Memory pipeline of a wavefront over its groups gi = ga + wave, +4, ...:
+  // Memory pipeline of a wavefront over its groups (see next_group):
   //   blob offset   loaded two groups ahead;
-  //   header        loaded at the start of the previous group (fields and lane states kept in registers);
+  //   header        loaded at the start of the previous group (fields and chain-start lane states kept in
+  //                 registers; the two state words are read for every group and used only by chain starts);
   //   word streams  copied into this wave's LDS buffer by global_load_lds (16 bytes per lane, 1 KiB per wave
   //                 instruction, whole 16-byte chunks: blobs are padded to 16 bytes) during the previous group's
   //                 softmax / V phase — the buffer is free once that group's decode loop has ended;
-  //   low parts     rolling prefetch: the next low-part group's 6 words per lane are always in flight (issued
-  //                 when the previous low group starts; across the group boundary for the last one).
+  //   raw words     rolling prefetch: the next sign group's 14 words per lane are always in flight (issued when the
+  //                 previous sign group starts; across the group boundary for the last one).
   // The next group's copies are awaited with s_waitcnt vmcnt(0) at the top of the loop.
   auto blob_at = [&](uint32_t g) { return d.pool + static_cast<size_t>(grow[g]) * 16; };
-  uint32_t off_next = (ga + wave + kWaves < gb) ? grow[ga + wave + kWaves] : 0u;
-  const uint8_t *blob = (ga + wave < gb) ? blob_at(ga + wave) : d.pool;
-  uint32_t h_cnt01 = 0, h_cnt23 = 0, h_tc = 0, h_codec = 0;
-  uint32_t h_st[4] = {0, 0, 0, 0};  // the group's four lane states (read for raw groups too: harmless, unused)
+  const uint32_t gfirst = (2 * (pa + wave) < gb) ? max(ga, 2 * (pa + wave)) : gb;
+  const uint32_t gsecond = gfirst < gb ? next_group(gfirst, gb) : gb;
+  uint32_t off_next = gsecond < gb ? grow[gsecond] : 0u;
+  const uint8_t *blob = gfirst < gb ? blob_at(gfirst) : d.pool;
+  uint32_t h_cnt = 0, h_chain = 0, h_tc = 0, h_codec = 0;
+  uint32_t h_st[2] = {0, 0};  // the group's chain-start lane states (read for every group: harmless, unused)
   float h_ks = 0.f, h_vs = 0.f;
-  if (ga + wave < gb) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) h_st[c] = reinterpret_cast<const uint32_t *>(blob + kHdr)[64 * c + lane];
-    h_cnt01 = *reinterpret_cast<const uint32_t *>(blob + 4);
-    h_cnt23 = *reinterpret_cast<const uint32_t *>(blob + 8);
-    h_tc = reinterpret_cast<const uint16_t *>(blob + 12)[G];
-    h_ks = reinterpret_cast<const float *>(blob + 32)[G];
-    h_vs = reinterpret_cast<const float *>(blob + 48)[G];
-    h_codec = *reinterpret_cast<const uint32_t *>(blob);
-  }
+  auto load_header = [&](const uint8_t *b) {
+    h_st[0] = reinterpret_cast<const uint32_t *>(b + kHdr)[lane];
+    h_st[1] = reinterpret_cast<const uint32_t *>(b + kHdr)[64 + lane];
+    h_cnt = *reinterpret_cast<const uint32_t *>(b + 4);
+    h_chain = *reinterpret_cast<const uint16_t *>(b + 8);
+    h_tc = reinterpret_cast<const uint16_t *>(b + 12)[G];
+    h_ks = reinterpret_cast<const float *>(b + 32)[G];
+    h_vs = reinterpret_cast<const float *>(b + 48)[G];
+    h_codec = *reinterpret_cast<const uint32_t *>(b);
+  };
+  if (gfirst < gb) load_header(blob);
+  // the raw words of a RANS group follow its header (and its states when it starts a chain); its word streams
+  // follow the raw words
+  auto raw_of = [&](const uint8_t *b, uint32_t chain) {
+    return reinterpret_cast<const uint32_t *>(b + kHdr + (chain ? kStateBytes : 0));
+  };
   constexpr int kStage16 = ((kCapWords * 2) + 1023) / 1024;  // 1 KiB copies per group
-  uint32_t pre[6] = {0, 0, 0, 0, 0, 0};
-  if (RANS && ga + wave < gb && h_codec == CF_KV_CODEC_RANS_HYBRID) {
-    {
-      const uint32_t *lw = reinterpret_cast<const uint32_t *>(blob + kHdr + kStateBytes);
-#pragma unroll
-      for (int w = 0; w < 3; ++w) {
-        pre[w] = lw[w * 64 + lane];
-        pre[3 + w] = lw[LOWS + w * 64 + lane];
-      }
-    }
-    const uint32_t nbytes = ((min(word_total(h_cnt01, h_cnt23), kCapWords) * 2u) + 15u) & ~15u;
-    const uint8_t *src = blob + kHdr + kStateBytes + 2 * LOWS * 4 + 16u * lane;  // this lane's 16-byte chunk
+  auto stage_words = [&](const uint8_t *b, uint32_t chain, uint32_t cnt) {
+    const uint32_t nbytes = ((min((cnt & 0xFFFFu) + (cnt >> 16), kCapWords) * 2u) + 15u) & ~15u;
+    const uint8_t *src = reinterpret_cast<const uint8_t *>(raw_of(b, chain) + 2 * RAW) + 16u * lane;
 #pragma unroll
     for (int k = 0; k < kStage16; ++k)
       if (1024u * k + 16u * lane < nbytes)
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t *>(src + 1024 * k),
-                                         (__attribute__((address_space(3))) void *)(buf + 256 * k), 16,
-                                         0, 0);
+                                         (__attribute__((address_space(3))) void *)(buf + 256 * k), 16, 0, 0);
+  };
+  uint32_t pre[14];
+#pragma unroll
+  for (int w = 0; w < 14; ++w) pre[w] = 0;
+  if (RANS && gfirst < gb && h_codec == CF_KV_CODEC_RANS_HYBRID) {
+    const uint32_t *lw = raw_of(blob, h_chain);
+#pragma unroll
+    for (int w = 0; w < 7; ++w) {
+      pre[w] = lw[w * 64 + lane];
+      pre[7 + w] = lw[RAW + w * 64 + lane];
+    }
+    stage_words(blob, h_chain, h_cnt);
   }
-  for (uint32_t gi = ga + wave; gi < gb; gi += kWaves) {
-    const uint32_t cnt01 = h_cnt01, cnt23 = h_cnt23, tcG = h_tc, gcodec = h_codec;  // gcodec is wave-uniform
+  uint32_t st[2] = {0, 0};     // lane states carried along a chain
+  uint32_t prev = 0xFFFFFFFFu;  // the group decoded before (a chain continues only from its own first group)
+  bool broken = false;          // a group continued a chain whose first group this wave did not decode
+  for (uint32_t gi = gfirst; gi < gb;) {
+    const uint32_t cnt = h_cnt, chain = h_chain, tcG = h_tc, gcodec = h_codec;  // gcodec, chain wave-uniform
     const float ks = h_ks, vs = h_vs;
     const uint8_t *cur = blob;
     const bool tok_ok = static_cast<uint32_t>(t) < tcG && 64 * gi + 16 * G + t < visible;
@@ -460,39 +491,37 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    const uint32_t st4[4] = {h_st[0], h_st[1], h_st[2], h_st[3]};
-    if (gi + kWaves < gb) {  // next group's header and states (its offset was loaded one group earlier)
-      blob = d.pool + static_cast<size_t>(off_next) * 16;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) h_st[c] = reinterpret_cast<const uint32_t *>(blob + kHdr)[64 * c + lane];
-      h_cnt01 = *reinterpret_cast<const uint32_t *>(blob + 4);
-      h_cnt23 = *reinterpret_cast<const uint32_t *>(blob + 8);
-      h_tc = reinterpret_cast<const uint16_t *>(blob + 12)[G];
-      h_ks = reinterpret_cast<const float *>(blob + 32)[G];
-      h_vs = reinterpret_cast<const float *>(blob + 48)[G];
-      h_codec = *reinterpret_cast<const uint32_t *>(blob);
-      off_next = (gi + 2 * kWaves < gb) ? grow[gi + 2 * kWaves] : 0u;
+    if (RANS && gcodec == CF_KV_CODEC_RANS_HYBRID) {
+      if (chain) {
+        st[0] = h_st[0];
+        st[1] = h_st[1];
+      } else {
+        broken |= prev + 1 != gi;
+      }
     }
-    const bool next_rans = RANS && gi + kWaves < gb && h_codec == CF_KV_CODEC_RANS_HYBRID;
-    const uint32_t *nlw = next_rans ? reinterpret_cast<const uint32_t *>(blob + kHdr + kStateBytes) : nullptr;
+    const uint32_t gn = next_group(gi, gb);
+    if (gn < gb) {  // next group's header and states (its offset was loaded one group earlier)
+      blob = d.pool + static_cast<size_t>(off_next) * 16;
+      load_header(blob);
+      const uint32_t gnn = next_group(gn, gb);
+      off_next = gnn < gb ? grow[gnn] : 0u;
+    }
+    const bool next_rans = RANS && gn < gb && h_codec == CF_KV_CODEC_RANS_HYBRID;
+    const uint32_t *nlw = next_rans ? raw_of(blob, h_chain) : nullptr;
     auto stage_next = [&]() {  // next group's word streams, straight into LDS (no VGPRs)
-      if (!next_rans) return;
-      const uint32_t nbytes = ((min(word_total(h_cnt01, h_cnt23), kCapWords) * 2u) + 15u) & ~15u;
-      const uint8_t *src = blob + kHdr + kStateBytes + 2 * LOWS * 4 + 16u * lane;
-#pragma unroll
-      for (int k = 0; k < kStage16; ++k)
-        if (1024u * k + 16u * lane < nbytes)
-          __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t *>(src + 1024 * k),
-                                           (__attribute__((address_space(3))) void *)(buf + 256 * k),
-                                           16, 0, 0);
+      if (next_rans) stage_words(blob, h_chain, h_cnt);
     };
     if (RANS && gcodec == CF_KV_CODEC_RANS_HYBRID) {
-      group_body<D, CF_KV_CODEC_RANS_HYBRID>(stage_next, pre, nlw, st4, cur, reinterpret_cast<const uint16_t *>(buf), cnt01, cnt23, s_tab, qhi,
-                                             qlo, qsum, s_p[wave], lane, tok_ok, ks, vs, e_run, m_run, l_run, acc_v);
-    } else {  // raw int8 group (the INT8 codec, or the raw fallback of a high-entropy group)
-      group_body<D, CF_KV_CODEC_INT8>(stage_next, pre, nlw, st4, cur, static_cast<const uint16_t *>(nullptr), 0, 0, s_tab, qhi, qlo,
-                                      qsum, s_p[wave], lane, tok_ok, ks, vs, e_run, m_run, l_run, acc_v);
+      group_body<D, CF_KV_CODEC_RANS_HYBRID>(stage_next, pre, nlw, st, raw_of(cur, chain),
+                                             reinterpret_cast<const uint16_t *>(buf), cnt, s_tab, qhi, qlo, qsum,
+                                             s_p[wave], lane, tok_ok, ks, vs, e_run, m_run, l_run, acc_v);
+    } else {  // raw int8 group (the INT8 codec, or the raw fallback of a group holding -128)
+      group_body<D, CF_KV_CODEC_INT8>(stage_next, pre, nlw, st, reinterpret_cast<const uint32_t *>(cur + kHdr),
+                                      static_cast<const uint16_t *>(nullptr), 0, s_tab, qhi, qlo, qsum, s_p[wave],
+                                      lane, tok_ok, ks, vs, e_run, m_run, l_run, acc_v);
     }
+    prev = gi;
+    gi = gn;
   }
 
   // ---- reduce the wavefront: sum the 4 page groups (lanes t, t+16, t+32, t+48) after taking each lane's P.V sums
@@ -510,7 +539,7 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
   for (int h = 0; h < kGqa; ++h)
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) l_run[h] += __shfl_xor(l_run[h], o);
-  // wave partial -> the wave's LDS buffer: [h][D] acc, then m, l
+  // wave partial -> the wave's LDS buffer: [h][D] acc, then m, l (m NaN for a broken chain: the output shows it)
   float *red = reinterpret_cast<float *>(buf);
   if (lane < 16) {
 #pragma unroll
@@ -519,7 +548,7 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
       for (int h = 0; h < kGqa; ++h) red[h * (D + 2) + t + 16 * i] = acc_v[i][h];
   }
   if (lane < kGqa) {
-    red[lane * (D + 2) + D] = m_run[lane];
+    red[lane * (D + 2) + D] = broken ? __builtin_nanf("") : m_run[lane];
     red[lane * (D + 2) + D + 1] = l_run[lane];
   }
   __syncthreads();
@@ -528,20 +557,27 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
   for (int i = threadIdx.x; i < kGqa * D; i += kThreads) {
     const int h = i / D, dd = i % D;
     float m = -INFINITY;
-    for (int w = 0; w < kWaves; ++w) m = fmaxf(m, reinterpret_cast<const float *>(s_buf[w])[h * (D + 2) + D]);
+    bool nan = false;
+    for (int w = 0; w < kWaves; ++w) {
+      const float mw = reinterpret_cast<const float *>(s_buf[w])[h * (D + 2) + D];
+      nan |= mw != mw;
+      m = fmaxf(m, mw);
+    }
     float l = 0.0f, o = 0.0f;
     if (m != -INFINITY)
       for (int w = 0; w < kWaves; ++w) {
         const float *rw = reinterpret_cast<const float *>(s_buf[w]);
         const float mw = rw[h * (D + 2) + D];
-        if (mw == -INFINITY) continue;
+        if (mw == -INFINITY || mw != mw) continue;
         const float sc = __expf(mw - m);
         l += rw[h * (D + 2) + D + 1] * sc;
         o += rw[h * (D + 2) + dd] * sc;
       }
+    if (nan) m = __builtin_nanf("");
     if (ss.slots == 1) {
       if (static_cast<uint32_t>(h) < gqa)
-        d.output[(static_cast<size_t>(seq) * d.query_head_count + head * gqa + h) * D + dd] = l > 0.0f ? o / l : 0.0f;
+        d.output[(static_cast<size_t>(seq) * d.query_head_count + head * gqa + h) * D + dd] =
+            nan ? m : l > 0.0f ? o / l : 0.0f;
     } else {
       float *pp = partial + ((static_cast<size_t>(seq) * d.kv_head_count + head) * ss.slots + ss.slot0 + split) *
                                 (kGqa * (D + 2));

@@ -1,20 +1,23 @@
 // kv_encode.hip — device-side sealing: quantise and entropy-code KV page groups on the GPU.
 //
 // The device twin of the host encoder cf_kv_encode_groups (kv_codec.cpp): same group blob format
-// (kv_codec_ext.h), same pool packing and offsets, byte for byte. It replaces the host quantise + encode step of
-// the append path (reference src/runtime/compressed_kv_cache.cu:89-109 seals pages on the host), so K/V that the
-// model produced in HBM never leave the device. Three launches on the caller's stream, nothing allocated:
+// (kv_codec_ext.h), same chain pairs, same pool packing and offsets, byte for byte. It replaces the host quantise +
+// encode step of the append path (reference src/runtime/compressed_kv_cache.cu:89-109 seals pages on the host), so
+// K/V that the model produced in HBM never leave the device. Three launches on the caller's stream, nothing
+// allocated:
 //   1. table_prep_kernel: one workgroup per table blob derives the compact (freq, cum) pairs of its 256 joint
 //      symbols (last slot with offset 0 wins, exactly the host loader's rule) and whether the table is usable;
 //      workgroup 0 also clears the status word.
-//   2. encode_kernel: one 4-wavefront workgroup per group. Phase 1: wavefront G quantises page G (absmax over the
-//      page's present tokens, IEEE division, round half to even) into LDS symbol tiles laid out for phase 2's
-//      reads (K token-major, V dim-major, both padded to odd word strides). Phase 2: each wavefront rANS-codes one
-//      of the four chains (K A, K B, V A, V B; 64 interleaved states each); the renormalisation words of one step
-//      are placed with a ballot prefix count, written from the top of an LDS buffer down so that the reversed
-//      stream needs no second pass. Phase 3 bit-slices the low parts and writes the blob (or the INT8 fallback when
-//      the words exceed CF_KV_RANS_MAX_GROUP_WORDS) into a fixed-capacity staging slot, and its size in 16-byte
-//      units.
+//   2. encode_kernel: one 4-wavefront workgroup per chain unit (a group alone, or a group and the group that
+//      continues its chain; the workgroup of a continuing group only checks its flag). Phase 1: wavefront G
+//      quantises page G of each group of the unit (absmax over the page's present tokens, IEEE division, round half
+//      to even) into LDS symbol tiles laid out for the later reads (K token-major, V dim-major, both padded to odd
+//      word strides). Phase 2: wavefronts 0 and 1 rANS-code the K and V chains across the unit's coded groups in
+//      reverse (64 interleaved states each); the renormalisation words of one step are placed with a ballot prefix
+//      count, written from the top of an LDS buffer down so that the reversed stream needs no second pass. At the
+//      same time wavefronts 2 and 3 write the K and V raw words (frame-rotated nibbles, crumbs and signs). Phase 3
+//      writes the headers and word streams (or the INT8 blob of a group holding -128) into fixed-capacity staging
+//      slots, and each blob's size in 16-byte units.
 //   3. an exclusive scan of the sizes (hipcub), then pack_kernel copies every blob to pool[pool_at + offset],
 //      writes offsets_out and *pool_end — or nothing at all when any group or the pool capacity failed, in which
 //      case the status word holds CF_ERR_INVALID_ARGUMENT.
@@ -29,15 +32,21 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr uint32_t kHeader = 64;
+constexpr uint32_t kStateBytes = 2 * 64 * 4;
 constexpr uint32_t kMaxDim = CF_KV_MAX_HEAD_DIM;
-constexpr uint32_t kChainCap = CF_KV_RANS_MAX_GROUP_WORDS / 2;  // per chain: D/8 quads x 64 lanes <= 1024 words
+constexpr uint32_t kStreamCap = CF_KV_RANS_MAX_GROUP_WORDS / 2;  // per stream and group: 64 lanes x D/8 steps
 constexpr int kKStride = kMaxDim / 4 + 1;              // words per K token row (odd: conflict-free lane reads)
 constexpr int kVStride = 5;                            // words per V dim row (4 token quads + 1)
 constexpr uint32_t kTableBytes = CF_KV_RANS_TABLE_BYTES;
+constexpr uint32_t kFrame[8] = {0, 4, 2, 6, 1, 5, 3, 7};  // frame of quad k of a sign group
+constexpr uint32_t kNWord[8] = {0, 0, 1, 1, 3, 3, 4, 4};  // raw word holding quad k's nibbles (N0 N1 C0 N2 N3 C1 S)
 
 __host__ __device__ inline uint64_t align16(uint64_t v) { return (v + 15) & ~uint64_t(15); }
 
-bool dim_ok(uint32_t d) { return d != 0 && d % 16 == 0 && d <= kMaxDim; }
+bool dim_ok(uint32_t codec, uint32_t d) {
+  if (d == 0 || d > kMaxDim) return false;
+  return codec == CF_KV_CODEC_RANS_HYBRID ? d % 32 == 0 : d % 16 == 0;
+}
 
 uint64_t stage_cap(uint32_t codec, uint32_t head_dim) {
   return align16(cf_kv_group_blob_max_bytes(codec, head_dim));
@@ -56,6 +65,8 @@ __device__ __forceinline__ float wave_max(float m) {
   for (int o = 32; o >= 1; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o));
   return m;
 }
+
+__device__ __forceinline__ uint32_t rotl(uint32_t v, uint32_t r) { return r ? (v << r) | (v >> (32 - r)) : v; }
 
 // ------------------------------------------------------------------------------------------------ 1. tables
 __global__ void __launch_bounds__(256) table_prep_kernel(const uint8_t *__restrict__ tables, uint32_t table_count,
@@ -93,7 +104,9 @@ struct EncodeArgs {
   const float *keys, *values;
   const uint64_t *first_page;
   const uint32_t *page_counts, *token_counts, *heads;
+  const uint8_t *continues;
   const uint32_t *ctab, *tvalid;
+  uint64_t ngroups;
   uint32_t table_count;
   uint32_t codec, head_dim;
   uint8_t *stage;
@@ -101,7 +114,7 @@ struct EncodeArgs {
   uint32_t *units, *status;
 };
 
-// Symbol word (4 symbols, symbol i in byte i) of lane (G, t), quad q, in the lane order of kv_codec_ext.h.
+// Symbol word (4 symbols q + 128, symbol i in byte i) of lane (G, t), quad q, in the lane order of kv_codec_ext.h.
 __device__ __forceinline__ uint32_t k_word(const uint32_t *kS, int G, int t, int q) {
   return kS[(G * 16 + t) * kKStride + q];
 }
@@ -109,31 +122,50 @@ __device__ __forceinline__ uint32_t v_word(const uint32_t *vT, int G, int t, int
   return vT[(G * kMaxDim + t + 16 * (q % ng)) * kVStride + q / ng];
 }
 
-__device__ __forceinline__ uint32_t joint_of(uint32_t w) {
-  return ((w >> 6) & 3u) | ((w >> 12) & 0xCu) | ((w >> 18) & 0x30u) | ((w >> 24) & 0xC0u);
+// big bits (|q| >= 64: symbol >= 192 or <= 64) of the 4 symbols of a word, bit i for symbol i
+__device__ __forceinline__ uint32_t bigs_of(uint32_t w) {
+  uint32_t j = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t b = (w >> (8 * i)) & 255u;
+    j |= (b >= 192u || b <= 64u ? 1u : 0u) << i;
+  }
+  return j;
 }
 
 __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
-  __shared__ uint32_t kS[4 * 16 * kKStride];
-  __shared__ uint32_t vT[4 * kMaxDim * kVStride];
-  __shared__ uint16_t s_words[4][kChainCap];
+  __shared__ uint32_t kS[2][4 * 16 * kKStride];
+  __shared__ uint32_t vT[2][4 * kMaxDim * kVStride];
+  __shared__ uint16_t s_words[2][2][kStreamCap];  // [stream][group of the unit]
   __shared__ uint32_t s_tab[2][256];
-  __shared__ float s_scale[2][4];
-  __shared__ uint32_t s_tc[4], s_count[4], s_bad;
+  __shared__ float s_scale[2][2][4];               // [group][K, V][page]
+  __shared__ uint32_t s_tc[2][4], s_count[2][2], s_bad, s_minus[2];
 
   const uint64_t g = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t D = a.head_dim, nq = D / 4, ng = D / 16;
-  const uint32_t pc = a.page_counts[g];
-  const uint64_t p0 = a.first_page[g];
-  const uint32_t head = a.heads ? a.heads[g] : 0u;
   const bool rans = a.codec == CF_KV_CODEC_RANS_HYBRID;
+  const uint32_t head = a.heads ? a.heads[g] : 0u;
+  if (a.continues && a.continues[g]) {  // the group before this one codes it: only check that it may
+    if (tid == 0 && (g == 0 || a.continues[g - 1] || (a.heads && a.heads[g - 1] != head))) {
+      *a.status = CF_ERR_INVALID_ARGUMENT;
+      a.units[g] = 0;
+    }
+    return;
+  }
+  const uint32_t ngu = (a.continues && g + 1 < a.ngroups && a.continues[g + 1]) ? 2u : 1u;  // groups of the unit
   if (tid == 0) {
-    uint32_t bad = (pc == 0 || pc > 4) ? 1u : 0u;
-    for (int G = 0; G < 4; ++G) {
-      const uint32_t tc = static_cast<uint32_t>(G) < pc ? (a.token_counts ? a.token_counts[p0 + G] : 16u) : 0u;
-      if (static_cast<uint32_t>(G) < pc && (tc == 0 || tc > 16)) bad = 1;
-      s_tc[G] = bad ? 0u : tc;
+    uint32_t bad = 0;
+    for (uint32_t X = 0; X < ngu; ++X) {
+      const uint32_t pc = a.page_counts[g + X];
+      const uint64_t p0 = a.first_page[g + X];
+      if (pc == 0 || pc > 4) bad = 1;
+      for (int G = 0; G < 4; ++G) {
+        const uint32_t tc = static_cast<uint32_t>(G) < pc ? (a.token_counts ? a.token_counts[p0 + G] : 16u) : 0u;
+        if (static_cast<uint32_t>(G) < pc && (tc == 0 || tc > 16)) bad = 1;
+        s_tc[X][G] = bad ? 0u : tc;
+      }
+      s_minus[X] = 0;
     }
     if (rans && (2ull * head + 1 >= a.table_count || !a.tvalid[2 * head] || !a.tvalid[2 * head + 1])) bad = 1;
     s_bad = bad;
@@ -142,7 +174,7 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
   if (s_bad) {
     if (tid == 0) {
       *a.status = CF_ERR_INVALID_ARGUMENT;
-      a.units[g] = 0;
+      for (uint32_t X = 0; X < ngu; ++X) a.units[g + X] = 0;
     }
     return;
   }
@@ -151,13 +183,15 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
       s_tab[i >> 8][i & 255] = a.ctab[(2ull * head + (i >> 8)) * 256 + (i & 255)];
   }
 
-  // ---- phase 1: wavefront G quantises page G of K and V
-  {
+  // ---- phase 1: wavefront G quantises page G of K and V of every group of the unit
+  for (uint32_t X = 0; X < ngu; ++X) {
     const int G = wave;
-    const uint32_t tc = s_tc[G];
+    const uint32_t tc = s_tc[X][G];
     const uint64_t page_vals = 16ull * D;
+    const uint64_t p0 = a.first_page[g + X];
     const float *kp = a.keys + (p0 + G) * page_vals;
     const float *vp = a.values + (p0 + G) * page_vals;
+    bool minus = false;  // a symbol 0 (q = -128) among the present tokens
     // K: float4 index i = r * 64 + lane -> token i / nq, quad i % nq (4 * D float4 per page, <= 8 per lane)
     float4 kx[8];
     float m = 0.0f;
@@ -181,9 +215,13 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
       if (i < 4 * D) {
         const uint32_t t = i / nq, q = i % nq;
         uint32_t w = 0x80808080u;
-        if (t < tc)
-          w = quant8(kx[r].x, ks) | quant8(kx[r].y, ks) << 8 | quant8(kx[r].z, ks) << 16 | quant8(kx[r].w, ks) << 24;
-        kS[(G * 16 + t) * kKStride + q] = w;
+        if (t < tc) {
+          const uint32_t b0 = quant8(kx[r].x, ks), b1 = quant8(kx[r].y, ks), b2 = quant8(kx[r].z, ks),
+                         b3 = quant8(kx[r].w, ks);
+          minus |= b0 == 0 || b1 == 0 || b2 == 0 || b3 == 0;
+          w = b0 | b1 << 8 | b2 << 16 | b3 << 24;
+        }
+        kS[X][(G * 16 + t) * kKStride + q] = w;
       }
     }
     // V: lane owns dims d = lane, lane + 64; 16 tokens each, packed as 4 token quads
@@ -213,113 +251,135 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const uint32_t t = 4 * tq + i;
-            w |= (t < tc ? quant8(vx[r][t], vs) : 128u) << (8 * i);
+            const uint32_t b = t < tc ? quant8(vx[r][t], vs) : 128u;
+            minus |= b == 0;
+            w |= b << (8 * i);
           }
-          vT[(G * kMaxDim + d) * kVStride + tq] = w;
+          vT[X][(G * kMaxDim + d) * kVStride + tq] = w;
         }
       }
     }
+    if (__ballot(minus) != 0 && lane == 0) atomicOr(&s_minus[X], 1u);
     if (lane == 0) {
-      s_scale[0][G] = tc ? ks : 1.0f;
-      s_scale[1][G] = tc ? vs : 1.0f;
+      s_scale[X][0][G] = tc ? ks : 1.0f;
+      s_scale[X][1][G] = tc ? vs : 1.0f;
     }
   }
   __syncthreads();
 
-  uint8_t *blob = a.stage + g * a.cap;
+  // the unit's coded groups, in chain order (a group holding -128 is stored INT8 instead)
+  uint32_t list[2], nlist = 0;
+  for (uint32_t X = 0; X < ngu; ++X)
+    if (rans && !s_minus[X]) list[nlist++] = X;
+  const uint32_t sgroups = D / 32, raw_words = 7 * sgroups * 64;
+  auto blob_of = [&](uint32_t X) { return a.stage + (g + X) * a.cap; };
+  auto raw_at = [&](uint32_t X) { return kHeader + (nlist && X == list[0] ? kStateBytes : 0u); };
   const int G = lane >> 4, t = lane & 15;
-  // ---- phase 2: rANS, one chain per wavefront: wave w codes stream w / 2 (K, V), chain w % 2 (its quads
-  // q = chain, chain + 2, ..., encoded in reverse)
-  if (rans) {
-    const int s = wave >> 1, ch = wave & 1;
+  if (wave < 2 && nlist) {
+    // ---- phase 2: rANS of stream `wave` over the chain, encoded in reverse (last group, last step first)
+    const int s = wave;
     uint32_t x = 1u << 16;
-    uint32_t base = 0;
-    for (int q = static_cast<int>(nq) - 2 + ch; q >= 0; q -= 2) {
-      const uint32_t w = s == 0 ? k_word(kS, G, t, q) : v_word(vT, G, t, q, ng);
-      const uint32_t e = s_tab[s][joint_of(w)];
-      const uint32_t f = e & 0xFFFFu, cum = e >> 16;
-      const bool emit = static_cast<uint64_t>(x) >= (static_cast<uint64_t>(f) << 21);  // (2^16 >> 11) << 16 = 2^21
-      const uint64_t mask = __ballot(emit);
-      if (emit) {
-        const uint32_t above = __popcll(mask & ~((2ull << lane) - 1ull));  // emitters at higher lanes go first
-        s_words[wave][kChainCap - 1 - (base + above)] = static_cast<uint16_t>(x & 0xFFFFu);
-        x >>= 16;
+    for (int li = static_cast<int>(nlist) - 1; li >= 0; --li) {
+      const uint32_t X = list[li];
+      uint32_t base = 0;
+      for (int p = static_cast<int>(D / 8) - 1; p >= 0; --p) {
+        const uint32_t w0 = s == 0 ? k_word(kS[X], G, t, 2 * p) : v_word(vT[X], G, t, 2 * p, ng);
+        const uint32_t w1 = s == 0 ? k_word(kS[X], G, t, 2 * p + 1) : v_word(vT[X], G, t, 2 * p + 1, ng);
+        const uint32_t e = s_tab[s][bigs_of(w0) | bigs_of(w1) << 4];
+        const uint32_t f = e & 0xFFFFu, cum = e >> 16;
+        const bool emit = static_cast<uint64_t>(x) >= (static_cast<uint64_t>(f) << 21);  // (2^16 >> 11) << 16
+        const uint64_t mask = __ballot(emit);
+        if (emit) {
+          const uint32_t above = __popcll(mask & ~((2ull << lane) - 1ull));  // emitters at higher lanes go first
+          s_words[s][X][kStreamCap - 1 - (base + above)] = static_cast<uint16_t>(x & 0xFFFFu);
+          x >>= 16;
+        }
+        base += __popcll(mask);
+        x = ((x / f) << CF_KV_RANS_PROB_BITS) + (x % f) + cum;
       }
-      base += __popcll(mask);
-      x = ((x / f) << CF_KV_RANS_PROB_BITS) + (x % f) + cum;
+      if (lane == 0) s_count[s][X] = base;
     }
-    *reinterpret_cast<uint32_t *>(blob + kHeader + 4 * (wave * 64 + lane)) = x;
-    if (lane == 0) s_count[wave] = base;
+    *reinterpret_cast<uint32_t *>(blob_of(list[0]) + kHeader + 4 * (s * 64 + lane)) = x;
+  } else if (wave >= 2) {
+    // ---- raw words of stream wave - 2 for every coded group: nibbles, crumbs and signs in their quads' frames
+    const int s = wave - 2;
+    for (uint32_t li = 0; li < nlist; ++li) {
+      const uint32_t X = list[li];
+      uint32_t *out = reinterpret_cast<uint32_t *>(blob_of(X) + raw_at(X)) + s * raw_words;
+      for (uint32_t sg = 0; sg < sgroups; ++sg) {
+        uint32_t wd[7] = {0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int q = 8 * sg + k;
+          const uint32_t w = s == 0 ? k_word(kS[X], G, t, q) : v_word(vT[X], G, t, q, ng);
+          uint32_t nib = 0, cr = 0, sn = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t b = (w >> (8 * i)) & 255u;
+            const uint32_t mag = b >= 128u ? b - 128u : 128u - b;
+            nib |= (mag & 15u) << (8 * i);
+            cr |= ((mag >> 4) & 3u) << (8 * i + 4);
+            sn |= (b < 128u ? 1u : 0u) << (8 * i + 7);
+          }
+          wd[kNWord[k]] |= rotl(nib, kFrame[k]);
+          wd[k < 4 ? 2 : 5] |= rotl(cr, kFrame[k]);
+          wd[6] |= rotl(sn, kFrame[k]);
+        }
+#pragma unroll
+        for (int w = 0; w < 7; ++w) out[(7 * sg + w) * 64 + lane] = wd[w];
+      }
+    }
   }
   __syncthreads();
 
-  // ---- phase 3: the blob
-  uint32_t wc[4] = {0, 0, 0, 0};
-  if (rans)
-    for (int c = 0; c < 4; ++c) wc[c] = s_count[c];
-  const uint32_t total = wc[0] + wc[1] + wc[2] + wc[3];
-  const uint32_t nlow = 3 * ng * 64;
-  const uint64_t wat = kHeader + 4 * 64 * 4 + 2ull * nlow * 4;  // first rANS word of the blob
-  // (the second bound never binds: the first one caps the words and the capacity covers it; it keeps the staging
-  // slot safe by construction)
-  const bool raw = !rans || total > CF_KV_RANS_MAX_GROUP_WORDS || wat + 2ull * total > a.cap;
-  uint64_t size;
-  if (raw) {
-    // INT8: word (q * 64 + L) of stream s = the 4 symbols of quad q of lane L
-    uint32_t *out = reinterpret_cast<uint32_t *>(blob + kHeader);
-    for (uint32_t i = tid; i < 2 * nq * 64; i += kThreads) {
-      const uint32_t s = i / (nq * 64), r = i % (nq * 64), q = r / 64, L = r % 64;
-      out[i] = s == 0 ? k_word(kS, L >> 4, L & 15, q) : v_word(vT, L >> 4, L & 15, q, ng);
-    }
-    size = kHeader + 2ull * nq * 64 * 4;
-  } else {
-    if (wave < 2) {  // bit-sliced low parts of stream `wave`
-      const int s = wave;
-      uint32_t *lo = reinterpret_cast<uint32_t *>(blob + kHeader + 4 * 64 * 4) + s * nlow;
-      for (uint32_t gi = 0; gi < ng; ++gi) {
-        uint32_t n0 = 0, n1 = 0, c = 0;
-#pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          const int q = 4 * gi + qd;
-          const uint32_t w = s == 0 ? k_word(kS, G, t, q) : v_word(vT, G, t, q, ng);
-          const uint32_t nib = (w & 0x0F0F0F0Fu) << (4 * (qd & 1));
-          if (qd < 2) n0 |= nib; else n1 |= nib;
-          c |= ((w >> 4) & 0x03030303u) << (2 * qd);
-        }
-        lo[(gi * 3 + 0) * 64 + lane] = n0;
-        lo[(gi * 3 + 1) * 64 + lane] = n1;
-        lo[(gi * 3 + 2) * 64 + lane] = c;
+  // ---- phase 3: word streams and headers of the coded groups, INT8 blobs of the others
+  for (uint32_t X = 0; X < ngu; ++X) {
+    uint8_t *blob = blob_of(X);
+    const bool coded = rans && !s_minus[X];
+    uint64_t size;
+    uint32_t wc[2] = {0, 0};
+    if (!coded) {
+      // INT8: word (q * 64 + L) of stream s = the 4 symbols of quad q of lane L
+      uint32_t *out = reinterpret_cast<uint32_t *>(blob + kHeader);
+      for (uint32_t i = tid; i < 2 * nq * 64; i += kThreads) {
+        const uint32_t s = i / (nq * 64), r = i % (nq * 64), q = r / 64, L = r % 64;
+        out[i] = s == 0 ? k_word(kS[X], L >> 4, L & 15, q) : v_word(vT[X], L >> 4, L & 15, q, ng);
       }
+      size = kHeader + 2ull * nq * 64 * 4;
+    } else {
+      wc[0] = s_count[0][X];
+      wc[1] = s_count[1][X];
+      const uint64_t wat = raw_at(X) + 2ull * raw_words * 4;  // first rANS word of the blob
+      uint16_t *wo = reinterpret_cast<uint16_t *>(blob + wat);  // K stream, then V
+      for (uint32_t i = tid; i < wc[0] + wc[1]; i += kThreads) {
+        const uint32_t s = i < wc[0] ? 0u : 1u, at = i - (s ? wc[0] : 0u);
+        wo[i] = s_words[s][X][kStreamCap - wc[s] + at];
+      }
+      const uint64_t end = wat + 2ull * (wc[0] + wc[1]);
+      size = align16(end);
+      for (uint64_t b = end + tid; b < size; b += kThreads) blob[b] = 0;
     }
-    uint16_t *wo = reinterpret_cast<uint16_t *>(blob + wat);  // streams K A, K B, V A, V B back to back
-    const uint32_t o1 = wc[0], o2 = o1 + wc[1], o3 = o2 + wc[2];
-    for (uint32_t i = tid; i < total; i += kThreads) {
-      const uint32_t c = i < o1 ? 0u : i < o2 ? 1u : i < o3 ? 2u : 3u;
-      const uint32_t at = i - (c == 0 ? 0u : c == 1 ? o1 : c == 2 ? o2 : o3);
-      wo[i] = s_words[c][kChainCap - wc[c] + at];
-    }
-    const uint64_t end = wat + 2ull * total;
-    size = align16(end);
-    for (uint64_t b = end + tid; b < size; b += kThreads) blob[b] = 0;
-  }
-  if (tid == 0) {
-    cf_kv_group_header h{};
-    h.codec = raw ? CF_KV_CODEC_INT8 : CF_KV_CODEC_RANS_HYBRID;
-    for (int c = 0; c < 4; ++c) h.word_count[c] = static_cast<uint16_t>(raw ? 0 : wc[c]);
-    for (int i = 0; i < 4; ++i) {
-      h.token_count[i] = static_cast<uint16_t>(s_tc[i]);
-      h.k_scale[i] = s_scale[0][i];
-      h.v_scale[i] = s_scale[1][i];
-    }
-    h.head_dim = static_cast<uint16_t>(D);
-    h.page_count = static_cast<uint16_t>(pc);
-    h.k_table = 2 * head;
-    h.v_table = 2 * head + 1;
-    const uint32_t *src = reinterpret_cast<const uint32_t *>(&h);
-    uint32_t *dst = reinterpret_cast<uint32_t *>(blob);
+    if (tid == 0) {
+      cf_kv_group_header h{};
+      h.codec = coded ? CF_KV_CODEC_RANS_HYBRID : CF_KV_CODEC_INT8;
+      h.word_count[0] = static_cast<uint16_t>(wc[0]);
+      h.word_count[1] = static_cast<uint16_t>(wc[1]);
+      h.chain = static_cast<uint16_t>(coded && X == list[0] ? 1 : 0);
+      for (int i = 0; i < 4; ++i) {
+        h.token_count[i] = static_cast<uint16_t>(s_tc[X][i]);
+        h.k_scale[i] = s_scale[X][0][i];
+        h.v_scale[i] = s_scale[X][1][i];
+      }
+      h.head_dim = static_cast<uint16_t>(D);
+      h.page_count = static_cast<uint16_t>(a.page_counts[g + X]);
+      h.k_table = 2 * head;
+      h.v_table = 2 * head + 1;
+      const uint32_t *src = reinterpret_cast<const uint32_t *>(&h);
+      uint32_t *dst = reinterpret_cast<uint32_t *>(blob);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) dst[i] = src[i];
-    a.units[g] = static_cast<uint32_t>(size / 16);
+      for (int i = 0; i < 16; ++i) dst[i] = src[i];
+      a.units[g + X] = static_cast<uint32_t>(size / 16);
+    }
   }
 }
 
@@ -380,8 +440,8 @@ Layout layout_of(uint32_t codec, uint32_t head_dim, uint64_t ngroups, uint32_t t
 
 extern "C" uint64_t cf_kv_encode_groups_workspace_bytes(uint32_t codec, uint32_t head_dim, uint64_t ngroups,
                                                         uint32_t table_count) {
-  if (!dim_ok(head_dim) || ngroups == 0 || ngroups >= (1ull << 31)) return 0;
   if (codec != CF_KV_CODEC_INT8 && codec != CF_KV_CODEC_RANS_HYBRID) return 0;
+  if (!dim_ok(codec, head_dim) || ngroups == 0 || ngroups >= (1ull << 31)) return 0;
   return layout_of(codec, head_dim, ngroups, codec == CF_KV_CODEC_RANS_HYBRID ? table_count : 0).total;
 }
 
@@ -389,7 +449,8 @@ extern "C" cf_status cf_kv_encode_groups_async(uint32_t codec, const float *keys
                                                uint64_t ngroups, const uint64_t *first_page,
                                                const uint32_t *page_counts, const uint32_t *token_counts,
                                                uint32_t head_dim, const uint8_t *tables, uint32_t table_count,
-                                               const uint32_t *heads, uint8_t *pool, uint64_t pool_capacity,
+                                               const uint32_t *heads, const uint8_t *continues, uint8_t *pool,
+                                               uint64_t pool_capacity,
                                                uint64_t pool_at, uint32_t *offsets_out, uint64_t *pool_end,
                                                uint32_t *status, void *workspace, uint64_t workspace_bytes,
                                                void *stream) {
@@ -399,7 +460,7 @@ extern "C" cf_status cf_kv_encode_groups_async(uint32_t codec, const float *keys
       reinterpret_cast<uintptr_t>(pool) % 16 != 0)
     return CF_ERR_INVALID_ARGUMENT;
   if (codec != CF_KV_CODEC_INT8 && codec != CF_KV_CODEC_RANS_HYBRID) return CF_ERR_UNSUPPORTED;
-  if (!dim_ok(head_dim)) return CF_ERR_UNSUPPORTED;
+  if (!dim_ok(codec, head_dim)) return CF_ERR_UNSUPPORTED;
   const bool rans = codec == CF_KV_CODEC_RANS_HYBRID;
   if (rans && (!tables || table_count < 2)) return CF_ERR_INVALID_ARGUMENT;
   if (!rans) table_count = 0;
@@ -416,8 +477,8 @@ extern "C" cf_status cf_kv_encode_groups_async(uint32_t codec, const float *keys
   table_prep_kernel<<<table_count ? table_count : 1, 256, 0, st>>>(tables, table_count, ctab, tvalid, status, units,
                                                                    ngroups);
   if (cfd::launch_status() != CF_OK) return CF_ERR_CUDA;
-  EncodeArgs a{keys, values, first_page, page_counts, token_counts, heads, ctab, tvalid, table_count, codec,
-               head_dim, ws + L.stage, L.cap, units, status};
+  EncodeArgs a{keys, values, first_page, page_counts, token_counts, heads, continues, ctab, tvalid, ngroups,
+               table_count, codec, head_dim, ws + L.stage, L.cap, units, status};
   encode_kernel<<<static_cast<unsigned>(ngroups), kThreads, 0, st>>>(a);
   if (cfd::launch_status() != CF_OK) return CF_ERR_CUDA;
   size_t scan_bytes = L.scan_bytes;

@@ -22,7 +22,7 @@ from . import _abi as A
 CODEC_INT8, CODEC_RANS_HYBRID = 1, 2
 PAGE_TOKENS = 16
 TABLE_BYTES = 16384
-EXT_ABI_VERSION = 3
+EXT_ABI_VERSION = 4
 GROUP_PAGES = 4
 GROUP_TOKENS = PAGE_TOKENS * GROUP_PAGES
 
@@ -35,8 +35,8 @@ class cf_kv_batched_desc(C.Structure):
                 ("workspace", A.P), ("workspace_bytes", A.U64)]
 
 
-A.declare("cf_kv_encode_groups", A.I32, [A.U32, A.P, A.P, A.U64, A.P, A.P, A.P, A.U32, A.P, A.P, A.P, A.U64, A.U64,
-                                         A.P, A.P, A.U32])
+A.declare("cf_kv_encode_groups", A.I32, [A.U32, A.P, A.P, A.U64, A.P, A.P, A.P, A.U32, A.P, A.P, A.P, A.P, A.U64,
+                                         A.U64, A.P, A.P, A.U32])
 A.declare("cf_kv_encode_group", A.I32, [A.U32, A.P, A.P, A.U32, A.P, A.U32, A.P, A.P, A.U32, A.U32, A.P, A.U64, A.P])
 A.declare("cf_kv_rans_build_table", A.I32, [A.P, A.P])
 A.declare("cf_kv_rans_page_histogram", A.I32, [A.P, A.U32, A.U32, A.P])
@@ -48,15 +48,23 @@ A.declare("cf_kv_cascade_workspace_bytes", A.U64, [A.P, A.U32])
 A.declare("cf_kv_paged_attention_cascade_async", A.I32, [A.P, A.U32, A.P])
 A.declare("cf_kv_encode_groups_workspace_bytes", A.U64, [A.U32, A.U32, A.U64, A.U32])
 A.declare("cf_kv_encode_groups_async", A.I32, [A.U32, A.P, A.P, A.U64, A.P, A.P, A.P, A.U32, A.P, A.U32, A.P, A.P,
-                                               A.U64, A.U64, A.P, A.P, A.P, A.P, A.U64, A.P])
+                                               A.P, A.U64, A.U64, A.P, A.P, A.P, A.P, A.U64, A.P])
 
 
 def _np_ptr(a: np.ndarray | None):
     return None if a is None else a.ctypes.data_as(C.c_void_p)
 
 
+def pair_flags(group_index: np.ndarray, first_coded: int = 0) -> np.ndarray:
+    """`continues` flags for groups listed in token order with absolute group indices `group_index` (one sequence and
+    head): an odd group continues the chain of the even group before it when that group is in the list and coded
+    (index >= first_coded)."""
+    g = np.asarray(group_index, np.int64)
+    return ((g % 2 == 1) & (g - 1 >= max(first_coded, int(g.min()) if g.size else 0))).astype(np.uint8)
+
+
 def build_table(pages: np.ndarray) -> np.ndarray:
-    """Table blob from the joint high-part histogram of sample pages [n, tokens<=16, D] (fp32)."""
+    """Table blob from the joint big-bit histogram of sample pages [n, tokens<=16, D] (fp32)."""
     L = A.lib()
     pages = np.ascontiguousarray(pages, np.float32)
     hist = np.zeros(256, np.uint64)
@@ -69,8 +77,10 @@ def build_table(pages: np.ndarray) -> np.ndarray:
 
 def encode_groups(codec: int, keys: np.ndarray, values: np.ndarray, head_dim: int, tables: np.ndarray | None,
                   first_page: np.ndarray, page_counts: np.ndarray, heads: np.ndarray | None = None,
-                  token_counts: np.ndarray | None = None, threads: int = 0) -> tuple[np.ndarray, np.ndarray]:
-    """Encode page groups of page-major pages keys/values [n_pages, 16, D] -> (blob bytes, offsets/16)."""
+                  token_counts: np.ndarray | None = None, threads: int = 0,
+                  continues: np.ndarray | None = None) -> tuple[np.ndarray, np.ndarray]:
+    """Encode page groups of page-major pages keys/values [n_pages, 16, D] -> (blob bytes, offsets/16).
+    continues[i] = 1 codes group i as the second group of group i - 1's chain pair (see pair_flags)."""
     L = A.lib()
     keys = np.ascontiguousarray(keys, np.float32)
     values = np.ascontiguousarray(values, np.float32)
@@ -83,9 +93,10 @@ def encode_groups(codec: int, keys: np.ndarray, values: np.ndarray, head_dim: in
     end = C.c_uint64(0)
     hd = None if heads is None else np.ascontiguousarray(heads, np.uint32)
     tc = None if token_counts is None else np.ascontiguousarray(token_counts, np.uint32)
+    ct = None if continues is None else np.ascontiguousarray(continues, np.uint8)
     st = L.cf_kv_encode_groups(codec, _np_ptr(keys), _np_ptr(values), n, _np_ptr(first_page), _np_ptr(page_counts),
-                               _np_ptr(tc), head_dim, _np_ptr(tables), _np_ptr(hd), _np_ptr(pool), cap, 0,
-                               _np_ptr(offs), C.byref(end), threads)
+                               _np_ptr(tc), head_dim, _np_ptr(tables), _np_ptr(hd), _np_ptr(ct), _np_ptr(pool), cap,
+                               0, _np_ptr(offs), C.byref(end), threads)
     A.check(st, "cf_kv_encode_groups")
     return pool[:end.value], offs
 
@@ -105,11 +116,11 @@ def encode_groups_device(codec: int, keys: torch.Tensor, values: torch.Tensor, h
                          tables: torch.Tensor | None, first_page: torch.Tensor, page_counts: torch.Tensor,
                          pool: torch.Tensor, pool_at: int = 0, heads: torch.Tensor | None = None,
                          token_counts: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
-                         stream=None) -> DeviceEncodeResult:
+                         stream=None, continues: torch.Tensor | None = None) -> DeviceEncodeResult:
     """cf_kv_encode_groups_async on device tensors: keys/values fp32 [n_pages, 16, D], first_page int64,
-    page_counts/heads/token_counts int32 (u32 bit patterns), tables uint8 (table blobs), pool uint8. Asynchronous:
-    read `status` after the stream has run. The workspace is allocated here when not given (the C entry point
-    itself allocates nothing)."""
+    page_counts/heads/token_counts int32 (u32 bit patterns), continues uint8 (see pair_flags), tables uint8 (table
+    blobs), pool uint8. Asynchronous: read `status` after the stream has run. The workspace is allocated here when
+    not given (the C entry point itself allocates nothing)."""
     L = A.lib()
     n = first_page.numel()
     tcount = 0 if tables is None else tables.numel() // TABLE_BYTES
@@ -124,7 +135,8 @@ def encode_groups_device(codec: int, keys: torch.Tensor, values: torch.Tensor, h
     s = (stream if stream is not None else torch.cuda.current_stream()).cuda_stream
     st = L.cf_kv_encode_groups_async(codec, keys.data_ptr(), values.data_ptr(), n, first_page.data_ptr(),
                                      page_counts.data_ptr(), _dptr(token_counts), head_dim, _dptr(tables), tcount,
-                                     _dptr(heads), pool.data_ptr(), pool.numel(), pool_at, offs.data_ptr(),
+                                     _dptr(heads), _dptr(continues), pool.data_ptr(), pool.numel(), pool_at,
+                                     offs.data_ptr(),
                                      end.data_ptr(), status.data_ptr(), workspace.data_ptr(), workspace.numel(), s)
     A.check(st, "cf_kv_encode_groups_async")
     return DeviceEncodeResult(offs, end, status)
@@ -216,10 +228,11 @@ def seal_device(codec: int, keys: torch.Tensor, values: torch.Tensor, tables: to
     first = (g // ngr) * npg + gl * GROUP_PAGES
     counts = torch.clamp(npg - gl * GROUP_PAGES, max=GROUP_PAGES).to(torch.int32)
     heads = ((g // ngr) % H).to(torch.int32)
+    cont = (gl % 2 == 1).to(torch.uint8)  # groups 2k, 2k + 1 of each (sequence, head) form one chain
     cap = int(A.lib().cf_kv_group_blob_max_bytes(codec, D)) * S * H * ngr
     pool = torch.empty(cap, dtype=torch.uint8, device=dev)
     r = encode_groups_device(codec, keys.view(-1, PAGE_TOKENS, D), values.view(-1, PAGE_TOKENS, D), D, tables, first,
-                             counts, pool, 0, heads, None, None, stream)
+                             counts, pool, 0, heads, None, None, stream, continues=cont)
     st, end = int(r.status.item()), int(r.pool_end.item())
     if st != 0:
         raise A.CfError(st, "cf_kv_encode_groups_async (device status)")
@@ -278,11 +291,13 @@ def build_batched(codec: int, kv_source, seq_count: int, kv_heads: int, seq_toke
         if on_device:
             if (raw_groups or {}).get(s):
                 raise ValueError("raw_groups needs the host encoder")
+            cont = np.tile(pair_flags(gl), kv_heads)
             r = encode_groups_device(codec, torch.from_numpy(Kp).to(device), torch.from_numpy(Vp).to(device),
                                      head_dim, d_tab, torch.from_numpy(first_page.astype(np.int64)).to(device),
                                      torch.from_numpy(page_counts.astype(np.int32)).to(device), dpool, at,
                                      torch.from_numpy(heads.view(np.int32)).to(device),
-                                     torch.from_numpy(tc.ravel().view(np.int32)).to(device))
+                                     torch.from_numpy(tc.ravel().view(np.int32)).to(device),
+                                     continues=torch.from_numpy(cont).to(device))
             if int(r.status.item()) != 0:
                 raise A.CfError(int(r.status.item()), "cf_kv_encode_groups_async (device status)")
             offsets[s, :, first:ngr] = r.offsets.cpu().numpy().view(np.uint32).reshape(kv_heads, gl.size)
@@ -294,8 +309,9 @@ def build_batched(codec: int, kv_source, seq_count: int, kv_heads: int, seq_toke
             if hi <= lo:
                 continue
             sel = np.concatenate([ph[lo:hi] for ph in per_head])
+            cont = np.tile(pair_flags(gl[lo:hi]), kv_heads) if cdc != CODEC_INT8 else None
             blob, offs = encode_groups(cdc, Kp, Vp, head_dim, tables if cdc != CODEC_INT8 else None,
-                                       first_page[sel], page_counts[sel], heads[sel], tc.ravel())
+                                       first_page[sel], page_counts[sel], heads[sel], tc.ravel(), continues=cont)
             offsets[s, :, first + lo:first + hi] = (offs + at // 16).reshape(kv_heads, hi - lo)
             blobs.append(blob)
             at += blob.size

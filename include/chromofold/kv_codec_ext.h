@@ -15,52 +15,63 @@
  * Lane L = 16 G + t belongs to page G of the group.
  *
  * Quantisation (per page and head; K and V separately): s = max|x| / 127 (1.0 if all zero),
- * sym = clamp(rint(x / s), -128, 127) + 128 (round half to even, IEEE fp32 division); x ~ (sym - 128) * s.
- * Absent pages and tokens are padded with symbol 128 (value 0); the kernel masks them.
+ * q = clamp(rint(x / s), -128, 127) (round half to even, IEEE fp32 division); x ~ q * s. |q| <= 127 for every finite
+ * page (only NaN inputs give -128). INT8 groups store sym = q + 128; absent pages and tokens are padded with
+ * q = 0 and the kernel masks them.
  *
- * CF_KV_CODEC_RANS_HYBRID: each symbol splits into a 2-bit high part h = sym >> 6 and a 6-bit low part
- * l = sym & 63 ("hybrid integer" coding, as in JPEG XL's HybridUint / CABAC bypass bins): the low parts of a
- * Gaussian-like int8 distribution are nearly uniform and stay raw; the high parts carry the skew. The four high
- * parts of a quad of values form one 8-bit joint symbol  j = h0 | h1 << 2 | h2 << 4 | h3 << 6  coded with rANS.
+ * CF_KV_CODEC_RANS_HYBRID (format 4): each value is kept as a sign-magnitude byte b = (q < 0) << 7 | |q| and split
+ * into a "big" bit (|q| >= 64), a raw sign bit and 6 raw low bits (|q| & 63): the low parts of a Gaussian-like int8
+ * distribution are nearly uniform and the sign is a fair coin, so they stay raw; the big bits carry the skew. The
+ * big bits of 8 values (two quads) form one 8-bit joint symbol coded with rANS.
  *
- * Value order per lane (D = head_dim, D % 16 == 0, D <= 128; every lane owns D values = D/4 quads):
+ * Value order per lane (D = head_dim, D % 32 == 0, D <= 128; every lane owns D values = D/4 quads):
  *   K stream: lane L owns token t of page G, dims d = 0..D-1; quad q = dims 4q..4q+3.
  *   V stream: lane L owns dims {t + 16 i : i < D/16} of page G; quads in the order (tq = 0..3, i = 0..D/16-1),
  *             quad = tokens 4tq..4tq+3 at dim t + 16 i.
+ * Step p of a stream (p = 0 .. D/8 - 1) decodes quads 2p and 2p + 1: joint symbol
+ *   j = sum_i big(quad 2p, value i) << i  |  big(quad 2p + 1, value i) << (4 + i).
  *
- * rANS: M = 2^11, state in [2^16, 2^32), 16-bit renormalisation words. Each stream (K, V) is coded as TWO
- * interleaved chains of 64 lane states: chain A holds the even quads (q = 0, 2, 4, ...) and chain B the odd quads,
- * each with its own word stream, so a lane advances four independent states (K A/B, V A/B) at once. Decode step of
- * a chain (all 64 lanes, its next quad q):
+ * rANS: M = 2^11, state in [2^16, 2^32), 16-bit renormalisation words. One chain of 64 lane states per stream, so
+ * a lane advances two independent states (K, V). Decode step (all 64 lanes, step p):
  *   slot = x & 2047; (f, c, j) = table[slot]; x = f * (x >> 11) + c; then the lanes with x < 2^16 read, in
- *   ascending lane order, the next words of the chain's stream: x = (x << 16) | word.  (c = slot - cum[j].)
- * The encoder runs the exact reverse per chain (its quads descending, lanes descending) starting every state at
- * 2^16, so a correct decode ends with all states at 2^16 and every cursor at its stream's word count.
+ *   ascending lane order, the next words of the stream: x = (x << 16) | word.  (c = slot - cum[j].)
+ * Chains span a group PAIR: the groups 2k and 2k + 1 of one (sequence, KV head) are coded as one chain (the lane
+ * states follow the header of group 2k only; group 2k + 1's header says "continues" and its decode starts from the
+ * states group 2k ends with). A group may also start a chain of its own (an odd group whose predecessor is stored
+ * raw or belongs to another sequence's shared prefix, or an even group with no coded successor). The encoder runs
+ * the exact reverse per chain (steps descending over the chain's groups, lanes descending) starting every state at
+ * 2^16, so a correct decode ends each chain with all states at 2^16 and each group with every cursor at its
+ * stream's word count.
  *
- * Low parts, bit-sliced per lane in groups of 16 values (4 quads qd = 0..3, position i = 0..3 inside a quad):
- *   N0 = sum_i (l(0,i) & 15) << 8i | (l(1,i) & 15) << (8i + 4)      (quads 0,1)
- *   N1 = same for quads 2,3
- *   C  = sum_{qd,i} (l(qd,i) >> 4) << (8i + 2qd)
- * The symbol bytes of quad qd: nibble (N0, N0 >> 4, N1, N1 >> 4) & 0x0F0F0F0F, bits 4-5 of every byte from
- * (C << 4, C << 2, C, C >> 2) & 0x30303030, bits 6-7 from the high parts.
- * The words of lane L, low group g, word w (0: N0, 1: N1, 2: C) sit at index (g*3 + w)*64 + L.
+ * Raw bits, per lane and stream, in "sign groups" of 32 values = quads 8s .. 8s + 7 (k = q % 8), seven words each:
+ *   N0 (quads k = 0, 1), N1 (k = 2, 3), C0 (k = 0..3), N2 (k = 4, 5), N3 (k = 6, 7), C1 (k = 4..7), S (k = 0..7),
+ *   word w of sign group s of lane L at index (7 s + w) * 64 + L.
+ * Quad k has a frame r_k = (0, 4, 2, 6, 1, 5, 3, 7)[k]: field bit f of value i (f = 0-3 nibble = |q| & 15,
+ * 4-5 crumb = (|q| >> 4) & 3, 6 big, 7 sign) sits at word bit (8 i + r_k + f) mod 32 of the word holding that
+ * field (nibbles in N, crumbs in C, signs in S). Rotating the assembled word right by r_k gives the quad's four
+ * sign-magnitude bytes (nibbles of quads k, k+1 fill an N word, crumbs of 4 quads a C word, signs of 8 quads the S
+ * word, without gaps).
  *
  * Group blob (16-byte aligned, little-endian):
  *   [0]    cf_kv_group_header (64 B)
- *   RANS_HYBRID: [64] states u32: K chain A [64], K chain B [64], V chain A [64], V chain B [64];
- *                [1088] k_lows[3*(D/16)*64] u32, v_lows[same];
- *                then the word streams u16 of K A, K B, V A, V B (word_count[0..3] words each), zero padding to 16
- *                bytes.
- *   INT8:        [64] K symbol bytes, word (q*64 + L) = the 4 bytes of quad q of lane L; then V the same way.
+ *   RANS_HYBRID: if header.chain == 1: [64] lane states u32: K [64], V [64];
+ *                then the raw words u32: K (D/32 sign groups x 7 x 64), V (the same);
+ *                then the word streams u16 of K and V (word_count[0..1] words each), zero padding to 16 bytes.
+ *   INT8:        [64] K symbol bytes q + 128, word (q*64 + L) = the 4 bytes of quad q of lane L; then V the same
+ *                way.
  *
  * Table blob (CF_KV_RANS_TABLE_BYTES = 16 KiB): 2048 slot entries of two u32:
  *   lo = f | c << 11 | j << 22     (every symbol has f >= 1, so f <= 1793 fits 11 bits)
- *   hi = spread(j) = sum_i ((j >> 2i) & 3) << (8i + 6)
+ *   hi = spread(j): the big bits in the frames of a quad pair with r = 0 and 4:
+ *        sum_i ((j >> i) & 1) << (8 i + 6)  |  ((j >> (4 + i)) & 1) << ((8 i + 10) mod 32)
+ *        (the pair of quads 8s + 2m, 8s + 2m + 1 uses it rotated left by the first quad's frame r_{2m}).
  * The batched launch uses table 2h for the K streams and 2h+1 for the V streams of KV head h.
  *
- * Raw fallback: a group whose rANS words (all four streams together) would exceed CF_KV_RANS_MAX_GROUP_WORDS
- * (data the tables do not fit, e.g. near-uniform high parts) is stored as an INT8 group instead (its header says
- * so); a RANS_HYBRID pool may therefore hold both kinds and the decoder dispatches per group.
+ * Word bound: a decode step reads at most one word per lane, so a group's streams hold at most 16 * D words
+ * together (CF_KV_RANS_MAX_GROUP_WORDS at D = 128).
+ * Raw fallback: a group that holds a q of -128 (only NaN inputs give one) is stored as an INT8 group instead (its
+ * header says so; the other group of its pair then starts a chain of its own); a RANS_HYBRID pool may therefore
+ * hold both kinds and the decoder dispatches per group.
  * ------------------------------------------------------------------------------------------------------------ */
 #ifndef CHROMOFOLD_KV_CODEC_EXT_H
 #define CHROMOFOLD_KV_CODEC_EXT_H
@@ -74,7 +85,7 @@
 extern "C" {
 #endif
 
-#define CF_KV_EXT_ABI_VERSION 3u
+#define CF_KV_EXT_ABI_VERSION 4u
 #define CF_KV_GROUP_PAGES 4u
 #define CF_KV_CODEC_INT8 1u
 #define CF_KV_CODEC_RANS_HYBRID 2u
@@ -86,7 +97,10 @@ extern "C" {
 
 typedef struct cf_kv_group_header {
     uint32_t codec;            /* CF_KV_CODEC_* */
-    uint16_t word_count[4];    /* 16-bit rANS words of the K A, K B, V A, V B streams (0 for INT8) */
+    uint16_t word_count[2];    /* 16-bit rANS words of the K and V streams of this group (0 for INT8) */
+    uint16_t chain;            /* RANS_HYBRID: 1 = the group starts a chain (lane states follow), 0 = it continues
+                                  the chain of the group before it (an odd group of its pair) */
+    uint16_t reserved;
     uint16_t token_count[4];   /* tokens of each page, 0 = page absent */
     uint16_t head_dim;
     uint16_t page_count;       /* 1..4 */
@@ -155,30 +169,33 @@ cf_status cf_kv_paged_attention_cascade_async(const cf_kv_batched_desc *desc, ui
  * a nonzero frequency, so any page can be coded with any table. */
 cf_status cf_kv_rans_build_table(const uint64_t *joint_histogram256, uint8_t *table_out);
 
-/* Joint-symbol histogram of one page's values [token_count, head_dim] in K lane order (accumulates). */
+/* Joint-symbol histogram of one page's values [token_count, head_dim] in K lane order (accumulates): the big bits
+ * of dims 8p .. 8p + 7 of each token (tokens past token_count count as zeros). head_dim % 32 == 0. */
 cf_status cf_kv_rans_page_histogram(const float *values, uint32_t token_count, uint32_t head_dim,
                                     uint64_t *hist256);
 
 /* Size bound for one encoded group blob at this head_dim (for pool allocation). */
 uint64_t cf_kv_group_blob_max_bytes(uint32_t codec, uint32_t head_dim);
 
-/* Quantise and encode one page group: K and V [page_count * 16, head_dim] fp32 (page-major), token_counts[page]
- * (1..16; pages past page_count absent). Tables are host copies of table blobs (RANS_HYBRID). Writes the blob
- * into `blob` (capacity `blob_capacity`) and its size to *blob_bytes. */
+/* Quantise and encode one page group that starts a chain of its own: K and V [page_count * 16, head_dim] fp32
+ * (page-major), token_counts[page] (1..16; pages past page_count absent). Tables are host copies of table blobs
+ * (RANS_HYBRID). Writes the blob into `blob` (capacity `blob_capacity`) and its size to *blob_bytes. */
 cf_status cf_kv_encode_group(uint32_t codec, const float *keys, const float *values, uint32_t page_count,
                              const uint32_t *token_counts, uint32_t head_dim, const uint8_t *k_table,
                              const uint8_t *v_table, uint32_t k_table_index, uint32_t v_table_index, uint8_t *blob,
                              uint64_t blob_capacity, uint64_t *blob_bytes);
 
 /* Batch form: ngroups groups, group i = page_counts[i] pages starting at page first_page[i] of the page-major
- * arrays keys/values ([*][16][head_dim]); table pair heads[i] (may be NULL: 0). Encoded on `threads` host
- * threads (0 = all), packed 16-byte aligned into pool[pool_at ..]; offsets_out[i] = byte offset / 16;
- * *pool_end = first free byte. token_counts is per page (NULL: all 16). */
+ * arrays keys/values ([*][16][head_dim]); table pair heads[i] (may be NULL: 0). continues[i] = 1 codes group i
+ * as the second group of a chain pair with group i - 1 (they must be the two groups 2k, 2k + 1 of one sequence
+ * and head, so heads[i] == heads[i - 1], and group i - 1 must not itself continue); NULL = every group starts its
+ * own chain. Encoded on `threads` host threads (0 = all), packed 16-byte aligned into pool[pool_at ..] in group
+ * order; offsets_out[i] = byte offset / 16; *pool_end = first free byte. token_counts is per page (NULL: all 16). */
 cf_status cf_kv_encode_groups(uint32_t codec, const float *keys, const float *values, uint64_t ngroups,
                               const uint64_t *first_page, const uint32_t *page_counts, const uint32_t *token_counts,
-                              uint32_t head_dim, const uint8_t *tables, const uint32_t *heads, uint8_t *pool,
-                              uint64_t pool_capacity, uint64_t pool_at, uint32_t *offsets_out, uint64_t *pool_end,
-                              uint32_t threads);
+                              uint32_t head_dim, const uint8_t *tables, const uint32_t *heads,
+                              const uint8_t *continues, uint8_t *pool, uint64_t pool_capacity, uint64_t pool_at,
+                              uint32_t *offsets_out, uint64_t *pool_end, uint32_t threads);
 
 /* ---- device-side page encoder (sealing on the GPU) --------------------------------------------------------- */
 
@@ -186,7 +203,8 @@ cf_status cf_kv_encode_groups(uint32_t codec, const float *keys, const float *va
  * at the same pool offsets, byte for byte (no counterpart in the reference, whose pages are always sealed on the
  * host: src/runtime/compressed_kv_cache.cu:89-109). Every array argument is DEVICE memory: keys/values (page-major
  * [*][16][head_dim] fp32, 16-byte aligned), first_page/page_counts/heads [ngroups], token_counts per page (NULL:
- * all 16), tables = table_count table blobs (RANS_HYBRID), pool (16-byte aligned), offsets_out [ngroups],
+ * all 16), tables = table_count table blobs (RANS_HYBRID), continues [ngroups] (NULL: none; as in
+ * cf_kv_encode_groups), pool (16-byte aligned), offsets_out [ngroups],
  * *pool_end, *status, workspace. Asynchronous on `stream`; allocates nothing and never synchronises.
  * Synchronous return: argument errors only. Device-side outcome in *status once the stream has run: CF_OK, or
  * CF_ERR_INVALID_ARGUMENT when a group has a bad page/token count or table pair (heads[i] must satisfy
@@ -197,7 +215,8 @@ uint64_t cf_kv_encode_groups_workspace_bytes(uint32_t codec, uint32_t head_dim, 
 cf_status cf_kv_encode_groups_async(uint32_t codec, const float *keys, const float *values, uint64_t ngroups,
                                     const uint64_t *first_page, const uint32_t *page_counts,
                                     const uint32_t *token_counts, uint32_t head_dim, const uint8_t *tables,
-                                    uint32_t table_count, const uint32_t *heads, uint8_t *pool,
+                                    uint32_t table_count, const uint32_t *heads, const uint8_t *continues,
+                                    uint8_t *pool,
                                     uint64_t pool_capacity, uint64_t pool_at, uint32_t *offsets_out,
                                     uint64_t *pool_end, uint32_t *status, void *workspace, uint64_t workspace_bytes,
                                     void *stream);

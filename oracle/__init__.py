@@ -87,7 +87,7 @@ def _declare(L):
                                              P, P, U32, U32, P]),
         "or_dense_attention_f64": (None, [P, U32, P, P, U32, C.c_float, P]),
         "or_kv_window_attention_f64": (None, [P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, P]),
-        "or_kv_decode_group": (C.c_int, [P, P, U32, P, P, P, P, P]),
+        "or_kv_decode_group": (C.c_int, [P, P, U32, P, P, P, P, P, P, P]),
         "or_kv_quantize_page_absmax": (None, [P, U32, P, P]),
         "or_nib_seal": (C.c_int, [P, U32, U32, P, P, P, P, P]),
         "or_nib_attention": (None, [U32, P, P, P, P, P, P, U32, P, P, U32, U32, P, U32, U32, U32, U32, U32,
@@ -325,20 +325,50 @@ def rrr_decode_all(classes, offsets, nblocks: int, off_base_bit: int = 0) -> np.
 
 
 # ------------------------------------------------------------------ paged KV
-def kv_decode_group(blob: np.ndarray, tables: np.ndarray | None, head: int, head_dim: int):
+def kv_decode_group(blob: np.ndarray, tables: np.ndarray | None, head: int, head_dim: int, states=None,
+                    full: bool = False):
     """Decode one kv_codec_ext group blob -> (k_sym [4, 16, D], v_sym [4, 16, D], k_scales[4], v_scales[4],
-    token_counts[4])."""
+    token_counts[4]); full=True appends (end_states [2, 64] uint32, chain flag). `states` [2, 64] are the lane states
+    the previous group of the chain ended with, needed when the blob continues a chain (header chain == 0)."""
     blob = np.ascontiguousarray(blob, np.uint8)
     ks = np.zeros((4, 16, head_dim), np.uint8)
     vs = np.zeros((4, 16, head_dim), np.uint8)
     ksc = np.zeros(4, np.float32)
     vsc = np.zeros(4, np.float32)
     tc = np.zeros(4, np.uint32)
+    st = np.zeros((2, 64), np.uint32) if states is None else np.array(states, np.uint32).reshape(2, 64)
+    chain = C.c_uint32(0)
+    if states is None and kv_group_continues(blob):
+        raise ValueError("the group continues a chain: pass the states its predecessor ended with")
     tab = None if tables is None else np.ascontiguousarray(tables, np.uint8)
-    rc = lib().or_kv_decode_group(_ptr(blob), _ptr(tab), head, _ptr(ks), _ptr(vs), _ptr(ksc), _ptr(vsc), _ptr(tc))
+    rc = lib().or_kv_decode_group(_ptr(blob), _ptr(tab), head, _ptr(ks), _ptr(vs), _ptr(ksc), _ptr(vsc), _ptr(tc),
+                                  _ptr(st), C.byref(chain))
     if rc != 0:
         raise ValueError("group blob failed to decode")
-    return ks, vs, ksc, vsc, tc
+    return (ks, vs, ksc, vsc, tc, st, chain.value) if full else (ks, vs, ksc, vsc, tc)
+
+
+def kv_group_continues(blob: np.ndarray) -> bool:
+    """True for a RANS_HYBRID group blob that continues the chain of the group before it."""
+    b = np.asarray(blob, np.uint8)
+    return int(b[:4].view(np.uint32)[0]) == 2 and int(b[8:10].view(np.uint16)[0]) == 0
+
+
+def kv_decode_run(blobs, tables, head: int, head_dim: int):
+    """Decode the groups of one (sequence, KV head) in token order, carrying each chain's lane states from a group
+    to the one that continues it, and check that every chain ends with all states at 2^16 (the encoder's start).
+    blobs: list of group blobs (each long enough to hold its group). Returns a list of 5-tuples as kv_decode_group."""
+    out, states = [], None
+    for g, blob in enumerate(blobs):
+        ks, vs, ksc, vsc, tc, st, chain = kv_decode_group(blob, tables, head, head_dim,
+                                                           states if kv_group_continues(blob) else None, full=True)
+        ends = g + 1 == len(blobs) or not kv_group_continues(blobs[g + 1])
+        is_rans = int(np.asarray(blob, np.uint8)[:4].view(np.uint32)[0]) == 2
+        if is_rans and ends and not (st == 65536).all():
+            raise ValueError(f"chain ending at group {g} does not return to the initial states")
+        states = st if is_rans else None
+        out.append((ks, vs, ksc, vsc, tc))
+    return out
 
 
 def kv_quantize_absmax(x: np.ndarray):

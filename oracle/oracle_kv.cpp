@@ -185,22 +185,29 @@ void or_kv_window_attention_f64(const float *K, const float *V, const float *Q, 
 }
 
 // ---------------------------------------------------------------------------------------- kv_codec_ext pages
-// Decode one INT8 / RANS_HYBRID page-group blob into symbols [4 pages][16 tokens][D] for K and V (token-major)
-// plus per-page scales and token counts. tables: table blobs (16 KiB each); K uses tables[2*head], V
-// tables[2*head+1]. Returns 0 on success, -1 on a format inconsistency (bad codec, stream over/under-run, a final
-// state != 2^16).
+// Decode one INT8 / RANS_HYBRID (format 4) page-group blob into symbols [4 pages][16 tokens][D] for K and V
+// (token-major, offset binary q + 128) plus per-page scales and token counts. tables: table blobs (16 KiB each);
+// K uses tables[2*head], V tables[2*head+1]. states_io [2 x 64] (K lanes, then V lanes): for a RANS group that
+// continues its chain (header chain == 0) the lane states the previous group of the chain ended with; on return
+// the states this group ends with (a chain must end with every state at 2^16: the caller checks that where a chain
+// ends). *chain_out = the header's chain flag (1 for INT8 groups). Returns 0 on success, -1 on a format
+// inconsistency (bad codec or head_dim, a table whose spread word disagrees with its symbol, a stream over-run, a
+// cursor short of its word count).
 int or_kv_decode_group(const uint8_t *blob, const uint8_t *tables, uint32_t head, uint8_t *k_sym, uint8_t *v_sym,
-                       float *k_scale, float *v_scale, uint32_t *token_count) {
+                       float *k_scale, float *v_scale, uint32_t *token_count, uint32_t *states_io,
+                       uint32_t *chain_out) {
   uint32_t codec;
-  uint16_t wc[4], tc[4], D, npg;
+  uint16_t wc[2], chain, tc[4], D, npg;
   std::memcpy(&codec, blob, 4);
-  std::memcpy(wc, blob + 4, 8);  // words of the K A, K B, V A, V B chains
+  std::memcpy(wc, blob + 4, 4);  // words of the K and V streams
+  std::memcpy(&chain, blob + 8, 2);
   std::memcpy(tc, blob + 12, 8);
   std::memcpy(&D, blob + 20, 2);
   std::memcpy(&npg, blob + 22, 2);
   std::memcpy(k_scale, blob + 32, 16);
   std::memcpy(v_scale, blob + 48, 16);
   for (int g = 0; g < 4; ++g) token_count[g] = tc[g];
+  *chain_out = 1;
   const uint32_t nq = D / 4, page = 16u * D;
   // lane L (page L/16, t = L%16), quad q, position i -> flat index into [4][16][D]
   auto where = [&](bool is_v, uint32_t L, uint32_t q, uint32_t i) -> size_t {
@@ -219,52 +226,61 @@ int or_kv_decode_group(const uint8_t *blob, const uint8_t *tables, uint32_t head
     }
     return 0;
   }
-  if (codec != 2) return -1;
-  const uint32_t nlow = 3 * (D / 16) * 64;
-  const uint32_t *states = reinterpret_cast<const uint32_t *>(blob + 64);  // K A, K B, V A, V B x 64 lanes
-  const uint32_t *lows = reinterpret_cast<const uint32_t *>(blob + 64 + 4 * 64 * 4);
-  const uint16_t *words = reinterpret_cast<const uint16_t *>(blob + 64 + 4 * 64 * 4 + 2 * (size_t)nlow * 4);
-  const uint16_t *cw[4];  // each chain's word stream, in the order K A, K B, V A, V B
-  cw[0] = words;
-  for (int c = 1; c < 4; ++c) cw[c] = cw[c - 1] + wc[c - 1];
+  if (codec != 2 || D == 0 || D % 32 != 0) return -1;
+  *chain_out = chain;
+  static const uint32_t frame[8] = {0, 4, 2, 6, 1, 5, 3, 7};
+  static const uint32_t nword[8] = {0, 0, 1, 1, 3, 3, 4, 4};  // N0 N1 C0 N2 N3 C1 S
+  const uint32_t steps = D / 8, raw_words = 7 * (D / 32) * 64;
+  const uint8_t *p = blob + 64;
+  if (chain) {
+    std::memcpy(states_io, p, 2 * 64 * 4);
+    p += 2 * 64 * 4;
+  }
+  const uint32_t *raw = reinterpret_cast<const uint32_t *>(p);  // K raw words, then V
+  const uint16_t *words = reinterpret_cast<const uint16_t *>(p + 2 * (size_t)raw_words * 4);
+  auto bit = [](uint32_t w, uint32_t pos) { return (w >> (pos % 32)) & 1u; };
   for (int s = 0; s < 2; ++s) {
     const uint8_t *tab = tables + (size_t)(2 * head + s) * 16384;
-    uint32_t x[2][64], cur[2] = {0, 0};
-    for (int ch = 0; ch < 2; ++ch)
-      for (int L = 0; L < 64; ++L) x[ch][L] = states[(2 * s + ch) * 64 + L];
+    const uint16_t *w = words + (s ? wc[0] : 0);
+    const uint32_t *rw = raw + (size_t)s * raw_words;
+    uint32_t *x = states_io + 64 * s, cur = 0;
     uint8_t *out = s ? v_sym : k_sym;
-    const uint32_t *lw = lows + (size_t)s * nlow;
-    for (uint32_t q = 0; q < nq; ++q) {  // quad q belongs to chain q % 2; chains are independent
-      const uint32_t ch = q % 2, nw = wc[2 * s + ch];
-      const uint16_t *w = cw[2 * s + ch];
+    for (uint32_t st = 0; st < steps; ++st) {
       uint32_t j[64];
-      for (uint32_t L = 0; L < 64; ++L) {  // all lanes decode quad q
-        uint32_t lo;
-        std::memcpy(&lo, tab + 8 * (x[ch][L] & 2047u), 4);
+      for (uint32_t L = 0; L < 64; ++L) {  // all lanes decode step st
+        uint32_t lo, hi;
+        std::memcpy(&lo, tab + 8 * (x[L] & 2047u), 4);
+        std::memcpy(&hi, tab + 8 * (x[L] & 2047u) + 4, 4);
         const uint32_t f = lo & 2047u, c = (lo >> 11) & 2047u;
         j[L] = (lo >> 22) & 255u;
-        x[ch][L] = f * (x[ch][L] >> 11) + c;
+        uint32_t spread = 0;  // the format's spread word of j
+        for (uint32_t i = 0; i < 4; ++i)
+          spread |= ((j[L] >> i) & 1u) << (8 * i + 6) | ((j[L] >> (4 + i)) & 1u) << ((8 * i + 10) % 32);
+        if (hi != spread) return -1;
+        x[L] = f * (x[L] >> 11) + c;
       }
       for (uint32_t L = 0; L < 64; ++L)  // renormalisation reads in ascending lane order
-        if (x[ch][L] < 65536u) {
-          if (cur[ch] >= nw) return -1;
-          x[ch][L] = (x[ch][L] << 16) | w[cur[ch]++];
+        if (x[L] < 65536u) {
+          if (cur >= wc[s]) return -1;
+          x[L] = (x[L] << 16) | w[cur++];
         }
-      const uint32_t g = q / 4, qd = q % 4;
-      for (uint32_t L = 0; L < 64; ++L) {
-        const uint32_t n = lw[(g * 3 + (qd >> 1)) * 64 + L], c = lw[(g * 3 + 2) * 64 + L];
-        for (uint32_t i = 0; i < 4; ++i) {
-          const uint32_t low = ((n >> (8 * i + 4 * (qd & 1))) & 15u) | (((c >> (8 * i + 2 * qd)) & 3u) << 4);
-          const uint32_t hi = (j[L] >> (2 * i)) & 3u;
-          out[where(s == 1, L, q, i)] = (uint8_t)((hi << 6) | low);
+      for (uint32_t h = 0; h < 2; ++h) {
+        const uint32_t q = 2 * st + h, k = q % 8, sg = q / 8, r = frame[k];
+        for (uint32_t L = 0; L < 64; ++L) {
+          const uint32_t N = rw[(7 * sg + nword[k]) * 64 + L], Cw = rw[(7 * sg + (k < 4 ? 2 : 5)) * 64 + L],
+                         S = rw[(7 * sg + 6) * 64 + L];
+          for (uint32_t i = 0; i < 4; ++i) {
+            uint32_t mag = 0;
+            for (uint32_t f = 0; f < 4; ++f) mag |= bit(N, 8 * i + r + f) << f;
+            for (uint32_t f = 0; f < 2; ++f) mag |= bit(Cw, 8 * i + r + 4 + f) << (4 + f);
+            mag |= ((j[L] >> (4 * h + i)) & 1u) << 6;
+            const int v = bit(S, 8 * i + r + 7) ? -(int)mag : (int)mag;
+            out[where(s == 1, L, q, i)] = (uint8_t)(v + 128);
+          }
         }
       }
     }
-    for (int ch = 0; ch < 2; ++ch) {
-      if (cur[ch] != wc[2 * s + ch]) return -1;
-      for (int L = 0; L < 64; ++L)
-        if (x[ch][L] != 65536u) return -1;
-    }
+    if (cur != wc[s]) return -1;
   }
   return 0;
 }

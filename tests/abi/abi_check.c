@@ -102,7 +102,7 @@ int main(void) {
   expect("cf_llama_kv_last_error", cf_llama_kv_last_error(NULL) != NULL, 1);
   expect("cf_kv_encode_fixed_page", cf_kv_encode_fixed_page(4, NULL, NULL, 1, 1, 64, NULL, NULL, NULL, NULL, NULL), INV);
   expect("cf_kv_encode_groups_async",
-         cf_kv_encode_groups_async(2, NULL, NULL, 1, NULL, NULL, NULL, 64, NULL, 2, NULL, NULL, 0, 0, NULL, NULL,
+         cf_kv_encode_groups_async(2, NULL, NULL, 1, NULL, NULL, NULL, 64, NULL, 2, NULL, NULL, NULL, 0, 0, NULL, NULL,
                                    NULL, NULL, 0, NULL), INV);
   expect("cf_kv_encode_groups_workspace_bytes", cf_kv_encode_groups_workspace_bytes(2, 20, 1, 2) == 0, 1);
   {

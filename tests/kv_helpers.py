@@ -25,12 +25,12 @@ def make_seqs(seq_tokens, kv_heads, D, seed, scale_spread=False, v_mult=None):
 
 
 def decoded_pages(kv, s, h, T):
-    """(token_begin, K, V) dequantised pages of sequence s, head h, decoded by the oracle from the host pool."""
+    """(token_begin, K, V) dequantised pages of sequence s, head h, decoded by the oracle from the host pool (the
+    groups in token order, chain states carried from each group to the one that continues it)."""
     D = kv.head_dim
     out = []
-    for g in range((T + 63) // 64):
-        off = int(kv.host_offsets[s, h, g]) * 16
-        ks, vs, ksc, vsc, tc = O.kv_decode_group(kv.host_pool[off:off + 65536], kv.host_tables, h, D)
+    blobs = [kv.host_pool[int(kv.host_offsets[s, h, g]) * 16:][:65536] for g in range((T + 63) // 64)]
+    for g, (ks, vs, ksc, vsc, tc) in enumerate(O.kv_decode_run(blobs, kv.host_tables, h, D)):
         for G in range(4):
             p = 4 * g + G
             n = min(16, T - 16 * p)

@@ -1,9 +1,10 @@
 """Device-side sealing (cf_kv_encode_groups_async) against the host encoder cf_kv_encode_groups: the same pool bytes,
-offsets and end, bit for bit, over head dims 16..128, both codecs, ragged pages, several table pairs, the INT8
-fallback inside a RANS_HYBRID pool, all-zero / non-finite / denormal / huge pages, and a non-zero pool_at. The host
-encoder is itself closed against the oracle here: the oracle decodes every device blob back to exactly the symbols
-of the oracle's quantiser. Error cases leave the pool untouched and report CF_ERR_INVALID_ARGUMENT in the device
-status word, where the host encoder returns the same status."""
+offsets and end, bit for bit, over head dims 16..128 (RANS_HYBRID at multiples of 32), both codecs, ragged pages,
+chain pairs and single groups, several table pairs, the INT8 fallback of a group holding -128 inside a RANS_HYBRID
+pool (its pair partner then starts its own chain), all-zero / non-finite / denormal / huge / all-big pages, and a
+non-zero pool_at. The host encoder is itself closed against the oracle here: the oracle decodes every device blob
+(chains in order) back to exactly the symbols of the oracle's quantiser. Error cases leave the pool untouched and
+report CF_ERR_INVALID_ARGUMENT in the device status word, where the host encoder returns the same status."""
 import numpy as np
 import pytest
 
@@ -21,19 +22,23 @@ def dev():
     return torch.device("cuda:0")
 
 
-def _groups(rng, pages_per_head, heads, ragged):
-    """Consecutive pages of each head cut into groups of 1..4 pages -> first_page, page_counts, heads, token counts."""
-    first, counts, hd = [], [], []
+def _groups(rng, pages_per_head, heads, ragged, paired=True):
+    """Consecutive pages of each head cut into groups of 1..4 pages -> first_page, page_counts, heads, token counts,
+    continues (the groups 2k + 1 of each head continue the chain of group 2k when `paired`)."""
+    first, counts, hd, cont = [], [], [], []
     for h in range(heads):
-        p = 0
+        p, j = 0, 0
         while p < pages_per_head:
             c = int(min(rng.integers(1, 5), pages_per_head - p))
             first.append(h * pages_per_head + p)
             counts.append(c)
             hd.append(h)
+            cont.append(1 if paired and j % 2 == 1 else 0)
             p += c
+            j += 1
     tc = rng.integers(1, 17, size=heads * pages_per_head) if ragged else np.full(heads * pages_per_head, 16)
-    return (np.array(first, np.uint64), np.array(counts, np.uint32), np.array(hd, np.uint32), tc.astype(np.uint32))
+    return (np.array(first, np.uint64), np.array(counts, np.uint32), np.array(hd, np.uint32), tc.astype(np.uint32),
+            np.array(cont, np.uint8))
 
 
 def _tables(rng, heads, D):
@@ -45,7 +50,7 @@ def _tables(rng, heads, D):
     return np.concatenate(parts)
 
 
-def _device(dev, codec, K, V, D, tables, first, counts, heads, tc, pool_bytes, pool_at, capacity=None):
+def _device(dev, codec, K, V, D, tables, first, counts, heads, tc, pool_bytes, pool_at, capacity=None, cont=None):
     import torch
     from chromofold_amd import kv
     pool = torch.full((pool_bytes,), SENTINEL, dtype=torch.uint8, device=dev)
@@ -55,7 +60,8 @@ def _device(dev, codec, K, V, D, tables, first, counts, heads, tc, pool_bytes, p
         codec, torch.from_numpy(K).to(dev), torch.from_numpy(V).to(dev), D,
         None if tables is None else torch.from_numpy(tables).to(dev),
         torch.from_numpy(first.astype(np.int64)).to(dev), torch.from_numpy(counts.view(np.int32)).to(dev), pool,
-        pool_at, torch.from_numpy(heads.view(np.int32)).to(dev), torch.from_numpy(tc.view(np.int32)).to(dev))
+        pool_at, torch.from_numpy(heads.view(np.int32)).to(dev), torch.from_numpy(tc.view(np.int32)).to(dev),
+        continues=None if cont is None else torch.from_numpy(cont).to(dev))
     torch.cuda.synchronize()
     return (int(r.status.item()), pool.cpu().numpy(), r.offsets.cpu().numpy().view(np.uint32),
             int(r.pool_end.item()))
@@ -76,45 +82,53 @@ def _special(K, V, rng, kind):
     elif kind == "huge":
         K[0] *= np.float32(1e38)
         V[0, 0, 0] = np.float32(3.4e38)
-    elif kind == "extremes":  # every value at +-absmax: high parts 0/3 only, the tables' rarest joint symbols, so
-        # both streams cost ~11 bits per quad and the group falls back to INT8
+    elif kind == "extremes":  # every value at +-absmax: every big bit set, the tables' rarest joint symbol, so
+        # every lane renormalises at (nearly) every step: the word bound of kv_codec_ext.h is reached, still coded
         K[:] = rng.choice([-1.0, 1.0], K.shape).astype(np.float32)
         V[:] = rng.choice([-1.0, 1.0], V.shape).astype(np.float32)
 
 
-CASES = [  # (D, codec, heads, pages per head, ragged, special)
-    (128, 2, 3, 9, True, None), (128, 1, 2, 6, True, None), (64, 2, 2, 7, False, None), (16, 2, 1, 5, True, None),
-    (32, 2, 2, 4, True, None), (48, 2, 1, 6, True, None), (96, 2, 2, 5, True, None), (112, 1, 1, 3, True, None),
-    (128, 2, 1, 4, False, "zero"), (128, 2, 2, 4, True, "nonfinite"), (64, 2, 2, 4, False, "denormal"),
-    (128, 2, 1, 4, True, "huge"), (128, 2, 1, 8, False, "extremes"), (64, 1, 1, 4, True, "nonfinite"),
+CASES = [  # (D, codec, heads, pages per head, ragged, special, paired)
+    (128, 2, 3, 9, True, None, True), (128, 2, 3, 9, True, None, False), (128, 1, 2, 6, True, None, True),
+    (64, 2, 2, 7, False, None, True), (16, 1, 1, 5, True, None, True), (32, 2, 2, 4, True, None, True),
+    (48, 1, 1, 6, True, None, True), (96, 2, 2, 5, True, None, True), (112, 1, 1, 3, True, None, True),
+    (128, 2, 1, 4, False, "zero", True), (128, 2, 2, 4, True, "nonfinite", True), (64, 2, 2, 4, False, "denormal", True),
+    (128, 2, 1, 4, True, "huge", True), (128, 2, 1, 8, False, "extremes", True), (64, 1, 1, 4, True, "nonfinite", True),
 ]
 
 
-@pytest.mark.parametrize("D,codec,heads,pph,ragged,special", CASES)
-def test_device_encoder_matches_host(dev, D, codec, heads, pph, ragged, special):
+@pytest.mark.parametrize("D,codec,heads,pph,ragged,special,paired", CASES)
+def test_device_encoder_matches_host(dev, D, codec, heads, pph, ragged, special, paired):
     from chromofold_amd import kv
     rng = np.random.default_rng(1000 * D + 10 * codec + heads + pph)
     K = rng.standard_normal((heads * pph, 16, D)).astype(np.float32)
     V = rng.standard_normal((heads * pph, 16, D)).astype(np.float32)
     _special(K, V, rng, special)
-    first, counts, hd, tc = _groups(rng, pph, heads, ragged)
+    first, counts, hd, tc, cont = _groups(rng, pph, heads, ragged, paired)
     tables = _tables(rng, heads, D) if codec == 2 else None
-    host, hoff = kv.encode_groups(codec, K, V, D, tables, first, counts, hd, tc)
+    host, hoff = kv.encode_groups(codec, K, V, D, tables, first, counts, hd, tc, continues=cont)
     pool_at = 48
     cap = pool_at + len(first) * int(kv.A.lib().cf_kv_group_blob_max_bytes(codec, D)) + 64
-    st, pool, off, end = _device(dev, codec, K, V, D, tables, first, counts, hd, tc, cap, pool_at)
+    st, pool, off, end = _device(dev, codec, K, V, D, tables, first, counts, hd, tc, cap, pool_at, cont=cont)
     assert st == 0
     assert end == pool_at + host.size
     assert np.array_equal(pool[pool_at:end], host)
     assert np.array_equal(off, hoff + pool_at // 16)
     assert (pool[:pool_at] == SENTINEL).all() and (pool[end:] == SENTINEL).all()
+    codecs = [int(host[int(o) * 16]) for o in hoff]
     if special == "extremes":
-        codecs = [int(host[int(o) * 16]) for o in hoff]  # full groups exceed the word budget, short ones may not
-        assert all(c == kv.CODEC_INT8 for c, n in zip(codecs, counts) if n >= 3) and kv.CODEC_INT8 in codecs
-    # close the loop without the host encoder: the oracle decodes the device blobs to the oracle quantiser's symbols
-    for i, o in enumerate(off):
-        blob = pool[int(o) * 16:]
-        ks, vs, ksc, vsc, gtc = O.kv_decode_group(blob[:65536], tables, int(hd[i]), D)
+        assert all(c == kv.CODEC_RANS_HYBRID for c in codecs)
+    if special == "nonfinite" and codec == 2:  # the groups holding -128 are INT8, the others coded
+        assert kv.CODEC_INT8 in codecs and kv.CODEC_RANS_HYBRID in codecs
+    # close the loop without the host encoder: the oracle decodes the device blobs (each head's chains in order) to
+    # the oracle quantiser's symbols
+    decoded = {}
+    for h in range(heads):
+        idx = [i for i in range(len(first)) if hd[i] == h]
+        for i, dec in zip(idx, O.kv_decode_run([pool[int(off[i]) * 16:][:65536] for i in idx], tables, h, D)):
+            decoded[i] = dec
+    for i in range(len(first)):
+        ks, vs, ksc, vsc, gtc = decoded[i]
         for G in range(int(counts[i])):
             p = int(first[i]) + G
             n = int(tc[p])
@@ -132,7 +146,7 @@ def test_device_encoder_errors_leave_pool_untouched(dev):
     D, heads, pph = 64, 2, 4
     K = rng.standard_normal((heads * pph, 16, D)).astype(np.float32)
     V = rng.standard_normal((heads * pph, 16, D)).astype(np.float32)
-    first, counts, hd, tc = _groups(rng, pph, heads, True)
+    first, counts, hd, tc, _ = _groups(rng, pph, heads, True, paired=False)
     tables = _tables(rng, heads, D)
     host, _ = kv.encode_groups(2, K, V, D, tables, first, counts, hd, tc)
     cap = 32 + len(first) * int(kv.A.lib().cf_kv_group_blob_max_bytes(2, D))
@@ -172,7 +186,7 @@ def test_device_sealed_pool_serves_batched_attention(dev):
     from chromofold_amd import kv
     from kv_helpers import make_seqs
     D, H, gqa = 128, 2, 4
-    toks = [300, 64, 1000, 17]
+    toks = [300, 64, 1000, 17, 200]
     data = make_seqs(toks, H, D, 4242)
     rng = np.random.default_rng(5)
     tables = _tables(rng, H, D)
