@@ -156,9 +156,9 @@ constexpr int buf_u32() {
 // Decode one page group (K scores, softmax, V accumulation).
 // RANS groups: `st` holds the chain's lane states on entry (K, V) and the states the group ends with on return;
 // the word streams are read through `wk` (the wave's LDS staging buffer, K stream then V); `raw` points at the
-// group's raw words. `pre` always holds the NEXT sign group's 14 raw words (7 K + 7 V): on entry the group's first,
-// and while sign group s is decoded, sign group s + 1's (or, during the last one, the first sign group of the next
-// RANS group at `nlw`, NULL if none) are in flight, a quarter of the group ahead of their use.
+// group's raw words. `pre` holds 14 raw words (7 K + 7 V): on entry the group's first sign group, on return the
+// first sign group of the next RANS group at `nlw` (NULL if none); in between, each word of sign group s + 1 is
+// loaded into its slot as soon as sign group s no longer needs that slot.
 // INT8 groups: `raw` points at the symbol words (offset binary).
 // `after_decode` runs as soon as the decode loop no longer needs the word buffer (the caller stages the next group
 // there).
@@ -186,29 +186,35 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
     // word cursors of the two streams (wave-uniform: scalar registers; their advance is scalar work)
     const uint32_t ckv = __builtin_amdgcn_readfirstlane(cnt_kv);
     WordPtr wkk = wk, wvv = wk + (ckv & 0xFFFFu);
-    uint32_t cw[14];  // this sign group's raw words: K N0 N1 C0 N2 N3 C1 S, then V the same
+    // pre[] holds this sign group's raw words (K N0 N1 C0 N2 N3 C1 S, then V the same); each slot is refilled with
+    // the next sign group's word right after its last use here (at least three steps before that word is needed),
+    // and the next sign words go to snx at the sign group's first step.
+    uint32_t snx[2] = {0, 0};
+    auto refill = [&](auto sgc, auto wc) {  // slots w (K) and 7 + w (V) <- word w of sign group sgc + 1
+      constexpr int sn = decltype(sgc)::value + 1, w = decltype(wc)::value;
+      if constexpr (sn < D / 32) {
+        pre[w] = raw[(7 * sn + w) * 64 + lane];
+        pre[7 + w] = raw[RAW + (7 * sn + w) * 64 + lane];
+      } else if (nlw) {
+        pre[w] = nlw[w * 64 + lane];
+        pre[7 + w] = nlw[RAW + w * 64 + lane];
+      }
+    };
     // step P decodes quads 2P and 2P + 1 of K and of V: two independent rANS steps
     [&]<int... P>(std::integer_sequence<int, P...>) {
       (
           [&] {
             constexpr int sg = P / 4, m = P % 4, q0 = 2 * P;
             constexpr uint32_t rA = kFrame[2 * m], rB = kFrame[2 * m + 1];
-            if constexpr (m == 0) {  // sign group sg: take the prefetched words, start the next group's
-#pragma unroll
-              for (int w = 0; w < 14; ++w) cw[w] = pre[w];
-              vsg[sg] = cw[13];
+            using SG = std::integral_constant<int, sg>;
+            if constexpr (m == 0) {
+              vsg[sg] = pre[13];  // V signs, kept for the V phase
               if constexpr (sg + 1 < D / 32) {
-#pragma unroll
-                for (int w = 0; w < 7; ++w) {
-                  pre[w] = raw[(7 * (sg + 1) + w) * 64 + lane];
-                  pre[7 + w] = raw[RAW + (7 * (sg + 1) + w) * 64 + lane];
-                }
+                snx[0] = raw[(7 * (sg + 1) + 6) * 64 + lane];
+                snx[1] = raw[RAW + (7 * (sg + 1) + 6) * 64 + lane];
               } else if (nlw) {
-#pragma unroll
-                for (int w = 0; w < 7; ++w) {
-                  pre[w] = nlw[w * 64 + lane];
-                  pre[7 + w] = nlw[RAW + w * 64 + lane];
-                }
+                snx[0] = nlw[6 * 64 + lane];
+                snx[1] = nlw[RAW + 6 * 64 + lane];
               }
             }
             const uint2 ek = rans_lookup(s_tab[0], xk), ev = rans_lookup(s_tab[1], xv);
@@ -222,11 +228,18 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
             const uint32_t spv = rA ? __builtin_amdgcn_alignbit(ev.y, ev.y, 32 - rA) : ev.y;
             constexpr int nw = kNWord[m], cwi = m < 2 ? 2 : 5;
             k_mfma(std::integral_constant<int, q0>{},
-                   sm_to_half4(quad_mag<rA>(cw[nw], cw[cwi], spk), quad_signs<rA>(cw[6])));
+                   sm_to_half4(quad_mag<rA>(pre[nw], pre[cwi], spk), quad_signs<rA>(pre[6])));
             k_mfma(std::integral_constant<int, q0 + 1>{},
-                   sm_to_half4(quad_mag<rB>(cw[nw], cw[cwi], spk), quad_signs<rB>(cw[6])));
-            vb[q0] = quad_mag<rA>(cw[7 + nw], cw[7 + cwi], spv);
-            vb[q0 + 1] = quad_mag<rB>(cw[7 + nw], cw[7 + cwi], spv);
+                   sm_to_half4(quad_mag<rB>(pre[nw], pre[cwi], spk), quad_signs<rB>(pre[6])));
+            vb[q0] = quad_mag<rA>(pre[7 + nw], pre[7 + cwi], spv);
+            vb[q0 + 1] = quad_mag<rB>(pre[7 + nw], pre[7 + cwi], spv);
+            // refill what this step used for the last time in this sign group
+            refill(SG{}, std::integral_constant<int, nw>{});
+            if constexpr (m == 1 || m == 3) refill(SG{}, std::integral_constant<int, cwi>{});
+            if constexpr (m == 3) {
+              pre[6] = snx[0];
+              pre[13] = snx[1];
+            }
           }(),
           ...);
     }(std::make_integer_sequence<int, D / 8>{});

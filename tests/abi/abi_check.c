@@ -17,6 +17,7 @@
 #include "chromofold/kv_codec_ext.h"
 #include "chromofold/kv_cuda.h"
 #include "chromofold/kv_runtime.h"
+#include "chromofold/chromofold_measure.h"
 
 static int failures = 0;
 
@@ -105,6 +106,8 @@ int main(void) {
          cf_kv_encode_groups_async(2, NULL, NULL, 1, NULL, NULL, NULL, 64, NULL, 2, NULL, NULL, NULL, 0, 0, NULL, NULL,
                                    NULL, NULL, 0, NULL), INV);
   expect("cf_kv_encode_groups_workspace_bytes", cf_kv_encode_groups_workspace_bytes(2, 20, 1, 2) == 0, 1);
+  /* chromofold_measure.h */
+  expect("cf_stream_read_async", cf_stream_read_async(NULL, 16, NULL, NULL), INV);
   {
     cf_rrrw_file_header rh;
     cf_fm_file_header fh;
