@@ -9,7 +9,8 @@ int8 per-page-per-head absmax scale + rANS per page), context 32768, batch 32. O
 32 sequences through one layer. The wavelet-rank figure (configs[0] shape, 1M rank queries) rides along under
 "secondary". Inputs are seeded synthetic data already resident in HBM when timing starts.
 
-Timing: W untimed warmup steps, then exactly K steps bracketed by torch.cuda.synchronize(); per-launch kernel
+Timing: untimed back-to-back launches for at least 3 s (and at least W of them), so that the chip's clocks settle
+where they stay under continuous load, then exactly K steps bracketed by torch.cuda.synchronize(); per-launch kernel
 durations come from HIP events recorded on the stream the kernels run on (torch's current stream, whose handle
 is what the C ABI receives).
 """
@@ -222,79 +223,125 @@ def bench_qw(steps: int, warmup: int, batches=(1, 4, 16, 64)) -> dict:
 
 
 # ------------------------------------------------------------------------------------------------ paged KV (C4)
-def bench_kv(steps: int, warmup: int, context: int = 32768, batch: int = 32, codec: int = 2, cpu: bool = True,
-             check_seqs: int = 2) -> dict:
+def _sustained_time(fn, steps: int, warmup: int, warm_s: float):
+    """Back-to-back launches for at least warm_s seconds (and `warmup` launches) so that the clocks reach the state
+    they hold under continuous load, then `steps` timed launches, each bracketed by events on the launch stream.
+    Returns (wall ms of the timed launches, per-launch ms)."""
+    import torch
+    t0 = time.perf_counter()
+    n = 0
+    while n < warmup or time.perf_counter() - t0 < warm_s:
+        for _ in range(20):
+            fn()
+        n += 20
+        torch.cuda.synchronize()
+    return _events_time(fn, steps, 0)
+
+
+def bench_stream_read(buf, steps: int = 20, warmup: int = 3) -> dict:
+    """The device's achievable HBM read bandwidth: cf_stream_read_async (16-byte loads, each byte read once) over
+    `buf` (a uint8 device tensor of >= 2 GB, e.g. the KV pool itself)."""
+    import torch
+    from chromofold_amd import _abi as A
+    A.declare("cf_stream_read_async", A.I32, [A.P, A.U64, A.P, A.P])
+    n = (buf.numel() // 16) * 16
+    sink = torch.zeros(1, dtype=torch.int32, device=buf.device)
+    s = torch.cuda.current_stream().cuda_stream
+
+    def read():
+        A.check(A.lib().cf_stream_read_async(buf.data_ptr(), n, sink.data_ptr(), s), "cf_stream_read_async")
+    _, per = _events_time(read, steps, warmup)
+    t = float(np.median(per)) * 1e-3
+    return {"bytes": n, "ms": t * 1e3, "read_gbs": n / t / 1e9}
+
+
+def bench_kv(steps: int, warmup: int, context: int = 32768, batch: int = 32, cpu: bool = True,
+             check_seqs: int = 8, warm_s: float = 3.0, stream_peak: bool = True) -> dict:
+    """Llama-3-8B layer shape (32 q / 8 KV heads, hd 128, 16-token pages), K/V ~ N(0,1) fp32
+    generated on the device (seeded), sealed on the device into RANS_HYBRID page groups (per-page-per-head int8
+    absmax, rANS) with cf_kv_encode_groups_async; one decode token per sequence per step.
+    Gate: the first check_seqs sequences' outputs against the float64 oracle over the pool's own blobs (decoded by
+    the oracle), every (sequence, head) row within 1e-3 normwise. The same oracle run on all host threads is the
+    CPU baseline (plus its 1-thread figure on one sequence)."""
     import torch
     from chromofold_amd import kv, synth
 
     H, QH, D = 8, 32, 128
     gqa = QH // H
-    rng = np.random.default_rng(synth.SEED_C4)
     t0 = time.perf_counter()
-    # synthetic K/V ~ N(0,1), one sequence at a time (host memory stays ~0.3 GB per sequence)
-    seeds = rng.integers(0, 2 ** 63, size=batch)
-
-    def source(s):
-        g = np.random.default_rng(int(seeds[s]))
-        return (g.standard_normal((H, context, D), dtype=np.float32),
-                g.standard_normal((H, context, D), dtype=np.float32))
-
-    tables = None
-    if codec == kv.CODEC_RANS_HYBRID:
-        K0, V0 = source(0)
-        tables = np.concatenate([t for h in range(H) for t in (kv.build_table(K0[h, :1024].reshape(-1, 16, D)),
-                                                               kv.build_table(V0[h, :1024].reshape(-1, 16, D)))])
-        del K0, V0
-    kvb = kv.build_batched(codec, source, batch, H, np.full(batch, context, np.uint32), D, tables, "cuda:0",
-                           keep_host=cpu or check_seqs > 0)
-    t_build = time.perf_counter() - t0
-    q = rng.standard_normal((batch, QH, D), dtype=np.float32)
-    qp = np.full(batch, context - 1, np.uint32)
-    sc = 1.0 / np.sqrt(D)
-    dq = torch.from_numpy(q).to("cuda:0")
-    dqp = torch.from_numpy(qp.view(np.int32)).to("cuda:0")
-    out = torch.empty_like(dq)
-    desc = kvb.desc(dq, out, dqp, sc)
-    kvb.attention(dq, out, dqp, sc, desc=desc)
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(synth.SEED_C4 + context)
+    K = torch.randn((batch, H, context, D), generator=gen, device="cuda:0")
+    V = torch.randn((batch, H, context, D), generator=gen, device="cuda:0")
+    Kh = K[0, 0, :1024].cpu().numpy().reshape(-1, 16, D)
+    Vh = V[0, 0, :1024].cpu().numpy().reshape(-1, 16, D)
+    tables = np.concatenate([t for _ in range(H) for t in (kv.build_table(Kh), kv.build_table(Vh))])
+    kvb = kv.seal_device(kv.CODEC_RANS_HYBRID, K, V, torch.from_numpy(tables).to("cuda:0"))
+    # order-0 entropy of the int8 symbols (sequence 0, every head, K and V; per-page absmax, half to even)
+    pg = torch.cat([K[0], V[0]]).reshape(-1, 16 * D)
+    sym = torch.round(pg / torch.where(pg.abs().amax(1, keepdim=True) == 0, 1.0, pg.abs().amax(1, keepdim=True) / 127))
+    cnt = torch.bincount((sym.clamp(-128, 127) + 128).to(torch.int64).ravel(), minlength=256).double()
+    pr = cnt[cnt > 0] / cnt.sum()
+    h0 = float(-(pr * torch.log2(pr)).sum())
+    del K, V, pg, sym
     torch.cuda.synchronize()
-    got = out.cpu().numpy()
-    res = {"build_s": t_build, "pool_bytes": kvb.pool_bytes}
-    cpu_s = None
-    if check_seqs > 0:  # correctness gate on a few sequences (fp64 oracle on the oracle-decoded pages)
-        sys.path.insert(0, os.path.join(ROOT, "tests"))
-        from kv_helpers import decoded_pages, normwise_err
+    t_build = time.perf_counter() - t0
+    q = torch.randn((batch, QH, D), generator=gen, device="cuda:0")
+    qp = torch.full((batch,), context - 1, dtype=torch.int32, device="cuda:0")
+    sc = 1.0 / np.sqrt(D)
+    out = torch.empty_like(q)
+    desc = kvb.desc(q, out, qp, sc)
+    kvb.attention(q, out, qp, sc, desc=desc)
+    torch.cuda.synchronize()
+    res = {"workload": f"{batch} seqs x {context} tokens, 32 q / 8 KV heads, hd {D}", "build_s": t_build,
+           "pool_bytes": kvb.pool_bytes}
+    if check_seqs > 0:
         import oracle as O
-        errs = []
+        pool_h = kvb.pool.cpu().numpy()
+        offs_h = kvb.group_offsets.cpu().numpy().view(np.uint32)
+        toks_h = np.full(batch, context, np.uint32)
+        qp_h = np.full(batch, context - 1, np.uint32)
+        q_h = q.cpu().numpy()
+        got = out.cpu().numpy()
+        th = O.num_threads()
         tc0 = time.perf_counter()
-        for s in range(check_seqs):
-            pages = []
-            for h in range(H):
-                pages += [(h, t0, k, v) for t0, k, v in decoded_pages(kvb, s, h, context)]
-            ref, _ = O.paged_attention_f64(q[s], QH, H, D, gqa, context - 1, 0, sc, pages)
-            errs.append(normwise_err(got[s], ref))
-        cpu_s = (time.perf_counter() - tc0) / check_seqs
-        res["max_normwise_err"] = max(errs)
-        assert max(errs) <= 1e-3, errs
-    wall, per = _events_time(lambda: kvb.attention(dq, out, dqp, sc, desc=desc), steps, warmup)
+        ref = O.kv_pool_attention(pool_h, offs_h, toks_h, qp_h, tables, q_h, H, D, sc, nseq=check_seqs)
+        t_all = time.perf_counter() - tc0
+        err = np.abs(got[:check_seqs] - ref).max(axis=2) / np.abs(ref).max(axis=2)  # per (sequence, head) row
+        res["max_normwise_err"] = float(err.max())
+        assert err.max() <= 1e-3, float(err.max())
+        if cpu:
+            tc1 = time.perf_counter()
+            O.kv_pool_attention(pool_h, offs_h, toks_h, qp_h, tables, q_h, H, D, sc, nseq=1, threads=1)
+            t_one = time.perf_counter() - tc1
+            res["cpu_baseline"] = {
+                "value": check_seqs / t_all, "unit": "tokens/s", "cores": th, "kind": "port",
+                "sample": f"{check_seqs} sequences x 1 decode token at {context} context (all 8 KV heads): oracle "
+                          f"group decode + float64 attention, OpenMP on {th} threads (nproc {os.cpu_count()})",
+                "one_thread": {"value": 1.0 / t_one, "unit": "tokens/s", "cores": 1,
+                               "sample": f"1 sequence x 1 decode token at {context} context, 1 thread"}}
+        del pool_h
+    wall, per = _sustained_time(lambda: kvb.attention(q, out, qp, sc, desc=desc), steps, warmup, warm_s)
     t_step = float(np.mean(per)) * 1e-3
     # algorithmic bytes per step: every visible page blob (payload + header + states), tables once, page table,
     # queries and outputs
-    table_bytes = 0 if tables is None else tables.size
-    step_bytes = kvb.pool_bytes + table_bytes + batch * H * (context // 64) * 4 + 2 * q.nbytes
+    step_bytes = kvb.pool_bytes + tables.size + batch * H * (context // 64) * 4 + 2 * q.numel() * 4
     values = 2 * batch * H * context * D
     res.update({
         "tokens_per_s": batch / t_step, "ms_per_step": wall / steps, "kernel_ms": t_step * 1e3,
-        "bits_per_value": kvb.pool_bytes * 8.0 / values,
+        "kernel_ms_min": float(np.min(per)), "kernel_ms_max": float(np.max(per)),
+        "bits_per_value": kvb.pool_bytes * 8.0 / values, "int8_bits_per_value": 8.0 + 8.0 * 64 / (16 * D * 4 * 2),
+        "symbol_entropy_bits": h0,
         "ratio_vs_bf16": (values * 2.0) / kvb.pool_bytes,
         "roofline": {"bound": "hbm", "achieved": step_bytes / t_step / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": step_bytes / t_step / 1e9 / HBM_PEAK_GBS,
                      "traffic": MEASURED_TRAFFIC.get(("kv", context, batch))},
         "step_bytes": step_bytes,
     })
-    if cpu_s is not None:
-        res["cpu_baseline"] = {"value": 1.0 / cpu_s, "unit": "tokens/s", "cores": 1, "kind": "port",
-                               "sample": f"{check_seqs} sequences x 1 decode token at {context} context: oracle "
-                                         f"page decode + fp64 paged attention (32 q heads), single thread"}
+    if stream_peak:
+        sr = bench_stream_read(kvb.pool)
+        res["hbm_read_peak_gbs"] = sr["read_gbs"]
+        res["frac_of_read_peak"] = res["roofline"]["achieved"] / sr["read_gbs"]
     return res
 
 
@@ -330,9 +377,12 @@ def bench_seal(steps: int, warmup: int, cpu: bool = True, seqs: int = 32, tokens
     ws = torch.empty(int(A.lib().cf_kv_encode_groups_workspace_bytes(kv.CODEC_RANS_HYBRID, D, ngroups, 2 * H)),
                      dtype=torch.uint8, device="cuda:0")
 
+    cont = ((np.arange(ngroups) % (tokens // 64)) % 2).astype(np.uint8)  # groups 2k, 2k + 1 of a head: one chain
+    d_cont = torch.from_numpy(cont).to("cuda:0")
+
     def seal():
         return kv.encode_groups_device(kv.CODEC_RANS_HYBRID, K, V, D, d_tab, d_first, d_counts, pool, 0, d_heads,
-                                       None, ws)
+                                       None, ws, continues=d_cont)
 
     r = seal()
     torch.cuda.synchronize()
@@ -340,7 +390,7 @@ def bench_seal(steps: int, warmup: int, cpu: bool = True, seqs: int = 32, tokens
     end = int(r.pool_end.item())
     n_chk = 64
     host, hoff = kv.encode_groups(kv.CODEC_RANS_HYBRID, Ks, Vs, D, tables, first[:n_chk], np.full(n_chk, 4),
-                                  heads[:n_chk].astype(np.uint32))
+                                  heads[:n_chk].astype(np.uint32), continues=cont[:n_chk])
     assert np.array_equal(r.offsets[:n_chk].cpu().numpy().view(np.uint32), hoff), "device offsets != host"
     assert np.array_equal(pool[:host.size].cpu().numpy(), host), "device-sealed bytes != host encoder bytes"
     wall, per = _events_time(seal, steps, warmup)
@@ -356,7 +406,7 @@ def bench_seal(steps: int, warmup: int, cpu: bool = True, seqs: int = 32, tokens
         th = min(16, os.cpu_count() or 1)  # the box's CPU share for one GPU
         t0 = time.perf_counter()
         kv.encode_groups(kv.CODEC_RANS_HYBRID, Kh, Vh, D, tables, first[:n], np.full(n, 4),
-                         heads[:n].astype(np.uint32), threads=th)
+                         heads[:n].astype(np.uint32), threads=th, continues=cont[:n])
         dt = time.perf_counter() - t0
         res["cpu_baseline"] = {"value": n / dt, "unit": "groups/s", "cores": th, "kind": "port",
                                "sample": f"{n} groups with the library's host encoder on {th} threads"}
@@ -675,27 +725,33 @@ def main() -> int:
         print(json.dumps({"nibble_pages": bench_nibble(args.steps, args.warmup, cpu=not args.no_cpu)}))
         return 0
     if args.workload in ("auto", "kv"):
-        kvr = bench_kv(args.steps, args.warmup, cpu=not args.no_cpu, check_seqs=0 if args.no_cpu else 2)
-        rrr = bench_rrr(args.steps, args.warmup, cpu=not args.no_cpu)
+        kvr = bench_kv(args.steps, args.warmup, cpu=not args.no_cpu, check_seqs=8)
         secondary = {k: v for k, v in kvr.items() if k not in ("roofline", "cpu_baseline", "tokens_per_s")}
-        secondary["wavelet_rank_mqs"] = rrr["rank_mqs"]
-        secondary["wavelet_access_mqs"] = rrr["access_mqs"]
-        secondary["wavelet_rank_roofline_frac"] = rrr["rank_roofline"]["frac"]
-        secondary["wavelet_cpu_baseline"] = rrr.get("cpu_baseline")
-        secondary["c1_rrr"] = {k: v for k, v in rrr.items() if k not in ("rank_roofline", "cpu_baseline")}
-        secondary["c2_fm"] = bench_fm(min(args.steps, 20), 2, cpu=not args.no_cpu)
-        secondary["c3_matmul"] = bench_qw(min(args.steps, 50), 3)
-        secondary["c5_long_context"] = bench_c5(min(args.steps, 20), 2)
-        secondary["device_seal"] = bench_seal(min(args.steps, 20), 2, cpu=not args.no_cpu)
-        secondary["nibble_pages"] = bench_nibble(min(args.steps, 20), 2, cpu=not args.no_cpu)
-        secondary["gathers"] = bench_gather(min(args.steps, 20), 2)
-        cp = bench_copy(10, 2)
-        secondary["stream_copy_gbs"] = cp["stream_copy_gbs"]
-        secondary["roofline_frac_of_stream_copy"] = kvr["roofline"]["achieved"] / cp["stream_copy_gbs"]
+        k4 = bench_kv(min(args.steps, 50), 3, context=4096, cpu=False, check_seqs=4, warm_s=1.0, stream_peak=False)
+        secondary["c4_4k"] = {k: k4[k] for k in ("workload", "tokens_per_s", "ms_per_step", "kernel_ms",
+                                                 "bits_per_value", "max_normwise_err")}
+        secondary["c4_4k"]["roofline_frac"] = k4["roofline"]["frac"]
+        if args.workload == "auto":
+            rrr = bench_rrr(args.steps, args.warmup, cpu=not args.no_cpu)
+            secondary["wavelet_rank_mqs"] = rrr["rank_mqs"]
+            secondary["wavelet_access_mqs"] = rrr["access_mqs"]
+            secondary["wavelet_rank_roofline_frac"] = rrr["rank_roofline"]["frac"]
+            secondary["wavelet_cpu_baseline"] = rrr.get("cpu_baseline")
+            secondary["c1_rrr"] = {k: v for k, v in rrr.items() if k not in ("rank_roofline", "cpu_baseline")}
+            secondary["c2_fm"] = bench_fm(min(args.steps, 20), 2, cpu=not args.no_cpu)
+            secondary["c3_matmul"] = bench_qw(min(args.steps, 50), 3)
+            secondary["c5_long_context"] = bench_c5(min(args.steps, 20), 2)
+            secondary["device_seal"] = bench_seal(min(args.steps, 20), 2, cpu=not args.no_cpu)
+            secondary["nibble_pages"] = bench_nibble(min(args.steps, 20), 2, cpu=not args.no_cpu)
+            secondary["gathers"] = bench_gather(min(args.steps, 20), 2)
+            cp = bench_copy(10, 2)
+            secondary["stream_copy_gbs"] = cp["stream_copy_gbs"]
+            secondary["roofline_frac_of_stream_copy"] = kvr["roofline"]["achieved"] / cp["stream_copy_gbs"]
         line = {
             "metric": METRIC, "value": kvr["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": kvr["ms_per_step"], "higher_is_better": True, "scaling": "weak",
-            "vs_baseline": None, "dtype": "u8->f16 MFMA, f32 accumulate", "data": "synthetic (seeded N(0,1) K/V)",
+            "vs_baseline": None, "dtype": "u8 (sign-magnitude int8 -> exact f16 MFMA operands), f32 accumulate",
+            "data": "synthetic (seeded N(0,1) K/V generated on the device)",
             "config": {"workload": "paged-KV decode, rANS-hybrid int8 pages, 32 seqs x 32768 ctx, 32 q / 8 kv heads, "
                                    "head_dim 128, 16-token pages, 1 layer, 1 decode token per seq"},
             "roofline": kvr["roofline"], "cpu_baseline": kvr.get("cpu_baseline"), "secondary": secondary,

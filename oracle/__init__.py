@@ -88,6 +88,7 @@ def _declare(L):
         "or_dense_attention_f64": (None, [P, U32, P, P, U32, C.c_float, P]),
         "or_kv_window_attention_f64": (None, [P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, P]),
         "or_kv_decode_group": (C.c_int, [P, P, U32, P, P, P, P, P, P, P]),
+        "or_kv_pool_attention": (C.c_int, [P, P, U32, P, P, P, P, U32, U32, U32, U32, C.c_float, P, C.c_int]),
         "or_kv_quantize_page_absmax": (None, [P, U32, P, P]),
         "or_nib_seal": (C.c_int, [P, U32, U32, P, P, P, P, P]),
         "or_nib_attention": (None, [U32, P, P, P, P, P, P, U32, P, P, U32, U32, P, U32, U32, U32, U32, U32,
@@ -368,6 +369,27 @@ def kv_decode_run(blobs, tables, head: int, head_dim: int):
             raise ValueError(f"chain ending at group {g} does not return to the initial states")
         states = st if is_rans else None
         out.append((ks, vs, ksc, vsc, tc))
+    return out
+
+
+def kv_pool_attention(pool, group_offsets, seq_tokens, query_pos, tables, queries, kv_heads: int, head_dim: int,
+                      softmax_scale: float, nseq: int | None = None, threads: int = 0):
+    """float64 attention of one query row per sequence over a batched pool (host copies of the cf_kv_batched_desc
+    arrays; group_offsets [S, H, max_groups]), for the first `nseq` sequences on `threads` OpenMP threads (0 = all).
+    Returns out [nseq, q_heads, D] float32; raises when a blob fails to decode."""
+    group_offsets = np.ascontiguousarray(group_offsets, np.uint32)
+    S, H, G = group_offsets.shape
+    nseq = S if nseq is None else nseq
+    queries = np.ascontiguousarray(queries, np.float32)
+    qh = queries.shape[1]
+    out = np.zeros((nseq, qh, head_dim), np.float32)
+    bad = lib().or_kv_pool_attention(_ptr(np.ascontiguousarray(pool, np.uint8)), _ptr(group_offsets), G,
+                                     _ptr(np.ascontiguousarray(seq_tokens, np.uint32)),
+                                     _ptr(np.ascontiguousarray(query_pos, np.uint32)),
+                                     _ptr(np.ascontiguousarray(tables, np.uint8)), _ptr(queries), nseq, H, qh,
+                                     head_dim, softmax_scale, _ptr(out), threads)
+    if bad:
+        raise ValueError(f"{bad} (sequence, head) units failed to decode")
     return out
 
 

@@ -285,6 +285,69 @@ int or_kv_decode_group(const uint8_t *blob, const uint8_t *tables, uint32_t head
   return 0;
 }
 
+// Batched pool attention on the host (the CPU baseline of the batched decode, and a checker at full size): for
+// every (sequence, KV head) of the first nseq sequences, decode its groups in token order with or_kv_decode_group
+// (chain states carried from a group to the one that continues it), dequantise (q - 128) * scale, and compute the
+// float64 softmax attention of the sequence's one query row for the gqa query heads of that KV head over the tokens
+// [0, min(seq_tokens, query_pos + 1)). Layouts as cf_kv_batched_desc (group_offsets [nseq][kv_heads][max_groups]
+// in 16-byte units, queries / out [nseq][q_heads][D]). Parallel over (sequence, head) on `threads` OpenMP threads
+// (0 = all). Returns the number of (sequence, head) units whose blobs failed to decode (their rows are NaN).
+int or_kv_pool_attention(const uint8_t *pool, const uint32_t *group_offsets, uint32_t max_groups,
+                         const uint32_t *seq_tokens, const uint32_t *query_pos, const uint8_t *tables,
+                         const float *queries, uint32_t nseq, uint32_t kv_heads, uint32_t q_heads, uint32_t D,
+                         float softmax_scale, float *out, int threads) {
+  const uint32_t gqa = q_heads / kv_heads;
+  int bad = 0;
+#pragma omp parallel for schedule(dynamic) reduction(+ : bad) num_threads(threads > 0 ? threads : omp_get_max_threads())
+  for (int64_t u = 0; u < (int64_t)nseq * kv_heads; ++u) {
+    const uint32_t s = (uint32_t)(u / kv_heads), h = (uint32_t)(u % kv_heads);
+    const uint32_t vis = std::min(seq_tokens[s], query_pos[s] + 1);
+    const uint32_t ng = (vis + 63) / 64;
+    std::vector<double> Kd((size_t)ng * 64 * D), Vd((size_t)ng * 64 * D);
+    std::vector<uint8_t> ks((size_t)4 * 16 * D), vs((size_t)4 * 16 * D);
+    float ksc[4], vsc[4];
+    uint32_t tc[4], st[128] = {0}, chain = 0;
+    bool ok = true;
+    for (uint32_t g = 0; g < ng && ok; ++g) {
+      const uint8_t *blob = pool + (size_t)group_offsets[((size_t)s * kv_heads + h) * max_groups + g] * 16;
+      ok = or_kv_decode_group(blob, tables, h, ks.data(), vs.data(), ksc, vsc, tc, st, &chain) == 0;
+      for (uint32_t G = 0; G < 4; ++G)
+        for (uint32_t t = 0; t < 16; ++t)
+          for (uint32_t d = 0; d < D; ++d) {
+            const size_t src = ((size_t)G * 16 + t) * D + d, dst = ((size_t)g * 64 + G * 16 + t) * D + d;
+            Kd[dst] = ((double)ks[src] - 128.0) * ksc[G];
+            Vd[dst] = ((double)vs[src] - 128.0) * vsc[G];
+          }
+    }
+    if (!ok) ++bad;
+    std::vector<double> p(vis);
+    for (uint32_t i = 0; i < gqa; ++i) {
+      const uint32_t qh = h * gqa + i;
+      const float *q = queries + ((size_t)s * q_heads + qh) * D;
+      float *o = out + ((size_t)s * q_heads + qh) * D;
+      if (!ok) {
+        for (uint32_t d = 0; d < D; ++d) o[d] = NAN;
+        continue;
+      }
+      double m = -INFINITY;
+      for (uint32_t t = 0; t < vis; ++t) {
+        double acc = 0;
+        for (uint32_t d = 0; d < D; ++d) acc += (double)q[d] * Kd[(size_t)t * D + d];
+        p[t] = acc * softmax_scale;
+        m = std::max(m, p[t]);
+      }
+      double l = 0;
+      for (uint32_t t = 0; t < vis; ++t) l += (p[t] = std::exp(p[t] - m));
+      for (uint32_t d = 0; d < D; ++d) {
+        double acc = 0;
+        for (uint32_t t = 0; t < vis; ++t) acc += p[t] * Vd[(size_t)t * D + d];
+        o[d] = vis ? (float)(acc / l) : 0.0f;
+      }
+    }
+  }
+  return bad;
+}
+
 // per-page-per-head absmax int8 quantiser of the benchmark configuration (scale = max|x|/127, 0 -> 1;
 // sym = clamp(lrint(x / scale), -128, 127) + 128) — the kv_gpu_fixture convention with one scale per page.
 void or_kv_quantize_page_absmax(const float *x, uint32_t n, uint8_t *sym, float *scale) {

@@ -283,3 +283,27 @@ def test_mixed_pool_raw_prefix(kv):
                 assert np.array_equal(mixed.host_offsets[s, h, :2], mixed.host_offsets[0, h, :2])
     with pytest.raises(ValueError):
         kv.build_batched(kv.CODEC_RANS_HYBRID, *args, tables, "cpu", encoder="device", raw_groups={0: 1})
+
+
+def test_pool_attention_matches_paged_oracle(kv):
+    """O.kv_pool_attention (the all-core CPU baseline: decode every group of a batched pool, chains in order, and
+    attend in float64) equals the paged fp64 oracle (O.paged_attention_f64, pinned against the reference's
+    kv_reference.cpp) over the same decoded pages, for ragged lengths, a causal query position, GQA 4, chain pairs
+    and a raw INT8 group inside the pool; and agrees with itself on 1 and on all threads."""
+    from kv_helpers import make_seqs, oracle_batched
+    D, H, gqa = 64, 2, 4
+    toks = [300, 129, 64, 700]
+    data = make_seqs(toks, H, D, 123)
+    tables = np.concatenate([kv.build_table(data[0][i][h][:256].reshape(-1, 16, D)) for h in range(H) for i in (0, 1)])
+    kvb = kv.build_batched(2, lambda s: data[s], len(toks), H, np.array(toks), D, tables, "cpu", keep_host=True,
+                           raw_groups={1: 1})
+    rng = np.random.default_rng(124)
+    q = rng.standard_normal((len(toks), H * gqa, D)).astype(np.float32)
+    qp = np.array([299, 100, 63, 699], np.uint32)
+    sc = 1.0 / np.sqrt(D)
+    ref = oracle_batched(kvb, data, q, qp, sc, gqa)
+    got = O.kv_pool_attention(kvb.host_pool, kvb.host_offsets, np.array(toks, np.uint32), qp, tables, q, H, D, sc)
+    assert np.abs(got - ref).max() <= 1e-6 * np.abs(ref).max()
+    one = O.kv_pool_attention(kvb.host_pool, kvb.host_offsets, np.array(toks, np.uint32), qp, tables, q, H, D, sc,
+                              nseq=2, threads=1)
+    assert np.array_equal(one, got[:2])
