@@ -694,9 +694,11 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="auto", choices=["auto", "kv", "rrr", "copy", "c5", "seal", "nibble",
-                                                                  "gather"])
+    ap.add_argument("--workload", default="auto", choices=["auto", "kv", "kv32", "rrr", "copy", "c5", "seal",
+                                                                  "nibble", "gather"])
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--warm-s", type=float, default=3.0,
+                    help="seconds of untimed back-to-back launches before the timed KV steps (0 for counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the hot path shards "
@@ -724,13 +726,16 @@ def main() -> int:
     if args.workload == "nibble":
         print(json.dumps({"nibble_pages": bench_nibble(args.steps, args.warmup, cpu=not args.no_cpu)}))
         return 0
-    if args.workload in ("auto", "kv"):
-        kvr = bench_kv(args.steps, args.warmup, cpu=not args.no_cpu, check_seqs=8)
+    if args.workload in ("auto", "kv", "kv32"):
+        kvr = bench_kv(args.steps, args.warmup, cpu=not args.no_cpu, check_seqs=0 if args.no_cpu else 8,
+                       warm_s=args.warm_s, stream_peak=args.workload != "kv32")
         secondary = {k: v for k, v in kvr.items() if k not in ("roofline", "cpu_baseline", "tokens_per_s")}
-        k4 = bench_kv(min(args.steps, 50), 3, context=4096, cpu=False, check_seqs=4, warm_s=1.0, stream_peak=False)
-        secondary["c4_4k"] = {k: k4[k] for k in ("workload", "tokens_per_s", "ms_per_step", "kernel_ms",
-                                                 "bits_per_value", "max_normwise_err")}
-        secondary["c4_4k"]["roofline_frac"] = k4["roofline"]["frac"]
+        if args.workload != "kv32":
+            k4 = bench_kv(min(args.steps, 50), 3, context=4096, cpu=False, check_seqs=4,
+                          warm_s=min(args.warm_s, 1.0), stream_peak=False)
+            secondary["c4_4k"] = {k: k4[k] for k in ("workload", "tokens_per_s", "ms_per_step", "kernel_ms",
+                                                     "bits_per_value", "max_normwise_err")}
+            secondary["c4_4k"]["roofline_frac"] = k4["roofline"]["frac"]
         if args.workload == "auto":
             rrr = bench_rrr(args.steps, args.warmup, cpu=not args.no_cpu)
             secondary["wavelet_rank_mqs"] = rrr["rank_mqs"]

@@ -1,7 +1,10 @@
 // kv_batched.hip — batched compressed paged-KV attention decode on gfx950 (kv_codec_ext.h entry point).
 //
-// One workgroup = 4 wavefronts serves one (sequence, KV head, context split). Each wavefront walks "page quads":
-// four consecutive 16-token pages, one per 16-lane group. Lane (G, t) = lane 16G + t:
+// One workgroup serves one (sequence, KV head, context split): 12 wavefronts (one workgroup per CU) for long
+// contexts, 4 (three workgroups per CU) for short ones. Its wavefronts take the chain pairs of the split from an LDS
+// counter one at a time, so that wavefronts the CU serves faster (issue arbitration favours the oldest) take more
+// pairs and all finish together. Each wavefront walks "page quads": four consecutive 16-token pages, one per
+// 16-lane group. Lane (G, t) = lane 16G + t:
 //   K phase: lane decodes token t of page G (its 16 interleaved rANS states are the 16 lanes of the group);
 //            every decoded quad of 4 dims goes straight into v_mfma_f32_4x4x4f16 as the B operand, with the
 //            GQA group's 4 query heads (split into f16 hi + lo parts for fp32-grade scores) as the A operand, so
@@ -36,13 +39,13 @@ namespace {
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
-// Occupancy floor for the compiler (3 wavefronts per SIMD: <= 168 VGPRs); the LDS footprint below allows 3
-// four-wavefront workgroups per CU.
+// Occupancy floor for the compiler (3 wavefronts per SIMD: <= 168 VGPRs); the LDS footprint below allows one
+// 12-wavefront or three 4-wavefront workgroups per CU.
 #ifndef CF_KV_WPE
 #define CF_KV_WPE 3
 #endif
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
+constexpr int kWavesWide = 12;   // one workgroup per CU
+constexpr int kWavesNarrow = 4;  // three workgroups per CU
 constexpr int kGqa = 4;            // MFMA rows: query heads of one KV head (gqa < 4 pads with zero queries)
 constexpr uint32_t kSlots = 1u << CF_KV_RANS_PROB_BITS;
 constexpr float kOffset = 1152.0f;  // f16 operand = 1024 + symbol, symbol = q + 128
@@ -162,18 +165,27 @@ constexpr int buf_u32() {
 // INT8 groups: `raw` points at the symbol words (offset binary).
 // `after_decode` runs as soon as the decode loop no longer needs the word buffer (the caller stages the next group
 // there).
-template <int D, int CODEC, typename WordPtr, typename Hook>
+// V quads 0..KL-1 do not wait for the V phase in registers: the decode parks them in the wave's LDS area `vl`
+// ([KL][64] words) (RANS), or the V phase loads them again from `raw` (INT8 groups, rare in the launches that use
+// KL > 0). The registers this frees keep the 12-wave kernel free of spills.
+template <int D, int CODEC, int KL, typename WordPtr, typename Hook>
 __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&pre)[14], const uint32_t *nlw,
                                            uint32_t (&st)[2], const uint32_t *__restrict__ raw, WordPtr wk,
                                            uint32_t cnt_kv, const uint2 (*__restrict__ s_tab)[kSlots],
                                            const half4_t *qhi, const half4_t *qlo, const float *qsum,
-                                           _Float16 (*s_pw)[kGqa][16], int lane, bool tok_ok, float ks, float vs,
-                                           int &e_run, float *m_run, float *l_run, float4_t *acc_v) {
+                                           _Float16 (*s_pw)[kGqa][16], uint32_t *__restrict__ vl, int lane,
+                                           bool tok_ok, float ks, float vs, int &e_run, float *m_run, float *l_run,
+                                           float4_t *acc_v) {
   constexpr int NQ = D / 4, RAW = raw_words<D>();
   constexpr bool RANS = CODEC == CF_KV_CODEC_RANS_HYBRID;
   const int G = lane >> 4, t = lane & 15;
   float4_t sa = {0, 0, 0, 0}, sb = {0, 0, 0, 0};
   uint32_t vb[NQ];                         // V: magnitude bytes (RANS) or offset-binary symbols (INT8) per quad
+  auto put_v = [&](auto qc, uint32_t v) {
+    constexpr int q = decltype(qc)::value;
+    if constexpr (q < KL) vl[q * 64 + lane] = v;
+    else vb[q] = v;
+  };
   uint32_t vsg[RANS ? D / 32 : 1];         // V sign words per sign group (RANS)
   // K MFMAs of quad q (A = the 4 query heads broadcast from block q % 16, hi and lo parts)
   auto k_mfma = [&](auto qc, half4_t bk) {
@@ -231,8 +243,8 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
                    sm_to_half4(quad_mag<rA>(pre[nw], pre[cwi], spk), quad_signs<rA>(pre[6])));
             k_mfma(std::integral_constant<int, q0 + 1>{},
                    sm_to_half4(quad_mag<rB>(pre[nw], pre[cwi], spk), quad_signs<rB>(pre[6])));
-            vb[q0] = quad_mag<rA>(pre[7 + nw], pre[7 + cwi], spv);
-            vb[q0 + 1] = quad_mag<rB>(pre[7 + nw], pre[7 + cwi], spv);
+            put_v(std::integral_constant<int, q0>{}, quad_mag<rA>(pre[7 + nw], pre[7 + cwi], spv));
+            put_v(std::integral_constant<int, q0 + 1>{}, quad_mag<rB>(pre[7 + nw], pre[7 + cwi], spv));
             // refill what this step used for the last time in this sign group
             refill(SG{}, std::integral_constant<int, nw>{});
             if constexpr (m == 1 || m == 3) refill(SG{}, std::integral_constant<int, cwi>{});
@@ -254,7 +266,7 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
       }
     }
     [&]<int... Q>(std::integer_sequence<int, Q...>) {
-      ((vb[Q] = raw[NQ * 64 + Q * 64 + lane],
+      ((Q < KL ? void() : void(vb[Q] = raw[NQ * 64 + Q * 64 + lane]),
         k_mfma(std::integral_constant<int, Q>{}, bytes_to_half4(raw[Q * 64 + lane]))), ...);
     }(std::make_integer_sequence<int, NQ>{});
   }
@@ -311,9 +323,9 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
           const half4_t pa = *reinterpret_cast<const half4_t *>(&s_pw[G][lane & 3][4 * tq]);
           half4_t bv;
           if constexpr (RANS)  // quad q is quad q % 8 of sign group q / 8
-            bv = sm_to_half4(vb[q], quad_signs<kFrame[q % 8]>(vsg[q / 8]));
+            bv = sm_to_half4(q < KL ? vl[q * 64 + lane] : vb[q], quad_signs<kFrame[q % 8]>(vsg[q / 8]));
           else
-            bv = bytes_to_half4_signed(vb[q]);
+            bv = bytes_to_half4_signed(q < KL ? raw[NQ * 64 + q * 64 + lane] : vb[q]);
           acc_v[i] = mfma4(pa, bv, acc_v[i]);
         }(),
         ...);
@@ -336,31 +348,36 @@ struct SplitSlots {
   uint32_t g0, slot0, slots;
 };
 
-// A wave's groups: the pairs (2k, 2k + 1), k = k0 + wave, k0 + wave + 4, ..., clipped to the split's [ga, gb). The
-// groups of a pair are decoded back to back by the same wave (a RANS chain may run across them).
-__device__ __forceinline__ uint32_t next_group(uint32_t g, uint32_t gb) {
+// Narrow workgroups: a wave's groups are the pairs (2k, 2k + 1), k = k0 + wave, k0 + wave + 4, ..., clipped to the
+// split's [ga, gb).
+__device__ __forceinline__ uint32_t next_group_static(uint32_t g, uint32_t gb) {
   if ((g & 1u) == 0 && g + 1 < gb) return g + 1;
-  const uint32_t n = ((g >> 1) + kWaves) * 2;
+  const uint32_t n = ((g >> 1) + kWavesNarrow) * 2;
   return n < gb ? n : gb;
 }
 
-template <int D, int CODEC>
-__global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_batched_desc d, uint32_t splits,
-                                                                         float *__restrict__ partial, SplitSlots ss) {
+template <int D, int CODEC, int W>
+__global__ CF_KV_OCC __launch_bounds__(64 * W) void kv_batched_kernel(cf_kv_batched_desc d, uint32_t splits,
+                                                                       float *__restrict__ partial, SplitSlots ss) {
   constexpr int NQ = D / 4;
   constexpr int RAW = raw_words<D>();
   constexpr bool RANS = CODEC == CF_KV_CODEC_RANS_HYBRID;
   constexpr int BUF = buf_u32<D>();
+  constexpr int kThreads = 64 * W;
+  constexpr bool kDyn = W == kWavesWide;            // pairs handed out by s_ticket (else statically)
+  constexpr int KL = kDyn && RANS ? 16 : 0;         // V quads parked in LDS (see group_body)
   __shared__ uint2 s_tab[RANS ? 2 : 1][kSlots];     // {f | c << 16, spread big bits} per slot, K and V tables
-  __shared__ _Float16 s_p[kWaves][4][kGqa][16];     // per wave: [page][head][token] probability * v_scale
-  __shared__ uint32_t s_buf[kWaves][BUF];           // per wave: staged words; query staging and partials alias it
+  __shared__ _Float16 s_p[W][4][kGqa][16];          // per wave: [page][head][token] probability * v_scale
+  __shared__ uint32_t s_buf[W][BUF];                // per wave: staged words; query staging and partials alias it
+  __shared__ uint32_t s_vl[KL ? W : 1][KL ? KL : 1][64];
+  __shared__ uint32_t s_ticket;                     // pairs of the split handed out so far
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int G = lane >> 4, t = lane & 15;
   const uint32_t split = blockIdx.x, head = blockIdx.y, seq = blockIdx.z;
   const uint32_t gqa = d.query_head_count / d.kv_head_count;
-  static_assert(2 * kGqa * D * 2 <= kWaves * BUF * 4, "query staging must fit the word buffers");
+  static_assert(2 * kGqa * D * 2 <= W * BUF * 4, "query staging must fit the word buffers");
   _Float16(*s_q)[kGqa][D] = reinterpret_cast<_Float16(*)[kGqa][D]>(&s_buf[0][0]);
 
   // ---- stage tables and queries
@@ -380,6 +397,7 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
     s_q[0][h][dd] = hi;
     s_q[1][h][dd] = static_cast<_Float16>(q - static_cast<float>(hi));
   }
+  if (threadIdx.x == 0) s_ticket = 0;
   __syncthreads();
 
   // Query operands held in registers for the whole kernel: lane (block b = lane/4, row i = lane%4) keeps head i's
@@ -434,7 +452,32 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
   for (int i = 0; i < D / 16; ++i) acc_v[i] = float4_t{0, 0, 0, 0};
 
   uint32_t *buf = s_buf[__builtin_amdgcn_readfirstlane(wave)];  // uniform base: cursor arithmetic stays scalar
-  // Memory pipeline of a wavefront over its groups (see next_group):
+  uint32_t *vl = &s_vl[KL ? __builtin_amdgcn_readfirstlane(wave) : 0][0][0];
+  // A wavefront's groups: pairs (2k, 2k + 1), clipped to the split's [ga, gb); the groups of a pair are decoded back
+  // to back by the same wavefront (a RANS chain may run across them). Wide workgroups: each pair is taken from
+  // s_ticket when the group stream below reaches it (about one pair ahead of the group being decoded). Narrow
+  // workgroups: next_group_static.
+  uint32_t q_g = gb;  // wide: next group the stream hands out (gb: none left)
+  auto take_pair_first = [&]() {
+    uint32_t t = 0;
+    if (lane == 0) t = atomicAdd(&s_ticket, 1u);
+    // broadcast with a lane shuffle, not readfirstlane: with the loop control provably wave-uniform the compiler
+    // schedules this loop with ~40 more VGPRs than the 168 that three waves per SIMD allow
+    t = __shfl(t, 0);
+    const uint32_t p = t < pb - pa ? pa + t : pb;
+    return p < pb ? max(ga, 2 * p) : gb;
+  };
+  auto stream_next = [&](uint32_t prev) {
+    if constexpr (kDyn) {
+      const uint32_t g = q_g;
+      if (g < gb) q_g = ((g & 1u) == 0 && g + 1 < gb) ? g + 1 : take_pair_first();
+      return g;
+    } else {
+      return prev < gb ? next_group_static(prev, gb) : gb;
+    }
+  };
+  if constexpr (kDyn) q_g = take_pair_first();
+  // Memory pipeline of a wavefront over its groups:
   //   blob offset   loaded two groups ahead;
   //   header        loaded at the start of the previous group (fields and chain-start lane states kept in
   //                 registers; the two state words are read for every group and used only by chain starts);
@@ -445,9 +488,9 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
   //                 previous sign group starts; across the group boundary for the last one).
   // The next group's copies are awaited with s_waitcnt vmcnt(0) at the top of the loop.
   auto blob_at = [&](uint32_t g) { return d.pool + static_cast<size_t>(grow[g]) * 16; };
-  const uint32_t gfirst = (2 * (pa + wave) < gb) ? max(ga, 2 * (pa + wave)) : gb;
-  const uint32_t gsecond = gfirst < gb ? next_group(gfirst, gb) : gb;
-  uint32_t off_next = gsecond < gb ? grow[gsecond] : 0u;
+  const uint32_t gfirst = kDyn ? stream_next(gb) : ((2 * (pa + wave) < gb) ? max(ga, 2 * (pa + wave)) : gb);
+  uint32_t g_next = stream_next(gfirst);
+  uint32_t off_next = g_next < gb ? grow[g_next] : 0u;
   const uint8_t *blob = gfirst < gb ? blob_at(gfirst) : d.pool;
   uint32_t h_cnt = 0, h_chain = 0, h_tc = 0, h_codec = 0;
   uint32_t h_st[2] = {0, 0};  // the group's chain-start lane states (read for every group: harmless, unused)
@@ -512,12 +555,12 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
         broken |= prev + 1 != gi;
       }
     }
-    const uint32_t gn = next_group(gi, gb);
+    const uint32_t gn = g_next;
     if (gn < gb) {  // next group's header and states (its offset was loaded one group earlier)
       blob = d.pool + static_cast<size_t>(off_next) * 16;
       load_header(blob);
-      const uint32_t gnn = next_group(gn, gb);
-      off_next = gnn < gb ? grow[gnn] : 0u;
+      g_next = stream_next(gn);
+      off_next = g_next < gb ? grow[g_next] : 0u;
     }
     const bool next_rans = RANS && gn < gb && h_codec == CF_KV_CODEC_RANS_HYBRID;
     const uint32_t *nlw = next_rans ? raw_of(blob, h_chain) : nullptr;
@@ -525,13 +568,13 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
       if (next_rans) stage_words(blob, h_chain, h_cnt);
     };
     if (RANS && gcodec == CF_KV_CODEC_RANS_HYBRID) {
-      group_body<D, CF_KV_CODEC_RANS_HYBRID>(stage_next, pre, nlw, st, raw_of(cur, chain),
-                                             reinterpret_cast<const uint16_t *>(buf), cnt, s_tab, qhi, qlo, qsum,
-                                             s_p[wave], lane, tok_ok, ks, vs, e_run, m_run, l_run, acc_v);
+      group_body<D, CF_KV_CODEC_RANS_HYBRID, KL>(stage_next, pre, nlw, st, raw_of(cur, chain),
+                                                 reinterpret_cast<const uint16_t *>(buf), cnt, s_tab, qhi, qlo, qsum,
+                                                 s_p[wave], vl, lane, tok_ok, ks, vs, e_run, m_run, l_run, acc_v);
     } else {  // raw int8 group (the INT8 codec, or the raw fallback of a group holding -128)
-      group_body<D, CF_KV_CODEC_INT8>(stage_next, pre, nlw, st, reinterpret_cast<const uint32_t *>(cur + kHdr),
-                                      static_cast<const uint16_t *>(nullptr), 0, s_tab, qhi, qlo, qsum, s_p[wave],
-                                      lane, tok_ok, ks, vs, e_run, m_run, l_run, acc_v);
+      group_body<D, CF_KV_CODEC_INT8, KL>(stage_next, pre, nlw, st, reinterpret_cast<const uint32_t *>(cur + kHdr),
+                                          static_cast<const uint16_t *>(nullptr), 0, s_tab, qhi, qlo, qsum,
+                                          s_p[wave], vl, lane, tok_ok, ks, vs, e_run, m_run, l_run, acc_v);
     }
     prev = gi;
     gi = gn;
@@ -566,19 +609,19 @@ __global__ CF_KV_OCC __launch_bounds__(kThreads) void kv_batched_kernel(cf_kv_ba
   }
   __syncthreads();
 
-  // ---- merge the 4 wavefronts; write the split partial (or the final output when splits == 1)
+  // ---- merge the wavefronts; write the split partial (or the final output when splits == 1)
   for (int i = threadIdx.x; i < kGqa * D; i += kThreads) {
     const int h = i / D, dd = i % D;
     float m = -INFINITY;
     bool nan = false;
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < W; ++w) {
       const float mw = reinterpret_cast<const float *>(s_buf[w])[h * (D + 2) + D];
       nan |= mw != mw;
       m = fmaxf(m, mw);
     }
     float l = 0.0f, o = 0.0f;
     if (m != -INFINITY)
-      for (int w = 0; w < kWaves; ++w) {
+      for (int w = 0; w < W; ++w) {
         const float *rw = reinterpret_cast<const float *>(s_buf[w]);
         const float mw = rw[h * (D + 2) + D];
         if (mw == -INFINITY || mw != mw) continue;
@@ -858,52 +901,78 @@ __global__ __launch_bounds__(kGqa * D) void kv_merge_kernel(cf_kv_batched_desc d
       nan ? __builtin_nanf("") : l == 0.0f ? 0.0f : o / l;
 }
 
-// Cascade plan: prefix splits (slots [0, ps)) sized so that the prefix pass has about two workgroups per CU, then the
-// suffix splits (slots [ps, ps + ss)) over each sequence's own groups.
-struct CascadePlan {
-  uint32_t psplits, ssplits, slots;
-};
-
-uint32_t resident_workgroups();
-uint32_t choose_splits(const cf_kv_batched_desc *d);
-
-CascadePlan cascade_plan(const cf_kv_batched_desc *d, uint32_t shared) {
-  CascadePlan p{};
-  const uint32_t tiles = ((d->seq_count + 15) / 16) * d->kv_head_count;
-  const uint32_t want = std::max<uint32_t>(1, (2 * resident_workgroups() / 3 + tiles - 1) / tiles);
-  p.psplits = std::min<uint32_t>(want, shared);
-  cf_kv_batched_desc rest = *d;
-  rest.max_groups = std::max<uint32_t>(1, d->max_groups - shared);
-  p.ssplits = choose_splits(&rest);
-  p.slots = p.psplits + p.ssplits;
-  return p;
-}
-
-// Workgroups resident at once: 3 per CU (the LDS and VGPR budget of kv_batched_kernel).
-uint32_t resident_workgroups() {
+// CUs of the current device (cached per thread and device).
+uint32_t cu_count() {
   static thread_local int cached_dev = -1;
   static thread_local uint32_t cached = 0;
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 768;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
   if (dev != cached_dev) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cached = 3u * static_cast<uint32_t>(cus);
+    cached = static_cast<uint32_t>(cus);
     cached_dev = dev;
   }
   return cached;
 }
 
-// Context splits per (sequence, KV head): enough workgroups to fill the chip in exactly one round when the
-// (sequence, head) units alone do not (a partial second round leaves most CUs idle at the tail), while keeping at
-// least one page group per wavefront.
-uint32_t choose_splits(const cf_kv_batched_desc *d) {
-  if (d->splits) return d->splits;
+// Launch shape of kv_batched_kernel: context splits per (sequence, KV head) and wavefronts per workgroup.
+// Narrow (4 wavefronts, three workgroups per CU) is the base shape. Issue arbitration favours the oldest wavefronts,
+// so the three workgroups of a CU finish far apart; when the grid is one round of workgroups (fewer units than three
+// per CU) that spread is the tail of the whole launch. Launches with at most one (sequence, head) unit per CU go
+// wide (12 wavefronts, one workgroup per CU, one round) when every wavefront still gets about 4 chain pairs or more: the LDS ticket then balances the wavefronts of a CU to
+// within one pair. Larger grids stay narrow: the dispatcher refills a CU as each workgroup ends, and three workgroups
+// of different sequences on one CU share its L1 when their pools share groups (a common prompt prefix).
+// Splits: enough workgroups to fill the chip in one round when the (sequence, head) units alone do not (a partial
+// second round leaves most CUs idle at the tail), keeping at least one page group per wavefront. A caller's d->splits
+// is kept.
+struct BatchedPlan {
+  uint32_t splits, waves;
+};
+constexpr uint32_t kWidePairsPerWave = 4;
+
+BatchedPlan batched_plan(const cf_kv_batched_desc *d) {
   const uint32_t units = d->seq_count * d->kv_head_count;
-  const uint32_t resident = resident_workgroups();
+  const uint32_t pairs = (d->max_groups + 1) / 2;
+  const uint32_t cus = cu_count();
+  auto wide_ok = [&](uint32_t s) { return pairs / s >= kWidePairsPerWave * kWavesWide; };
+  const uint32_t resident = 3 * cus;
+  if (d->splits) return {d->splits, units * d->splits <= cus && wide_ok(d->splits) ? 12u : 4u};
+  if (units <= cus) {
+    const uint32_t s = std::max<uint32_t>(1, std::min<uint32_t>(cus / units, 64));
+    if (wide_ok(s)) return {s, 12u};
+  }
   uint32_t s = units >= resident ? 1u : resident / units;
-  s = std::min<uint32_t>(s, std::max<uint32_t>(1, d->max_groups / kWaves));
-  return std::max<uint32_t>(1, std::min<uint32_t>(s, 64));
+  s = std::min<uint32_t>(s, std::max<uint32_t>(1, d->max_groups / kWavesNarrow));
+  return {std::max<uint32_t>(1, std::min<uint32_t>(s, 64)), 4u};
+}
+
+// Cascade plan: prefix splits (slots [0, ps)) sized so that the prefix pass has about two workgroups per CU, then the
+// suffix splits (slots [ps, ps + ss)) over each sequence's own groups.
+struct CascadePlan {
+  uint32_t psplits, slots;
+  BatchedPlan suffix;
+};
+
+CascadePlan cascade_plan(const cf_kv_batched_desc *d, uint32_t shared) {
+  CascadePlan p{};
+  const uint32_t tiles = ((d->seq_count + 15) / 16) * d->kv_head_count;
+  const uint32_t want = std::max<uint32_t>(1, (2 * cu_count() + tiles - 1) / tiles);
+  p.psplits = std::min<uint32_t>(want, shared);
+  cf_kv_batched_desc rest = *d;
+  rest.max_groups = std::max<uint32_t>(1, d->max_groups - shared);
+  p.suffix = batched_plan(&rest);
+  p.slots = p.psplits + p.suffix.splits;
+  return p;
+}
+
+template <int D, int C>
+void launch_batched(const cf_kv_batched_desc &d, const BatchedPlan &p, dim3 grid, float *ws, SplitSlots ss,
+                    hipStream_t s) {
+  if (p.waves == 12)
+    kv_batched_kernel<D, C, kWavesWide><<<grid, 64 * kWavesWide, 0, s>>>(d, p.splits, ws, ss);
+  else
+    kv_batched_kernel<D, C, kWavesNarrow><<<grid, 64 * kWavesNarrow, 0, s>>>(d, p.splits, ws, ss);
 }
 
 }  // namespace
@@ -925,7 +994,7 @@ extern "C" cf_status cf_kv_validate_batched_desc(const cf_kv_batched_desc *d) {
 
 extern "C" uint64_t cf_kv_batched_workspace_bytes(const cf_kv_batched_desc *d) {
   if (cf_kv_validate_batched_desc(d) != CF_OK) return 0;
-  const uint32_t s = choose_splits(d);
+  const uint32_t s = batched_plan(d).splits;
   if (s <= 1) return 0;
   return static_cast<uint64_t>(d->seq_count) * d->kv_head_count * s * kGqa * (d->head_dim + 2) * sizeof(float);
 }
@@ -933,22 +1002,21 @@ extern "C" uint64_t cf_kv_batched_workspace_bytes(const cf_kv_batched_desc *d) {
 extern "C" cf_status cf_kv_paged_attention_batched_async(const cf_kv_batched_desc *d, void *stream) {
   const cf_status v = cf_kv_validate_batched_desc(d);
   if (v != CF_OK) return v;
-  const uint32_t splits = choose_splits(d);
+  const BatchedPlan plan = batched_plan(d);
+  const uint32_t splits = plan.splits;
   const uint64_t need = cf_kv_batched_workspace_bytes(d);
   if (need && (!d->workspace || d->workspace_bytes < need)) return CF_ERR_INVALID_ARGUMENT;
   const hipStream_t s = cfd::as_stream(stream);
   float *ws = static_cast<float *>(d->workspace);
   const dim3 grid(splits, d->kv_head_count, d->seq_count);
   const SplitSlots ss{0, 0, splits};
-#define CF_LAUNCH(D, C) kv_batched_kernel<D, C><<<grid, kThreads, 0, s>>>(*d, splits, ws, ss)
   if (d->head_dim == 128) {
-    if (d->codec == CF_KV_CODEC_RANS_HYBRID) CF_LAUNCH(128, CF_KV_CODEC_RANS_HYBRID);
-    else CF_LAUNCH(128, CF_KV_CODEC_INT8);
+    if (d->codec == CF_KV_CODEC_RANS_HYBRID) launch_batched<128, CF_KV_CODEC_RANS_HYBRID>(*d, plan, grid, ws, ss, s);
+    else launch_batched<128, CF_KV_CODEC_INT8>(*d, plan, grid, ws, ss, s);
   } else {
-    if (d->codec == CF_KV_CODEC_RANS_HYBRID) CF_LAUNCH(64, CF_KV_CODEC_RANS_HYBRID);
-    else CF_LAUNCH(64, CF_KV_CODEC_INT8);
+    if (d->codec == CF_KV_CODEC_RANS_HYBRID) launch_batched<64, CF_KV_CODEC_RANS_HYBRID>(*d, plan, grid, ws, ss, s);
+    else launch_batched<64, CF_KV_CODEC_INT8>(*d, plan, grid, ws, ss, s);
   }
-#undef CF_LAUNCH
   if (splits > 1) {
     const dim3 g2(d->kv_head_count, d->seq_count);
     if (d->head_dim == 128) kv_merge_kernel<128><<<g2, kGqa * 128, 0, s>>>(*d, splits, ws);
@@ -979,11 +1047,11 @@ extern "C" cf_status cf_kv_paged_attention_cascade_async(const cf_kv_batched_des
   kv_prefix_kernel<<<dim3((d->seq_count + 15) / 16, d->kv_head_count, p.psplits), kPfxThreads, 0, s>>>(
       *d, shared_groups, p.psplits, ws, SplitSlots{0, 0, p.slots});
   const SplitSlots rest{shared_groups, p.psplits, p.slots};
-  const dim3 grid(p.ssplits, d->kv_head_count, d->seq_count);
+  const dim3 grid(p.suffix.splits, d->kv_head_count, d->seq_count);
   if (d->codec == CF_KV_CODEC_RANS_HYBRID)
-    kv_batched_kernel<128, CF_KV_CODEC_RANS_HYBRID><<<grid, kThreads, 0, s>>>(*d, p.ssplits, ws, rest);
+    launch_batched<128, CF_KV_CODEC_RANS_HYBRID>(*d, p.suffix, grid, ws, rest, s);
   else
-    kv_batched_kernel<128, CF_KV_CODEC_INT8><<<grid, kThreads, 0, s>>>(*d, p.ssplits, ws, rest);
+    launch_batched<128, CF_KV_CODEC_INT8>(*d, p.suffix, grid, ws, rest, s);
   kv_merge_kernel<128><<<dim3(d->kv_head_count, d->seq_count), kGqa * 128, 0, s>>>(*d, p.slots, ws);
   return cfd::launch_status();
 }

@@ -112,6 +112,27 @@ def test_batched_v_magnitudes_hd64(dev):
     _run(dev, 2, [4096, 4096, 4100, 4096, 4160], 2, 4, 64, seed=43, splits=(0, 3), v_mult=V_MULTS)
 
 
+# Wide workgroups (12 wavefronts taking chain pairs from an LDS ticket, V quads parked in LDS) serve launches with
+# at most one (sequence, head) unit per CU whose splits keep >= 48 chain pairs each; splits=1 on these >= 6144-token
+# contexts selects them (units x 1 <= CUs, >= 71 pairs), splits=2 and the automatic choice the narrow shape.
+@pytest.mark.parametrize("codec", [1, 2])
+@pytest.mark.parametrize("D", [128, 64])
+def test_batched_wide_workgroups(dev, codec, D):
+    _run(dev, codec, [6200, 7000, 6145, 9000, 1, 6400], 2, 4, D, seed=51 + D + codec, splits=(1, 2, 0),
+         query_pos=[6199, 3500, 6144, 8999, 0, 100])
+
+
+def test_batched_wide_raw_and_shared_groups(dev):
+    # INT8 groups inside the rANS pool under the wide shape: a shared 4-group prefix (sequences 1, 2 reuse sequence
+    # 0's blobs), sequence 3 with 7 leading raw groups (its first coded group, 7, starts its own chain mid-pair)
+    _run(dev, 2, [6500, 6300, 7100, 8000], 2, 4, 128, seed=57, splits=(1, 0),
+         shared={1: (0, 4), 2: (0, 4)}, raw_groups={0: 4, 3: 7})
+
+
+def test_batched_wide_v_magnitudes(dev):
+    _run(dev, 2, [6144, 6200, 7000, 6150, 6400], 2, 4, 128, seed=59, splits=(1,), v_mult=V_MULTS)
+
+
 def test_batched_rejects_bad_desc(dev):
     import ctypes as C
     import torch
@@ -177,7 +198,7 @@ def test_batched_full_c4_32k_every_sequence_torch_reference(dev):
 
 
 def _cascade_case(dev, gqa, seq_tokens, shared, seed, query_pos=None, raw_prefix=True, D=128, kv_heads=2,
-                  v_mult=None):
+                  v_mult=None, splits=0):
     import torch
     from chromofold_amd import kv
     data = make_seqs(seq_tokens, kv_heads, D, seed, v_mult=v_mult)
@@ -200,7 +221,7 @@ def _cascade_case(dev, gqa, seq_tokens, shared, seed, query_pos=None, raw_prefix
     dq = torch.from_numpy(q).to(dev)
     dqp = torch.from_numpy(qp.view(np.int32)).to(dev)
     out = torch.full_like(dq, float("nan"))
-    kvb.attention(dq, out, dqp, sc, shared_groups=shared)
+    kvb.attention(dq, out, dqp, sc, splits=splits, shared_groups=shared)
     return kvb, data, q, qp, sc, out.cpu().numpy()
 
 
@@ -257,6 +278,17 @@ def test_cascade_random_suffixes(dev, seed):
     tokens = [192 + int(rng.integers(0, 700)) for _ in range(S)]
     qpos = [int(rng.integers(100, t)) if rng.random() < 0.3 else t - 1 for t in tokens]
     kvb, data, q, qp, sc, got = _cascade_case(dev, 4, tokens, shared, seed=90 + seed, query_pos=qpos)
+    assert np.isfinite(got).all()
+    ref = oracle_batched(kvb, data, q, qp, sc, 4)
+    assert head_err(got, ref) <= TOL
+
+
+def test_cascade_wide_suffix_after_odd_prefix(dev):
+    """A 3-group (odd) INT8 prefix, then long own suffixes decoded by wide workgroups (splits=1: 110 suffix groups):
+    the suffix launch starts at group 3, in the middle of chain pair (2, 3)."""
+    tokens = [192 + 6400, 192 + 7000, 192 + 6200]
+    kvb, data, q, qp, sc, got = _cascade_case(dev, 4, tokens, 3, seed=63, splits=1,
+                                              query_pos=[192 + 6399, 150, 192 + 3000])
     assert np.isfinite(got).all()
     ref = oracle_batched(kvb, data, q, qp, sc, 4)
     assert head_err(got, ref) <= TOL
