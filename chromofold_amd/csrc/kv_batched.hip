@@ -1,10 +1,10 @@
 // kv_batched.hip — batched compressed paged-KV attention decode on gfx950 (kv_codec_ext.h entry point).
 //
 // One workgroup serves one (sequence, KV head, context split): 12 wavefronts (one workgroup per CU) for long
-// contexts, 4 (three workgroups per CU) for short ones. Its wavefronts take the chain pairs of the split from an LDS
-// counter one at a time, so that wavefronts the CU serves faster (issue arbitration favours the oldest) take more
-// pairs and all finish together. Each wavefront walks "page quads": four consecutive 16-token pages, one per
-// 16-lane group. Lane (G, t) = lane 16G + t:
+// contexts, 4 (three workgroups per CU) for short ones. In a 12-wavefront workgroup each wavefront takes a contiguous
+// block of the split's chain pairs sized by its issue priority (arbitration favours the oldest wavefront of a SIMD),
+// so that all finish together. Each wavefront walks "page quads": four consecutive 16-token pages, one per 16-lane
+// group. Lane (G, t) = lane 16G + t:
 //   K phase: lane decodes token t of page G (its 16 interleaved rANS states are the 16 lanes of the group);
 //            every decoded quad of 4 dims goes straight into v_mfma_f32_4x4x4f16 as the B operand, with the
 //            GQA group's 4 query heads (split into f16 hi + lo parts for fp32-grade scores) as the A operand, so
@@ -350,10 +350,27 @@ struct SplitSlots {
 
 // Narrow workgroups: a wave's groups are the pairs (2k, 2k + 1), k = k0 + wave, k0 + wave + 4, ..., clipped to the
 // split's [ga, gb).
-__device__ __forceinline__ uint32_t next_group_static(uint32_t g, uint32_t gb) {
+__device__ __forceinline__ uint32_t next_group_strided(uint32_t g, uint32_t gb) {
   if ((g & 1u) == 0 && g + 1 < gb) return g + 1;
   const uint32_t n = ((g >> 1) + kWavesNarrow) * 2;
   return n < gb ? n : gb;
+}
+
+// Wide workgroups: wavefront w (SIMD w % 4; the w / 4-th oldest of that SIMD's three) takes a contiguous block of the
+// split's pairs in proportion to kSlotWeight[w / 4], the relative rates at which MI355X's issue arbitration lets the
+// oldest, middle and youngest wavefront of a SIMD progress in this kernel (measured on the C4 shape: with the ticket
+// that handed pairs out dynamically, the three took 48 : 44 : 36 groups in 359 : 368 : 372 us). Static blocks keep
+// the result bitwise reproducible; equal blocks left the youngest wavefronts finishing ~15 % after the oldest.
+constexpr uint32_t kSlotWeight[3] = {139, 124, 100};
+constexpr uint32_t kSlotWeightSum = 4 * (kSlotWeight[0] + kSlotWeight[1] + kSlotWeight[2]);
+
+// Pairs [lo, hi) of `np` that wavefront w of a wide workgroup takes.
+__device__ __forceinline__ void wide_block(uint32_t w, uint32_t np, uint32_t &lo, uint32_t &hi) {
+  const uint32_t slot = w >> 2, sub = w & 3;
+  const uint32_t mine = kSlotWeight[slot < 3 ? slot : 2];
+  const uint32_t before = (slot > 0 ? 4 * kSlotWeight[0] : 0) + (slot > 1 ? 4 * kSlotWeight[1] : 0) + sub * mine;
+  lo = static_cast<uint32_t>((static_cast<uint64_t>(np) * before) / kSlotWeightSum);
+  hi = static_cast<uint32_t>((static_cast<uint64_t>(np) * (before + mine)) / kSlotWeightSum);
 }
 
 template <int D, int CODEC, int W>
@@ -364,13 +381,12 @@ __global__ CF_KV_OCC __launch_bounds__(64 * W) void kv_batched_kernel(cf_kv_batc
   constexpr bool RANS = CODEC == CF_KV_CODEC_RANS_HYBRID;
   constexpr int BUF = buf_u32<D>();
   constexpr int kThreads = 64 * W;
-  constexpr bool kDyn = W == kWavesWide;            // pairs handed out by s_ticket (else statically)
-  constexpr int KL = kDyn && RANS ? 16 : 0;         // V quads parked in LDS (see group_body)
+  constexpr bool kWide = W == kWavesWide;           // contiguous weighted pair blocks (else strided pairs)
+  constexpr int KL = kWide && RANS ? 16 : 0;        // V quads parked in LDS (see group_body)
   __shared__ uint2 s_tab[RANS ? 2 : 1][kSlots];     // {f | c << 16, spread big bits} per slot, K and V tables
   __shared__ _Float16 s_p[W][4][kGqa][16];          // per wave: [page][head][token] probability * v_scale
   __shared__ uint32_t s_buf[W][BUF];                // per wave: staged words; query staging and partials alias it
   __shared__ uint32_t s_vl[KL ? W : 1][KL ? KL : 1][64];
-  __shared__ uint32_t s_ticket;                     // pairs of the split handed out so far
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -397,7 +413,6 @@ __global__ CF_KV_OCC __launch_bounds__(64 * W) void kv_batched_kernel(cf_kv_batc
     s_q[0][h][dd] = hi;
     s_q[1][h][dd] = static_cast<_Float16>(q - static_cast<float>(hi));
   }
-  if (threadIdx.x == 0) s_ticket = 0;
   __syncthreads();
 
   // Query operands held in registers for the whole kernel: lane (block b = lane/4, row i = lane%4) keeps head i's
@@ -454,29 +469,22 @@ __global__ CF_KV_OCC __launch_bounds__(64 * W) void kv_batched_kernel(cf_kv_batc
   uint32_t *buf = s_buf[__builtin_amdgcn_readfirstlane(wave)];  // uniform base: cursor arithmetic stays scalar
   uint32_t *vl = &s_vl[KL ? __builtin_amdgcn_readfirstlane(wave) : 0][0][0];
   // A wavefront's groups: pairs (2k, 2k + 1), clipped to the split's [ga, gb); the groups of a pair are decoded back
-  // to back by the same wavefront (a RANS chain may run across them). Wide workgroups: each pair is taken from
-  // s_ticket when the group stream below reaches it (about one pair ahead of the group being decoded). Narrow
-  // workgroups: next_group_static.
-  uint32_t q_g = gb;  // wide: next group the stream hands out (gb: none left)
-  auto take_pair_first = [&]() {
-    uint32_t t = 0;
-    if (lane == 0) t = atomicAdd(&s_ticket, 1u);
-    // broadcast with a lane shuffle, not readfirstlane: with the loop control provably wave-uniform the compiler
-    // schedules this loop with ~40 more VGPRs than the 168 that three waves per SIMD allow
-    t = __shfl(t, 0);
-    const uint32_t p = t < pb - pa ? pa + t : pb;
-    return p < pb ? max(ga, 2 * p) : gb;
-  };
-  auto stream_next = [&](uint32_t prev) {
-    if constexpr (kDyn) {
-      const uint32_t g = q_g;
-      if (g < gb) q_g = ((g & 1u) == 0 && g + 1 < gb) ? g + 1 : take_pair_first();
-      return g;
-    } else {
-      return prev < gb ? next_group_static(prev, gb) : gb;
+  // to back by the same wavefront (a RANS chain may run across them). Wide workgroups: one contiguous block of pairs
+  // per wavefront (wide_block), i.e. the consecutive groups [w_begin, w_end). Narrow: next_group_strided.
+  uint32_t w_begin = gb, w_end = gb;
+  if constexpr (kWide) {
+    uint32_t lo, hi;
+    wide_block(static_cast<uint32_t>(wave), pb - pa, lo, hi);
+    if (lo < hi) {
+      w_begin = max(ga, 2 * (pa + lo));
+      w_end = min(gb, 2 * (pa + hi));
     }
+  }
+  auto stream_next = [&](uint32_t prev) {
+    if (prev >= gb) return gb;
+    if constexpr (kWide) return prev + 1 < w_end ? prev + 1 : gb;
+    else return next_group_strided(prev, gb);
   };
-  if constexpr (kDyn) q_g = take_pair_first();
   // Memory pipeline of a wavefront over its groups:
   //   blob offset   loaded two groups ahead;
   //   header        loaded at the start of the previous group (fields and chain-start lane states kept in
@@ -488,7 +496,8 @@ __global__ CF_KV_OCC __launch_bounds__(64 * W) void kv_batched_kernel(cf_kv_batc
   //                 previous sign group starts; across the group boundary for the last one).
   // The next group's copies are awaited with s_waitcnt vmcnt(0) at the top of the loop.
   auto blob_at = [&](uint32_t g) { return d.pool + static_cast<size_t>(grow[g]) * 16; };
-  const uint32_t gfirst = kDyn ? stream_next(gb) : ((2 * (pa + wave) < gb) ? max(ga, 2 * (pa + wave)) : gb);
+  const uint32_t gfirst = kWide ? (w_begin < w_end ? w_begin : gb)
+                               : ((2 * (pa + wave) < gb) ? max(ga, 2 * (pa + wave)) : gb);
   uint32_t g_next = stream_next(gfirst);
   uint32_t off_next = g_next < gb ? grow[g_next] : 0u;
   const uint8_t *blob = gfirst < gb ? blob_at(gfirst) : d.pool;
@@ -920,9 +929,10 @@ uint32_t cu_count() {
 // Narrow (4 wavefronts, three workgroups per CU) is the base shape. Issue arbitration favours the oldest wavefronts,
 // so the three workgroups of a CU finish far apart; when the grid is one round of workgroups (fewer units than three
 // per CU) that spread is the tail of the whole launch. Launches with at most one (sequence, head) unit per CU go
-// wide (12 wavefronts, one workgroup per CU, one round) when every wavefront still gets about 4 chain pairs or more: the LDS ticket then balances the wavefronts of a CU to
-// within one pair. Larger grids stay narrow: the dispatcher refills a CU as each workgroup ends, and three workgroups
-// of different sequences on one CU share its L1 when their pools share groups (a common prompt prefix).
+// wide (12 wavefronts, one workgroup per CU, one round) when every wavefront still gets about 4 chain pairs or more:
+// the priority-weighted pair blocks (wide_block) then let the wavefronts of a CU finish together. Larger grids stay
+// narrow: the dispatcher refills a CU as each workgroup ends, and three workgroups of different sequences on one CU
+// share its L1 when their pools share groups (a common prompt prefix).
 // Splits: enough workgroups to fill the chip in one round when the (sequence, head) units alone do not (a partial
 // second round leaves most CUs idle at the tail), keeping at least one page group per wavefront. A caller's d->splits
 // is kept.
@@ -999,15 +1009,13 @@ extern "C" uint64_t cf_kv_batched_workspace_bytes(const cf_kv_batched_desc *d) {
   return static_cast<uint64_t>(d->seq_count) * d->kv_head_count * s * kGqa * (d->head_dim + 2) * sizeof(float);
 }
 
-extern "C" cf_status cf_kv_paged_attention_batched_async(const cf_kv_batched_desc *d, void *stream) {
-  const cf_status v = cf_kv_validate_batched_desc(d);
-  if (v != CF_OK) return v;
-  const BatchedPlan plan = batched_plan(d);
+namespace {
+
+// The batched launch (decode kernel, then the split merge when the plan splits the context) with the split partials
+// in `ws` (at least cf_kv_batched_workspace_bytes(d) bytes; unused when the plan does not split).
+cf_status launch_batched_all(const cf_kv_batched_desc *d, const BatchedPlan &plan, float *ws, void *stream) {
   const uint32_t splits = plan.splits;
-  const uint64_t need = cf_kv_batched_workspace_bytes(d);
-  if (need && (!d->workspace || d->workspace_bytes < need)) return CF_ERR_INVALID_ARGUMENT;
   const hipStream_t s = cfd::as_stream(stream);
-  float *ws = static_cast<float *>(d->workspace);
   const dim3 grid(splits, d->kv_head_count, d->seq_count);
   const SplitSlots ss{0, 0, splits};
   if (d->head_dim == 128) {
@@ -1023,6 +1031,17 @@ extern "C" cf_status cf_kv_paged_attention_batched_async(const cf_kv_batched_des
     else kv_merge_kernel<64><<<g2, kGqa * 64, 0, s>>>(*d, splits, ws);
   }
   return cfd::launch_status();
+}
+
+}  // namespace
+
+extern "C" cf_status cf_kv_paged_attention_batched_async(const cf_kv_batched_desc *d, void *stream) {
+  const cf_status v = cf_kv_validate_batched_desc(d);
+  if (v != CF_OK) return v;
+  const BatchedPlan plan = batched_plan(d);
+  const uint64_t need = cf_kv_batched_workspace_bytes(d);
+  if (need && (!d->workspace || d->workspace_bytes < need)) return CF_ERR_INVALID_ARGUMENT;
+  return launch_batched_all(d, plan, static_cast<float *>(d->workspace), stream);
 }
 
 extern "C" uint64_t cf_kv_cascade_workspace_bytes(const cf_kv_batched_desc *d, uint32_t shared_groups) {
@@ -1055,3 +1074,4 @@ extern "C" cf_status cf_kv_paged_attention_cascade_async(const cf_kv_batched_des
   kv_merge_kernel<128><<<dim3(d->kv_head_count, d->seq_count), kGqa * 128, 0, s>>>(*d, p.slots, ws);
   return cfd::launch_status();
 }
+

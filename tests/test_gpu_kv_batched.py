@@ -112,9 +112,10 @@ def test_batched_v_magnitudes_hd64(dev):
     _run(dev, 2, [4096, 4096, 4100, 4096, 4160], 2, 4, 64, seed=43, splits=(0, 3), v_mult=V_MULTS)
 
 
-# Wide workgroups (12 wavefronts taking chain pairs from an LDS ticket, V quads parked in LDS) serve launches with
-# at most one (sequence, head) unit per CU whose splits keep >= 48 chain pairs each; splits=1 on these >= 6144-token
-# contexts selects them (units x 1 <= CUs, >= 71 pairs), splits=2 and the automatic choice the narrow shape.
+# Wide workgroups (12 wavefronts, each taking a priority-weighted block of chain pairs, V quads parked in LDS) serve
+# launches with at most one (sequence, head) unit per CU whose splits keep >= 48 chain pairs each; splits=1 on these
+# >= 6144-token contexts selects them (units x 1 <= CUs, >= 71 pairs), splits=2 and the automatic choice the narrow
+# shape. The pair blocks are static, so the outputs are bitwise reproducible.
 @pytest.mark.parametrize("codec", [1, 2])
 @pytest.mark.parametrize("D", [128, 64])
 def test_batched_wide_workgroups(dev, codec, D):
