@@ -29,6 +29,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <utility>
 
 #include "cf_device.hpp"
@@ -1075,3 +1076,47 @@ extern "C" cf_status cf_kv_paged_attention_cascade_async(const cf_kv_batched_des
   return cfd::launch_status();
 }
 
+// ---- allocation-free variant of the batched entry point
+// The split partials live in `scratch`, a file-scope device array of CF_KV_BATCHED_NOALLOC_SCRATCH_BYTES that each
+// GPU holds until the process ends. In host code `scratch` only names the symbol: its device address on the current
+// GPU comes from hipGetSymbolAddress, looked up once per device on the first call there and kept in
+// g_scratch_addr. Every call on a GPU uses that GPU's one array, so calls that overlap on one GPU (other streams,
+// other threads) race on it. Nothing in it needs clearing: every split workgroup writes its whole partial slot
+// before the merge reads it.
+static __device__ __align__(256) uint8_t scratch[CF_KV_BATCHED_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_addr[kMaxDevices] = {};
+
+cf_status scratch_address(void **out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return CF_ERR_CUDA;
+  if (dev < 0 || dev >= kMaxDevices) return CF_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void *addr = nullptr;
+    if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || !addr) return CF_ERR_CUDA;
+    g_scratch_addr[dev] = addr;
+  }
+  *out = g_scratch_addr[dev];
+  return CF_OK;
+}
+
+}  // namespace
+
+extern "C" cf_status cf_kv_paged_attention_batched_noalloc_async(const cf_kv_batched_desc *d, void *stream) {
+  const cf_status v = cf_kv_validate_batched_desc(d);
+  if (v != CF_OK) return v;
+  const BatchedPlan plan = batched_plan(d);
+  const uint64_t need = cf_kv_batched_workspace_bytes(d);
+  if (need > CF_KV_BATCHED_NOALLOC_SCRATCH_BYTES) return CF_ERR_UNSUPPORTED;
+  void *ws = nullptr;
+  if (need) {
+    const cf_status st = scratch_address(&ws);
+    if (st != CF_OK) return st;
+  }
+  return launch_batched_all(d, plan, static_cast<float *>(ws), stream);
+}

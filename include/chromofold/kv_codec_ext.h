@@ -150,6 +150,16 @@ cf_status cf_kv_validate_batched_desc(const cf_kv_batched_desc *desc);
  * semantics of one (sequence, query head) equal cf_kv_paged_attention_async with one query row and no tail. */
 cf_status cf_kv_paged_attention_batched_async(const cf_kv_batched_desc *desc, void *stream);
 
+/* Allocation-free variant of cf_kv_paged_attention_batched_async: the same launches and results, but the split
+ * partials go to a library-owned device array of CF_KV_BATCHED_NOALLOC_SCRATCH_BYTES per GPU instead of
+ * desc->workspace (ignored). No counterpart in the reference; it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It calls no allocator. A
+ * descriptor whose cf_kv_batched_workspace_bytes() exceeds that size returns CF_ERR_UNSUPPORTED (use the workspace
+ * entry point, or fewer splits). Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (concurrent streams or threads) race and must be serialised by the caller. */
+#define CF_KV_BATCHED_NOALLOC_SCRATCH_BYTES (8u << 20)
+cf_status cf_kv_paged_attention_batched_noalloc_async(const cf_kv_batched_desc *desc, void *stream);
+
 /* Cascade decode for a prefix shared by every sequence: the first `shared_groups` groups of each sequence are the
  * same blobs (sequence 0's group_offsets rows give them; the other sequences' entries for those groups are not
  * read). The prefix is streamed once per KV head for all sequences' queries (a dense pass on the matrix cores) and

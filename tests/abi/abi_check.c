@@ -84,6 +84,7 @@ int main(void) {
   /* kv_codec_ext.h */
   expect("cf_kv_validate_batched_desc", cf_kv_validate_batched_desc(NULL), INV);
   expect("cf_kv_paged_attention_batched_async", cf_kv_paged_attention_batched_async(NULL, NULL), INV);
+  expect("cf_kv_paged_attention_batched_noalloc_async", cf_kv_paged_attention_batched_noalloc_async(NULL, NULL), INV);
   /* kv_runtime.h */
   expect("cf_kv_validate_page", cf_kv_validate_page(NULL), INV);
   expect("cf_kv_validate_layout", cf_kv_validate_layout(NULL), INV);
