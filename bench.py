@@ -30,7 +30,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the dominant kernel, from rocprofv3 FETCH_SIZE + WRITE_SIZE runs calibrated on a copy of
 # known size (profiles/kv_batched_c4_32k.md): only quoted for the workload shape it was measured on.
-MEASURED_TRAFFIC = {("kv", 32768, 32): 2.129e9}
+MEASURED_TRAFFIC = {("kv", 32768, 32): 2.0848e9}
 METRIC = "compressed-KV attn decode tokens/s + HBM GB/s fraction; wavelet rank Mq/s"
 
 
