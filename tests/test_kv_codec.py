@@ -307,3 +307,49 @@ def test_pool_attention_matches_paged_oracle(kv):
     one = O.kv_pool_attention(kvb.host_pool, kvb.host_offsets, np.array(toks, np.uint32), qp, tables, q, H, D, sc,
                               nseq=2, threads=1)
     assert np.array_equal(one, got[:2])
+
+
+def test_planted_mistakes_change_the_decode(kv):
+    """The oracle decoder reads every part of a format-4 blob: one flipped bit in a raw word changes exactly that
+    value's symbol; a flipped bit in the rANS word stream, or decoding with another head's table, either changes
+    the symbols or leaves the chain's end states off 2^16 (kv_decode_run raises)."""
+    rng = np.random.default_rng(77)
+    D = 128
+    K = rng.standard_normal((4, 16, D)).astype(np.float32)
+    V = rng.standard_normal((4, 16, D)).astype(np.float32)
+    tc = np.full(4, 16, np.uint32)
+    tab = np.concatenate([kv.build_table(K), kv.build_table(V)])
+    other = np.concatenate([kv.build_table(V * 0.02), kv.build_table(K * 0.02)])  # a different distribution
+    first, counts, heads = np.array([0], np.uint64), np.array([4], np.uint32), np.array([0], np.uint32)
+    blob, _ = kv.encode_groups(2, K, V, D, tab, first, counts, heads, tc)
+    good = O.kv_decode_run([blob], tab, 0, D)[0]
+    _check_group(good, K, V, 0, 4, tc)
+    raw0 = 64 + 512  # header + the chain start's lane states
+    RAW = 7 * (D // 32) * 64
+
+    def decoded_or_failed(b, t):
+        try:
+            return O.kv_decode_run([b], t, 0, D)[0]
+        except ValueError:
+            return None
+
+    # a raw K nibble word (word 0 of sign group 1, lane 5): one bit -> one value
+    bad = blob.copy()
+    bad[raw0 + ((7 * 1 + 0) * 64 + 5) * 4] ^= 0x01
+    got = decoded_or_failed(bad, tab)
+    assert got is not None
+    diff = (got[0] != good[0]).sum() + (got[1] != good[1]).sum()
+    assert diff == 1
+    # a raw V sign word: one value's sign
+    bad = blob.copy()
+    bad[raw0 + RAW * 4 + ((7 * 2 + 6) * 64 + 9) * 4 + 3] ^= 0x10
+    got = decoded_or_failed(bad, tab)
+    assert got is not None and (got[1] != good[1]).sum() == 1 and (got[0] == good[0]).all()
+    # the K word stream (first rANS word after the raw words)
+    bad = blob.copy()
+    bad[raw0 + 2 * RAW * 4 + 1] ^= 0x40
+    got = decoded_or_failed(bad, tab)
+    assert got is None or not (np.array_equal(got[0], good[0]) and np.array_equal(got[1], good[1]))
+    # another table
+    got = decoded_or_failed(blob, other)
+    assert got is None or not (np.array_equal(got[0], good[0]) and np.array_equal(got[1], good[1]))
