@@ -15,11 +15,11 @@
 //   V phase: lane decodes dims {t + 16i} of page G, 4 tokens per quad, again straight into a 4x4x4 MFMA
 //            (A = probabilities of those 4 tokens for the 4 heads, B = the 4 decoded values as exact signed f16)
 //            accumulating the lane's 4 heads x 8 dims output.
-// Codec decode per quad: one rANS step (LDS slot table, 64-bit entry = freq/offset + the four 2-bit high parts
-// already spread to their bytes; SDWA reads the 16-bit freq/offset halves in place), three bit-sliced low-part
-// words per 4 quads merged with two bit-field inserts, and two v_perm to build the f16 operand (1024 + symbol). For
-// K the constant 1024+128 offset is folded out with the sum of the query operand; for V it is subtracted from the
-// operand (two packed f16 adds), so the P.V accumulator holds no offset term.
+// Codec decode (format 4): one rANS step per 8 values of a stream (LDS slot table, 64-bit entry = freq/offset +
+// the symbol's 8 big bits spread to their frame positions; SDWA reads the 16-bit freq/offset halves in place); the
+// raw nibble, crumb and sign words of the lane merged with two bit-field inserts and a rotation per quad; two
+// v_perm build the exact f16 operand (sign-magnitude bytes read as f16 denormals = q * 2^-24). INT8 groups (the
+// raw fallback) use 1024 + symbol operands with the 1152 offset folded out of the scores and subtracted from V.
 // Memory: a wavefront's next group is in flight while it works on the current one (header in registers, word
 // streams copied straight into LDS by global_load_lds after the current decode loop, first low-part words in
 // registers), so a group starts without a memory round trip.
@@ -34,6 +34,7 @@
 
 #include "cf_device.hpp"
 #include "chromofold/kv_codec_ext.h"
+#include "kv_group_decode.hpp"
 
 namespace {
 
@@ -48,7 +49,16 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 constexpr int kWavesWide = 12;   // one workgroup per CU
 constexpr int kWavesNarrow = 4;  // three workgroups per CU
 constexpr int kGqa = 4;            // MFMA rows: query heads of one KV head (gqa < 4 pads with zero queries)
-constexpr uint32_t kSlots = 1u << CF_KV_RANS_PROB_BITS;
+using cfkv::bfi;
+using cfkv::kFrame;
+using cfkv::kHdr;
+using cfkv::kNWord;
+using cfkv::kSlots;
+using cfkv::kStateBytes;
+using cfkv::quad_mag;
+using cfkv::quad_signs;
+using cfkv::rans_advance;
+using cfkv::rans_lookup;
 constexpr float kOffset = 1152.0f;  // f16 operand = 1024 + symbol, symbol = q + 128
 
 __device__ __forceinline__ half4_t bytes_to_half4(uint32_t b) {
@@ -75,62 +85,6 @@ __device__ __forceinline__ float4_t mfma4(half4_t a, half4_t b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 0, 0, 0);
 }
 
-// (a & mask) | (b & ~mask) in one v_bfi_b32
-__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
-  uint32_t r;
-  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(b));
-  return r;
-}
-
-// rANS decode of one 64-lane stream, split in three so that the two chains of a lane overlap their LDS round
-// trips: the slot entry lookups of both chains are issued first, then the state updates with their
-// renormalisation-word fetches, then the word merges. x = lane state; wbase = wave-uniform address of the current
-// word (cursor) of the stream staged in LDS. The slot entry is {f | c << 16, spread big bits}.
-__device__ __forceinline__ uint2 rans_lookup(const uint2 *__restrict__ tab, uint32_t x) {
-  return tab[x & (kSlots - 1)];
-}
-
-template <typename WordPtr>
-__device__ __forceinline__ uint32_t rans_advance(uint32_t ex, uint32_t &x, WordPtr &wbase, uint32_t &sel) {
-  // x = f * (x >> 11) + c with f, c the two 16-bit halves of ex, read in place by SDWA operand selects
-  const uint32_t xs = x >> CF_KV_RANS_PROB_BITS;
-  uint32_t fx;
-  asm("v_mul_u32_u24_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD"
-      : "=v"(fx) : "v"(ex), "v"(xs));
-  asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:DWORD"
-      : "=v"(x) : "v"(ex), "v"(fx));
-  const bool need = x < 65536u;
-  const uint64_t m = __builtin_amdgcn_ballot_w64(need);
-  const uint32_t idx = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
-                                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
-  const uint32_t w = wbase[idx];  // lanes that do not renormalise read a harmless in-bounds word
-  wbase += __builtin_popcountll(m);
-  sel = need ? 0x05040100u : 0x07060504u;  // (x << 16) | w  or  x
-  return w;
-}
-
-// ---- format-4 value assembly (kv_codec_ext.h): quad k of a sign group sits in frame r = kFrame[k]
-constexpr uint32_t kFrame[8] = {0, 4, 2, 6, 1, 5, 3, 7};
-constexpr uint32_t kNWord[4] = {0, 1, 3, 4};  // raw word with the nibbles of quads 2m, 2m + 1 (N0 N1 C0 N2 N3 C1 S)
-constexpr uint32_t rotl_c(uint32_t v, uint32_t r) { return r ? (v << r) | (v >> (32 - r)) : v; }
-
-template <uint32_t R>
-__device__ __forceinline__ uint32_t rotr(uint32_t v) {
-  if constexpr (R == 0) return v;
-  else return __builtin_amdgcn_alignbit(v, v, R);
-}
-
-// The magnitude bytes |q| (bit 7 clear) of the quad in frame R: nibbles from n, crumbs from c, big bits from the
-// pair's spread word (already in the pair's frames), then rotated back to byte alignment.
-template <uint32_t R>
-__device__ __forceinline__ uint32_t quad_mag(uint32_t n, uint32_t c, uint32_t spread) {
-  return rotr<R>(bfi(rotl_c(0x0F0F0F0Fu, R), n, bfi(rotl_c(0x30303030u, R), c, spread)));
-}
-
-// The sign bytes (0x80 or 0x00) of the quad in frame R.
-template <uint32_t R>
-__device__ __forceinline__ uint32_t quad_signs(uint32_t s) { return rotr<R>(s) & 0x80808080u; }
-
 // Exact f16 operand of four sign-magnitude values: the f16 denormals (sign << 15) | |q| = q * 2^-24.
 __device__ __forceinline__ half4_t sm_to_half4(uint32_t mag, uint32_t signs) {
   half4_t h;
@@ -140,14 +94,12 @@ __device__ __forceinline__ half4_t sm_to_half4(uint32_t mag, uint32_t signs) {
   return h;
 }
 
-constexpr int kHdr = 64;                 // group header bytes
-constexpr int kStateBytes = 2 * 64 * 4;  // K and V lane states of a chain start
 constexpr uint32_t kCapWords = CF_KV_RANS_MAX_GROUP_WORDS;  // K+V words staged in LDS per wavefront
 constexpr uint32_t kSlackWords = 64;     // reads past the last word by non-renormalising lanes stay in the buffer
 
 template <int D>
 constexpr int raw_words() {  // u32 raw words of one stream of a RANS group
-  return 7 * (D / 32) * 64;
+  return cfkv::raw_words_of(D);
 }
 
 template <int D>

@@ -12,6 +12,13 @@
 // include/chromofold/detail/block_huffman_device.cuh:12-19) with block_offsets every block_size symbols. The
 // reference routes any head_dim % 32 == 0 page to a fixed-width-only kernel even when it is Huffman coded (its
 // warp kernel shifts by 32 - 0); here every page is decoded by its own codec.
+// rANS pages (fixed_code_length == 0 and k_max_code_length == 0, an additive tag of this build): k_words points at
+// one kv_codec_ext.h group blob coded on its own (a chain start: it holds its lane states) of up to 64 tokens, k_lut
+// and v_lut at the K and V decode tables (CF_KV_RANS_TABLE_BYTES each); the scales come from the blob header (per
+// 16-token page) and the other page fields are not read. The wavefront decodes the group into the same LDS symbol
+// tiles as the other codecs (offset binary, zero point 128) and applies the K scale per token to the scores. A blob
+// that continues a chain, whose header disagrees with the page (head_dim, token counts, page gaps) or whose rANS
+// chain does not end where the encoder started makes that (query row, KV head) NaN.
 //
 // Layout on gfx950: one wavefront per (query row, KV head) serves all gqa query heads of that KV head, so each
 // page is decoded once per row instead of once per query head. The wavefront decodes a chunk of the page's K and V
@@ -19,9 +26,12 @@
 // the chunk start, with the page's LUTs staged in LDS), then lane = token computes the scores of the chunk for every query head, the wavefront
 // folds them into the running (max, sum), and lane = dims accumulates the V rows. Nothing decoded leaves the CU.
 #include <cmath>
+#include <utility>
 
 #include "cf_device.hpp"
+#include "chromofold/kv_codec_ext.h"
 #include "chromofold/kv_cuda.h"
+#include "kv_group_decode.hpp"
 
 namespace {
 
@@ -75,13 +85,126 @@ __device__ void decode_span(const uint32_t *__restrict__ words, const int32_t *_
   }
 }
 
+// ---- rANS pages (kv_codec_ext.h format 4)
+constexpr uint32_t kRansWords = CF_KV_RANS_MAX_GROUP_WORDS + 64;  // staged K+V words + slack for idle lanes' reads
+
+// Sign-magnitude bytes (mag: |q|, signs: 0x80 per negative byte) -> offset-binary symbols q + 128, per byte.
+__device__ __forceinline__ uint32_t sm_to_offset_binary(uint32_t mag, uint32_t signs) {
+  const uint32_t neg = mag & ((signs >> 7) * 0xFFu);  // |q| of the negative bytes
+  return 0x80808080u + mag - (neg << 1);              // 128 + |q| or 128 - |q|, no carry between bytes
+}
+
+// Decode one self-contained group blob (RANS_HYBRID chain start, or the INT8 raw fallback) of `ntok` tokens and
+// head_dim hd (% 16 == 0, % 32 for RANS) into dk[token * stride + dim] / dv[token * stride + dim] as offset-binary
+// symbols, with the per-token K and V scales in kt / vt. A RANS group's K and V tables (ktab, vtab in HBM; not read
+// for an INT8 group) are staged in `tab` (LDS), its word streams in `s_w`.
+// Returns false (wave-uniform) when the blob is not a valid self-contained group for this page.
+__device__ bool rans_group_to_lds(const uint8_t *__restrict__ blob, const uint2 *__restrict__ ktab,
+                                  const uint2 *__restrict__ vtab, uint2 (*tab)[cfkv::kSlots], uint16_t *s_w,
+                                  uint32_t hd, uint32_t ntok, uint8_t *dk, uint8_t *dv, uint32_t stride, float *kt,
+                                  float *vt, int lane) {
+  const uint32_t codec = *reinterpret_cast<const uint32_t *>(blob);
+  const uint32_t cnt = *reinterpret_cast<const uint32_t *>(blob + 4);
+  const uint32_t chain = *reinterpret_cast<const uint16_t *>(blob + 8);
+  const uint16_t *tc = reinterpret_cast<const uint16_t *>(blob + 12);
+  const uint32_t D = *reinterpret_cast<const uint16_t *>(blob + 20);
+  if (D != hd || hd % 16 != 0 || hd > 128) return false;
+  if (codec != CF_KV_CODEC_INT8 && (codec != CF_KV_CODEC_RANS_HYBRID || hd % 32 != 0 || chain != 1)) return false;
+  // tokens must be contiguous: full 16-token pages, then at most one partial page, then empty pages
+  uint32_t total = 0;
+  bool open = true;
+  for (int G = 0; G < 4; ++G) {
+    const uint32_t n = tc[G];
+    if (n > 16 || (n && !open)) return false;
+    if (n < 16) open = false;
+    total += n;
+  }
+  if (total != ntok || total == 0) return false;
+  const float *ks = reinterpret_cast<const float *>(blob + 32), *vs = reinterpret_cast<const float *>(blob + 48);
+  kt[lane] = ks[lane >> 4];
+  vt[lane] = vs[lane >> 4];
+  const uint32_t NQ = hd / 4, G = static_cast<uint32_t>(lane) >> 4, t = static_cast<uint32_t>(lane) & 15;
+  // V quad q of a lane = tokens 4 tq .. 4 tq + 3 of its page at dim t + 16 i (tq = q / (hd / 16), i = q % (hd / 16))
+  auto put_v = [&](uint32_t q, uint32_t w) {
+    const uint32_t tq = q / (hd / 16), i = q % (hd / 16);
+    uint8_t *col = dv + (16 * G + 4 * tq) * stride + t + 16 * i;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) col[j * stride] = static_cast<uint8_t>(w >> (8 * j));
+  };
+  if (codec == CF_KV_CODEC_INT8) {
+    const uint32_t *raw = reinterpret_cast<const uint32_t *>(blob + cfkv::kHdr);
+    for (uint32_t q = 0; q < NQ; ++q) {
+      *reinterpret_cast<uint32_t *>(dk + lane * stride + 4 * q) = raw[q * 64 + lane];
+      put_v(q, raw[(NQ + q) * 64 + lane]);
+    }
+    return true;
+  }
+  const uint32_t nk = cnt & 0xFFFFu, nv = cnt >> 16;
+  if (nk + nv > CF_KV_RANS_MAX_GROUP_WORDS) return false;
+  for (uint32_t i = lane; i < cfkv::kSlots; i += kLanes) {  // {f | c << 16, spread} as the decoder reads it
+    const uint2 a = ktab[i], b = vtab[i];
+    tab[0][i] = uint2{(a.x & 2047u) | (((a.x >> 11) & 2047u) << 16), a.y};
+    tab[1][i] = uint2{(b.x & 2047u) | (((b.x >> 11) & 2047u) << 16), b.y};
+  }
+  const int RAW = cfkv::raw_words_of(static_cast<int>(hd));
+  const uint32_t *st = reinterpret_cast<const uint32_t *>(blob + cfkv::kHdr);
+  uint32_t xk = st[lane], xv = st[64 + lane];
+  const uint32_t *raw = st + 2 * 64;
+  // stage both word streams (u16, K then V) in LDS; whole u32 pairs (blobs are padded to 16 bytes)
+  const uint32_t *wsrc = raw + 2 * RAW;
+  for (uint32_t i = lane; i < (nk + nv + 1) / 2; i += kLanes) reinterpret_cast<uint32_t *>(s_w)[i] = wsrc[i];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const uint16_t *wk = s_w, *wv = s_w + nk;
+  for (uint32_t sg = 0; sg < hd / 32; ++sg) {
+    uint32_t wK[7], wV[7];
+#pragma unroll
+    for (int w = 0; w < 7; ++w) {
+      wK[w] = raw[(7 * sg + w) * 64 + lane];
+      wV[w] = raw[RAW + (7 * sg + w) * 64 + lane];
+    }
+    [&]<int... M>(std::integer_sequence<int, M...>) {
+      (
+          [&] {
+            constexpr int m = M;
+            constexpr uint32_t rA = cfkv::kFrame[2 * m], rB = cfkv::kFrame[2 * m + 1];
+            constexpr int nw = cfkv::kNWord[m], cwi = m < 2 ? 2 : 5;
+            const uint2 ek = cfkv::rans_lookup(tab[0], xk), ev = cfkv::rans_lookup(tab[1], xv);
+            uint32_t selk, selv;
+            const uint32_t wdk = cfkv::rans_advance(ek.x, xk, wk, selk);
+            const uint32_t wdv = cfkv::rans_advance(ev.x, xv, wv, selv);
+            xk = __builtin_amdgcn_perm(xk, wdk, selk);
+            xv = __builtin_amdgcn_perm(xv, wdv, selv);
+            const uint32_t spk = rA ? __builtin_amdgcn_alignbit(ek.y, ek.y, 32 - rA) : ek.y;
+            const uint32_t spv = rA ? __builtin_amdgcn_alignbit(ev.y, ev.y, 32 - rA) : ev.y;
+            const uint32_t q0 = 8 * sg + 2 * m;
+            *reinterpret_cast<uint32_t *>(dk + lane * stride + 4 * q0) =
+                sm_to_offset_binary(cfkv::quad_mag<rA>(wK[nw], wK[cwi], spk), cfkv::quad_signs<rA>(wK[6]));
+            *reinterpret_cast<uint32_t *>(dk + lane * stride + 4 * (q0 + 1)) =
+                sm_to_offset_binary(cfkv::quad_mag<rB>(wK[nw], wK[cwi], spk), cfkv::quad_signs<rB>(wK[6]));
+            put_v(q0, sm_to_offset_binary(cfkv::quad_mag<rA>(wV[nw], wV[cwi], spv), cfkv::quad_signs<rA>(wV[6])));
+            put_v(q0 + 1, sm_to_offset_binary(cfkv::quad_mag<rB>(wV[nw], wV[cwi], spv), cfkv::quad_signs<rB>(wV[6])));
+          }(),
+          ...);
+    }(std::make_integer_sequence<int, 4>{});
+  }
+  // a group coded on its own ends where the encoder started (2^16 in every lane of both streams) and has consumed
+  // exactly its words
+  const bool ok = xk == 65536u && xv == 65536u && wk == s_w + nk && wv == s_w + nk + nv;
+  return __builtin_amdgcn_ballot_w64(!ok) == 0;
+}
+
 template <int DPL>  // dims per lane: head_dim <= 64 * DPL
 __global__ __launch_bounds__(kLanes) void legacy_kernel(cf_kv_paged_attention_desc d) {
   __shared__ uint8_t s_k[kChunkSyms + kLanes * kRowPad], s_v[kChunkSyms + kLanes * kRowPad];
   __shared__ float s_q[kHeadsPass][64 * DPL];
   __shared__ float s_p[kHeadsPass][kLanes];
   __shared__ float s_ks[64 * DPL];
-  __shared__ int32_t s_lut[2][1 << kLutMaxLen];
+  __shared__ __align__(16) int32_t s_lut[2][1 << kLutMaxLen];  // Huffman LUTs, or the rANS K and V tables
+  __shared__ __align__(16) uint16_t s_w[kRansWords];
+  __shared__ float s_kt[kLanes], s_vt[kLanes];  // rANS pages: per-token K and V scales
+  static_assert(sizeof(s_lut) >= 2 * cfkv::kSlots * sizeof(uint2), "the rANS tables share the LUT area");
 
   const int lane = threadIdx.x;
   const uint32_t row = blockIdx.x, kvh = blockIdx.y;
@@ -90,6 +213,7 @@ __global__ __launch_bounds__(kLanes) void legacy_kernel(cf_kv_paged_attention_de
   const uint32_t qtok = d.query_token_begin + row;
   const uint32_t wbegin = (d.causal_window == 0 || qtok + 1 <= d.causal_window) ? 0u : qtok + 1 - d.causal_window;
 
+  bool bad = false;  // a rANS page that is not a valid self-contained group for its descriptor (see the file header)
   for (uint32_t h0 = 0; h0 < gqa; h0 += kHeadsPass) {
     const int nh = static_cast<int>(min<uint32_t>(kHeadsPass, gqa - h0));
     // queries of this pass (softmax scale applied to the dot product, as the reference does)
@@ -111,7 +235,7 @@ __global__ __launch_bounds__(kLanes) void legacy_kernel(cf_kv_paged_attention_de
 
     // fold a chunk of up to 64 tokens: lane = token scores, then lane = dims V accumulation
     auto fold = [&](int ntok, bool dense, const float *kd, const float *vd, const float *vsc, int zp,
-                    uint32_t tok0, uint32_t hd, uint32_t stride) {
+                    uint32_t tok0, uint32_t hd, uint32_t stride, const float *kt = nullptr) {
       float sc[kHeadsPass];
       const uint32_t token = tok0 + lane;
       const bool vis = lane < ntok && token >= wbegin && token <= qtok;
@@ -126,6 +250,10 @@ __global__ __launch_bounds__(kLanes) void legacy_kernel(cf_kv_paged_attention_de
 #pragma unroll
           for (int h = 0; h < kHeadsPass; ++h) sc[h] += s_q[h][dd] * kv;
         }
+      }
+      if (kt && lane < ntok) {
+#pragma unroll
+        for (int h = 0; h < kHeadsPass; ++h) sc[h] *= kt[lane];
       }
 #pragma unroll
       for (int h = 0; h < kHeadsPass; ++h) {
@@ -174,6 +302,27 @@ __global__ __launch_bounds__(kLanes) void legacy_kernel(cf_kv_paged_attention_de
       if (pg.token_count == 0) continue;
       // skip pages entirely outside the visible window
       if (pg.token_begin > qtok || pg.token_begin + pg.token_count <= wbegin) continue;
+      if (pg.fixed_code_length == 0 && pg.k_max_code_length == 0) {  // rANS page (kv_codec_ext.h group blob)
+        if (pg.token_count > static_cast<uint32_t>(kLanes) || pg.head_dim > D) {
+          bad = true;
+          continue;
+        }
+        for (uint32_t dd = lane; dd < D; dd += kLanes) s_ks[dd] = 1.0f;
+        uint2(*tab)[cfkv::kSlots] = reinterpret_cast<uint2(*)[cfkv::kSlots]>(&s_lut[0][0]);
+        const uint32_t stride = pg.head_dim + kRowPad;
+        if (!rans_group_to_lds(reinterpret_cast<const uint8_t *>(pg.k_words),
+                               reinterpret_cast<const uint2 *>(pg.k_lut), reinterpret_cast<const uint2 *>(pg.v_lut),
+                               tab, s_w, pg.head_dim, pg.token_count, s_k, s_v, stride, s_kt, s_vt, lane)) {
+          bad = true;
+          continue;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        fold(static_cast<int>(pg.token_count), false, nullptr, nullptr, s_vt, 128, pg.token_begin, pg.head_dim,
+             stride, s_kt);
+        continue;
+      }
       for (uint32_t dd = lane; dd < min(D, pg.head_dim); dd += kLanes) s_ks[dd] = pg.k_scales[dd];
       if (pg.head_dim == 0 || pg.head_dim > CF_KV_MAX_HEAD_DIM) continue;
       // Huffman pages: stage both LUTs in LDS when they fit (the lookups are the decoder's hot loop)
@@ -214,7 +363,7 @@ __global__ __launch_bounds__(kLanes) void legacy_kernel(cf_kv_paged_attention_de
 #pragma unroll
       for (int j = 0; j < DPL; ++j) {
         const uint32_t dd = lane + 64 * j;
-        if (dd < D) out[dd] = acc[h][j] * inv;
+        if (dd < D) out[dd] = bad ? __builtin_nanf("") : acc[h][j] * inv;
       }
     }
   }

@@ -156,3 +156,44 @@ def rans_encode_blocks(sym, freq, block):
     data.extend([0] * 8)
     return (np.array(data, np.uint8), np.array(boff, np.int32), np.array(st0, np.uint32), slot2sym,
             freq.astype(np.int32), cum.astype(np.int32))
+
+
+def rans_page(k, v, kv_head, token_begin, codec=2, tables=None, continues=False, second=None):
+    """An rANS page of the reference seam (tag: fixed_code_length == 0 and k_max_code_length == 0): one
+    kv_codec_ext.h group of up to 64 tokens, coded on its own by the library's host encoder (codec 2 = RANS_HYBRID,
+    1 = INT8), k_words = the blob, k_lut / v_lut = its K and V tables. kd / vd are the values the oracle decodes from
+    the blob. `continues` codes it as the second group of a chain pair after `second` (k, v of the first group) and
+    returns that second blob: a page the seam must refuse."""
+    from chromofold_amd import kv
+    T, D = k.shape
+
+    def pages_of(x):
+        n = (x.shape[0] + 15) // 16
+        P = np.zeros((n, 16, D), np.float32)
+        P.reshape(-1, D)[:x.shape[0]] = x
+        return P, np.array([min(16, x.shape[0] - 16 * g) for g in range(n)], np.uint32)
+    K, tc = pages_of(k)
+    V, _ = pages_of(v)
+    npg = K.shape[0]
+    if tables is None:
+        tables = np.concatenate([kv.build_table(K), kv.build_table(V)])
+    if continues:
+        K0, tc0 = pages_of(second[0])
+        V0, _ = pages_of(second[1])
+        blob, offs = kv.encode_groups(codec, np.concatenate([K0, K]), np.concatenate([V0, V]), D, tables,
+                                      np.array([0, K0.shape[0]], np.uint64), np.array([K0.shape[0], npg], np.uint32),
+                                      np.array([0, 0], np.uint32), np.concatenate([tc0, tc]),
+                                      continues=np.array([0, 1], np.uint8))
+        blob = blob[int(offs[1]) * 16:].copy()
+        kd = vd = None
+    else:
+        blob, _ = kv.encode_groups(codec, K, V, D, tables, np.array([0], np.uint64), np.array([npg], np.uint32),
+                                   np.array([0], np.uint32), tc)
+        ks, vs, ksc, vsc, _ = O.kv_decode_group(blob, tables, 0, D)
+        kd = np.concatenate([(ks[g, :tc[g]].astype(np.float32) - 128) * ksc[g] for g in range(npg)])
+        vd = np.concatenate([(vs[g, :tc[g]].astype(np.float32) - 128) * vsc[g] for g in range(npg)])
+    tb = kv.TABLE_BYTES
+    zi, zf = np.zeros(4, np.int32), np.zeros(4, np.float32)
+    page = HostPage(kv_head, token_begin, T, D, blob, zi, tables[:tb], zf, blob[:16], zi, tables[tb:2 * tb], zf,
+                    64, 0, 0, 128, 0)
+    return page, kd, vd

@@ -119,3 +119,62 @@ def test_page_order_window_and_empty(dev):
     pk = PagedKv(pages, str(dev))
     out = pk.attention(torch.from_numpy(q).to(dev), kvh, gqa, 10, 0.125).cpu().numpy()
     assert (out == 0).all()
+
+
+@pytest.mark.parametrize("hd", [32, 64, 96, 128])
+def test_rans_pages_with_fixed_huffman_and_tail(dev, hd):
+    """The rANS page tag of the seam (kv_cuda.h: fixed_code_length == 0, k_max_code_length == 0): kv_codec_ext.h
+    groups coded on their own (full and partial, RANS_HYBRID and the INT8 raw fallback of a group holding -128)
+    mixed with fixed-width and Huffman pages of the same heads, a dense tail, GQA 7, a causal window; against the
+    fp64 oracle over the values the oracle decodes from each page."""
+    from legacy_helpers import rans_page
+    rng = np.random.default_rng(900 + hd)
+    kvh, gqa = 2, 7
+    pages, deq = [], []
+    for h in range(kvh):
+        tok = 0
+        for kind, n in (("rans", 64), ("fixed", 32), ("rans", 40), ("huff", 48), ("int8", 64), ("rans", 7)):
+            k = rng.standard_normal((n, hd)).astype(np.float32)
+            v = (rng.standard_normal((n, hd)) * 0.3).astype(np.float32)
+            if kind == "fixed":
+                page, kd, vd = fixed_page(k, v, h, tok, 8)
+            elif kind == "huff":
+                page, kd, vd = huffman_page(k, v, h, tok)
+            else:
+                if kind == "int8":
+                    k[3, 5] = np.nan  # quantises to -128 (lrint semantics): the encoder stores the group as INT8
+                page, kd, vd = rans_page(k, v, h, tok)
+            pages.append(page)
+            deq.append((h, tok, kd, vd))
+            tok += n
+    T = tok
+    tail_k = rng.standard_normal((5, kvh, hd)).astype(np.float32)
+    tail_v = rng.standard_normal((5, kvh, hd)).astype(np.float32)
+    q = rng.standard_normal((3, kvh * gqa, hd)).astype(np.float32)
+    got, ref = _run(dev, deq, pages, q, kvh, gqa, T + 2, 1 / np.sqrt(hd), tail=(T, tail_k, tail_v))
+    assert np.isfinite(got).all()
+    assert np.abs(got - ref).max() <= ABS_TOL
+    got, ref = _run(dev, deq, pages, q, kvh, gqa, T - 30, 1 / np.sqrt(hd), window=90)
+    assert np.abs(got - ref).max() <= ABS_TOL
+
+
+def test_rans_pages_refused_as_nan(dev):
+    """Pages the seam cannot decode on their own give NaN for their (row, KV head) and leave the other head
+    untouched: a group that continues a chain (its states live in the group before it), a descriptor whose
+    token_count disagrees with the blob, and one whose head_dim disagrees."""
+    from legacy_helpers import rans_page
+    rng = np.random.default_rng(77)
+    hd, kvh, gqa = 64, 2, 2
+    k0, v0 = rng.standard_normal((64, hd)).astype(np.float32), rng.standard_normal((64, hd)).astype(np.float32)
+    k1, v1 = rng.standard_normal((64, hd)).astype(np.float32), rng.standard_normal((64, hd)).astype(np.float32)
+    good, kd, vd = rans_page(k1, v1, 1, 0)
+    q = rng.standard_normal((1, kvh * gqa, hd)).astype(np.float32)
+    cont, _, _ = rans_page(k1, v1, 0, 0, continues=True, second=(k0, v0))
+    wrong_count, _, _ = rans_page(k0, v0, 0, 0)
+    wrong_count.token_count = 60
+    wrong_dim, _, _ = rans_page(k0, v0, 0, 0)
+    wrong_dim.head_dim = 32
+    for bad in (cont, wrong_count, wrong_dim):
+        got, ref = _run(dev, [(1, 0, kd, vd)], [bad, good], q, kvh, gqa, 63, 0.125)
+        assert np.isnan(got[:, :gqa]).all()                       # KV head 0: the refused page
+        assert np.abs(got[:, gqa:] - ref[:, gqa:]).max() <= ABS_TOL  # KV head 1: decoded normally
