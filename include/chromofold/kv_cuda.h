@@ -7,7 +7,11 @@
  * Codec selection per page (legacy pages decode bit-for-bit as in the reference):
  *   fixed_code_length > 0                       fixed-width MSB-first codes of that many bits
  *   fixed_code_length == 0, k_max_code_length>0  canonical-Huffman LUT codes (lut[look] = sym | len << 8)
- *   fixed_code_length == 0, k_max_code_length==0 rANS page (additive codec, see kv_codec_ext.h)
+ *   fixed_code_length == 0, k_max_code_length==0 rANS page (additive to the reference): k_words points at one
+ *       kv_codec_ext.h group blob of up to 64 tokens coded on its own (a chain start, or the INT8 raw fallback),
+ *       k_lut / v_lut at its K and V tables (CF_KV_RANS_TABLE_BYTES each); the scales come from the blob header,
+ *       the other page fields are not read. A blob that continues a chain or disagrees with the page's head_dim
+ *       or token_count makes the outputs of that (query row, KV head) NaN.
  */
 #ifndef CHROMOFOLD_KV_CUDA_H
 #define CHROMOFOLD_KV_CUDA_H
