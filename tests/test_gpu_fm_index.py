@@ -192,3 +192,39 @@ def test_staged_kernels_many_items_per_lane(dev):
     pos = torch.empty(rows.size, dtype=torch.int32, device=dev)
     fm.locate(_i32(rows, dev), pos)
     assert np.array_equal(pos.cpu().numpy(), O.fm_locate(f, rows))
+
+
+def test_gpu_suffix_array_c2_size(dev):
+    """BASELINE C2's full text: 2^24 Zipf tokens (V = 32000) plus the sentinel. The GPU suffix array (prefix doubling
+    on hipCUB radix sorts) equals the oracle's radix-doubling suffix array, every entry."""
+    from chromofold_amd import synth
+    from chromofold_amd.search import gpu_suffix_array
+    tok = synth.zipf_tokens(1 << 24, 32000, 1.1, synth.SEED_C1 + 24)
+    s = O.fm_text(tok)
+    assert np.array_equal(gpu_suffix_array(_i32(s, dev)).cpu().numpy(), O.suffix_array(s))
+
+
+def test_fm_c2_shape_patterns_8_to_32(dev):
+    """BASELINE C2's shape: the FM index of 2^24 Zipf tokens built on the GPU, queried with patterns of length 8-32
+    (cut from the text, plus random ones that almost never occur). Count and ranges of 300K patterns and locate of
+    256K rows, against the oracle over the same index arrays, bit for bit; the cut patterns all occur."""
+    import torch
+    from chromofold_amd import synth
+    from chromofold_amd.search import build_fm
+    vocab, n = 32000, 1 << 24
+    tok = synth.zipf_tokens(n, vocab, 1.1, synth.SEED_C1 + 25)
+    fm, _ = build_fm(torch.from_numpy(tok.view(np.int32)).to(dev), 32)
+    flat, pstart, plen = synth.fm_patterns(tok, 270_000, 30_000, vocab, 46, 8, 32)
+    assert plen.min() == 8 and plen.max() == 32
+    dpat, dps, dpl = (_i32(a, dev) for a in (flat, pstart, plen))
+    cnt = fm.count(dpat, dps, dpl).cpu().numpy().view(np.uint32)
+    lo, hi = (x.cpu().numpy() for x in fm.ranges(dpat, dps, dpl))
+    f = _fm_oracle_view(fm)
+    assert np.array_equal(cnt, O.fm_count(f, flat, pstart, plen))
+    assert (cnt[:270_000] >= 1).all()
+    rlo, rhi = O.fm_ranges(f, flat, pstart, plen)
+    assert np.array_equal(lo, rlo) and np.array_equal(hi, rhi)
+    rows = np.concatenate([np.arange(a, b, dtype=np.int32) for a, b in zip(lo, hi) if b > a])[:256 * 1024]
+    pos = torch.empty(rows.size, dtype=torch.int32, device=dev)
+    fm.locate(_i32(rows, dev), pos)
+    assert np.array_equal(pos.cpu().numpy(), O.fm_locate(f, rows))

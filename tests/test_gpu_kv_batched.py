@@ -305,3 +305,36 @@ def test_cascade_v_magnitudes(dev, v_mult):
     assert np.isfinite(got).all()
     ref = oracle_batched(kvb, data, q, qp, sc, 4)
     assert head_err(got, ref) <= TOL
+
+
+def test_c5_long_context_131k_every_row(dev):
+    """BASELINE C5's long-context shape: 4 sequences x 131072 tokens, 8 KV / 32 q heads, hd 128, sealed on the
+    device (2048 groups per sequence and head), one decode token each. Every (sequence, query head) row against the
+    float64 oracle decoding the pool's own blobs (O.kv_pool_attention, all host threads), normwise <= 1e-3."""
+    import torch
+    import oracle as O
+    from chromofold_amd import kv
+    S, T, H, QH, D = 4, 131072, 8, 32, 128
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0xC5)
+    K = torch.randn((S, H, T, D), generator=gen, device=dev)
+    V = torch.randn((S, H, T, D), generator=gen, device=dev)
+    Kh = K[0, 0, :512].cpu().numpy().reshape(-1, 16, D)
+    Vh = V[0, 0, :512].cpu().numpy().reshape(-1, 16, D)
+    tables = np.concatenate([t for _ in range(H) for t in (kv.build_table(Kh), kv.build_table(Vh))])
+    kvb = kv.seal_device(kv.CODEC_RANS_HYBRID, K, V, torch.from_numpy(tables).to(dev))
+    del K, V
+    q = torch.randn((S, QH, D), generator=gen, device=dev)
+    qp = torch.tensor([T - 1, T - 1, 70000, 131000], dtype=torch.int32, device=dev)
+    out = torch.full_like(q, float("nan"))
+    sc = 1.0 / np.sqrt(D)
+    kvb.attention(q, out, qp, sc)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all()
+    ref = O.kv_pool_attention(kvb.pool.cpu().numpy(), kvb.group_offsets.cpu().numpy().view(np.uint32),
+                              np.full(S, T, np.uint32), qp.cpu().numpy().view(np.uint32), tables, q.cpu().numpy(),
+                              H, D, sc)
+    err = np.abs(got - ref).max(axis=2) / np.abs(ref).max(axis=2)
+    assert err.max() <= TOL, err.max()
+    print(f"C5 4 x 131072: worst normwise error over {err.size} rows {err.max():.3e}")
