@@ -15,17 +15,24 @@
 // rANS pages (fixed_code_length == 0 and k_max_code_length == 0, an additive tag of this build): k_words points at
 // one kv_codec_ext.h group blob coded on its own (a chain start: it holds its lane states) of up to 64 tokens, k_lut
 // and v_lut at the K and V decode tables (CF_KV_RANS_TABLE_BYTES each); the scales come from the blob header (per
-// 16-token page) and the other page fields are not read. The wavefront decodes the group into the same LDS symbol
-// tiles as the other codecs (offset binary, zero point 128) and applies the K scale per token to the scores. A blob
-// that continues a chain, whose header disagrees with the page (head_dim, token counts, page gaps) or whose rANS
-// chain does not end where the encoder started makes that (query row, KV head) NaN.
+// 16-token page) and the other page fields are not read. A blob that continues a chain, whose header disagrees with
+// the page (head_dim, token counts, page gaps) or whose rANS chain does not end where the encoder started makes that
+// (query row, KV head) NaN.
 //
-// Layout on gfx950: one wavefront per (query row, KV head) serves all gqa query heads of that KV head, so each
-// page is decoded once per row instead of once per query head. The wavefront decodes a chunk of the page's K and V
-// symbols into LDS (fixed-width: lane-strided random access; Huffman: one lane per code block, skip-decoding to
-// the chunk start, with the page's LUTs staged in LDS), then lane = token computes the scores of the chunk for every query head, the wavefront
-// folds them into the running (max, sum), and lane = dims accumulates the V rows. Nothing decoded leaves the CU.
+// Layout on gfx950. The query vectors of a KV head are its (query row, query head) pairs, vector v = row * gqa +
+// head. One 4-wavefront workgroup serves 64 vectors (16 per wavefront) of one KV head over one context split (the
+// head's pages taken round-robin by their order in the descriptor array; the dense tail in 64-token chunks after
+// them). Per page chunk of up to 64 tokens the workgroup decodes K and V once into LDS as integer symbols (K
+// token-major, V dim-major), then every wavefront runs its 16 vectors through:
+//   QK^T  v_mfma_f32_16x16x16f16: A = the queries times the page's per-channel K scale, split into f16 hi + lo
+//         parts; B = K symbol - zero point, exact in f16. The scores are fp32-grade.
+//   softmax online per vector in fp32 (each vector's row of the 16x16 tile lives in 16 lanes);
+//   P.V   the same MFMA: A = p times the token's V scale, f16 hi + lo, through a small LDS tile; B = V symbol - zero
+//         point, exact.
+// The dense tail (fp32) takes the same softmax on VALU. Split partials (m, l, acc) go to a per-GPU device array and
+// a second kernel merges them; with one split the workgroup writes the output itself.
 #include <cmath>
+#include <mutex>
 #include <utility>
 
 #include "cf_device.hpp"
@@ -35,11 +42,19 @@
 
 namespace {
 
-constexpr int kLanes = 64;
-constexpr int kChunkSyms = 8192;  // symbols of K (and of V) staged per chunk: 64 tokens at head_dim 128
-constexpr int kRowPad = 4;        // bytes added to each staged row
-constexpr int kHeadsPass = 8;     // query heads served per pass over the pages
-constexpr int kLutMaxLen = 12;    // Huffman LUTs of up to 2^12 entries are staged in LDS
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kVecs = 16 * kWaves;                      // query vectors per workgroup
+constexpr int kChunk = 64;                              // tokens staged per chunk
+constexpr int kMaxD = CF_KV_MAX_HEAD_DIM;
+constexpr int kKStride = kMaxD + 4;                     // bytes per staged K row (token-major)
+constexpr int kVStride = kChunk + 4;                    // bytes per staged V row (dim-major)
+constexpr int kPStride = kChunk + 4;                    // halves per P row
+constexpr int kLutMaxLen = 12;                          // Huffman LUTs of up to 2^12 entries are staged in LDS
+constexpr uint32_t kRansWords = CF_KV_RANS_MAX_GROUP_WORDS + 64;  // staged rANS words + slack for idle lanes' reads
 
 // canonical-Huffman LUT decode at bit `pos` (MSB-first), returns sym | len << 8
 __device__ __forceinline__ int huff_at(const uint32_t *__restrict__ words, const int32_t *__restrict__ lut, int maxlen,
@@ -59,34 +74,34 @@ __device__ __forceinline__ int fixed_at(const uint32_t *__restrict__ words, uint
   return static_cast<int>((w >> ((32u - bits) - static_cast<uint32_t>(bit & 31))) & ((1u << bits) - 1u));
 }
 
-// Decode symbols [s0, s1) of one stream (rows of hd symbols) into dst, row r at dst + r * stride (a padded row
-// stride keeps the lane-per-token reads of the scoring loop off a single LDS bank).
+// Decode symbols [s0, s1) of one stream (rows of hd symbols) with the workgroup's threads; put(token, dim, sym) with
+// the token relative to s0 / hd.
+template <typename Put>
 __device__ void decode_span(const uint32_t *__restrict__ words, const int32_t *__restrict__ boff,
                             const int32_t *__restrict__ lut, uint32_t maxlen, uint32_t fixed_bits, uint32_t block,
-                            int64_t s0, int64_t s1, uint32_t hd, uint32_t stride, uint8_t *__restrict__ dst, int lane) {
-  auto put = [&](int64_t i, int sym) {
+                            int64_t s0, int64_t s1, uint32_t hd, int tid, const Put &put) {
+  auto at = [&](int64_t i, int sym) {
     const uint32_t rel = static_cast<uint32_t>(i - s0), r = rel / hd;
-    dst[r * stride + (rel - r * hd)] = static_cast<uint8_t>(sym);
+    put(r, rel - r * hd, static_cast<uint32_t>(sym));
   };
   if (fixed_bits) {
-    for (int64_t i = s0 + lane; i < s1; i += kLanes) put(i, fixed_at(words, fixed_bits, i));
+    for (int64_t i = s0 + tid; i < s1; i += kThreads) at(i, fixed_at(words, fixed_bits, i));
     return;
   }
-  // Huffman: one lane per code block intersecting [s0, s1); skip-decode up to s0 inside the first block
+  // Huffman: one thread per code block intersecting [s0, s1); skip-decode up to s0 inside the first block
   const int64_t b0 = s0 / block, b1 = (s1 + block - 1) / block;
-  for (int64_t b = b0 + lane; b < b1; b += kLanes) {
+  for (int64_t b = b0 + tid; b < b1; b += kThreads) {
     int64_t pos = boff[b];
     const int64_t first = b * block, last = min(first + static_cast<int64_t>(block), s1);
     for (int64_t i = first; i < last; ++i) {
       const int e = huff_at(words, lut, static_cast<int>(maxlen), pos);
       pos += e >> 8;
-      if (i >= s0) put(i, e & 0xff);
+      if (i >= s0) at(i, e & 0xff);
     }
   }
 }
 
 // ---- rANS pages (kv_codec_ext.h format 4)
-constexpr uint32_t kRansWords = CF_KV_RANS_MAX_GROUP_WORDS + 64;  // staged K+V words + slack for idle lanes' reads
 
 // Sign-magnitude bytes (mag: |q|, signs: 0x80 per negative byte) -> offset-binary symbols q + 128, per byte.
 __device__ __forceinline__ uint32_t sm_to_offset_binary(uint32_t mag, uint32_t signs) {
@@ -94,21 +109,21 @@ __device__ __forceinline__ uint32_t sm_to_offset_binary(uint32_t mag, uint32_t s
   return 0x80808080u + mag - (neg << 1);              // 128 + |q| or 128 - |q|, no carry between bytes
 }
 
-// Decode one self-contained group blob (RANS_HYBRID chain start, or the INT8 raw fallback) of `ntok` tokens and
-// head_dim hd (% 16 == 0, % 32 for RANS) into dk[token * stride + dim] / dv[token * stride + dim] as offset-binary
-// symbols, with the per-token K and V scales in kt / vt. A RANS group's K and V tables (ktab, vtab in HBM; not read
-// for an INT8 group) are staged in `tab` (LDS), its word streams in `s_w`.
+// One wavefront decodes a self-contained group blob (RANS_HYBRID chain start, or the INT8 raw fallback) of `ntok`
+// tokens and head_dim hd (% 16 == 0, % 32 for RANS) into sk[token * kKStride + dim] and svt[dim * kVStride + token]
+// as offset-binary symbols, with the per-token K and V scales in kt / vt. A RANS group's K and V tables (ktab, vtab
+// in HBM; not read for an INT8 group) are staged in `tab` (LDS), its word streams in `s_w`.
 // Returns false (wave-uniform) when the blob is not a valid self-contained group for this page.
 __device__ bool rans_group_to_lds(const uint8_t *__restrict__ blob, const uint2 *__restrict__ ktab,
                                   const uint2 *__restrict__ vtab, uint2 (*tab)[cfkv::kSlots], uint16_t *s_w,
-                                  uint32_t hd, uint32_t ntok, uint8_t *dk, uint8_t *dv, uint32_t stride, float *kt,
-                                  float *vt, int lane) {
+                                  uint32_t hd, uint32_t ntok, uint8_t *sk, uint8_t *svt, float *kt, float *vt,
+                                  int lane) {
   const uint32_t codec = *reinterpret_cast<const uint32_t *>(blob);
   const uint32_t cnt = *reinterpret_cast<const uint32_t *>(blob + 4);
   const uint32_t chain = *reinterpret_cast<const uint16_t *>(blob + 8);
   const uint16_t *tc = reinterpret_cast<const uint16_t *>(blob + 12);
   const uint32_t D = *reinterpret_cast<const uint16_t *>(blob + 20);
-  if (D != hd || hd % 16 != 0 || hd > 128) return false;
+  if (D != hd || hd % 16 != 0 || hd > kMaxD) return false;
   if (codec != CF_KV_CODEC_INT8 && (codec != CF_KV_CODEC_RANS_HYBRID || hd % 32 != 0 || chain != 1)) return false;
   // tokens must be contiguous: full 16-token pages, then at most one partial page, then empty pages
   uint32_t total = 0;
@@ -124,24 +139,24 @@ __device__ bool rans_group_to_lds(const uint8_t *__restrict__ blob, const uint2 
   kt[lane] = ks[lane >> 4];
   vt[lane] = vs[lane >> 4];
   const uint32_t NQ = hd / 4, G = static_cast<uint32_t>(lane) >> 4, t = static_cast<uint32_t>(lane) & 15;
-  // V quad q of a lane = tokens 4 tq .. 4 tq + 3 of its page at dim t + 16 i (tq = q / (hd / 16), i = q % (hd / 16))
+  // V quad q of a lane = tokens 4 tq .. 4 tq + 3 of its page at dim t + 16 i (tq = q / (hd / 16), i = q % (hd / 16)):
+  // four consecutive bytes of a dim-major row
   auto put_v = [&](uint32_t q, uint32_t w) {
     const uint32_t tq = q / (hd / 16), i = q % (hd / 16);
-    uint8_t *col = dv + (16 * G + 4 * tq) * stride + t + 16 * i;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) col[j * stride] = static_cast<uint8_t>(w >> (8 * j));
+    *reinterpret_cast<uint32_t *>(svt + (t + 16 * i) * kVStride + 16 * G + 4 * tq) = w;
   };
+  auto put_k = [&](uint32_t q, uint32_t w) { *reinterpret_cast<uint32_t *>(sk + lane * kKStride + 4 * q) = w; };
   if (codec == CF_KV_CODEC_INT8) {
     const uint32_t *raw = reinterpret_cast<const uint32_t *>(blob + cfkv::kHdr);
     for (uint32_t q = 0; q < NQ; ++q) {
-      *reinterpret_cast<uint32_t *>(dk + lane * stride + 4 * q) = raw[q * 64 + lane];
+      put_k(q, raw[q * 64 + lane]);
       put_v(q, raw[(NQ + q) * 64 + lane]);
     }
     return true;
   }
   const uint32_t nk = cnt & 0xFFFFu, nv = cnt >> 16;
   if (nk + nv > CF_KV_RANS_MAX_GROUP_WORDS) return false;
-  for (uint32_t i = lane; i < cfkv::kSlots; i += kLanes) {  // {f | c << 16, spread} as the decoder reads it
+  for (uint32_t i = lane; i < cfkv::kSlots; i += 64) {  // {f | c << 16, spread} as the decoder reads it
     const uint2 a = ktab[i], b = vtab[i];
     tab[0][i] = uint2{(a.x & 2047u) | (((a.x >> 11) & 2047u) << 16), a.y};
     tab[1][i] = uint2{(b.x & 2047u) | (((b.x >> 11) & 2047u) << 16), b.y};
@@ -152,7 +167,7 @@ __device__ bool rans_group_to_lds(const uint8_t *__restrict__ blob, const uint2 
   const uint32_t *raw = st + 2 * 64;
   // stage both word streams (u16, K then V) in LDS; whole u32 pairs (blobs are padded to 16 bytes)
   const uint32_t *wsrc = raw + 2 * RAW;
-  for (uint32_t i = lane; i < (nk + nv + 1) / 2; i += kLanes) reinterpret_cast<uint32_t *>(s_w)[i] = wsrc[i];
+  for (uint32_t i = lane; i < (nk + nv + 1) / 2; i += 64) reinterpret_cast<uint32_t *>(s_w)[i] = wsrc[i];
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -179,10 +194,8 @@ __device__ bool rans_group_to_lds(const uint8_t *__restrict__ blob, const uint2 
             const uint32_t spk = rA ? __builtin_amdgcn_alignbit(ek.y, ek.y, 32 - rA) : ek.y;
             const uint32_t spv = rA ? __builtin_amdgcn_alignbit(ev.y, ev.y, 32 - rA) : ev.y;
             const uint32_t q0 = 8 * sg + 2 * m;
-            *reinterpret_cast<uint32_t *>(dk + lane * stride + 4 * q0) =
-                sm_to_offset_binary(cfkv::quad_mag<rA>(wK[nw], wK[cwi], spk), cfkv::quad_signs<rA>(wK[6]));
-            *reinterpret_cast<uint32_t *>(dk + lane * stride + 4 * (q0 + 1)) =
-                sm_to_offset_binary(cfkv::quad_mag<rB>(wK[nw], wK[cwi], spk), cfkv::quad_signs<rB>(wK[6]));
+            put_k(q0, sm_to_offset_binary(cfkv::quad_mag<rA>(wK[nw], wK[cwi], spk), cfkv::quad_signs<rA>(wK[6])));
+            put_k(q0 + 1, sm_to_offset_binary(cfkv::quad_mag<rB>(wK[nw], wK[cwi], spk), cfkv::quad_signs<rB>(wK[6])));
             put_v(q0, sm_to_offset_binary(cfkv::quad_mag<rA>(wV[nw], wV[cwi], spv), cfkv::quad_signs<rA>(wV[6])));
             put_v(q0 + 1, sm_to_offset_binary(cfkv::quad_mag<rB>(wV[nw], wV[cwi], spv), cfkv::quad_signs<rB>(wV[6])));
           }(),
@@ -195,178 +208,418 @@ __device__ bool rans_group_to_lds(const uint8_t *__restrict__ blob, const uint2 
   return __builtin_amdgcn_ballot_w64(!ok) == 0;
 }
 
-template <int DPL>  // dims per lane: head_dim <= 64 * DPL
-__global__ __launch_bounds__(kLanes) void legacy_kernel(cf_kv_paged_attention_desc d) {
-  __shared__ uint8_t s_k[kChunkSyms + kLanes * kRowPad], s_v[kChunkSyms + kLanes * kRowPad];
-  __shared__ float s_q[kHeadsPass][64 * DPL];
-  __shared__ float s_p[kHeadsPass][kLanes];
-  __shared__ float s_ks[64 * DPL];
-  __shared__ __align__(16) int32_t s_lut[2][1 << kLutMaxLen];  // Huffman LUTs, or the rANS K and V tables
+// ---- the attention kernel
+
+// Four symbol bytes b (offset binary around zp) as exact f16 values b - zp: 1024 + b from the 0x64 exponent byte,
+// minus 1024 + zp (integers below 2048 are exact in f16).
+__device__ __forceinline__ half4_t sym4_to_half4(uint32_t b, _Float16 base) {
+  half4_t h;
+  uint32_t *w = reinterpret_cast<uint32_t *>(&h);
+  w[0] = __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u);
+  w[1] = __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u);
+  const half4_t off = {base, base, base, base};
+  return h - off;
+}
+
+__device__ __forceinline__ float4_t mfma16(half4_t a, half4_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Split s of the (vectors, KV head) unit writes slot s of `partial`: [split][kv head][vector][head_dim + 2] = acc,
+// m, l.
+template <int D>  // staged query dims: desc head_dim <= D (64 or 128)
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void seam_kernel(cf_kv_paged_attention_desc d, uint32_t splits,
+                                                        float *__restrict__ partial) {
+  constexpr int KS = D / 16;  // 16-dim k-steps of QK^T, 16-dim tiles of the output
+  __shared__ __align__(16) uint8_t s_k[kChunk * kKStride];
+  __shared__ __align__(16) uint8_t s_vt[kMaxD * kVStride];
+  __shared__ __align__(16) _Float16 s_p[kWaves][2][16][kPStride];  // per wavefront: P hi and lo [vector][token]
+  __shared__ __align__(16) int32_t s_lut[2][1 << kLutMaxLen];      // Huffman LUTs, rANS tables, or tail queries
   __shared__ __align__(16) uint16_t s_w[kRansWords];
-  __shared__ float s_kt[kLanes], s_vt[kLanes];  // rANS pages: per-token K and V scales
+  __shared__ float s_ks[kMaxD];                  // K scale per channel of the staged page (rANS pages: 1)
+  __shared__ float s_kt[kChunk], s_vs[kChunk];   // per token: K scale (legacy pages: 1) and V scale
+  __shared__ int s_bad;
   static_assert(sizeof(s_lut) >= 2 * cfkv::kSlots * sizeof(uint2), "the rANS tables share the LUT area");
+  static_assert(sizeof(s_lut) >= kVecs * kMaxD * sizeof(float), "the tail's queries share the LUT area");
 
-  const int lane = threadIdx.x;
-  const uint32_t row = blockIdx.x, kvh = blockIdx.y;
-  const uint32_t D = d.head_dim;
-  const uint32_t gqa = d.gqa_group_size;
-  const uint32_t qtok = d.query_token_begin + row;
-  const uint32_t wbegin = (d.causal_window == 0 || qtok + 1 <= d.causal_window) ? 0u : qtok + 1 - d.causal_window;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t kvh = blockIdx.y, split = blockIdx.z;
+  const uint32_t gqa = d.gqa_group_size, HD = d.head_dim;
+  const uint32_t M = d.query_count * gqa;                    // query vectors of this KV head
+  const uint32_t wv0 = blockIdx.x * kVecs + wave * 16;       // this wavefront's first vector
+  const bool wave_active = wv0 < M;
+  const float scale = d.softmax_scale;
 
-  bool bad = false;  // a rANS page that is not a valid self-contained group for its descriptor (see the file header)
-  for (uint32_t h0 = 0; h0 < gqa; h0 += kHeadsPass) {
-    const int nh = static_cast<int>(min<uint32_t>(kHeadsPass, gqa - h0));
-    // queries of this pass (softmax scale applied to the dot product, as the reference does)
-    for (int i = lane; i < kHeadsPass * 64 * DPL; i += kLanes) {
-      const int h = i / (64 * DPL), dd = i % (64 * DPL);
-      float q = 0.0f;
-      if (h < nh && static_cast<uint32_t>(dd) < D)
-        q = d.queries[(static_cast<size_t>(row) * d.query_head_count + kvh * gqa + h0 + h) * D + dd];
-      s_q[h][dd] = q;
+  auto row_of = [&](uint32_t v) { return v / gqa; };
+  auto qtok_of = [&](uint32_t r) { return d.query_token_begin + r; };
+  auto wbegin_of = [&](uint32_t r) {
+    const uint32_t qt = qtok_of(r);
+    return (d.causal_window == 0 || qt + 1 <= d.causal_window) ? 0u : qt + 1 - d.causal_window;
+  };
+  // visible token range of the workgroup's rows (pages wholly outside it are skipped)
+  const uint32_t wg_v1 = min(M, (blockIdx.x + 1) * kVecs) - 1;
+  const uint32_t vis_lo = wbegin_of(row_of(blockIdx.x * kVecs)), vis_hi = qtok_of(row_of(wg_v1));
+
+  // A-operand vector of this lane (row lane % 16 of the wavefront's 16) and its raw query values: k-step kk holds
+  // dims 16 kk + 4 (lane / 16) .. + 3
+  const uint32_t av = wv0 + (lane & 15);
+  float qraw[KS][4];
+  {
+    const bool ok = av < M;
+    const uint32_t r = ok ? row_of(av) : 0, g = ok ? av % gqa : 0;
+    const float *qp = d.queries + (static_cast<size_t>(r) * d.query_head_count + kvh * gqa + g) * HD;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t dd = 16 * kk + 4 * (lane >> 4) + j;
+        qraw[kk][j] = (ok && dd < HD) ? qp[dd] : 0.0f;
+      }
+  }
+  // A operands of one page: the queries times its per-channel K scales (s_ks; 1 for rANS pages), f16 hi + lo
+  auto build_q = [&](half4_t (&qhi)[KS], half4_t (&qlo)[KS]) {
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float x = qraw[kk][j] * s_ks[16 * kk + 4 * (lane >> 4) + j];
+        const _Float16 h = static_cast<_Float16>(x);
+        qhi[kk][j] = h;
+        qlo[kk][j] = static_cast<_Float16>(x - static_cast<float>(h));
+      }
+  };
+
+  // C-layout vectors of this lane: wv0 + 4 (lane / 16) + i, i < 4; their rows' visible token ranges
+  uint32_t c_lo[4], c_hi[4];
+  bool c_ok[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t v = wv0 + 4 * (lane >> 4) + i;
+    c_ok[i] = v < M;
+    const uint32_t r = c_ok[i] ? row_of(v) : 0;
+    c_lo[i] = wbegin_of(r);
+    c_hi[i] = qtok_of(r);
+  }
+  float m_run[4], l_run[4];
+  float4_t acc[KS];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m_run[i] = -INFINITY;
+    l_run[i] = 0.0f;
+  }
+#pragma unroll
+  for (int t = 0; t < KS; ++t) acc[t] = float4_t{0, 0, 0, 0};
+  if (tid == 0) s_bad = 0;
+
+  // Online softmax over one chunk: s[i][j] = score of vector i (C layout) with token 16 j + lane % 16 (-inf when
+  // not visible); rescales acc, updates (m, l), returns p in s.
+  auto softmax_chunk = [&](float (&s)[4][4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float mx = fmaxf(fmaxf(s[i][0], s[i][1]), fmaxf(s[i][2], s[i][3]));
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+      const float mn = fmaxf(m_run[i], mx);
+      const float alpha = (m_run[i] == -INFINITY) ? 0.0f : __expf(m_run[i] - mn);
+      float ps = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        s[i][j] = (s[i][j] == -INFINITY) ? 0.0f : __expf(s[i][j] - mn);
+        ps += s[i][j];
+      }
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) ps += __shfl_xor(ps, o);
+      if (mn != -INFINITY) {
+        l_run[i] = l_run[i] * alpha + ps;
+#pragma unroll
+        for (int t = 0; t < KS; ++t) acc[t][i] *= alpha;
+        m_run[i] = mn;
+      }
     }
-    float m[kHeadsPass], l[kHeadsPass], acc[kHeadsPass][DPL];
-#pragma unroll
-    for (int h = 0; h < kHeadsPass; ++h) {
-      m[h] = -INFINITY;
-      l[h] = 0.0f;
-#pragma unroll
-      for (int j = 0; j < DPL; ++j) acc[h][j] = 0.0f;
-    }
+  };
 
-    // fold a chunk of up to 64 tokens: lane = token scores, then lane = dims V accumulation
-    auto fold = [&](int ntok, bool dense, const float *kd, const float *vd, const float *vsc, int zp,
-                    uint32_t tok0, uint32_t hd, uint32_t stride, const float *kt = nullptr) {
-      float sc[kHeadsPass];
-      const uint32_t token = tok0 + lane;
-      const bool vis = lane < ntok && token >= wbegin && token <= qtok;
-#pragma unroll
-      for (int h = 0; h < kHeadsPass; ++h) sc[h] = 0.0f;
-      if (lane < ntok) {
-        for (uint32_t dd = 0; dd < D; ++dd) {
-          float kv;
-          if (dense) kv = kd[(static_cast<size_t>(lane) * d.kv_head_count + kvh) * D + dd];
-          else if (dd < hd) kv = static_cast<float>(static_cast<int>(s_k[lane * stride + dd]) - zp) * s_ks[dd];
-          else kv = 0.0f;
-#pragma unroll
-          for (int h = 0; h < kHeadsPass; ++h) sc[h] += s_q[h][dd] * kv;
-        }
-      }
-      if (kt && lane < ntok) {
-#pragma unroll
-        for (int h = 0; h < kHeadsPass; ++h) sc[h] *= kt[lane];
-      }
-#pragma unroll
-      for (int h = 0; h < kHeadsPass; ++h) {
-        float s = vis ? sc[h] * d.softmax_scale : -INFINITY;
-        float mx = s;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-        const float mn = fmaxf(m[h], mx);
-        const float alpha = (m[h] == -INFINITY) ? 0.0f : expf(m[h] - mn);
-        const float p = vis ? expf(s - mn) : 0.0f;
-        float ps = p;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) ps += __shfl_xor(ps, o);
-        if (mn != -INFINITY) {
-          l[h] = l[h] * alpha + ps;
-#pragma unroll
-          for (int j = 0; j < DPL; ++j) acc[h][j] *= alpha;
-          m[h] = mn;
-        }
-        s_p[h][lane] = p * (dense ? 1.0f : vsc[lane < ntok ? lane : 0]);
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      for (int t = 0; t < ntok; ++t) {
-#pragma unroll
-        for (int j = 0; j < DPL; ++j) {
-          const uint32_t dd = lane + 64 * j;
-          if (dd >= D) continue;
-          float vv;
-          if (dense) vv = vd[(static_cast<size_t>(t) * d.kv_head_count + kvh) * D + dd];
-          else if (dd < hd) vv = static_cast<float>(static_cast<int>(s_v[t * stride + dd]) - zp);
-          else vv = 0.0f;
-#pragma unroll
-          for (int h = 0; h < kHeadsPass; ++h) acc[h][j] += s_p[h][t] * vv;
-        }
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    };
-
-    for (uint32_t p = 0; p < d.page_count; ++p) {
-      if (d.pages[p].kv_head != kvh) continue;  // wave-uniform
+  // ---- pages of this KV head, round-robin over the splits by their order in the descriptor array
+  uint32_t ord = 0;
+  for (uint32_t pb = 0; pb < d.page_count; pb += 64) {
+    const uint32_t pi = pb + lane;
+    uint64_t mine = __builtin_amdgcn_ballot_w64(pi < d.page_count && d.pages[pi].kv_head == kvh);
+    while (mine) {
+      const uint32_t p = pb + static_cast<uint32_t>(__builtin_ctzll(mine));
+      mine &= mine - 1;
+      if (ord++ % splits != split) continue;
       const cf_kv_device_page pg = d.pages[p];
       if (pg.token_count == 0) continue;
-      // skip pages entirely outside the visible window
-      if (pg.token_begin > qtok || pg.token_begin + pg.token_count <= wbegin) continue;
-      if (pg.fixed_code_length == 0 && pg.k_max_code_length == 0) {  // rANS page (kv_codec_ext.h group blob)
-        if (pg.token_count > static_cast<uint32_t>(kLanes) || pg.head_dim > D) {
-          bad = true;
-          continue;
-        }
-        for (uint32_t dd = lane; dd < D; dd += kLanes) s_ks[dd] = 1.0f;
-        uint2(*tab)[cfkv::kSlots] = reinterpret_cast<uint2(*)[cfkv::kSlots]>(&s_lut[0][0]);
-        const uint32_t stride = pg.head_dim + kRowPad;
-        if (!rans_group_to_lds(reinterpret_cast<const uint8_t *>(pg.k_words),
-                               reinterpret_cast<const uint2 *>(pg.k_lut), reinterpret_cast<const uint2 *>(pg.v_lut),
-                               tab, s_w, pg.head_dim, pg.token_count, s_k, s_v, stride, s_kt, s_vt, lane)) {
-          bad = true;
-          continue;
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        fold(static_cast<int>(pg.token_count), false, nullptr, nullptr, s_vt, 128, pg.token_begin, pg.head_dim,
-             stride, s_kt);
+      if (pg.token_begin > vis_hi || pg.token_begin + pg.token_count <= vis_lo) continue;
+      const bool rans = pg.fixed_code_length == 0 && pg.k_max_code_length == 0;
+      if (rans && (pg.token_count > static_cast<uint32_t>(kChunk) || pg.head_dim == 0 || pg.head_dim > kMaxD)) {
+        if (tid == 0) s_bad = 1;
         continue;
       }
-      for (uint32_t dd = lane; dd < min(D, pg.head_dim); dd += kLanes) s_ks[dd] = pg.k_scales[dd];
-      if (pg.head_dim == 0 || pg.head_dim > CF_KV_MAX_HEAD_DIM) continue;
-      // Huffman pages: stage both LUTs in LDS when they fit (the lookups are the decoder's hot loop)
+      if (!rans && (pg.head_dim == 0 || pg.head_dim > kMaxD)) continue;
+      const uint32_t phd = pg.head_dim;
+      const uint32_t zp = rans ? 128u : pg.zero_point;
+      const _Float16 zbase = static_cast<_Float16>(1024.0f + static_cast<float>(zp));
+      // Huffman pages: both LUTs in LDS when they fit (the lookups are the decoder's hot loop)
       const int32_t *klut = pg.k_lut, *vlut = pg.v_lut;
-      if (!pg.fixed_code_length && pg.k_max_code_length <= kLutMaxLen && pg.v_max_code_length <= kLutMaxLen) {
-        for (uint32_t i = lane; i < (1u << pg.k_max_code_length); i += kLanes) s_lut[0][i] = pg.k_lut[i];
-        for (uint32_t i = lane; i < (1u << pg.v_max_code_length); i += kLanes) s_lut[1][i] = pg.v_lut[i];
+      if (!rans && !pg.fixed_code_length && pg.k_max_code_length <= kLutMaxLen && pg.v_max_code_length <= kLutMaxLen) {
+        __syncthreads();  // the previous chunk's readers of s_lut are done
+        for (uint32_t i = tid; i < (1u << pg.k_max_code_length); i += kThreads) s_lut[0][i] = pg.k_lut[i];
+        for (uint32_t i = tid; i < (1u << pg.v_max_code_length); i += kThreads) s_lut[1][i] = pg.v_lut[i];
         klut = s_lut[0];
         vlut = s_lut[1];
       }
-      const uint32_t chunk = max(1u, min<uint32_t>(kLanes, kChunkSyms / pg.head_dim));
-      for (uint32_t t0 = 0; t0 < pg.token_count; t0 += chunk) {
-        const uint32_t nt = min(chunk, pg.token_count - t0);
-        // chunk symbols [t0*hd, (t0+nt)*hd) of each stream; lane-token t reads row t at t*hd (page row stride)
-        const int64_t s0 = static_cast<int64_t>(t0) * pg.head_dim, s1 = s0 + static_cast<int64_t>(nt) * pg.head_dim;
-        const uint32_t stride = pg.head_dim + kRowPad;
-        decode_span(pg.k_words, pg.k_block_offsets, klut, pg.k_max_code_length, pg.fixed_code_length,
-                    pg.block_size, s0, s1, pg.head_dim, stride, s_k, lane);
-        decode_span(pg.v_words, pg.v_block_offsets, vlut, pg.v_max_code_length, pg.fixed_code_length,
-                    pg.block_size, s0, s1, pg.head_dim, stride, s_v, lane);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        fold(static_cast<int>(nt), false, nullptr, nullptr, pg.v_scales + t0, static_cast<int>(pg.zero_point),
-             pg.token_begin + t0, pg.head_dim, stride);
-      }
-    }
-    // dense fp32 active tail [active_token_count, kv_head_count, head_dim]
-    for (uint32_t t0 = 0; t0 < d.active_token_count; t0 += kLanes) {
-      const uint32_t nt = min<uint32_t>(kLanes, d.active_token_count - t0);
-      fold(static_cast<int>(nt), true, d.active_k + static_cast<size_t>(t0) * d.kv_head_count * D,
-           d.active_v + static_cast<size_t>(t0) * d.kv_head_count * D, nullptr, 0, d.active_token_begin + t0, D, D);
-    }
-    // finalize: w / sum, zeros when nothing was visible
-    for (int h = 0; h < nh; ++h) {
-      const float inv = (l[h] > 0.0f) ? 1.0f / l[h] : 0.0f;
-      float *out = d.output + (static_cast<size_t>(row) * d.query_head_count + kvh * gqa + h0 + h) * D;
+      for (uint32_t t0 = 0; t0 < pg.token_count; t0 += kChunk) {
+        const uint32_t nt = min<uint32_t>(kChunk, pg.token_count - t0);
+        const uint32_t tok0 = pg.token_begin + t0;
+        __syncthreads();  // the previous chunk's compute no longer reads the staged tiles
+        for (uint32_t dd = tid; dd < kMaxD; dd += kThreads) s_ks[dd] = rans ? 1.0f : (dd < phd ? pg.k_scales[dd] : 0.0f);
+        if (rans) {
+          if (wave == 0) {
+            uint2(*tab)[cfkv::kSlots] = reinterpret_cast<uint2(*)[cfkv::kSlots]>(&s_lut[0][0]);
+            const bool ok = rans_group_to_lds(reinterpret_cast<const uint8_t *>(pg.k_words),
+                                              reinterpret_cast<const uint2 *>(pg.k_lut),
+                                              reinterpret_cast<const uint2 *>(pg.v_lut), tab, s_w, phd, nt, s_k, s_vt,
+                                              s_kt, s_vs, lane);
+            if (!ok && lane == 0) s_bad = 1;
+          }
+        } else {
+          for (int t = tid; t < kChunk; t += kThreads) {
+            s_kt[t] = 1.0f;
+            s_vs[t] = t < static_cast<int>(nt) ? pg.v_scales[t0 + t] : 0.0f;
+          }
+          const int64_t s0 = static_cast<int64_t>(t0) * phd, s1 = s0 + static_cast<int64_t>(nt) * phd;
+          decode_span(pg.k_words, pg.k_block_offsets, klut, pg.k_max_code_length, pg.fixed_code_length,
+                      pg.block_size, s0, s1, phd, tid,
+                      [&](uint32_t r, uint32_t c, uint32_t sym) { s_k[r * kKStride + c] = static_cast<uint8_t>(sym); });
+          decode_span(pg.v_words, pg.v_block_offsets, vlut, pg.v_max_code_length, pg.fixed_code_length,
+                      pg.block_size, s0, s1, phd, tid,
+                      [&](uint32_t r, uint32_t c, uint32_t sym) { s_vt[c * kVStride + r] = static_cast<uint8_t>(sym); });
+        }
+        // dims the page does not have read as V = 0 (the query side zeroes K through s_ks)
+        for (uint32_t i = tid; i < (HD > phd ? HD - phd : 0u) * kChunk; i += kThreads)
+          s_vt[(phd + i / kChunk) * kVStride + i % kChunk] = static_cast<uint8_t>(zp);
+        __syncthreads();
+        if (s_bad) continue;
+        if (!wave_active) continue;
+        half4_t qhi[KS], qlo[KS];
+        build_q(qhi, qlo);
+        const int ntile = static_cast<int>((nt + 15) / 16);
+        // scores
+        float s[4][4];
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) {
-        const uint32_t dd = lane + 64 * j;
-        if (dd < D) out[dd] = bad ? __builtin_nanf("") : acc[h][j] * inv;
+        for (int j = 0; j < 4; ++j) {
+          float4_t c = {0, 0, 0, 0};
+          if (j < ntile) {
+            const uint8_t *krow = s_k + (16 * j + (lane & 15)) * kKStride + 4 * (lane >> 4);
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk) {
+              const half4_t b = sym4_to_half4(*reinterpret_cast<const uint32_t *>(krow + 16 * kk), zbase);
+              c = mfma16(qhi[kk], b, c);
+              c = mfma16(qlo[kk], b, c);
+            }
+          }
+          const uint32_t tt = 16 * j + (lane & 15), tok = tok0 + tt;
+          const float kts = s_kt[tt];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool vis = j < ntile && tt < nt && c_ok[i] && tok >= c_lo[i] && tok <= c_hi[i];
+            s[i][j] = vis ? c[i] * kts * scale : -INFINITY;
+          }
+        }
+        softmax_chunk(s);
+        // P (times the token's V scale) -> this wavefront's LDS tile as f16 hi + lo [vector][token]
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t tt = 16 * j + (lane & 15);
+          const float vsc = s_vs[tt];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float x = s[i][j] * vsc;
+            const _Float16 h = static_cast<_Float16>(x);
+            s_p[wave][0][4 * (lane >> 4) + i][tt] = h;
+            s_p[wave][1][4 * (lane >> 4) + i][tt] = static_cast<_Float16>(x - static_cast<float>(h));
+          }
+        }
+        wave_sync();
+        // P.V: acc[t] (vector rows, dims 16 t + lane % 16) += P[16 x tokens] V[tokens x 16]
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          if (ks >= ntile) break;
+          const half4_t ph = *reinterpret_cast<const half4_t *>(&s_p[wave][0][lane & 15][16 * ks + 4 * (lane >> 4)]);
+          const half4_t pl = *reinterpret_cast<const half4_t *>(&s_p[wave][1][lane & 15][16 * ks + 4 * (lane >> 4)]);
+#pragma unroll
+          for (int t = 0; t < KS; ++t) {
+            const uint32_t w = *reinterpret_cast<const uint32_t *>(s_vt + (16 * t + (lane & 15)) * kVStride + 16 * ks +
+                                                                   4 * (lane >> 4));
+            const half4_t b = sym4_to_half4(w, zbase);
+            acc[t] = mfma16(ph, b, acc[t]);
+            acc[t] = mfma16(pl, b, acc[t]);
+          }
+        }
+        wave_sync();
       }
     }
   }
+
+  // ---- dense fp32 tail [active_token_count, kv_head_count, head_dim], 64-token chunks continuing the round-robin
+  if (d.active_token_count) {
+    __syncthreads();
+    float *s_qf = reinterpret_cast<float *>(&s_lut[0][0]) + wave * 16 * kMaxD;  // this wavefront's 16 queries
+    for (uint32_t i = lane; i < 16u * HD; i += 64) {
+      const uint32_t v = wv0 + i / HD, dd = i % HD;
+      float q = 0.0f;
+      if (v < M) q = d.queries[(static_cast<size_t>(row_of(v)) * d.query_head_count + kvh * gqa + v % gqa) * HD + dd];
+      s_qf[(i / HD) * kMaxD + dd] = q;
+    }
+    wave_sync();
+    float *s_pf = reinterpret_cast<float *>(&s_p[wave][0][0][0]);  // p [vector][token] in fp32 (same bytes)
+    static_assert(sizeof(s_p[0]) >= 16 * kChunk * sizeof(float), "fp32 tail weights share the P tile");
+    for (uint32_t t0 = 0; t0 < d.active_token_count; t0 += kChunk) {
+      if (ord++ % splits != split) continue;
+      if (!wave_active) continue;
+      const uint32_t nt = min<uint32_t>(kChunk, d.active_token_count - t0);
+      const uint32_t tok0 = d.active_token_begin + t0;
+      float s[4][4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t tt = 16 * j + (lane & 15), tok = tok0 + tt;
+        float dot[4] = {0, 0, 0, 0};
+        if (tt < nt) {
+          const float *kr = d.active_k + (static_cast<size_t>(t0 + tt) * d.kv_head_count + kvh) * HD;
+          for (uint32_t dd = 0; dd < HD; ++dd) {
+            const float kv = kr[dd];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dot[i] += s_qf[(4 * (lane >> 4) + i) * kMaxD + dd] * kv;
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bool vis = tt < nt && c_ok[i] && tok >= c_lo[i] && tok <= c_hi[i];
+          s[i][j] = vis ? dot[i] * scale : -INFINITY;
+        }
+      }
+      softmax_chunk(s);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s_pf[(4 * (lane >> 4) + i) * kChunk + 16 * j + (lane & 15)] = s[i][j];
+      wave_sync();
+      for (uint32_t tt = 0; tt < nt; ++tt) {
+        const float *vr = d.active_v + (static_cast<size_t>(t0 + tt) * d.kv_head_count + kvh) * HD;
+#pragma unroll
+        for (int t = 0; t < KS; ++t) {
+          const uint32_t dd = 16 * t + (lane & 15);
+          const float vv = dd < HD ? vr[dd] : 0.0f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[t][i] += s_pf[(4 * (lane >> 4) + i) * kChunk + tt] * vv;
+        }
+      }
+      wave_sync();
+    }
+  }
+
+  // ---- output (one split) or this split's partial
+  __syncthreads();
+  const bool bad = s_bad != 0;
+  if (!wave_active) return;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t v = wv0 + 4 * (lane >> 4) + i;
+    if (v >= M) continue;
+    if (splits == 1) {
+      const float inv = l_run[i] > 0.0f ? 1.0f / l_run[i] : 0.0f;
+      float *out = d.output + (static_cast<size_t>(row_of(v)) * d.query_head_count + kvh * gqa + v % gqa) * HD;
+#pragma unroll
+      for (int t = 0; t < KS; ++t) {
+        const uint32_t dd = 16 * t + (lane & 15);
+        if (dd < HD) out[dd] = bad ? __builtin_nanf("") : acc[t][i] * inv;
+      }
+    } else {
+      float *pp = partial + ((static_cast<size_t>(split) * d.kv_head_count + kvh) * M + v) * (HD + 2);
+#pragma unroll
+      for (int t = 0; t < KS; ++t) {
+        const uint32_t dd = 16 * t + (lane & 15);
+        if (dd < HD) pp[dd] = acc[t][i];
+      }
+      if ((lane & 15) == 0) {
+        pp[HD] = bad ? __builtin_nanf("") : m_run[i];
+        pp[HD + 1] = l_run[i];
+      }
+    }
+  }
+}
+
+// Merge the split partials of one (vector, KV head) per workgroup: out = sum_s acc_s e^(m_s - m) / sum_s l_s
+// e^(m_s - m); zeros when nothing was visible; NaN when a split saw a refused page.
+__global__ __launch_bounds__(kMaxD) void seam_merge_kernel(cf_kv_paged_attention_desc d, uint32_t splits,
+                                                           const float *__restrict__ partial) {
+  const uint32_t v = blockIdx.x, kvh = blockIdx.y, dd = threadIdx.x;
+  const uint32_t gqa = d.gqa_group_size, HD = d.head_dim, M = d.query_count * gqa;
+  if (dd >= HD) return;
+  float m = -INFINITY;
+  bool nan = false;
+  for (uint32_t s = 0; s < splits; ++s) {
+    const float ms = partial[((static_cast<size_t>(s) * d.kv_head_count + kvh) * M + v) * (HD + 2) + HD];
+    nan |= ms != ms;
+    m = fmaxf(m, ms);
+  }
+  float l = 0.0f, o = 0.0f;
+  if (m != -INFINITY)
+    for (uint32_t s = 0; s < splits; ++s) {
+      const float *pp = partial + ((static_cast<size_t>(s) * d.kv_head_count + kvh) * M + v) * (HD + 2);
+      if (pp[HD] == -INFINITY) continue;
+      const float sc = __expf(pp[HD] - m);
+      l += pp[HD + 1] * sc;
+      o += pp[dd] * sc;
+    }
+  d.output[(static_cast<size_t>(v / gqa) * d.query_head_count + kvh * gqa + v % gqa) * HD + dd] =
+      nan ? __builtin_nanf("") : (l > 0.0f ? o / l : 0.0f);
+}
+
+}  // namespace
+
+// Split partials of the seam: a file-scope device array of CF_KV_SEAM_SCRATCH_BYTES per GPU (the seam's signature
+// has no workspace and it allocates nothing). Its device address is looked up once per device with
+// hipGetSymbolAddress. Calls that overlap on one GPU share it (see kv_cuda.h).
+#define CF_KV_SEAM_SCRATCH_BYTES (16u << 20)
+static __device__ __align__(256) uint8_t seam_scratch[CF_KV_SEAM_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_seam_mu;
+void *g_seam_addr[kMaxDevices] = {};
+
+void *seam_scratch_address() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_seam_mu);
+  if (!g_seam_addr[dev]) {
+    void *addr = nullptr;
+    if (hipGetSymbolAddress(&addr, HIP_SYMBOL(seam_scratch)) != hipSuccess) return nullptr;
+    g_seam_addr[dev] = addr;
+  }
+  return g_seam_addr[dev];
+}
+
+uint32_t seam_cus() {
+  static thread_local int cached_dev = -1;
+  static thread_local uint32_t cached = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev != cached_dev) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached = static_cast<uint32_t>(cus);
+    cached_dev = dev;
+  }
+  return cached;
 }
 
 }  // namespace
@@ -393,13 +646,35 @@ extern "C" cf_status cf_kv_validate_paged_attention_desc(const cf_kv_paged_atten
 }
 
 // reference src/cuda/paged_kv_attention.cu:301-327
+// Context splits: about two workgroups per CU over the (64-vector tile, KV head) units, at least two page chunks
+// per split, and no more partials than the scratch array holds (one split writes the output directly).
 extern "C" cf_status cf_kv_paged_attention_async(const cf_kv_paged_attention_desc *desc, void *stream) {
   const cf_status valid = cf_kv_validate_paged_attention_desc(desc);
   if (valid != CF_OK) return valid;
   if (desc->kv_head_count > 65535) return CF_ERR_UNSUPPORTED;
+  const uint64_t M = static_cast<uint64_t>(desc->query_count) * desc->gqa_group_size;
+  const uint64_t tiles = (M + kVecs - 1) / kVecs;
+  if (tiles > 0x7FFFFFFFu || M > 0x7FFFFFFFu) return CF_ERR_UNSUPPORTED;
+  const uint64_t units = tiles * desc->kv_head_count;
+  const uint64_t chunks_per_head = (desc->page_count + desc->kv_head_count - 1) / desc->kv_head_count +
+                                   (desc->active_token_count + kChunk - 1) / kChunk;
+  uint64_t splits = units >= 2ull * seam_cus() ? 1 : (2ull * seam_cus()) / units;
+  splits = std::min<uint64_t>(splits, std::max<uint64_t>(1, chunks_per_head / 2));
+  splits = std::min<uint64_t>(splits, 64);
+  const uint64_t part_bytes = M * desc->kv_head_count * (desc->head_dim + 2) * sizeof(float);
+  if (splits > 1 && part_bytes * splits > CF_KV_SEAM_SCRATCH_BYTES)
+    splits = std::max<uint64_t>(1, CF_KV_SEAM_SCRATCH_BYTES / part_bytes);
+  float *partial = nullptr;
+  if (splits > 1) {
+    partial = static_cast<float *>(seam_scratch_address());
+    if (!partial) return CF_ERR_CUDA;
+  }
   const hipStream_t s = cfd::as_stream(stream);
-  const dim3 grid(desc->query_count, desc->kv_head_count);
-  if (desc->head_dim <= 64) legacy_kernel<1><<<grid, kLanes, 0, s>>>(*desc);
-  else legacy_kernel<2><<<grid, kLanes, 0, s>>>(*desc);
+  const dim3 grid(static_cast<uint32_t>(tiles), desc->kv_head_count, static_cast<uint32_t>(splits));
+  if (desc->head_dim <= 64) seam_kernel<64><<<grid, kThreads, 0, s>>>(*desc, static_cast<uint32_t>(splits), partial);
+  else seam_kernel<128><<<grid, kThreads, 0, s>>>(*desc, static_cast<uint32_t>(splits), partial);
+  if (splits > 1)
+    seam_merge_kernel<<<dim3(static_cast<uint32_t>(M), desc->kv_head_count), kMaxD, 0, s>>>(
+        *desc, static_cast<uint32_t>(splits), partial);
   return cfd::launch_status();
 }

@@ -178,3 +178,36 @@ def test_rans_pages_refused_as_nan(dev):
         got, ref = _run(dev, [(1, 0, kd, vd)], [bad, good], q, kvh, gqa, 63, 0.125)
         assert np.isnan(got[:, :gqa]).all()                       # KV head 0: the refused page
         assert np.abs(got[:, gqa:] - ref[:, gqa:]).max() <= ABS_TOL  # KV head 1: decoded normally
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_many_rows_long_context_splits(dev, hd):
+    """The launch shapes small tests never reach: 64 query rows x GQA 7 (448 query vectors = 7 tiles per KV head),
+    2 KV heads, 4096 context tokens in 128 pages per head (fixed-width int4, rANS and Huffman pages interleaved across
+    heads in the descriptor array), a 20-token dense tail: the context is split over many workgroups whose partials
+    are merged by a second kernel. Causal rows (each row sees its own prefix), then a 300-token window."""
+    from legacy_helpers import rans_page
+    rng = np.random.default_rng(4000 + hd)
+    kvh, gqa, T, P = 2, 7, 4096, 32
+    pages, deq = [], []
+    for p0 in range(0, T, P):
+        for h in range(kvh):
+            k = rng.standard_normal((P, hd)).astype(np.float32)
+            v = rng.standard_normal((P, hd)).astype(np.float32)
+            kind = (p0 // P + h) % 5
+            if kind == 3:
+                page, kd, vd = rans_page(k, v, h, p0)
+            elif kind == 4:
+                page, kd, vd = huffman_page(k, v, h, p0)
+            else:
+                page, kd, vd = fixed_page(k, v, h, p0, 4)
+            pages.append(page)
+            deq.append((h, p0, kd, vd))
+    tail_k = rng.standard_normal((20, kvh, hd)).astype(np.float32)
+    tail_v = rng.standard_normal((20, kvh, hd)).astype(np.float32)
+    q = rng.standard_normal((64, kvh * gqa, hd)).astype(np.float32)
+    got, ref = _run(dev, deq, pages, q, kvh, gqa, T + 20 - 64, 1 / np.sqrt(hd), tail=(T, tail_k, tail_v))
+    assert np.isfinite(got).all()
+    assert np.abs(got - ref).max() <= ABS_TOL
+    got, ref = _run(dev, deq, pages, q, kvh, gqa, T - 100, 1 / np.sqrt(hd), window=300, tail=(T, tail_k, tail_v))
+    assert np.abs(got - ref).max() <= ABS_TOL
