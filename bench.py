@@ -583,6 +583,59 @@ def bench_nibble(steps: int, warmup: int, cpu: bool = True, seqs: int = 32, toke
 
 
 # ------------------------------------------------------------------------------------------------ long context (C5)
+def bench_seam(steps: int, warmup: int, shapes=((64, 4096), (64, 65536), (128, 4096), (128, 65536))) -> dict:
+    """The reference seam (cf_kv_paged_attention_async) through the llama adapter (cf_llama_kv_*), at the shape of
+    the reference's own seam benchmark (reference product/native-kv-performance.json: Qwen2.5-0.5B-derived
+    attention, 2 KV / 14 query heads, 64 query tokens per call, contexts 4096-65536, head_dim 64 and 128): int4
+    fixed-width pages of 32 tokens, 65536 tokens = 4096 pages = the seam's per-launch page limit. One call = the 64
+    query tokens at the end of the context, causal. Gate: the last query row against the float64 oracle over the
+    fixture-quantised pages. The reference published 2528 us for its final kernel on an RTX 2080 Ti
+    (native-kv-performance.json:10)."""
+    import torch
+    import oracle as O
+    from chromofold_amd import llama
+
+    out = {"workload": "llama adapter seam: 2 KV / 14 q heads, 64 queries, int4 pages of 32 tokens",
+           "reference_us": 2528, "reference_hw": "RTX 2080 Ti (native-kv-performance.json:10)"}
+    kvh, qh, gqa, qn, ps = 2, 14, 7, 64, 32
+    for hd, n in shapes:
+        ad = llama.KvAdapter(llama.options(1, kvh, qh, hd, ps, gqa, 4))
+        rng = np.random.default_rng(0x5EA + n + hd)
+        keys, vals = [], []
+        for h in range(kvh):
+            k = rng.standard_normal((n, hd)).astype(np.float32)
+            v = rng.standard_normal((n, hd)).astype(np.float32)
+            ad.append(0, h, 0, k, v)
+            keys.append(k)
+            vals.append(v)
+        q = torch.from_numpy(rng.standard_normal((qn, qh, hd)).astype(np.float32)).to("cuda:0")
+        o = torch.empty_like(q)
+        s = torch.cuda.current_stream().cuda_stream
+        sc = 1.0 / np.sqrt(hd)
+        run = lambda: ad.attention(0, q.data_ptr(), o.data_ptr(), qn, qh, gqa, n - qn, sc, 0, s)  # noqa: E731
+        run()
+        torch.cuda.synchronize()
+        pages = []
+        for h in range(kvh):
+            for p0 in range(0, n, ps):
+                *_, kd, vd = O.kv_fixture_quantize(keys[h][p0:p0 + ps], vals[h][p0:p0 + ps], 4)
+                pages.append((h, p0, kd, vd))
+        ref, _ = O.paged_attention_f64(q[qn - 1].cpu().numpy(), qh, kvh, hd, gqa, n - 1, 0, sc, pages)
+        got = o[qn - 1].cpu().numpy()
+        err = float(np.abs(got - ref).max())
+        assert err <= 2e-4, err
+        _, per = _events_time(run, steps, warmup)
+        t = float(np.median(per)) * 1e-3
+        st = ad.stats()
+        nbytes = st.compressed_bytes + st.descriptor_bytes + 2 * q.numel() * 4
+        out[f"hd{hd}_n{n}"] = {"us": t * 1e6, "compressed_bytes": int(st.compressed_bytes),
+                               "gbs": nbytes / t / 1e9, "roofline_frac": nbytes / t / 1e9 / HBM_PEAK_GBS,
+                               "x_vs_reference": 2528e-6 / t, "max_abs_err_last_row": err}
+        ad.close()
+        del pages
+    return out
+
+
 def bench_c5(steps: int, warmup: int) -> dict:
     """C4 shapes (8 KV / 32 q heads, hd 128, rANS-hybrid pages). (a) 256 sequences sharing one 8192-token prefix
     (stored once, referenced by every sequence's page table) plus 512 unique tokens each; (b) 4 sequences x 131072
@@ -695,7 +748,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="auto", choices=["auto", "kv", "kv32", "rrr", "copy", "c5", "seal",
-                                                                  "nibble", "gather"])
+                                                                  "nibble", "gather", "seam"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--warm-s", type=float, default=3.0,
                     help="seconds of untimed back-to-back launches before the timed KV steps (0 for counter runs)")
@@ -719,6 +772,9 @@ def main() -> int:
         return 0
     if args.workload == "c5":
         print(json.dumps({"c5": bench_c5(args.steps, args.warmup)}))
+        return 0
+    if args.workload == "seam":
+        print(json.dumps({"seam": bench_seam(args.steps, args.warmup)}))
         return 0
     if args.workload == "gather":
         print(json.dumps({"gather": bench_gather(args.steps, args.warmup)}))
@@ -749,6 +805,7 @@ def main() -> int:
             secondary["device_seal"] = bench_seal(min(args.steps, 20), 2, cpu=not args.no_cpu)
             secondary["nibble_pages"] = bench_nibble(min(args.steps, 20), 2, cpu=not args.no_cpu)
             secondary["gathers"] = bench_gather(min(args.steps, 20), 2)
+            secondary["seam"] = bench_seam(min(args.steps, 20), 2)
             cp = bench_copy(10, 2)
             secondary["stream_copy_gbs"] = cp["stream_copy_gbs"]
             secondary["roofline_frac_of_stream_copy"] = kvr["roofline"]["achieved"] / cp["stream_copy_gbs"]
