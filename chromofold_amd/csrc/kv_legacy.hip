@@ -556,30 +556,49 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 }
 
 // Merge the split partials of one (vector, KV head) per workgroup: out = sum_s acc_s e^(m_s - m) / sum_s l_s
-// e^(m_s - m); zeros when nothing was visible; NaN when a split saw a refused page.
+// e^(m_s - m); zeros when nothing was visible; NaN when a split saw a refused page. The splits' (m, l) pairs are read
+// once into LDS; each thread then streams its dim of every split with 8 loads in flight.
 __global__ __launch_bounds__(kMaxD) void seam_merge_kernel(cf_kv_paged_attention_desc d, uint32_t splits,
                                                            const float *__restrict__ partial) {
+  __shared__ float s_sc[64];  // e^(m_s - m) per split (0 for splits that saw nothing)
+  __shared__ float s_l, s_m;
+  __shared__ int s_nan;
   const uint32_t v = blockIdx.x, kvh = blockIdx.y, dd = threadIdx.x;
   const uint32_t gqa = d.gqa_group_size, HD = d.head_dim, M = d.query_count * gqa;
-  if (dd >= HD) return;
-  float m = -INFINITY;
-  bool nan = false;
-  for (uint32_t s = 0; s < splits; ++s) {
-    const float ms = partial[((static_cast<size_t>(s) * d.kv_head_count + kvh) * M + v) * (HD + 2) + HD];
-    nan |= ms != ms;
-    m = fmaxf(m, ms);
-  }
-  float l = 0.0f, o = 0.0f;
-  if (m != -INFINITY)
-    for (uint32_t s = 0; s < splits; ++s) {
-      const float *pp = partial + ((static_cast<size_t>(s) * d.kv_head_count + kvh) * M + v) * (HD + 2);
-      if (pp[HD] == -INFINITY) continue;
-      const float sc = __expf(pp[HD] - m);
-      l += pp[HD + 1] * sc;
-      o += pp[dd] * sc;
+  const size_t stride = static_cast<size_t>(d.kv_head_count) * M * (HD + 2);
+  const float *base = partial + (static_cast<size_t>(kvh) * M + v) * (HD + 2);
+  if (dd < 64) {  // one wavefront: the splits' maxima, their merge, the scales and l
+    const float ms = dd < splits ? base[dd * stride + HD] : -INFINITY;
+    const float ls = dd < splits ? base[dd * stride + HD + 1] : 0.0f;
+    const bool nan = __builtin_amdgcn_ballot_w64(ms != ms) != 0;
+    float m = (ms != ms) ? -INFINITY : ms;
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const float sc = (m == -INFINITY || ms == -INFINITY || ms != ms) ? 0.0f : __expf(ms - m);
+    s_sc[dd] = sc;
+    float l = ls * sc;
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
+    if (dd == 0) {
+      s_l = l;
+      s_m = m;
+      s_nan = nan;
     }
+  }
+  __syncthreads();
+  if (dd >= HD) return;
+  float o = 0.0f;
+  uint32_t s = 0;
+  for (; s + 8 <= splits; s += 8) {
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = base[(s + j) * stride + dd];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o += x[j] * s_sc[s + j];
+  }
+  for (; s < splits; ++s) o += base[s * stride + dd] * s_sc[s];
+  const float l = s_l;
   d.output[(static_cast<size_t>(v / gqa) * d.query_head_count + kvh * gqa + v % gqa) * HD + dd] =
-      nan ? __builtin_nanf("") : (l > 0.0f ? o / l : 0.0f);
+      s_nan ? __builtin_nanf("") : (l > 0.0f ? o / l : 0.0f);
+  (void)s_m;
 }
 
 }  // namespace
@@ -646,8 +665,9 @@ extern "C" cf_status cf_kv_validate_paged_attention_desc(const cf_kv_paged_atten
 }
 
 // reference src/cuda/paged_kv_attention.cu:301-327
-// Context splits: about two workgroups per CU over the (64-vector tile, KV head) units, at least two page chunks
-// per split, and no more partials than the scratch array holds (one split writes the output directly).
+// Context splits: about two workgroups per CU over the (64-vector tile, KV head) units, at least four page chunks
+// per split, at most 64 splits, and no more partials than the scratch array holds (one split writes the output
+// directly).
 extern "C" cf_status cf_kv_paged_attention_async(const cf_kv_paged_attention_desc *desc, void *stream) {
   const cf_status valid = cf_kv_validate_paged_attention_desc(desc);
   if (valid != CF_OK) return valid;
@@ -659,7 +679,7 @@ extern "C" cf_status cf_kv_paged_attention_async(const cf_kv_paged_attention_des
   const uint64_t chunks_per_head = (desc->page_count + desc->kv_head_count - 1) / desc->kv_head_count +
                                    (desc->active_token_count + kChunk - 1) / kChunk;
   uint64_t splits = units >= 2ull * seam_cus() ? 1 : (2ull * seam_cus()) / units;
-  splits = std::min<uint64_t>(splits, std::max<uint64_t>(1, chunks_per_head / 2));
+  splits = std::min<uint64_t>(splits, std::max<uint64_t>(1, chunks_per_head / 4));
   splits = std::min<uint64_t>(splits, 64);
   const uint64_t part_bytes = M * desc->kv_head_count * (desc->head_dim + 2) * sizeof(float);
   if (splits > 1 && part_bytes * splits > CF_KV_SEAM_SCRATCH_BYTES)
