@@ -30,7 +30,10 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the dominant kernel, from rocprofv3 FETCH_SIZE + WRITE_SIZE runs calibrated on a copy of
 # known size (profiles/kv_batched_c4_32k.md): only quoted for the workload shape it was measured on.
-MEASURED_TRAFFIC = {("kv", 32768, 32): 2.0848e9}
+# For the FM search kernels the index is cache-resident, so FETCH_SIZE there is the L2-miss traffic that the
+# Infinity Cache (or HBM) serves (profiles/fm_c2.md).
+MEASURED_TRAFFIC = {("kv", 32768, 32): 2.0848e9, ("fm_count", 1 << 24, 1_000_000): 95.537e9,
+                    ("fm_locate", 1 << 24, 900_000): 49.336e9}
 METRIC = "compressed-KV attn decode tokens/s + HBM GB/s fraction; wavelet rank Mq/s"
 
 
@@ -158,6 +161,16 @@ def bench_fm(steps: int, warmup: int, cpu: bool = True) -> dict:
     res = {"count_mpats": pstart.size / t_c / 1e6, "count_ms": t_c * 1e3, "occurrences": occ,
            "locate_mocc": occ / t_l / 1e6, "locate_ms": t_l * 1e3, "gpu_sa_build_s": info["sa_s"],
            "gpu_index_build_s": info["build_s"], "index_bytes": fm.w.device_bytes()}
+    # cost model (algorithmic bytes): count = 1920 B per pattern symbol (2 rank1 per level x 15 levels x 32 B, twice:
+    # lo and hi) + C[] 8 B; locate = 22.4 KB per occurrence (15.5 expected LF steps x (access 480 + rank 960 + mark
+    # word 4) + sval 4 + msb 4)
+    bytes_count = float(plen.astype(np.int64).sum()) * (1920 + 8)
+    bytes_locate = occ * (15.5 * (480 + 960 + 4) + 8)
+    for key, b, t, tr in (("count_roofline", bytes_count, t_c, MEASURED_TRAFFIC.get(("fm_count", n, pstart.size))),
+                          ("locate_roofline", bytes_locate, t_l, MEASURED_TRAFFIC.get(("fm_locate", n, occ)))):
+        res[key] = {"bound": "hbm (nominal; the index is L2-resident)", "achieved": b / t / 1e9,
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": b / t / 1e9 / HBM_PEAK_GBS, "model_bytes": b,
+                    "traffic": tr, "traffic_gbs": tr / t / 1e9 if tr else None}
     if cpu:
         import oracle as O
         from chromofold_amd.search import to_u32
@@ -253,6 +266,34 @@ def bench_stream_read(buf, steps: int = 20, warmup: int = 3) -> dict:
     _, per = _events_time(read, steps, warmup)
     t = float(np.median(per)) * 1e-3
     return {"bytes": n, "ms": t * 1e3, "read_gbs": n / t / 1e9}
+
+
+def bench_cache_peaks(steps: int = 10, warmup: int = 2) -> dict:
+    """Read bandwidth of the on-chip levels, as references for the index kernels whose data is L2/LDS resident:
+    cf_cache_read_async over 16 MiB (2 MiB per XCD: each XCD's L2 after the first pass; 128 passes) and over 128 MiB
+    (beyond the L2s: the Infinity Cache; 16 passes), 2 GiB read per launch; cf_lds_read_async (64 KiB of LDS per
+    workgroup, 2 per CU, 64 passes)."""
+    import torch
+    from chromofold_amd import _abi as A
+    A.declare("cf_cache_read_async", A.I32, [A.P, A.U64, A.U32, A.P, A.P])
+    A.declare("cf_lds_read_async", A.I32, [A.U32, A.P, A.P])
+    A.declare("cf_lds_read_bytes", A.U64, [A.U32])
+    L = A.lib()
+    s = torch.cuda.current_stream().cuda_stream
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+    res = {}
+    for name, nbytes, passes in (("l2_read_gbs", 16 << 20, 128), ("mall_read_gbs", 128 << 20, 16)):
+        buf = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda:0")
+        fn = lambda: A.check(L.cf_cache_read_async(buf.data_ptr(), nbytes, passes, sink.data_ptr(), s),  # noqa
+                             "cf_cache_read_async")
+        _, per = _events_time(fn, steps, warmup)
+        res[name] = passes * nbytes / (float(np.median(per)) * 1e-3) / 1e9
+        del buf
+    passes = 64
+    _, per = _events_time(lambda: A.check(L.cf_lds_read_async(passes, sink.data_ptr(), s), "cf_lds_read_async"),
+                          steps, warmup)
+    res["lds_read_gbs"] = int(L.cf_lds_read_bytes(passes)) / (float(np.median(per)) * 1e-3) / 1e9
+    return res
 
 
 def bench_kv(steps: int, warmup: int, context: int = 32768, batch: int = 32, cpu: bool = True,
@@ -748,7 +789,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="auto", choices=["auto", "kv", "kv32", "rrr", "copy", "c5", "seal",
-                                                                  "nibble", "gather", "seam"])
+                                                                  "nibble", "gather", "seam", "fm"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--warm-s", type=float, default=3.0,
                     help="seconds of untimed back-to-back launches before the timed KV steps (0 for counter runs)")
@@ -772,6 +813,10 @@ def main() -> int:
         return 0
     if args.workload == "c5":
         print(json.dumps({"c5": bench_c5(args.steps, args.warmup)}))
+        return 0
+    if args.workload == "fm":
+        print(json.dumps({"c2_fm": bench_fm(args.steps, args.warmup, cpu=not args.no_cpu),
+                          "cache_peaks": bench_cache_peaks()}))
         return 0
     if args.workload == "seam":
         print(json.dumps({"seam": bench_seam(args.steps, args.warmup)}))
@@ -806,6 +851,15 @@ def main() -> int:
             secondary["nibble_pages"] = bench_nibble(min(args.steps, 20), 2, cpu=not args.no_cpu)
             secondary["gathers"] = bench_gather(min(args.steps, 20), 2)
             secondary["seam"] = bench_seam(min(args.steps, 20), 2)
+            peaks = bench_cache_peaks()
+            secondary["cache_peaks"] = peaks
+            l2 = peaks["l2_read_gbs"]
+            secondary["c1_rrr"]["rank_frac_of_l2"] = rrr["rank_roofline"]["achieved"] / l2
+            for k in ("count_roofline", "locate_roofline"):
+                r = secondary["c2_fm"][k]
+                r["frac_of_l2"] = r["achieved"] / l2
+                if r["traffic_gbs"]:  # L2-miss traffic against the Infinity Cache's read rate
+                    r["traffic_frac_of_mall"] = r["traffic_gbs"] / peaks["mall_read_gbs"]
             cp = bench_copy(10, 2)
             secondary["stream_copy_gbs"] = cp["stream_copy_gbs"]
             secondary["roofline_frac_of_stream_copy"] = kvr["roofline"]["achieved"] / cp["stream_copy_gbs"]

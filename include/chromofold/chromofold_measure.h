@@ -19,6 +19,17 @@ extern "C" {
  * bytes / kernel time. */
 cf_status cf_stream_read_async(const void *src, uint64_t bytes, uint32_t *sink, void *stream);
 
+/* Cache bandwidth: `passes` passes over `bytes` at `src` with ordinary 16-byte loads, each pass giving every
+ * workgroup another workgroup's chunk on the same XCD (so after the first pass the data comes from that XCD's L2,
+ * or from the Infinity Cache when `bytes` exceeds the L2s, and never from the CU's own L1). Achieved rate =
+ * passes * bytes / kernel time. Same argument rules as cf_stream_read_async; passes >= 1. */
+cf_status cf_cache_read_async(const void *src, uint64_t bytes, uint32_t passes, uint32_t *sink, void *stream);
+
+/* LDS bandwidth: two workgroups per CU each fill 64 KiB of LDS and read it `passes` times with conflict-free
+ * 16-byte reads; cf_lds_read_bytes(passes) is the bytes read per launch (on the current device). */
+cf_status cf_lds_read_async(uint32_t passes, uint32_t *sink, void *stream);
+uint64_t cf_lds_read_bytes(uint32_t passes);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif
