@@ -194,8 +194,9 @@ def bench_fm(steps: int, warmup: int, cpu: bool = True) -> dict:
 
 
 # ------------------------------------------------------------------------------------------------ matmul (C3)
-def bench_qw(steps: int, warmup: int, batches=(1, 4, 16, 64)) -> dict:
-    """4096 x 4096 int4 weights (N(0,1), per (row, 64-col) absmax), per-band Huffman, bf16 x: y = x W^T."""
+def bench_qw(steps: int, warmup: int, batches=(1, 4, 16, 64), codecs=("huffman", "rans")) -> dict:
+    """4096 x 4096 int4 weights (N(0,1), per (row, 64-col) absmax), per-band Huffman or pair-rANS tables, bf16 x:
+    y = x W^T. Roofline per batch: bytes = coded matrix + x + y over the per-call time (HBM-bound at small B)."""
     import torch
     import oracle as O
     from chromofold_amd import qw, synth
@@ -204,34 +205,40 @@ def bench_qw(steps: int, warmup: int, batches=(1, 4, 16, 64)) -> dict:
     REPS = 20
     rng = np.random.default_rng(synth.SEED_C3)
     W = rng.standard_normal((M, K), dtype=np.float32)
-    h = qw.encode_int4(W)
-    mat = qw.QwMatrix(h, "cuda:0")
-    res = {"coded_bytes": h.nbytes, "bits_per_weight": h.nbytes * 8.0 / (M * K)}
-    scales = np.repeat(h.scales, 64, axis=1)
-    for B in batches:
-        x = torch.from_numpy(rng.standard_normal((B, K), dtype=np.float32)).to(torch.bfloat16)
-        dx = x.to("cuda:0")
-        y = torch.empty((B, M), device="cuda:0")
-        mat.matmul_into(dx, y)
-        torch.cuda.synchronize()
-        if B <= 16:  # gate against the fp64 oracle
-            ref = O.qmatmul_f64(x.float().numpy(), h.sym, scales, 8)
-            err = float(np.abs(y.cpu().numpy() - ref).max() / np.abs(ref).max())
-            assert err <= 1e-3, err
-        # One call takes ~10-30 us, about what Python needs to issue it, so per-call events would time the host.
-        # Instead REPS back-to-back calls are captured in a graph (as a model's forward pass would issue them) and
-        # each replay is timed; every replay must reproduce the eager result bit for bit.
-        y_eager = y.clone()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for _ in range(REPS):
-                mat.matmul_into(dx, y)
-        torch.cuda.synchronize()
-        _, per = _events_time(g.replay, steps, warmup)
-        assert torch.equal(y, y_eager), "graph replay differs from the eager call"
-        t = float(np.mean(per)) * 1e-3 / REPS
-        byts = h.nbytes + 2 * B * K + 4 * B * M
-        res[f"B{B}"] = {"us": t * 1e6, "gbs": byts / t / 1e9, "tflops": 2.0 * B * M * K / t / 1e12}
+    sym, sc = qw.quantize_int4(W)
+    scales = np.repeat(sc, 64, axis=1)
+    xs = {B: torch.from_numpy(rng.standard_normal((B, K), dtype=np.float32)).to(torch.bfloat16) for B in batches}
+    refs = {B: O.qmatmul_f64(xs[B].float().numpy(), sym, scales, 8) for B in batches if B <= 16}
+    res = {}
+    for name in codecs:
+        codec = qw.QW_CODEC_HUFFMAN if name == "huffman" else qw.QW_CODEC_RANS
+        h = qw.encode_symbols(sym, sc, codec)
+        mat = qw.QwMatrix(h, "cuda:0")
+        r = {"coded_bytes": h.nbytes, "bits_per_weight": h.nbytes * 8.0 / (M * K)}
+        for B in batches:
+            dx = xs[B].to("cuda:0")
+            y = torch.empty((B, M), device="cuda:0")
+            mat.matmul_into(dx, y)
+            torch.cuda.synchronize()
+            if B in refs:  # gate against the fp64 oracle
+                err = float(np.abs(y.cpu().numpy() - refs[B]).max() / np.abs(refs[B]).max())
+                assert err <= 1e-3, (name, B, err)
+            # One call takes a few us, about what Python needs to issue it, so per-call events would time the host.
+            # Instead REPS back-to-back calls are captured in a graph (as a model's forward pass would issue them)
+            # and each replay is timed; every replay must reproduce the eager result bit for bit.
+            y_eager = y.clone()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(REPS):
+                    mat.matmul_into(dx, y)
+            torch.cuda.synchronize()
+            _, per = _events_time(g.replay, steps, warmup)
+            assert torch.equal(y, y_eager), "graph replay differs from the eager call"
+            t = float(np.mean(per)) * 1e-3 / REPS
+            byts = h.nbytes + 2 * B * K + 4 * B * M
+            r[f"B{B}"] = {"us": t * 1e6, "gbs": byts / t / 1e9, "frac": byts / t / 1e9 / HBM_PEAK_GBS,
+                          "tflops": 2.0 * B * M * K / t / 1e12}
+        res[name] = r
     return res
 
 
@@ -789,7 +796,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="auto", choices=["auto", "kv", "kv32", "rrr", "copy", "c5", "seal",
-                                                                  "nibble", "gather", "seam", "fm"])
+                                                                  "nibble", "gather", "seam", "fm", "qw"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--warm-s", type=float, default=3.0,
                     help="seconds of untimed back-to-back launches before the timed KV steps (0 for counter runs)")
@@ -817,6 +824,9 @@ def main() -> int:
     if args.workload == "fm":
         print(json.dumps({"c2_fm": bench_fm(args.steps, args.warmup, cpu=not args.no_cpu),
                           "cache_peaks": bench_cache_peaks()}))
+        return 0
+    if args.workload == "qw":
+        print(json.dumps({"c3_matmul": bench_qw(args.steps, args.warmup)}))
         return 0
     if args.workload == "seam":
         print(json.dumps({"seam": bench_seam(args.steps, args.warmup)}))

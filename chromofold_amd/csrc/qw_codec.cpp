@@ -139,3 +139,173 @@ extern "C" cf_status cf_qw_huffman_encode(const uint8_t *sym, uint32_t rows, uin
   }
   return CF_OK;
 }
+
+// ------------------------------------------------------------------------------------------------ rANS (pairs)
+namespace {
+
+constexpr uint32_t kProbM = 1u << CF_QW_RANS_PROB_BITS;  // 4096
+constexpr uint32_t kRansL = 1u << 16;                    // lane states live in [2^16, 2^32)
+
+struct RansGeom {
+  uint64_t bands, nstripes, nchunks;
+};
+
+RansGeom rans_geom(uint32_t rows, uint32_t cols) {
+  RansGeom g;
+  g.bands = (rows + CF_QW_BAND_ROWS - 1) / CF_QW_BAND_ROWS;
+  g.nstripes = (static_cast<uint64_t>(cols) + CF_QW_STRIPE_COLS - 1) / CF_QW_STRIPE_COLS;
+  g.nchunks = (g.nstripes + CF_QW_CHUNK_STRIPES - 1) / CF_QW_CHUNK_STRIPES;
+  return g;
+}
+
+// The pair lane l decodes at step t of stripe `stripe` in band b (the column order of chromofold_qw.h).
+inline uint32_t rans_pair(const uint8_t *sym, uint32_t rows, uint32_t cols, uint8_t zero, uint64_t b,
+                          uint64_t stripe, int l, int t) {
+  const int g = l >> 4, r = l & 15;
+  const uint64_t row = b * CF_QW_BAND_ROWS + r;
+  const uint64_t c = stripe * CF_QW_STRIPE_COLS + 64 * (t >> 3) + 16 * g + 4 * ((t >> 1) & 3) + 2 * (t & 1);
+  const auto at = [&](uint64_t col) -> uint32_t { return row < rows && col < cols ? sym[row * cols + col] : zero; };
+  return at(c) | (at(c + 1) << 4);
+}
+
+// Counts -> frequencies summing to 4096: largest remainder, then every present pair raised to >= 1 by taking from
+// the largest frequencies (ties: lower symbol first).
+void normalise_pairs(const uint64_t *cnt, uint16_t *freq) {
+  uint64_t total = 0;
+  for (int s = 0; s < 256; ++s) total += cnt[s];
+  int64_t f[256];
+  uint64_t rem[256];
+  int64_t sum = 0;
+  for (int s = 0; s < 256; ++s) {
+    f[s] = static_cast<int64_t>(cnt[s] * kProbM / total);
+    rem[s] = cnt[s] * kProbM % total;
+    sum += f[s];
+  }
+  std::vector<int> order;
+  for (int s = 0; s < 256; ++s)
+    if (cnt[s]) order.push_back(s);
+  std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return rem[a] > rem[b]; });
+  for (size_t i = 0; sum < kProbM; i = (i + 1) % order.size()) {
+    ++f[order[i]];
+    ++sum;
+  }
+  for (int s = 0; s < 256; ++s)
+    if (cnt[s] && f[s] == 0) {
+      f[s] = 1;
+      ++sum;
+    }
+  while (sum > kProbM) {
+    int pick = -1;
+    for (int s = 0; s < 256; ++s)
+      if (f[s] > 1 && (pick < 0 || f[s] > f[pick])) pick = s;
+    --f[pick];
+    --sum;
+  }
+  for (int s = 0; s < 256; ++s) freq[s] = static_cast<uint16_t>(f[s]);
+}
+
+// Encodes one stripe: the 64 lane states (in) are 2^16, out the decoder's initial states; `out` receives the
+// stream's 16-bit words in decoding order. Returns false for a pair without frequency.
+bool rans_encode_stripe(const uint8_t *sym, uint32_t rows, uint32_t cols, uint8_t zero, uint64_t b, uint64_t stripe,
+                        const uint16_t *freq, const uint32_t *cum, uint32_t *x, std::vector<uint16_t> &out) {
+  out.clear();
+  for (int l = 0; l < 64; ++l) x[l] = kRansL;
+  // decoding runs t = 0..31 with lanes in increasing order, so encoding runs backwards: t = 31..0, lanes 63..0,
+  // and the emitted words are reversed at the end
+  for (int t = 31; t >= 0; --t)
+    for (int l = 63; l >= 0; --l) {
+      const uint32_t s = rans_pair(sym, rows, cols, zero, b, stripe, l, t);
+      const uint32_t f = freq[s];
+      if (f == 0) return false;
+      const uint64_t xmax = static_cast<uint64_t>(kRansL >> CF_QW_RANS_PROB_BITS << 16) * f;
+      if (x[l] >= xmax) {
+        out.push_back(static_cast<uint16_t>(x[l] & 0xFFFFu));
+        x[l] >>= 16;
+      }
+      x[l] = (x[l] / f) * kProbM + x[l] % f + cum[s];
+    }
+  std::reverse(out.begin(), out.end());
+  return true;
+}
+
+}  // namespace
+
+extern "C" cf_status cf_qw_rans_plan(const uint8_t *sym, uint32_t rows, uint32_t cols, uint8_t zero,
+                                     uint16_t *freqs, uint32_t *chunk_words, uint32_t *last_words) {
+  if (!sym || !freqs || !chunk_words || !last_words || rows == 0 || cols == 0 || zero > 15)
+    return CF_ERR_INVALID_ARGUMENT;
+  const RansGeom g = rans_geom(rows, cols);
+  for (uint64_t i = 0; i < static_cast<uint64_t>(rows) * cols; ++i)
+    if (sym[i] > 15) return CF_ERR_INVALID_ARGUMENT;
+  uint64_t full_max = 0, last_max = 0;
+  std::vector<uint16_t> words;
+  for (uint64_t b = 0; b < g.bands; ++b) {
+    uint64_t cnt[256] = {};
+    for (uint64_t st = 0; st < g.nstripes; ++st)
+      for (int t = 0; t < 32; ++t)
+        for (int l = 0; l < 64; ++l) ++cnt[rans_pair(sym, rows, cols, zero, b, st, l, t)];
+    uint16_t *f = freqs + b * 256;
+    normalise_pairs(cnt, f);
+    uint32_t cum[256], c = 0;
+    for (int s = 0; s < 256; ++s) {
+      cum[s] = c;
+      c += f[s];
+    }
+    for (uint64_t ch = 0; ch < g.nchunks; ++ch) {
+      uint64_t slot = 0;
+      uint32_t x[64];
+      for (uint64_t st = ch * CF_QW_CHUNK_STRIPES; st < std::min<uint64_t>(g.nstripes, (ch + 1) * CF_QW_CHUNK_STRIPES);
+           ++st) {
+        if (!rans_encode_stripe(sym, rows, cols, zero, b, st, f, cum, x, words)) return CF_ERR_INVALID_ARGUMENT;
+        slot += words.size();
+      }
+      uint64_t &mx = ch + 1 == g.nchunks ? last_max : full_max;
+      mx = std::max(mx, slot);
+    }
+  }
+  const uint64_t cw = (full_max + 7) / 8 * 8, lw = std::max<uint64_t>(8, (last_max + 7) / 8 * 8);
+  if (cw > CF_QW_MAX_CHUNK_WORDS || lw > CF_QW_MAX_CHUNK_WORDS) return CF_ERR_UNSUPPORTED;
+  *chunk_words = static_cast<uint32_t>(cw);
+  *last_words = static_cast<uint32_t>(lw);
+  return CF_OK;
+}
+
+extern "C" cf_status cf_qw_rans_encode(const uint8_t *sym, uint32_t rows, uint32_t cols, uint8_t zero,
+                                       const uint16_t *freqs, uint32_t chunk_words, uint32_t last_words,
+                                       uint32_t *words, uint64_t word_capacity, uint32_t *offsets, uint32_t *states) {
+  if (!sym || !freqs || !words || !offsets || !states || rows == 0 || cols == 0 || zero > 15)
+    return CF_ERR_INVALID_ARGUMENT;
+  const RansGeom g = rans_geom(rows, cols);
+  if (chunk_words % 8 != 0 || chunk_words > CF_QW_MAX_CHUNK_WORDS || (g.nchunks > 1 && chunk_words == 0))
+    return CF_ERR_INVALID_ARGUMENT;
+  if (last_words == 0 || last_words % 8 != 0 || last_words > CF_QW_MAX_CHUNK_WORDS) return CF_ERR_INVALID_ARGUMENT;
+  const uint64_t band_words = (g.nchunks - 1) * chunk_words + last_words;
+  if (word_capacity < g.bands * band_words / 2) return CF_ERR_INVALID_ARGUMENT;
+  std::memset(words, 0, word_capacity * 4);
+  uint16_t *w16 = reinterpret_cast<uint16_t *>(words);  // little-endian: 16-bit word 2i + 1 is the high half
+  std::vector<uint16_t> stream;
+  for (uint64_t b = 0; b < g.bands; ++b) {
+    const uint16_t *f = freqs + b * 256;
+    uint32_t cum[256], c = 0;
+    for (int s = 0; s < 256; ++s) {
+      cum[s] = c;
+      c += f[s];
+    }
+    if (c != kProbM) return CF_ERR_INVALID_ARGUMENT;
+    for (uint64_t ch = 0; ch < g.nchunks; ++ch) {
+      uint16_t *slot = w16 + b * band_words + ch * chunk_words;
+      const uint64_t cap = ch + 1 == g.nchunks ? last_words : chunk_words;
+      uint64_t at = 0;
+      for (uint64_t st = ch * CF_QW_CHUNK_STRIPES; st < std::min<uint64_t>(g.nstripes, (ch + 1) * CF_QW_CHUNK_STRIPES);
+           ++st) {
+        uint32_t *x = states + (b * g.nstripes + st) * 64;
+        if (!rans_encode_stripe(sym, rows, cols, zero, b, st, f, cum, x, stream)) return CF_ERR_INVALID_ARGUMENT;
+        if (at + stream.size() > cap) return CF_ERR_INVALID_ARGUMENT;
+        offsets[b * g.nstripes + st] = static_cast<uint32_t>(at);
+        std::copy(stream.begin(), stream.end(), slot + at);
+        at += stream.size();
+      }
+    }
+  }
+  return CF_OK;
+}

@@ -1,4 +1,5 @@
-// qw_matmul.hip — decode-in-matmul over the band-table int4 format (include/chromofold/chromofold_qw.h) on gfx950:
+// qw_matmul.hip — decode-in-matmul over the band-table int4 Huffman format (CF_QW_CODEC_HUFFMAN,
+// include/chromofold/chromofold_qw.h; the rANS codec's kernel is in qw_rans.hip) on gfx950:
 // y[b, m] = sum_k x[b, k] * (sym[m, k] - zero) * scale[m, k / 64], the weight matrix held only in its coded form.
 //
 // One 1024-thread workgroup (16 waves) owns one band of 16 rows (so one code table) and walks K in chunks of 4096
@@ -22,6 +23,7 @@
 
 #include "cf_device.hpp"
 #include "chromofold/chromofold_qw.h"
+#include "qw_internal.hpp"
 
 namespace {
 
@@ -365,13 +367,12 @@ void launch_qw(const QwArgs &a, unsigned grid, hipStream_t s) {
 extern "C" cf_status cf_qw_validate(const cf_qw_matrix *w) {
   if (!w || w->struct_size != sizeof(cf_qw_matrix) || w->abi_version != CF_QW_ABI_VERSION)
     return CF_ERR_INVALID_ARGUMENT;
-  if (w->codec != CF_QW_CODEC_HUFFMAN) return CF_ERR_UNSUPPORTED;
+  if (w->codec != CF_QW_CODEC_HUFFMAN && w->codec != CF_QW_CODEC_RANS) return CF_ERR_UNSUPPORTED;
   if (w->rows == 0 || w->cols == 0 || w->rows > (1u << 30) || w->cols > (1u << 30)) return CF_ERR_INVALID_ARGUMENT;
-  if (!w->words || !w->seg_offsets || !w->code_lengths || !w->scales || w->word_count == 0)
-    return CF_ERR_INVALID_ARGUMENT;
+  if (!w->words || !w->offsets || !w->tables || !w->scales || w->word_count == 0) return CF_ERR_INVALID_ARGUMENT;
   if (w->zero < 0 || w->zero > 15) return CF_ERR_INVALID_ARGUMENT;
-  if ((reinterpret_cast<uintptr_t>(w->code_lengths) & 15) != 0) return CF_ERR_INVALID_ARGUMENT;
-  return CF_OK;
+  if ((reinterpret_cast<uintptr_t>(w->tables) & 15) != 0) return CF_ERR_INVALID_ARGUMENT;
+  return w->codec == CF_QW_CODEC_RANS ? cfqw::rans_validate(w) : CF_OK;
 }
 
 extern "C" cf_status cf_qw_matmul_async(const cf_qw_matrix *w, const uint16_t *x, float *y, uint32_t batch,
@@ -381,11 +382,12 @@ extern "C" cf_status cf_qw_matmul_async(const cf_qw_matrix *w, const uint16_t *x
   if (!x || !y) return CF_ERR_INVALID_ARGUMENT;
   if (batch == 0) return CF_OK;
   if (batch > (1u << 20)) return CF_ERR_UNSUPPORTED;
+  if (w->codec == CF_QW_CODEC_RANS) return cfqw::rans_matmul(w, x, y, batch, cfd::as_stream(stream));
   QwArgs a{};
   a.words = w->words;
   a.word_count = w->word_count;
-  a.seg_off = w->seg_offsets;
-  a.code_len = w->code_lengths;
+  a.seg_off = w->offsets;
+  a.code_len = w->tables;
   a.scales = w->scales;
   a.x = x;
   a.y = y;

@@ -13,13 +13,14 @@ import torch
 
 from . import _abi as A
 
-QW_ABI_VERSION, QW_CODEC_HUFFMAN, QW_BAND_ROWS, QW_SEG_COLS = 2, 1, 16, 64
+QW_ABI_VERSION, QW_CODEC_HUFFMAN, QW_CODEC_RANS, QW_BAND_ROWS, QW_SEG_COLS = 3, 1, 2, 16, 64
+QW_STRIPE_COLS, QW_CHUNK_STRIPES = 256, 16
 
 
 class cf_qw_matrix(C.Structure):
     _fields_ = [("struct_size", A.U32), ("abi_version", A.U32), ("codec", A.U32), ("rows", A.U32),
-                ("cols", A.U32), ("zero", A.I32), ("word_count", A.U64), ("words", A.P), ("seg_offsets", A.P), ("code_lengths", A.P),
-                ("scales", A.P)]
+                ("cols", A.U32), ("zero", A.I32), ("word_count", A.U64), ("words", A.P), ("offsets", A.P),
+                ("tables", A.P), ("scales", A.P), ("states", A.P), ("chunk_words", A.U32), ("last_words", A.U32)]
 
 
 A.declare("cf_qw_validate", A.I32, [C.POINTER(cf_qw_matrix)])
@@ -27,6 +28,8 @@ A.declare("cf_qw_matmul_async", A.I32, [C.POINTER(cf_qw_matrix), A.P, A.P, A.U32
 A.declare("cf_qw_quantize_int4", A.I32, [A.P, A.U32, A.U32, A.P, A.P])
 A.declare("cf_qw_huffman_plan", A.U64, [A.P, A.U32, A.U32, A.P])
 A.declare("cf_qw_huffman_encode", A.I32, [A.P, A.U32, A.U32, A.P, A.P, A.U64, A.P])
+A.declare("cf_qw_rans_plan", A.I32, [A.P, A.U32, A.U32, C.c_uint8, A.P, A.P, A.P])
+A.declare("cf_qw_rans_encode", A.I32, [A.P, A.U32, A.U32, C.c_uint8, A.P, A.U32, A.U32, A.P, A.U64, A.P, A.P])
 
 
 def _np_ptr(a: np.ndarray):
@@ -39,18 +42,24 @@ class QwHost:
     cols: int
     sym: np.ndarray           # [rows, cols] u8 (q + 8)
     scales: np.ndarray        # [rows, nseg] f32
-    code_lengths: np.ndarray  # [bands * 16] u8
+    tables: np.ndarray        # HUFFMAN [bands * 16] u8 code lengths; RANS [bands * 256] u16 pair frequencies
     words: np.ndarray         # u32
-    seg_offsets: np.ndarray   # [rows, nseg] u32
+    offsets: np.ndarray       # HUFFMAN [rows, nseg] bit offsets; RANS [bands * nstripes] slot offsets (u32)
+    codec: int = QW_CODEC_HUFFMAN
+    states: np.ndarray | None = None  # RANS [bands * nstripes * 64] u32
+    chunk_words: int = 0              # RANS 16-bit words per full-chunk slot
+    last_words: int = 0               # RANS 16-bit words of a band's last slot
+    zero: int = 8
 
     @property
     def nbytes(self) -> int:
-        """Resident bytes of the coded matrix: payload + segment offsets + scales + code tables."""
-        return self.words.nbytes + self.seg_offsets.nbytes + self.scales.nbytes + self.code_lengths.nbytes
+        """Resident bytes of the coded matrix: payload + offsets + scales + code tables (+ lane states)."""
+        n = self.words.nbytes + self.offsets.nbytes + self.scales.nbytes + self.tables.nbytes
+        return n + (self.states.nbytes if self.states is not None else 0)
 
 
-def encode_int4(w: np.ndarray) -> QwHost:
-    """Quantise (per row x 64-column absmax) and Huffman-code a row-major f32 matrix with the library encoder."""
+def quantize_int4(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Per (row, 64-column segment) absmax int4 quantisation with the library: (sym [rows, cols] u8, scales)."""
     w = np.ascontiguousarray(w, np.float32)
     rows, cols = w.shape
     nseg = (cols + QW_SEG_COLS - 1) // QW_SEG_COLS
@@ -58,11 +67,19 @@ def encode_int4(w: np.ndarray) -> QwHost:
     scales = np.zeros((rows, nseg), np.float32)
     L = A.lib()
     A.check(L.cf_qw_quantize_int4(_np_ptr(w), rows, cols, _np_ptr(sym), _np_ptr(scales)), "cf_qw_quantize_int4")
-    return encode_symbols(sym, scales)
+    return sym, scales
 
 
-def encode_symbols(sym: np.ndarray, scales: np.ndarray) -> QwHost:
+def encode_int4(w: np.ndarray, codec: int = QW_CODEC_HUFFMAN) -> QwHost:
+    """Quantise (per row x 64-column absmax) and entropy-code a row-major f32 matrix with the library encoder."""
+    sym, scales = quantize_int4(w)
+    return encode_symbols(sym, scales, codec)
+
+
+def encode_symbols(sym: np.ndarray, scales: np.ndarray, codec: int = QW_CODEC_HUFFMAN, zero: int = 8) -> QwHost:
     sym = np.ascontiguousarray(sym, np.uint8)
+    if codec == QW_CODEC_RANS:
+        return encode_symbols_rans(sym, scales, zero)
     rows, cols = sym.shape
     nseg = (cols + QW_SEG_COLS - 1) // QW_SEG_COLS
     bands = (rows + QW_BAND_ROWS - 1) // QW_BAND_ROWS
@@ -75,7 +92,29 @@ def encode_symbols(sym: np.ndarray, scales: np.ndarray) -> QwHost:
     offs = np.zeros((rows, nseg), np.uint32)
     A.check(L.cf_qw_huffman_encode(_np_ptr(sym), rows, cols, _np_ptr(lens), _np_ptr(words), nw, _np_ptr(offs)),
             "cf_qw_huffman_encode")
-    return QwHost(rows, cols, sym, np.ascontiguousarray(scales, np.float32), lens, words, offs)
+    return QwHost(rows, cols, sym, np.ascontiguousarray(scales, np.float32), lens, words, offs, zero=zero)
+
+
+def encode_symbols_rans(sym: np.ndarray, scales: np.ndarray, zero: int = 8) -> QwHost:
+    sym = np.ascontiguousarray(sym, np.uint8)
+    rows, cols = sym.shape
+    bands = (rows + QW_BAND_ROWS - 1) // QW_BAND_ROWS
+    nstripes = (cols + QW_STRIPE_COLS - 1) // QW_STRIPE_COLS
+    nchunks = (nstripes + QW_CHUNK_STRIPES - 1) // QW_CHUNK_STRIPES
+    freqs = np.zeros(bands * 256, np.uint16)
+    L = A.lib()
+    cw, lw = C.c_uint32(0), C.c_uint32(0)
+    A.check(L.cf_qw_rans_plan(_np_ptr(sym), rows, cols, zero, _np_ptr(freqs), C.byref(cw), C.byref(lw)),
+            "cf_qw_rans_plan")
+    cw, lw = cw.value, lw.value
+    nw = bands * ((nchunks - 1) * cw + lw) // 2
+    words = np.zeros(nw, np.uint32)
+    offs = np.zeros(bands * nstripes, np.uint32)
+    states = np.zeros(bands * nstripes * 64, np.uint32)
+    A.check(L.cf_qw_rans_encode(_np_ptr(sym), rows, cols, zero, _np_ptr(freqs), cw, lw, _np_ptr(words), nw,
+                                _np_ptr(offs), _np_ptr(states)), "cf_qw_rans_encode")
+    return QwHost(rows, cols, sym, np.ascontiguousarray(scales, np.float32), freqs, words, offs, QW_CODEC_RANS,
+                  states, cw, lw, zero)
 
 
 class QwMatrix:
@@ -86,14 +125,17 @@ class QwMatrix:
         dev = torch.device(device)
         self.t = {
             "words": torch.from_numpy(h.words.view(np.int32)).to(dev),
-            "offs": torch.from_numpy(h.seg_offsets.view(np.int32)).to(dev),
-            "lens": torch.from_numpy(h.code_lengths).to(dev),
+            "offs": torch.from_numpy(h.offsets.view(np.int32)).to(dev),
+            "tables": torch.from_numpy(h.tables.view(np.uint8)).to(dev),
             "scales": torch.from_numpy(h.scales).to(dev),
         }
+        if h.states is not None:
+            self.t["states"] = torch.from_numpy(h.states.view(np.int32)).to(dev)
         t = self.t
-        self.desc = cf_qw_matrix(C.sizeof(cf_qw_matrix), QW_ABI_VERSION, QW_CODEC_HUFFMAN, h.rows, h.cols, 8,
-                                 h.words.size, t["words"].data_ptr(), t["offs"].data_ptr(), t["lens"].data_ptr(),
-                                 t["scales"].data_ptr())
+        self.desc = cf_qw_matrix(C.sizeof(cf_qw_matrix), QW_ABI_VERSION, h.codec, h.rows, h.cols, h.zero,
+                                 h.words.size, t["words"].data_ptr(), t["offs"].data_ptr(), t["tables"].data_ptr(),
+                                 t["scales"].data_ptr(), t["states"].data_ptr() if "states" in t else None,
+                                 h.chunk_words, h.last_words)
 
     def matmul_into(self, x: torch.Tensor, y: torch.Tensor, stream=None) -> None:
         assert x.dtype == torch.bfloat16 and x.is_contiguous() and x.shape[1] == self.host.cols

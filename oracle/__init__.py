@@ -83,6 +83,7 @@ def _declare(L):
         "or_pack_fixed": (None, [P, C.c_uint64, U32, P]),
         "or_huffman_decode": (None, [P, P, C.c_int, I64, I64, P]),
         "or_rans_block_decode": (None, [P, P, P, P, P, P, C.c_int, C.c_int, P]),
+        "or_qw_rans_decode": (C.c_int, [P, U32, U32, P, P, P, U32, U32, C.c_int, P]),
         "or_paged_attention_f64": (C.c_int, [P, U32, U32, U32, U32, U32, U32, C.c_float, U32, P, P, P, P, P, P,
                                              P, P, U32, U32, P]),
         "or_dense_attention_f64": (None, [P, U32, P, P, U32, C.c_float, P]),
@@ -433,6 +434,18 @@ def rans_block_decode(data, byte_off, state0, slot2sym, freq, cum, block: int, n
          np.ascontiguousarray(freq, np.int32), np.ascontiguousarray(cum, np.int32)]
     lib().or_rans_block_decode(*[_ptr(x) for x in a], block, n, _ptr(out))
     return out
+
+
+def qw_rans_decode(words, chunk_words: int, last_words: int, offsets, states, freqs, rows: int, cols: int,
+                   mistake: int = 0):
+    """Decode a CF_QW_CODEC_RANS matrix (chromofold_qw.h) to its [rows, cols] u8 symbols; returns (symbols, number of
+    inconsistent stripes)."""
+    out = np.zeros((rows, cols), np.uint8)
+    a = [np.ascontiguousarray(words).view(np.uint16), np.ascontiguousarray(offsets, np.uint32),
+         np.ascontiguousarray(states, np.uint32), np.ascontiguousarray(freqs, np.uint16)]
+    bad = lib().or_qw_rans_decode(_ptr(a[0]), chunk_words, last_words, _ptr(a[1]), _ptr(a[2]), _ptr(a[3]), rows,
+                                  cols, mistake, _ptr(out))
+    return out, int(bad)
 
 
 def paged_attention_f64(q, q_heads, kv_heads, D, gqa, query_token, window, scale, pages, tail=None):

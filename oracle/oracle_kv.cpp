@@ -105,6 +105,65 @@ void or_rans_block_decode(const uint8_t *data, const int32_t *byte_off, const ui
   }
 }
 
+// Interleaved pair-rANS matrix decode (the CF_QW_CODEC_RANS layout of include/chromofold/chromofold_qw.h): per
+// band a 256-pair table (sum 4096), per 256-column stripe 64 lane states decoding 32 pairs each, the words of a step
+// taken by the lanes that need one in lane order; a band's slots are nchunks - 1 of chunk_words and one of
+// last_words 16-bit words. The decode step is the block-rANS step of reference
+// src/cuda/rans.cu:16-24 (slot lookup, x = f * (x >> 12) + slot - cum) with 16-bit renormalisation words and
+// L = 2^16. Writes sym[rows * cols]; returns the number of stripes whose lanes do not end at 2^16 or whose word
+// cursor does not end at the next stripe's first word (0 for a consistent matrix).
+// `mistake` plants an error for the tests that show the checks catch one: 1 = words taken in reverse lane order,
+// 2 = stripe columns with the roles of g and (t >> 1) & 3 swapped, 3 = x off by one after the update.
+int or_qw_rans_decode(const uint16_t *w16, uint32_t chunk_words, uint32_t last_words, const uint32_t *offsets,
+                      const uint32_t *states, const uint16_t *freqs, uint32_t rows, uint32_t cols, int mistake,
+                      uint8_t *sym) {
+  const uint64_t bands = (rows + 15) / 16, nstripes = (cols + 255ull) / 256, nchunks = (nstripes + 15) / 16;
+  const uint64_t band_words = (nchunks - 1) * chunk_words + last_words;
+  int bad = 0;
+  for (uint64_t b = 0; b < bands; ++b) {
+    const uint16_t *f = freqs + b * 256;
+    uint32_t cum[257];
+    cum[0] = 0;
+    for (int s = 0; s < 256; ++s) cum[s + 1] = cum[s] + f[s];
+    std::vector<uint8_t> of_slot(4096);
+    for (int s = 0; s < 256; ++s)
+      for (uint32_t k = cum[s]; k < cum[s + 1] && k < 4096; ++k) of_slot[k] = static_cast<uint8_t>(s);
+    for (uint64_t st = 0; st < nstripes; ++st) {
+      const uint64_t ch = st / 16;
+      const uint16_t *slot = w16 + b * band_words + ch * chunk_words;
+      const uint64_t slot_words = ch + 1 == nchunks ? last_words : chunk_words;
+      uint64_t cur = offsets[b * nstripes + st];
+      uint32_t x[64];
+      for (int l = 0; l < 64; ++l) x[l] = states[(b * nstripes + st) * 64 + l];
+      for (int t = 0; t < 32; ++t) {
+        bool need[64];
+        for (int l = 0; l < 64; ++l) {
+          const uint32_t slot_i = x[l] & 4095u;
+          const int s = of_slot[slot_i];
+          x[l] = f[s] * (x[l] >> 12) + slot_i - cum[s] + (mistake == 3 ? 1u : 0u);
+          need[l] = x[l] < 65536u;
+          const int g = l >> 4, r = l & 15, jj = (t >> 1) & 3;
+          const int c0 = 64 * (t >> 3) + (mistake == 2 ? 16 * jj + 4 * g : 16 * g + 4 * jj) + 2 * (t & 1);
+          const uint64_t row = b * 16 + r;
+          for (int e = 0; e < 2; ++e) {
+            const uint64_t c = st * 256 + c0 + e;
+            if (row < rows && c < cols) sym[row * cols + c] = static_cast<uint8_t>((s >> (4 * e)) & 15);
+          }
+        }
+        for (int i = 0; i < 64; ++i) {
+          const int l = mistake == 1 ? 63 - i : i;
+          if (need[l]) x[l] = (x[l] << 16) | slot[cur++];
+        }
+      }
+      for (int l = 0; l < 64; ++l) bad += x[l] != 65536u ? 1 : 0;
+      const bool last_in_chunk = st + 1 == nstripes || (st + 1) % 16 == 0;
+      if (!last_in_chunk && cur != offsets[b * nstripes + st + 1]) ++bad;
+      if (cur > slot_words) ++bad;
+    }
+  }
+  return bad;
+}
+
 // ---------------------------------------------------------------------------------------- paged attention
 // One query row per call. Pages: for page p, kv head kvh[p], tokens [tok0[p], tok0[p]+ntok[p]), dequantised K/V
 // at k + off[p]*D ([ntok, D] row-major). Tail: [tail_n, kv_heads, D] starting at tail_tok0. Output [q_heads, D].

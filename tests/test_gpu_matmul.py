@@ -5,8 +5,10 @@ relative (north star; the kernels reach ~1e-6 because every MFMA product is exac
     inside code blocks (K not a multiple of the block), block sizes 64 / 100 / 37, batches 1..65 (two passes),
     a K beyond one staged 4096-column chunk, a LUT too long for LDS (maxlen 14), a zero point outside the u8 range;
     dense W must hold the reference's exact dequantised values;
-  * cf_qw_matmul_async at the C3 shape (4096 x 4096 int4, per-band Huffman, per (row, 64-col) scale, bf16 x,
-    B in 1/4/16/64) plus ragged shapes.
+  * cf_qw_matmul_async at the C3 shape (4096 x 4096 int4, per-band Huffman or pair-rANS tables, per (row, 64-col)
+    scale, bf16 x, B in 1/4/16/64) plus ragged shapes, for both codecs;
+  * an identity input (x = I, B = K) through cf_qw_matmul_async gives every dequantised weight bit for bit
+    (y[k, m] = (sym[m, k] - zero) * scale[m, k / 64]: one exact product per output), for both codecs.
 """
 import numpy as np
 import pytest
@@ -80,11 +82,14 @@ def test_reference_stream_contract(dev):
     assert L.cf_dense_matmul_async(p, p, p, 8, 64, p, None, p, 1, 1, 1, 1.0, 8, None) == _abi.CF_ERR_INVALID_ARGUMENT
 
 
-def _qw_check(dev, W, batches):
+HUFF, RANS = 1, 2  # CF_QW_CODEC_HUFFMAN, CF_QW_CODEC_RANS
+
+
+def _qw_check(dev, W, batches, codec=HUFF):
     import torch
     from chromofold_amd import qw
     M, K = W.shape
-    h = qw.encode_int4(W)
+    h = qw.encode_int4(W, codec)
     mat = qw.QwMatrix(h, dev)
     scales = np.repeat(h.scales, 64, axis=1)[:, :K]
     for B in batches:
@@ -99,13 +104,37 @@ def _qw_check(dev, W, batches):
     return h
 
 
+@pytest.mark.parametrize("codec", [HUFF, RANS])
 @pytest.mark.parametrize("M,K,batches", [(4096, 4096, (1, 4, 16, 64)), (40, 1000, (3, 17)), (24, 8200, (64,)),
-                                         (33, 1001, (70, 1))])
-def test_qw_matmul(dev, M, K, batches):
+                                         (33, 1001, (70, 1)), (20, 12288, (33,))])
+def test_qw_matmul(dev, M, K, batches, codec):
     # ragged rows (not a band multiple), K not a multiple of 64 (or of 4: scalar x loads), K over one 4096-column
-    # chunk, and 70 batch rows (two launches: 4 tiles + 1)
+    # chunk (rANS: a full chunk and a short last one; three full chunks), 70 batch rows (two launches: 4 tiles + 1)
     rng = np.random.default_rng(M * 3 + K)
-    _qw_check(dev, rng.standard_normal((M, K)).astype(np.float32), batches)
+    _qw_check(dev, rng.standard_normal((M, K)).astype(np.float32), batches, codec)
+
+
+@pytest.mark.parametrize("codec", [HUFF, RANS])
+@pytest.mark.parametrize("M,K", [(512, 4096), (40, 1000), (17, 4160)])
+def test_qw_identity_decodes_every_weight(dev, M, K, codec):
+    """x = I (B = K rows): y[k, m] = (sym[m, k] - zero) * scale[m, k / 64] is one exact product, so every weight the
+    kernel decodes (and its scale) is checked bit for bit against the quantiser's symbols; the weights get a per-row
+    spread of magnitudes and a few all-zero segments."""
+    import torch
+    from chromofold_amd import qw
+    rng = np.random.default_rng(M + K + codec)
+    W = (rng.standard_normal((M, K)) * np.exp(rng.uniform(-2, 2, (M, 1)))).astype(np.float32)
+    W[1, :min(K, 128)] = 0.0
+    h = qw.encode_int4(W, codec)
+    mat = qw.QwMatrix(h, dev)
+    x = torch.eye(K, dtype=torch.bfloat16, device=dev)
+    y = torch.full((K, M), float("nan"), device=dev)
+    mat.matmul_into(x, y)
+    torch.cuda.synchronize()
+    want = ((h.sym.astype(np.float32) - 8.0) * np.repeat(h.scales, 64, axis=1)[:, :K]).T
+    got = y.cpu().numpy()
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, (bad[:5], got[tuple(bad[0])], want[tuple(bad[0])])
 
 
 def test_qw_matmul_skewed_band(dev):
@@ -119,21 +148,23 @@ def test_qw_matmul_skewed_band(dev):
     W[15] = rng.uniform(-1, 1, K)
     W[16:] = rng.standard_normal((32, K))
     h = _qw_check(dev, W, (1, 16))
-    offs = h.seg_offsets.astype(np.int64).ravel()
+    offs = h.offsets.astype(np.int64).ravel()
     ends = np.append(offs[1:], h.words.size * 32).reshape(M, -1)
     first = offs.reshape(M, -1)[:, 0]
     need = (ends[:, -1] >> 5) + 6 - ((first >> 5) & ~3)
     assert need[15] > 640 and need[16:].max() <= 640, need
+    _qw_check(dev, W, (1, 16), RANS)  # rANS: the band's table gives the uniform row's pairs ~8 bits each
 
 
-def test_qw_matmul_graph_replays(dev):
+@pytest.mark.parametrize("codec", [HUFF, RANS])
+def test_qw_matmul_graph_replays(dev, codec):
     """cf_qw_matmul_async captured in a HIP graph: every replay (with eager work changing x in between) equals the
     eager call on the same x bit for bit."""
     import torch
     from chromofold_amd import qw
     rng = np.random.default_rng(7)
     M, K, B = 64, 4096, 16
-    mat = qw.QwMatrix(qw.encode_int4(rng.standard_normal((M, K)).astype(np.float32)), dev)
+    mat = qw.QwMatrix(qw.encode_int4(rng.standard_normal((M, K)).astype(np.float32), codec), dev)
     x = torch.zeros((B, K), dtype=torch.bfloat16, device=dev)
     y = torch.zeros((B, M), device=dev)
     mat.matmul_into(x, y)  # warm up outside the capture
@@ -152,8 +183,9 @@ def test_qw_matmul_graph_replays(dev):
         assert torch.equal(got, want), r
 
 
+@pytest.mark.parametrize("codec", [HUFF, RANS])
 @pytest.mark.parametrize("seed", [1, 2, 3])
-def test_qw_matmul_random_shapes(dev, seed):
+def test_qw_matmul_random_shapes(dev, seed, codec):
     """Random M (not a band multiple), K (ragged last segment, sometimes over one 4096-column chunk) and batch
     (1 .. 140: up to three launches), weights with a per-row spread of magnitudes."""
     rng = np.random.default_rng(1000 + seed)
@@ -161,4 +193,4 @@ def test_qw_matmul_random_shapes(dev, seed):
     K = int(rng.integers(1, 9000))
     B = int(rng.integers(1, 141))
     W = (rng.standard_normal((M, K)) * np.exp(rng.uniform(-3, 3, (M, 1)))).astype(np.float32)
-    _qw_check(dev, W, (B,))
+    _qw_check(dev, W, (B,), codec)
