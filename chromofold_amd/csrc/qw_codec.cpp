@@ -231,8 +231,8 @@ bool rans_encode_stripe(const uint8_t *sym, uint32_t rows, uint32_t cols, uint8_
 }  // namespace
 
 extern "C" cf_status cf_qw_rans_plan(const uint8_t *sym, uint32_t rows, uint32_t cols, uint8_t zero,
-                                     uint16_t *freqs, uint32_t *chunk_words, uint32_t *last_words) {
-  if (!sym || !freqs || !chunk_words || !last_words || rows == 0 || cols == 0 || zero > 15)
+                                     uint16_t *cum_out, uint32_t *chunk_words, uint32_t *last_words) {
+  if (!sym || !cum_out || !chunk_words || !last_words || rows == 0 || cols == 0 || zero > 15)
     return CF_ERR_INVALID_ARGUMENT;
   const RansGeom g = rans_geom(rows, cols);
   for (uint64_t i = 0; i < static_cast<uint64_t>(rows) * cols; ++i)
@@ -244,11 +244,12 @@ extern "C" cf_status cf_qw_rans_plan(const uint8_t *sym, uint32_t rows, uint32_t
     for (uint64_t st = 0; st < g.nstripes; ++st)
       for (int t = 0; t < 32; ++t)
         for (int l = 0; l < 64; ++l) ++cnt[rans_pair(sym, rows, cols, zero, b, st, l, t)];
-    uint16_t *f = freqs + b * 256;
+    uint16_t f[256];
     normalise_pairs(cnt, f);
     uint32_t cum[256], c = 0;
     for (int s = 0; s < 256; ++s) {
       cum[s] = c;
+      cum_out[b * 256 + s] = static_cast<uint16_t>(c);
       c += f[s];
     }
     for (uint64_t ch = 0; ch < g.nchunks; ++ch) {
@@ -271,9 +272,9 @@ extern "C" cf_status cf_qw_rans_plan(const uint8_t *sym, uint32_t rows, uint32_t
 }
 
 extern "C" cf_status cf_qw_rans_encode(const uint8_t *sym, uint32_t rows, uint32_t cols, uint8_t zero,
-                                       const uint16_t *freqs, uint32_t chunk_words, uint32_t last_words,
+                                       const uint16_t *cum_in, uint32_t chunk_words, uint32_t last_words,
                                        uint32_t *words, uint64_t word_capacity, uint32_t *offsets, uint32_t *states) {
-  if (!sym || !freqs || !words || !offsets || !states || rows == 0 || cols == 0 || zero > 15)
+  if (!sym || !cum_in || !words || !offsets || !states || rows == 0 || cols == 0 || zero > 15)
     return CF_ERR_INVALID_ARGUMENT;
   const RansGeom g = rans_geom(rows, cols);
   if (chunk_words % 8 != 0 || chunk_words > CF_QW_MAX_CHUNK_WORDS || (g.nchunks > 1 && chunk_words == 0))
@@ -285,13 +286,16 @@ extern "C" cf_status cf_qw_rans_encode(const uint8_t *sym, uint32_t rows, uint32
   uint16_t *w16 = reinterpret_cast<uint16_t *>(words);  // little-endian: 16-bit word 2i + 1 is the high half
   std::vector<uint16_t> stream;
   for (uint64_t b = 0; b < g.bands; ++b) {
-    const uint16_t *f = freqs + b * 256;
-    uint32_t cum[256], c = 0;
+    const uint16_t *cb = cum_in + b * 256;
+    uint16_t f[256];
+    uint32_t cum[256];
+    if (cb[0] != 0) return CF_ERR_INVALID_ARGUMENT;
     for (int s = 0; s < 256; ++s) {
-      cum[s] = c;
-      c += f[s];
+      const uint32_t next = s < 255 ? cb[s + 1] : kProbM;
+      if (next < cb[s]) return CF_ERR_INVALID_ARGUMENT;
+      cum[s] = cb[s];
+      f[s] = static_cast<uint16_t>(next - cb[s]);
     }
-    if (c != kProbM) return CF_ERR_INVALID_ARGUMENT;
     for (uint64_t ch = 0; ch < g.nchunks; ++ch) {
       uint16_t *slot = w16 + b * band_words + ch * chunk_words;
       const uint64_t cap = ch + 1 == g.nchunks ? last_words : chunk_words;

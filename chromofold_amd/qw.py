@@ -42,7 +42,7 @@ class QwHost:
     cols: int
     sym: np.ndarray           # [rows, cols] u8 (q + 8)
     scales: np.ndarray        # [rows, nseg] f32
-    tables: np.ndarray        # HUFFMAN [bands * 16] u8 code lengths; RANS [bands * 256] u16 pair frequencies
+    tables: np.ndarray        # HUFFMAN [bands * 16] u8 code lengths; RANS [bands * 256] u16 cumulative starts
     words: np.ndarray         # u32
     offsets: np.ndarray       # HUFFMAN [rows, nseg] bit offsets; RANS [bands * nstripes] slot offsets (u32)
     codec: int = QW_CODEC_HUFFMAN
@@ -101,19 +101,19 @@ def encode_symbols_rans(sym: np.ndarray, scales: np.ndarray, zero: int = 8) -> Q
     bands = (rows + QW_BAND_ROWS - 1) // QW_BAND_ROWS
     nstripes = (cols + QW_STRIPE_COLS - 1) // QW_STRIPE_COLS
     nchunks = (nstripes + QW_CHUNK_STRIPES - 1) // QW_CHUNK_STRIPES
-    freqs = np.zeros(bands * 256, np.uint16)
+    cum = np.zeros(bands * 256, np.uint16)
     L = A.lib()
     cw, lw = C.c_uint32(0), C.c_uint32(0)
-    A.check(L.cf_qw_rans_plan(_np_ptr(sym), rows, cols, zero, _np_ptr(freqs), C.byref(cw), C.byref(lw)),
+    A.check(L.cf_qw_rans_plan(_np_ptr(sym), rows, cols, zero, _np_ptr(cum), C.byref(cw), C.byref(lw)),
             "cf_qw_rans_plan")
     cw, lw = cw.value, lw.value
     nw = bands * ((nchunks - 1) * cw + lw) // 2
     words = np.zeros(nw, np.uint32)
     offs = np.zeros(bands * nstripes, np.uint32)
     states = np.zeros(bands * nstripes * 64, np.uint32)
-    A.check(L.cf_qw_rans_encode(_np_ptr(sym), rows, cols, zero, _np_ptr(freqs), cw, lw, _np_ptr(words), nw,
+    A.check(L.cf_qw_rans_encode(_np_ptr(sym), rows, cols, zero, _np_ptr(cum), cw, lw, _np_ptr(words), nw,
                                 _np_ptr(offs), _np_ptr(states)), "cf_qw_rans_encode")
-    return QwHost(rows, cols, sym, np.ascontiguousarray(scales, np.float32), freqs, words, offs, QW_CODEC_RANS,
+    return QwHost(rows, cols, sym, np.ascontiguousarray(scales, np.float32), cum, words, offs, QW_CODEC_RANS,
                   states, cw, lw, zero)
 
 

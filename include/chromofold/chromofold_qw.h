@@ -18,7 +18,8 @@
  *     symbol) order), 16 bytes per band, 16-byte aligned.
  * CF_QW_CODEC_RANS
  *   - symbols are coded in pairs: pair = sym[c] | sym[c + 1] << 4 (c even), one 256-symbol rANS alphabet per band;
- *     tables: per band 256 u16 pair frequencies summing to 4096 (CF_QW_RANS_PROB_BITS = 12);
+ *     tables: per band the 256 pairs' cumulative starts cum_s (u16, cum_0 = 0, non-decreasing, cum_256 = 4096
+ *     implied): pair s has frequency f_s = cum_{s+1} - cum_s out of 4096 (CF_QW_RANS_PROB_BITS = 12);
  *   - a stripe is 256 columns of one band (nstripes = ceil(cols / 256); columns past `cols` and rows past `rows`
  *     hold the pair (zero, zero)). A stripe is one stream of 16-bit words decoded by 64 interleaved lane states:
  *     lane l = 16 g + r (row r of the band) decodes at step t = 0..31 the pair at stripe column
@@ -67,7 +68,7 @@ typedef struct cf_qw_matrix {
   uint64_t word_count;  /* 32-bit words of `words` (bounds the decoder's reads) */
   const uint32_t *words;   /* device: code stream */
   const uint32_t *offsets; /* device: HUFFMAN [rows * nseg] bit offsets; RANS [bands * nstripes] slot offsets */
-  const uint8_t *tables;   /* device: HUFFMAN [bands * 16] code lengths; RANS [bands * 256] u16 frequencies;
+  const uint8_t *tables;   /* device: HUFFMAN [bands * 16] code lengths; RANS [bands * 256] u16 cumulative starts;
                               16-byte aligned */
   const float *scales;     /* device: [rows * nseg] */
   const uint32_t *states;  /* device: RANS [bands * nstripes * 64] initial lane states; HUFFMAN unused (NULL) */
@@ -96,15 +97,15 @@ uint64_t cf_qw_huffman_plan(const uint8_t *sym, uint32_t rows, uint32_t cols, ui
 cf_status cf_qw_huffman_encode(const uint8_t *sym, uint32_t rows, uint32_t cols, const uint8_t *code_lengths,
                                uint32_t *words, uint64_t word_capacity, uint32_t *seg_offsets);
 
-/* rANS plan: per-band pair frequencies freqs[ceil(rows / 16) * 256] (each band's sum 4096; every pair the band holds,
- * padding pairs (zero, zero) included, gets >= 1) and the slot sizes chunk_words / last_words of the descriptor.
- * `words` then needs bands * ((nchunks - 1) * chunk_words + last_words) / 2 32-bit words. */
-cf_status cf_qw_rans_plan(const uint8_t *sym, uint32_t rows, uint32_t cols, uint8_t zero, uint16_t *freqs,
+/* rANS plan: per-band pair tables cum[ceil(rows / 16) * 256] (cumulative starts, frequencies summing to 4096; every
+ * pair the band holds, padding pairs (zero, zero) included, gets f >= 1) and the slot sizes chunk_words / last_words
+ * of the descriptor. `words` then needs bands * ((nchunks - 1) * chunk_words + last_words) / 2 32-bit words. */
+cf_status cf_qw_rans_plan(const uint8_t *sym, uint32_t rows, uint32_t cols, uint8_t zero, uint16_t *cum,
                           uint32_t *chunk_words, uint32_t *last_words);
 
-/* rANS encode with the planned frequencies and slot sizes: words[word_capacity] (slots zero padded),
+/* rANS encode with the planned tables and slot sizes: words[word_capacity] (slots zero padded),
  * offsets[bands * nstripes], states[bands * nstripes * 64]. */
-cf_status cf_qw_rans_encode(const uint8_t *sym, uint32_t rows, uint32_t cols, uint8_t zero, const uint16_t *freqs,
+cf_status cf_qw_rans_encode(const uint8_t *sym, uint32_t rows, uint32_t cols, uint8_t zero, const uint16_t *cum,
                             uint32_t chunk_words, uint32_t last_words, uint32_t *words, uint64_t word_capacity,
                             uint32_t *offsets, uint32_t *states);
 

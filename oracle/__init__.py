@@ -436,13 +436,13 @@ def rans_block_decode(data, byte_off, state0, slot2sym, freq, cum, block: int, n
     return out
 
 
-def qw_rans_decode(words, chunk_words: int, last_words: int, offsets, states, freqs, rows: int, cols: int,
+def qw_rans_decode(words, chunk_words: int, last_words: int, offsets, states, cums, rows: int, cols: int,
                    mistake: int = 0):
     """Decode a CF_QW_CODEC_RANS matrix (chromofold_qw.h) to its [rows, cols] u8 symbols; returns (symbols, number of
     inconsistent stripes)."""
     out = np.zeros((rows, cols), np.uint8)
     a = [np.ascontiguousarray(words).view(np.uint16), np.ascontiguousarray(offsets, np.uint32),
-         np.ascontiguousarray(states, np.uint32), np.ascontiguousarray(freqs, np.uint16)]
+         np.ascontiguousarray(states, np.uint32), np.ascontiguousarray(cums, np.uint16)]
     bad = lib().or_qw_rans_decode(_ptr(a[0]), chunk_words, last_words, _ptr(a[1]), _ptr(a[2]), _ptr(a[3]), rows,
                                   cols, mistake, _ptr(out))
     return out, int(bad)

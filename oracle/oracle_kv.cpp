@@ -106,7 +106,7 @@ void or_rans_block_decode(const uint8_t *data, const int32_t *byte_off, const ui
 }
 
 // Interleaved pair-rANS matrix decode (the CF_QW_CODEC_RANS layout of include/chromofold/chromofold_qw.h): per
-// band a 256-pair table (sum 4096), per 256-column stripe 64 lane states decoding 32 pairs each, the words of a step
+// band a 256-pair table of cumulative starts (frequencies summing to 4096), per 256-column stripe 64 lane states decoding 32 pairs each, the words of a step
 // taken by the lanes that need one in lane order; a band's slots are nchunks - 1 of chunk_words and one of
 // last_words 16-bit words. The decode step is the block-rANS step of reference
 // src/cuda/rans.cu:16-24 (slot lookup, x = f * (x >> 12) + slot - cum) with 16-bit renormalisation words and
@@ -115,16 +115,16 @@ void or_rans_block_decode(const uint8_t *data, const int32_t *byte_off, const ui
 // `mistake` plants an error for the tests that show the checks catch one: 1 = words taken in reverse lane order,
 // 2 = stripe columns with the roles of g and (t >> 1) & 3 swapped, 3 = x off by one after the update.
 int or_qw_rans_decode(const uint16_t *w16, uint32_t chunk_words, uint32_t last_words, const uint32_t *offsets,
-                      const uint32_t *states, const uint16_t *freqs, uint32_t rows, uint32_t cols, int mistake,
+                      const uint32_t *states, const uint16_t *cums, uint32_t rows, uint32_t cols, int mistake,
                       uint8_t *sym) {
   const uint64_t bands = (rows + 15) / 16, nstripes = (cols + 255ull) / 256, nchunks = (nstripes + 15) / 16;
   const uint64_t band_words = (nchunks - 1) * chunk_words + last_words;
   int bad = 0;
   for (uint64_t b = 0; b < bands; ++b) {
-    const uint16_t *f = freqs + b * 256;
-    uint32_t cum[257];
-    cum[0] = 0;
-    for (int s = 0; s < 256; ++s) cum[s + 1] = cum[s] + f[s];
+    uint32_t cum[257], f[256];
+    for (int s = 0; s < 256; ++s) cum[s] = cums[b * 256 + s];
+    cum[256] = 4096;
+    for (int s = 0; s < 256; ++s) f[s] = cum[s + 1] - cum[s];
     std::vector<uint8_t> of_slot(4096);
     for (int s = 0; s < 256; ++s)
       for (uint32_t k = cum[s]; k < cum[s + 1] && k < 4096; ++k) of_slot[k] = static_cast<uint8_t>(s);

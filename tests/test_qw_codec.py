@@ -117,6 +117,12 @@ def _rans(W):
     return qw.encode_int4(W, qw.QW_CODEC_RANS)
 
 
+def _freqs(h):
+    """[bands, 256] pair frequencies from the descriptor's cumulative starts."""
+    cum = h.tables.reshape(-1, 256).astype(np.int64)
+    return np.diff(np.concatenate([cum, np.full((cum.shape[0], 1), 4096)], 1), axis=1)
+
+
 def _rans_decode(h, mistake=0):
     return O.qw_rans_decode(h.words, h.chunk_words, h.last_words, h.offsets, h.states, h.tables, h.rows, h.cols,
                             mistake)
@@ -149,7 +155,8 @@ def test_rans_planted_mistakes_fail_the_roundtrip():
 
 
 def test_rans_tables_and_closed_forms():
-    """Frequencies: every band sums to 4096, a pair the band holds has f >= 1 and an absent pair f = 0. Closed form:
+    """Tables: cumulative starts from 0, frequencies summing to 4096, a pair the band holds has f >= 1 and an absent
+    pair f = 0. Closed form:
     a band holding one pair only (an all-zero band: (zero, zero) everywhere) gets f = 4096 for it, its encoder
     never renormalises (f * (x >> 12) + (x & 4095) = x when f = 4096), so its lanes keep the initial 2^16 and it
     emits no word; the oracle still decodes it."""
@@ -157,8 +164,8 @@ def test_rans_tables_and_closed_forms():
     W = rng.standard_normal((48, 4096)).astype(np.float32)
     W[16:32] = 0.0
     h = _rans(W)
-    F = h.tables.reshape(-1, 256).astype(np.int64)
-    assert (F.sum(1) == 4096).all()
+    F = _freqs(h)
+    assert (F.sum(1) == 4096).all() and (h.tables.reshape(-1, 256)[:, 0] == 0).all()
     for b in range(3):
         s = h.sym[16 * b:16 * b + 16]
         pairs = np.unique(s[:, 0::2].astype(np.int64) | (s[:, 1::2].astype(np.int64) << 4))
@@ -181,7 +188,7 @@ def test_rans_stream_length_matches_the_table_cost():
     rng = np.random.default_rng(13)
     rows, cols = 32, 4096
     h = _rans(rng.standard_normal((rows, cols)).astype(np.float32))
-    F = h.tables.reshape(-1, 256).astype(np.float64)
+    F = _freqs(h).astype(np.float64)
     ns = cols // 256
     offs = h.offsets.reshape(-1, ns).astype(np.int64)
     states = h.states.reshape(-1, ns, 64).astype(np.float64)
