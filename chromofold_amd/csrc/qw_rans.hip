@@ -302,13 +302,19 @@ __global__ void __launch_bounds__(kThreads) qw_rans_kernel(RansArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) red[(wave * NT + i) * 256 + lane * 4 + e] = acc[i][e];
   __syncthreads();
-  for (int o = t; o < NT * 256; o += kThreads) {  // NT * 256 outputs, up to two per thread
+  // four threads per output, each summing a quarter of the waves, then two lane swaps (fixed order throughout)
+  static_assert(kWaves % 4 == 0, "four partial sums per output");
+  for (int o4 = t; o4 < NT * 256 * 4; o4 += kThreads) {
+    const int o = o4 >> 2, part = o4 & 3;
     const int i = o >> 8, idx = o & 255;
+    float s = 0.f;
+#pragma unroll
+    for (int w = part * (kWaves / 4); w < (part + 1) * (kWaves / 4); ++w) s += red[(w * NT + i) * 256 + idx];
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
     const int fl = idx >> 2, fr = idx & 3;
     const int b = (a.bt0 + i) * 16 + 4 * (fl >> 4) + fr, m = m0 + (fl & 15);
-    float s = 0.f;
-    for (int w = 0; w < kWaves; ++w) s += red[(w * NT + i) * 256 + idx];
-    if (b < B && m < M) a.y[static_cast<int64_t>(b) * M + m] = s;
+    if (part == 0 && b < B && m < M) a.y[static_cast<int64_t>(b) * M + m] = s;
   }
 }
 
