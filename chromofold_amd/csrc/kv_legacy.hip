@@ -67,28 +67,48 @@ __device__ __forceinline__ int huff_at(const uint32_t *__restrict__ words, const
   return lut[look];
 }
 
-// fixed-width MSB-first code of symbol i (bits dividing 32, as the reference packer writes them)
-__device__ __forceinline__ int fixed_at(const uint32_t *__restrict__ words, uint32_t bits, int64_t i) {
-  const int64_t bit = i * bits;
-  const uint32_t w = words[bit >> 5];
-  return static_cast<int>((w >> ((32u - bits) - static_cast<uint32_t>(bit & 31))) & ((1u << bits) - 1u));
+// Fixed-width MSB-first codes (bits dividing 32, as the reference packer writes them) of symbols [s0, s1) of two
+// streams (K and V of a page) with the workgroup's threads: whole 32-bit words per thread, every load of both spans
+// issued before any symbol is used (one memory latency per page chunk instead of one per symbol and stream);
+// putk / putv(token, dim, sym) with the token relative to s0 / hd.
+template <typename PutK, typename PutV>
+__device__ void decode_fixed_pair(const uint32_t *__restrict__ kw, const uint32_t *__restrict__ vw, uint32_t bits,
+                                  int64_t s0, int64_t s1, uint32_t hd, int tid, const PutK &putk, const PutV &putv) {
+  const uint32_t spw = 32u / bits, mask = (1u << bits) - 1u;
+  const int64_t w0 = s0 / spw, w1 = (s1 + spw - 1) / spw;
+  for (int64_t wb = w0; wb < w1; wb += 2 * kThreads) {
+    const int64_t wa = wb + tid, wc = wa + kThreads;
+    const bool ha = wa < w1, hc = wc < w1;
+    const int64_t la = ha ? wa : w0, lc = hc ? wc : w0;  // clamped: loads issued unconditionally
+    const uint32_t ka = kw[la], kc = kw[lc], va = vw[la], vc = vw[lc];
+    for (uint32_t k = 0; k < spw; ++k) {
+      const uint32_t sh = 32u - bits * (k + 1);
+      const int64_t ia = wa * spw + k, ic = wc * spw + k;
+      if (ha && ia >= s0 && ia < s1) {
+        const uint32_t rel = static_cast<uint32_t>(ia - s0), r = rel / hd;
+        putk(r, rel - r * hd, (ka >> sh) & mask);
+        putv(r, rel - r * hd, (va >> sh) & mask);
+      }
+      if (hc && ic >= s0 && ic < s1) {
+        const uint32_t rel = static_cast<uint32_t>(ic - s0), r = rel / hd;
+        putk(r, rel - r * hd, (kc >> sh) & mask);
+        putv(r, rel - r * hd, (vc >> sh) & mask);
+      }
+    }
+  }
 }
 
-// Decode symbols [s0, s1) of one stream (rows of hd symbols) with the workgroup's threads; put(token, dim, sym) with
-// the token relative to s0 / hd.
+// Decode symbols [s0, s1) of one Huffman stream (rows of hd symbols) with the workgroup's threads; put(token, dim,
+// sym) with the token relative to s0 / hd.
 template <typename Put>
 __device__ void decode_span(const uint32_t *__restrict__ words, const int32_t *__restrict__ boff,
-                            const int32_t *__restrict__ lut, uint32_t maxlen, uint32_t fixed_bits, uint32_t block,
-                            int64_t s0, int64_t s1, uint32_t hd, int tid, const Put &put) {
+                            const int32_t *__restrict__ lut, uint32_t maxlen, uint32_t block, int64_t s0, int64_t s1,
+                            uint32_t hd, int tid, const Put &put) {
   auto at = [&](int64_t i, int sym) {
     const uint32_t rel = static_cast<uint32_t>(i - s0), r = rel / hd;
     put(r, rel - r * hd, static_cast<uint32_t>(sym));
   };
-  if (fixed_bits) {
-    for (int64_t i = s0 + tid; i < s1; i += kThreads) at(i, fixed_at(words, fixed_bits, i));
-    return;
-  }
-  // Huffman: one thread per code block intersecting [s0, s1); skip-decode up to s0 inside the first block
+  // Huffman (fixed-width pages go through decode_fixed_pair): one thread per code block intersecting [s0, s1); skip-decode up to s0 inside the first block
   const int64_t b0 = s0 / block, b1 = (s1 + block - 1) / block;
   for (int64_t b = b0 + tid; b < b1; b += kThreads) {
     int64_t pos = boff[b];
@@ -394,12 +414,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
             s_vs[t] = t < static_cast<int>(nt) ? pg.v_scales[t0 + t] : 0.0f;
           }
           const int64_t s0 = static_cast<int64_t>(t0) * phd, s1 = s0 + static_cast<int64_t>(nt) * phd;
-          decode_span(pg.k_words, pg.k_block_offsets, klut, pg.k_max_code_length, pg.fixed_code_length,
-                      pg.block_size, s0, s1, phd, tid,
-                      [&](uint32_t r, uint32_t c, uint32_t sym) { s_k[r * kKStride + c] = static_cast<uint8_t>(sym); });
-          decode_span(pg.v_words, pg.v_block_offsets, vlut, pg.v_max_code_length, pg.fixed_code_length,
-                      pg.block_size, s0, s1, phd, tid,
-                      [&](uint32_t r, uint32_t c, uint32_t sym) { s_vt[c * kVStride + r] = static_cast<uint8_t>(sym); });
+          const auto putk = [&](uint32_t r, uint32_t c, uint32_t sym) { s_k[r * kKStride + c] = static_cast<uint8_t>(sym); };
+          const auto putv = [&](uint32_t r, uint32_t c, uint32_t sym) { s_vt[c * kVStride + r] = static_cast<uint8_t>(sym); };
+          if (pg.fixed_code_length) {
+            decode_fixed_pair(pg.k_words, pg.v_words, pg.fixed_code_length, s0, s1, phd, tid, putk, putv);
+          } else {
+            decode_span(pg.k_words, pg.k_block_offsets, klut, pg.k_max_code_length, pg.block_size, s0, s1, phd, tid,
+                        putk);
+            decode_span(pg.v_words, pg.v_block_offsets, vlut, pg.v_max_code_length, pg.block_size, s0, s1, phd, tid,
+                        putv);
+          }
         }
         // dims the page does not have read as V = 0 (the query side zeroes K through s_ks)
         for (uint32_t i = tid; i < (HD > phd ? HD - phd : 0u) * kChunk; i += kThreads)
