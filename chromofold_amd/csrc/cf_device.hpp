@@ -115,4 +115,17 @@ __device__ __forceinline__ int nibble_width_sum(uint32_t x) {
 
 __device__ __forceinline__ int width_of(int k) { return static_cast<int>((kWidthNibbles >> (4 * k)) & 15u); }
 
+// a * b as f16 hi + lo (hi + lo = the product to about 21 bits), the MFMA operands of fp32-grade inputs.
+// hi comes from one explicit conversion (round toward zero) whose result is both stored and subtracted. Written as
+// (half)(a * b), the compiler may form the subtracted hi as v_fma_mix (one rounding of the exact product) and the
+// stored hi as v_cvt_pk_f16_f32 of the fp32 product (two roundings); they differ by an f16 ulp when the double
+// rounding crosses a tie, and hi + lo then misses the product by that ulp (measured: 2e-4 relative on a few
+// attention rows). Pragmas do not stop it: hipcc contracts with -ffp-contract=fast.
+__device__ __forceinline__ void split_mul_f16(float a, float b, _Float16 &hi, _Float16 &lo) {
+  const float x = a * b;
+  const _Float16 h = static_cast<_Float16>(__builtin_amdgcn_cvt_pkrtz(x, 0.0f)[0]);
+  hi = h;
+  lo = static_cast<_Float16>(x - static_cast<float>(h));
+}
+
 }  // namespace cfd

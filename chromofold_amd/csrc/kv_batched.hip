@@ -359,12 +359,10 @@ __global__ CF_KV_OCC __launch_bounds__(64 * W) void kv_batched_kernel(cf_kv_batc
   }
   for (int i = threadIdx.x; i < kGqa * D; i += kThreads) {
     const int h = i / D, dd = i % D;
-    float q = 0.0f;
-    if (static_cast<uint32_t>(h) < gqa)
-      q = d.queries[(static_cast<size_t>(seq) * d.query_head_count + head * gqa + h) * D + dd] * d.softmax_scale;
-    const _Float16 hi = static_cast<_Float16>(q);
-    s_q[0][h][dd] = hi;
-    s_q[1][h][dd] = static_cast<_Float16>(q - static_cast<float>(hi));
+    const float q = static_cast<uint32_t>(h) < gqa
+                        ? d.queries[(static_cast<size_t>(seq) * d.query_head_count + head * gqa + h) * D + dd]
+                        : 0.0f;
+    cfd::split_mul_f16(q, d.softmax_scale, s_q[0][h][dd], s_q[1][h][dd]);
   }
   __syncthreads();
 
@@ -660,10 +658,12 @@ __global__ __launch_bounds__(kPfxThreads) void kv_prefix_kernel(cf_kv_batched_de
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float q = row_ok ? d.queries[(static_cast<size_t>(rseq) * d.query_head_count + head * gqa + rh) * D +
-                                         32 * ks + 8 * kg + e] * d.softmax_scale
+                                         32 * ks + 8 * kg + e]
                              : 0.0f;
-      qh[ks][e] = static_cast<_Float16>(q);
-      ql[ks][e] = static_cast<_Float16>(q - static_cast<float>(qh[ks][e]));
+      _Float16 h, l;
+      cfd::split_mul_f16(q, d.softmax_scale, h, l);
+      qh[ks][e] = h;
+      ql[ks][e] = l;
     }
   const uint32_t vis = row_ok ? min(d.seq_tokens[rseq], d.query_pos[rseq] + 1) : 0u;
   // wave-wide: the fewest visible tokens over the valid rows (invalid rows are never written)

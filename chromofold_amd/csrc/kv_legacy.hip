@@ -22,8 +22,10 @@
 // Layout on gfx950. The query vectors of a KV head are its (query row, query head) pairs, vector v = row * gqa +
 // head. One 4-wavefront workgroup serves 64 vectors (16 per wavefront) of one KV head over one context split (the
 // head's pages taken round-robin by their order in the descriptor array; the dense tail in 64-token chunks after
-// them). Per page chunk of up to 64 tokens the workgroup decodes K and V once into LDS as integer symbols (K
-// token-major, V dim-major), then every wavefront runs its 16 vectors through:
+// them). Wave 0 lists the workgroup's pages, up to 64 per scan, with their fields (one memory latency per list, not
+// per page). Per page chunk of up to 64 tokens the workgroup decodes K and V once into LDS as integer symbols (K
+// token-major, V dim-major; a fixed-width chunk's words and scales were loaded during the previous chunk's
+// MFMAs), then every wavefront runs its 16 vectors through:
 //   QK^T  v_mfma_f32_16x16x16f16: A = the queries times the page's per-channel K scale, split into f16 hi + lo
 //         parts; B = K symbol - zero point, exact in f16. The scores are fp32-grade.
 //   softmax online per vector in fp32 (each vector's row of the 16x16 tile lives in 16 lanes);
@@ -55,6 +57,7 @@ constexpr int kVStride = kChunk + 4;                    // bytes per staged V ro
 constexpr int kPStride = kChunk + 4;                    // halves per P row
 constexpr int kLutMaxLen = 12;                          // Huffman LUTs of up to 2^12 entries are staged in LDS
 constexpr uint32_t kRansWords = CF_KV_RANS_MAX_GROUP_WORDS + 64;  // staged rANS words + slack for idle lanes' reads
+constexpr int kList = 64;                               // pages listed per round (one lane of wave 0 each)
 
 // canonical-Huffman LUT decode at bit `pos` (MSB-first), returns sym | len << 8
 __device__ __forceinline__ int huff_at(const uint32_t *__restrict__ words, const int32_t *__restrict__ lut, int maxlen,
@@ -65,37 +68,6 @@ __device__ __forceinline__ int huff_at(const uint32_t *__restrict__ words, const
   if (b + maxlen > 32) v |= words[wi + 1];
   const uint32_t look = static_cast<uint32_t>((v << b) >> (64 - maxlen));
   return lut[look];
-}
-
-// Fixed-width MSB-first codes (bits dividing 32, as the reference packer writes them) of symbols [s0, s1) of two
-// streams (K and V of a page) with the workgroup's threads: whole 32-bit words per thread, every load of both spans
-// issued before any symbol is used (one memory latency per page chunk instead of one per symbol and stream);
-// putk / putv(token, dim, sym) with the token relative to s0 / hd.
-template <typename PutK, typename PutV>
-__device__ void decode_fixed_pair(const uint32_t *__restrict__ kw, const uint32_t *__restrict__ vw, uint32_t bits,
-                                  int64_t s0, int64_t s1, uint32_t hd, int tid, const PutK &putk, const PutV &putv) {
-  const uint32_t spw = 32u / bits, mask = (1u << bits) - 1u;
-  const int64_t w0 = s0 / spw, w1 = (s1 + spw - 1) / spw;
-  for (int64_t wb = w0; wb < w1; wb += 2 * kThreads) {
-    const int64_t wa = wb + tid, wc = wa + kThreads;
-    const bool ha = wa < w1, hc = wc < w1;
-    const int64_t la = ha ? wa : w0, lc = hc ? wc : w0;  // clamped: loads issued unconditionally
-    const uint32_t ka = kw[la], kc = kw[lc], va = vw[la], vc = vw[lc];
-    for (uint32_t k = 0; k < spw; ++k) {
-      const uint32_t sh = 32u - bits * (k + 1);
-      const int64_t ia = wa * spw + k, ic = wc * spw + k;
-      if (ha && ia >= s0 && ia < s1) {
-        const uint32_t rel = static_cast<uint32_t>(ia - s0), r = rel / hd;
-        putk(r, rel - r * hd, (ka >> sh) & mask);
-        putv(r, rel - r * hd, (va >> sh) & mask);
-      }
-      if (hc && ic >= s0 && ic < s1) {
-        const uint32_t rel = static_cast<uint32_t>(ic - s0), r = rel / hd;
-        putk(r, rel - r * hd, (kc >> sh) & mask);
-        putv(r, rel - r * hd, (vc >> sh) & mask);
-      }
-    }
-  }
 }
 
 // Decode symbols [s0, s1) of one Huffman stream (rows of hd symbols) with the workgroup's threads; put(token, dim,
@@ -265,6 +237,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   __shared__ float s_ks[kMaxD];                  // K scale per channel of the staged page (rANS pages: 1)
   __shared__ float s_kt[kChunk], s_vs[kChunk];   // per token: K scale (legacy pages: 1) and V scale
   __shared__ int s_bad;
+  // this workgroup's current list of pages: fields {token_begin, token_count, head_dim, fixed bits | zero point << 8 |
+  // kind << 16}, word and scale pointers, descriptor index; count, more-to-come flag, pages of the head seen
+  __shared__ uint4 s_pmeta[kList];
+  __shared__ uint64_t s_pptr[kList][4];
+  __shared__ uint32_t s_pidx[kList];
+  __shared__ uint32_t s_pn, s_pmore, s_ord;
   static_assert(sizeof(s_lut) >= 2 * cfkv::kSlots * sizeof(uint2), "the rANS tables share the LUT area");
   static_assert(sizeof(s_lut) >= kVecs * kMaxD * sizeof(float), "the tail's queries share the LUT area");
 
@@ -308,10 +286,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     for (int kk = 0; kk < KS; ++kk)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float x = qraw[kk][j] * s_ks[16 * kk + 4 * (lane >> 4) + j];
-        const _Float16 h = static_cast<_Float16>(x);
+        _Float16 h, l;
+        cfd::split_mul_f16(qraw[kk][j], s_ks[16 * kk + 4 * (lane >> 4) + j], h, l);
         qhi[kk][j] = h;
-        qlo[kk][j] = static_cast<_Float16>(x - static_cast<float>(h));
+        qlo[kk][j] = l;
       }
   };
 
@@ -364,132 +342,305 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     }
   };
 
-  // ---- pages of this KV head, round-robin over the splits by their order in the descriptor array
-  uint32_t ord = 0;
-  for (uint32_t pb = 0; pb < d.page_count; pb += 64) {
-    const uint32_t pi = pb + lane;
-    uint64_t mine = __builtin_amdgcn_ballot_w64(pi < d.page_count && d.pages[pi].kv_head == kvh);
-    while (mine) {
-      const uint32_t p = pb + static_cast<uint32_t>(__builtin_ctzll(mine));
-      mine &= mine - 1;
-      if (ord++ % splits != split) continue;
-      const cf_kv_device_page pg = d.pages[p];
-      if (pg.token_count == 0) continue;
-      if (pg.token_begin > vis_hi || pg.token_begin + pg.token_count <= vis_lo) continue;
-      const bool rans = pg.fixed_code_length == 0 && pg.k_max_code_length == 0;
-      if (rans && (pg.token_count > static_cast<uint32_t>(kChunk) || pg.head_dim == 0 || pg.head_dim > kMaxD)) {
-        if (tid == 0) s_bad = 1;
-        continue;
+  // Scores, online softmax and P.V of the staged chunk: nt tokens from tok0, K in s_k, V in s_vt, scales in s_ks /
+  // s_kt / s_vs, symbols around the page's zero point (zbase = 1024 + zero point).
+  auto compute_chunk = [&](uint32_t tok0, uint32_t nt, _Float16 zbase) {
+    half4_t qhi[KS], qlo[KS];
+    build_q(qhi, qlo);
+    const int ntile = static_cast<int>((nt + 15) / 16);
+    // scores
+    float s[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float4_t c = {0, 0, 0, 0};
+      if (j < ntile) {
+        const uint8_t *krow = s_k + (16 * j + (lane & 15)) * kKStride + 4 * (lane >> 4);
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+          const half4_t b = sym4_to_half4(*reinterpret_cast<const uint32_t *>(krow + 16 * kk), zbase);
+          c = mfma16(qhi[kk], b, c);
+          c = mfma16(qlo[kk], b, c);
+        }
       }
-      if (!rans && (pg.head_dim == 0 || pg.head_dim > kMaxD)) continue;
-      const uint32_t phd = pg.head_dim;
-      const uint32_t zp = rans ? 128u : pg.zero_point;
-      const _Float16 zbase = static_cast<_Float16>(1024.0f + static_cast<float>(zp));
-      // Huffman pages: both LUTs in LDS when they fit (the lookups are the decoder's hot loop)
-      const int32_t *klut = pg.k_lut, *vlut = pg.v_lut;
-      if (!rans && !pg.fixed_code_length && pg.k_max_code_length <= kLutMaxLen && pg.v_max_code_length <= kLutMaxLen) {
-        __syncthreads();  // the previous chunk's readers of s_lut are done
-        for (uint32_t i = tid; i < (1u << pg.k_max_code_length); i += kThreads) s_lut[0][i] = pg.k_lut[i];
-        for (uint32_t i = tid; i < (1u << pg.v_max_code_length); i += kThreads) s_lut[1][i] = pg.v_lut[i];
-        klut = s_lut[0];
-        vlut = s_lut[1];
-      }
-      for (uint32_t t0 = 0; t0 < pg.token_count; t0 += kChunk) {
-        const uint32_t nt = min<uint32_t>(kChunk, pg.token_count - t0);
-        const uint32_t tok0 = pg.token_begin + t0;
-        __syncthreads();  // the previous chunk's compute no longer reads the staged tiles
-        for (uint32_t dd = tid; dd < kMaxD; dd += kThreads) s_ks[dd] = rans ? 1.0f : (dd < phd ? pg.k_scales[dd] : 0.0f);
-        if (rans) {
-          if (wave == 0) {
-            uint2(*tab)[cfkv::kSlots] = reinterpret_cast<uint2(*)[cfkv::kSlots]>(&s_lut[0][0]);
-            const bool ok = rans_group_to_lds(reinterpret_cast<const uint8_t *>(pg.k_words),
-                                              reinterpret_cast<const uint2 *>(pg.k_lut),
-                                              reinterpret_cast<const uint2 *>(pg.v_lut), tab, s_w, phd, nt, s_k, s_vt,
-                                              s_kt, s_vs, lane);
-            if (!ok && lane == 0) s_bad = 1;
-          }
-        } else {
-          for (int t = tid; t < kChunk; t += kThreads) {
-            s_kt[t] = 1.0f;
-            s_vs[t] = t < static_cast<int>(nt) ? pg.v_scales[t0 + t] : 0.0f;
-          }
-          const int64_t s0 = static_cast<int64_t>(t0) * phd, s1 = s0 + static_cast<int64_t>(nt) * phd;
-          const auto putk = [&](uint32_t r, uint32_t c, uint32_t sym) { s_k[r * kKStride + c] = static_cast<uint8_t>(sym); };
-          const auto putv = [&](uint32_t r, uint32_t c, uint32_t sym) { s_vt[c * kVStride + r] = static_cast<uint8_t>(sym); };
-          if (pg.fixed_code_length) {
-            decode_fixed_pair(pg.k_words, pg.v_words, pg.fixed_code_length, s0, s1, phd, tid, putk, putv);
-          } else {
-            decode_span(pg.k_words, pg.k_block_offsets, klut, pg.k_max_code_length, pg.block_size, s0, s1, phd, tid,
-                        putk);
-            decode_span(pg.v_words, pg.v_block_offsets, vlut, pg.v_max_code_length, pg.block_size, s0, s1, phd, tid,
-                        putv);
-          }
-        }
-        // dims the page does not have read as V = 0 (the query side zeroes K through s_ks)
-        for (uint32_t i = tid; i < (HD > phd ? HD - phd : 0u) * kChunk; i += kThreads)
-          s_vt[(phd + i / kChunk) * kVStride + i % kChunk] = static_cast<uint8_t>(zp);
-        __syncthreads();
-        if (s_bad) continue;
-        if (!wave_active) continue;
-        half4_t qhi[KS], qlo[KS];
-        build_q(qhi, qlo);
-        const int ntile = static_cast<int>((nt + 15) / 16);
-        // scores
-        float s[4][4];
+      const uint32_t tt = 16 * j + (lane & 15), tok = tok0 + tt;
+      const float kts = s_kt[tt];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float4_t c = {0, 0, 0, 0};
-          if (j < ntile) {
-            const uint8_t *krow = s_k + (16 * j + (lane & 15)) * kKStride + 4 * (lane >> 4);
-#pragma unroll
-            for (int kk = 0; kk < KS; ++kk) {
-              const half4_t b = sym4_to_half4(*reinterpret_cast<const uint32_t *>(krow + 16 * kk), zbase);
-              c = mfma16(qhi[kk], b, c);
-              c = mfma16(qlo[kk], b, c);
-            }
-          }
-          const uint32_t tt = 16 * j + (lane & 15), tok = tok0 + tt;
-          const float kts = s_kt[tt];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const bool vis = j < ntile && tt < nt && c_ok[i] && tok >= c_lo[i] && tok <= c_hi[i];
-            s[i][j] = vis ? c[i] * kts * scale : -INFINITY;
-          }
-        }
-        softmax_chunk(s);
-        // P (times the token's V scale) -> this wavefront's LDS tile as f16 hi + lo [vector][token]
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t tt = 16 * j + (lane & 15);
-          const float vsc = s_vs[tt];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float x = s[i][j] * vsc;
-            const _Float16 h = static_cast<_Float16>(x);
-            s_p[wave][0][4 * (lane >> 4) + i][tt] = h;
-            s_p[wave][1][4 * (lane >> 4) + i][tt] = static_cast<_Float16>(x - static_cast<float>(h));
-          }
-        }
-        wave_sync();
-        // P.V: acc[t] (vector rows, dims 16 t + lane % 16) += P[16 x tokens] V[tokens x 16]
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          if (ks >= ntile) break;
-          const half4_t ph = *reinterpret_cast<const half4_t *>(&s_p[wave][0][lane & 15][16 * ks + 4 * (lane >> 4)]);
-          const half4_t pl = *reinterpret_cast<const half4_t *>(&s_p[wave][1][lane & 15][16 * ks + 4 * (lane >> 4)]);
-#pragma unroll
-          for (int t = 0; t < KS; ++t) {
-            const uint32_t w = *reinterpret_cast<const uint32_t *>(s_vt + (16 * t + (lane & 15)) * kVStride + 16 * ks +
-                                                                   4 * (lane >> 4));
-            const half4_t b = sym4_to_half4(w, zbase);
-            acc[t] = mfma16(ph, b, acc[t]);
-            acc[t] = mfma16(pl, b, acc[t]);
-          }
-        }
-        wave_sync();
+      for (int i = 0; i < 4; ++i) {
+        const bool vis = j < ntile && tt < nt && c_ok[i] && tok >= c_lo[i] && tok <= c_hi[i];
+        s[i][j] = vis ? c[i] * kts * scale : -INFINITY;
       }
     }
+    softmax_chunk(s);
+    // P (times the token's V scale) -> this wavefront's LDS tile as f16 hi + lo [vector][token]
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t tt = 16 * j + (lane & 15);
+      const float vsc = s_vs[tt];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        cfd::split_mul_f16(s[i][j], vsc, s_p[wave][0][4 * (lane >> 4) + i][tt], s_p[wave][1][4 * (lane >> 4) + i][tt]);
+      }
+    }
+    wave_sync();
+    // P.V: acc[t] (vector rows, dims 16 t + lane % 16) += P[16 x tokens] V[tokens x 16]
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (ks >= ntile) break;
+      const half4_t ph = *reinterpret_cast<const half4_t *>(&s_p[wave][0][lane & 15][16 * ks + 4 * (lane >> 4)]);
+      const half4_t pl = *reinterpret_cast<const half4_t *>(&s_p[wave][1][lane & 15][16 * ks + 4 * (lane >> 4)]);
+#pragma unroll
+      for (int t = 0; t < KS; ++t) {
+        const uint32_t w = *reinterpret_cast<const uint32_t *>(s_vt + (16 * t + (lane & 15)) * kVStride + 16 * ks +
+                                                               4 * (lane >> 4));
+        const half4_t b = sym4_to_half4(w, zbase);
+        acc[t] = mfma16(ph, b, acc[t]);
+        acc[t] = mfma16(pl, b, acc[t]);
+      }
+    }
+    wave_sync();
+  };
+
+  // ---- pages of this KV head, round-robin over the splits by their order in the descriptor array.
+  // Wave 0 lists this workgroup's pages, up to kList at a time, with the fields the fixed-width path needs (one
+  // lane per listed page: one memory latency per list instead of one per page). The listed pages' chunks then run
+  // in order; for fixed-width pages the next chunk's words and scales load while the current chunk computes, so a
+  // chunk waits for memory only when the previous one was not fixed-width.
+  uint32_t scan_pb = 0, scan_ord = 0;  // wave 0: next descriptor to examine, ordinal of the head's next page there
+  for (;;) {
+    if (wave == 0) {
+      // pass 1: which descriptors are this workgroup's (kv head, ordinal % splits), 256 descriptors per step with
+      // their loads in flight together, selection and compaction lane-parallel
+      uint32_t cnt = 0;
+      bool full = false;
+      while (!full && scan_pb < d.page_count) {
+        uint32_t hv[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t pi = scan_pb + 64 * q + lane;
+          hv[q] = pi < d.page_count ? d.pages[pi].kv_head : 0xFFFFFFFFu;
+        }
+        uint32_t ord_run = scan_ord;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (full) break;
+          const uint32_t pi = scan_pb + 64 * q + lane;
+          const bool match = hv[q] == kvh && pi < d.page_count;
+          const uint64_t m = __builtin_amdgcn_ballot_w64(match);
+          const uint32_t ordl = ord_run + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u));
+          const bool sel = match && ordl % splits == split;
+          const uint64_t ms = __builtin_amdgcn_ballot_w64(sel);
+          const uint32_t rk = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(ms >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(ms), 0u));
+          const uint32_t nsel = static_cast<uint32_t>(__builtin_popcountll(ms));
+          if (cnt + nsel > static_cast<uint32_t>(kList)) {
+            // the list is full inside this batch: take the first pages, resume at the first one not taken
+            const uint32_t take = static_cast<uint32_t>(kList) - cnt;
+            if (sel && rk < take) s_pidx[cnt + rk] = pi;
+            const uint64_t mr = __builtin_amdgcn_ballot_w64(sel && rk == take);
+            const int lr = __builtin_ctzll(mr);
+            scan_pb = __builtin_amdgcn_readlane(pi, lr);
+            scan_ord = __builtin_amdgcn_readlane(ordl, lr);
+            cnt = kList;
+            full = true;
+            break;
+          }
+          if (sel) s_pidx[cnt + rk] = pi;
+          cnt += nsel;
+          ord_run += static_cast<uint32_t>(__builtin_popcountll(m));
+        }
+        if (!full) {
+          scan_pb += 256;
+          scan_ord = ord_run;
+        }
+      }
+      wave_sync();
+      const uint32_t my_p = static_cast<uint32_t>(lane) < cnt ? s_pidx[lane] : 0u;
+      wave_sync();
+      // the listed pages' fields, one lane each; empty pages and pages wholly outside the workgroup's visible
+      // range are dropped, the others compacted in order
+      bool keep = false;
+      uint4 meta = make_uint4(0, 0, 0, 0);
+      const cf_kv_device_page *pg = d.pages + my_p;
+      if (static_cast<uint32_t>(lane) < cnt) {
+        const uint32_t tb = pg->token_begin, tc = pg->token_count, fixed = pg->fixed_code_length;
+        keep = tc != 0 && !(tb > vis_hi || tb + tc <= vis_lo);
+        const uint32_t kind = fixed ? 0u : (pg->k_max_code_length == 0 ? 2u : 1u);  // fixed / Huffman / rANS
+        meta = make_uint4(tb, tc, pg->head_dim, (fixed & 0xFFu) | ((pg->zero_point & 0xFFu) << 8) | (kind << 16));
+      }
+      const uint64_t km = __builtin_amdgcn_ballot_w64(keep);
+      const uint32_t at = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(km >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(km), 0u));
+      if (keep) {
+        s_pmeta[at] = meta;
+        s_pptr[at][0] = reinterpret_cast<uintptr_t>(pg->k_words);
+        s_pptr[at][1] = reinterpret_cast<uintptr_t>(pg->v_words);
+        s_pptr[at][2] = reinterpret_cast<uintptr_t>(pg->k_scales);
+        s_pptr[at][3] = reinterpret_cast<uintptr_t>(pg->v_scales);
+        s_pidx[at] = my_p;
+      }
+      if (lane == 0) {
+        s_pn = static_cast<uint32_t>(__builtin_popcountll(km));
+        s_pmore = full ? 1u : 0u;
+        s_ord = scan_ord;
+      }
+    }
+    __syncthreads();
+    const uint32_t n = __builtin_amdgcn_readfirstlane(s_pn);
+    const bool more = __builtin_amdgcn_readfirstlane(s_pmore) != 0;
+
+    // prefetch of a fixed-width chunk (li, t0): the first 2 * kThreads words of K and of V, the thread's K scale
+    // (channel tid) and V scale (token t0 + tid)
+    struct Pre {
+      uint32_t ka, kc, va, vc;
+      float ks, vs;
+    };
+    auto prefetch = [&](uint32_t li, uint32_t t0) {
+      Pre r{0u, 0u, 0u, 0u, 0.0f, 0.0f};
+      if (li >= n) return r;
+      const uint4 mt = s_pmeta[li];
+      if ((mt.w >> 16) != 0) return r;  // not fixed-width
+      const uint32_t bits = mt.w & 0xFFu, phd = mt.z, nt = min<uint32_t>(kChunk, mt.y - t0);
+      if (bits == 0 || phd == 0 || phd > kMaxD) return r;
+      const uint32_t *kw = reinterpret_cast<const uint32_t *>(s_pptr[li][0]);
+      const uint32_t *vw = reinterpret_cast<const uint32_t *>(s_pptr[li][1]);
+      const float *ksc = reinterpret_cast<const float *>(s_pptr[li][2]);
+      const float *vsc = reinterpret_cast<const float *>(s_pptr[li][3]);
+      const uint32_t spw = 32u / bits;
+      const int64_t s0 = static_cast<int64_t>(t0) * phd, s1 = s0 + static_cast<int64_t>(nt) * phd;
+      const int64_t w0 = s0 / spw, w1 = (s1 + spw - 1) / spw;
+      const int64_t wa = min<int64_t>(w0 + tid, w1 - 1), wc = min<int64_t>(w0 + tid + kThreads, w1 - 1);
+      r.ka = kw[wa];
+      r.kc = kw[wc];
+      r.va = vw[wa];
+      r.vc = vw[wc];
+      r.ks = ksc[min<uint32_t>(static_cast<uint32_t>(tid), phd - 1)];
+      r.vs = vsc[t0 + min<uint32_t>(static_cast<uint32_t>(tid), nt - 1)];
+      return r;
+    };
+
+    uint32_t li = 0, t0 = 0;
+    Pre cur = prefetch(0, 0);
+    while (li < n) {
+      const uint4 mt = s_pmeta[li];
+      const uint32_t tb = __builtin_amdgcn_readfirstlane(mt.x), tc = __builtin_amdgcn_readfirstlane(mt.y);
+      const uint32_t phd = __builtin_amdgcn_readfirstlane(mt.z), mw = __builtin_amdgcn_readfirstlane(mt.w);
+      const uint32_t kind = mw >> 16;
+      if (kind != 0) {
+        // Huffman and rANS pages: staged at their turn (no prefetch), every chunk of the page; a page this kernel
+        // cannot stage leaves the do-while early
+        do {
+        const cf_kv_device_page pg = d.pages[__builtin_amdgcn_readfirstlane(s_pidx[li])];
+        const bool rans = pg.fixed_code_length == 0 && pg.k_max_code_length == 0;
+        if (rans && (pg.token_count > static_cast<uint32_t>(kChunk) || pg.head_dim == 0 || pg.head_dim > kMaxD)) {
+          if (tid == 0) s_bad = 1;
+          continue;
+        }
+        if (!rans && (pg.head_dim == 0 || pg.head_dim > kMaxD)) continue;
+        const uint32_t phd = pg.head_dim;
+        const uint32_t zp = rans ? 128u : pg.zero_point;
+        const _Float16 zbase = static_cast<_Float16>(1024.0f + static_cast<float>(zp));
+        // Huffman pages: both LUTs in LDS when they fit (the lookups are the decoder's hot loop)
+        const int32_t *klut = pg.k_lut, *vlut = pg.v_lut;
+        if (!rans && !pg.fixed_code_length && pg.k_max_code_length <= kLutMaxLen && pg.v_max_code_length <= kLutMaxLen) {
+          __syncthreads();  // the previous chunk's readers of s_lut are done
+          for (uint32_t i = tid; i < (1u << pg.k_max_code_length); i += kThreads) s_lut[0][i] = pg.k_lut[i];
+          for (uint32_t i = tid; i < (1u << pg.v_max_code_length); i += kThreads) s_lut[1][i] = pg.v_lut[i];
+          klut = s_lut[0];
+          vlut = s_lut[1];
+        }
+        for (uint32_t t0 = 0; t0 < pg.token_count; t0 += kChunk) {
+          const uint32_t nt = min<uint32_t>(kChunk, pg.token_count - t0);
+          const uint32_t tok0 = pg.token_begin + t0;
+          __syncthreads();  // the previous chunk's compute no longer reads the staged tiles
+          for (uint32_t dd = tid; dd < kMaxD; dd += kThreads) s_ks[dd] = rans ? 1.0f : (dd < phd ? pg.k_scales[dd] : 0.0f);
+          if (rans) {
+            if (wave == 0) {
+              uint2(*tab)[cfkv::kSlots] = reinterpret_cast<uint2(*)[cfkv::kSlots]>(&s_lut[0][0]);
+              const bool ok = rans_group_to_lds(reinterpret_cast<const uint8_t *>(pg.k_words),
+                                                reinterpret_cast<const uint2 *>(pg.k_lut),
+                                                reinterpret_cast<const uint2 *>(pg.v_lut), tab, s_w, phd, nt, s_k, s_vt,
+                                                s_kt, s_vs, lane);
+              if (!ok && lane == 0) s_bad = 1;
+            }
+          } else {
+            for (int t = tid; t < kChunk; t += kThreads) {
+              s_kt[t] = 1.0f;
+              s_vs[t] = t < static_cast<int>(nt) ? pg.v_scales[t0 + t] : 0.0f;
+            }
+            const int64_t s0 = static_cast<int64_t>(t0) * phd, s1 = s0 + static_cast<int64_t>(nt) * phd;
+            decode_span(pg.k_words, pg.k_block_offsets, klut, pg.k_max_code_length, pg.block_size, s0, s1, phd, tid,
+                        [&](uint32_t r, uint32_t c, uint32_t sym) { s_k[r * kKStride + c] = static_cast<uint8_t>(sym); });
+            decode_span(pg.v_words, pg.v_block_offsets, vlut, pg.v_max_code_length, pg.block_size, s0, s1, phd, tid,
+                        [&](uint32_t r, uint32_t c, uint32_t sym) { s_vt[c * kVStride + r] = static_cast<uint8_t>(sym); });
+          }
+          // dims the page does not have read as V = 0 (the query side zeroes K through s_ks)
+          for (uint32_t i = tid; i < (HD > phd ? HD - phd : 0u) * kChunk; i += kThreads)
+            s_vt[(phd + i / kChunk) * kVStride + i % kChunk] = static_cast<uint8_t>(zp);
+          __syncthreads();
+          if (!s_bad && wave_active) compute_chunk(tok0, nt, zbase);
+        }
+        } while (false);
+        ++li;
+        t0 = 0;
+        cur = prefetch(li, 0);
+        continue;
+      }
+      // fixed-width chunk (li, t0)
+      const uint32_t bits = mw & 0xFFu, zp = (mw >> 8) & 0xFFu;
+      if (phd == 0 || phd > kMaxD) {  // not a page this kernel can stage: skipped
+        ++li;
+        t0 = 0;
+        cur = prefetch(li, 0);
+        continue;
+      }
+      const uint32_t nt = min<uint32_t>(kChunk, tc - t0), tok0 = tb + t0;
+      uint32_t li2 = li, t02 = t0 + kChunk;
+      if (t02 >= tc) {
+        li2 = li + 1;
+        t02 = 0;
+      }
+      const _Float16 zbase = static_cast<_Float16>(1024.0f + static_cast<float>(zp));
+      __syncthreads();  // the previous chunk's compute no longer reads the staged tiles
+      if (static_cast<uint32_t>(tid) < kMaxD) s_ks[tid] = static_cast<uint32_t>(tid) < phd ? cur.ks : 0.0f;
+      if (tid < kChunk) {
+        s_kt[tid] = 1.0f;
+        s_vs[tid] = static_cast<uint32_t>(tid) < nt ? cur.vs : 0.0f;
+      }
+      {
+        const uint32_t spw = 32u / bits, mask = (1u << bits) - 1u;
+        const int64_t s0 = static_cast<int64_t>(t0) * phd, s1 = s0 + static_cast<int64_t>(nt) * phd;
+        const int64_t w0 = s0 / spw, w1 = (s1 + spw - 1) / spw;
+        auto put = [&](int64_t w, uint32_t kword, uint32_t vword) {
+          for (uint32_t k = 0; k < spw; ++k) {
+            const int64_t i = w * spw + k;
+            if (i < s0 || i >= s1) continue;
+            const uint32_t sh = 32u - bits * (k + 1), rel = static_cast<uint32_t>(i - s0), r = rel / phd, c = rel - r * phd;
+            s_k[r * kKStride + c] = static_cast<uint8_t>((kword >> sh) & mask);
+            s_vt[c * kVStride + r] = static_cast<uint8_t>((vword >> sh) & mask);
+          }
+        };
+        if (w0 + tid < w1) put(w0 + tid, cur.ka, cur.va);
+        if (w0 + tid + kThreads < w1) put(w0 + tid + kThreads, cur.kc, cur.vc);
+        // words past the prefetched 2 * kThreads (chunks of more than 2 KiB per stream) are loaded here
+        const uint32_t *kw = reinterpret_cast<const uint32_t *>(s_pptr[li][0]);
+        const uint32_t *vw = reinterpret_cast<const uint32_t *>(s_pptr[li][1]);
+        for (int64_t w = w0 + 2 * kThreads + tid; w < w1; w += kThreads) put(w, kw[w], vw[w]);
+      }
+      // dims the page does not have read as V = 0 (the query side zeroes K through s_ks)
+      for (uint32_t i = tid; i < (HD > phd ? HD - phd : 0u) * kChunk; i += kThreads)
+        s_vt[(phd + i / kChunk) * kVStride + i % kChunk] = static_cast<uint8_t>(zp);
+      const Pre nxt = prefetch(li2, t02);  // in flight during this chunk's compute
+      __syncthreads();
+      if (!s_bad && wave_active) compute_chunk(tok0, nt, zbase);
+      cur = nxt;
+      li = li2;
+      t0 = t02;
+    }
+    if (!more) break;
+    __syncthreads();  // the list is rewritten by the next round
   }
+  const uint32_t ord = __builtin_amdgcn_readfirstlane(s_ord);
 
   // ---- dense fp32 tail [active_token_count, kv_head_count, head_dim], 64-token chunks continuing the round-robin
   if (d.active_token_count) {
@@ -504,8 +655,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     wave_sync();
     float *s_pf = reinterpret_cast<float *>(&s_p[wave][0][0][0]);  // p [vector][token] in fp32 (same bytes)
     static_assert(sizeof(s_p[0]) >= 16 * kChunk * sizeof(float), "fp32 tail weights share the P tile");
+    uint32_t tord = ord;
     for (uint32_t t0 = 0; t0 < d.active_token_count; t0 += kChunk) {
-      if (ord++ % splits != split) continue;
+      if (tord++ % splits != split) continue;
       if (!wave_active) continue;
       const uint32_t nt = min<uint32_t>(kChunk, d.active_token_count - t0);
       const uint32_t tok0 = d.active_token_begin + t0;

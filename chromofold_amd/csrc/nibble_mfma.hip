@@ -27,6 +27,7 @@
 #include <cstdint>
 #include <utility>
 
+#include "cf_device.hpp"
 #include "nibble_kv.hpp"
 
 namespace cfnib {
@@ -134,11 +135,8 @@ __global__ __launch_bounds__(256) void nib_mfma_kernel(const AttnItem *__restric
     float q = 0.0f;
     if (qc * 4 + j < gqa)
       q = load_q(it.q, it.q_type, uint64_t(qt) * it.q_token_stride + uint64_t(h * gqa + qc * 4 + j) * it.q_head_stride +
-                                       uint64_t(dd) * it.q_elem_stride) *
-          it.scale_log2;
-    const _Float16 hi = static_cast<_Float16>(q);
-    s_q[0][j][dd] = hi;
-    s_q[1][j][dd] = static_cast<_Float16>(q - static_cast<float>(hi));
+                                       uint64_t(dd) * it.q_elem_stride);
+    cfd::split_mul_f16(q, it.scale_log2, s_q[0][j][dd], s_q[1][j][dd]);
   }
   __syncthreads();
   half4_t qhi[2], qlo[2];
@@ -335,13 +333,14 @@ __global__ __launch_bounds__(256) void nib_mfma_kernel(const AttnItem *__restric
       for (int tq = 0; tq < 4; ++tq) {
         const int slot = 16 * G + 4 * tq;
         const float4 pp = *reinterpret_cast<const float4 *>(&s_p[wave][lane & 3][slot]);
-        const float pv[4] = {pp.x * s_vs[wave][slot][vset], pp.y * s_vs[wave][slot + 1][vset],
-                             pp.z * s_vs[wave][slot + 2][vset], pp.w * s_vs[wave][slot + 3][vset]};
+        const float pk[4] = {pp.x, pp.y, pp.z, pp.w};
         half4_t a, al;  // p * v_scale as f16 hi + lo (fp32-grade weights, like the query operand)
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          a[k] = static_cast<_Float16>(pv[k]);
-          al[k] = static_cast<_Float16>(pv[k] - static_cast<float>(a[k]));
+          _Float16 h, l;
+          cfd::split_mul_f16(pk[k], s_vs[wave][slot + k][vset], h, l);
+          a[k] = h;
+          al[k] = l;
         }
         uint32_t wk[4];
 #pragma unroll

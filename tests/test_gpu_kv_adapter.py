@@ -136,3 +136,37 @@ def test_many_pages_arena_growth_and_misaligned_tails(dev):
         a.attention(1, dq.data_ptr(), out.data_ptr(), 1, kvh * gqa, gqa, N, 1.0 / np.sqrt(hd))
     with pytest.raises(Lm.CfAdapterError, match="invalid ChromoFold attention request"):
         a.attention(1, dq.data_ptr(), out.data_ptr(), 1, 7, 2, N, 1.0)
+
+
+@pytest.mark.parametrize("kvh,gqa,qn,N,hd,bits", [(1, 7, 32, 32, 64, 4), (2, 7, 64, 1024, 64, 4),
+                                                  (2, 7, 64, 1024, 128, 8)])
+def test_attention_fp32_grade(dev, kvh, gqa, qn, N, hd, bits):
+    """Many query rows (causal, one query token per row) over whole sealed pages. The seam's MFMA operands are f16
+    hi + lo splits of fp32 values (queries x K scale, P x V scale) with fp32 accumulation, so on the stored values
+    it lands within fp32 rounding of the fp64 oracle: max abs error <= 2e-6 for N(0,1) inputs (measured <= 6e-7).
+    A split whose hi and lo come from differently rounded products misses by an f16 ulp on a few rows (measured
+    6.5e-5 on the first case), which this bar catches and the reference's 2e-4 does not."""
+    import torch
+    page, qh = 32, kvh * gqa
+    rng = np.random.default_rng(4242 + N + hd)
+    K = [rng.standard_normal((N, hd)).astype(np.float32) for _ in range(kvh)]
+    V = [rng.standard_normal((N, hd)).astype(np.float32) for _ in range(kvh)]
+    Q = rng.standard_normal((qn, qh, hd)).astype(np.float32)
+    a = _adapter(kvh, qh, hd, page, gqa, bits)
+    for h in range(kvh):
+        a.append(0, h, 0, K[h], V[h])
+    assert a.stats().active_tokens == 0
+    dq = torch.from_numpy(Q).to(dev)
+    out = torch.full_like(dq, float("nan"))
+    a.attention(0, dq.data_ptr(), out.data_ptr(), qn, qh, gqa, N - qn, 1.0 / np.sqrt(hd))
+    torch.cuda.synchronize()
+    pages = []
+    for h in range(kvh):
+        for tb in range(0, N, page):
+            _, _, _, _, kd, vd = O.kv_fixture_quantize(K[h][tb:tb + page], V[h][tb:tb + page], bits)
+            pages.append((h, tb, kd, vd))
+    exp = np.stack([O.paged_attention_f64(Q[r], qh, kvh, hd, gqa, N - qn + r, 0, 1.0 / np.sqrt(hd), pages)[0]
+                    for r in range(qn)])
+    err = np.abs(out.cpu().numpy() - exp).max()
+    assert err <= 2e-6, err
+    a.close()
