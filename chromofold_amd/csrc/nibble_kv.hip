@@ -11,7 +11,9 @@
 //   The attention replaces the reference's one-block-per-(head, token) kernels (device_kv_seal_attention.cu:
 //   126-194, multisequence_cuda_resolver.cu:136-195) with the same arithmetic contract: key position p is used by
 //   query position P when p <= P and, with window w > 0, p + w > P; softmax with a running maximum; empty rows
-//   produce 0.
+//   produce 0. Requests flagged for the batched-items contract (reference src/cuda/production_attention.cu:59-139)
+//   instead read two's-complement nibbles (each loaded word xor 0x88888888 gives the offset-8 form), count scale
+//   blocks per (token, KV head) row, skip pages with a NULL pointer, and use p unless w > 0 and p + w < P.
 //
 // Attention layout: a workgroup takes `hw` KV heads x LG lanes; each lane owns 8 consecutive dims (one 32-bit word
 // of nibbles) of one KV head for G query heads of that head's group, and walks the split's tokens. A token's
@@ -237,8 +239,15 @@ __device__ inline void consume(RowState<G> &st, const float (&qv)[G][8], const f
   }
 }
 
-__device__ inline bool key_visible(uint32_t pos, uint32_t qpos, uint32_t window) {
-  return pos <= qpos && (window == 0u || uint64_t(pos) + window > qpos);
+// Visible positions [lo, hi] of query position qpos: p <= q and, with a window, p + window > q; with kOpenWindow
+// every p except those with window > 0 and p + window < q.
+struct Visible {
+  uint32_t lo, hi;
+  __device__ bool operator()(uint32_t pos) const { return pos >= lo && pos <= hi; }
+};
+__device__ inline Visible visible_range(uint32_t qpos, uint32_t window, uint32_t flags) {
+  if (flags & kOpenWindow) return {window != 0u && qpos >= window ? qpos - window : 0u, 0xFFFFFFFFu};
+  return {window != 0u && qpos >= window ? qpos - window + 1u : 0u, qpos};
 }
 
 template <int LG, int G>
@@ -261,7 +270,9 @@ __global__ __launch_bounds__(256) void nib_attn_kernel(const AttnItem *__restric
   const uint32_t j0 = qc * G;
   const uint32_t qpos = it.q_begin + qt;
   const float scale_log2 = it.scale_log2;
-  const uint32_t window = it.window;
+  const uint32_t flags = it.flags;
+  const Visible key_visible = visible_range(qpos, it.window, flags);
+  const uint32_t sx = (flags & kSignedNibbles) ? 0x88888888u : 0u;  // n ^ 8 - 8 is the two's-complement value
 
   float qv[G][8], qsum[G];
 #pragma unroll
@@ -298,7 +309,10 @@ __global__ __launch_bounds__(256) void nib_attn_kernel(const AttnItem *__restric
       const uint32_t *vw = reinterpret_cast<const uint32_t *>(pg.value_payload);
       const float *ksc = pg.key_scales;
       const float *vsc = pg.value_scales;
-      if ((bs & 7u) == 0u) {
+      if (!kw || !vw || !ksc || !vsc || bs == 0u) continue;
+      const bool row_blocks = (flags & kRowBlocks) != 0u;
+      const uint32_t bpr = row_blocks ? (pg.head_dim + bs - 1u) / bs : 0u;  // blocks per (token, KV head) row
+      if ((bs & 7u) == 0u && (!row_blocks || (pg.head_dim == D && D % bs == 0u))) {  // flat index / bs is the block
         const uint32_t bw = bs / 8u;  // words per block
         for (uint32_t t0 = 0; t0 < tcount; t0 += 4u) {
           uint32_t kwv[4], vwv[4];
@@ -309,8 +323,8 @@ __global__ __launch_bounds__(256) void nib_attn_kernel(const AttnItem *__restric
             const bool ok = lane_ok && tok < tcount;
             const uint32_t wi = tok * words_per_token + lane_word;
             const uint32_t blk = wi / bw;
-            kwv[u] = ok ? kw[wi] : 0x88888888u;
-            vwv[u] = ok ? vw[wi] : 0x88888888u;
+            kwv[u] = ok ? kw[wi] ^ sx : 0x88888888u;
+            vwv[u] = ok ? vw[wi] ^ sx : 0x88888888u;
             kss[u] = ok ? ksc[blk] : 0.0f;
             vss[u] = ok ? vsc[blk] : 0.0f;
           }
@@ -321,25 +335,23 @@ __global__ __launch_bounds__(256) void nib_attn_kernel(const AttnItem *__restric
             float kf[8], vf[8];
             unpack_word(kwv[u], kf);
             unpack_word(vwv[u], vf);
-            consume<LG, G>(st, qv, qsum, kf, kss[u], 8.0f, vf, vss[u], 8.0f, key_visible(tbegin + tok, qpos, window),
-                           scale_log2);
+            consume<LG, G>(st, qv, qsum, kf, kss[u], 8.0f, vf, vss[u], 8.0f, key_visible(tbegin + tok), scale_log2);
           }
         }
-      } else {  // block boundaries inside a word: dequantise value by value
+      } else {  // block boundaries inside a word, or per-row blocks: dequantise value by value
         for (uint32_t tok = 0; tok < tcount; ++tok) {
           const uint32_t wi = tok * words_per_token + lane_word;
           float kf[8], vf[8], kraw[8], vraw[8];
-          unpack_word(lane_ok ? kw[wi] : 0x88888888u, kraw);
-          unpack_word(lane_ok ? vw[wi] : 0x88888888u, vraw);
+          unpack_word(lane_ok ? kw[wi] ^ sx : 0x88888888u, kraw);
+          unpack_word(lane_ok ? vw[wi] ^ sx : 0x88888888u, vraw);
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const uint32_t blk = (wi * 8u + e) / bs;
+            const uint32_t blk = row_blocks ? (tok * kvh + h) * bpr + (8u * c + e) / bs : (wi * 8u + e) / bs;
             const int pos = nib_pos(e);
             kf[pos] = (kraw[pos] - 8.0f) * (lane_ok ? ksc[blk] : 0.0f);
             vf[pos] = (vraw[pos] - 8.0f) * (lane_ok ? vsc[blk] : 0.0f);
           }
-          consume<LG, G>(st, qv, qsum, kf, 1.0f, 0.0f, vf, 1.0f, 0.0f, key_visible(tbegin + tok, qpos, window),
-                         scale_log2);
+          consume<LG, G>(st, qv, qsum, kf, 1.0f, 0.0f, vf, 1.0f, 0.0f, key_visible(tbegin + tok), scale_log2);
         }
       }
     }
@@ -359,8 +371,7 @@ __global__ __launch_bounds__(256) void nib_attn_kernel(const AttnItem *__restric
 #pragma unroll
         for (int e = 0; e < 8; ++e) kf[e] = vf[e] = 0.0f;
       }
-      consume<LG, G>(st, qv, qsum, kf, 1.0f, 0.0f, vf, 1.0f, 0.0f, key_visible(it.active_begin + tok, qpos, window),
-                     scale_log2);
+      consume<LG, G>(st, qv, qsum, kf, 1.0f, 0.0f, vf, 1.0f, 0.0f, key_visible(it.active_begin + tok), scale_log2);
     }
   }
 
@@ -493,7 +504,7 @@ hipError_t AttnRunner::run(const std::vector<AttnRequest> &reqs, const AttnShape
   std::vector<uint32_t> nb(reqs.size());
   for (size_t i = 0; i < reqs.size(); ++i) {
     const auto &r = reqs[i];
-    nb[i] = mfma_sets(D, r.block_size);
+    nb[i] = r.flags ? 0u : mfma_sets(D, r.block_size);
     if (nb[i]) tile_work += uint64_t((r.page_count * cpp + 3u) / 4u) * r.query.token_count * ((sh.gqa + 3u) / 4u);
     else page_work += uint64_t(r.page_count) * r.query.token_count * hgroups * qchunks;
   }
@@ -540,7 +551,7 @@ hipError_t AttnRunner::run(const std::vector<AttnRequest> &reqs, const AttnShape
     it.q_begin = r.query_begin;
     it.window = r.window;
     it.scale_log2 = r.softmax_scale * 1.4426950408889634f;
-    it.pad = 0;
+    it.flags = r.flags;
     it.nsplit = it.page_splits + (it.active_count > 0u ? 1u : 0u);
     if (it.nsplit == 0u) it.nsplit = 1u;  // nothing visible: one empty split, the row comes out 0
     it.ws_offset = floats;

@@ -38,6 +38,15 @@ hipError_t launch_convert(const cf_device_tensor_view &src, float *dst, uint32_t
 // Clears `count` SealStatus records with a kernel (safe under graph capture).
 hipError_t launch_clear_status(SealStatus *status, uint32_t count, hipStream_t stream);
 
+// Request flags (AttnRequest::flags, AttnItem::flags); 0 = the sealed-page format and causal visibility above.
+// A flagged request always runs on the VALU kernel.
+constexpr uint32_t kSignedNibbles = 1u;  // payload nibbles are two's-complement int4 (n - 16 for n >= 8)
+constexpr uint32_t kOpenWindow = 2u;     // position p visible unless window > 0 and p + window < query position
+                                         // (no causal bound; default: p <= q and, with a window, p + window > q)
+constexpr uint32_t kRowBlocks = 4u;      // scale blocks counted per (token, KV head) row of ceil(page head_dim /
+                                         // block_size) blocks (default: blocks over the page's flat value index);
+                                         // pages with a NULL payload / scale pointer or block_size 0 are skipped
+
 // One attention request as the kernel reads it (built on the host, uploaded as a table).
 struct AttnItem {
   const void *q;
@@ -56,7 +65,7 @@ struct AttnItem {
   uint32_t active_begin, active_count;
   uint32_t q_begin, window;
   float scale_log2;  // softmax_scale * log2(e)
-  uint32_t pad;
+  uint32_t flags;
   uint64_t ws_offset;  // float offset of the item's split partials
 };
 
@@ -90,6 +99,7 @@ struct AttnRequest {
   uint32_t query_begin, window;
   float softmax_scale;
   uint32_t block_size;  // the block size of every page of the request, 0 when mixed or unknown
+  uint32_t flags;       // kSignedNibbles | kOpenWindow | kRowBlocks
 };
 
 // Runs a batch of requests: one split-context attention launch over every item, then one merge launch.

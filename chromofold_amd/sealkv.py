@@ -1,9 +1,10 @@
-"""Host mirror of the device seal engine, the device KV dataplane and the multi-sequence resolver.
+"""Host mirror of the device seal engine, the device KV dataplane, the multi-sequence resolver and the batched
+attention runtime.
 
 ctypes structs and thin classes over libchromofold.so for include/chromofold/device_kv_dataplane.h,
-device_kv_seal_attention.h and multisequence_cuda_resolver.h (the reference's headers of the same names:
-reference include/chromofold/device_kv_dataplane.h:11-89, device_kv_seal_attention.h:11-121,
-multisequence_cuda_resolver.h:12-93). Functions of those APIs return 0 / -1; the classes raise SealError with the
+device_kv_seal_attention.h, multisequence_cuda_resolver.h and production_attention.h (the reference's headers of
+the same names: reference include/chromofold/device_kv_dataplane.h:11-89, device_kv_seal_attention.h:11-121,
+multisequence_cuda_resolver.h:12-93, production_attention.h:11-105). Functions of those APIs return 0 / -1; the classes raise SealError with the
 library's last-error message on -1. Device tensors are torch tensors on the GPU; no host fallback exists.
 """
 from __future__ import annotations
@@ -100,6 +101,38 @@ class cf_ms_cuda_counters(C.Structure):
         "dense_fallback_launches", "cuda_errors")]
 
 
+CF_ATTENTION_REFERENCE, CF_ATTENTION_OPTIMIZED = 0, 1
+
+
+class cf_attention_tuning(C.Structure):
+    _fields_ = [(k, U32) for k in ("threads_per_block", "warps_per_block", "heads_per_block", "pages_per_work_unit",
+                                   "vector_width", "enable_cuda_graphs", "enable_async_sealing")]
+
+
+class cf_attention_runtime_config(C.Structure):
+    _fields_ = [(k, U32) for k in ("layer_count", "query_head_count", "kv_head_count", "head_dim", "page_size",
+                                   "block_size", "gqa_group_size", "cuda_device", "use_async_allocator")] + \
+               [("mode", C.c_int), ("tuning", cf_attention_tuning)]
+
+
+class cf_attention_batch_item(C.Structure):
+    _fields_ = [("sequence_id", I64), ("layer", U32), ("query", cf_device_tensor_view), ("output", P),
+                ("output_type", U32), ("output_token_stride_bytes", U64), ("output_head_stride_bytes", U64),
+                ("output_element_stride_bytes", U64), ("query_token_begin", U32), ("softmax_scale", F32),
+                ("causal_window", U32), ("sealed_pages", P), ("sealed_page_count", U32), ("active_keys", P),
+                ("active_values", P), ("active_token_begin", U32), ("active_token_count", U32)]
+
+
+class cf_attention_counters(C.Structure):
+    _fields_ = [(k, U64) for k in (
+        "reference_launches", "optimized_launches", "decode_launches", "prefill_launches", "grouped_batches",
+        "grouped_items", "kernel_launches_avoided", "graph_captures", "graph_replays", "graph_invalidations",
+        "graph_replay_failures", "async_seal_submissions", "async_seal_overlaps", "descriptor_bytes_read",
+        "compressed_payload_bytes_read", "scale_bytes_read", "allocation_count", "pool_hits", "pool_misses",
+        "peak_reserved_bytes", "peak_live_bytes", "numerical_failures", "cross_sequence_contamination",
+        "dense_fallback_launches", "cuda_errors")]
+
+
 _SIGS = {
     "cf_device_tensor_validate": (C.c_int, [P]),
     "cf_device_seal_create": (P, [P]),
@@ -135,6 +168,13 @@ _SIGS = {
     "cf_ms_cuda_audit": (C.c_int, [P]),
     "cf_ms_cuda_get_counters": (C.c_int, [P, P]),
     "cf_ms_cuda_last_error": (C.c_char_p, [P]),
+    "cf_attention_runtime_create": (P, [P]),
+    "cf_attention_runtime_destroy": (None, [P, P]),
+    "cf_attention_execute_async": (C.c_int, [P, P, U32, P]),
+    "cf_attention_compare_async": (C.c_int, [P, P, U32, F32, F32, P]),
+    "cf_attention_invalidate_graphs": (C.c_int, [P]),
+    "cf_attention_get_counters": (C.c_int, [P, P]),
+    "cf_attention_last_error": (C.c_char_p, [P]),
 }
 for _n, (_r, _a) in _SIGS.items():
     A.declare(_n, _r, _a)
@@ -336,4 +376,45 @@ class MsResolver:
     def counters(self) -> dict:
         c = cf_ms_cuda_counters()
         self._rc(A.lib().cf_ms_cuda_get_counters(self.h, C.byref(c)), "counters")
+        return {k: getattr(c, k) for k, _ in c._fields_}
+
+
+class AttentionRuntime:
+    """cf_attention_runtime: batched decode attention over caller-held two's-complement int4 nibble pages."""
+
+    def __init__(self, layer_count, kv_heads, q_heads, head_dim, gqa=None, page_size=0, block_size=0,
+                 mode=CF_ATTENTION_OPTIMIZED):
+        gqa = q_heads // kv_heads if gqa is None else gqa
+        self.config = cf_attention_runtime_config(layer_count, q_heads, kv_heads, head_dim, page_size, block_size,
+                                                  gqa, 0, 0, mode, cf_attention_tuning())
+        self.h = A.lib().cf_attention_runtime_create(C.byref(self.config))
+        if not self.h:
+            raise SealError("cf_attention_runtime_create rejected the config")
+
+    def close(self, stream=None):
+        if self.h:
+            A.lib().cf_attention_runtime_destroy(self.h, _stream(stream))
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def last_error(self) -> str:
+        return A.lib().cf_attention_last_error(self.h).decode()
+
+    def execute_items(self, items, stream=None) -> int:
+        """items: a ctypes array of cf_attention_batch_item; returns the library's status (0 / -1)."""
+        return A.lib().cf_attention_execute_async(self.h, items, len(items), _stream(stream))
+
+    def execute(self, items, stream=None):
+        if self.execute_items(items, stream) != 0:
+            raise SealError(f"execute: {self.last_error()}")
+
+    def counters(self) -> dict:
+        c = cf_attention_counters()
+        if A.lib().cf_attention_get_counters(self.h, C.byref(c)) != 0:
+            raise SealError("counters")
         return {k: getattr(c, k) for k, _ in c._fields_}

@@ -571,6 +571,92 @@ def nib_attention(pages: list, block_size: int, q: np.ndarray, query_begin: int,
     return out
 
 
+@dataclass
+class RtPage:
+    """One page of the batched attention runtime (cf_attention_execute_async, production_attention.h): K and V
+    [tokens][kv_heads][head_dim] as two's-complement int4 nibbles, two per byte with the even index in the low
+    nibble, one scale per block of `block_size` values of a (token, KV head) row. A payload or scale of None is a
+    page with a NULL pointer."""
+    k_payload: np.ndarray | None
+    v_payload: np.ndarray | None
+    k_scales: np.ndarray | None
+    v_scales: np.ndarray | None
+    token_begin: int
+    token_count: int
+    head_dim: int
+    block_size: int
+
+
+def rt_quantize(x: np.ndarray, block_size: int):
+    """Test-fixture encoder of the runtime's page format (the reference has none: its seal engine writes offset-8
+    symbols): x [tokens, kv_heads, head_dim] -> (payload u8, scales f32). Per row block: scale = absmax / 7 (1 for
+    an all-zero block), value = clamp(rint(x / scale), -8, 7) stored as its low 4 bits."""
+    x = np.ascontiguousarray(x, np.float32)
+    T, H, D = x.shape
+    bpr = (D + block_size - 1) // block_size
+    pad = np.zeros((T, H, bpr * block_size), np.float32)
+    pad[:, :, :D] = x
+    blocks = pad.reshape(T, H, bpr, block_size)
+    amax = np.abs(blocks).max(axis=3)
+    scales = np.where(amax > 0, amax / np.float32(7.0), np.float32(1.0)).astype(np.float32)
+    q = np.clip(np.rint(blocks / scales[..., None]), -8, 7).astype(np.int64)
+    nib = (q.reshape(T, H, bpr * block_size)[:, :, :D].ravel() & 15).astype(np.uint8)
+    if nib.size % 2:
+        nib = np.concatenate([nib, np.zeros(1, np.uint8)])
+    payload = (nib[0::2] | (nib[1::2] << 4)).astype(np.uint8)
+    return payload, scales.ravel()
+
+
+def rt_dequant(payload: np.ndarray, scales: np.ndarray, tokens: int, kv_heads: int, head_dim: int,
+               page_head_dim: int, block_size: int) -> np.ndarray:
+    """[tokens, kv_heads, head_dim] float64 of one runtime page stream: reference production_attention.cu:41-46
+    (two's-complement nibble times its scale) with the scale index of :85-86 / :106-107
+    ((token * kv_heads + kv_head) * ceil(page head_dim / block_size) + d / block_size)."""
+    n = tokens * kv_heads * head_dim
+    i = np.arange(n)
+    byte = payload[i >> 1].astype(np.int64)
+    nib = np.where(i & 1, byte >> 4, byte & 15)
+    val = np.where(nib >= 8, nib - 16, nib)
+    bph = (page_head_dim + block_size - 1) // block_size
+    sidx = (i // head_dim) * bph + (i % head_dim) // block_size
+    return (val * scales[sidx].astype(np.float64)).reshape(tokens, kv_heads, head_dim)
+
+
+def rt_attention_f64(q: np.ndarray, kv_heads: int, gqa: int, query_token_begin: int, window: int, scale: float,
+                     pages: list, active_k=None, active_v=None, active_begin: int = 0) -> np.ndarray:
+    """One batch item of cf_attention_execute_async in float64: reference production_attention.cu:59-139. q is
+    [q_heads, head_dim] (the query values as the kernel reads them); query head h reads KV head h // gqa; pages in
+    order, then the active tail ([n, kv_heads, head_dim] fp32); a page with a NULL pointer is skipped (:81); a
+    position p is attended unless window > 0 and p + window < query_token_begin (:83, :116: no causal bound; the
+    sum is taken without 32-bit wraparound); score = q.k * scale; a head with nothing attended is zeros."""
+    q = np.asarray(q, np.float64)
+    QH, D = q.shape
+    ks, vs, pos = [], [], []
+    for pg in pages:
+        if pg.k_payload is None or pg.v_payload is None or pg.k_scales is None or pg.v_scales is None:
+            continue
+        ks.append(rt_dequant(pg.k_payload, pg.k_scales, pg.token_count, kv_heads, D, pg.head_dim, pg.block_size))
+        vs.append(rt_dequant(pg.v_payload, pg.v_scales, pg.token_count, kv_heads, D, pg.head_dim, pg.block_size))
+        pos.append(pg.token_begin + np.arange(pg.token_count, dtype=np.int64))
+    if active_k is not None and len(active_k):
+        ks.append(np.asarray(active_k, np.float64).reshape(-1, kv_heads, D))
+        vs.append(np.asarray(active_v, np.float64).reshape(-1, kv_heads, D))
+        pos.append(active_begin + np.arange(len(active_k), dtype=np.int64))
+    out = np.zeros((QH, D))
+    if not ks:
+        return out
+    K, V, P = np.concatenate(ks), np.concatenate(vs), np.concatenate(pos)
+    vis = np.ones(len(P), bool) if window == 0 else P + window >= query_token_begin
+    if not vis.any():
+        return out
+    for h in range(QH):
+        kv = h // gqa
+        s = (K[vis, kv, :] @ q[h]) * scale
+        w = np.exp(s - s.max())
+        out[h] = (w @ V[vis, kv, :]) / w.sum()
+    return out
+
+
 def ref_lib() -> C.CDLL | None:
     """oracle/_ref/libcfref.so (reference kv_gpu_fixture/kv_reference/kv_runtime behind ref_shim.cpp) or None."""
     global _ref

@@ -14,6 +14,7 @@
 #include "chromofold/device_kv_dataplane.h"
 #include "chromofold/device_kv_seal_attention.h"
 #include "chromofold/multisequence_cuda_resolver.h"
+#include "chromofold/production_attention.h"
 #include "chromofold/kv_codec_ext.h"
 #include "chromofold/kv_cuda.h"
 #include "chromofold/kv_runtime.h"
@@ -148,6 +149,50 @@ int main(void) {
     expect("cf_ms_cuda_execute_batch_async", cf_ms_cuda_execute_batch_async(NULL, NULL, 0, NULL), -1);
     expect("cf_ms_cuda_audit", cf_ms_cuda_audit(NULL), -1);
     expect("cf_ms_cuda_last_error", cf_ms_cuda_last_error(NULL) != NULL, 1);
+  }
+  {
+    printf("sizeof cf_attention_runtime_config %zu\n", sizeof(cf_attention_runtime_config));
+    printf("sizeof cf_attention_batch_item %zu\n", sizeof(cf_attention_batch_item));
+    printf("sizeof cf_attention_counters %zu\n", sizeof(cf_attention_counters));
+    expect("cf_attention_runtime_create", cf_attention_runtime_create(NULL) == NULL, 1);
+    cf_attention_runtime_config cfg;
+    memset(&cfg, 0, sizeof cfg);
+    cfg.layer_count = 1;
+    cfg.query_head_count = 8;
+    cfg.kv_head_count = 2;
+    cfg.head_dim = 64;
+    cfg.gqa_group_size = 4;
+    cfg.mode = CF_ATTENTION_REFERENCE;
+    cf_attention_runtime *rt = cf_attention_runtime_create(&cfg);
+    expect("cf_attention_runtime_create (valid)", rt != NULL, 1);
+    cfg.gqa_group_size = 3;
+    expect("cf_attention_runtime_create (heads != kv * gqa)", cf_attention_runtime_create(&cfg) == NULL, 1);
+    cf_attention_batch_item item;
+    memset(&item, 0, sizeof item);
+    expect("cf_attention_execute_async (NULL)", cf_attention_execute_async(NULL, &item, 1, NULL), -1);
+    expect("cf_attention_execute_async (no items)", cf_attention_execute_async(rt, NULL, 1, NULL), -1);
+    expect("cf_attention_execute_async (reference mode)", cf_attention_execute_async(rt, &item, 1, NULL), -1);
+    expect("cf_attention_compare_async", cf_attention_compare_async(rt, &item, 1, 1e-3f, 1e-4f, NULL), -1);
+    expect("cf_attention_compare_async (bad tolerance)", cf_attention_compare_async(rt, &item, 1, 0.0f, 1.0f, NULL), -1);
+    expect("cf_attention_invalidate_graphs", cf_attention_invalidate_graphs(rt), 0);
+    cf_attention_counters c;
+    expect("cf_attention_get_counters", cf_attention_get_counters(rt, &c), 0);
+    expect("reference_launches", (int)c.reference_launches, 1);
+    expect("graph_invalidations", (int)c.graph_invalidations, 1);
+    expect("cf_attention_get_counters (NULL)", cf_attention_get_counters(NULL, &c), -1);
+    expect("cf_attention_last_error", cf_attention_last_error(rt)[0] != 0, 1);
+    expect("cf_attention_last_error (NULL)", cf_attention_last_error(NULL) != NULL, 1);
+    cf_attention_runtime_destroy(rt, NULL);
+    cf_attention_runtime_destroy(NULL, NULL);
+    cfg.gqa_group_size = 4;
+    cfg.mode = CF_ATTENTION_OPTIMIZED;
+    rt = cf_attention_runtime_create(&cfg);
+    /* an item with a NULL query is refused before any device work */
+    expect("cf_attention_execute_async (NULL query)", cf_attention_execute_async(rt, &item, 1, NULL), -1);
+    expect("cf_attention_last_error (NULL query)", strstr(cf_attention_last_error(rt), "NULL") != NULL, 1);
+    cf_attention_runtime_destroy(rt, NULL);
+    cfg.head_dim = 12;
+    expect("cf_attention_runtime_create (head_dim 12)", cf_attention_runtime_create(&cfg) == NULL, 1);
   }
   printf("%s (%d failure%s)\n", failures ? "FAIL" : "PASS", failures, failures == 1 ? "" : "s");
   return failures ? 1 : 0;

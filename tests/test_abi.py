@@ -79,7 +79,10 @@ def test_c_headers_link_and_null_contract(tmp_path):
                "cf_device_seal_counters": sealkv.cf_device_seal_counters,
                "cf_device_kv_counters": sealkv.cf_device_kv_counters,
                "cf_ms_page_publication": sealkv.cf_ms_page_publication,
-               "cf_ms_batch_item": sealkv.cf_ms_batch_item, "cf_ms_cuda_counters": sealkv.cf_ms_cuda_counters}
+               "cf_ms_batch_item": sealkv.cf_ms_batch_item, "cf_ms_cuda_counters": sealkv.cf_ms_cuda_counters,
+               "cf_attention_runtime_config": sealkv.cf_attention_runtime_config,
+               "cf_attention_batch_item": sealkv.cf_attention_batch_item,
+               "cf_attention_counters": sealkv.cf_attention_counters}
     sizes = dict(re.findall(r"^sizeof (\w+) (\d+)$", r.stdout, flags=re.M))
     assert set(sizes) == set(mirrors)
     for name, cls in mirrors.items():
