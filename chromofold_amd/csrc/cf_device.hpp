@@ -115,6 +115,17 @@ __device__ __forceinline__ int nibble_width_sum(uint32_t x) {
 
 __device__ __forceinline__ int width_of(int k) { return static_cast<int>((kWidthNibbles >> (4 * k)) & 15u); }
 
+// Global-address-space view of a generic pointer (one read from a struct or from LDS): its loads become global_load
+// (vmcnt only) instead of flat_load, which also counts in lgkmcnt, so that every wait for an LDS access would wait
+// for those loads too.
+#ifndef CF_GLOBAL
+#define CF_GLOBAL __attribute__((address_space(1)))
+#endif
+template <typename T>
+__device__ __forceinline__ const CF_GLOBAL T *global_ptr(const T *p) {
+  return (const CF_GLOBAL T *)p;  // an address-space conversion (C-style cast)
+}
+
 // a * b as f16 hi + lo (hi + lo = the product to about 21 bits), the MFMA operands of fp32-grade inputs.
 // hi comes from one explicit conversion (round toward zero) whose result is both stored and subtracted. Written as
 // (half)(a * b), the compiler may form the subtracted hi as v_fma_mix (one rounding of the exact product) and the

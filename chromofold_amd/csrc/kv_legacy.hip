@@ -217,6 +217,26 @@ __device__ __forceinline__ float4_t mfma16(half4_t a, half4_t b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
+// Max / sum over the 16 lanes of a row (every lane of the row gets the result) with DPP moves inside the row:
+// quad_perm [1,0,3,2], [2,3,0,1], then row_half_mirror and row_mirror (a ds_bpermute per step would put an LDS
+// round trip on the softmax's dependency chain: 8 per row and chunk).
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_max(float x) {
+  x = fmaxf(x, dpp_row<0xb1>(x));
+  x = fmaxf(x, dpp_row<0x4e>(x));
+  x = fmaxf(x, dpp_row<0x141>(x));
+  return fmaxf(x, dpp_row<0x140>(x));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_row<0xb1>(x);
+  x += dpp_row<0x4e>(x);
+  x += dpp_row<0x141>(x);
+  return x + dpp_row<0x140>(x);
+}
+
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -320,9 +340,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   auto softmax_chunk = [&](float (&s)[4][4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float mx = fmaxf(fmaxf(s[i][0], s[i][1]), fmaxf(s[i][2], s[i][3]));
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+      const float mx = row16_max(fmaxf(fmaxf(s[i][0], s[i][1]), fmaxf(s[i][2], s[i][3])));
       const float mn = fmaxf(m_run[i], mx);
       const float alpha = (m_run[i] == -INFINITY) ? 0.0f : __expf(m_run[i] - mn);
       float ps = 0.0f;
@@ -331,8 +349,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         s[i][j] = (s[i][j] == -INFINITY) ? 0.0f : __expf(s[i][j] - mn);
         ps += s[i][j];
       }
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) ps += __shfl_xor(ps, o);
+      ps = row16_sum(ps);
       if (mn != -INFINITY) {
         l_run[i] = l_run[i] * alpha + ps;
 #pragma unroll
@@ -417,7 +434,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const uint32_t pi = scan_pb + 64 * q + lane;
-          hv[q] = pi < d.page_count ? d.pages[pi].kv_head : 0xFFFFFFFFu;
+          hv[q] = pi < d.page_count ? cfd::global_ptr(d.pages)[pi].kv_head : 0xFFFFFFFFu;
         }
         uint32_t ord_run = scan_ord;
 #pragma unroll
@@ -461,7 +478,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       // range are dropped, the others compacted in order
       bool keep = false;
       uint4 meta = make_uint4(0, 0, 0, 0);
-      const cf_kv_device_page *pg = d.pages + my_p;
+      const CF_GLOBAL cf_kv_device_page *pg = cfd::global_ptr(d.pages) + my_p;
       if (static_cast<uint32_t>(lane) < cnt) {
         const uint32_t tb = pg->token_begin, tc = pg->token_count, fixed = pg->fixed_code_length;
         keep = tc != 0 && !(tb > vis_hi || tb + tc <= vis_lo);
@@ -502,10 +519,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       if ((mt.w >> 16) != 0) return r;  // not fixed-width
       const uint32_t bits = mt.w & 0xFFu, phd = mt.z, nt = min<uint32_t>(kChunk, mt.y - t0);
       if (bits == 0 || phd == 0 || phd > kMaxD) return r;
-      const uint32_t *kw = reinterpret_cast<const uint32_t *>(s_pptr[li][0]);
-      const uint32_t *vw = reinterpret_cast<const uint32_t *>(s_pptr[li][1]);
-      const float *ksc = reinterpret_cast<const float *>(s_pptr[li][2]);
-      const float *vsc = reinterpret_cast<const float *>(s_pptr[li][3]);
+      const CF_GLOBAL uint32_t *kw = cfd::global_ptr(reinterpret_cast<const uint32_t *>(s_pptr[li][0]));
+      const CF_GLOBAL uint32_t *vw = cfd::global_ptr(reinterpret_cast<const uint32_t *>(s_pptr[li][1]));
+      const CF_GLOBAL float *ksc = cfd::global_ptr(reinterpret_cast<const float *>(s_pptr[li][2]));
+      const CF_GLOBAL float *vsc = cfd::global_ptr(reinterpret_cast<const float *>(s_pptr[li][3]));
       const uint32_t spw = 32u / bits;
       const int64_t s0 = static_cast<int64_t>(t0) * phd, s1 = s0 + static_cast<int64_t>(nt) * phd;
       const int64_t w0 = s0 / spw, w1 = (s1 + spw - 1) / spw;
@@ -611,7 +628,36 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         const uint32_t spw = 32u / bits, mask = (1u << bits) - 1u;
         const int64_t s0 = static_cast<int64_t>(t0) * phd, s1 = s0 + static_cast<int64_t>(nt) * phd;
         const int64_t w0 = s0 / spw, w1 = (s1 + spw - 1) / spw;
+        // int4 / int8 codes with head_dim a multiple of the codes per word (every shape the adapter seals): each
+        // word lies inside one token row, its row from one multiply-high (rel < 2^13 and the reciprocal's error
+        // below head_dim keep it exact) and its symbols reordered by byte permutes into one K row piece
+        const bool whole = (bits == 4u || bits == 8u) && phd % spw == 0u;
+        const uint32_t inv = 0xFFFFFFFFu / phd + 1u;  // ceil(2^32 / phd) for phd >= 2
         auto put = [&](int64_t w, uint32_t kword, uint32_t vword) {
+          if (whole) {
+            const uint32_t rel = static_cast<uint32_t>(w * spw - s0), r = __umulhi(rel, inv), c = rel - r * phd;
+            uint8_t *kd = s_k + r * kKStride + c;
+            uint8_t *vd = s_vt + c * kVStride + r;
+            const uint32_t yk = __builtin_bswap32(kword), yv = __builtin_bswap32(vword);  // first code in byte 0
+            if (bits == 8u) {
+              *reinterpret_cast<uint32_t *>(kd) = yk;
+#pragma unroll
+              for (int k = 0; k < 4; ++k) vd[k * kVStride] = static_cast<uint8_t>(yv >> (8 * k));
+            } else {
+              // byte b of y holds codes 2b (high nibble) and 2b + 1: codes 0..3 = {h0, l0, h1, l1}, 4..7 = {h2, ...}
+              const uint32_t hk = (yk >> 4) & 0x0F0F0F0Fu, lk = yk & 0x0F0F0F0Fu;
+              const uint32_t hv = (yv >> 4) & 0x0F0F0F0Fu, lv = yv & 0x0F0F0F0Fu;
+              reinterpret_cast<uint32_t *>(kd)[0] = __builtin_amdgcn_perm(hk, lk, 0x01050004u);
+              reinterpret_cast<uint32_t *>(kd)[1] = __builtin_amdgcn_perm(hk, lk, 0x03070206u);
+              const uint32_t v0 = __builtin_amdgcn_perm(hv, lv, 0x01050004u), v1 = __builtin_amdgcn_perm(hv, lv, 0x03070206u);
+#pragma unroll
+              for (int k = 0; k < 4; ++k) {
+                vd[k * kVStride] = static_cast<uint8_t>(v0 >> (8 * k));
+                vd[(k + 4) * kVStride] = static_cast<uint8_t>(v1 >> (8 * k));
+              }
+            }
+            return;
+          }
           for (uint32_t k = 0; k < spw; ++k) {
             const int64_t i = w * spw + k;
             if (i < s0 || i >= s1) continue;
@@ -623,8 +669,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         if (w0 + tid < w1) put(w0 + tid, cur.ka, cur.va);
         if (w0 + tid + kThreads < w1) put(w0 + tid + kThreads, cur.kc, cur.vc);
         // words past the prefetched 2 * kThreads (chunks of more than 2 KiB per stream) are loaded here
-        const uint32_t *kw = reinterpret_cast<const uint32_t *>(s_pptr[li][0]);
-        const uint32_t *vw = reinterpret_cast<const uint32_t *>(s_pptr[li][1]);
+        const CF_GLOBAL uint32_t *kw = cfd::global_ptr(reinterpret_cast<const uint32_t *>(s_pptr[li][0]));
+        const CF_GLOBAL uint32_t *vw = cfd::global_ptr(reinterpret_cast<const uint32_t *>(s_pptr[li][1]));
         for (int64_t w = w0 + 2 * kThreads + tid; w < w1; w += kThreads) put(w, kw[w], vw[w]);
       }
       // dims the page does not have read as V = 0 (the query side zeroes K through s_ks)
