@@ -254,7 +254,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   __shared__ __align__(16) _Float16 s_p[kWaves][2][16][kPStride];  // per wavefront: P hi and lo [vector][token]
   __shared__ __align__(16) int32_t s_lut[2][1 << kLutMaxLen];      // Huffman LUTs, rANS tables, or tail queries
   __shared__ __align__(16) uint16_t s_w[kRansWords];
-  __shared__ float s_ks[kMaxD];                  // K scale per channel of the staged page (rANS pages: 1)
+  __shared__ float s_ks[2][kMaxD];               // K scale per channel of the staged page(s) (rANS pages: 1)
   __shared__ float s_kt[kChunk], s_vs[kChunk];   // per token: K scale (legacy pages: 1) and V scale
   __shared__ int s_bad;
   // this workgroup's current list of pages: fields {token_begin, token_count, head_dim, fixed bits | zero point << 8 |
@@ -300,14 +300,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         qraw[kk][j] = (ok && dd < HD) ? qp[dd] : 0.0f;
       }
   }
-  // A operands of one page: the queries times its per-channel K scales (s_ks; 1 for rANS pages), f16 hi + lo
-  auto build_q = [&](half4_t (&qhi)[KS], half4_t (&qlo)[KS]) {
+  // A operands of one page: the queries times its per-channel K scales (s_ks[p]; 1 for rANS pages), f16 hi + lo
+  auto build_q = [&](half4_t (&qhi)[KS], half4_t (&qlo)[KS], uint32_t p) {
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         _Float16 h, l;
-        cfd::split_mul_f16(qraw[kk][j], s_ks[16 * kk + 4 * (lane >> 4) + j], h, l);
+        cfd::split_mul_f16(qraw[kk][j], s_ks[p][16 * kk + 4 * (lane >> 4) + j], h, l);
         qhi[kk][j] = h;
         qlo[kk][j] = l;
       }
@@ -359,32 +359,36 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     }
   };
 
-  // Scores, online softmax and P.V of the staged chunk: nt tokens from tok0, K in s_k, V in s_vt, scales in s_ks /
-  // s_kt / s_vs, symbols around the page's zero point (zbase = 1024 + zero point).
-  auto compute_chunk = [&](uint32_t tok0, uint32_t nt, _Float16 zbase) {
-    half4_t qhi[KS], qlo[KS];
-    build_q(qhi, qlo);
-    const int ntile = static_cast<int>((nt + 15) / 16);
-    // scores
+  // Scores, online softmax and P.V of the staged chunk. Rows 0-31 (half 0) and 32-63 (half 1) of s_k / s_vt hold
+  // nh[h] tokens from position tok[h] (a half is one page's tokens, or the continuation of half 0's page);
+  // half h's K scales are s_ks[h ? kp1 : 0], its symbols sit around zb[h] (1024 + the page's zero point); per-token
+  // scales in s_kt / s_vs.
+  auto compute_chunk = [&](const uint32_t (&tok)[2], const uint32_t (&nh)[2], const _Float16 (&zb)[2], uint32_t kp1) {
     float s[4][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float4_t c = {0, 0, 0, 0};
-      if (j < ntile) {
-        const uint8_t *krow = s_k + (16 * j + (lane & 15)) * kKStride + 4 * (lane >> 4);
+    for (int h = 0; h < 2; ++h) {
+      half4_t qhi[KS], qlo[KS];
+      if (h == 0 || nh[1] != 0) build_q(qhi, qlo, h ? kp1 : 0u);
 #pragma unroll
-        for (int kk = 0; kk < KS; ++kk) {
-          const half4_t b = sym4_to_half4(*reinterpret_cast<const uint32_t *>(krow + 16 * kk), zbase);
-          c = mfma16(qhi[kk], b, c);
-          c = mfma16(qlo[kk], b, c);
+      for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * h + jj;
+        float4_t c = {0, 0, 0, 0};
+        if (16u * jj < nh[h]) {
+          const uint8_t *krow = s_k + (16 * j + (lane & 15)) * kKStride + 4 * (lane >> 4);
+#pragma unroll
+          for (int kk = 0; kk < KS; ++kk) {
+            const half4_t b = sym4_to_half4(*reinterpret_cast<const uint32_t *>(krow + 16 * kk), zb[h]);
+            c = mfma16(qhi[kk], b, c);
+            c = mfma16(qlo[kk], b, c);
+          }
         }
-      }
-      const uint32_t tt = 16 * j + (lane & 15), tok = tok0 + tt;
-      const float kts = s_kt[tt];
+        const uint32_t r = 16 * jj + (lane & 15), tk = tok[h] + r;
+        const float kts = s_kt[16 * j + (lane & 15)];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bool vis = j < ntile && tt < nt && c_ok[i] && tok >= c_lo[i] && tok <= c_hi[i];
-        s[i][j] = vis ? c[i] * kts * scale : -INFINITY;
+        for (int i = 0; i < 4; ++i) {
+          const bool vis = r < nh[h] && c_ok[i] && tk >= c_lo[i] && tk <= c_hi[i];
+          s[i][j] = vis ? c[i] * kts * scale : -INFINITY;
+        }
       }
     }
     softmax_chunk(s);
@@ -402,14 +406,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     // P.V: acc[t] (vector rows, dims 16 t + lane % 16) += P[16 x tokens] V[tokens x 16]
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      if (ks >= ntile) break;
+      if (16u * (ks & 1) >= nh[ks >> 1]) continue;
       const half4_t ph = *reinterpret_cast<const half4_t *>(&s_p[wave][0][lane & 15][16 * ks + 4 * (lane >> 4)]);
       const half4_t pl = *reinterpret_cast<const half4_t *>(&s_p[wave][1][lane & 15][16 * ks + 4 * (lane >> 4)]);
 #pragma unroll
       for (int t = 0; t < KS; ++t) {
         const uint32_t w = *reinterpret_cast<const uint32_t *>(s_vt + (16 * t + (lane & 15)) * kVStride + 16 * ks +
                                                                4 * (lane >> 4));
-        const half4_t b = sym4_to_half4(w, zbase);
+        const half4_t b = sym4_to_half4(w, zb[ks >> 1]);
         acc[t] = mfma16(ph, b, acc[t]);
         acc[t] = mfma16(pl, b, acc[t]);
       }
@@ -506,36 +510,81 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     const uint32_t n = __builtin_amdgcn_readfirstlane(s_pn);
     const bool more = __builtin_amdgcn_readfirstlane(s_pmore) != 0;
 
-    // prefetch of a fixed-width chunk (li, t0): the first 2 * kThreads words of K and of V, the thread's K scale
-    // (channel tid) and V scale (token t0 + tid)
+    // Fixed-width chunks: two halves of up to 32 tokens (rows 0-31 and 32-63 of the staged tiles). Half 0 takes
+    // page li from token t0; half 1 the page's next 32 tokens, or, when the page has none left, page li + 1 if it is
+    // a fixed-width page of the same head_dim and code width with at most 32 tokens (two 32-token pages per
+    // chunk: one staging, one softmax and one barrier pair per 64 tokens).
+    struct Plan {
+      uint32_t li[2], t0[2], nt[2];
+      uint32_t nli, nt0;  // the chunk after this one
+    };
+    auto plan_at = [&](uint32_t li, uint32_t t0) {
+      Plan p{};
+      const uint4 mt = s_pmeta[li];
+      const uint32_t tc = __builtin_amdgcn_readfirstlane(mt.y), mw = __builtin_amdgcn_readfirstlane(mt.w);
+      const uint32_t rem = tc - t0;
+      p.li[0] = li;
+      p.t0[0] = t0;
+      p.nt[0] = min(rem, 32u);
+      p.li[1] = li;
+      p.t0[1] = t0 + 32u;
+      p.nt[1] = rem > 32u ? min(rem - 32u, 32u) : 0u;
+      p.nli = rem > 64u ? li : li + 1u;
+      p.nt0 = rem > 64u ? t0 + 64u : 0u;
+      if (rem <= 32u && li + 1u < n) {
+        const uint4 mb = s_pmeta[li + 1u];
+        const uint32_t bw = __builtin_amdgcn_readfirstlane(mb.w), bc = __builtin_amdgcn_readfirstlane(mb.y);
+        const uint32_t bd = __builtin_amdgcn_readfirstlane(mb.z), ad = __builtin_amdgcn_readfirstlane(mt.z);
+        if ((bw >> 16) == 0u && (bw & 0xFFu) == (mw & 0xFFu) && bd == ad && bc <= 32u) {
+          p.li[1] = li + 1u;
+          p.t0[1] = 0u;
+          p.nt[1] = bc;
+          p.nli = li + 2u;
+        }
+      }
+      return p;
+    };
+    // what a thread loads for a chunk ahead of its turn: per half the first 2 * kThreads words of K and of V, the
+    // K scale of channel tid; the V scale of token tid of the chunk
     struct Pre {
-      uint32_t ka, kc, va, vc;
-      float ks, vs;
+      uint32_t k[2][2], v[2][2];
+      float ks[2], vs;
+    };
+    auto fixed_ok = [&](uint32_t li) {  // a fixed-width page this kernel stages
+      if (li >= n) return false;
+      const uint4 mt = s_pmeta[li];
+      const uint32_t mw = __builtin_amdgcn_readfirstlane(mt.w), phd = __builtin_amdgcn_readfirstlane(mt.z);
+      return (mw >> 16) == 0u && (mw & 0xFFu) != 0u && phd != 0u && phd <= static_cast<uint32_t>(kMaxD);
     };
     auto prefetch = [&](uint32_t li, uint32_t t0) {
-      Pre r{0u, 0u, 0u, 0u, 0.0f, 0.0f};
-      if (li >= n) return r;
+      Pre r{};
+      if (!fixed_ok(li)) return r;
+      const Plan p = plan_at(li, t0);
       const uint4 mt = s_pmeta[li];
-      if ((mt.w >> 16) != 0) return r;  // not fixed-width
-      const uint32_t bits = mt.w & 0xFFu, phd = mt.z, nt = min<uint32_t>(kChunk, mt.y - t0);
-      if (bits == 0 || phd == 0 || phd > kMaxD) return r;
-      const CF_GLOBAL uint32_t *kw = cfd::global_ptr(reinterpret_cast<const uint32_t *>(s_pptr[li][0]));
-      const CF_GLOBAL uint32_t *vw = cfd::global_ptr(reinterpret_cast<const uint32_t *>(s_pptr[li][1]));
-      const CF_GLOBAL float *ksc = cfd::global_ptr(reinterpret_cast<const float *>(s_pptr[li][2]));
-      const CF_GLOBAL float *vsc = cfd::global_ptr(reinterpret_cast<const float *>(s_pptr[li][3]));
+      const uint32_t bits = __builtin_amdgcn_readfirstlane(mt.w) & 0xFFu, phd = __builtin_amdgcn_readfirstlane(mt.z);
       const uint32_t spw = 32u / bits;
-      const int64_t s0 = static_cast<int64_t>(t0) * phd, s1 = s0 + static_cast<int64_t>(nt) * phd;
-      const int64_t w0 = s0 / spw, w1 = (s1 + spw - 1) / spw;
-      const int64_t wa = min<int64_t>(w0 + tid, w1 - 1), wc = min<int64_t>(w0 + tid + kThreads, w1 - 1);
-      r.ka = kw[wa];
-      r.kc = kw[wc];
-      r.va = vw[wa];
-      r.vc = vw[wc];
-      r.ks = ksc[min<uint32_t>(static_cast<uint32_t>(tid), phd - 1)];
-      r.vs = vsc[t0 + min<uint32_t>(static_cast<uint32_t>(tid), nt - 1)];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t ph = p.nt[h] ? p.li[h] : p.li[0];  // an empty half loads half 0's page (never used)
+        const CF_GLOBAL uint32_t *kw = cfd::global_ptr(reinterpret_cast<const uint32_t *>(s_pptr[ph][0]));
+        const CF_GLOBAL uint32_t *vw = cfd::global_ptr(reinterpret_cast<const uint32_t *>(s_pptr[ph][1]));
+        const CF_GLOBAL float *ksc = cfd::global_ptr(reinterpret_cast<const float *>(s_pptr[ph][2]));
+        const uint32_t nt = p.nt[h] ? p.nt[h] : p.nt[0], t0h = p.nt[h] ? p.t0[h] : p.t0[0];
+        const int64_t s0 = static_cast<int64_t>(t0h) * phd, s1 = s0 + static_cast<int64_t>(nt) * phd;
+        const int64_t w0 = s0 / spw, w1 = (s1 + spw - 1) / spw;
+        const int64_t wa = min<int64_t>(w0 + tid, w1 - 1), wc = min<int64_t>(w0 + tid + kThreads, w1 - 1);
+        r.k[h][0] = kw[wa];
+        r.k[h][1] = kw[wc];
+        r.v[h][0] = vw[wa];
+        r.v[h][1] = vw[wc];
+        r.ks[h] = ksc[min<uint32_t>(static_cast<uint32_t>(tid), phd - 1)];
+      }
+      const bool h1 = ((static_cast<uint32_t>(tid) >> 5) & 1u) && p.nt[1];  // the thread's token is in half 1
+      const uint32_t pv = h1 ? p.li[1] : p.li[0], tv = h1 ? p.t0[1] : p.t0[0], nv = h1 ? p.nt[1] : p.nt[0];
+      const CF_GLOBAL float *vsc = cfd::global_ptr(reinterpret_cast<const float *>(s_pptr[pv][3]));
+      r.vs = vsc[tv + min<uint32_t>(static_cast<uint32_t>(tid) & 31u, nv - 1u)];
       return r;
     };
-
     uint32_t li = 0, t0 = 0;
     Pre cur = prefetch(0, 0);
     while (li < n) {
@@ -570,7 +619,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
           const uint32_t nt = min<uint32_t>(kChunk, pg.token_count - t0);
           const uint32_t tok0 = pg.token_begin + t0;
           __syncthreads();  // the previous chunk's compute no longer reads the staged tiles
-          for (uint32_t dd = tid; dd < kMaxD; dd += kThreads) s_ks[dd] = rans ? 1.0f : (dd < phd ? pg.k_scales[dd] : 0.0f);
+          for (uint32_t dd = tid; dd < kMaxD; dd += kThreads) s_ks[0][dd] = rans ? 1.0f : (dd < phd ? pg.k_scales[dd] : 0.0f);
           if (rans) {
             if (wave == 0) {
               uint2(*tab)[cfkv::kSlots] = reinterpret_cast<uint2(*)[cfkv::kSlots]>(&s_lut[0][0]);
@@ -595,7 +644,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
           for (uint32_t i = tid; i < (HD > phd ? HD - phd : 0u) * kChunk; i += kThreads)
             s_vt[(phd + i / kChunk) * kVStride + i % kChunk] = static_cast<uint8_t>(zp);
           __syncthreads();
-          if (!s_bad && wave_active) compute_chunk(tok0, nt, zbase);
+          if (!s_bad && wave_active) {
+            const uint32_t tk[2] = {tok0, tok0 + 32u}, nh[2] = {min(nt, 32u), nt > 32u ? nt - 32u : 0u};
+            const _Float16 zb[2] = {zbase, zbase};
+            compute_chunk(tk, nh, zb, 0u);
+          }
         }
         } while (false);
         ++li;
@@ -603,41 +656,48 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         cur = prefetch(li, 0);
         continue;
       }
-      // fixed-width chunk (li, t0)
-      const uint32_t bits = mw & 0xFFu, zp = (mw >> 8) & 0xFFu;
-      if (phd == 0 || phd > kMaxD) {  // not a page this kernel can stage: skipped
+      // fixed-width chunk at (li, t0)
+      if (!fixed_ok(li)) {  // not a page this kernel can stage: skipped
         ++li;
         t0 = 0;
         cur = prefetch(li, 0);
         continue;
       }
-      const uint32_t nt = min<uint32_t>(kChunk, tc - t0), tok0 = tb + t0;
-      uint32_t li2 = li, t02 = t0 + kChunk;
-      if (t02 >= tc) {
-        li2 = li + 1;
-        t02 = 0;
+      const Plan p = plan_at(li, t0);
+      const uint32_t bits = mw & 0xFFu, spw = 32u / bits, mask = (1u << bits) - 1u;
+      uint32_t zp[2], tk[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint4 mh = s_pmeta[p.li[h]];
+        zp[h] = (__builtin_amdgcn_readfirstlane(mh.w) >> 8) & 0xFFu;
+        tk[h] = __builtin_amdgcn_readfirstlane(mh.x) + p.t0[h];
       }
-      const _Float16 zbase = static_cast<_Float16>(1024.0f + static_cast<float>(zp));
+      const uint32_t kp1 = p.li[1] != p.li[0] ? 1u : 0u;  // half 1's K scales: its own page's, or half 0's
       __syncthreads();  // the previous chunk's compute no longer reads the staged tiles
-      if (static_cast<uint32_t>(tid) < kMaxD) s_ks[tid] = static_cast<uint32_t>(tid) < phd ? cur.ks : 0.0f;
+      if (static_cast<uint32_t>(tid) < kMaxD) {
+        s_ks[0][tid] = static_cast<uint32_t>(tid) < phd ? cur.ks[0] : 0.0f;
+        s_ks[1][tid] = static_cast<uint32_t>(tid) < phd ? cur.ks[1] : 0.0f;
+      }
       if (tid < kChunk) {
         s_kt[tid] = 1.0f;
-        s_vs[tid] = static_cast<uint32_t>(tid) < nt ? cur.vs : 0.0f;
+        s_vs[tid] = (static_cast<uint32_t>(tid) & 31u) < (tid < 32 ? p.nt[0] : p.nt[1]) ? cur.vs : 0.0f;
       }
-      {
-        const uint32_t spw = 32u / bits, mask = (1u << bits) - 1u;
-        const int64_t s0 = static_cast<int64_t>(t0) * phd, s1 = s0 + static_cast<int64_t>(nt) * phd;
+      // int4 / int8 codes with head_dim a multiple of the codes per word (every shape the adapter seals): each word
+      // lies inside one token row, its row from one multiply-high (rel < 2^13 and the reciprocal's error below
+      // head_dim keep it exact) and its codes reordered by byte permutes into one piece of a K row
+      const bool whole = (bits == 4u || bits == 8u) && phd % spw == 0u;
+      const uint32_t inv = 0xFFFFFFFFu / phd + 1u;  // ceil(2^32 / phd) for phd >= 2
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (p.nt[h] == 0u) continue;  // uniform
+        const int64_t s0 = static_cast<int64_t>(p.t0[h]) * phd, s1 = s0 + static_cast<int64_t>(p.nt[h]) * phd;
         const int64_t w0 = s0 / spw, w1 = (s1 + spw - 1) / spw;
-        // int4 / int8 codes with head_dim a multiple of the codes per word (every shape the adapter seals): each
-        // word lies inside one token row, its row from one multiply-high (rel < 2^13 and the reciprocal's error
-        // below head_dim keep it exact) and its symbols reordered by byte permutes into one K row piece
-        const bool whole = (bits == 4u || bits == 8u) && phd % spw == 0u;
-        const uint32_t inv = 0xFFFFFFFFu / phd + 1u;  // ceil(2^32 / phd) for phd >= 2
+        const uint32_t rbase = 32u * h;
         auto put = [&](int64_t w, uint32_t kword, uint32_t vword) {
           if (whole) {
             const uint32_t rel = static_cast<uint32_t>(w * spw - s0), r = __umulhi(rel, inv), c = rel - r * phd;
-            uint8_t *kd = s_k + r * kKStride + c;
-            uint8_t *vd = s_vt + c * kVStride + r;
+            uint8_t *kd = s_k + (rbase + r) * kKStride + c;
+            uint8_t *vd = s_vt + c * kVStride + rbase + r;
             const uint32_t yk = __builtin_bswap32(kword), yv = __builtin_bswap32(vword);  // first code in byte 0
             if (bits == 8u) {
               *reinterpret_cast<uint32_t *>(kd) = yk;
@@ -662,26 +722,31 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
             const int64_t i = w * spw + k;
             if (i < s0 || i >= s1) continue;
             const uint32_t sh = 32u - bits * (k + 1), rel = static_cast<uint32_t>(i - s0), r = rel / phd, c = rel - r * phd;
-            s_k[r * kKStride + c] = static_cast<uint8_t>((kword >> sh) & mask);
-            s_vt[c * kVStride + r] = static_cast<uint8_t>((vword >> sh) & mask);
+            s_k[(rbase + r) * kKStride + c] = static_cast<uint8_t>((kword >> sh) & mask);
+            s_vt[c * kVStride + rbase + r] = static_cast<uint8_t>((vword >> sh) & mask);
           }
         };
-        if (w0 + tid < w1) put(w0 + tid, cur.ka, cur.va);
-        if (w0 + tid + kThreads < w1) put(w0 + tid + kThreads, cur.kc, cur.vc);
-        // words past the prefetched 2 * kThreads (chunks of more than 2 KiB per stream) are loaded here
-        const CF_GLOBAL uint32_t *kw = cfd::global_ptr(reinterpret_cast<const uint32_t *>(s_pptr[li][0]));
-        const CF_GLOBAL uint32_t *vw = cfd::global_ptr(reinterpret_cast<const uint32_t *>(s_pptr[li][1]));
+        if (w0 + tid < w1) put(w0 + tid, cur.k[h][0], cur.v[h][0]);
+        if (w0 + tid + kThreads < w1) put(w0 + tid + kThreads, cur.k[h][1], cur.v[h][1]);
+        // words past the prefetched 2 * kThreads (halves of more than 1 KiB per stream) are loaded here
+        const CF_GLOBAL uint32_t *kw = cfd::global_ptr(reinterpret_cast<const uint32_t *>(s_pptr[p.li[h]][0]));
+        const CF_GLOBAL uint32_t *vw = cfd::global_ptr(reinterpret_cast<const uint32_t *>(s_pptr[p.li[h]][1]));
         for (int64_t w = w0 + 2 * kThreads + tid; w < w1; w += kThreads) put(w, kw[w], vw[w]);
       }
       // dims the page does not have read as V = 0 (the query side zeroes K through s_ks)
       for (uint32_t i = tid; i < (HD > phd ? HD - phd : 0u) * kChunk; i += kThreads)
-        s_vt[(phd + i / kChunk) * kVStride + i % kChunk] = static_cast<uint8_t>(zp);
-      const Pre nxt = prefetch(li2, t02);  // in flight during this chunk's compute
+        s_vt[(phd + i / kChunk) * kVStride + i % kChunk] = static_cast<uint8_t>(i % kChunk < 32u ? zp[0] : zp[1]);
+      const Pre nxt = prefetch(p.nli, p.nt0);  // in flight during this chunk's compute
       __syncthreads();
-      if (!s_bad && wave_active) compute_chunk(tok0, nt, zbase);
+      if (!s_bad && wave_active) {
+        const _Float16 zb[2] = {static_cast<_Float16>(1024.0f + static_cast<float>(zp[0])),
+                                static_cast<_Float16>(1024.0f + static_cast<float>(zp[1]))};
+        const uint32_t nh[2] = {p.nt[0], p.nt[1]};
+        compute_chunk(tk, nh, zb, kp1);
+      }
       cur = nxt;
-      li = li2;
-      t0 = t02;
+      li = p.nli;
+      t0 = p.nt0;
     }
     if (!more) break;
     __syncthreads();  // the list is rewritten by the next round
