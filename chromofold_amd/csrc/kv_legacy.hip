@@ -23,9 +23,10 @@
 // head. One 4-wavefront workgroup serves 64 vectors (16 per wavefront) of one KV head over one context split (the
 // head's pages taken round-robin by their order in the descriptor array; the dense tail in 64-token chunks after
 // them). Wave 0 lists the workgroup's pages, up to 64 per scan, with their fields (one memory latency per list, not
-// per page). Per page chunk of up to 64 tokens the workgroup decodes K and V once into LDS as integer symbols (K
-// token-major, V dim-major; a fixed-width chunk's words and scales were loaded during the previous chunk's
-// MFMAs), then every wavefront runs its 16 vectors through:
+// per page). Per chunk of up to 64 tokens, two halves of 32 (a page's tokens, or two consecutive fixed-width pages
+// of 32 tokens or fewer), the workgroup decodes K and V once into LDS as integer symbols (K token-major, V
+// dim-major; a fixed-width chunk's words and scales were loaded during the previous chunk's MFMAs), then every
+// wavefront runs its 16 vectors through:
 //   QK^T  v_mfma_f32_16x16x16f16: A = the queries times the page's per-channel K scale, split into f16 hi + lo
 //         parts; B = K symbol - zero point, exact in f16. The scores are fp32-grade.
 //   softmax online per vector in fp32 (each vector's row of the 16x16 tile lives in 16 lanes);
