@@ -177,8 +177,14 @@ __device__ __forceinline__ uint4 x_frag8(const uint16_t *__restrict__ x, int b, 
   }
 }
 
-template <int NT, bool FAST>
+template <int NT, bool FAST, int XR>
 __global__ void __launch_bounds__(kThreads) qw_matmul_kernel(QwArgs a) {
+  static_assert(XR == 0 || (XR == 1 && NT == 1 && FAST), "a staged x row: one batch row, whole segments");
+  // XR = 1 (a batch of one row): the chunk's x columns staged once per workgroup (8 bytes per thread) instead of
+  // every lane loading its 16-byte fragments from global memory, where the 16 row lanes of a lane group would all
+  // fetch the same row
+  __shared__ __attribute__((aligned(16))) uint16_t s_x[XR ? kKC : 8];
+  static_assert(kKC == 4 * kThreads, "one 8-byte x load per thread covers a chunk");
   // one LDS block so that the table sits at address 0 (its lookups need no base add)
   constexpr int kLutB = (1 << kLook) * 4, kTileB = kRows * kLdB, kCodeB = kRows * kRowWords * 4;
   __shared__ __attribute__((aligned(16))) uint8_t smem[kLutB + kTileB + kCodeB + 32 * 4];
@@ -258,10 +264,18 @@ __global__ void __launch_bounds__(kThreads) qw_matmul_kernel(QwArgs a) {
 #pragma unroll
       for (int p = 0; p < 2; ++p)
 #pragma unroll
-        for (int i = 0; i < NT; ++i)
-          f[p][i] = x_frag8<FAST>(a.x, (a.bt0 + i) * 16 + (lane & 15), B, kc0 + 64 * sg + 32 * p + 2 * bk, K);
+        for (int i = 0; i < NT; ++i) {
+          if constexpr (XR)
+            f[p][i] = *reinterpret_cast<const uint4 *>(s_x + 64 * sg + 32 * p + 2 * bk);
+          else
+            f[p][i] = x_frag8<FAST>(a.x, (a.bt0 + i) * 16 + (lane & 15), B, kc0 + 64 * sg + 32 * p + 2 * bk, K);
+        }
     };
-    if constexpr (XB == 2) load_x(0, xf[0]);  // in flight during the table build and the decode
+    uint2 xs = make_uint2(0u, 0u);
+    if constexpr (XR)  // columns kc0 + 4 t .. + 3 of row 0 (clamped inside the matrix: K is a multiple of 64)
+      xs = *reinterpret_cast<const uint2 *>(a.x + min(kc0 + 4 * t, K - 4));
+    else if constexpr (XB == 2)
+      load_x(0, xf[0]);  // in flight during the table build and the decode
     // ---- the band's table (first chunk only; LDS work while the loads above are in flight)
     if (!table_done) {
       build_table(lens, s_lut, reinterpret_cast<uint32_t *>(s_tile), s_meta);
@@ -271,6 +285,7 @@ __global__ void __launch_bounds__(kThreads) qw_matmul_kernel(QwArgs a) {
 #pragma unroll
       for (int r = 0; r < kStageWords; ++r) s_code[wave][64 * r + lane] = stage[r];
     }
+    if constexpr (XR) *reinterpret_cast<uint2 *>(s_x + 4 * t) = xs;
     __syncthreads();  // staged words and the table visible; table pass 1 is done with the tile
     // ---- decode: lane = segment of the wave's row
     {
@@ -292,6 +307,7 @@ __global__ void __launch_bounds__(kThreads) qw_matmul_kernel(QwArgs a) {
       for (int j = n; j < 64; ++j) dst[j] = static_cast<uint8_t>(zc);
     }
     __syncthreads();
+    if constexpr (XR) load_x(0, xf[0]);
     // ---- MFMA: the wave owns segments wave, wave + 16, wave + 32, wave + 48 of the chunk; segment j + 1's x
     // fragments load while segment j's MFMAs run
 #pragma unroll
@@ -357,9 +373,12 @@ template <int NT>
 void launch_qw(const QwArgs &a, unsigned grid, hipStream_t s) {
   // 16-byte x loads need whole segments and a 16-byte aligned x
   if ((a.K & 63) == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0)
-    qw_matmul_kernel<NT, true><<<grid, kThreads, 0, s>>>(a);
+    if (NT == 1 && a.B == 1)
+      qw_matmul_kernel<NT, true, NT == 1 ? 1 : 0><<<grid, kThreads, 0, s>>>(a);
+    else
+      qw_matmul_kernel<NT, true, 0><<<grid, kThreads, 0, s>>>(a);
   else
-    qw_matmul_kernel<NT, false><<<grid, kThreads, 0, s>>>(a);
+    qw_matmul_kernel<NT, false, 0><<<grid, kThreads, 0, s>>>(a);
 }
 
 }  // namespace

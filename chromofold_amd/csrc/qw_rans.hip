@@ -134,15 +134,21 @@ __device__ __forceinline__ uint32_t rans_step(const uint2 *__restrict__ tab, uin
   return e.y;
 }
 
-template <int NT, bool FAST, int SL>
+template <int NT, bool FAST, int SL, int XR>
 __global__ void __launch_bounds__(kThreads) qw_rans_kernel(RansArgs a) {
   static_assert(kThreads == 1024 && (SL == 2 || SL == 4), "staging loads per thread");
+  static_assert(XR == 0 || (NT == 1 && FAST), "x rows staged in LDS: one batch tile, whole stripes");
   __shared__ __attribute__((aligned(16))) uint2 s_tab[kSlots];
   // the chunk slot; reused by the reduction. A stripe's cursor starts at most at the slot's end (clamped) and a step
   // moves it by at most 64, with reads up to 63 words past it: 32 steps stay within kSlotW16 + 64 * 33 words
   // whatever the stream holds.
   __shared__ __attribute__((aligned(16))) uint16_t s_slot[kSlotW16 + 64 * 33];
   __shared__ __attribute__((aligned(16))) uint32_t s_cum[260];
+  // XR > 0 (a batch of at most XR rows): the chunk's x columns of rows 0..XR-1, staged once per workgroup (8 bytes
+  // per thread and row) instead of every lane loading its 16-byte fragments from global memory, where the 16 row
+  // lanes of a lane group would all fetch the same row (B = 1: 9.2 -> 8.8 us per call)
+  constexpr int kXCols = CF_QW_CHUNK_STRIPES * CF_QW_STRIPE_COLS;
+  __shared__ __attribute__((aligned(16))) uint16_t s_x[XR > 0 ? XR * kXCols : 8];
   static_assert(sizeof(s_slot) >= kWaves * NT * 256 * 4, "reduction fits the slot buffer");
 
   const int t = threadIdx.x, lane = t & 63;
@@ -231,14 +237,25 @@ __global__ void __launch_bounds__(kThreads) qw_rans_kernel(RansArgs a) {
 #pragma unroll
         for (int i = 0; i < NT; ++i) {
           const int col = st[c] * 256 + 64 * (h >> 1) + 8 * (h & 1);
-          if constexpr (FAST)
+          if constexpr (XR > 0)
+            xf[c][h % XH][i] = *reinterpret_cast<const uint4 *>(
+                s_x + min(r, XR - 1) * kXCols + (col - ch * kXCols) + 16 * g);
+          else if constexpr (FAST)
             xf[c][h % XH][i] = *reinterpret_cast<const uint4 *>(xb + xoff[i] + col);
           else
             xf[c][h % XH][i] = x_frag8(a.x, (a.bt0 + i) * 16 + r, B, col + 16 * g, K);
         }
     };
+    uint2 xs[XR > 0 ? XR : 1];
+    if constexpr (XR > 0) {  // x rows 0..XR-1 (rows past the batch repeat its last row), 4 columns per thread
+      const int c4 = min(ch * kXCols + 4 * t, K - 4);
 #pragma unroll
-    for (int h = 0; h < XH - 1; ++h) load_x(h);
+      for (int rr = 0; rr < XR; ++rr)
+        xs[rr] = *reinterpret_cast<const uint2 *>(xb + static_cast<uint32_t>(min(rr, B - 1)) * static_cast<uint32_t>(K) + c4);
+    } else {
+#pragma unroll
+      for (int h = 0; h < XH - 1; ++h) load_x(h);
+    }
     // ---- the band's table while the loads are in flight (rebuilt for every chunk: a build under a branch would
     // let the compiler sink the table load into it, behind the others)
     build_table(cw, a.zero, s_tab, s_cum);
@@ -250,7 +267,15 @@ __global__ void __launch_bounds__(kThreads) qw_rans_kernel(RansArgs a) {
       if (tt + 2 * kThreads < n) s_slot4[tt + 2 * kThreads] = st2;
       if (tt + 3 * kThreads < n) s_slot4[tt + 3 * kThreads] = st3;
     }
+    if constexpr (XR > 0) {
+#pragma unroll
+      for (int rr = 0; rr < XR; ++rr) *reinterpret_cast<uint2 *>(s_x + rr * kXCols + 4 * t) = xs[rr];
+    }
     __syncthreads();
+    if constexpr (XR > 0) {
+#pragma unroll
+      for (int h = 0; h < XH - 1; ++h) load_x(h);
+    }
     // ---- decode + MFMA: the wave's two stripes step together (two independent chains); a stripe past the
     // matrix (last chunk) decodes the matrix's last stripe again and its partials are dropped
     const uint16_t *cur[kPer];
@@ -318,12 +343,12 @@ __global__ void __launch_bounds__(kThreads) qw_rans_kernel(RansArgs a) {
   }
 }
 
-template <int NT, bool FAST>
+template <int NT, bool FAST, int XR>
 void launch_rans_sl(const RansArgs &a, unsigned grid, hipStream_t s) {
   if (max(a.chunk_words, a.last_words) <= 2 * kThreads * 8)
-    qw_rans_kernel<NT, FAST, 2><<<grid, kThreads, 0, s>>>(a);
+    qw_rans_kernel<NT, FAST, 2, XR><<<grid, kThreads, 0, s>>>(a);
   else
-    qw_rans_kernel<NT, FAST, 4><<<grid, kThreads, 0, s>>>(a);
+    qw_rans_kernel<NT, FAST, 4, XR><<<grid, kThreads, 0, s>>>(a);
 }
 
 template <int NT>
@@ -332,10 +357,14 @@ void launch_rans(const RansArgs &a, unsigned grid, hipStream_t s) {
   // (64 rows of x, and the scales)
   const bool fast = (a.K & 255) == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && a.K <= (1 << 24) &&
                     static_cast<uint64_t>(a.M) * (a.K / 64) < (1ull << 30);
-  if (fast)
-    launch_rans_sl<NT, true>(a, grid, s);
+  // a batch of one row stages its x row in LDS (staging four rows for batches of up to four measured slower: 9.6
+  // against 9.4 us at B = 4)
+  if (fast && NT == 1 && a.B == 1)
+    launch_rans_sl<NT, true, NT == 1 ? 1 : 0>(a, grid, s);
+  else if (fast)
+    launch_rans_sl<NT, true, 0>(a, grid, s);
   else
-    launch_rans_sl<NT, false>(a, grid, s);
+    launch_rans_sl<NT, false, 0>(a, grid, s);
 }
 
 }  // namespace
