@@ -335,8 +335,9 @@ __global__ void __launch_bounds__(kThreads) qw_rans_kernel(RansArgs a) {
     float s = 0.f;
 #pragma unroll
     for (int w = part * (kWaves / 4); w < (part + 1) * (kWaves / 4); ++w) s += red[(w * NT + i) * 256 + idx];
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
+    // the quad's four quarter sums by DPP moves (quad_perm [1,0,3,2], then [2,3,0,1]), no LDS round trip
+    s += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(s), 0xb1, 0xf, 0xf, false));
+    s += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(s), 0x4e, 0xf, 0xf, false));
     const int fl = idx >> 2, fr = idx & 3;
     const int b = (a.bt0 + i) * 16 + 4 * (fl >> 4) + fr, m = m0 + (fl & 15);
     if (part == 0 && b < B && m < M) a.y[static_cast<int64_t>(b) * M + m] = s;
