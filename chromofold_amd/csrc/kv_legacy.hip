@@ -59,6 +59,9 @@ constexpr int kPStride = kChunk + 4;                    // halves per P row
 constexpr int kLutMaxLen = 12;                          // Huffman LUTs of up to 2^12 entries are staged in LDS
 constexpr uint32_t kRansWords = CF_KV_RANS_MAX_GROUP_WORDS + 64;  // staged rANS words + slack for idle lanes' reads
 constexpr int kList = 64;                               // pages listed per round (one lane of wave 0 each)
+// 16-byte units per thread that stage an rANS page's body (at most the INT8 group: 2 streams x hd / 4 quads x 64
+// lanes x 4 bytes) into the P tile's bytes
+constexpr int kStageA = (2 * (kMaxD / 4) * 64 * 4 / 16 + kThreads - 1) / kThreads;
 
 // canonical-Huffman LUT decode at bit `pos` (MSB-first), returns sym | len << 8
 __device__ __forceinline__ int huff_at(const uint32_t *__restrict__ words, const int32_t *__restrict__ lut, int maxlen,
@@ -102,20 +105,23 @@ __device__ __forceinline__ uint32_t sm_to_offset_binary(uint32_t mag, uint32_t s
   return 0x80808080u + mag - (neg << 1);              // 128 + |q| or 128 - |q|, no carry between bytes
 }
 
-// One wavefront decodes a self-contained group blob (RANS_HYBRID chain start, or the INT8 raw fallback) of `ntok`
-// tokens and head_dim hd (% 16 == 0, % 32 for RANS) into sk[token * kKStride + dim] and svt[dim * kVStride + token]
-// as offset-binary symbols, with the per-token K and V scales in kt / vt. A RANS group's K and V tables (ktab, vtab
-// in HBM; not read for an INT8 group) are staged in `tab` (LDS), its word streams in `s_w`.
-// Returns false (wave-uniform) when the blob is not a valid self-contained group for this page.
-__device__ bool rans_group_to_lds(const uint8_t *__restrict__ blob, const uint2 *__restrict__ ktab,
-                                  const uint2 *__restrict__ vtab, uint2 (*tab)[cfkv::kSlots], uint16_t *s_w,
-                                  uint32_t hd, uint32_t ntok, uint8_t *sk, uint8_t *svt, float *kt, float *vt,
-                                  int lane) {
-  const uint32_t codec = *reinterpret_cast<const uint32_t *>(blob);
-  const uint32_t cnt = *reinterpret_cast<const uint32_t *>(blob + 4);
-  const uint32_t chain = *reinterpret_cast<const uint16_t *>(blob + 8);
-  const uint16_t *tc = reinterpret_cast<const uint16_t *>(blob + 12);
-  const uint32_t D = *reinterpret_cast<const uint16_t *>(blob + 20);
+// Stream `stm` (0 = K, 1 = V) of a self-contained group blob (RANS_HYBRID chain start, or the INT8 raw fallback) of
+// `ntok` tokens and head_dim hd (% 16 == 0, % 32 for RANS), decoded by one wavefront: K into sk[token * kKStride +
+// dim], V into svt[dim * kVStride + token], as offset-binary symbols, with the stream's per-token scales in `sc`.
+// The blob's body is already in LDS: `sa` holds the bytes after the header (RANS: lane states, then raw words;
+// INT8: the symbol words), `s_w` the RANS word streams (K from s_w[0], V after them), `tab` the stream's table.
+// Returns false (wave-uniform) when the blob is not a valid self-contained group for this page. Two wavefronts
+// decode K and V at once.
+__device__ bool rans_stream_to_lds(const uint8_t *__restrict__ blob_in, const uint32_t *sa, const uint2 *__restrict__ tab,
+                                   const uint16_t *s_w, uint32_t hd, uint32_t ntok, uint8_t *sk, uint8_t *svt,
+                                   float *sc, int lane, uint32_t stm) {
+  const CF_GLOBAL uint8_t *blob = cfd::global_ptr(blob_in);  // global loads: no wait shared with the LDS traffic
+  const uint32_t codec = *reinterpret_cast<const CF_GLOBAL uint32_t *>(blob);
+  const uint32_t cnt = *reinterpret_cast<const CF_GLOBAL uint32_t *>(blob + 4);
+  const uint32_t chain = *reinterpret_cast<const CF_GLOBAL uint16_t *>(blob + 8);
+  const CF_GLOBAL uint16_t *tc = reinterpret_cast<const CF_GLOBAL uint16_t *>(blob + 12);
+  const uint32_t D = *reinterpret_cast<const CF_GLOBAL uint16_t *>(blob + 20);
+  const float scale = reinterpret_cast<const CF_GLOBAL float *>(blob + 32 + 16 * stm)[lane >> 4];
   if (D != hd || hd % 16 != 0 || hd > kMaxD) return false;
   if (codec != CF_KV_CODEC_INT8 && (codec != CF_KV_CODEC_RANS_HYBRID || hd % 32 != 0 || chain != 1)) return false;
   // tokens must be contiguous: full 16-token pages, then at most one partial page, then empty pages
@@ -128,76 +134,54 @@ __device__ bool rans_group_to_lds(const uint8_t *__restrict__ blob, const uint2 
     total += n;
   }
   if (total != ntok || total == 0) return false;
-  const float *ks = reinterpret_cast<const float *>(blob + 32), *vs = reinterpret_cast<const float *>(blob + 48);
-  kt[lane] = ks[lane >> 4];
-  vt[lane] = vs[lane >> 4];
+  sc[lane] = scale;
   const uint32_t NQ = hd / 4, G = static_cast<uint32_t>(lane) >> 4, t = static_cast<uint32_t>(lane) & 15;
   // V quad q of a lane = tokens 4 tq .. 4 tq + 3 of its page at dim t + 16 i (tq = q / (hd / 16), i = q % (hd / 16)):
-  // four consecutive bytes of a dim-major row
-  auto put_v = [&](uint32_t q, uint32_t w) {
-    const uint32_t tq = q / (hd / 16), i = q % (hd / 16);
-    *reinterpret_cast<uint32_t *>(svt + (t + 16 * i) * kVStride + 16 * G + 4 * tq) = w;
-  };
-  auto put_k = [&](uint32_t q, uint32_t w) { *reinterpret_cast<uint32_t *>(sk + lane * kKStride + 4 * q) = w; };
-  if (codec == CF_KV_CODEC_INT8) {
-    const uint32_t *raw = reinterpret_cast<const uint32_t *>(blob + cfkv::kHdr);
-    for (uint32_t q = 0; q < NQ; ++q) {
-      put_k(q, raw[q * 64 + lane]);
-      put_v(q, raw[(NQ + q) * 64 + lane]);
+  // four consecutive bytes of a dim-major row; K quad q = dims 4q .. 4q + 3 of the lane's token
+  auto put = [&](uint32_t q, uint32_t w) {
+    if (stm == 0) {
+      *reinterpret_cast<uint32_t *>(sk + lane * kKStride + 4 * q) = w;
+    } else {
+      const uint32_t tq = q / (hd / 16), i = q % (hd / 16);
+      *reinterpret_cast<uint32_t *>(svt + (t + 16 * i) * kVStride + 16 * G + 4 * tq) = w;
     }
+  };
+  if (codec == CF_KV_CODEC_INT8) {
+    const uint32_t *raw = sa + stm * NQ * 64;
+    for (uint32_t q = 0; q < NQ; ++q) put(q, raw[q * 64 + lane]);
     return true;
   }
   const uint32_t nk = cnt & 0xFFFFu, nv = cnt >> 16;
   if (nk + nv > CF_KV_RANS_MAX_GROUP_WORDS) return false;
-  for (uint32_t i = lane; i < cfkv::kSlots; i += 64) {  // {f | c << 16, spread} as the decoder reads it
-    const uint2 a = ktab[i], b = vtab[i];
-    tab[0][i] = uint2{(a.x & 2047u) | (((a.x >> 11) & 2047u) << 16), a.y};
-    tab[1][i] = uint2{(b.x & 2047u) | (((b.x >> 11) & 2047u) << 16), b.y};
-  }
   const int RAW = cfkv::raw_words_of(static_cast<int>(hd));
-  const uint32_t *st = reinterpret_cast<const uint32_t *>(blob + cfkv::kHdr);
-  uint32_t xk = st[lane], xv = st[64 + lane];
-  const uint32_t *raw = st + 2 * 64;
-  // stage both word streams (u16, K then V) in LDS; whole u32 pairs (blobs are padded to 16 bytes)
-  const uint32_t *wsrc = raw + 2 * RAW;
-  for (uint32_t i = lane; i < (nk + nv + 1) / 2; i += 64) reinterpret_cast<uint32_t *>(s_w)[i] = wsrc[i];
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const uint16_t *wk = s_w, *wv = s_w + nk;
+  uint32_t x = sa[stm * 64 + lane];
+  const uint32_t *raw = sa + 2 * 64 + stm * RAW;
+  const uint16_t *w0 = s_w + (stm ? nk : 0u), *wend = w0 + (stm ? nv : nk);
+  const uint16_t *wp = w0;
   for (uint32_t sg = 0; sg < hd / 32; ++sg) {
-    uint32_t wK[7], wV[7];
+    uint32_t wr[7];
 #pragma unroll
-    for (int w = 0; w < 7; ++w) {
-      wK[w] = raw[(7 * sg + w) * 64 + lane];
-      wV[w] = raw[RAW + (7 * sg + w) * 64 + lane];
-    }
+    for (int w = 0; w < 7; ++w) wr[w] = raw[(7 * sg + w) * 64 + lane];
     [&]<int... M>(std::integer_sequence<int, M...>) {
       (
           [&] {
             constexpr int m = M;
             constexpr uint32_t rA = cfkv::kFrame[2 * m], rB = cfkv::kFrame[2 * m + 1];
             constexpr int nw = cfkv::kNWord[m], cwi = m < 2 ? 2 : 5;
-            const uint2 ek = cfkv::rans_lookup(tab[0], xk), ev = cfkv::rans_lookup(tab[1], xv);
-            uint32_t selk, selv;
-            const uint32_t wdk = cfkv::rans_advance(ek.x, xk, wk, selk);
-            const uint32_t wdv = cfkv::rans_advance(ev.x, xv, wv, selv);
-            xk = __builtin_amdgcn_perm(xk, wdk, selk);
-            xv = __builtin_amdgcn_perm(xv, wdv, selv);
-            const uint32_t spk = rA ? __builtin_amdgcn_alignbit(ek.y, ek.y, 32 - rA) : ek.y;
-            const uint32_t spv = rA ? __builtin_amdgcn_alignbit(ev.y, ev.y, 32 - rA) : ev.y;
+            const uint2 e = cfkv::rans_lookup(tab, x);
+            uint32_t sel;
+            const uint32_t wd = cfkv::rans_advance(e.x, x, wp, sel);
+            x = __builtin_amdgcn_perm(x, wd, sel);
+            const uint32_t sp = rA ? __builtin_amdgcn_alignbit(e.y, e.y, 32 - rA) : e.y;
             const uint32_t q0 = 8 * sg + 2 * m;
-            put_k(q0, sm_to_offset_binary(cfkv::quad_mag<rA>(wK[nw], wK[cwi], spk), cfkv::quad_signs<rA>(wK[6])));
-            put_k(q0 + 1, sm_to_offset_binary(cfkv::quad_mag<rB>(wK[nw], wK[cwi], spk), cfkv::quad_signs<rB>(wK[6])));
-            put_v(q0, sm_to_offset_binary(cfkv::quad_mag<rA>(wV[nw], wV[cwi], spv), cfkv::quad_signs<rA>(wV[6])));
-            put_v(q0 + 1, sm_to_offset_binary(cfkv::quad_mag<rB>(wV[nw], wV[cwi], spv), cfkv::quad_signs<rB>(wV[6])));
+            put(q0, sm_to_offset_binary(cfkv::quad_mag<rA>(wr[nw], wr[cwi], sp), cfkv::quad_signs<rA>(wr[6])));
+            put(q0 + 1, sm_to_offset_binary(cfkv::quad_mag<rB>(wr[nw], wr[cwi], sp), cfkv::quad_signs<rB>(wr[6])));
           }(),
           ...);
     }(std::make_integer_sequence<int, 4>{});
   }
-  // a group coded on its own ends where the encoder started (2^16 in every lane of both streams) and has consumed
-  // exactly its words
-  const bool ok = xk == 65536u && xv == 65536u && wk == s_w + nk && wv == s_w + nk + nv;
+  // a group coded on its own ends where the encoder started (2^16 in every lane) and has consumed exactly its words
+  const bool ok = x == 65536u && wp == wend;
   return __builtin_amdgcn_ballot_w64(!ok) == 0;
 }
 
@@ -428,6 +412,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   // in order; for fixed-width pages the next chunk's words and scales load while the current chunk computes, so a
   // chunk waits for memory only when the previous one was not fixed-width.
   uint32_t scan_pb = 0, scan_ord = 0;  // wave 0: next descriptor to examine, ordinal of the head's next page there
+  const int32_t *tab_k = nullptr, *tab_v = nullptr;  // the rANS tables staged in s_lut (uniform)
   for (;;) {
     if (wave == 0) {
       // pass 1: which descriptors are this workgroup's (kv head, ordinal % splits), 256 descriptors per step with
@@ -586,6 +571,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       r.vs = vsc[tv + min<uint32_t>(static_cast<uint32_t>(tid) & 31u, nv - 1u)];
       return r;
     };
+    // 16-byte units of a self-contained group blob of head_dim hd after its header: part 0 = lane states and raw
+    // words (RANS) or the symbol words (INT8), part 1 = the RANS word streams; 0 when the header does not describe
+    // such a group (the decode refuses the blob), so that staging never reads past a blob
+    auto blob_units = [&](const uint8_t *b, uint32_t hd, int part) -> uint32_t {
+      const CF_GLOBAL uint8_t *g = cfd::global_ptr(b);
+      const uint32_t codec = *reinterpret_cast<const CF_GLOBAL uint32_t *>(g);
+      const uint32_t cnt = *reinterpret_cast<const CF_GLOBAL uint32_t *>(g + 4);
+      const uint32_t chain = *reinterpret_cast<const CF_GLOBAL uint16_t *>(g + 8);
+      const uint32_t bd = *reinterpret_cast<const CF_GLOBAL uint16_t *>(g + 20);
+      if (bd != hd || hd == 0 || hd > static_cast<uint32_t>(kMaxD) || hd % 16 != 0) return 0u;
+      if (codec == CF_KV_CODEC_INT8) return part ? 0u : 2u * (hd / 4) * 64u * 4u / 16u;
+      const uint32_t words = (cnt & 0xFFFFu) + (cnt >> 16);
+      if (codec != CF_KV_CODEC_RANS_HYBRID || chain != 1 || hd % 32 != 0 || words > CF_KV_RANS_MAX_GROUP_WORDS)
+        return 0u;
+      if (part) return (2u * words + 15u) / 16u;
+      return (cfkv::kStateBytes + 8u * static_cast<uint32_t>(cfkv::raw_words_of(static_cast<int>(hd)))) / 16u;
+    };
+
     uint32_t li = 0, t0 = 0;
     Pre cur = prefetch(0, 0);
     while (li < n) {
@@ -613,6 +616,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
           __syncthreads();  // the previous chunk's readers of s_lut are done
           for (uint32_t i = tid; i < (1u << pg.k_max_code_length); i += kThreads) s_lut[0][i] = pg.k_lut[i];
           for (uint32_t i = tid; i < (1u << pg.v_max_code_length); i += kThreads) s_lut[1][i] = pg.v_lut[i];
+          tab_k = tab_v = nullptr;  // the rANS tables staged there are gone
           klut = s_lut[0];
           vlut = s_lut[1];
         }
@@ -622,12 +626,50 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
           __syncthreads();  // the previous chunk's compute no longer reads the staged tiles
           for (uint32_t dd = tid; dd < kMaxD; dd += kThreads) s_ks[0][dd] = rans ? 1.0f : (dd < phd ? pg.k_scales[dd] : 0.0f);
           if (rans) {
-            if (wave == 0) {
-              uint2(*tab)[cfkv::kSlots] = reinterpret_cast<uint2(*)[cfkv::kSlots]>(&s_lut[0][0]);
-              const bool ok = rans_group_to_lds(reinterpret_cast<const uint8_t *>(pg.k_words),
-                                                reinterpret_cast<const uint2 *>(pg.k_lut),
-                                                reinterpret_cast<const uint2 *>(pg.v_lut), tab, s_w, phd, nt, s_k, s_vt,
-                                                s_kt, s_vs, lane);
+            uint2(*tab)[cfkv::kSlots] = reinterpret_cast<uint2(*)[cfkv::kSlots]>(&s_lut[0][0]);
+            const uint8_t *blob = reinterpret_cast<const uint8_t *>(pg.k_words);
+            const uint32_t codec = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const uint32_t *>(blob));
+            if (codec == CF_KV_CODEC_RANS_HYBRID && (pg.k_lut != tab_k || pg.v_lut != tab_v)) {
+              // the K and V tables as the decoder reads them ({f | c << 16, spread}), staged by every thread; kept
+              // for the next rANS page with the same tables
+              const uint2 *kt = reinterpret_cast<const uint2 *>(pg.k_lut), *vt = reinterpret_cast<const uint2 *>(pg.v_lut);
+              for (uint32_t i = tid; i < cfkv::kSlots; i += kThreads) {
+                const uint2 a = kt[i], b = vt[i];
+                tab[0][i] = uint2{(a.x & 2047u) | (((a.x >> 11) & 2047u) << 16), a.y};
+                tab[1][i] = uint2{(b.x & 2047u) | (((b.x >> 11) & 2047u) << 16), b.y};
+              }
+              tab_k = pg.k_lut;
+              tab_v = pg.v_lut;
+              __syncthreads();
+            }
+            // the blob's body after the header into LDS with every thread's 16-byte loads in flight together:
+            // states and raw words (or INT8 symbol words) into the P tile's bytes (free until this chunk's compute),
+            // the word streams into s_w; a header that does not describe a group of this head_dim stages nothing
+            // (the decode refuses it), so no byte past a blob is read
+            static_assert(sizeof(s_p) >= kStageA * kThreads * 16, "an rANS page body fits the P tile");
+            static_assert(sizeof(s_w) >= 2 * CF_KV_RANS_MAX_GROUP_WORDS && kThreads * 16 >= 2 * CF_KV_RANS_MAX_GROUP_WORDS,
+                          "one 16-byte unit per thread stages the word streams");
+            uint32_t *sa = reinterpret_cast<uint32_t *>(&s_p[0][0][0][0]);
+            {
+              const uint32_t ua = blob_units(blob, phd, 0), uw = blob_units(blob, phd, 1);
+              typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+              const CF_GLOBAL u32x4 *g16 = cfd::global_ptr(reinterpret_cast<const u32x4 *>(blob + cfkv::kHdr));
+              if (ua) {  // uniform
+                u32x4 v[kStageA];
+#pragma unroll
+                for (int k = 0; k < kStageA; ++k) v[k] = g16[min<uint32_t>(tid + kThreads * k, ua - 1)];
+                u32x4 vw = v[0];
+                if (uw) vw = g16[ua + min<uint32_t>(tid, uw - 1)];  // uniform
+#pragma unroll
+                for (int k = 0; k < kStageA; ++k)
+                  if (tid + kThreads * k < ua) reinterpret_cast<u32x4 *>(sa)[tid + kThreads * k] = v[k];
+                if (static_cast<uint32_t>(tid) < uw) reinterpret_cast<u32x4 *>(s_w)[tid] = vw;
+              }
+            }
+            __syncthreads();
+            if (wave < 2) {  // wave 0 decodes K, wave 1 V
+              const bool ok = rans_stream_to_lds(blob, sa, tab[wave], s_w, phd, nt, s_k, s_vt, wave ? s_vs : s_kt, lane,
+                                                 static_cast<uint32_t>(wave));
               if (!ok && lane == 0) s_bad = 1;
             }
           } else {
