@@ -681,7 +681,72 @@ def bench_seam(steps: int, warmup: int, shapes=((64, 4096), (64, 65536), (128, 4
                                "x_vs_reference": 2528e-6 / t, "max_abs_err_last_row": err}
         ad.close()
         del pages
+    out["rans_pages"] = bench_seam_rans(steps, warmup)
     return out
+
+
+def bench_seam_rans(steps: int, warmup: int, hd: int = 128, n: int = 65536) -> dict:
+    """The same seam call over rANS pages (the seam's rANS tag, kv_cuda.h: fixed_code_length == 0 and
+    k_max_code_length == 0): every 64 tokens of a KV head one kv_codec_ext.h RANS_HYBRID group coded on its own,
+    the head's pages sharing one K and one V table. Gate: the last query row against the float64 oracle over the
+    values the oracle decodes from every group."""
+    import ctypes as C
+    import torch
+    import oracle as O
+    from chromofold_amd import _abi as A
+    from chromofold_amd import kv, legacy
+
+    kvh, qh, gqa, qn = 2, 14, 7, 64
+    rng = np.random.default_rng(0x5EB + n + hd)
+    ng = n // 64
+    descs = (A.cf_kv_device_page * (kvh * ng))()
+    keep, pages, coded = [], [], 0
+    for h in range(kvh):
+        K = rng.standard_normal((n // 16, 16, hd)).astype(np.float32)
+        V = rng.standard_normal((n // 16, 16, hd)).astype(np.float32)
+        tables = np.concatenate([kv.build_table(K[:256]), kv.build_table(V[:256])])
+        blob, offs = kv.encode_groups(kv.CODEC_RANS_HYBRID, K, V, hd, tables, np.arange(ng, dtype=np.uint64) * 4,
+                                      np.full(ng, 4, np.uint32))
+        coded += blob.size + tables.size
+        dpool = torch.from_numpy(blob).to("cuda:0")
+        dtab = torch.from_numpy(tables).to("cuda:0")
+        keep += [dpool, dtab]
+        ends = list(offs[1:].astype(np.int64) * 16) + [blob.size]
+        for g in range(ng):
+            d = descs[h * ng + g]
+            d.k_words = dpool.data_ptr() + int(offs[g]) * 16
+            d.k_lut, d.v_lut = dtab.data_ptr(), dtab.data_ptr() + kv.TABLE_BYTES
+            d.token_begin, d.token_count, d.head_dim, d.block_size = 64 * g, 64, hd, 64
+            d.zero_point, d.kv_head = 128, h
+            ks, vs, ksc, vsc, _ = O.kv_decode_group(blob[int(offs[g]) * 16:ends[g]], tables, 0, hd)
+            kd = np.concatenate([(ks[p].astype(np.float32) - 128) * ksc[p] for p in range(4)])
+            vd = np.concatenate([(vs[p].astype(np.float32) - 128) * vsc[p] for p in range(4)])
+            pages.append((h, 64 * g, kd, vd))
+    dd = torch.from_numpy(np.frombuffer(bytes(descs), np.uint8).copy()).to("cuda:0")
+    q = torch.from_numpy(rng.standard_normal((qn, qh, hd)).astype(np.float32)).to("cuda:0")
+    o = torch.empty_like(q)
+    desc = A.cf_kv_paged_attention_desc()
+    desc.struct_size, desc.abi_version = C.sizeof(A.cf_kv_paged_attention_desc), legacy.CF_KV_CUDA_ABI_VERSION
+    desc.pages, desc.page_count, desc.kv_head_count = dd.data_ptr(), kvh * ng, kvh
+    desc.query_head_count, desc.gqa_group_size = qh, gqa
+    desc.queries, desc.output = q.data_ptr(), o.data_ptr()
+    desc.query_token_begin, desc.query_count, desc.head_dim = n - qn, qn, hd
+    desc.softmax_scale = 1.0 / np.sqrt(hd)
+    s = torch.cuda.current_stream().cuda_stream
+    run = lambda: A.check(A.lib().cf_kv_paged_attention_async(C.byref(desc), s), "cf_kv_paged_attention_async")  # noqa: E731
+    run()
+    torch.cuda.synchronize()
+    ref, _ = O.paged_attention_f64(q[qn - 1].cpu().numpy(), qh, kvh, hd, gqa, n - 1, 0, desc.softmax_scale, pages)
+    err = float(np.abs(o[qn - 1].cpu().numpy() - ref).max())
+    assert err <= 2e-4, err
+    _, per = _events_time(run, steps, warmup)
+    t = float(np.median(per)) * 1e-3
+    nbytes = coded + C.sizeof(A.cf_kv_device_page) * kvh * ng + 2 * q.numel() * 4
+    del keep
+    return {"workload": f"seam over rANS pages: 2 KV / 14 q heads, 64 queries, hd {hd}, {n} tokens, one self-coded "
+                        "64-token RANS_HYBRID group per page, one K and one V table per head",
+            "us": t * 1e6, "coded_bytes": coded, "bits_per_value": 8.0 * coded / (2 * kvh * n * hd),
+            "gbs": nbytes / t / 1e9, "roofline_frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "max_abs_err_last_row": err}
 
 
 def bench_c5(steps: int, warmup: int) -> dict:
