@@ -115,6 +115,26 @@ __device__ __forceinline__ int nibble_width_sum(uint32_t x) {
 
 __device__ __forceinline__ int width_of(int k) { return static_cast<int>((kWidthNibbles >> (4 * k)) & 15u); }
 
+// Max / sum over the 16 lanes of a row (every lane of the row gets the result) with DPP moves inside the row:
+// quad_perm [1,0,3,2], [2,3,0,1], then row_half_mirror and row_mirror (a ds_bpermute per step would put an LDS
+// round trip on a softmax's dependency chain).
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_max(float x) {
+  x = fmaxf(x, dpp_row<0xb1>(x));
+  x = fmaxf(x, dpp_row<0x4e>(x));
+  x = fmaxf(x, dpp_row<0x141>(x));
+  return fmaxf(x, dpp_row<0x140>(x));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_row<0xb1>(x);
+  x += dpp_row<0x4e>(x);
+  x += dpp_row<0x141>(x);
+  return x + dpp_row<0x140>(x);
+}
+
 // Global-address-space view of a generic pointer (one read from a struct or from LDS): its loads become global_load
 // (vmcnt only) instead of flat_load, which also counts in lgkmcnt, so that every wait for an LDS access would wait
 // for those loads too.

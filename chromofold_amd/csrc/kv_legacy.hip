@@ -202,26 +202,6 @@ __device__ __forceinline__ float4_t mfma16(half4_t a, half4_t b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
-// Max / sum over the 16 lanes of a row (every lane of the row gets the result) with DPP moves inside the row:
-// quad_perm [1,0,3,2], [2,3,0,1], then row_half_mirror and row_mirror (a ds_bpermute per step would put an LDS
-// round trip on the softmax's dependency chain: 8 per row and chunk).
-template <int CTRL>
-__device__ __forceinline__ float dpp_row(float x) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
-}
-__device__ __forceinline__ float row16_max(float x) {
-  x = fmaxf(x, dpp_row<0xb1>(x));
-  x = fmaxf(x, dpp_row<0x4e>(x));
-  x = fmaxf(x, dpp_row<0x141>(x));
-  return fmaxf(x, dpp_row<0x140>(x));
-}
-__device__ __forceinline__ float row16_sum(float x) {
-  x += dpp_row<0xb1>(x);
-  x += dpp_row<0x4e>(x);
-  x += dpp_row<0x141>(x);
-  return x + dpp_row<0x140>(x);
-}
-
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -325,7 +305,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   auto softmax_chunk = [&](float (&s)[4][4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float mx = row16_max(fmaxf(fmaxf(s[i][0], s[i][1]), fmaxf(s[i][2], s[i][3])));
+      const float mx = cfd::row16_max(fmaxf(fmaxf(s[i][0], s[i][1]), fmaxf(s[i][2], s[i][3])));
       const float mn = fmaxf(m_run[i], mx);
       const float alpha = (m_run[i] == -INFINITY) ? 0.0f : __expf(m_run[i] - mn);
       float ps = 0.0f;
@@ -334,7 +314,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         s[i][j] = (s[i][j] == -INFINITY) ? 0.0f : __expf(s[i][j] - mn);
         ps += s[i][j];
       }
-      ps = row16_sum(ps);
+      ps = cfd::row16_sum(ps);
       if (mn != -INFINITY) {
         l_run[i] = l_run[i] * alpha + ps;
 #pragma unroll
