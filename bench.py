@@ -749,6 +749,67 @@ def bench_seam_rans(steps: int, warmup: int, hd: int = 128, n: int = 65536) -> d
             "gbs": nbytes / t / 1e9, "roofline_frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "max_abs_err_last_row": err}
 
 
+def bench_runtime(steps: int, warmup: int, items: int = 32, context: int = 4096, kvh: int = 8, gqa: int = 4,
+                  hd: int = 128, page: int = 32, block: int = 32) -> dict:
+    """The batched-items decode contract (cf_attention_execute_async, reference production_attention.h): `items`
+    decode requests in one call, each over its own device table of `context / page` two's-complement int4 pages
+    ([token][kv head][dim], one scale per `block` values of a row), fp32 query and output, no tail. Pages hold
+    random nibbles and scales generated on the device. Gate: item 0 against the float64 oracle."""
+    import ctypes as C
+    import torch
+    import oracle as O
+    from chromofold_amd import sealkv as S
+
+    qh, npg = kvh * gqa, context // page
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(0xA77E)
+    pay_bytes = page * kvh * hd // 2
+    nsc = page * kvh * ((hd + block - 1) // block)
+    kp = torch.randint(0, 256, (items, npg, pay_bytes), generator=gen, device="cuda:0", dtype=torch.uint8)
+    vp = torch.randint(0, 256, (items, npg, pay_bytes), generator=gen, device="cuda:0", dtype=torch.uint8)
+    ks = torch.rand((items, npg, nsc), generator=gen, device="cuda:0") * 0.3 + 0.05
+    vs = torch.rand((items, npg, nsc), generator=gen, device="cuda:0") * 0.3 + 0.05
+    q = torch.randn((items, qh, hd), generator=gen, device="cuda:0")
+    out = torch.full_like(q, float("nan"))
+    tables = []
+    arr = (S.cf_attention_batch_item * items)()
+    for i in range(items):
+        descs = (S.cf_device_page_descriptor * npg)()
+        for p in range(npg):
+            d = descs[p]
+            d.key_payload, d.value_payload = kp[i, p].data_ptr(), vp[i, p].data_ptr()
+            d.key_scales, d.value_scales = ks[i, p].data_ptr(), vs[i, p].data_ptr()
+            d.token_begin, d.token_count, d.kv_head_count, d.head_dim, d.block_size = p * page, page, kvh, hd, block
+        t = torch.frombuffer(bytearray(descs), dtype=torch.uint8).to("cuda:0")
+        tables.append(t)
+        it = arr[i]
+        it.sequence_id, it.layer = i, 0
+        it.query = S.cf_device_tensor_view(q[i].data_ptr(), S.CF_DEVICE_F32, 1, qh, hd, 0, hd * 4, 4, 0)
+        it.output, it.output_type = out[i].data_ptr(), S.CF_DEVICE_F32
+        it.output_head_stride_bytes, it.output_element_stride_bytes = hd * 4, 4
+        it.query_token_begin, it.softmax_scale = context, 1.0 / np.sqrt(hd)
+        it.sealed_pages, it.sealed_page_count = t.data_ptr(), npg
+    rt = S.AttentionRuntime(1, kvh, qh, hd, gqa=gqa, page_size=page, block_size=block)
+    rt.execute(arr)
+    torch.cuda.synchronize()
+    pages = [O.RtPage(kp[0, p].cpu().numpy(), vp[0, p].cpu().numpy(), ks[0, p].cpu().numpy(), vs[0, p].cpu().numpy(),
+                      p * page, page, hd, block) for p in range(npg)]
+    ref = O.rt_attention_f64(q[0].cpu().numpy(), kvh, gqa, context, 0, 1.0 / np.sqrt(hd), pages)
+    got = out[0].double().cpu().numpy()
+    err = float((np.abs(got - ref).max(axis=1) / np.abs(ref).max(axis=1)).max())
+    assert err <= 1e-3, err
+    _, per = _events_time(lambda: rt.execute(arr), steps, warmup)
+    t = float(np.median(per)) * 1e-3
+    nbytes = (kp.numel() + vp.numel() + 4 * (ks.numel() + vs.numel()) + items * npg * C.sizeof(S.cf_device_page_descriptor)
+              + 2 * q.numel() * 4)
+    rt.close()
+    del tables
+    return {"workload": f"{items} items x {context} tokens, {qh} q / {kvh} KV heads, hd {hd}, int4 pages of {page} "
+                        f"tokens, scale blocks of {block}",
+            "us": t * 1e6, "tokens_per_s": items / t, "bytes": int(nbytes), "gbs": nbytes / t / 1e9,
+            "roofline_frac": nbytes / t / 1e9 / HBM_PEAK_GBS, "max_normwise_err_item0": err}
+
+
 def bench_c5(steps: int, warmup: int) -> dict:
     """C4 shapes (8 KV / 32 q heads, hd 128, rANS-hybrid pages). (a) 256 sequences sharing one 8192-token prefix
     (stored once, referenced by every sequence's page table) plus 512 unique tokens each; (b) 4 sequences x 131072
@@ -861,7 +922,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="auto", choices=["auto", "kv", "kv32", "rrr", "copy", "c5", "seal",
-                                                                  "nibble", "gather", "seam", "fm", "qw"])
+                                                                  "nibble", "gather", "seam", "fm", "qw",
+                                                                  "runtime"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--warm-s", type=float, default=3.0,
                     help="seconds of untimed back-to-back launches before the timed KV steps (0 for counter runs)")
@@ -896,6 +958,9 @@ def main() -> int:
     if args.workload == "seam":
         print(json.dumps({"seam": bench_seam(args.steps, args.warmup)}))
         return 0
+    if args.workload == "runtime":
+        print(json.dumps({"attention_runtime": bench_runtime(args.steps, args.warmup)}))
+        return 0
     if args.workload == "gather":
         print(json.dumps({"gather": bench_gather(args.steps, args.warmup)}))
         return 0
@@ -926,6 +991,7 @@ def main() -> int:
             secondary["nibble_pages"] = bench_nibble(min(args.steps, 20), 2, cpu=not args.no_cpu)
             secondary["gathers"] = bench_gather(min(args.steps, 20), 2)
             secondary["seam"] = bench_seam(min(args.steps, 20), 2)
+            secondary["attention_runtime"] = bench_runtime(min(args.steps, 20), 2)
             peaks = bench_cache_peaks()
             secondary["cache_peaks"] = peaks
             l2 = peaks["l2_read_gbs"]
