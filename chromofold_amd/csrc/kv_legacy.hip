@@ -573,7 +573,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     Pre cur = prefetch(0, 0);
     while (li < n) {
       const uint4 mt = s_pmeta[li];
-      const uint32_t tb = __builtin_amdgcn_readfirstlane(mt.x), tc = __builtin_amdgcn_readfirstlane(mt.y);
       const uint32_t phd = __builtin_amdgcn_readfirstlane(mt.z), mw = __builtin_amdgcn_readfirstlane(mt.w);
       const uint32_t kind = mw >> 16;
       if (kind != 0) {
