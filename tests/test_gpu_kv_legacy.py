@@ -211,3 +211,44 @@ def test_many_rows_long_context_splits(dev, hd):
     assert np.abs(got - ref).max() <= ABS_TOL
     got, ref = _run(dev, deq, pages, q, kvh, gqa, T - 100, 1 / np.sqrt(hd), window=300, tail=(T, tail_k, tail_v))
     assert np.abs(got - ref).max() <= ABS_TOL
+
+
+def _zp_page(k, v, kv_head, token_begin, zp):
+    """An int4 fixed-width page whose codes sit around zero point `zp` instead of 8: the fixture's symbols (q + 8,
+    q in [-7, 7]) moved by zp - 8, so the page dequantises to the same values."""
+    ks, vs, ksc, vsc, kd, vd = O.kv_fixture_quantize(k, v, 4)
+    assert ks.min() >= 8 - zp and vs.min() >= 8 - zp and ks.max() <= 23 - zp
+    page, _, _ = fixed_page(k, v, kv_head, token_begin, 4)
+    page.k_words = O.pack_fixed((ks.astype(np.int64) - (8 - zp)).astype(ks.dtype), 4)
+    page.v_words = O.pack_fixed((vs.astype(np.int64) - (8 - zp)).astype(vs.dtype), 4)
+    page.zero_point = zp
+    for words, sym in ((page.k_words, ks), (page.v_words, vs)):
+        got = O.huffman_decode(words, page.k_lut, 4, 0, sym.size).astype(np.int64)
+        assert np.array_equal(got - zp, sym.reshape(-1).astype(np.int64) - 8)  # same signed codes, other offset
+    return page, kd, vd
+
+
+def test_fixed_pages_paired_with_their_own_zero_points(dev):
+    """Consecutive fixed-width pages of 32 tokens or fewer share one 64-token chunk of the seam kernel (two halves,
+    each with its page's zero point, K scales and positions); pages of more than 32 tokens fill both halves
+    themselves. Pages of 16 tokens alternating zero points 8 and 7, a 5-token page, a 40-token page and a 23-token
+    page, 2 KV heads, GQA 7, many query rows; bar 2e-6 (fp32-grade, the values are exact)."""
+    rng = np.random.default_rng(515)
+    kvh, gqa, D = 2, 7, 64
+    pages, deq = [], []
+    for h in range(kvh):
+        tok = 0
+        for i, n in enumerate((16, 16, 16, 5, 16, 40, 16, 23, 16)):
+            k = rng.standard_normal((n, D)).astype(np.float32)
+            v = rng.standard_normal((n, D)).astype(np.float32)
+            page, kd, vd = _zp_page(k, v, h, tok, 8 if i % 2 == 0 else 7)
+            pages.append(page)
+            deq.append((h, tok, kd, vd))
+            tok += n
+    T = tok
+    q = rng.standard_normal((24, kvh * gqa, D)).astype(np.float32)
+    got, ref = _run(dev, deq, pages, q, kvh, gqa, T - 24, 1 / np.sqrt(D))
+    assert np.isfinite(got).all()
+    assert np.abs(got - ref).max() <= 2e-6
+    got, ref = _run(dev, deq, pages, q, kvh, gqa, T - 24, 1 / np.sqrt(D), window=50)
+    assert np.abs(got - ref).max() <= 2e-6
