@@ -197,8 +197,10 @@ def bench_fm(steps: int, warmup: int, cpu: bool = True) -> dict:
 def bench_qw(steps: int, warmup: int, batches=(1, 4, 16, 64), codecs=("huffman", "rans")) -> dict:
     """4096 x 4096 int4 weights (N(0,1), per (row, 64-col) absmax), per-band Huffman or pair-rANS tables, bf16 x:
     y = x W^T. Roofline per batch: bytes = coded matrix + x + y over the per-call time (HBM-bound at small B)."""
+    import ctypes as C
     import torch
     import oracle as O
+    from chromofold_amd import _abi as A
     from chromofold_amd import qw, synth
 
     M = K = 4096
@@ -225,28 +227,65 @@ def bench_qw(steps: int, warmup: int, batches=(1, 4, 16, 64), codecs=("huffman",
                 assert err <= 1e-3, (name, B, err)
             # One call takes a few us, about what Python needs to issue it, so per-call events would time the host.
             # Instead REPS back-to-back calls are captured in a graph (as a model's forward pass would issue them)
-            # and each replay is timed; every replay must reproduce the eager result bit for bit.
+            # and `steps` replays run back to back between one pair of events, the start event queued behind a
+            # first replay so that the device never waits for the host to submit the next one (events around each
+            # replay would add the submission gap, ~1 us per call at 20 calls a replay); every replay must
+            # reproduce the eager result bit for bit.
             y_eager = y.clone()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
                 for _ in range(REPS):
                     mat.matmul_into(dx, y)
             torch.cuda.synchronize()
-            _, per = _events_time(g.replay, steps, warmup)
+            _warm(g.replay, warmup, 0.1)  # sustained clocks: ~0.1 s of back-to-back calls first
+            g.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
             assert torch.equal(y, y_eager), "graph replay differs from the eager call"
-            t = float(np.mean(per)) * 1e-3 / REPS
+            t_graph = e0.elapsed_time(e1) * 1e-3 / (steps * REPS)
+            # The same calls as plain stream launches (the C entry point called directly, its arguments prepared
+            # once), steps * REPS of them between one pair of events. A graph's kernel nodes measured ~0.7 us
+            # slower each than stream launches of the same kernel. The stream figure counts only when the host
+            # issues the calls faster than the device runs them (host_us below us_stream, checked here).
+            fn = A.lib().cf_qw_matmul_async
+            args = (C.byref(mat.desc), dx.data_ptr(), y.data_ptr(), B, torch.cuda.current_stream().cuda_stream)
+            bad = 0
+
+            def stream_calls():
+                nonlocal bad
+                for _ in range(REPS):
+                    bad |= fn(*args)
+
+            _warm(stream_calls, warmup, 0.1)
+            n = steps * REPS
+            bad |= fn(*args)
+            e0.record()
+            h0 = time.perf_counter()
+            for _ in range(n):
+                bad |= fn(*args)
+            host = (time.perf_counter() - h0) / n
+            e1.record()
+            torch.cuda.synchronize()
+            assert bad == 0 and torch.equal(y, y_eager), "stream launches differ from the eager call"
+            t_stream = e0.elapsed_time(e1) * 1e-3 / n
+            device_bound = host < 0.8 * t_stream
+            t = min(t_graph, t_stream) if device_bound else t_graph
             byts = h.nbytes + 2 * B * K + 4 * B * M
-            r[f"B{B}"] = {"us": t * 1e6, "gbs": byts / t / 1e9, "frac": byts / t / 1e9 / HBM_PEAK_GBS,
+            r[f"B{B}"] = {"us": t * 1e6, "us_graph": t_graph * 1e6, "us_stream": t_stream * 1e6,
+                          "host_us": host * 1e6, "gbs": byts / t / 1e9, "frac": byts / t / 1e9 / HBM_PEAK_GBS,
                           "tflops": 2.0 * B * M * K / t / 1e12}
         res[name] = r
     return res
 
 
 # ------------------------------------------------------------------------------------------------ paged KV (C4)
-def _sustained_time(fn, steps: int, warmup: int, warm_s: float):
+def _warm(fn, warmup: int, warm_s: float) -> None:
     """Back-to-back launches for at least warm_s seconds (and `warmup` launches) so that the clocks reach the state
-    they hold under continuous load, then `steps` timed launches, each bracketed by events on the launch stream.
-    Returns (wall ms of the timed launches, per-launch ms)."""
+    they hold under continuous load."""
     import torch
     t0 = time.perf_counter()
     n = 0
@@ -255,6 +294,12 @@ def _sustained_time(fn, steps: int, warmup: int, warm_s: float):
             fn()
         n += 20
         torch.cuda.synchronize()
+
+
+def _sustained_time(fn, steps: int, warmup: int, warm_s: float):
+    """_warm, then `steps` timed launches, each bracketed by events on the launch stream.
+    Returns (wall ms of the timed launches, per-launch ms)."""
+    _warm(fn, warmup, warm_s)
     return _events_time(fn, steps, 0)
 
 
