@@ -37,11 +37,12 @@ MEASURED_TRAFFIC = {("kv", 32768, 32): 2.0848e9, ("fm_count", 1 << 24, 1_000_000
 METRIC = "compressed-KV attn decode tokens/s + HBM GB/s fraction; wavelet rank Mq/s"
 
 
-def _events_time(fn, steps: int, warmup: int):
-    """Run fn() warmup times, then `steps` times each bracketed by events; returns (total_ms_wall, per_launch_ms)."""
+def _events_time(fn, steps: int, warmup: int, warm_s: float = 0.05):
+    """Run fn() back to back for at least `warmup` launches and warm_s seconds (clocks at their sustained state),
+    then `steps` times each bracketed by events; returns (total_ms_wall, per_launch_ms)."""
     import torch
-    for _ in range(warmup):
-        fn()
+    if warmup > 0 or warm_s > 0:
+        _warm(fn, warmup, warm_s)
     torch.cuda.synchronize()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     t0 = time.perf_counter()
@@ -300,7 +301,7 @@ def _sustained_time(fn, steps: int, warmup: int, warm_s: float):
     """_warm, then `steps` timed launches, each bracketed by events on the launch stream.
     Returns (wall ms of the timed launches, per-launch ms)."""
     _warm(fn, warmup, warm_s)
-    return _events_time(fn, steps, 0)
+    return _events_time(fn, steps, 0, 0.0)
 
 
 def bench_stream_read(buf, steps: int = 20, warmup: int = 3) -> dict:
