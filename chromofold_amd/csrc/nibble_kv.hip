@@ -30,6 +30,7 @@
 #include <cstdint>
 
 #include "nibble_kv.hpp"
+#include "nibble_page.hpp"
 
 namespace cfnib {
 
@@ -296,13 +297,29 @@ __global__ __launch_bounds__(256) void nib_attn_kernel(const AttnItem *__restric
     for (int e = 0; e < 8; ++e) st.acc[j][e] = 0.0f;
   }
 
-  const uint32_t page_splits = it.page_splits;
-  if (it.mfma_nb && split < page_splits) return;  // the MFMA kernel reads these pages
+  // splits [0, vbase) are the MFMA kernel's, then vsplits page splits of this kernel, then the active page
+  const uint32_t vbase = it.mfma_nb ? it.page_splits : 0u;
+  if (split < vbase) return;  // the MFMA kernel reads these pages
   const uint32_t words_per_token = kvh * (D / 8u);
   const uint32_t lane_word = h * (D / 8u) + c;
-  if (split < page_splits) {
-    const uint32_t p_end = min(it.page_count, (split + 1u) * it.units_per_split);
-    for (uint32_t p = split * it.units_per_split; p < p_end; ++p) {
+  if (split < vbase + it.vsplits) {
+    const uint32_t p0 = (split - vbase) * it.vunits;
+    const uint32_t p_end = min(it.page_count, p0 + it.vunits);
+    // with the MFMA kernel on the request, only the pages it refuses: each lane of a wave tests one page of the
+    // split (vunits <= 64), and the wave's ballot is the same in every wave of the workgroup
+    uint64_t mine = ~0ull;
+    if (it.mfma_nb) {
+      const uint32_t pl = p0 + (threadIdx.x & 63u);
+      bool refused = false;
+      if (pl < p_end) {
+        const cf_device_page_descriptor &q = it.pages[pl];
+        refused = !mfma_page_ok(q.key_payload, q.value_payload, q.key_scales, q.value_scales, q.block_size,
+                                q.head_dim, q.token_count, it.mfma_cap);
+      }
+      mine = __ballot(refused);
+    }
+    for (uint32_t p = p0; p < p_end; ++p) {
+      if (!((mine >> (p - p0)) & 1ull)) continue;  // wave-uniform
       const cf_device_page_descriptor &pg = it.pages[p];
       const uint32_t tcount = pg.token_count, tbegin = pg.token_begin, bs = pg.block_size;
       const uint32_t *kw = reinterpret_cast<const uint32_t *>(pg.key_payload);
@@ -504,7 +521,10 @@ hipError_t AttnRunner::run(const std::vector<AttnRequest> &reqs, const AttnShape
   std::vector<uint32_t> nb(reqs.size());
   for (size_t i = 0; i < reqs.size(); ++i) {
     const auto &r = reqs[i];
-    nb[i] = r.flags ? 0u : mfma_sets(D, r.block_size);
+    // batched-items requests (the contract's three flags) run on the MFMA kernel in its per-page mode when
+    // head_dim is 128 and pages have a planned size; other flagged requests stay on the VALU kernel
+    nb[i] = r.flags == kContractFlags ? (D == 128u && cpp > 0u ? kMfmaContract : 0u)
+                                      : r.flags ? 0u : mfma_sets(D, r.block_size);
     if (nb[i]) tile_work += uint64_t((r.page_count * cpp + 3u) / 4u) * r.query.token_count * ((sh.gqa + 3u) / 4u);
     else page_work += uint64_t(r.page_count) * r.query.token_count * hgroups * qchunks;
   }
@@ -517,6 +537,7 @@ hipError_t AttnRunner::run(const std::vector<AttnRequest> &reqs, const AttnShape
   uint64_t floats = 0;
   uint32_t max_split = 1, max_qtok = 1, max_mfma_split = 0;
   bool any_nb[5] = {false, false, false, false, false};
+  const uint32_t wave_lanes = std::min(64u, hw * lg);  // lanes of the VALU kernel's first wave
   for (size_t i = 0; i < reqs.size(); ++i) {
     const AttnRequest &r = reqs[i];
     AttnItem &it = items[i];
@@ -540,9 +561,15 @@ hipError_t AttnRunner::run(const std::vector<AttnRequest> &reqs, const AttnShape
       it.page_splits = (tiles + tps - 1u) / tps;
       max_mfma_split = std::max(max_mfma_split, it.page_splits);
       any_nb[nb[i]] = true;
+      it.vunits = nb[i] == kMfmaContract ? wave_lanes : 0u;  // one lane per page tests it
+      it.vsplits = it.vunits ? (r.page_count + it.vunits - 1u) / it.vunits : 0u;
+      it.mfma_cap = 16u * cpp;
     } else {
       it.units_per_split = pps;
       it.page_splits = (r.page_count + pps - 1u) / pps;
+      it.vunits = pps;
+      it.vsplits = it.page_splits;
+      it.mfma_cap = 0u;
     }
     it.active_k = r.active_k;
     it.active_v = r.active_v;
@@ -552,7 +579,7 @@ hipError_t AttnRunner::run(const std::vector<AttnRequest> &reqs, const AttnShape
     it.window = r.window;
     it.scale_log2 = r.softmax_scale * 1.4426950408889634f;
     it.flags = r.flags;
-    it.nsplit = it.page_splits + (it.active_count > 0u ? 1u : 0u);
+    it.nsplit = (it.mfma_nb ? it.page_splits : 0u) + it.vsplits + (it.active_count > 0u ? 1u : 0u);
     if (it.nsplit == 0u) it.nsplit = 1u;  // nothing visible: one empty split, the row comes out 0
     it.ws_offset = floats;
     floats += uint64_t(it.nsplit) * it.q_tokens * sh.q_heads * (D + 4u);
@@ -599,7 +626,7 @@ hipError_t AttnRunner::run(const std::vector<AttnRequest> &reqs, const AttnShape
     default: e = launch_attn_lg<32>(G, grid, block, stream, d_items, sh, hw, hgroups, qchunks, partials); break;
   }
   if (e != hipSuccess) return e;
-  for (uint32_t n : {1u, 2u, 4u}) {
+  for (uint32_t n : {1u, 2u, kMfmaContract, 4u}) {
     if (!any_nb[n]) continue;
     e = launch_nib_mfma(n, d_items, static_cast<uint32_t>(items.size()), max_mfma_split, max_qtok, sh, partials,
                         stream);

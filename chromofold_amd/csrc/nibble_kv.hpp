@@ -59,7 +59,12 @@ struct AttnItem {
   uint32_t page_count;
   uint32_t units_per_split;  // pages (VALU kernel) or 64-token tiles (MFMA kernel) per context split
   uint32_t page_splits;      // splits over the sealed pages; split page_splits is the active page (when present)
-  uint32_t mfma_nb;          // 0: the VALU kernel reads the pages; 1/2/4: the MFMA kernel, scale blocks per row
+  uint32_t mfma_nb;          // 0: the VALU kernel reads the pages; 1/2/4: the MFMA kernel, scale blocks per row;
+                             // kMfmaContract: the MFMA kernel reads the pages mfma_page_ok accepts (nibble_page.hpp)
+  uint32_t vsplits;          // splits of the VALU kernel over the pages, after the MFMA kernel's page_splits (none
+                             // for 1/2/4; for kMfmaContract they take only the pages the MFMA kernel refuses)
+  uint32_t vunits;           // pages per VALU split (at most 64)
+  uint32_t mfma_cap;         // kMfmaContract: tokens a page may hold on the MFMA path (16 per planned chunk)
   const float *active_k;
   const float *active_v;
   uint32_t active_begin, active_count;
@@ -73,6 +78,11 @@ struct AttnShape {
   uint32_t kv_heads, q_heads, gqa, head_dim;
   uint32_t page_size;  // tokens per page (pages may hold fewer)
 };
+
+// mfma_nb of a batched-items request (all three flags above) on the MFMA path: block size per page, read on the
+// device; the kernel runs with one scale per 32-dim quarter of a row.
+constexpr uint32_t kContractFlags = kSignedNibbles | kOpenWindow | kRowBlocks;
+constexpr uint32_t kMfmaContract = 3u;
 
 // Scale blocks per 128-dim row for the MFMA path (0 = not eligible): block_size 32 / 64 / any multiple of 128.
 inline uint32_t mfma_sets(uint32_t head_dim, uint32_t block_size) {

@@ -29,6 +29,7 @@
 
 #include "cf_device.hpp"
 #include "nibble_kv.hpp"
+#include "nibble_page.hpp"
 
 namespace cfnib {
 namespace {
@@ -107,14 +108,21 @@ __device__ inline void wave_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int NB>
+// MODE 1 / 2 / 4: sealed pages with that many scale blocks per row (block size known for the request).
+// MODE kMfmaContract: a batched-items request (two's-complement nibbles, per-row scale blocks, no causal bound and
+// an inclusive window): each page's own block size (a multiple of 32) gives one scale per 32-dim quarter of a row,
+// and pages that mfma_page_ok refuses are left to the VALU kernel.
+template <int MODE>
 __global__ __launch_bounds__(256) void nib_mfma_kernel(const AttnItem *__restrict__ items, AttnShape sh,
                                                        uint32_t qchunks, float *__restrict__ ws) {
+  constexpr bool PG = MODE == static_cast<int>(kMfmaContract);
+  constexpr int NB = PG ? 4 : MODE;
+  constexpr uint32_t sx = PG ? 0x88888888u : 0u;  // two's-complement nibbles -> offset-8 (n ^ 8 = n + 8 mod 16)
   __shared__ __attribute__((aligned(16))) uint8_t s_kv[kWaves][2][2][kTileBytes];  // [wave][buffer][K, V]
   __shared__ __attribute__((aligned(16))) float s_p[kWaves][4][64];                // p per [head][slot]
   __shared__ float s_vs[kWaves][64][NB];                                           // V scales per slot
   const AttnItem &it = items[blockIdx.z];
-  if (it.mfma_nb != static_cast<uint32_t>(NB)) return;
+  if (it.mfma_nb != static_cast<uint32_t>(MODE)) return;
   const uint32_t split = blockIdx.x;
   if (split >= it.page_splits) return;
   const uint32_t kvh = sh.kv_heads, gqa = sh.gqa;
@@ -190,6 +198,11 @@ __global__ __launch_bounds__(256) void nib_mfma_kernel(const AttnItem *__restric
         d.kp[C] = gp[p].key_payload;
         d.vp[C] = gp[p].value_payload;
         d.tc[C] = gp[p].token_count;
+        if constexpr (PG) {  // a refused page: no tokens here (the VALU kernel reads it)
+          if (!mfma_page_ok(d.kp[C], d.vp[C], gp[p].key_scales, gp[p].value_scales, gp[p].block_size,
+                            gp[p].head_dim, d.tc[C], it.mfma_cap))
+            d.tc[C] = 0u;
+        }
       }
     }
     const uint32_t mine = 4u * tile + G;
@@ -226,14 +239,26 @@ __global__ __launch_bounds__(256) void nib_mfma_kernel(const AttnItem *__restric
     if (mine < nchunks && off < my_tc) {
       const uint32_t tok = off + static_cast<uint32_t>(t);
       const uint32_t pos = d.tb + tok;
-      n_ok = tok < my_tc && pos <= qpos && (window == 0u || uint64_t(pos) + window > qpos);
       const uint32_t row = min(tok, my_tc - 1u) * kvh + h;  // token-head row of the page
-      // first scale of the row: block = row * 128 / block_size (block_size 32 / 64 / a multiple of 128)
-      const uint32_t bi = NB == 4 ? row * 4u : NB == 2 ? row * 2u : row / (d.bs / 128u);
+      if constexpr (PG) {
+        n_ok = tok < my_tc && (window == 0u || uint64_t(pos) + window >= qpos);
+        // ceil(128 / block_size) blocks per row; quarter s (dims 32 s .. 32 s + 31) lies in block 32 s / block_size
+        const uint32_t bs = d.bs, rb = row * ((128u + bs - 1u) / bs);
 #pragma unroll
-      for (int s = 0; s < NB; ++s) {
-        n_ks[s] = gptr(d.ks)[bi + s];
-        n_vs[s] = gptr(d.vs)[bi + s];
+        for (int s = 0; s < 4; ++s) {
+          const uint32_t bi = rb + (32u * s) / bs;
+          n_ks[s] = gptr(d.ks)[bi];
+          n_vs[s] = gptr(d.vs)[bi];
+        }
+      } else {
+        n_ok = tok < my_tc && pos <= qpos && (window == 0u || uint64_t(pos) + window > qpos);
+        // first scale of the row: block = row * 128 / block_size (block_size 32 / 64 / a multiple of 128)
+        const uint32_t bi = NB == 4 ? row * 4u : NB == 2 ? row * 2u : row / (d.bs / 128u);
+#pragma unroll
+        for (int s = 0; s < NB; ++s) {
+          n_ks[s] = gptr(d.ks)[bi + s];
+          n_vs[s] = gptr(d.vs)[bi + s];
+        }
       }
     }
   };
@@ -274,8 +299,9 @@ __global__ __launch_bounds__(256) void nib_mfma_kernel(const AttnItem *__restric
       uint4 pc[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) pc[k] = *reinterpret_cast<const uint4 *>(kb + 16 * (k ^ (t & 3)));
-      const uint32_t w16[16] = {pc[0].x, pc[0].y, pc[0].z, pc[0].w, pc[1].x, pc[1].y, pc[1].z, pc[1].w,
-                                pc[2].x, pc[2].y, pc[2].z, pc[2].w, pc[3].x, pc[3].y, pc[3].z, pc[3].w};
+      const uint32_t w16[16] = {pc[0].x ^ sx, pc[0].y ^ sx, pc[0].z ^ sx, pc[0].w ^ sx, pc[1].x ^ sx, pc[1].y ^ sx,
+                                pc[1].z ^ sx, pc[1].w ^ sx, pc[2].x ^ sx, pc[2].y ^ sx, pc[2].z ^ sx, pc[2].w ^ sx,
+                                pc[3].x ^ sx, pc[3].y ^ sx, pc[3].z ^ sx, pc[3].w ^ sx};
       [&]<int... I>(std::integer_sequence<int, I...>) {
         (
             [&] {
@@ -345,7 +371,8 @@ __global__ __launch_bounds__(256) void nib_mfma_kernel(const AttnItem *__restric
         uint32_t wk[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-          wk[k] = *reinterpret_cast<const uint32_t *>(vb + (4 * tq + k) * kRowBytes + 16 * ((t >> 2) ^ k) + 4 * (t & 3));
+          wk[k] = *reinterpret_cast<const uint32_t *>(vb + (4 * tq + k) * kRowBytes + 16 * ((t >> 2) ^ k) + 4 * (t & 3)) ^
+                  sx;
         half4_t bv[8];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {  // byte j of the four words: dims 8t + 2j (low nibbles), 8t + 2j + 1 (high)
@@ -443,6 +470,7 @@ hipError_t launch_nib_mfma(uint32_t nb, const AttnItem *items, uint32_t nitems, 
   switch (nb) {
     case 1: nib_mfma_kernel<1><<<grid, 256, 0, stream>>>(items, sh, qchunks, ws); break;
     case 2: nib_mfma_kernel<2><<<grid, 256, 0, stream>>>(items, sh, qchunks, ws); break;
+    case kMfmaContract: nib_mfma_kernel<kMfmaContract><<<grid, 256, 0, stream>>>(items, sh, qchunks, ws); break;
     default: nib_mfma_kernel<4><<<grid, 256, 0, stream>>>(items, sh, qchunks, ws); break;
   }
   return hipPeekAtLastError();

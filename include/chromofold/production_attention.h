@@ -26,12 +26,16 @@
  * CF_ATTENTION_REFERENCE mode has no kernel (the call fails and counts a reference launch), as in the reference;
  * cf_attention_compare_async validates its arguments and fails, as in the reference.
  *
- * MI355X build: every item of a call runs in ONE split-context attention launch plus one merge launch from a
- * device item table (the reference: one 32-thread block per (item, query head) reading K and V once per query
- * head). head_dim must be a multiple of 8 and at most 256 (create returns NULL otherwise); payload and scale
+ * MI355X build: every item of a call runs from one device item table in at most three launches (the reference:
+ * one 32-thread block per (item, query head) reading K and V once per query head): with head_dim 128, a
+ * matrix-core kernel reads every page whose payloads are 16-byte aligned, whose block_size is a multiple of 32 and
+ * which holds at most page_size tokens; a VALU kernel reads the other pages (each page is tested on the device by
+ * both kernels, so the host never reads the page table) and the active tail; a merge kernel combines the
+ * context splits. head_dim must be a multiple of 8 and at most 256 (create returns NULL otherwise); payload and scale
  * pointers must be 4-byte aligned. The item table and split partials live in a runtime-owned device workspace
  * grown on demand (allocation_count / pool_* count its growth); calls on one runtime must be ordered on one stream.
- * The tuning fields, cuda_device, use_async_allocator, block_size and page_size are accepted and not used.
+ * The tuning fields, cuda_device, use_async_allocator and block_size are accepted and not used; page_size only
+ * sets the page length the matrix-core kernel plans for (longer pages go to the VALU kernel).
  */
 #ifndef CHROMOFOLD_PRODUCTION_ATTENTION_H
 #define CHROMOFOLD_PRODUCTION_ATTENTION_H

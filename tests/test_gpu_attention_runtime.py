@@ -40,19 +40,22 @@ def _pages(rng, kvh, D, bs, n_pages, page, begin=0, gap=0, amp=1.0):
 class _Dev:
     """Device copies of host pages, page tables and tails; keeps every tensor alive until the call is done."""
 
-    def __init__(self, dev, kvh):
-        self.dev, self.kvh, self.keep = dev, kvh, []
+    def __init__(self, dev, kvh, shifted=()):
+        self.dev, self.kvh, self.keep, self.shifted = dev, kvh, [], set(shifted)
 
-    def tensor(self, a):
+    def tensor(self, a, shift=0):
+        """Device copy of `a`; shift = 4 places it 4 bytes into its allocation (4-byte but not 16-byte aligned)."""
         import torch
         if a is None:
             return 0
         a = np.ascontiguousarray(a)
         if a.dtype == np.uint8 and a.size % 4:  # whole 32-bit words for the kernel's loads
             a = np.concatenate([a, np.zeros(4 - a.size % 4, np.uint8)])
+        if shift:
+            a = np.concatenate([np.zeros(shift, np.uint8), a.view(np.uint8).reshape(-1)])
         t = torch.from_numpy(a).to(self.dev)
         self.keep.append(t)
-        return t.data_ptr()
+        return t.data_ptr() + shift
 
     def table(self, pages):
         import torch
@@ -62,7 +65,8 @@ class _Dev:
         descs = (S.cf_device_page_descriptor * len(pages))()
         for i, p in enumerate(pages):
             d = descs[i]
-            d.key_payload, d.value_payload = self.tensor(p.k_payload), self.tensor(p.v_payload)
+            sh = 4 if i in self.shifted else 0
+            d.key_payload, d.value_payload = self.tensor(p.k_payload, sh), self.tensor(p.v_payload, sh)
             d.key_scales, d.value_scales = self.tensor(p.k_scales), self.tensor(p.v_scales)
             d.token_begin, d.token_count, d.kv_head_count = p.token_begin, p.token_count, self.kvh
             d.head_dim, d.block_size = p.head_dim, p.block_size
@@ -90,7 +94,7 @@ def _item(D_, i, q, out, qpos, scale, window, pages, ak=None, av=None, abegin=0)
     return it
 
 
-def _run(dev, kvh, gqa, D, specs, q_dtype=None, out_dtype=None, layout="contiguous"):
+def _run(dev, kvh, gqa, D, specs, q_dtype=None, out_dtype=None, layout="contiguous", shifted=()):
     """specs: list of (pages, qpos, window, active_k, active_v, active_begin). Returns (got [items, qh, D],
     ref [items, qh, D]) with got in float64."""
     import torch
@@ -99,7 +103,7 @@ def _run(dev, kvh, gqa, D, specs, q_dtype=None, out_dtype=None, layout="contiguo
     out_dtype = out_dtype or torch.float32
     qh = kvh * gqa
     rt = S.AttentionRuntime(1, kvh, qh, D, gqa=gqa, page_size=32, block_size=32)
-    D_ = _Dev(dev, kvh)
+    D_ = _Dev(dev, kvh, shifted)
     rng = np.random.default_rng(D * 7 + len(specs))
     items = (S.cf_attention_batch_item * len(specs))()
     outs, refs = [], []
@@ -211,3 +215,34 @@ def test_invalid_item_fails_the_call_before_any_launch(dev):
     assert not out.any()  # nothing attended: zeros
     assert rt.counters()["optimized_launches"] == 1
     rt.close()
+
+
+def test_matrix_core_and_valu_pages_in_one_request(dev):
+    """head_dim 128 requests run on the matrix-core kernel for every page whose block size is a multiple of 32,
+    whose payloads are 16-byte aligned and which holds at most the runtime's page size (32 tokens); the VALU kernel
+    takes the others (block sizes 16 and 48, a 40-token page, a payload 4 bytes off 16-byte alignment, NULL
+    pages) out of the same page table. Every page must count exactly once: one request over all of them, others
+    over subsets, windows cutting through both kinds, against the float64 oracle."""
+    kvh, gqa, D = 2, 4, 128
+    rng = np.random.default_rng(31)
+    pages, begin = [], 0
+    for bs, n, tok in ((32, 3, 32), (16, 2, 32), (64, 2, 24), (48, 2, 32), (128, 2, 32), (256, 1, 16), (32, 1, 40),
+                       (96, 2, 32)):
+        pages += _pages(rng, kvh, D, bs, n, tok, begin=begin)
+        begin += n * tok
+    p0 = pages[0]
+    null_page = O.RtPage(p0.k_payload, p0.v_payload, None, p0.v_scales, begin, 32, D, 32)
+    pages.append(null_page)
+    shifted = [1, 6]  # page 1 (block size 32) and page 6 (block size 128) start 4 bytes into their allocations
+    ak = rng.standard_normal((6, kvh, D)).astype(np.float32)
+    av = rng.standard_normal((6, kvh, D)).astype(np.float32)
+    specs = [
+        (pages, begin + 40, 0, ak, av, begin + 32),
+        (pages, 200, 90, None, None, 0),          # window from position 110: both kinds on either side
+        (pages[::-1], 400, 0, ak, av, begin + 32),  # table order does not matter
+        (pages[3:9], 150, 0, None, None, 0),
+    ]
+    got, ref, c = _run(dev, kvh, gqa, D, specs, shifted=shifted)
+    assert np.isfinite(got).all()
+    assert head_err(got, ref) <= 2e-5
+    assert c["optimized_launches"] == 1 and c["cuda_errors"] == 0
