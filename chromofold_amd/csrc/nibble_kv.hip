@@ -257,6 +257,9 @@ __global__ __launch_bounds__(256) void nib_attn_kernel(const AttnItem *__restric
   const AttnItem &it = items[blockIdx.z];
   const uint32_t split = blockIdx.x;
   if (split >= it.nsplit) return;
+  // splits [0, vbase) are the MFMA kernel's, then vsplits page splits of this kernel, then the active page
+  const uint32_t vbase = it.mfma_nb ? it.page_splits : 0u;
+  if (split < vbase) return;  // the MFMA kernel reads these pages
   const uint32_t per_tok = hgroups * qchunks;
   const uint32_t qt = blockIdx.y / per_tok;
   if (qt >= it.q_tokens) return;
@@ -297,9 +300,6 @@ __global__ __launch_bounds__(256) void nib_attn_kernel(const AttnItem *__restric
     for (int e = 0; e < 8; ++e) st.acc[j][e] = 0.0f;
   }
 
-  // splits [0, vbase) are the MFMA kernel's, then vsplits page splits of this kernel, then the active page
-  const uint32_t vbase = it.mfma_nb ? it.page_splits : 0u;
-  if (split < vbase) return;  // the MFMA kernel reads these pages
   const uint32_t words_per_token = kvh * (D / 8u);
   const uint32_t lane_word = h * (D / 8u) + c;
   if (split < vbase + it.vsplits) {
@@ -425,18 +425,38 @@ __global__ __launch_bounds__(64) void nib_merge_kernel(const AttnItem *__restric
   float M = kNegInf;
   for (uint32_t s = 0; s < it.nsplit; ++s) M = fmaxf(M, row0[s * split_stride + D]);
   float L = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (M != kNegInf) {
-    for (uint32_t s = 0; s < it.nsplit; ++s) {
-      const float *row = row0 + s * split_stride;
-      const float ms = row[D];
-      if (ms == kNegInf) continue;
-      const float w = __builtin_amdgcn_exp2f(ms - M);
-      L = fmaf(w, row[D + 1], L);
+  // splits in ascending order (the same sums in the same order for any grouping); four splits' loads are issued
+  // together so that their latencies overlap, and a split with nothing attended (m = -inf) changes nothing
+  auto add = [&](float ms, float ls, const float (&v)[4]) {
+    if (ms == kNegInf) return;
+    const float w = __builtin_amdgcn_exp2f(ms - M);
+    L = fmaf(w, ls, L);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t d = lane + 64u * k;
-        if (d < D) o[k] = fmaf(w, row[d], o[k]);
-      }
+    for (int k = 0; k < 4; ++k) o[k] = fmaf(w, v[k], o[k]);
+  };
+  auto load = [&](uint32_t s, float &ms, float &ls, float (&v)[4]) {
+    const float *row = row0 + s * split_stride;
+    ms = row[D];
+    ls = row[D + 1];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t d = lane + 64u * k;
+      v[k] = d < D ? row[d] : 0.0f;
+    }
+  };
+  if (M != kNegInf) {
+    uint32_t s = 0;
+    for (; s + 4u <= it.nsplit; s += 4u) {
+      float ms[4], ls[4], v[4][4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) load(s + u, ms[u], ls[u], v[u]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) add(ms[u], ls[u], v[u]);
+    }
+    for (; s < it.nsplit; ++s) {
+      float ms, ls, v[4];
+      load(s, ms, ls, v);
+      add(ms, ls, v);
     }
   }
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
