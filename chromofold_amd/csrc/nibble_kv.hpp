@@ -39,7 +39,8 @@ hipError_t launch_convert(const cf_device_tensor_view &src, float *dst, uint32_t
 hipError_t launch_clear_status(SealStatus *status, uint32_t count, hipStream_t stream);
 
 // Request flags (AttnRequest::flags, AttnItem::flags); 0 = the sealed-page format and causal visibility above.
-// A flagged request always runs on the VALU kernel.
+// A flagged request runs on the VALU kernel, except one with all three (kContractFlags) at head_dim 128, whose
+// pages the MFMA kernel reads where it can (kMfmaContract).
 constexpr uint32_t kSignedNibbles = 1u;  // payload nibbles are two's-complement int4 (n - 16 for n >= 8)
 constexpr uint32_t kOpenWindow = 2u;     // position p visible unless window > 0 and p + window < query position
                                          // (no causal bound; default: p <= q and, with a window, p + window > q)
@@ -112,7 +113,8 @@ struct AttnRequest {
   uint32_t flags;       // kSignedNibbles | kOpenWindow | kRowBlocks
 };
 
-// Runs a batch of requests: one split-context attention launch over every item, then one merge launch.
+// Runs a batch of requests: the split-context attention launches over every item (the VALU kernel, the MFMA kernel
+// per mfma_nb mode), then one merge launch.
 // Owns a device workspace (item table + split partials) grown on demand; calls must be ordered on one stream.
 class AttnRunner {
  public:
