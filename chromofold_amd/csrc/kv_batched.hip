@@ -11,10 +11,12 @@
 //            the lane ends up holding its token's 4 head scores. Nothing decoded is written anywhere.
 //   softmax: one running max per head for the whole wavefront (so the 4 page groups can be summed at the end),
 //            probabilities times the page's V scale (in units of a power of two per lane, so that the f16 value
-//            neither underflows nor overflows) go to a 512-byte LDS tile.
-//   V phase: lane decodes dims {t + 16i} of page G, 4 tokens per quad, again straight into a 4x4x4 MFMA
-//            (A = probabilities of those 4 tokens for the 4 heads, B = the 4 decoded values as exact signed f16)
-//            accumulating the lane's 4 heads x 8 dims output.
+//            neither underflows nor overflows), split into f16 hi + lo parts, go to two 512-byte LDS tiles.
+//   V phase: lane decodes dims {t + 16i} of page G, 4 tokens per quad, again straight into 4x4x4 MFMAs
+//            (A = the hi, then the lo parts of those 4 tokens' weights for the 4 heads, B = the 4 decoded values
+//            as exact signed f16) accumulating the lane's 4 heads x 8 dims output. With one f16 per weight (11
+//            significant bits) an output made of near-cancelling terms (weights of different pages, whose V scales
+//            differ) would carry an error of ~2^-12 of the terms themselves; hi + lo leaves ~2^-22.
 // Codec decode (format 4): one rANS step per 8 values of a stream (LDS slot table, 64-bit entry = freq/offset +
 // the symbol's 8 big bits spread to their frame positions; SDWA reads the 16-bit freq/offset halves in place); the
 // raw nibble, crumb and sign words of the lane merged with two bit-field inserts and a rotation per quad; two
@@ -126,7 +128,7 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
                                            uint32_t (&st)[2], const uint32_t *__restrict__ raw, WordPtr wk,
                                            uint32_t cnt_kv, const uint2 (*__restrict__ s_tab)[kSlots],
                                            const half4_t *qhi, const half4_t *qlo, const float *qsum,
-                                           _Float16 (*s_pw)[kGqa][16], uint32_t *__restrict__ vl, int lane,
+                                           _Float16 (*s_pw)[4][kGqa][16], uint32_t *__restrict__ vl, int lane,
                                            bool tok_ok, float ks, float vs, int &e_run, float *m_run, float *l_run,
                                            float4_t *acc_v) {
   constexpr int NQ = D / 4, RAW = raw_words<D>();
@@ -257,7 +259,7 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
     const float pr = tok_ok ? __expf(s[h] - mn) : 0.0f;
     l_run[h] = l_run[h] * a + pr;
     alpha[h] = ldexpf(a, de);  // ldexp(0, .) = 0 before the first visible token
-    s_pw[G][h][t] = static_cast<_Float16>(pr * vsn);
+    cfd::split_mul_f16(pr, vsn, s_pw[0][G][h][t], s_pw[1][G][h][t]);
     m_run[h] = mn;
   }
 #pragma unroll
@@ -273,13 +275,14 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
     (
         [&] {
           constexpr int q = Q, tq = q / (D / 16), i = q % (D / 16);  // quad q = tokens 4tq.. at dim t + 16i
-          const half4_t pa = *reinterpret_cast<const half4_t *>(&s_pw[G][lane & 3][4 * tq]);
+          const half4_t pa = *reinterpret_cast<const half4_t *>(&s_pw[0][G][lane & 3][4 * tq]);
+          const half4_t pl = *reinterpret_cast<const half4_t *>(&s_pw[1][G][lane & 3][4 * tq]);
           half4_t bv;
           if constexpr (RANS)  // quad q is quad q % 8 of sign group q / 8
             bv = sm_to_half4(q < KL ? vl[q * 64 + lane] : vb[q], quad_signs<kFrame[q % 8]>(vsg[q / 8]));
           else
             bv = bytes_to_half4_signed(q < KL ? raw[NQ * 64 + q * 64 + lane] : vb[q]);
-          acc_v[i] = mfma4(pa, bv, acc_v[i]);
+          acc_v[i] = mfma4(pl, bv, mfma4(pa, bv, acc_v[i]));
         }(),
         ...);
   }(std::make_integer_sequence<int, NQ>{});
@@ -337,7 +340,7 @@ __global__ CF_KV_OCC __launch_bounds__(64 * W) void kv_batched_kernel(cf_kv_batc
   constexpr bool kWide = W == kWavesWide;           // contiguous weighted pair blocks (else strided pairs)
   constexpr int KL = kWide && RANS ? 16 : 0;        // V quads parked in LDS (see group_body)
   __shared__ uint2 s_tab[RANS ? 2 : 1][kSlots];     // {f | c << 16, spread big bits} per slot, K and V tables
-  __shared__ _Float16 s_p[W][4][kGqa][16];          // per wave: [page][head][token] probability * v_scale
+  __shared__ _Float16 s_p[W][2][4][kGqa][16];       // per wave: [hi, lo][page][head][token] probability * v_scale
   __shared__ uint32_t s_buf[W][BUF];                // per wave: staged words; query staging and partials alias it
   __shared__ uint32_t s_vl[KL ? W : 1][KL ? KL : 1][64];
 
@@ -616,7 +619,8 @@ __global__ CF_KV_OCC __launch_bounds__(64 * W) void kv_batched_kernel(cf_kv_batc
 //   softmax  online per row (its values live in the 4 lanes sharing lane & 15);
 //   P V      those same registers ARE the A operand of the P V product when the k index of a 32-token step is
 //            ordered {4kg + r of page 2s, 4kg + r of page 2s + 1}: no transpose. B = V[those tokens][dim] is two raw
-//            u32 V quads of the INT8 layout as they are; P is pre-multiplied by each page's V scale.
+//            u32 V quads of the INT8 layout as they are; P is pre-multiplied by each page's V scale and split into
+//            f16 hi + lo parts, one MFMA each (one f16 per weight loses near-cancelling outputs).
 // Operands: each group is converted once per workgroup into double-buffered LDS (see the kernel body).
 // A non-INT8 group in the prefix makes the prefix partials NaN, so every output is NaN (the prefix must be raw).
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -796,19 +800,27 @@ __global__ __launch_bounds__(kPfxThreads) void kv_prefix_kernel(cf_kv_batched_de
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt) acc[dt][r] *= ar;
     }
-    // P V over page pairs (2s, 2s + 1)
+    // P V over page pairs (2s, 2s + 1); the weights p * v_scale as f16 hi + lo parts
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
-      half8_t pa;
+      half8_t pa, pl;
       const float v0 = ldexpf(vscale[2 * s2], -ev), v1 = ldexpf(vscale[2 * s2 + 1], -ev);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        pa[r] = static_cast<_Float16>(st[2 * s2][r] * v0);
-        pa[4 + r] = static_cast<_Float16>(st[2 * s2 + 1][r] * v1);
+        _Float16 h, lo;
+        cfd::split_mul_f16(st[2 * s2][r], v0, h, lo);
+        pa[r] = h;
+        pl[r] = lo;
+        cfd::split_mul_f16(st[2 * s2 + 1][r], v1, h, lo);
+        pa[4 + r] = h;
+        pl[4 + r] = lo;
       }
 #pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt)
-        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, s_op[buf][1][8 * s2 + dt][lane], acc[dt], 0, 0, 0);
+      for (int dt = 0; dt < D / 16; ++dt) {
+        const half8_t vb = s_op[buf][1][8 * s2 + dt][lane];
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, acc[dt], 0, 0, 0);
+        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vb, acc[dt], 0, 0, 0);
+      }
     }
     if (g + 1 < gb) store(buf ^ 1);  // the other buffer: every wave finished with it before the last barrier
     __syncthreads();

@@ -35,7 +35,9 @@
 // The dense tail (fp32) takes the same softmax on VALU. Split partials (m, l, acc) go to a per-GPU device array and
 // a second kernel merges them; with one split the workgroup writes the output itself.
 #include <cmath>
+#include <functional>
 #include <mutex>
+#include <thread>
 #include <utility>
 
 #include "cf_device.hpp"
@@ -912,28 +914,86 @@ __global__ __launch_bounds__(kMaxD) void seam_merge_kernel(cf_kv_paged_attention
 
 }  // namespace
 
-// Split partials of the seam: a file-scope device array of CF_KV_SEAM_SCRATCH_BYTES per GPU (the seam's signature
-// has no workspace and it allocates nothing). Its device address is looked up once per device with
-// hipGetSymbolAddress. Calls that overlap on one GPU share it (see kv_cuda.h).
-#define CF_KV_SEAM_SCRATCH_BYTES (16u << 20)
-static __device__ __align__(256) uint8_t seam_scratch[CF_KV_SEAM_SCRATCH_BYTES];
+// Split partials of the seam. Its signature has no workspace and it allocates nothing, so the partial softmax
+// states of split contexts go to kSeamRegions regions of one file-scope device array per GPU (its address looked up
+// once per device with hipGetSymbolAddress). Each region belongs to one stream at a time, so calls on different
+// streams or threads never share partials in flight. A stream is known by its handle: the legacy default stream
+// under either of its names (NULL, hipStreamLegacy) is one stream, and the per-thread default stream
+// (hipStreamPerThread) is a different stream in each host thread. A handle the runtime reuses for a new stream after
+// hipStreamDestroy counts as the same stream, so a stream is destroyed only after its seam calls completed, as any
+// buffer its pending work reads:
+//   * a stream that owns a region uses it; calls on one stream are ordered by the stream itself;
+//   * a stream without one takes a free region;
+//   * with every region owned by other streams, the device switches to handover mode for the rest of the process:
+//     from then on each split call records an event on its stream after its merge launch, and a stream without a
+//     region takes the least recently used region whose owner has recorded one, after making its own stream wait
+//     for that event (hipStreamWaitEvent). Until such a region exists the call runs unsplit and uses none.
+// Programs that run the seam on at most kSeamRegions streams never record an event (an event record costs ~4.5 us
+// of stream time per call, 10-15 % of a short seam call). The host mutex is held from choosing the region to the
+// last launch, so two threads on one stream cannot interleave their kernel and merge launches. A stream under graph
+// capture cannot wait for an event recorded outside it, so there the call runs unsplit and touches no region.
+constexpr uint32_t kSeamRegions = 4;
+constexpr uint64_t kSeamRegionBytes = 16ull << 20;
+static __device__ __align__(256) uint8_t seam_scratch[kSeamRegions * kSeamRegionBytes];
 
 namespace {
 
 constexpr int kMaxDevices = 64;
-std::mutex g_seam_mu;
-void *g_seam_addr[kMaxDevices] = {};
 
-void *seam_scratch_address() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
-  std::lock_guard<std::mutex> lock(g_seam_mu);
-  if (!g_seam_addr[dev]) {
-    void *addr = nullptr;
-    if (hipGetSymbolAddress(&addr, HIP_SYMBOL(seam_scratch)) != hipSuccess) return nullptr;
-    g_seam_addr[dev] = addr;
+struct StreamKey {
+  uintptr_t handle = 0;
+  size_t thread = 0;  // the host thread, for the per-thread default stream only
+  bool operator==(const StreamKey &o) const { return handle == o.handle && thread == o.thread; }
+};
+
+StreamKey stream_key(hipStream_t s) {
+  if (s == nullptr || s == hipStreamLegacy) return {};
+  if (s == hipStreamPerThread)
+    return {reinterpret_cast<uintptr_t>(s), std::hash<std::thread::id>{}(std::this_thread::get_id()) | 1u};
+  return {reinterpret_cast<uintptr_t>(s), 0};
+}
+
+struct SeamRegion {
+  StreamKey owner;  // the owning stream
+  bool owned = false;
+  hipEvent_t done = nullptr;  // handover mode: recorded on the owner's stream after its last call
+  bool done_valid = false;    // `done` was recorded after the owner's most recent call
+  uint64_t stamp = 0;         // call counter when last used
+};
+
+struct SeamDevice {
+  uint8_t *base = nullptr;
+  bool handover = false;  // some stream once found every region owned by others
+  uint64_t calls = 0;
+  SeamRegion r[kSeamRegions];
+};
+
+std::mutex g_seam_mu;
+SeamDevice g_seam[kMaxDevices];
+
+// Region for a call on the stream `sid` (g_seam_mu held); `wait` is set when the caller must order its
+// stream after the region's previous owner first. nullptr: run unsplit.
+SeamRegion *seam_pick(SeamDevice &d, const StreamKey &sid, bool &wait) {
+  wait = false;
+  SeamRegion *fresh = nullptr, *lru = nullptr;
+  for (SeamRegion &r : d.r) {
+    if (r.owned && r.owner == sid) return &r;
+    if (!r.owned && !fresh) fresh = &r;
+    if (r.owned && r.done_valid && (!lru || r.stamp < lru->stamp)) lru = &r;
   }
-  return g_seam_addr[dev];
+  if (fresh) return fresh;
+  d.handover = true;
+  if (lru) wait = true;
+  return lru;
+}
+
+bool stream_capturing(hipStream_t s) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &st) != hipSuccess) {
+    (void)hipGetLastError();
+    return true;  // unknown: take the path that needs no ordering
+  }
+  return st != hipStreamCaptureStatusNone;
 }
 
 uint32_t seam_cus() {
@@ -975,8 +1035,8 @@ extern "C" cf_status cf_kv_validate_paged_attention_desc(const cf_kv_paged_atten
 
 // reference src/cuda/paged_kv_attention.cu:301-327
 // Context splits: about two workgroups per CU over the (64-vector tile, KV head) units, at least four page chunks
-// per split, at most 64 splits, and no more partials than the scratch array holds (one split writes the output
-// directly).
+// per split, at most 64 splits, and no more partials than one scratch region holds (one split writes the output
+// directly and uses no region).
 extern "C" cf_status cf_kv_paged_attention_async(const cf_kv_paged_attention_desc *desc, void *stream) {
   const cf_status valid = cf_kv_validate_paged_attention_desc(desc);
   if (valid != CF_OK) return valid;
@@ -991,19 +1051,53 @@ extern "C" cf_status cf_kv_paged_attention_async(const cf_kv_paged_attention_des
   splits = std::min<uint64_t>(splits, std::max<uint64_t>(1, chunks_per_head / 4));
   splits = std::min<uint64_t>(splits, 64);
   const uint64_t part_bytes = M * desc->kv_head_count * (desc->head_dim + 2) * sizeof(float);
-  if (splits > 1 && part_bytes * splits > CF_KV_SEAM_SCRATCH_BYTES)
-    splits = std::max<uint64_t>(1, CF_KV_SEAM_SCRATCH_BYTES / part_bytes);
-  float *partial = nullptr;
-  if (splits > 1) {
-    partial = static_cast<float *>(seam_scratch_address());
-    if (!partial) return CF_ERR_CUDA;
-  }
+  if (splits > 1 && part_bytes * splits > kSeamRegionBytes)
+    splits = std::max<uint64_t>(1, kSeamRegionBytes / part_bytes);
   const hipStream_t s = cfd::as_stream(stream);
-  const dim3 grid(static_cast<uint32_t>(tiles), desc->kv_head_count, static_cast<uint32_t>(splits));
-  if (desc->head_dim <= 64) seam_kernel<64><<<grid, kThreads, 0, s>>>(*desc, static_cast<uint32_t>(splits), partial);
-  else seam_kernel<128><<<grid, kThreads, 0, s>>>(*desc, static_cast<uint32_t>(splits), partial);
-  if (splits > 1)
-    seam_merge_kernel<<<dim3(static_cast<uint32_t>(M), desc->kv_head_count), kMaxD, 0, s>>>(
-        *desc, static_cast<uint32_t>(splits), partial);
-  return cfd::launch_status();
+  if (splits > 1 && stream_capturing(s)) splits = 1;
+  const auto launch = [&](float *partial) {
+    const dim3 grid(static_cast<uint32_t>(tiles), desc->kv_head_count, static_cast<uint32_t>(splits));
+    if (desc->head_dim <= 64) seam_kernel<64><<<grid, kThreads, 0, s>>>(*desc, static_cast<uint32_t>(splits), partial);
+    else seam_kernel<128><<<grid, kThreads, 0, s>>>(*desc, static_cast<uint32_t>(splits), partial);
+    if (splits > 1)
+      seam_merge_kernel<<<dim3(static_cast<uint32_t>(M), desc->kv_head_count), kMaxD, 0, s>>>(
+          *desc, static_cast<uint32_t>(splits), partial);
+  };
+  if (splits == 1) {
+    launch(nullptr);
+    return cfd::launch_status();
+  }
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return CF_ERR_CUDA;
+  const StreamKey sid = stream_key(s);
+  std::lock_guard<std::mutex> lock(g_seam_mu);  // held from choosing the region to the last launch
+  SeamDevice &sd = g_seam[dev];
+  if (!sd.base) {
+    void *addr = nullptr;
+    if (hipGetSymbolAddress(&addr, HIP_SYMBOL(seam_scratch)) != hipSuccess) return CF_ERR_CUDA;
+    sd.base = static_cast<uint8_t *>(addr);
+  }
+  bool wait = false;
+  SeamRegion *r = seam_pick(sd, sid, wait);
+  if (!r) {  // every region is owned by another stream that has not recorded an event yet
+    splits = 1;
+    launch(nullptr);
+    return cfd::launch_status();
+  }
+  if (wait && hipStreamWaitEvent(s, r->done, 0) != hipSuccess) return CF_ERR_CUDA;
+  r->owner = sid;
+  r->owned = true;
+  r->done_valid = false;
+  r->stamp = ++sd.calls;
+  launch(reinterpret_cast<float *>(sd.base + static_cast<uint64_t>(r - sd.r) * kSeamRegionBytes));
+  const cf_status st = cfd::launch_status();
+  if (sd.handover) {
+    if (!r->done && hipEventCreateWithFlags(&r->done, hipEventDisableTiming) != hipSuccess) {
+      r->done = nullptr;
+      return CF_ERR_CUDA;
+    }
+    if (hipEventRecord(r->done, s) != hipSuccess) return CF_ERR_CUDA;
+    r->done_valid = true;
+  }
+  return st;
 }

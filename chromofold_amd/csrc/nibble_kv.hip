@@ -305,18 +305,26 @@ __global__ __launch_bounds__(256) void nib_attn_kernel(const AttnItem *__restric
   if (split < vbase + it.vsplits) {
     const uint32_t p0 = (split - vbase) * it.vunits;
     const uint32_t p_end = min(it.page_count, p0 + it.vunits);
-    // with the MFMA kernel on the request, only the pages it refuses: each lane of a wave tests one page of the
-    // split (vunits <= 64), and the wave's ballot is the same in every wave of the workgroup
+    // with the MFMA kernel on the request, only the pages it refuses: each lane of wave 0 tests one page of the
+    // split (vunits is the lane count of wave 0, at most 64). The workgroup is hw * LG threads, which need not be
+    // whole waves (5 KV heads of 16 lanes make 80), so a later wave may have fewer lanes than the split has pages:
+    // wave 0's ballot reaches every wave through LDS.
     uint64_t mine = ~0ull;
     if (it.mfma_nb) {
-      const uint32_t pl = p0 + (threadIdx.x & 63u);
-      bool refused = false;
-      if (pl < p_end) {
-        const cf_device_page_descriptor &q = it.pages[pl];
-        refused = !mfma_page_ok(q.key_payload, q.value_payload, q.key_scales, q.value_scales, q.block_size,
-                                q.head_dim, q.token_count, it.mfma_cap);
+      __shared__ uint64_t s_refused;
+      if (threadIdx.x < 64u) {
+        const uint32_t pl = p0 + threadIdx.x;
+        bool refused = false;
+        if (pl < p_end) {
+          const cf_device_page_descriptor &q = it.pages[pl];
+          refused = !mfma_page_ok(q.key_payload, q.value_payload, q.key_scales, q.value_scales, q.block_size,
+                                  q.head_dim, q.token_count, it.mfma_cap);
+        }
+        const uint64_t b = __ballot(refused);
+        if (threadIdx.x == 0u) s_refused = b;
       }
-      mine = __ballot(refused);
+      __syncthreads();  // the branches above are uniform over the workgroup (blockIdx and the item only)
+      mine = s_refused;
     }
     for (uint32_t p = p0; p < p_end; ++p) {
       if (!((mine >> (p - p0)) & 1ull)) continue;  // wave-uniform

@@ -85,10 +85,12 @@ cf_status cf_kv_validate_paged_attention_desc(const cf_kv_paged_attention_desc *
 
 /* Paged attention, decoding each page inside the kernel. Allocates nothing, never synchronizes.
  * Replaces reference kv_cuda.h:86 (src/cuda/paged_kv_attention.cu:301-327).
- * Long contexts are split over many workgroups; their partial softmax states go to a device array the library
- * owns (16 MiB per GPU) and a second launch on the same stream merges them. Calls that overlap in time on one GPU
- * (on different streams or from different threads) share that array and must be serialised by the caller;
- * consecutive calls on one stream need nothing. */
+ * Long contexts are split over many workgroups; their partial softmax states go to one of four 16 MiB regions of
+ * a device array the library owns (per GPU), each region held by one stream at a time, and a second launch on the
+ * same stream merges them. Calls on different streams or threads are therefore safe without serialisation by the
+ * caller (the reference keeps no cross-call state either). Beyond four streams, a stream takes over a region only
+ * after an event wait on the previous holder's stream, or runs unsplit. A stream under graph capture runs the
+ * call unsplit. */
 cf_status cf_kv_paged_attention_async(const cf_kv_paged_attention_desc *desc, void *stream);
 
 #ifdef __cplusplus

@@ -87,3 +87,19 @@ def test_c_headers_link_and_null_contract(tmp_path):
     assert set(sizes) == set(mirrors)
     for name, cls in mirrors.items():
         assert C.sizeof(cls) == int(sizes[name]), name
+
+
+@needs_lib
+def test_hip_imports_resolve_in_torchs_runtime():
+    """The library is loaded after torch, into torch's own libamdhip64 (ROCm 7.0 in this image, older than the
+    hipcc that builds the library): every versioned HIP symbol the library imports must be exported by that
+    runtime at that version, or the library fails to load on the GPU box."""
+    import torch
+    rt = glob.glob(os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so*"))
+    if not rt:
+        pytest.skip("torch ships no libamdhip64 here")
+    need = subprocess.run(["nm", "-D", "--undefined-only", LIB], capture_output=True, text=True, check=True).stdout
+    have = subprocess.run(["nm", "-D", "--defined-only", rt[0]], capture_output=True, text=True, check=True).stdout
+    have_set = {line.split()[-1].replace("@@", "@") for line in have.splitlines() if line.strip()}
+    missing = [s for s in (line.split()[-1] for line in need.splitlines() if "@hip_" in line) if s not in have_set]
+    assert not missing, missing

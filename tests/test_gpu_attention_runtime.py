@@ -246,3 +246,23 @@ def test_matrix_core_and_valu_pages_in_one_request(dev):
     assert np.isfinite(got).all()
     assert head_err(got, ref) <= 2e-5
     assert c["optimized_launches"] == 1 and c["cuda_errors"] == 0
+
+
+@pytest.mark.parametrize("kvh", [5, 6])
+def test_refused_pages_reach_every_wave(dev, kvh):
+    """With 5 or 6 KV heads of 16 lanes each (head_dim 128) the VALU kernel's workgroup is 80 or 96 threads: its
+    second wave has 16 or 32 lanes, fewer than the 64 pages one split tests. Pages the matrix cores refuse
+    (block sizes 16 and 48) sit at table indices 16 and above, so the second wave's KV heads must learn of them
+    from the first wave's test, not from their own lanes."""
+    gqa, D = 2, 128
+    rng = np.random.default_rng(40 + kvh)
+    pages, begin = [], 0
+    for bs, n in ((32, 16), (16, 3), (32, 10), (48, 4), (64, 8), (16, 2)):
+        pages += _pages(rng, kvh, D, bs, n, 32, begin=begin)
+        begin += n * 32
+    assert len(pages) == 43
+    specs = [(pages, begin + 5, 0, None, None, 0), (pages[::-1], 900, 300, None, None, 0)]
+    got, ref, c = _run(dev, kvh, gqa, D, specs)
+    assert np.isfinite(got).all()
+    assert head_err(got, ref) <= 2e-5
+    assert c["optimized_launches"] == 1 and c["cuda_errors"] == 0

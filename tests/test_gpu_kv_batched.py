@@ -19,10 +19,10 @@ def dev():
 
 
 def _run(dev, codec, seq_tokens, kv_heads, gqa, D, seed, query_pos=None, splits=(0,), shared=None,
-         scale_spread=False, raw_groups=None, v_mult=None):
+         scale_spread=False, raw_groups=None, v_mult=None, cancel=None):
     import torch
     from chromofold_amd import kv
-    data = make_seqs(seq_tokens, kv_heads, D, seed, scale_spread, v_mult)
+    data = make_seqs(seq_tokens, kv_heads, D, seed, scale_spread, v_mult, cancel)
     tables = None
     if codec == kv.CODEC_RANS_HYBRID:
         parts = []
@@ -134,6 +134,33 @@ def test_batched_wide_v_magnitudes(dev):
     _run(dev, 2, [6144, 6200, 7000, 6150, 6400], 2, 4, 128, seed=59, splits=(1,), v_mult=V_MULTS)
 
 
+# Cancellation: outputs that are sums of near-opposite page pairs (make_seqs(cancel=1/64)), ~64x smaller than
+# sum p |v|. A P.V weight p * v_scale rounded to one f16 (11 significant bits) errs by up to 2^-12 of p v per token,
+# independently in the two pages of a pair: about 2e-2 of such an output (a float64 simulation of this data gives
+# 1.9e-2 for one f16 and 3.4e-6 for an f16 hi + lo pair). The reference accumulates p v in fp32
+# (src/cuda/paged_kv_attention.cu:228-240). Narrow and wide shapes, splits 0/1/2/3, both codecs, head_dim 128 and
+# 64, raw and coded groups, every (sequence, query head) row on its own.
+@pytest.mark.parametrize("codec", [1, 2])
+@pytest.mark.parametrize("D", [128, 64])
+def test_batched_cancellation(dev, codec, D):
+    _run(dev, codec, [6200, 7000, 6145, 9000, 1, 6400], 2, 4, D, seed=71 + D + codec, splits=(1, 2, 0, 3),
+         query_pos=[6199, 3500, 6144, 8999, 0, 100], cancel=1 / 64)
+
+
+def test_batched_cancellation_short_and_shared(dev):
+    _run(dev, 2, [300, 1029, 64, 4096, 700], 3, 4, 128, seed=77, splits=(0, 1, 3), cancel=1 / 64,
+         shared={1: (0, 1), 3: (0, 1)}, raw_groups={0: 1, 4: 3})
+
+
+def test_cascade_cancellation(dev):
+    """The cascade's INT8 prefix pass and the batched suffix pass over near-cancelling pairs."""
+    tokens = [4096, 4160, 1100, 4200, 700]
+    kvb, data, q, qp, sc, got = _cascade_case(dev, 4, tokens, 10, seed=101, cancel=1 / 64)
+    assert np.isfinite(got).all()
+    ref = oracle_batched(kvb, data, q, qp, sc, 4)
+    assert head_err(got, ref) <= TOL
+
+
 def test_batched_rejects_bad_desc(dev):
     import ctypes as C
     import torch
@@ -199,10 +226,10 @@ def test_batched_full_c4_32k_every_sequence_torch_reference(dev):
 
 
 def _cascade_case(dev, gqa, seq_tokens, shared, seed, query_pos=None, raw_prefix=True, D=128, kv_heads=2,
-                  v_mult=None, splits=0):
+                  v_mult=None, splits=0, cancel=None):
     import torch
     from chromofold_amd import kv
-    data = make_seqs(seq_tokens, kv_heads, D, seed, v_mult=v_mult)
+    data = make_seqs(seq_tokens, kv_heads, D, seed, v_mult=v_mult, cancel=cancel)
     n = shared * 64
     for s in range(1, len(seq_tokens)):  # every sequence starts with sequence 0's prefix
         data[s][0][:, :n] = data[0][0][:, :n]
@@ -338,3 +365,86 @@ def test_c5_long_context_131k_every_row(dev):
     err = np.abs(got - ref).max(axis=2) / np.abs(ref).max(axis=2)
     assert err.max() <= TOL, err.max()
     print(f"C5 4 x 131072: worst normwise error over {err.size} rows {err.max():.3e}")
+
+
+def test_c5_shared_prefix_full_shape_every_row(dev):
+    """BASELINE C5's shared-prefix shape at full size: 256 sequences x (8192 shared + 512 own) tokens, 8 KV / 32 q
+    heads, hd 128. The prefix is stored once, as INT8 groups inside the rANS pool, and referenced from every
+    sequence's group table; each sequence's own 512 tokens are rANS-coded. The cascade entry point (the prefix
+    streamed once per KV head for all 256 query sets) and the batched entry point on the same pool; query positions
+    at the end, inside the own tokens and inside the prefix. Every (sequence, query head) row against the float64
+    oracle decoding the pool's own blobs (O.kv_pool_attention), normwise <= 1e-3."""
+    import torch
+    import oracle as O
+    from chromofold_amd import kv
+    S, P, U, H, QH, D = 256, 8192, 512, 8, 32, 128
+    T, pg = P + U, P // 64
+    rng = np.random.default_rng(0xC5A)
+    prefix = (rng.standard_normal((H, P, D), dtype=np.float32), rng.standard_normal((H, P, D), dtype=np.float32))
+    seeds = rng.integers(0, 2 ** 63, size=S)
+
+    def src(s):
+        g = np.random.default_rng(int(seeds[s]))
+        Ks = np.zeros((H, T, D), np.float32)
+        Vs = np.zeros((H, T, D), np.float32)
+        if s == 0:
+            Ks[:, :P], Vs[:, :P] = prefix
+        Ks[:, P:] = g.standard_normal((H, U, D), dtype=np.float32)
+        Vs[:, P:] = g.standard_normal((H, U, D), dtype=np.float32)
+        return Ks, Vs
+
+    tables = np.concatenate([t for h in range(H) for t in (kv.build_table(prefix[0][h, :512].reshape(-1, 16, D)),
+                                                           kv.build_table(prefix[1][h, :512].reshape(-1, 16, D)))])
+    kvb = kv.build_batched(kv.CODEC_RANS_HYBRID, src, S, H, np.full(S, T, np.uint32), D, tables, dev,
+                           shared={s: (0, pg) for s in range(1, S)}, raw_groups={0: pg})
+    q = rng.standard_normal((S, QH, D), dtype=np.float32)
+    qp = np.full(S, T - 1, np.uint32)
+    qp[1::7] = rng.integers(P, T - 1, size=qp[1::7].size)  # inside the own tokens
+    qp[3::11] = rng.integers(0, P, size=qp[3::11].size)    # inside the shared prefix
+    dq = torch.from_numpy(q).to(dev)
+    dqp = torch.from_numpy(qp.view(np.int32)).to(dev)
+    sc = 1.0 / np.sqrt(D)
+    ref = O.kv_pool_attention(kvb.pool.cpu().numpy(), kvb.group_offsets.cpu().numpy().view(np.uint32),
+                              np.full(S, T, np.uint32), qp, tables, q, H, D, sc)
+    for shared_groups in (pg, 0):  # cascade, then batched
+        out = torch.full_like(dq, float("nan"))
+        kvb.attention(dq, out, dqp, sc, shared_groups=shared_groups)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        assert np.isfinite(got).all(), shared_groups
+        err = np.abs(got - ref).max(axis=2) / np.abs(ref).max(axis=2)
+        assert err.max() <= TOL, (shared_groups, err.max())
+        print(f"C5 256 x (8192 + 512), shared_groups={shared_groups}: worst normwise error {err.max():.3e}")
+
+
+def test_c4_4k_batch_32_every_row(dev):
+    """BASELINE C4 at its 4k context: 32 sequences x 4096 tokens, 8 KV / 32 q heads, hd 128, sealed on the device,
+    run with the automatic launch plan (the narrow shape with context splits and the merge kernel). Every
+    (sequence, query head) row against the float64 oracle decoding the pool's own blobs, normwise <= 1e-3."""
+    import torch
+    import oracle as O
+    from chromofold_amd import kv
+    S, T, H, QH, D = 32, 4096, 8, 32, 128
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0xC44)
+    K = torch.randn((S, H, T, D), generator=gen, device=dev)
+    V = torch.randn((S, H, T, D), generator=gen, device=dev)
+    tables = np.concatenate([t for _ in range(H) for t in (kv.build_table(K[0, 0, :512].cpu().numpy().reshape(-1, 16, D)),
+                                                           kv.build_table(V[0, 0, :512].cpu().numpy().reshape(-1, 16, D)))])
+    kvb = kv.seal_device(kv.CODEC_RANS_HYBRID, K, V, torch.from_numpy(tables).to(dev))
+    del K, V
+    q = torch.randn((S, QH, D), generator=gen, device=dev)
+    qp = torch.full((S,), T - 1, dtype=torch.int32, device=dev)
+    qp[5], qp[17] = 2000, 63
+    out = torch.full_like(q, float("nan"))
+    sc = 1.0 / np.sqrt(D)
+    kvb.attention(q, out, qp, sc)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all()
+    ref = O.kv_pool_attention(kvb.pool.cpu().numpy(), kvb.group_offsets.cpu().numpy().view(np.uint32),
+                              np.full(S, T, np.uint32), qp.cpu().numpy().view(np.uint32), tables, q.cpu().numpy(),
+                              H, D, sc)
+    err = np.abs(got - ref).max(axis=2) / np.abs(ref).max(axis=2)
+    assert err.max() <= TOL, err.max()
+    print(f"C4 32 x 4096: worst normwise error over {err.size} rows {err.max():.3e}")
