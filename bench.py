@@ -731,6 +731,98 @@ def bench_seam(steps: int, warmup: int, shapes=((64, 4096), (64, 65536), (128, 4
     return out
 
 
+def bench_seam_c4(steps: int, warmup: int, context: int = 32768, batch: int = 32) -> dict:
+    """The headline configuration through the unchanged reference seam (the llama.cpp integration's call,
+    reference integrations/llama.cpp/chromofold_kv_adapter.cpp:127): C4's 32 sequences x 32768 tokens, 8 KV / 32 q
+    heads, hd 128, every 64 tokens of a (sequence, KV head) one self-coded RANS_HYBRID group (a chain start, the
+    seam's rANS page tag), sealed on the device. 8 x 512 = 4096 pages per sequence = the seam's per-launch page
+    limit (reference include/chromofold/kv_cuda.h:13), so one step is 32 cf_kv_paged_attention_async calls, one
+    per sequence, each with its decode token's 32 query heads. Gate: sequence 0's output against the float64 oracle
+    decoding the pool's own blobs."""
+    import ctypes as C
+    import torch
+    import oracle as O
+    from chromofold_amd import _abi as A
+    from chromofold_amd import kv, legacy, synth
+
+    H, QH, D = 8, 32, 128
+    gqa = QH // H
+    ngr = context // 64
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(synth.SEED_C4 + context)
+    K = torch.randn((batch, H, context, D), generator=gen, device="cuda:0")
+    V = torch.randn((batch, H, context, D), generator=gen, device="cuda:0")
+    Kh = K[0, 0, :1024].cpu().numpy().reshape(-1, 16, D)
+    Vh = V[0, 0, :1024].cpu().numpy().reshape(-1, 16, D)
+    tables = np.concatenate([t for _ in range(H) for t in (kv.build_table(Kh), kv.build_table(Vh))])
+    d_tab = torch.from_numpy(tables).to("cuda:0")
+    n = batch * H * ngr
+    g = torch.arange(n, device="cuda:0", dtype=torch.int64)
+    first = (g // ngr) * (context // 16) + (g % ngr) * 4
+    heads = ((g // ngr) % H).to(torch.int32)
+    cap = int(A.lib().cf_kv_group_blob_max_bytes(kv.CODEC_RANS_HYBRID, D)) * n
+    pool = torch.empty(cap, dtype=torch.uint8, device="cuda:0")
+    r = kv.encode_groups_device(kv.CODEC_RANS_HYBRID, K.view(-1, 16, D), V.view(-1, 16, D), D, d_tab, first,
+                                torch.full((n,), 4, dtype=torch.int32, device="cuda:0"), pool, 0, heads,
+                                continues=torch.zeros(n, dtype=torch.uint8, device="cuda:0"))
+    st, end = int(r.status.item()), int(r.pool_end.item())
+    assert st == 0, st
+    del K, V
+    offs = r.offsets.cpu().numpy().view(np.uint32).astype(np.uint64).reshape(batch, H, ngr)
+    page_dt = np.dtype({"names": ["k_words", "k_lut", "v_lut", "token_begin", "token_count", "head_dim",
+                                  "block_size", "zero_point", "kv_head"],
+                        "formats": ["<u8", "<u8", "<u8", "<u4", "<u4", "<u4", "<u4", "<u4", "<u4"],
+                        "offsets": [0, 16, 48, 64, 68, 72, 76, 88, 92], "itemsize": C.sizeof(A.cf_kv_device_page)})
+    descs = np.zeros((batch, H * ngr), page_dt)
+    hh = np.repeat(np.arange(H, dtype=np.uint64), ngr)
+    gg = np.tile(np.arange(ngr, dtype=np.uint32), H)
+    base, tb = pool.data_ptr(), d_tab.data_ptr()
+    for s_ in range(batch):
+        d_ = descs[s_]
+        d_["k_words"] = base + offs[s_].reshape(-1) * 16
+        d_["k_lut"] = tb + hh * (2 * kv.TABLE_BYTES)
+        d_["v_lut"] = tb + hh * (2 * kv.TABLE_BYTES) + kv.TABLE_BYTES
+        d_["token_begin"], d_["token_count"], d_["head_dim"], d_["block_size"] = 64 * gg, 64, D, 64
+        d_["zero_point"], d_["kv_head"] = 128, hh.astype(np.uint32)
+    d_descs = torch.from_numpy(descs.view(np.uint8)).to("cuda:0")
+    q = torch.randn((batch, 1, QH, D), generator=gen, device="cuda:0")
+    out = torch.empty_like(q)
+    sc = 1.0 / np.sqrt(D)
+    row = descs.itemsize * H * ngr
+    ds = []
+    for s_ in range(batch):
+        d = A.cf_kv_paged_attention_desc()
+        d.struct_size, d.abi_version = C.sizeof(A.cf_kv_paged_attention_desc), legacy.CF_KV_CUDA_ABI_VERSION
+        d.pages, d.page_count = d_descs.data_ptr() + s_ * row, H * ngr
+        d.kv_head_count, d.query_head_count, d.gqa_group_size = H, QH, gqa
+        d.queries, d.output = q[s_].data_ptr(), out[s_].data_ptr()
+        d.query_token_begin, d.query_count, d.head_dim, d.softmax_scale = context - 1, 1, D, sc
+        ds.append(d)
+    L = A.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        for d in ds:
+            A.check(L.cf_kv_paged_attention_async(C.byref(d), stream), "cf_kv_paged_attention_async")
+
+    step()
+    torch.cuda.synchronize()
+    got = out[0, 0].cpu().numpy()
+    ref = O.kv_pool_attention(pool[:end].cpu().numpy(), offs[:1].astype(np.uint32), np.full(1, context, np.uint32),
+                              np.full(1, context - 1, np.uint32), tables, q[:1, 0].cpu().numpy(), H, D, sc, nseq=1)
+    err = float((np.abs(got - ref[0]).max(axis=1) / np.abs(ref[0]).max(axis=1)).max())
+    assert err <= 1e-3, err
+    _, per = _events_time(step, steps, warmup)
+    t = float(np.mean(per)) * 1e-3
+    step_bytes = end + tables.size + d_descs.numel() + 2 * q.numel() * 4
+    return {"workload": f"reference seam at C4: {batch} seqs x {context} tokens, 32 q / 8 KV heads, hd {D}, "
+                        f"{H * ngr} self-coded 64-token rANS pages per call, {batch} calls per step",
+            "tokens_per_s": batch / t, "ms_per_step": t * 1e3, "us_per_call": t * 1e6 / batch,
+            "pool_bytes": end, "bits_per_value": end * 8.0 / (2 * batch * H * context * D),
+            "gbs": step_bytes / t / 1e9, "roofline_frac": step_bytes / t / 1e9 / HBM_PEAK_GBS,
+            "max_normwise_err_seq0": err}
+
+
 def bench_seam_rans(steps: int, warmup: int, hd: int = 128, n: int = 65536) -> dict:
     """The same seam call over rANS pages (the seam's rANS tag, kv_cuda.h: fixed_code_length == 0 and
     k_max_code_length == 0): every 64 tokens of a KV head one kv_codec_ext.h RANS_HYBRID group coded on its own,
@@ -1002,7 +1094,8 @@ def main() -> int:
         print(json.dumps({"c3_matmul": bench_qw(args.steps, args.warmup)}))
         return 0
     if args.workload == "seam":
-        print(json.dumps({"seam": bench_seam(args.steps, args.warmup)}))
+        print(json.dumps({"seam": bench_seam(args.steps, args.warmup),
+                          "seam_c4": bench_seam_c4(min(args.steps, 10), 1)}))
         return 0
     if args.workload == "runtime":
         print(json.dumps({"attention_runtime": bench_runtime(args.steps, args.warmup)}))
@@ -1037,6 +1130,7 @@ def main() -> int:
             secondary["nibble_pages"] = bench_nibble(min(args.steps, 20), 2, cpu=not args.no_cpu)
             secondary["gathers"] = bench_gather(min(args.steps, 20), 2)
             secondary["seam"] = bench_seam(min(args.steps, 20), 2)
+            secondary["seam_c4"] = bench_seam_c4(5, 1)
             secondary["attention_runtime"] = bench_runtime(min(args.steps, 20), 2)
             peaks = bench_cache_peaks()
             secondary["cache_peaks"] = peaks

@@ -159,4 +159,16 @@ __device__ __forceinline__ void split_mul_f16(float a, float b, _Float16 &hi, _F
   lo = static_cast<_Float16>(x - static_cast<float>(h));
 }
 
+// Two products a0 * b and a1 * b split the same way, with one packed round-toward-zero conversion for both hi parts
+// and each lo part from a fused multiply-add of the exact product minus its hi (hi + lo then misses a * b by at most
+// the rounding of lo): 5 VALU for the pair instead of 8.
+__device__ __forceinline__ void split2_mul_f16(float a0, float a1, float b, _Float16 &hi0, _Float16 &lo0,
+                                               _Float16 &hi1, _Float16 &lo1) {
+  const auto h = __builtin_amdgcn_cvt_pkrtz(a0 * b, a1 * b);
+  hi0 = static_cast<_Float16>(h[0]);
+  hi1 = static_cast<_Float16>(h[1]);
+  lo0 = static_cast<_Float16>(__builtin_fmaf(a0, b, -static_cast<float>(h[0])));
+  lo1 = static_cast<_Float16>(__builtin_fmaf(a1, b, -static_cast<float>(h[1])));
+}
+
 }  // namespace cfd

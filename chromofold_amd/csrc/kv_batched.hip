@@ -10,11 +10,12 @@
 //            GQA group's 4 query heads (split into f16 hi + lo parts for fp32-grade scores) as the A operand, so
 //            the lane ends up holding its token's 4 head scores. Nothing decoded is written anywhere.
 //   softmax: one running max per head for the whole wavefront (so the 4 page groups can be summed at the end),
-//            probabilities times the page's V scale (in units of a power of two per lane, so that the f16 value
+//            probabilities times the page's V scale (in units of a power of two per wavefront, so that the f16 value
 //            neither underflows nor overflows), split into f16 hi + lo parts, go to two 512-byte LDS tiles.
-//   V phase: lane decodes dims {t + 16i} of page G, 4 tokens per quad, again straight into 4x4x4 MFMAs
-//            (A = the hi, then the lo parts of those 4 tokens' weights for the 4 heads, B = the 4 decoded values
-//            as exact signed f16) accumulating the lane's 4 heads x 8 dims output. With one f16 per weight (11
+//   V phase: lane decodes dims {t + 16i} of page G, 4 tokens per quad; two quads (8 tokens) of each of the 4 pages
+//            are the k = 32 of one v_mfma_f32_16x16x32_f16 whose rows are 4 heads x {hi, lo} weight parts and whose
+//            16 columns are dims 16i .. 16i + 15 (B = the decoded values as exact signed f16): 16 MFMAs per group
+//            where 4x4x4 MFMAs would take 64. With one f16 per weight (11
 //            significant bits) an output made of near-cancelling terms (weights of different pages, whose V scales
 //            differ) would carry an error of ~2^-12 of the terms themselves; hi + lo leaves ~2^-22.
 // Codec decode (format 4): one rANS step per 8 values of a stream (LDS slot table, 64-bit entry = freq/offset +
@@ -41,6 +42,8 @@
 namespace {
 
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
 // Occupancy floor for the compiler (3 wavefronts per SIMD: <= 168 VGPRs); the LDS footprint below allows one
@@ -240,28 +243,41 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
   for (int o = 32; o > 0; o >>= 1)
 #pragma unroll
     for (int h = 0; h < kGqa; ++h) mx[h] = fmaxf(mx[h], __shfl_xor(mx[h], o));
-  // The lane's P.V sums (acc_v) only ever hold tokens of its own page slot G, so they are kept in units of 2^e with
-  // e = (exponent of that page's V scale) - 15 (+ 24 for RANS groups, whose V operands are q * 2^-24): the f16
-  // operand p * vs * 2^-(e - 0|24) lies in [0, 2^15) whatever the V magnitude (no overflow for huge V), and weights
-  // p down to 2^-29 of the running maximum stay normal f16 numbers (a row whose heaviest tokens have V = 0 is carried
-  // by such small weights). Moving to the next page's units is an exact power-of-two factor folded into the softmax
-  // rescale; a drop of more than 2^60 between consecutive pages is clamped so that the rescale cannot overflow.
+  // P.V runs on v_mfma_f32_16x16x32_f16 with k = 8 tokens of each of the 4 pages (page G's from lane group G), so
+  // one MFMA sums all four pages: rows 0-3 are the 4 heads' hi parts of the weights p * v_scale, rows 4-7 their lo
+  // parts (rows 8-15 repeat rows 0-7 and are dropped), 16 dims per MFMA. The lane's accumulators acc_v hold rows
+  // 4G..4G+3: the hi (G = 0) or lo (G = 1) sums. The wavefront keeps them in units of 2^e_run with e = (exponent of
+  // the group's largest V scale among its pages with a visible token) - 15 (+ 24 for RANS groups, whose V operands
+  // are q * 2^-24): every f16 weight lies in [0, 2^15) whatever the V magnitude, weights down to 2^-29 of the
+  // running maximum stay normal f16 numbers (a row whose heaviest tokens have V = 0 is carried by such small
+  // weights), and hi + lo keep ~22 bits for every page within 2^18 of the group's largest V scale (the lo part of a
+  // page further below loses bits gradually: ~16 bits at 2^24, those of one f16 at 2^29). Moving to new units is an
+  // exact power-of-two factor folded into the softmax rescale; a drop of more than 2^60 is clamped so that the
+  // rescale cannot overflow.
   constexpr int kOpExp = RANS ? 24 : 0;
-  const int ev = max(__builtin_amdgcn_frexp_expf(vs) - 15 + kOpExp, e_run - 60);
-  const int de = e_run - ev;
-  e_run = ev;
-  const float vsn = ldexpf(vs, kOpExp - ev);
-  float alpha[kGqa];
+  constexpr int kNone = -(1 << 24);
+  // tokens are visible as a prefix of each page, so a page's lane 16 G is visible iff any of its tokens is
+  const int ep = tok_ok ? __builtin_amdgcn_frexp_expf(vs) - 15 + kOpExp : kNone;
+  const int eb = max(max(__builtin_amdgcn_readlane(ep, 0), __builtin_amdgcn_readlane(ep, 16)),
+                     max(__builtin_amdgcn_readlane(ep, 32), __builtin_amdgcn_readlane(ep, 48)));
+  const int nb = eb != kNone ? max(eb, e_run - 60) : e_run;
+  const int de = e_run - nb;
+  e_run = nb;
+  const float vsn = ldexpf(vs, kOpExp - nb);
+  float alpha[kGqa], pr[kGqa];
 #pragma unroll
   for (int h = 0; h < kGqa; ++h) {
     const float mn = fmaxf(m_run[h], mx[h]);
     const float a = (m_run[h] == -INFINITY) ? 0.0f : __expf(m_run[h] - mn);
-    const float pr = tok_ok ? __expf(s[h] - mn) : 0.0f;
-    l_run[h] = l_run[h] * a + pr;
+    pr[h] = tok_ok ? __expf(s[h] - mn) : 0.0f;
+    l_run[h] = l_run[h] * a + pr[h];
     alpha[h] = ldexpf(a, de);  // ldexp(0, .) = 0 before the first visible token
-    cfd::split_mul_f16(pr, vsn, s_pw[0][G][h][t], s_pw[1][G][h][t]);
     m_run[h] = mn;
   }
+#pragma unroll
+  for (int h = 0; h < kGqa; h += 2)
+    cfd::split2_mul_f16(pr[h], pr[h + 1], vsn, s_pw[0][G][h][t], s_pw[1][G][h][t], s_pw[0][G][h + 1][t],
+                        s_pw[1][G][h + 1][t]);
 #pragma unroll
   for (int i = 0; i < D / 16; ++i)
 #pragma unroll
@@ -270,22 +286,43 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // ---- V MFMAs: out[h][t + 16i] += sum over the quad's 4 tokens of p * v
-  [&]<int... Q>(std::integer_sequence<int, Q...>) {
+  // ---- V MFMAs: rows {hi, lo} x heads, k = tokens 8 tp .. 8 tp + 7 of every page, cols = dims 16 i .. 16 i + 15.
+  // A: lane (G, t) gives row t for page G (rows 8-15 read rows 0-7's weights); B: its V quads of tokens
+  // 8 tp .. + 3 and 8 tp + 4 .. + 7 at dim 16 i + t.
+  auto v_quad = [&](auto qc) {
+    constexpr int q = decltype(qc)::value;  // quad q = tokens 4 (q / (D / 16)) .. + 3 at dim t + 16 (q % (D / 16))
+    if constexpr (RANS)  // quad q is quad q % 8 of sign group q / 8
+      return sm_to_half4(q < KL ? vl[q * 64 + lane] : vb[q], quad_signs<kFrame[q % 8]>(vsg[q / 8]));
+    else
+      return bytes_to_half4_signed(q < KL ? raw[NQ * 64 + q * 64 + lane] : vb[q]);
+  };
+  [&]<int... TP>(std::integer_sequence<int, TP...>) {
     (
         [&] {
-          constexpr int q = Q, tq = q / (D / 16), i = q % (D / 16);  // quad q = tokens 4tq.. at dim t + 16i
-          const half4_t pa = *reinterpret_cast<const half4_t *>(&s_pw[0][G][lane & 3][4 * tq]);
-          const half4_t pl = *reinterpret_cast<const half4_t *>(&s_pw[1][G][lane & 3][4 * tq]);
-          half4_t bv;
-          if constexpr (RANS)  // quad q is quad q % 8 of sign group q / 8
-            bv = sm_to_half4(q < KL ? vl[q * 64 + lane] : vb[q], quad_signs<kFrame[q % 8]>(vsg[q / 8]));
-          else
-            bv = bytes_to_half4_signed(q < KL ? raw[NQ * 64 + q * 64 + lane] : vb[q]);
-          acc_v[i] = mfma4(pl, bv, mfma4(pa, bv, acc_v[i]));
+          constexpr int tp = TP;
+          // Read in inline asm: the compiler cannot tell this tile from the word buffer that the next group's
+          // global_load_lds copies are filling, and for a plain LDS read it would first wait for those copies
+          // (s_waitcnt vmcnt(0)), i.e. for the next group's whole prefetch, in the middle of every group. The
+          // tile was written by this wavefront's own ds_write instructions, which the LDS executes in order.
+          half8_t pa;
+          asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)"
+                       : "=v"(pa)
+                       : "v"(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(&s_pw[(t >> 2) & 1][G][t & 3][8 * tp])))
+                       : "memory");
+          [&]<int... I>(std::integer_sequence<int, I...>) {
+            (
+                [&] {
+                  constexpr int i = I;
+                  const half4_t b0 = v_quad(std::integral_constant<int, (2 * tp) * (D / 16) + i>{});
+                  const half4_t b1 = v_quad(std::integral_constant<int, (2 * tp + 1) * (D / 16) + i>{});
+                  const half8_t bv = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+                  acc_v[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, bv, acc_v[i], 0, 0, 0);
+                }(),
+                ...);
+          }(std::make_integer_sequence<int, D / 16>{});
         }(),
         ...);
-  }(std::make_integer_sequence<int, NQ>{});
+  }(std::make_integer_sequence<int, 2>{});
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -340,7 +377,8 @@ __global__ CF_KV_OCC __launch_bounds__(64 * W) void kv_batched_kernel(cf_kv_batc
   constexpr bool kWide = W == kWavesWide;           // contiguous weighted pair blocks (else strided pairs)
   constexpr int KL = kWide && RANS ? 16 : 0;        // V quads parked in LDS (see group_body)
   __shared__ uint2 s_tab[RANS ? 2 : 1][kSlots];     // {f | c << 16, spread big bits} per slot, K and V tables
-  __shared__ _Float16 s_p[W][2][4][kGqa][16];       // per wave: [hi, lo][page][head][token] probability * v_scale
+  __shared__ __attribute__((aligned(16))) _Float16 s_p[W][2][4][kGqa][16];  // per wave: [hi, lo][page][head][token]
+                                                                          // probability * v_scale
   __shared__ uint32_t s_buf[W][BUF];                // per wave: staged words; query staging and partials alias it
   __shared__ uint32_t s_vl[KL ? W : 1][KL ? KL : 1][64];
 
@@ -410,7 +448,7 @@ __global__ CF_KV_OCC __launch_bounds__(64 * W) void kv_batched_kernel(cf_kv_batc
   const uint32_t *grow = d.group_offsets + (static_cast<size_t>(seq) * d.kv_head_count + head) * d.max_groups;
 
   float m_run[kGqa], l_run[kGqa];
-  int e_run = -(1 << 20);  // exponent of the lane's P.V units (set by its first group)
+  int e_run = -(1 << 20);  // exponent of the wavefront's P.V units (set by its first group; see group_body)
   float4_t acc_v[D / 16];
 #pragma unroll
   for (int h = 0; h < kGqa; ++h) {
@@ -543,13 +581,13 @@ __global__ CF_KV_OCC __launch_bounds__(64 * W) void kv_batched_kernel(cf_kv_batc
     gi = gn;
   }
 
-  // ---- reduce the wavefront: sum the 4 page groups (lanes t, t+16, t+32, t+48) after taking each lane's P.V sums
-  // back to absolute units, l over all lanes
+  // ---- reduce the wavefront: sum the hi and lo parts (lanes t and t + 16; lanes 32-63 hold the repeated rows
+  // 8-15) in absolute units, l over all lanes
 #pragma unroll
   for (int i = 0; i < D / 16; ++i)
 #pragma unroll
     for (int h = 0; h < kGqa; ++h) {
-      float v = ldexpf(acc_v[i][h], e_run);
+      float v = G < 2 ? ldexpf(acc_v[i][h], e_run) : 0.0f;
       v += __shfl_xor(v, 16);
       v += __shfl_xor(v, 32);
       acc_v[i][h] = v;
@@ -623,8 +661,6 @@ __global__ CF_KV_OCC __launch_bounds__(64 * W) void kv_batched_kernel(cf_kv_batc
 //            f16 hi + lo parts, one MFMA each (one f16 per weight loses near-cancelling outputs).
 // Operands: each group is converted once per workgroup into double-buffered LDS (see the kernel body).
 // A non-INT8 group in the prefix makes the prefix partials NaN, so every output is NaN (the prefix must be raw).
-typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ half8_t sym8_to_f16(uint32_t w0, uint32_t w1) {
   const half2_t off = {static_cast<_Float16>(-1152.0f), static_cast<_Float16>(-1152.0f)};

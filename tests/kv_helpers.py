@@ -6,14 +6,16 @@ import numpy as np
 import oracle as O
 
 
-def make_seqs(seq_tokens, kv_heads, D, seed, scale_spread=False, v_mult=None, cancel=None):
+def make_seqs(seq_tokens, kv_heads, D, seed, scale_spread=False, v_mult=None, cancel=None, page_spread=None):
     """K, V ~ N(0,1) per sequence [kv_heads, T, D]. v_mult[s][h] (optional) multiplies all of V of sequence s,
     head h: whole sequences / heads of small or huge V magnitude, so every page scale of that head is small or
     huge (not only single tokens inside a page, as scale_spread does).
     cancel = eps (optional): 16-token pages 2j and 2j + 1 get equal keys (so equal softmax weights) and values v
     and -(1 - eps) v (so the odd page's V scale is the even page's times 1 - eps and its symbols are the negated
     ones): every output is a sum of near-cancelling pairs p (v1 + v2) ~ eps p v, while a kernel that rounds each
-    token's weight p * v_scale on its own makes errors of the size of p v that no longer cancel."""
+    token's weight p * v_scale on its own makes errors of the size of p v that no longer cancel.
+    page_spread = b (optional): V of every 16-token page multiplied by 2^u, u uniform in [0, b), so the pages of one
+    64-token group have V scales up to 2^b apart."""
     rng = np.random.default_rng(seed)
     data = []
     for s, T in enumerate(seq_tokens):
@@ -24,6 +26,10 @@ def make_seqs(seq_tokens, kv_heads, D, seed, scale_spread=False, v_mult=None, ca
             V *= rng.choice([1e-3, 1.0, 8.0], size=(1, T, 1)).astype(np.float32)
         if v_mult is not None:
             V *= np.asarray(v_mult[s], np.float32).reshape(kv_heads, 1, 1)
+        if page_spread is not None:
+            npg = (T + 15) // 16
+            f = np.exp2(rng.uniform(0, page_spread, size=(kv_heads, npg))).astype(np.float32)
+            V *= np.repeat(f, 16, axis=1)[:, :T, None]
         if cancel is not None:
             for p0 in range(0, T - 31, 32):
                 K[:, p0 + 16:p0 + 32] = K[:, p0:p0 + 16]

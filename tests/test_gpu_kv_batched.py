@@ -19,10 +19,10 @@ def dev():
 
 
 def _run(dev, codec, seq_tokens, kv_heads, gqa, D, seed, query_pos=None, splits=(0,), shared=None,
-         scale_spread=False, raw_groups=None, v_mult=None, cancel=None):
+         scale_spread=False, raw_groups=None, v_mult=None, cancel=None, page_spread=None):
     import torch
     from chromofold_amd import kv
-    data = make_seqs(seq_tokens, kv_heads, D, seed, scale_spread, v_mult, cancel)
+    data = make_seqs(seq_tokens, kv_heads, D, seed, scale_spread, v_mult, cancel, page_spread)
     tables = None
     if codec == kv.CODEC_RANS_HYBRID:
         parts = []
@@ -145,6 +145,15 @@ def test_batched_wide_v_magnitudes(dev):
 def test_batched_cancellation(dev, codec, D):
     _run(dev, codec, [6200, 7000, 6145, 9000, 1, 6400], 2, 4, D, seed=71 + D + codec, splits=(1, 2, 0, 3),
          query_pos=[6199, 3500, 6144, 8999, 0, 100], cancel=1 / 64)
+
+
+@pytest.mark.parametrize("codec", [1, 2])
+def test_batched_page_scale_spread(dev, codec):
+    """The pages of one 64-token group share P.V units (the group's largest V scale): V scales spread by up to 2^16
+    across the pages of each group (every page of its own magnitude), alone and with cancelling page pairs, through
+    the narrow and wide shapes."""
+    _run(dev, codec, [6200, 7000, 300, 6400], 2, 4, 128, seed=87 + codec, splits=(1, 0, 3), page_spread=16)
+    _run(dev, codec, [6200, 700, 6145], 2, 4, 128, seed=89 + codec, splits=(1, 0), page_spread=12, cancel=1 / 64)
 
 
 def test_batched_cancellation_short_and_shared(dev):

@@ -252,3 +252,70 @@ def test_fixed_pages_paired_with_their_own_zero_points(dev):
     assert np.abs(got - ref).max() <= 2e-6
     got, ref = _run(dev, deq, pages, q, kvh, gqa, T - 24, 1 / np.sqrt(D), window=50)
     assert np.abs(got - ref).max() <= 2e-6
+
+
+@pytest.mark.parametrize("hd", [40, 80])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_scalar_route_head_dims(dev, hd, bits):
+    """head_dim not a multiple of 32 (80 is a real model head size): the reference sends these to its scalar kernel
+    (src/cuda/paged_kv_attention.cu:306-324). The adapter matrix's shape (2 KV heads, GQA 7, 32-token sealed pages
+    + a dense fp32 tail) with fixed-width pages, then Huffman pages whose rows start mid-way through 64-symbol
+    blocks, mixed with fixed-width ones, and a causal window."""
+    rng = np.random.default_rng(7000 + hd + bits)
+    kvh, gqa, N, P = 2, 7, 70, 32
+    K = rng.standard_normal((kvh, N, hd)).astype(np.float32)
+    V = rng.standard_normal((kvh, N, hd)).astype(np.float32)
+    pages, deq = [], []
+    for h in range(kvh):
+        for p0 in range(0, (N // P) * P, P):
+            page, kd, vd = fixed_page(K[h, p0:p0 + P], V[h, p0:p0 + P], h, p0, bits)
+            pages.append(page)
+            deq.append((h, p0, kd, vd))
+    t0 = (N // P) * P
+    tail = (t0, np.ascontiguousarray(K[:, t0:].transpose(1, 0, 2)), np.ascontiguousarray(V[:, t0:].transpose(1, 0, 2)))
+    q = rng.standard_normal((3, kvh * gqa, hd)).astype(np.float32)
+    got, ref = _run(dev, deq, pages, q, kvh, gqa, N - 3, 1 / np.sqrt(hd), tail=tail)
+    assert np.abs(got - ref).max() <= ABS_TOL
+    # Huffman pages (40 and 56 tokens: rows cross code blocks) after fixed-width ones
+    pages, deq = [], []
+    for h in range(kvh):
+        tok = 0
+        for kind, n in (("fixed", 32), ("huff", 40), ("huff", 56), ("fixed", 16)):
+            k = (rng.standard_normal((n, hd)) ** 3).astype(np.float32)
+            v = rng.standard_normal((n, hd)).astype(np.float32)
+            if kind == "huff":
+                page, kd, vd = huffman_page(k, v, h, tok, 8, 12)
+            else:
+                page, kd, vd = fixed_page(k, v, h, tok, bits)
+            pages.append(page)
+            deq.append((h, tok, kd, vd))
+            tok += n
+    q = rng.standard_normal((2, kvh * gqa, hd)).astype(np.float32)
+    got, ref = _run(dev, deq, pages, q, kvh, gqa, tok - 2, 1 / np.sqrt(hd))
+    assert np.abs(got - ref).max() <= ABS_TOL
+    got, ref = _run(dev, deq, pages, q, kvh, gqa, tok - 40, 1 / np.sqrt(hd), window=60)
+    assert np.abs(got - ref).max() <= ABS_TOL
+
+
+def test_scalar_route_head_dim_80_long_context_splits(dev):
+    """head_dim 80 at the split shapes: 64 query rows x GQA 7, 2 KV heads, 4096 tokens of int4 and Huffman pages
+    and a dense tail: the context is split over many workgroups and merged."""
+    rng = np.random.default_rng(8080)
+    kvh, gqa, T, P, hd = 2, 7, 4096, 32, 80
+    pages, deq = [], []
+    for p0 in range(0, T, P):
+        for h in range(kvh):
+            k = rng.standard_normal((P, hd)).astype(np.float32)
+            v = rng.standard_normal((P, hd)).astype(np.float32)
+            if (p0 // P + h) % 4 == 3:
+                page, kd, vd = huffman_page(k, v, h, p0)
+            else:
+                page, kd, vd = fixed_page(k, v, h, p0, 4 if (p0 // P) % 2 else 8)
+            pages.append(page)
+            deq.append((h, p0, kd, vd))
+    tail_k = rng.standard_normal((9, kvh, hd)).astype(np.float32)
+    tail_v = rng.standard_normal((9, kvh, hd)).astype(np.float32)
+    q = rng.standard_normal((64, kvh * gqa, hd)).astype(np.float32)
+    got, ref = _run(dev, deq, pages, q, kvh, gqa, T + 9 - 64, 1 / np.sqrt(hd), tail=(T, tail_k, tail_v))
+    assert np.isfinite(got).all()
+    assert np.abs(got - ref).max() <= ABS_TOL
