@@ -8,16 +8,18 @@
 //   1. table_prep_kernel: one workgroup per table blob derives the compact (freq, cum) pairs of its 256 joint
 //      symbols (last slot with offset 0 wins, exactly the host loader's rule) and whether the table is usable;
 //      workgroup 0 also clears the status word.
-//   2. encode_kernel: one 4-wavefront workgroup per chain unit (a group alone, or a group and the group that
-//      continues its chain; the workgroup of a continuing group only checks its flag). Phase 1: wavefront G
-//      quantises page G of each group of the unit (absmax over the page's present tokens, IEEE division, round half
-//      to even) into LDS symbol tiles laid out for the later reads (K token-major, V dim-major, both padded to odd
-//      word strides). Phase 2: wavefronts 0 and 1 rANS-code the K and V chains across the unit's coded groups in
+//   2. encode_kernel: one 8-wavefront workgroup per chain unit (a group alone, or a group and the group that
+//      continues its chain; the workgroup of a continuing group only checks its flag). The unit's fields all
+//      depend only on the group index, so they are requested at once, and every wavefront issues its page's K/V
+//      loads before the first barrier (two memory latencies before any compute, not one per field). Phase 1:
+//      wavefront 4 X + G quantises page G of group X (absmax over the page's present tokens, IEEE division, round
+//      half to even) into LDS symbol tiles laid out for the later reads (K token-major, V dim-major, both padded to
+//      odd word strides). Phase 2: wavefronts 0 and 1 rANS-code the K and V chains across the unit's coded groups in
 //      reverse (64 interleaved states each); the renormalisation words of one step are placed with a ballot prefix
 //      count, written from the top of an LDS buffer down so that the reversed stream needs no second pass. At the
-//      same time wavefronts 2 and 3 write the K and V raw words (frame-rotated nibbles, crumbs and signs). Phase 3
-//      writes the headers and word streams (or the INT8 blob of a group holding -128) into fixed-capacity staging
-//      slots, and each blob's size in 16-byte units.
+//      same time wavefronts 2-5 write the raw words of the (group, stream) pairs (frame-rotated nibbles, crumbs and
+//      signs). Phase 3 writes the headers and word streams (or the INT8 blob of a group holding -128) into
+//      fixed-capacity staging slots, and each blob's size in 16-byte units.
 //   3. an exclusive scan of the sizes (hipcub), then pack_kernel copies every blob to pool[pool_at + offset],
 //      writes offsets_out and *pool_end — or nothing at all when any group or the pool capacity failed, in which
 //      case the status word holds CF_ERR_INVALID_ARGUMENT.
@@ -30,7 +32,7 @@
 
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kEncThreads = 512;  // encode_kernel: 8 wavefronts, one per page of the unit's (up to) two groups
 constexpr uint32_t kHeader = 64;
 constexpr uint32_t kStateBytes = 2 * 64 * 4;
 constexpr uint32_t kMaxDim = CF_KV_MAX_HEAD_DIM;
@@ -133,7 +135,7 @@ __device__ __forceinline__ uint32_t bigs_of(uint32_t w) {
   return j;
 }
 
-__global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
+__global__ void __launch_bounds__(kEncThreads) encode_kernel(EncodeArgs a) {
   __shared__ uint32_t kS[2][4 * 16 * kKStride];
   __shared__ uint32_t vT[2][4 * kMaxDim * kVStride];
   __shared__ uint16_t s_words[2][2][kStreamCap];  // [stream][group of the unit]
@@ -141,34 +143,72 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
   __shared__ float s_scale[2][2][4];               // [group][K, V][page]
   __shared__ uint32_t s_tc[2][4], s_count[2][2], s_bad, s_minus[2];
 
-  const uint64_t g = blockIdx.x;
+  // Group of this workgroup: the even groups first, then the odd ones. Chain units usually start at even groups
+  // (pairs 2k, 2k + 1), and the workgroup of a continuing group ends almost at once. With g = blockIdx.x the two kinds
+  // alternate in dispatch order, and the dispatcher's round-robin over the CUs of an XCD then placed every unit on
+  // the same half of the CUs (measured: units on 128 of 256 CUs, the near-empty workgroups on the other 128); this
+  // order dispatches the units over every CU first. A bijection on [0, ngroups).
+  const uint64_t half = (a.ngroups + 1) / 2, b = blockIdx.x;
+  const uint64_t g = b < half ? 2 * b : 2 * (b - half) + 1;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t D = a.head_dim, nq = D / 4, ng = D / 16;
   const bool rans = a.codec == CF_KV_CODEC_RANS_HYBRID;
+  // Every per-unit field depends only on g, so all of them are requested at once (one memory latency), and each
+  // wavefront starts loading its page's K/V right after (a second one) before any barrier.
   const uint32_t head = a.heads ? a.heads[g] : 0u;
-  if (a.continues && a.continues[g]) {  // the group before this one codes it: only check that it may
+  const bool cont = a.continues && a.continues[g];
+  const bool cont_next = a.continues && g + 1 < a.ngroups && a.continues[g + 1];
+  if (cont) {  // the group before this one codes it: only check that it may
     if (tid == 0 && (g == 0 || a.continues[g - 1] || (a.heads && a.heads[g - 1] != head))) {
       *a.status = CF_ERR_INVALID_ARGUMENT;
       a.units[g] = 0;
     }
     return;
   }
-  const uint32_t ngu = (a.continues && g + 1 < a.ngroups && a.continues[g + 1]) ? 2u : 1u;  // groups of the unit
-  if (tid == 0) {
-    uint32_t bad = 0;
-    for (uint32_t X = 0; X < ngu; ++X) {
+  const uint32_t ngu = cont_next ? 2u : 1u;  // groups of the unit
+  // wavefront w quantises page G = w % 4 of group X = w / 4 of the unit
+  const uint32_t X1 = static_cast<uint32_t>(wave) >> 2, G1 = static_cast<uint32_t>(wave) & 3u;
+  const uint32_t pc1 = X1 < ngu ? a.page_counts[g + X1] : 0u;
+  const uint64_t p01 = X1 < ngu ? a.first_page[g + X1] : 0u;
+  const bool page_ok = G1 < pc1 && pc1 <= 4;  // the page exists (pc1 > 4 fails the unit below)
+  const uint64_t page_vals = 16ull * D;
+  const float *kp = a.keys + (p01 + G1) * page_vals;
+  const float *vp = a.values + (p01 + G1) * page_vals;
+  // K: float4 index i = r * 64 + lane -> token i / nq, quad i % nq (4 * D float4 per page, <= 8 per lane); all 16
+  // token slots of the page are read (page-major [*][16][D] arrays), tokens past its count are masked below
+  float4 kx[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const uint32_t i = r * 64 + lane;
+    kx[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (page_ok && i < 4 * D) kx[r] = *reinterpret_cast<const float4 *>(kp + 4ull * i);
+  }
+  // V: lane owns dims d = lane, lane + 64; 16 tokens each
+  float vx[2][16];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const uint32_t d = r * 64 + lane;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) vx[r][t] = (page_ok && d < D) ? vp[static_cast<uint64_t>(t) * D + d] : 0.0f;
+  }
+  if (tid < 8) {  // thread 4 X + G checks page G of group X
+    const uint32_t X = static_cast<uint32_t>(tid) >> 2, G = static_cast<uint32_t>(tid) & 3u;
+    bool bad = false;
+    uint32_t tc = 0;
+    if (X < ngu) {
       const uint32_t pc = a.page_counts[g + X];
-      const uint64_t p0 = a.first_page[g + X];
-      if (pc == 0 || pc > 4) bad = 1;
-      for (int G = 0; G < 4; ++G) {
-        const uint32_t tc = static_cast<uint32_t>(G) < pc ? (a.token_counts ? a.token_counts[p0 + G] : 16u) : 0u;
-        if (static_cast<uint32_t>(G) < pc && (tc == 0 || tc > 16)) bad = 1;
-        s_tc[X][G] = bad ? 0u : tc;
+      bad = pc == 0 || pc > 4;
+      if (!bad && G < pc) {
+        tc = a.token_counts ? a.token_counts[a.first_page[g + X] + G] : 16u;
+        bad = tc == 0 || tc > 16;
       }
-      s_minus[X] = 0;
+      s_tc[X][G] = tc;
+      if (G == 0) s_minus[X] = 0;
     }
-    if (rans && (2ull * head + 1 >= a.table_count || !a.tvalid[2 * head] || !a.tvalid[2 * head + 1])) bad = 1;
-    s_bad = bad;
+    if (tid == 0 && rans && (2ull * head + 1 >= a.table_count || !a.tvalid[2 * head] || !a.tvalid[2 * head + 1]))
+      bad = true;
+    const uint64_t any = __ballot(bad);
+    if (tid == 0) s_bad = any != 0 ? 1u : 0u;
   }
   __syncthreads();
   if (s_bad) {
@@ -179,28 +219,20 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
     return;
   }
   if (rans) {  // head validated above: tables 2 head and 2 head + 1 exist
-    for (int i = tid; i < 512; i += kThreads)
+    for (int i = tid; i < 512; i += kEncThreads)
       s_tab[i >> 8][i & 255] = a.ctab[(2ull * head + (i >> 8)) * 256 + (i & 255)];
   }
 
-  // ---- phase 1: wavefront G quantises page G of K and V of every group of the unit
-  for (uint32_t X = 0; X < ngu; ++X) {
-    const int G = wave;
+  // ---- phase 1: wavefront (X, G) quantises page G of K and V of group X of the unit
+  if (X1 < ngu) {
+    const uint32_t X = X1, G = G1;
     const uint32_t tc = s_tc[X][G];
-    const uint64_t page_vals = 16ull * D;
-    const uint64_t p0 = a.first_page[g + X];
-    const float *kp = a.keys + (p0 + G) * page_vals;
-    const float *vp = a.values + (p0 + G) * page_vals;
     bool minus = false;  // a symbol 0 (q = -128) among the present tokens
-    // K: float4 index i = r * 64 + lane -> token i / nq, quad i % nq (4 * D float4 per page, <= 8 per lane)
-    float4 kx[8];
     float m = 0.0f;
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       const uint32_t i = r * 64 + lane;
-      kx[r] = make_float4(0.f, 0.f, 0.f, 0.f);
       if (i < 4 * D && i / nq < tc) {
-        kx[r] = *reinterpret_cast<const float4 *>(kp + 4ull * i);
         m = __builtin_fmaxf(m, __builtin_fabsf(kx[r].x));
         m = __builtin_fmaxf(m, __builtin_fabsf(kx[r].y));
         m = __builtin_fmaxf(m, __builtin_fabsf(kx[r].z));
@@ -224,20 +256,13 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
         kS[X][(G * 16 + t) * kKStride + q] = w;
       }
     }
-    // V: lane owns dims d = lane, lane + 64; 16 tokens each, packed as 4 token quads
-    float vx[2][16];
     m = 0.0f;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const uint32_t d = r * 64 + lane;
 #pragma unroll
-      for (int t = 0; t < 16; ++t) {
-        vx[r][t] = 0.0f;
-        if (d < D && static_cast<uint32_t>(t) < tc) {
-          vx[r][t] = vp[static_cast<uint64_t>(t) * D + d];
-          m = __builtin_fmaxf(m, __builtin_fabsf(vx[r][t]));
-        }
-      }
+      for (int t = 0; t < 16; ++t)
+        if (d < D && static_cast<uint32_t>(t) < tc) m = __builtin_fmaxf(m, __builtin_fabsf(vx[r][t]));
     }
     m = wave_max(m);
     const float vs = m == 0.0f ? 1.0f : m / 127.0f;
@@ -300,34 +325,32 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
       if (lane == 0) s_count[s][X] = base;
     }
     *reinterpret_cast<uint32_t *>(blob_of(list[0]) + kHeader + 4 * (s * 64 + lane)) = x;
-  } else if (wave >= 2) {
-    // ---- raw words of stream wave - 2 for every coded group: nibbles, crumbs and signs in their quads' frames
-    const int s = wave - 2;
-    for (uint32_t li = 0; li < nlist; ++li) {
-      const uint32_t X = list[li];
-      uint32_t *out = reinterpret_cast<uint32_t *>(blob_of(X) + raw_at(X)) + s * raw_words;
-      for (uint32_t sg = 0; sg < sgroups; ++sg) {
-        uint32_t wd[7] = {0, 0, 0, 0, 0, 0, 0};
+  } else if (wave >= 2 && wave < 6 && static_cast<uint32_t>(wave - 2) / 2 < nlist) {
+    // ---- raw words of stream s of coded group list[li]: nibbles, crumbs and signs in their quads' frames
+    const int s = (wave - 2) & 1;
+    const uint32_t X = list[(wave - 2) / 2];
+    uint32_t *out = reinterpret_cast<uint32_t *>(blob_of(X) + raw_at(X)) + s * raw_words;
+    for (uint32_t sg = 0; sg < sgroups; ++sg) {
+      uint32_t wd[7] = {0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const int q = 8 * sg + k;
-          const uint32_t w = s == 0 ? k_word(kS[X], G, t, q) : v_word(vT[X], G, t, q, ng);
-          uint32_t nib = 0, cr = 0, sn = 0;
+      for (int k = 0; k < 8; ++k) {
+        const int q = 8 * sg + k;
+        const uint32_t w = s == 0 ? k_word(kS[X], G, t, q) : v_word(vT[X], G, t, q, ng);
+        uint32_t nib = 0, cr = 0, sn = 0;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint32_t b = (w >> (8 * i)) & 255u;
-            const uint32_t mag = b >= 128u ? b - 128u : 128u - b;
-            nib |= (mag & 15u) << (8 * i);
-            cr |= ((mag >> 4) & 3u) << (8 * i + 4);
-            sn |= (b < 128u ? 1u : 0u) << (8 * i + 7);
-          }
-          wd[kNWord[k]] |= rotl(nib, kFrame[k]);
-          wd[k < 4 ? 2 : 5] |= rotl(cr, kFrame[k]);
-          wd[6] |= rotl(sn, kFrame[k]);
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t b = (w >> (8 * i)) & 255u;
+          const uint32_t mag = b >= 128u ? b - 128u : 128u - b;
+          nib |= (mag & 15u) << (8 * i);
+          cr |= ((mag >> 4) & 3u) << (8 * i + 4);
+          sn |= (b < 128u ? 1u : 0u) << (8 * i + 7);
         }
-#pragma unroll
-        for (int w = 0; w < 7; ++w) out[(7 * sg + w) * 64 + lane] = wd[w];
+        wd[kNWord[k]] |= rotl(nib, kFrame[k]);
+        wd[k < 4 ? 2 : 5] |= rotl(cr, kFrame[k]);
+        wd[6] |= rotl(sn, kFrame[k]);
       }
+#pragma unroll
+      for (int w = 0; w < 7; ++w) out[(7 * sg + w) * 64 + lane] = wd[w];
     }
   }
   __syncthreads();
@@ -341,7 +364,7 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
     if (!coded) {
       // INT8: word (q * 64 + L) of stream s = the 4 symbols of quad q of lane L
       uint32_t *out = reinterpret_cast<uint32_t *>(blob + kHeader);
-      for (uint32_t i = tid; i < 2 * nq * 64; i += kThreads) {
+      for (uint32_t i = tid; i < 2 * nq * 64; i += kEncThreads) {
         const uint32_t s = i / (nq * 64), r = i % (nq * 64), q = r / 64, L = r % 64;
         out[i] = s == 0 ? k_word(kS[X], L >> 4, L & 15, q) : v_word(vT[X], L >> 4, L & 15, q, ng);
       }
@@ -351,13 +374,13 @@ __global__ void __launch_bounds__(kThreads) encode_kernel(EncodeArgs a) {
       wc[1] = s_count[1][X];
       const uint64_t wat = raw_at(X) + 2ull * raw_words * 4;  // first rANS word of the blob
       uint16_t *wo = reinterpret_cast<uint16_t *>(blob + wat);  // K stream, then V
-      for (uint32_t i = tid; i < wc[0] + wc[1]; i += kThreads) {
+      for (uint32_t i = tid; i < wc[0] + wc[1]; i += kEncThreads) {
         const uint32_t s = i < wc[0] ? 0u : 1u, at = i - (s ? wc[0] : 0u);
         wo[i] = s_words[s][X][kStreamCap - wc[s] + at];
       }
       const uint64_t end = wat + 2ull * (wc[0] + wc[1]);
       size = align16(end);
-      for (uint64_t b = end + tid; b < size; b += kThreads) blob[b] = 0;
+      for (uint64_t b = end + tid; b < size; b += kEncThreads) blob[b] = 0;
     }
     if (tid == 0) {
       cf_kv_group_header h{};
@@ -479,7 +502,7 @@ extern "C" cf_status cf_kv_encode_groups_async(uint32_t codec, const float *keys
   if (cfd::launch_status() != CF_OK) return CF_ERR_CUDA;
   EncodeArgs a{keys, values, first_page, page_counts, token_counts, heads, continues, ctab, tvalid, ngroups,
                table_count, codec, head_dim, ws + L.stage, L.cap, units, status};
-  encode_kernel<<<static_cast<unsigned>(ngroups), kThreads, 0, st>>>(a);
+  encode_kernel<<<static_cast<unsigned>(ngroups), kEncThreads, 0, st>>>(a);
   if (cfd::launch_status() != CF_OK) return CF_ERR_CUDA;
   size_t scan_bytes = L.scan_bytes;
   if (hipcub::DeviceScan::ExclusiveSum(ws + L.scan, scan_bytes, units, offs, static_cast<int>(ngroups + 1), st) !=
