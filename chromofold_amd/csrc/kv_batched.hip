@@ -930,8 +930,9 @@ uint32_t cu_count() {
 // Narrow (4 wavefronts, three workgroups per CU) is the base shape. Issue arbitration favours the oldest wavefronts,
 // so the three workgroups of a CU finish far apart; when the grid is one round of workgroups (fewer units than three
 // per CU) that spread is the tail of the whole launch. Launches with at most one (sequence, head) unit per CU go
-// wide (12 wavefronts, one workgroup per CU, one round) when every wavefront still gets about 4 chain pairs or more:
-// the priority-weighted pair blocks (wide_block) then let the wavefronts of a CU finish together. Larger grids stay
+// wide (12 wavefronts, one workgroup per CU, one round) when every wavefront still gets about 2 chain pairs or more:
+// the priority-weighted pair blocks (wide_block) then let the wavefronts of a CU finish together (C4 at 4k tokens:
+// 59-60 us wide with one split against 68 us for three narrow splits and their merge). Larger grids stay
 // narrow: the dispatcher refills a CU as each workgroup ends, and three workgroups of different sequences on one CU
 // share its L1 when their pools share groups (a common prompt prefix).
 // Splits: enough workgroups to fill the chip in one round when the (sequence, head) units alone do not (a partial
@@ -940,7 +941,7 @@ uint32_t cu_count() {
 struct BatchedPlan {
   uint32_t splits, waves;
 };
-constexpr uint32_t kWidePairsPerWave = 4;
+constexpr uint32_t kWidePairsPerWave = 2;
 
 BatchedPlan batched_plan(const cf_kv_batched_desc *d) {
   const uint32_t units = d->seq_count * d->kv_head_count;

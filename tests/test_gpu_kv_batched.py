@@ -113,9 +113,9 @@ def test_batched_v_magnitudes_hd64(dev):
 
 
 # Wide workgroups (12 wavefronts, each taking a priority-weighted block of chain pairs, V quads parked in LDS) serve
-# launches with at most one (sequence, head) unit per CU whose splits keep >= 48 chain pairs each; splits=1 on these
-# >= 6144-token contexts selects them (units x 1 <= CUs, >= 71 pairs), splits=2 and the automatic choice the narrow
-# shape. The pair blocks are static, so the outputs are bitwise reproducible.
+# launches with at most one (sequence, head) unit per CU whose splits keep >= 24 chain pairs each; splits=1 and 2 on
+# these >= 6144-token contexts select them (units x splits <= CUs, 71 and 35 pairs per split), the automatic choice
+# (21 splits of 3 pairs) the narrow shape. The pair blocks are static, so the outputs are bitwise reproducible.
 @pytest.mark.parametrize("codec", [1, 2])
 @pytest.mark.parametrize("D", [128, 64])
 def test_batched_wide_workgroups(dev, codec, D):
