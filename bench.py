@@ -155,23 +155,45 @@ def bench_fm(steps: int, warmup: int, cpu: bool = True) -> dict:
         j = owner[k]
         a = int(p_h[k])
         assert np.array_equal(s[a:a + plen[j]], flat[pstart[j]:pstart[j] + plen[j]]), "located position mismatch"
+    # the derived line layout (built once at load): same results, timed beside the RRR kernels
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    fm.build_lines()
+    torch.cuda.synchronize()
+    t_lines_build = time.perf_counter() - t0
+    cnt_l = fm.count_lines(dpat, dps, dpl)
+    lo_l, hi_l = fm.ranges_lines(dpat, dps, dpl)
+    pos_l = torch.empty_like(rows)
+    fm.locate_lines(rows, pos_l)
+    assert torch.equal(cnt_l, cnt) and torch.equal(lo_l, lo) and torch.equal(hi_l, hi), "line layout != RRR search"
+    assert torch.equal(pos_l, pos), "line layout != RRR locate"
     _, per_c = _events_time(lambda: fm.count(dpat, dps, dpl), steps, warmup)
     _, per_l = _events_time(lambda: fm.locate(rows, pos), steps, warmup)
-    t_c = float(np.mean(per_c)) * 1e-3
-    t_l = float(np.mean(per_l)) * 1e-3
-    res = {"count_mpats": pstart.size / t_c / 1e6, "count_ms": t_c * 1e3, "occurrences": occ,
-           "locate_mocc": occ / t_l / 1e6, "locate_ms": t_l * 1e3, "gpu_sa_build_s": info["sa_s"],
-           "gpu_index_build_s": info["build_s"], "index_bytes": fm.w.device_bytes()}
-    # cost model (algorithmic bytes): count = 1920 B per pattern symbol (2 rank1 per level x 15 levels x 32 B, twice:
-    # lo and hi) + C[] 8 B; locate = 22.4 KB per occurrence (15.5 expected LF steps x (access 480 + rank 960 + mark
-    # word 4) + sval 4 + msb 4)
-    bytes_count = float(plen.astype(np.int64).sum()) * (1920 + 8)
-    bytes_locate = occ * (15.5 * (480 + 960 + 4) + 8)
-    for key, b, t, tr in (("count_roofline", bytes_count, t_c, MEASURED_TRAFFIC.get(("fm_count", n, pstart.size))),
-                          ("locate_roofline", bytes_locate, t_l, MEASURED_TRAFFIC.get(("fm_locate", n, occ)))):
-        res[key] = {"bound": "hbm (nominal; the index is L2-resident)", "achieved": b / t / 1e9,
+    _, per_cl = _events_time(lambda: fm.count_lines(dpat, dps, dpl, out=cnt_l), steps, warmup)
+    _, per_ll = _events_time(lambda: fm.locate_lines(rows, pos_l), steps, warmup)
+    t_c, t_l, t_cl, t_ll = (float(np.mean(x)) * 1e-3 for x in (per_c, per_l, per_cl, per_ll))
+    res = {"count_mpats": pstart.size / t_cl / 1e6, "count_ms": t_cl * 1e3, "occurrences": occ,
+           "locate_mocc": occ / t_ll / 1e6, "locate_ms": t_ll * 1e3,
+           "rrr_count_mpats": pstart.size / t_c / 1e6, "rrr_count_ms": t_c * 1e3,
+           "rrr_locate_mocc": occ / t_l / 1e6, "rrr_locate_ms": t_l * 1e3,
+           "gpu_sa_build_s": info["sa_s"], "gpu_index_build_s": info["build_s"], "lines_build_s": t_lines_build,
+           "index_bytes": fm.w.device_bytes(), "lines_bytes": fm.lines.numel()}
+    # cost models (algorithmic bytes), symbols = pattern symbols per launch:
+    #   RRR count: 1928 B per symbol (rank(c, lo) and rank(c, hi), each 2 rank1 per level x 15 levels x 32 B, + 8 B
+    #   of C[]); RRR locate: 15.5 expected LF steps x (access 480 + rank 960 + mark word 4) + sval 4 + msb 4;
+    #   line count: 1928 B per symbol (2 rank1 per level x 15 levels x one 64-B record, + lfb 4 B + the symbol 4 B);
+    #   line locate: 15.5 LF steps x (15 records x 64 B + lfb 4 + mark word 4) + sval 4 + msb 4.
+    syms = float(plen.astype(np.int64).sum())
+    models = {"count_roofline": (syms * (2 * 15 * 64 + 8), t_cl, ("fm_count_lines", n, pstart.size)),
+              "locate_roofline": (occ * (15.5 * (15 * 64 + 8) + 8), t_ll, ("fm_locate_lines", n, occ)),
+              "rrr_count_roofline": (syms * (1920 + 8), t_c, ("fm_count", n, pstart.size)),
+              "rrr_locate_roofline": (occ * (15.5 * (480 + 960 + 4) + 8), t_l, ("fm_locate", n, occ))}
+    for key, (b, t, tk) in models.items():
+        tr = MEASURED_TRAFFIC.get(tk)
+        res[key] = {"bound": "hbm (nominal; the index is cache-resident)", "achieved": b / t / 1e9,
                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": b / t / 1e9 / HBM_PEAK_GBS, "model_bytes": b,
-                    "traffic": tr, "traffic_gbs": tr / t / 1e9 if tr else None}
+                    "traffic": tr, "traffic_gbs": tr / t / 1e9 if tr else None,
+                    "traffic_over_model": tr / b if tr else None}
     if cpu:
         import oracle as O
         from chromofold_amd.search import to_u32
@@ -350,15 +372,17 @@ def bench_cache_peaks(steps: int = 10, warmup: int = 2) -> dict:
 
 
 def bench_kv(steps: int, warmup: int, context: int = 32768, batch: int = 32, cpu: bool = True,
-             check_seqs: int = 8, warm_s: float = 3.0, stream_peak: bool = True) -> dict:
+             check_seqs: int = 8, warm_s: float = 3.0, stream_peak: bool = True, codec: int | None = None) -> dict:
     """Llama-3-8B layer shape (32 q / 8 KV heads, hd 128, 16-token pages), K/V ~ N(0,1) fp32
     generated on the device (seeded), sealed on the device into RANS_HYBRID page groups (per-page-per-head int8
     absmax, rANS) with cf_kv_encode_groups_async; one decode token per sequence per step.
     Gate: the first check_seqs sequences' outputs against the float64 oracle over the pool's own blobs (decoded by
     the oracle), every (sequence, head) row within 1e-3 normwise. The same oracle run on all host threads is the
-    CPU baseline (plus its 1-thread figure on one sequence)."""
+    CPU baseline (plus its 1-thread figure on one sequence). codec=kv.CODEC_INT8 seals the same data as raw int8
+    groups instead (the decode-free codec, 8.03 b/value), to show what the rANS decode costs against raw bytes."""
     import torch
     from chromofold_amd import kv, synth
+    codec = kv.CODEC_RANS_HYBRID if codec is None else codec
 
     H, QH, D = 8, 32, 128
     gqa = QH // H
@@ -370,7 +394,9 @@ def bench_kv(steps: int, warmup: int, context: int = 32768, batch: int = 32, cpu
     Kh = K[0, 0, :1024].cpu().numpy().reshape(-1, 16, D)
     Vh = V[0, 0, :1024].cpu().numpy().reshape(-1, 16, D)
     tables = np.concatenate([t for _ in range(H) for t in (kv.build_table(Kh), kv.build_table(Vh))])
-    kvb = kv.seal_device(kv.CODEC_RANS_HYBRID, K, V, torch.from_numpy(tables).to("cuda:0"))
+    if codec == kv.CODEC_INT8:
+        tables = np.zeros(0, np.uint8)
+    kvb = kv.seal_device(codec, K, V, torch.from_numpy(tables).to("cuda:0") if tables.size else None)
     # order-0 entropy of the int8 symbols (sequence 0, every head, K and V; per-page absmax, half to even)
     pg = torch.cat([K[0], V[0]]).reshape(-1, 16 * D)
     sym = torch.round(pg / torch.where(pg.abs().amax(1, keepdim=True) == 0, 1.0, pg.abs().amax(1, keepdim=True) / 127))
@@ -1113,6 +1139,12 @@ def main() -> int:
         if args.workload != "kv32":
             k4 = bench_kv(min(args.steps, 50), 3, context=4096, cpu=False, check_seqs=4,
                           warm_s=min(args.warm_s, 1.0), stream_peak=False)
+            from chromofold_amd import kv as _kv
+            k8 = bench_kv(min(args.steps, 20), 2, cpu=False, check_seqs=2, warm_s=min(args.warm_s, 1.0),
+                          stream_peak=False, codec=_kv.CODEC_INT8)
+            secondary["c4_32k_int8_codec"] = {k: k8[k] for k in ("workload", "tokens_per_s", "ms_per_step", "kernel_ms",
+                                                                 "bits_per_value", "max_normwise_err")}
+            secondary["c4_32k_int8_codec"]["roofline_frac"] = k8["roofline"]["frac"]
             secondary["c4_4k"] = {k: k4[k] for k in ("workload", "tokens_per_s", "ms_per_step", "kernel_ms",
                                                      "bits_per_value", "max_normwise_err")}
             secondary["c4_4k"]["roofline_frac"] = k4["roofline"]["frac"]
@@ -1136,7 +1168,7 @@ def main() -> int:
             secondary["cache_peaks"] = peaks
             l2 = peaks["l2_read_gbs"]
             secondary["c1_rrr"]["rank_frac_of_l2"] = rrr["rank_roofline"]["achieved"] / l2
-            for k in ("count_roofline", "locate_roofline"):
+            for k in ("count_roofline", "locate_roofline", "rrr_count_roofline", "rrr_locate_roofline"):
                 r = secondary["c2_fm"][k]
                 r["frac_of_l2"] = r["achieved"] / l2
                 if r["traffic_gbs"]:  # L2-miss traffic against the Infinity Cache's read rate

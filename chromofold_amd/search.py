@@ -115,6 +115,7 @@ class FmIndex:
     n: int
     sa_sample: int
     tensors: dict
+    lines: "torch.Tensor | None" = None  # the derived line layout, built on first use (build_lines)
 
     @classmethod
     def from_host(cls, arrays, device="cuda") -> "FmIndex":
@@ -149,6 +150,40 @@ class FmIndex:
                 "cf_fm_locate_async")
         return out
 
+    # ---- the derived line layout (cf_fm_lines_*): same results, one 64-byte line per rank1
+    def build_lines(self, stream=None) -> torch.Tensor:
+        """Builds (once) and returns the line layout of this index (a uint8 device tensor)."""
+        if self.lines is None:
+            v = self.view()
+            nb = int(A.lib().cf_fm_lines_bytes(v))
+            if nb == 0:
+                raise A.CfError(A.CF_ERR_INVALID_ARGUMENT, "cf_fm_lines_bytes")
+            lines = torch.empty(nb, dtype=torch.uint8, device=self.tensors["C"].device)
+            A.check(A.lib().cf_fm_lines_build_async(v, _ptr(lines), nb, stream_ptr(stream)), "cf_fm_lines_build_async")
+            self.lines = lines
+        return self.lines
+
+    def count_lines(self, pat, pstart, plen, out=None, stream=None) -> torch.Tensor:
+        out = torch.empty(pstart.numel(), dtype=torch.int32, device=pstart.device) if out is None else out
+        A.check(A.lib().cf_fm_count_lines_async(self.view(), _ptr(self.build_lines(stream)), _ptr(pat), _ptr(pstart),
+                                                _ptr(plen), _ptr(out), pstart.numel(), stream_ptr(stream)),
+                "cf_fm_count_lines_async")
+        return out
+
+    def ranges_lines(self, pat, pstart, plen, stream=None):
+        lo = torch.empty(pstart.numel(), dtype=torch.int32, device=pstart.device)
+        hi = torch.empty_like(lo)
+        A.check(A.lib().cf_fm_ranges_lines_async(self.view(), _ptr(self.build_lines(stream)), _ptr(pat), _ptr(pstart),
+                                                 _ptr(plen), _ptr(lo), _ptr(hi), pstart.numel(), stream_ptr(stream)),
+                "cf_fm_ranges_lines_async")
+        return lo, hi
+
+    def locate_lines(self, rows: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+        out = torch.empty_like(rows, dtype=torch.int32) if out is None else out
+        A.check(A.lib().cf_fm_locate_lines_async(self.view(), _ptr(self.build_lines(stream)), _ptr(rows), _ptr(out),
+                                                 rows.numel(), stream_ptr(stream)), "cf_fm_locate_lines_async")
+        return out
+
 
 def gpu_suffix_array(s: torch.Tensor, stream=None) -> torch.Tensor:
     """Suffix array of the int32 device text `s` (sentinel-terminated) via cf_suffix_array."""
@@ -177,6 +212,11 @@ A.declare("cf_rrrw_build_workspace_bytes", A.U64, [A.U64, A.U32])
 A.declare("cf_rrrw_build", A.I32, [A.P, A.U64, A.U32, A.P, A.U64, C.POINTER(cf_rrrw_layout), A.P])
 A.declare("cf_rrrw_build_copy", A.I32, [A.P, C.POINTER(cf_rrrw_layout), C.POINTER(cf_rrrw_arrays), A.P])
 A.declare("cf_fm_build_workspace_bytes", A.U64, [A.I32, A.I32])
+A.declare("cf_fm_lines_bytes", A.U64, [A.cf_fm_view])
+A.declare("cf_fm_lines_build_async", A.I32, [A.cf_fm_view, A.P, A.U64, A.P])
+A.declare("cf_fm_count_lines_async", A.I32, [A.cf_fm_view, A.P, A.P, A.P, A.P, A.P, A.SZ, A.P])
+A.declare("cf_fm_ranges_lines_async", A.I32, [A.cf_fm_view, A.P, A.P, A.P, A.P, A.P, A.P, A.SZ, A.P])
+A.declare("cf_fm_locate_lines_async", A.I32, [A.cf_fm_view, A.P, A.P, A.P, A.SZ, A.P])
 A.declare("cf_fm_build_aux", A.I32, [A.P, A.P, A.I32, A.I32, A.I32, A.P, A.P, A.P, A.P, A.P, C.POINTER(C.c_int32),
                                      A.P, A.U64, A.P])
 

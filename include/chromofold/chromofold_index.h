@@ -11,6 +11,7 @@
 #include <stdint.h>
 
 #include "chromofold/chromofold.h"
+#include "chromofold/chromofold_search.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -72,6 +73,30 @@ uint64_t cf_fm_build_workspace_bytes(int32_t n, int32_t sigma);
 cf_status cf_fm_build_aux(const int32_t *s, const int32_t *sa, int32_t n, int32_t sigma, int32_t sa_sample,
                           uint32_t *bwt, int32_t *C, uint32_t *mwords, int32_t *msb, int32_t *sval, int32_t *sval_count,
                           void *workspace, uint64_t workspace_bytes, void *stream);
+
+/* ---- derived on-device line layout for FM search (no counterpart in the reference; the .cffm on disk and the
+ * cf_fm_view arrays are unchanged). Built once per loaded index from its cf_fm_view; the search entry points below
+ * return exactly what cf_fm_count_async / cf_fm_ranges_async / cf_fm_locate_async return for the same view, with one
+ * 64-byte line per rank1 instead of the RRR level's three or four and fewer rank1 per step (2 per level for
+ * backward search, 1 for an LF step). Layout of `lines` (u32 words, 64-byte aligned):
+ *   [bits][nrec][16] records, nrec = n / 480 + 1: word 0 = ones of the level before bit 480 r, words 1..15 = level
+ *   bits [480 r, 480 r + 480) LSB-first;
+ *   then [sigma] int32 lfb[c] = C[c] - (position where the wavelet rank walk of symbol c from 0 ends).
+ * Size: (bits * nrec * 16 + sigma) * 4 bytes, about 1.07 bits per BWT bit per level. */
+
+/* Bytes of the line layout of `v` (0 if the view is out of range). Host only. */
+uint64_t cf_fm_lines_bytes(cf_fm_view v);
+/* Builds the line layout of `v` into `lines` (device, >= cf_fm_lines_bytes(v) bytes, 16-byte aligned), stream
+ * ordered after whatever wrote the view's arrays. Reads the view's RRR arrays, C and zeros. */
+cf_status cf_fm_lines_build_async(cf_fm_view v, uint32_t *lines, uint64_t bytes, void *stream);
+/* cf_fm_count_async / cf_fm_ranges_async / cf_fm_locate_async (chromofold_search.h) over the line layout built
+ * from the same view: same arguments, same results. */
+cf_status cf_fm_count_lines_async(cf_fm_view v, const uint32_t *lines, const int32_t *pat, const int32_t *pstart,
+                                  const int32_t *plen, uint32_t *out, size_t npat, void *stream);
+cf_status cf_fm_ranges_lines_async(cf_fm_view v, const uint32_t *lines, const int32_t *pat, const int32_t *pstart,
+                                   const int32_t *plen, int32_t *lo_out, int32_t *hi_out, size_t npat, void *stream);
+cf_status cf_fm_locate_lines_async(cf_fm_view v, const uint32_t *lines, const int32_t *r_in, int32_t *out,
+                                   size_t nocc, void *stream);
 
 /* ---- on-disk formats: .cfrw v1 and .cffm v1 (host files; host arrays) ----
  * Byte-compatible with the reference writer (tools/build_index.cpp:413-438 and 496-526; exporter docstrings
