@@ -90,20 +90,41 @@ def bench_rrr(steps: int, warmup: int, cpu: bool = True) -> dict:
     idx.rank_into(dc, di, out)
     rank_gpu = to_u32(out)
 
-    wall_r, per_r = _events_time(lambda: idx.rank_into(dc, di, out), steps, warmup)
-    wall_a, per_a = _events_time(lambda: idx.access_into(dpos, out), steps, warmup)
-    t_rank = float(np.mean(per_r)) * 1e-3
-    t_acc = float(np.mean(per_a)) * 1e-3
-    bytes_rank = 960.0 * nq   # 15 levels x 2 rank1 x 32 B algorithmic (samples 12 + class scan 16 + offset 4)
-    bytes_acc = 480.0 * nq
+    # the derived line layout (built once at load): same results, timed beside the RRR kernels
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    idx.build_lines()
+    torch.cuda.synchronize()
+    t_lines = time.perf_counter() - t0
+    out_l = torch.empty_like(out)
+    idx.rank_lines_into(dc, di, out_l)
+    assert np.array_equal(to_u32(out_l), rank_gpu), "line-layout rank != RRR rank"
+    idx.access_lines_into(dpos, out_l)
+    assert np.array_equal(to_u32(out_l), tok[pos]), "line-layout access mismatch"
+
+    wall_r, per_r = _events_time(lambda: idx.rank_lines_into(dc, di, out_l), steps, warmup)
+    _, per_a = _events_time(lambda: idx.access_lines_into(dpos, out_l), steps, warmup)
+    _, per_rr = _events_time(lambda: idx.rank_into(dc, di, out), steps, warmup)
+    _, per_ra = _events_time(lambda: idx.access_into(dpos, out), steps, warmup)
+    t_rank, t_acc, t_rrank, t_racc = (float(np.mean(x)) * 1e-3 for x in (per_r, per_a, per_rr, per_ra))
+    # algorithmic bytes: line layout = 15 levels x one 64-B record per query (rank and access alike) + the query
+    # words + the result; RRR = 15 levels x 32 B per rank1 (samples 12 + class scan 16 + offset 4), 2 rank1 per level
+    # for rank (960 B), 1 for access (480 B)
+    bytes_rank = nq * (15 * 64 + 12.0)
+    bytes_acc = nq * (15 * 64 + 8.0)
     res = {
         "rank_mqs": nq / t_rank / 1e6, "access_mqs": nq / t_acc / 1e6,
         "rank_ms": t_rank * 1e3, "access_ms": t_acc * 1e3,
         "rank_wall_ms_per_step": wall_r / steps,
-        "rank_roofline": {"bound": "hbm", "achieved": bytes_rank / t_rank / 1e9, "peak": HBM_PEAK_GBS,
-                          "unit": "GB/s", "frac": bytes_rank / t_rank / 1e9 / HBM_PEAK_GBS, "traffic": None},
+        "rank_roofline": {"bound": "hbm (nominal; the index is L2-resident)", "achieved": bytes_rank / t_rank / 1e9,
+                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": bytes_rank / t_rank / 1e9 / HBM_PEAK_GBS,
+                          "traffic": None},
         "access_gbs": bytes_acc / t_acc / 1e9,
+        "rrr_rank_mqs": nq / t_rrank / 1e6, "rrr_access_mqs": nq / t_racc / 1e6,
+        "rrr_rank_ms": t_rrank * 1e3, "rrr_access_ms": t_racc * 1e3,
+        "rrr_rank_gbs": 960.0 * nq / t_rrank / 1e9,
         "index_bytes": idx.device_bytes(), "bits_per_token": idx.device_bytes() * 8.0 / n,
+        "lines_bytes": idx.lines.numel(), "lines_build_ms": t_lines * 1e3,
         "gpu_index_build_ms": t_build * 1e3,
     }
     if cpu:

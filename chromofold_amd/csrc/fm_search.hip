@@ -12,6 +12,7 @@
 #include "cf_device.hpp"
 #include "packed_core.hpp"
 #include "rrr_core.hpp"
+#include "lines_core.hpp"
 
 namespace {
 
@@ -228,120 +229,10 @@ __global__ __launch_bounds__(kStagedThreads) void fm_locate_staged_kernel(cf_fm_
     }                                                                                                         \
   } while (0)
 
-// ---- the line layout (chromofold_index.h, cf_fm_lines_*), derived on the device from the RRR levels:
-//   * level l's bitvector as records of 16 u32: word 0 = ones in bits [0, 480 r) of the level, words 1..15 = bits
-//     [480 r, 480 r + 480) LSB-first (32 RRR blocks). A rank1 reads one 64-byte line; on the RRR level it reads
-//     three or four (samples, class words, offset bits) plus the unrank table;
-//   * a per-symbol table lfb[c] = C[c] - e(c), e(c) = where the rank walk of c from position 0 ends on the last
-//     level. The walk of rank(c, i) maps its start-of-c chain p and its position chain a by the same rule and p
-//     never depends on i, so rank(c, i) = a_L - e(c) and LF(i) = C[c] + rank(c, i) = a_L + lfb[c].
-// Backward search then takes 2 rank1 per level (lo and hi) and the LF step of locate 1 (the access walk of i is the
-// rank walk of i for c = BWT[i]); every result equals the RRR kernels' above.
-
-constexpr uint32_t kLineBits = 480;  // payload bits of a 64-byte record (word 0 is the rank before it)
-__host__ __device__ inline uint32_t lines_nrec(int n) { return static_cast<uint32_t>(n) / kLineBits + 1u; }
-
-// Records of the line layout: one wavefront per pair of records (2 sb, 2 sb + 1) of a level = RRR superblock sb
-// (64 blocks x 15 bits = 960 bits). Lane i decodes block 64 sb + i (class nibble, offset at the superblock's offset
-// sample + the wave's exclusive prefix sum of the widths, table unrank) and ORs its 15 bits into the record payload
-// in LDS. Word 0 of record 2 sb is the superblock's rank sample; of record 2 sb + 1 that + the ones of blocks 0..31.
-// Pairs past the last superblock (the record at bit n when n is a multiple of 960) hold the level's total ones.
-constexpr unsigned kLinesBuildThreads = 256;
-__global__ __launch_bounds__(kLinesBuildThreads) void fm_lines_build_kernel(cf_fm_view v, uint32_t *__restrict__ lines,
-                                                                            uint32_t nrec, uint32_t npairs) {
-  __shared__ uint32_t s_pay[kLinesBuildThreads / 64][2][16];
-  const cf_rrrw_view &w = v.w;
-  const uint32_t wv = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-  const uint32_t gw = blockIdx.x * (kLinesBuildThreads / 64) + wv;
-  const uint32_t lvl = gw / npairs, sb = gw - lvl * npairs;
-  const bool live = lvl < static_cast<uint32_t>(w.bits);
-  if (lane < 32u) s_pay[wv][lane >> 4][lane & 15u] = 0u;
-  __syncthreads();
-  const uint32_t nblocks = (static_cast<uint32_t>(v.n) + cfd::kRrrT - 1) / cfd::kRrrT;
-  const uint32_t blk = sb * 64u + lane;
-  const bool inside = live && sb < static_cast<uint32_t>(w.nsb) && blk < nblocks;
-  uint32_t k = 0;
-  if (inside) k = (w.classes[static_cast<size_t>(lvl) * w.cwords + (blk >> 3)] >> (4u * (blk & 7u))) & 15u;
-  const int wd = cfd::width_of(static_cast<int>(k));
-  int pre = wd;  // inclusive prefix sum of the widths over the wave
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int o = __shfl_up(pre, d);
-    if (lane >= static_cast<uint32_t>(d)) pre += o;
-  }
-  int ones = static_cast<int>(k);  // ones of blocks 0..31 of the superblock (lanes 0..31)
-#pragma unroll
-  for (int d = 1; d < 32; d <<= 1) ones += __shfl_xor(ones, d);
-  ones = __shfl(ones, 0);
-  uint32_t rank0 = 0;
-  if (live) {
-    if (sb < static_cast<uint32_t>(w.nsb)) {
-      const size_t srow = static_cast<size_t>(lvl) * (w.nsb + 1) + sb, arow = static_cast<size_t>(lvl) * w.na + (sb >> 5);
-      rank0 = static_cast<uint32_t>(w.rank_a[arow] + w.rank_d[srow]);
-      if (inside && wd > 0) {
-        const int64_t at = static_cast<int64_t>(w.offbase[lvl]) + w.off_a[arow] + w.off_d[srow] + (pre - wd);
-        k = cfr::kTab.unrank[cfr::kTab.base[k] + cfr::read_bits(w.offsets, at, wd)];
-      } else if (inside) {
-        k = cfr::kTab.unrank[cfr::kTab.base[k]];
-      }
-    } else {
-      rank0 = static_cast<uint32_t>(v.n - w.zeros[lvl]);
-    }
-  }
-  if (inside) {  // k = the block's 15 bits now
-    const uint32_t bit = 15u * (lane & 31u);
-    uint32_t *pay = s_pay[wv][lane >> 5] + 1;
-    atomicOr(pay + (bit >> 5), k << (bit & 31u));
-    if ((bit & 31u) > 17u) atomicOr(pay + (bit >> 5) + 1, k >> (32u - (bit & 31u)));
-  }
-  __syncthreads();
-  const uint32_t r = lane >> 4, j = lane & 15u, rec = 2u * sb + r;
-  if (live && lane < 32u && rec < nrec) {
-    const uint32_t word = j == 0 ? rank0 + (r ? static_cast<uint32_t>(ones) : 0u) : s_pay[wv][r][j];
-    lines[(static_cast<size_t>(lvl) * nrec + rec) * 16u + j] = word;
-  }
-}
-
-// lfb[c] = C[c] - e(c), one thread per symbol (the start-of-c chain on the RRR levels).
-template <int LEVELS>
-__global__ __launch_bounds__(kThreads) void fm_lines_lfb_kernel(cf_fm_view v, int32_t *__restrict__ lfb) {
-  const int c = blockIdx.x * static_cast<int>(kThreads) + static_cast<int>(threadIdx.x);
-  if (c >= v.sigma) return;
-  const int L = LEVELS > 0 ? LEVELS : v.w.bits;
-  int p = 0;
-  for (int lvl = 0; lvl < L; ++lvl) {
-    const int rp = cfr::rank1_lvl<false>(v.w, lvl, p, nullptr);
-    p = (c >> (L - 1 - lvl)) & 1 ? v.w.zeros[lvl] + rp : p - rp;
-  }
-  lfb[c] = v.C[c] - p;
-}
-
-// One line record into registers (four 16-byte loads).
-__device__ __forceinline__ void load_record(const uint32_t *__restrict__ rec, uint32_t (&w)[16]) {
-  const uint4 *q = reinterpret_cast<const uint4 *>(rec);
-  const uint4 a = q[0], b = q[1], c = q[2], d = q[3];
-  w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
-  w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
-  w[8] = c.x; w[9] = c.y; w[10] = c.z; w[11] = c.w;
-  w[12] = d.x; w[13] = d.y; w[14] = d.z; w[15] = d.w;
-}
-
-// Ones of the level before bit `off` of the record (word 0 + the payload's bits [0, off)); with kBit the bit at off.
-template <bool kBit>
-__device__ __forceinline__ int record_rank(const uint32_t (&w)[16], uint32_t off, int *bit) {
-  const uint32_t full = off >> 5, sh = off & 31u;
-  int r = static_cast<int>(w[0]);
-  uint32_t tw = 0;
-#pragma unroll
-  for (uint32_t i = 0; i < 15; ++i) {
-    const uint32_t x = w[1 + i];
-    if (kBit && i == full) tw = x;
-    r += __popc(i < full ? x : (i == full ? x & ((1u << sh) - 1u) : 0u));
-  }
-  if constexpr (kBit) *bit = static_cast<int>((tw >> sh) & 1u);
-  return r;
-}
-
+// ---- the line layout (lines_core.hpp, chromofold_index.h cf_fm_lines_*): with base[c] = C[c] - e(c) an LF step is
+// LF(i) = a_L(i) + base[c], so backward search takes 2 rank1 per level (lo and hi) and the LF step of locate 1 (the
+// access walk of i is the rank walk of i for c = BWT[i]), one 64-byte record each; every result equals the RRR
+// kernels' above.
 struct LinesArgs {
   const uint32_t *rec;   // level records, [bits][nrec][16]
   const int32_t *lfb;    // [sigma]
@@ -349,8 +240,9 @@ struct LinesArgs {
 };
 
 __host__ inline LinesArgs lines_args(const cf_fm_view &v, const uint32_t *lines) {
-  const uint32_t nrec = lines_nrec(v.n);
-  return {lines, reinterpret_cast<const int32_t *>(lines + static_cast<size_t>(v.w.bits) * nrec * 16u), nrec};
+  const uint32_t nrec = cfl::nrec_for(static_cast<uint64_t>(v.n));
+  return {lines, reinterpret_cast<const int32_t *>(lines + static_cast<size_t>(v.w.bits) * nrec * cfl::kRecWords),
+          nrec};
 }
 
 // One backward-search step on the line layout: [lo, hi) -> [lfb[c] + a_L, lfb[c] + b_L). When a and b fall in
@@ -360,13 +252,8 @@ __device__ __forceinline__ void lines_step(const cf_fm_view &v, const LinesArgs 
   const int L = LEVELS > 0 ? LEVELS : v.w.bits;
   uint32_t a = static_cast<uint32_t>(lo), b = static_cast<uint32_t>(hi);
   for (int lvl = 0; lvl < L; ++lvl) {
-    const uint32_t *lv = la.rec + static_cast<size_t>(lvl) * la.nrec * 16u;
-    const uint32_t ra_rec = a / kLineBits, rb_rec = b / kLineBits;
-    uint32_t wa[16], wb[16];
-    load_record(lv + ra_rec * 16u, wa);
-    load_record(lv + rb_rec * 16u, wb);
-    const int ra = record_rank<false>(wa, a - ra_rec * kLineBits, nullptr);
-    const int rb = record_rank<false>(wb, b - rb_rec * kLineBits, nullptr);
+    const int ra = cfl::rank1<false>(la.rec, la.nrec, lvl, a, nullptr);
+    const int rb = cfl::rank1<false>(la.rec, la.nrec, lvl, b, nullptr);
     if ((c >> (L - 1 - lvl)) & 1) {
       const uint32_t z = static_cast<uint32_t>(v.w.zeros[lvl]);
       a = z + ra;
@@ -458,11 +345,8 @@ __global__ __launch_bounds__(kThreads) void fm_locate_lines_kernel(cf_fm_view v,
         uint32_t a = static_cast<uint32_t>(p);
         int c = 0;
         for (int lvl = 0; lvl < L; ++lvl) {
-          const uint32_t rec = a / kLineBits;
-          uint32_t w[16];
-          load_record(la.rec + (static_cast<size_t>(lvl) * la.nrec + rec) * 16u, w);
           int bit;
-          const int r = record_rank<true>(w, a - rec * kLineBits, &bit);
+          const int r = cfl::rank1<true>(la.rec, la.nrec, lvl, a, &bit);
           c = (c << 1) | bit;
           a = bit ? static_cast<uint32_t>(v.w.zeros[lvl] + r) : a - static_cast<uint32_t>(r);
         }
@@ -536,7 +420,8 @@ extern "C" cf_status cf_fm_locate_async(cf_fm_view v, const int32_t *r_in, int32
 // ---- line layout entry points (chromofold_index.h) ----
 extern "C" uint64_t cf_fm_lines_bytes(cf_fm_view v) {
   if (v.w.bits <= 0 || v.w.bits > 31 || v.n <= 0 || v.sigma <= 0) return 0;
-  return (static_cast<uint64_t>(v.w.bits) * lines_nrec(v.n) * 16u + static_cast<uint64_t>(v.sigma)) * 4u;
+  return (static_cast<uint64_t>(v.w.bits) * cfl::nrec_for(static_cast<uint64_t>(v.n)) * cfl::kRecWords +
+          static_cast<uint64_t>(v.sigma)) * 4u;
 }
 
 // The view fields the line-layout kernels read, and a 16-byte aligned `lines` (records are read as uint4).
@@ -550,18 +435,9 @@ extern "C" cf_status cf_fm_lines_build_async(cf_fm_view v, uint32_t *lines, uint
       !v.w.offbase)
     return CF_ERR_INVALID_ARGUMENT;
   if (bytes < cf_fm_lines_bytes(v)) return CF_ERR_INVALID_ARGUMENT;
-  const hipStream_t s = cfd::as_stream(stream);
-  const uint32_t nrec = lines_nrec(v.n), npairs = (nrec + 1) / 2;
-  const uint64_t waves = static_cast<uint64_t>(v.w.bits) * npairs;
-  const uint64_t blocks = (waves + kLinesBuildThreads / 64 - 1) / (kLinesBuildThreads / 64);
-  if (blocks > 0x7fffffffu) return CF_ERR_INVALID_ARGUMENT;
-  fm_lines_build_kernel<<<static_cast<unsigned>(blocks), kLinesBuildThreads, 0, s>>>(v, lines, nrec, npairs);
-  int32_t *lfb = reinterpret_cast<int32_t *>(lines + static_cast<size_t>(v.w.bits) * nrec * 16u);
-  const unsigned g = cfd::grid_for(static_cast<size_t>(v.sigma), kThreads);
-#define CF_LAUNCH(L) fm_lines_lfb_kernel<L><<<g, kThreads, 0, s>>>(v, lfb)
-  CF_FM_DISPATCH(CF_LAUNCH)
-#undef CF_LAUNCH
-  return cfd::launch_status();
+  const uint32_t nblocks = static_cast<uint32_t>((static_cast<int64_t>(v.n) + cfd::kRrrT - 1) / cfd::kRrrT);
+  return cfl::build(v.w, lines, cfl::nrec_for(static_cast<uint64_t>(v.n)), nblocks, v.n, v.sigma, v.C,
+                    cfd::as_stream(stream));
 }
 
 static unsigned lines_grid(size_t count) {

@@ -16,6 +16,8 @@
 #include "chromofold/chromofold_search.h"
 #include "cf_device.hpp"
 #include "rrr_core.hpp"
+#include "lines_core.hpp"
+#include "chromofold/chromofold_index.h"
 
 namespace {
 
@@ -67,7 +69,98 @@ __global__ __launch_bounds__(kLdsThreads) void rrrw_rank_lds_kernel(cf_rrrw_view
                                                                      static_cast<int>(pos[q]));
 }
 
+// ---- the line layout (lines_core.hpp, chromofold_index.h cf_rrrw_lines_*): access walks one record per level;
+// rank(c, i) = a_L(i) + base[c] with base[c] = -e(c), one record per level instead of the RRR walk's two rank1.
+// One lane per query; results equal the kernels above for every position in [0, n].
+template <int LEVELS>
+__global__ __launch_bounds__(kThreads) void rrrw_access_lines_kernel(cf_rrrw_view v, const uint32_t *__restrict__ lines,
+                                                                     uint32_t nrec, const uint32_t *__restrict__ pos,
+                                                                     uint32_t *__restrict__ out, size_t count) {
+  const size_t t = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x;
+  if (t >= count) return;
+  const int L = LEVELS > 0 ? LEVELS : v.bits;
+  uint32_t a = pos[t], val = 0;
+  for (int lvl = 0; lvl < L; ++lvl) {
+    int bit;
+    const int r = cfl::rank1<true>(lines, nrec, lvl, a, &bit);
+    val = (val << 1) | static_cast<uint32_t>(bit);
+    a = bit ? static_cast<uint32_t>(v.zeros[lvl] + r) : a - static_cast<uint32_t>(r);
+  }
+  out[t] = val;
+}
+
+template <int LEVELS>
+__global__ __launch_bounds__(kThreads) void rrrw_rank_lines_kernel(cf_rrrw_view v, const uint32_t *__restrict__ lines,
+                                                                   uint32_t nrec, const uint32_t *__restrict__ sym,
+                                                                   const uint32_t *__restrict__ pos,
+                                                                   uint32_t *__restrict__ out, size_t count) {
+  const size_t t = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x;
+  if (t >= count) return;
+  const int L = LEVELS > 0 ? LEVELS : v.bits;
+  const uint32_t c = sym[t] & ((1u << L) - 1u);  // the RRR walk reads the symbol's low L bits only
+  uint32_t a = pos[t];
+  for (int lvl = 0; lvl < L; ++lvl) {
+    const int r = cfl::rank1<false>(lines, nrec, lvl, a, nullptr);
+    a = (c >> (L - 1 - lvl)) & 1u ? static_cast<uint32_t>(v.zeros[lvl] + r) : a - static_cast<uint32_t>(r);
+  }
+  const int32_t *base = reinterpret_cast<const int32_t *>(lines + static_cast<size_t>(L) * nrec * cfl::kRecWords);
+  out[t] = a + static_cast<uint32_t>(base[c]);
+}
+
 }  // namespace
+
+// Records per level of the wavelet line layout: positions up to 960 * nsb resolve (n <= 960 * nsb).
+static uint32_t rrrw_nrec(const cf_rrrw_view &v) { return 2u * static_cast<uint32_t>(v.nsb) + 1u; }
+constexpr int kLinesMaxBits = 24;  // the per-symbol table has 2^bits entries
+
+extern "C" uint64_t cf_rrrw_lines_bytes(cf_rrrw_view v) {
+  if (v.bits <= 0 || v.bits > kLinesMaxBits || v.nsb < 0 || v.na <= (v.nsb >> 5)) return 0;
+  return (static_cast<uint64_t>(v.bits) * rrrw_nrec(v) * cfl::kRecWords + (uint64_t{1} << v.bits)) * 4u;
+}
+
+static bool rrrw_lines_ok(const cf_rrrw_view &v, const uint32_t *lines) {
+  return lines && (reinterpret_cast<uintptr_t>(lines) & 15u) == 0 && v.zeros && cf_rrrw_lines_bytes(v) != 0;
+}
+
+extern "C" cf_status cf_rrrw_lines_build_async(cf_rrrw_view v, uint32_t *lines, uint64_t bytes, void *stream) {
+  if (!rrrw_lines_ok(v, lines) || !v.classes || !v.offsets || !v.rank_a || !v.rank_d || !v.off_a || !v.off_d ||
+      !v.offbase || v.cwords < 0)
+    return CF_ERR_INVALID_ARGUMENT;
+  if (bytes < cf_rrrw_lines_bytes(v)) return CF_ERR_INVALID_ARGUMENT;
+  // blocks past the last real one have class nibble 0 in the zero-padded class words
+  return cfl::build(v, lines, rrrw_nrec(v), 8u * static_cast<uint32_t>(v.cwords), -1, int32_t{1} << v.bits,
+                    nullptr, cfd::as_stream(stream));
+}
+
+extern "C" cf_status cf_rrrw_access_lines_async(cf_rrrw_view v, const uint32_t *lines, const uint32_t *positions,
+                                                uint32_t *out, size_t count, void *stream) {
+  if (!rrrw_lines_ok(v, lines) || !positions || !out) return CF_ERR_INVALID_ARGUMENT;
+  if (count == 0) return CF_OK;
+  const hipStream_t s = cfd::as_stream(stream);
+  const unsigned g = cfd::grid_for(count, kThreads);
+  const uint32_t nrec = rrrw_nrec(v);
+  switch (v.bits) {
+    case 15: rrrw_access_lines_kernel<15><<<g, kThreads, 0, s>>>(v, lines, nrec, positions, out, count); break;
+    case 16: rrrw_access_lines_kernel<16><<<g, kThreads, 0, s>>>(v, lines, nrec, positions, out, count); break;
+    default: rrrw_access_lines_kernel<0><<<g, kThreads, 0, s>>>(v, lines, nrec, positions, out, count); break;
+  }
+  return cfd::launch_status();
+}
+
+extern "C" cf_status cf_rrrw_rank_lines_async(cf_rrrw_view v, const uint32_t *lines, const uint32_t *symbols,
+                                              const uint32_t *positions, uint32_t *out, size_t count, void *stream) {
+  if (!rrrw_lines_ok(v, lines) || !symbols || !positions || !out) return CF_ERR_INVALID_ARGUMENT;
+  if (count == 0) return CF_OK;
+  const hipStream_t s = cfd::as_stream(stream);
+  const unsigned g = cfd::grid_for(count, kThreads);
+  const uint32_t nrec = rrrw_nrec(v);
+  switch (v.bits) {
+    case 15: rrrw_rank_lines_kernel<15><<<g, kThreads, 0, s>>>(v, lines, nrec, symbols, positions, out, count); break;
+    case 16: rrrw_rank_lines_kernel<16><<<g, kThreads, 0, s>>>(v, lines, nrec, symbols, positions, out, count); break;
+    default: rrrw_rank_lines_kernel<0><<<g, kThreads, 0, s>>>(v, lines, nrec, symbols, positions, out, count); break;
+  }
+  return cfd::launch_status();
+}
 
 extern "C" cf_status cf_rrrw_access_async(cf_rrrw_view v, const uint32_t *positions, uint32_t *out, size_t count,
                                           void *stream) {

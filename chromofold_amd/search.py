@@ -51,6 +51,7 @@ class RrrWaveletIndex:
     nsb: int
     na: int
     tensors: dict
+    lines: "torch.Tensor | None" = None  # the derived line layout, built on first use (build_lines)
 
     @classmethod
     def from_host(cls, arrays, device="cuda") -> "RrrWaveletIndex":
@@ -87,6 +88,30 @@ class RrrWaveletIndex:
         out = torch.empty_like(positions, dtype=torch.int32)
         self.access_into(positions, out)
         return out
+
+    # ---- the derived line layout (cf_rrrw_lines_*): same results, one 64-byte line per level
+    def build_lines(self, stream=None) -> torch.Tensor:
+        """Builds (once) and returns the line layout of this matrix (a uint8 device tensor)."""
+        if self.lines is None:
+            v = self.view()
+            nb = int(A.lib().cf_rrrw_lines_bytes(v))
+            if nb == 0:
+                raise A.CfError(A.CF_ERR_UNSUPPORTED, "cf_rrrw_lines_bytes")
+            lines = torch.empty(nb, dtype=torch.uint8, device=self.tensors["classes"].device)
+            A.check(A.lib().cf_rrrw_lines_build_async(v, _ptr(lines), nb, stream_ptr(stream)),
+                    "cf_rrrw_lines_build_async")
+            self.lines = lines
+        return self.lines
+
+    def access_lines_into(self, positions: torch.Tensor, out: torch.Tensor, stream=None) -> None:
+        A.check(A.lib().cf_rrrw_access_lines_async(self.view(), _ptr(self.build_lines(stream)), _ptr(positions),
+                                                   _ptr(out), positions.numel(), stream_ptr(stream)),
+                "cf_rrrw_access_lines_async")
+
+    def rank_lines_into(self, symbols: torch.Tensor, positions: torch.Tensor, out: torch.Tensor, stream=None) -> None:
+        A.check(A.lib().cf_rrrw_rank_lines_async(self.view(), _ptr(self.build_lines(stream)), _ptr(symbols),
+                                                 _ptr(positions), _ptr(out), positions.numel(), stream_ptr(stream)),
+                "cf_rrrw_rank_lines_async")
 
     def rank(self, symbols: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
         out = torch.empty_like(positions, dtype=torch.int32)
@@ -212,6 +237,10 @@ A.declare("cf_rrrw_build_workspace_bytes", A.U64, [A.U64, A.U32])
 A.declare("cf_rrrw_build", A.I32, [A.P, A.U64, A.U32, A.P, A.U64, C.POINTER(cf_rrrw_layout), A.P])
 A.declare("cf_rrrw_build_copy", A.I32, [A.P, C.POINTER(cf_rrrw_layout), C.POINTER(cf_rrrw_arrays), A.P])
 A.declare("cf_fm_build_workspace_bytes", A.U64, [A.I32, A.I32])
+A.declare("cf_rrrw_lines_bytes", A.U64, [A.cf_rrrw_view])
+A.declare("cf_rrrw_lines_build_async", A.I32, [A.cf_rrrw_view, A.P, A.U64, A.P])
+A.declare("cf_rrrw_access_lines_async", A.I32, [A.cf_rrrw_view, A.P, A.P, A.P, A.SZ, A.P])
+A.declare("cf_rrrw_rank_lines_async", A.I32, [A.cf_rrrw_view, A.P, A.P, A.P, A.P, A.SZ, A.P])
 A.declare("cf_fm_lines_bytes", A.U64, [A.cf_fm_view])
 A.declare("cf_fm_lines_build_async", A.I32, [A.cf_fm_view, A.P, A.U64, A.P])
 A.declare("cf_fm_count_lines_async", A.I32, [A.cf_fm_view, A.P, A.P, A.P, A.P, A.P, A.SZ, A.P])

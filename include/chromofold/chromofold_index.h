@@ -74,6 +74,24 @@ cf_status cf_fm_build_aux(const int32_t *s, const int32_t *sa, int32_t n, int32_
                           uint32_t *bwt, int32_t *C, uint32_t *mwords, int32_t *msb, int32_t *sval, int32_t *sval_count,
                           void *workspace, uint64_t workspace_bytes, void *stream);
 
+/* ---- derived on-device line layout of an RRR wavelet matrix (no counterpart in the reference; the .cfrw on disk
+ * and the cf_rrrw_view arrays are unchanged). Built once per loaded matrix from its view; access and rank over it
+ * return exactly what cf_rrrw_access_async / cf_rrrw_rank_async return for positions in [0, n] (positions past n
+ * give unspecified values, never an out-of-bounds read). One 64-byte line per level for access and for rank (the
+ * RRR rank walks two chains of three or four lines per level). Layout of `lines` (u32 words, 16-byte aligned):
+ *   [bits][nrec][16] records, nrec = 2 * nsb + 1: word 0 = ones of the level before bit 480 r, words 1..15 = level
+ *   bits [480 r, 480 r + 480) LSB-first;
+ *   then [2^bits] int32 base[c] = -(position where the wavelet rank walk of symbol c from 0 ends), so that
+ *   rank(c, i) = (end of the walk of i) + base[c].
+ * Size: (bits * nrec * 16 + 2^bits) * 4 bytes; supported for bits <= 24 (cf_rrrw_lines_bytes returns 0 otherwise,
+ * or when the view's anchors do not cover superblock nsb). */
+uint64_t cf_rrrw_lines_bytes(cf_rrrw_view v);
+cf_status cf_rrrw_lines_build_async(cf_rrrw_view v, uint32_t *lines, uint64_t bytes, void *stream);
+cf_status cf_rrrw_access_lines_async(cf_rrrw_view v, const uint32_t *lines, const uint32_t *positions, uint32_t *out,
+                                     size_t count, void *stream);
+cf_status cf_rrrw_rank_lines_async(cf_rrrw_view v, const uint32_t *lines, const uint32_t *symbols,
+                                   const uint32_t *positions, uint32_t *out, size_t count, void *stream);
+
 /* ---- derived on-device line layout for FM search (no counterpart in the reference; the .cffm on disk and the
  * cf_fm_view arrays are unchanged). Built once per loaded index from its cf_fm_view; the search entry points below
  * return exactly what cf_fm_count_async / cf_fm_ranges_async / cf_fm_locate_async return for the same view, with one

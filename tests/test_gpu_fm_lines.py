@@ -46,11 +46,14 @@ def _wm_levels(bwt: np.ndarray, bits: int) -> list[np.ndarray]:
     return levels
 
 
-def _expected_lines(bwt: np.ndarray, bits: int, C: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
-    n = bwt.size
-    nrec = n // LINE_BITS + 1
+def expected_lines(seq: np.ndarray, bits: int, X: np.ndarray, nrec: int | None = None):
+    """Records and per-symbol table of the line layout of the wavelet matrix of `seq`: (records [bits][nrec][16],
+    base[c] = X[c] - e(c) for c < X.size)."""
+    n = seq.size
+    nrec = n // LINE_BITS + 1 if nrec is None else nrec
+    assert nrec * LINE_BITS > n
     recs = np.zeros((bits, nrec, 16), np.uint32)
-    levels = _wm_levels(bwt, bits)
+    levels = _wm_levels(seq, bits)
     for lvl, b in enumerate(levels):
         padded = np.zeros(nrec * LINE_BITS, np.uint8)
         padded[:n] = b
@@ -58,7 +61,7 @@ def _expected_lines(bwt: np.ndarray, bits: int, C: np.ndarray) -> tuple[np.ndarr
         recs[lvl, :, 0] = np.concatenate([[0], np.cumsum(blk.sum(1, dtype=np.int64))[:-1]])
         recs[lvl, :, 1:] = np.packbits(blk.reshape(nrec, 15, 32), axis=2, bitorder="little").view("<u4")[..., 0]
     # end of each symbol's rank walk from position 0
-    sigma = C.size
+    sigma = X.size
     c = np.arange(sigma, dtype=np.int64)
     p = np.zeros(sigma, np.int64)
     for lvl, b in enumerate(levels):
@@ -66,20 +69,25 @@ def _expected_lines(bwt: np.ndarray, bits: int, C: np.ndarray) -> tuple[np.ndarr
         rp = pre[p]
         zeros = n - int(b.sum())
         p = np.where((c >> (bits - 1 - lvl)) & 1, zeros + rp, p - rp)
-    return recs, (C.astype(np.int64) - p).astype(np.int32)
+    return recs, (X.astype(np.int64) - p).astype(np.int32)
 
 
-def _check_layout(idx, bwt):
-    lines = idx.build_lines().cpu().numpy().view(np.uint32)
-    bits = idx.w.bits
-    recs, lfb = _expected_lines(bwt, bits, idx.tensors["C"].cpu().numpy())
+def check_layout(lines, bits, recs, base):
+    """The built layout (uint8 device tensor) against expected_lines' records and table, word for word."""
+    lines = lines.cpu().numpy().view(np.uint32)
     nw = recs.size
-    assert lines.size == nw + lfb.size
+    assert lines.size == nw + base.size
     got = lines[:nw].reshape(recs.shape)
     for lvl in range(bits):
         bad = np.nonzero((got[lvl] != recs[lvl]).any(1))[0]
         assert bad.size == 0, f"level {lvl}: {bad.size} records differ, first {bad[:5]}"
-    assert np.array_equal(lines[nw:].view(np.int32), lfb)
+    assert np.array_equal(lines[nw:].view(np.int32), base)
+
+
+def _check_layout(idx, bwt):
+    bits = idx.w.bits
+    recs, lfb = expected_lines(bwt, bits, idx.tensors["C"].cpu().numpy())
+    check_layout(idx.build_lines(), bits, recs, lfb)
 
 
 def _search_both(idx, pat, ps, pl, dev):

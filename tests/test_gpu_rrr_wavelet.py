@@ -2,6 +2,8 @@
 
 Mirrors the reference's own check (benchmarks/rrr_wavelet.cu:135-143: access and rank std::equal to the golden
 arrays) and adds closed-form ground truth at the C1 shape: access(i) == tokens[i], rank(c, i) == #{j < i: t_j = c}.
+The derived line layout (cf_rrrw_lines_*, chromofold_index.h) answers the same queries in every test and must equal
+the RRR entry points; its records are checked word for word against the textbook wavelet matrix of the tokens.
 Bit-exact throughout.
 """
 import numpy as np
@@ -26,6 +28,28 @@ def _index(arrays, dev):
     return RrrWaveletIndex.from_host(arrays, dev)
 
 
+def _lines_access(idx, pos):
+    from chromofold_amd.search import to_u32, u32_dev
+    dp = u32_dev(pos)
+    out = dp.clone()
+    idx.access_lines_into(dp, out)
+    return to_u32(out)
+
+
+def _lines_rank(idx, c, i):
+    from chromofold_amd.search import to_u32, u32_dev
+    dc, di = u32_dev(c), u32_dev(i)
+    out = di.clone()
+    idx.rank_lines_into(dc, di, out)
+    return to_u32(out)
+
+
+def _check_lines_layout(idx, tok, bits):
+    from test_gpu_fm_lines import check_layout, expected_lines
+    recs, base = expected_lines(np.asarray(tok), bits, np.zeros(1 << bits, np.int32), 2 * idx.nsb + 1)
+    check_layout(idx.build_lines(), bits, recs, base)
+
+
 def test_tiny_cfrw_fixture(dev):
     from chromofold_amd.search import to_u32, u32_dev
     d = F.load_cfrw()
@@ -36,7 +60,12 @@ def test_tiny_cfrw_fixture(dev):
     allpos = np.arange(d["n"], dtype=np.uint32)
     w = O.RrrwArrays(d["bits"], d["cwords"], d["nsb"], d["na"], d["classes"], d["offsets"], d["rank_a"],
                      d["rank_d"], d["off_a"], d["off_d"], d["offbase"], d["zeros"])
-    assert np.array_equal(to_u32(idx.access(u32_dev(allpos))), O.rrrw_access(w, allpos))
+    ref = O.rrrw_access(w, allpos)
+    assert np.array_equal(to_u32(idx.access(u32_dev(allpos))), ref)
+    _check_lines_layout(idx, ref, d["bits"])
+    assert np.array_equal(_lines_access(idx, allpos), ref)
+    assert np.array_equal(_lines_access(idx, d["pos"]), d["access_golden"])
+    assert np.array_equal(_lines_rank(idx, d["rank_c"], d["rank_i"]), d["rank_golden"])
 
 
 @pytest.mark.parametrize("n,bits,seed", [(1, 1, 1), (15, 3, 2), (16, 4, 3), (961, 5, 4), (4095, 9, 5),
@@ -54,6 +83,11 @@ def test_random_shapes_vs_closed_form(dev, n, bits, seed):
     i[:3] = [0, n, n // 2]  # edges: empty prefix, whole sequence
     got = to_u32(idx.rank(u32_dev(c), u32_dev(i)))
     assert np.array_equal(got, O.rrrw_rank(w, c, i))
+    _check_lines_layout(idx, tok, bits)
+    assert np.array_equal(_lines_access(idx, allpos), tok)
+    assert np.array_equal(_lines_rank(idx, c, i), got)
+    hi = c | np.uint32(1 << 31)  # bits above the levels are ignored, as by the RRR walk
+    assert np.array_equal(_lines_rank(idx, hi, i), to_u32(idx.rank(u32_dev(hi), u32_dev(i))))
 
 
 def test_c1_shape_zipf_closed_form(dev):
@@ -76,4 +110,7 @@ def test_c1_shape_zipf_closed_form(dev):
         lo, hi = np.searchsorted(sorted_tok, c[t], "left"), np.searchsorted(sorted_tok, c[t], "right")
         assert gr[t] == np.count_nonzero(order[lo:hi] < i[t]), t
     assert np.array_equal(gr, O.rrrw_rank(w, c, i))
+    assert np.array_equal(_lines_access(idx, pos), got)
+    assert np.array_equal(_lines_rank(idx, c, i), gr)
+    _check_lines_layout(idx, tok, 15)
     torch.cuda.synchronize()
