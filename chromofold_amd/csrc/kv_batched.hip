@@ -357,13 +357,34 @@ __device__ __forceinline__ uint32_t next_group_strided(uint32_t g, uint32_t gb) 
 constexpr uint32_t kSlotWeight[3] = {139, 124, 100};
 constexpr uint32_t kSlotWeightSum = 4 * (kSlotWeight[0] + kSlotWeight[1] + kSlotWeight[2]);
 
-// Pairs [lo, hi) of `np` that wavefront w of a wide workgroup takes.
+// Pairs [lo, hi) of `np` that wavefront w of a wide workgroup takes: counts c_w that minimise the latest finish
+// max_w c_w / rate_w (rate = kSlotWeight of w's age slot), in wavefront order. Every wavefront first takes
+// floor(np * rate / sum of rates); the remaining d < 12 pairs go one each to the d wavefronts that would finish
+// their extra pair earliest ((c_w + 1) / rate_w, ties to the lower index). With few pairs per wavefront (short
+// contexts) this keeps the slowest age slot from being the one that rounds up.
 __device__ __forceinline__ void wide_block(uint32_t w, uint32_t np, uint32_t &lo, uint32_t &hi) {
-  const uint32_t slot = w >> 2, sub = w & 3;
-  const uint32_t mine = kSlotWeight[slot < 3 ? slot : 2];
-  const uint32_t before = (slot > 0 ? 4 * kSlotWeight[0] : 0) + (slot > 1 ? 4 * kSlotWeight[1] : 0) + sub * mine;
-  lo = static_cast<uint32_t>((static_cast<uint64_t>(np) * before) / kSlotWeightSum);
-  hi = static_cast<uint32_t>((static_cast<uint64_t>(np) * (before + mine)) / kSlotWeightSum);
+  auto rate = [](uint32_t v) { return kSlotWeight[(v >> 2) < 3 ? (v >> 2) : 2]; };
+  auto base = [&](uint32_t v) {
+    return static_cast<uint32_t>((static_cast<uint64_t>(np) * rate(v)) / kSlotWeightSum);
+  };
+  uint32_t given = 0;
+  for (uint32_t v = 0; v < kWavesWide; ++v) given += base(v);
+  const uint32_t d = np - given;  // < kWavesWide
+  // wavefront v gets an extra pair iff fewer than d wavefronts precede it in the order (c + 1) / rate, index
+  auto extra = [&](uint32_t v) {
+    const uint64_t kv = static_cast<uint64_t>(base(v) + 1);
+    uint32_t ahead = 0;
+    for (uint32_t u = 0; u < kWavesWide; ++u) {
+      const uint64_t ku = static_cast<uint64_t>(base(u) + 1);
+      // (ku / rate(u) < kv / rate(v)) or equal with u < v
+      const uint64_t l = ku * rate(v), r = kv * rate(u);
+      ahead += (l < r || (l == r && u < v)) ? 1u : 0u;
+    }
+    return ahead < d ? 1u : 0u;
+  };
+  lo = 0;
+  for (uint32_t v = 0; v < w; ++v) lo += base(v) + extra(v);
+  hi = lo + base(w) + extra(w);
 }
 
 template <int D, int CODEC, int W>
