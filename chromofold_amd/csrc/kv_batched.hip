@@ -38,6 +38,7 @@
 #include "cf_device.hpp"
 #include "chromofold/kv_codec_ext.h"
 #include "kv_group_decode.hpp"
+#include "kv_seam_route.hpp"
 
 namespace {
 
@@ -126,14 +127,18 @@ constexpr int buf_u32() {
 // V quads 0..KL-1 do not wait for the V phase in registers: the decode parks them in the wave's LDS area `vl`
 // ([KL][64] words) (RANS), or the V phase loads them again from `raw` (INT8 groups, rare in the launches that use
 // KL > 0). The registers this frees keep the 12-wave kernel free of spills.
-template <int D, int CODEC, int KL, typename WordPtr, typename Hook>
+// With kEnds (RANS groups), `ends` receives where the K and V word cursors stopped (words from the K stream's start),
+// so that a caller can check that a self-contained group consumed exactly its words. With kPageVis, `page_vis`
+// tells whether any token of the lane's 16-token page is visible (for callers whose visible tokens are not a prefix
+// of each page, e.g. behind a causal window); otherwise tok_ok of the page's first lane says it.
+template <int D, int CODEC, int KL, typename WordPtr, typename Hook, bool kEnds = false, bool kPageVis = false>
 __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&pre)[14], const uint32_t *nlw,
                                            uint32_t (&st)[2], const uint32_t *__restrict__ raw, WordPtr wk,
                                            uint32_t cnt_kv, const uint2 (*__restrict__ s_tab)[kSlots],
                                            const half4_t *qhi, const half4_t *qlo, const float *qsum,
                                            _Float16 (*s_pw)[4][kGqa][16], uint32_t *__restrict__ vl, int lane,
                                            bool tok_ok, float ks, float vs, int &e_run, float *m_run, float *l_run,
-                                           float4_t *acc_v) {
+                                           float4_t *acc_v, uint32_t *ends = nullptr, bool page_vis = false) {
   constexpr int NQ = D / 4, RAW = raw_words<D>();
   constexpr bool RANS = CODEC == CF_KV_CODEC_RANS_HYBRID;
   const int G = lane >> 4, t = lane & 15;
@@ -215,6 +220,10 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
     }(std::make_integer_sequence<int, D / 8>{});
     st[0] = xk;
     st[1] = xv;
+    if constexpr (kEnds) {
+      ends[0] = static_cast<uint32_t>(wkk - wk);
+      ends[1] = static_cast<uint32_t>(wvv - wk);
+    }
   } else {
     if (nlw) {  // a raw group: start the next RANS group's first raw words now
 #pragma unroll
@@ -257,7 +266,7 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
   constexpr int kOpExp = RANS ? 24 : 0;
   constexpr int kNone = -(1 << 24);
   // tokens are visible as a prefix of each page, so a page's lane 16 G is visible iff any of its tokens is
-  const int ep = tok_ok ? __builtin_amdgcn_frexp_expf(vs) - 15 + kOpExp : kNone;
+  const int ep = (kPageVis ? page_vis : tok_ok) ? __builtin_amdgcn_frexp_expf(vs) - 15 + kOpExp : kNone;
   const int eb = max(max(__builtin_amdgcn_readlane(ep, 0), __builtin_amdgcn_readlane(ep, 16)),
                      max(__builtin_amdgcn_readlane(ep, 32), __builtin_amdgcn_readlane(ep, 48)));
   const int nb = eb != kNone ? max(eb, e_run - 60) : e_run;
@@ -932,6 +941,289 @@ __global__ __launch_bounds__(kGqa * D) void kv_merge_kernel(cf_kv_batched_desc d
       nan ? __builtin_nanf("") : l == 0.0f ? 0.0f : o / l;
 }
 
+// ---- decode-shape route of the reference seam (kv_seam_route.hpp)
+
+constexpr unsigned kListThreads = 1024;
+
+// One workgroup per KV head: the head's pages in descriptor order (lists[head][0 .. counts[head])) and whether the
+// route takes the head (taken[head]): every page of the head a rANS page of the call's head_dim with 1..64 tokens,
+// all with the same K and V table pointers (compared as the minimum and maximum of each pointer's two halves).
+__global__ __launch_bounds__(kListThreads) void seam_list_kernel(cf_kv_paged_attention_desc d,
+                                                                 uint32_t *__restrict__ lists,
+                                                                 uint32_t *__restrict__ counts,
+                                                                 uint32_t *__restrict__ taken) {
+  __shared__ uint32_t s_wc[kListThreads / 64];
+  __shared__ uint32_t s_base, s_bad;
+  __shared__ uint32_t s_lo[4], s_hi[4];  // min / max of k_lut and v_lut, low and high words
+  const uint32_t head = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  if (t < 4) {
+    s_lo[t] = 0xFFFFFFFFu;
+    s_hi[t] = 0u;
+  }
+  if (t == 0) {
+    s_base = 0;
+    s_bad = 0;
+  }
+  __syncthreads();
+  uint32_t *list = lists + static_cast<size_t>(head) * d.page_count;
+  for (uint32_t c0 = 0; c0 < d.page_count; c0 += kListThreads) {
+    const uint32_t p = c0 + t;
+    bool match = false;
+    if (p < d.page_count) {
+      const cf_kv_device_page &pg = d.pages[p];
+      match = pg.kv_head == head;
+      if (match) {
+        const bool rans = pg.fixed_code_length == 0 && pg.k_max_code_length == 0;
+        if (!rans || pg.head_dim != d.head_dim || pg.token_count == 0 || pg.token_count > 64 || !pg.k_words ||
+            !pg.k_lut || !pg.v_lut)
+          s_bad = 1u;  // every writer stores the same value
+        const uint64_t k = reinterpret_cast<uintptr_t>(pg.k_lut), v = reinterpret_cast<uintptr_t>(pg.v_lut);
+        const uint32_t w[4] = {static_cast<uint32_t>(k), static_cast<uint32_t>(k >> 32), static_cast<uint32_t>(v),
+                               static_cast<uint32_t>(v >> 32)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          atomicMin(&s_lo[i], w[i]);
+          atomicMax(&s_hi[i], w[i]);
+        }
+      }
+    }
+    const uint64_t m = __builtin_amdgcn_ballot_w64(match);
+    if (lane == 0) s_wc[wave] = static_cast<uint32_t>(__builtin_popcountll(m));
+    __syncthreads();
+    uint32_t at = s_base;
+    for (uint32_t w = 0; w < wave; ++w) at += s_wc[w];
+    if (match)
+      list[at + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                          __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u))] = p;
+    __syncthreads();  // every thread has read s_base and s_wc
+    if (t == 0) {
+      uint32_t nn = 0;
+      for (uint32_t w = 0; w < kListThreads / 64; ++w) nn += s_wc[w];
+      s_base += nn;
+    }
+    __syncthreads();
+  }
+  if (t == 0) {
+    bool same = true;
+    for (int i = 0; i < 4; ++i) same &= s_base == 0 || s_lo[i] == s_hi[i];
+    counts[head] = s_base;
+    taken[head] = (s_bad == 0 && same) ? 1u : 0u;
+  }
+}
+
+// One (context split, KV head) per 4-wavefront workgroup for the heads seam_list_kernel took: wavefront w decodes the
+// head's listed pages of ordinals split + splits * (w + 4 k), each page one self-contained group (RANS_HYBRID chain
+// start or INT8 fallback) run through group_body with the page's token positions, then the workgroup writes slot
+// `split` of the seam's partials ([slot][kv head][vector][head_dim + 2] = acc, m, l; m NaN when a page was
+// refused). Heads the route did not take, and splits without pages, get empty slots (m = -inf, l = 0).
+template <int D>
+__global__ CF_KV_OCC __launch_bounds__(64 * kWavesNarrow) void seam_group_kernel(cf_kv_paged_attention_desc d, uint32_t splits,
+                                                                       const uint32_t *__restrict__ lists,
+                                                                       const uint32_t *__restrict__ counts,
+                                                                       const uint32_t *__restrict__ taken,
+                                                                       float *__restrict__ partial) {
+  constexpr int W = kWavesNarrow, NQ = D / 4, RAW = raw_words<D>(), BUF = buf_u32<D>(), kThreads = 64 * W;
+  __shared__ uint2 s_tab[2][kSlots];
+  __shared__ __attribute__((aligned(16))) _Float16 s_p[W][2][4][kGqa][16];
+  __shared__ uint32_t s_buf[W][BUF];  // per wave: staged words; query staging and partials alias it
+  // (no other shared variable: with 53,760 bytes or less three workgroups fit a CU)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int G = lane >> 4, t = lane & 15;
+  const uint32_t split = blockIdx.x, head = blockIdx.y, gqa = d.gqa_group_size;
+  const uint32_t n = counts[head];
+  float *pp = partial + (static_cast<size_t>(split) * d.kv_head_count + head) * gqa * (D + 2);
+  if (!taken[head] || split >= n) {
+    for (uint32_t i = threadIdx.x; i < gqa * (D + 2); i += kThreads) pp[i] = i % (D + 2) == D ? -INFINITY : 0.0f;
+    return;
+  }
+  const uint32_t *list = lists + static_cast<size_t>(head) * d.page_count;
+  {  // the head's tables (every listed page has these), as the decoder reads them
+    const cf_kv_device_page &p0 = d.pages[list[0]];
+    const uint2 *tk = reinterpret_cast<const uint2 *>(p0.k_lut), *tv = reinterpret_cast<const uint2 *>(p0.v_lut);
+    for (uint32_t i = threadIdx.x; i < kSlots; i += kThreads) {
+      const uint2 a = tk[i], b = tv[i];
+      s_tab[0][i] = uint2{(a.x & 2047u) | (((a.x >> 11) & 2047u) << 16), a.y};
+      s_tab[1][i] = uint2{(b.x & 2047u) | (((b.x >> 11) & 2047u) << 16), b.y};
+    }
+  }
+  static_assert(2 * kGqa * D * 2 <= W * BUF * 4, "query staging must fit the word buffers");
+  _Float16(*s_q)[kGqa][D] = reinterpret_cast<_Float16(*)[kGqa][D]>(&s_buf[0][0]);
+  for (int i = threadIdx.x; i < kGqa * D; i += kThreads) {  // the call's one query row
+    const int h = i / D, dd = i % D;
+    const float q = static_cast<uint32_t>(h) < gqa ? d.queries[(static_cast<size_t>(head) * gqa + h) * D + dd] : 0.0f;
+    cfd::split_mul_f16(q, d.softmax_scale, s_q[0][h][dd], s_q[1][h][dd]);
+  }
+  __syncthreads();
+  constexpr int NC = NQ / 16 > 0 ? NQ / 16 : 1;
+  half4_t qhi[NC], qlo[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int qd = 16 * c + (lane >> 2);
+    qhi[c] = (4 * qd < D) ? *reinterpret_cast<const half4_t *>(&s_q[0][lane & 3][4 * qd]) : half4_t{0, 0, 0, 0};
+    qlo[c] = (4 * qd < D) ? *reinterpret_cast<const half4_t *>(&s_q[1][lane & 3][4 * qd]) : half4_t{0, 0, 0, 0};
+  }
+  float qsum[kGqa];
+  {
+    float part = 0.0f;
+    const int h = lane >> 4;
+#pragma unroll
+    for (int k = 0; k < D / 16; ++k) {
+      const int dd = (lane & 15) * (D / 16) + k;
+      part += static_cast<float>(s_q[0][h][dd]) + static_cast<float>(s_q[1][h][dd]);
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) part += __shfl_xor(part, o);
+#pragma unroll
+    for (int hh = 0; hh < kGqa; ++hh) qsum[hh] = __shfl(part, 16 * hh);
+  }
+  __syncthreads();  // s_q (aliasing the word buffers) is dead from here on
+
+  // the seam's visible range of the query row: [window begin, query token]
+  const uint32_t qtok = d.query_token_begin;
+  const uint32_t wlo = (d.causal_window == 0 || qtok + 1 <= d.causal_window) ? 0u : qtok + 1 - d.causal_window;
+  float m_run[kGqa], l_run[kGqa];
+  int e_run = -(1 << 20);
+  float4_t acc_v[D / 16];
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h) {
+    m_run[h] = -INFINITY;
+    l_run[h] = 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < D / 16; ++i) acc_v[i] = float4_t{0, 0, 0, 0};
+  uint32_t *buf = s_buf[__builtin_amdgcn_readfirstlane(wave)];
+  bool bad = false;
+  uint32_t pre[14];
+  auto noop = []() {};
+  for (uint32_t o = split + splits * static_cast<uint32_t>(wave); o < n; o += splits * W) {
+    const cf_kv_device_page &pg = d.pages[list[o]];
+    const uint32_t tb = pg.token_begin, tcnt = pg.token_count;
+    if (tb > qtok || tb + tcnt <= wlo) continue;  // wholly outside the visible range: skipped unread
+    const uint8_t *blob = reinterpret_cast<const uint8_t *>(pg.k_words);
+    const uint32_t codec = *reinterpret_cast<const uint32_t *>(blob);
+    const uint32_t cnt = *reinterpret_cast<const uint32_t *>(blob + 4);
+    const uint32_t chain = *reinterpret_cast<const uint16_t *>(blob + 8);
+    const uint32_t bd = *reinterpret_cast<const uint16_t *>(blob + 20);
+    const uint16_t *tch = reinterpret_cast<const uint16_t *>(blob + 12);
+    // a self-contained group of this head_dim whose token counts match the page: full 16-token pages, then at most
+    // one partial page, then empty ones (the seam's rule, kv_legacy.hip rans_stream_to_lds)
+    uint32_t total = 0;
+    bool valid = bd == static_cast<uint32_t>(D) &&
+                 (codec == CF_KV_CODEC_INT8 || (codec == CF_KV_CODEC_RANS_HYBRID && chain == 1));
+    bool open = true;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t c = tch[g];
+      valid &= c <= 16u && (c == 0 || open);
+      open &= c == 16u;
+      total += c;
+    }
+    const uint32_t nk = cnt & 0xFFFFu, nv = cnt >> 16;
+    valid &= total == tcnt && (codec != CF_KV_CODEC_RANS_HYBRID || nk + nv <= kCapWords);
+    if (!valid) {
+      bad = true;
+      continue;
+    }
+    const uint32_t tcG = tch[G];
+    const float ks = reinterpret_cast<const float *>(blob + 32)[G];
+    const float vs = reinterpret_cast<const float *>(blob + 48)[G];
+    const uint32_t pos = tb + 16u * static_cast<uint32_t>(G) + static_cast<uint32_t>(t);
+    const bool tok_ok = static_cast<uint32_t>(t) < tcG && pos >= wlo && pos <= qtok;
+    // any token of the lane's 16-token page visible (behind a window the visible tokens can be a page's suffix)
+    const uint32_t pg0 = tb + 16u * static_cast<uint32_t>(G);
+    const bool page_vis = tcG > 0 && pg0 <= qtok && pg0 + tcG - 1 >= wlo;
+    if (codec == CF_KV_CODEC_RANS_HYBRID) {
+      const uint32_t *hs = reinterpret_cast<const uint32_t *>(blob + kHdr);
+      uint32_t st[2] = {hs[lane], hs[64 + lane]};
+      const uint32_t *raw = reinterpret_cast<const uint32_t *>(blob + kHdr + kStateBytes);
+#pragma unroll
+      for (int w = 0; w < 7; ++w) {
+        pre[w] = raw[w * 64 + lane];
+        pre[7 + w] = raw[RAW + w * 64 + lane];
+      }
+      // the word streams into the wave's buffer (whole 16-byte chunks: blobs are padded to 16 bytes)
+      constexpr int kStage16 = ((kCapWords * 2) + 1023) / 1024;
+      const uint32_t nbytes = ((nk + nv) * 2u + 15u) & ~15u;
+      const uint8_t *src = reinterpret_cast<const uint8_t *>(raw + 2 * RAW) + 16u * lane;
+#pragma unroll
+      for (int k = 0; k < kStage16; ++k)
+        if (1024u * k + 16u * lane < nbytes)
+          __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t *>(src + 1024 * k),
+                                           (__attribute__((address_space(3))) void *)(buf + 256 * k), 16, 0, 0);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      uint32_t ends[2];
+      group_body<D, CF_KV_CODEC_RANS_HYBRID, 0, const uint16_t *, decltype(noop), true, true>(
+          noop, pre, nullptr, st, raw, reinterpret_cast<const uint16_t *>(buf), cnt, s_tab, qhi, qlo, qsum,
+          s_p[wave], nullptr, lane, tok_ok, ks, vs, e_run, m_run, l_run, acc_v, ends, page_vis);
+      // a group coded on its own ends where the encoder started (2^16 in every lane) and consumed exactly its words
+      const bool ok = st[0] == 65536u && st[1] == 65536u && ends[0] == nk && ends[1] == nk + nv;
+      bad |= __builtin_amdgcn_ballot_w64(!ok) != 0;
+    } else {
+      uint32_t st[2] = {0, 0};
+      group_body<D, CF_KV_CODEC_INT8, 0, const uint16_t *, decltype(noop), false, true>(
+          noop, pre, nullptr, st, reinterpret_cast<const uint32_t *>(blob + kHdr),
+          static_cast<const uint16_t *>(nullptr), 0, s_tab, qhi, qlo, qsum, s_p[wave], nullptr, lane, tok_ok, ks, vs,
+          e_run, m_run, l_run, acc_v, nullptr, page_vis);
+    }
+  }
+
+  // ---- reduce the wavefront (as kv_batched_kernel), then merge the wavefronts into the slot
+#pragma unroll
+  for (int i = 0; i < D / 16; ++i)
+#pragma unroll
+    for (int h = 0; h < kGqa; ++h) {
+      float v = G < 2 ? ldexpf(acc_v[i][h], e_run) : 0.0f;
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      acc_v[i][h] = v;
+    }
+#pragma unroll
+  for (int h = 0; h < kGqa; ++h)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) l_run[h] += __shfl_xor(l_run[h], o);
+  float *red = reinterpret_cast<float *>(buf);  // the wave's m is NaN when it refused a page
+  if (lane < 16) {
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i)
+#pragma unroll
+      for (int h = 0; h < kGqa; ++h) red[h * (D + 2) + t + 16 * i] = acc_v[i][h];
+  }
+  if (lane < kGqa) {
+    red[lane * (D + 2) + D] = bad ? __builtin_nanf("") : m_run[lane];
+    red[lane * (D + 2) + D + 1] = l_run[lane];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < kGqa * D; i += kThreads) {
+    const int h = i / D, dd = i % D;
+    if (static_cast<uint32_t>(h) >= gqa) continue;
+    float m = -INFINITY;
+    bool any_bad = false;
+    for (int w = 0; w < W; ++w) {
+      const float mw = reinterpret_cast<const float *>(s_buf[w])[h * (D + 2) + D];
+      any_bad |= mw != mw;
+      m = fmaxf(m, mw);  // fmaxf drops a NaN, hence the flag
+    }
+    float l = 0.0f, o = 0.0f;
+    if (m != -INFINITY)
+      for (int w = 0; w < W; ++w) {
+        const float *rw = reinterpret_cast<const float *>(s_buf[w]);
+        const float mw = rw[h * (D + 2) + D];
+        if (mw == -INFINITY || mw != mw) continue;
+        const float sc = __expf(mw - m);
+        l += rw[h * (D + 2) + D + 1] * sc;
+        o += rw[h * (D + 2) + dd] * sc;
+      }
+    pp[h * (D + 2) + dd] = o;
+    if (dd == 0) {
+      pp[h * (D + 2) + D] = any_bad ? __builtin_nanf("") : m;
+      pp[h * (D + 2) + D + 1] = l;
+    }
+  }
+}
+
 // CUs of the current device (cached per thread and device).
 uint32_t cu_count() {
   static thread_local int cached_dev = -1;
@@ -1142,3 +1434,40 @@ extern "C" cf_status cf_kv_paged_attention_batched_noalloc_async(const cf_kv_bat
   }
   return launch_batched_all(d, plan, static_cast<float *>(ws), stream);
 }
+
+// ---- the seam's decode-shape route, host side (kv_seam_route.hpp)
+namespace cfkv {
+
+bool seam_route_applies(const cf_kv_paged_attention_desc &d) {
+  return d.query_count == 1 && d.gqa_group_size >= 1 && d.gqa_group_size <= static_cast<uint32_t>(kGqa) &&
+         (d.head_dim == 64 || d.head_dim == 128) && d.active_token_count == 0 && d.page_count > 0 && d.pages &&
+         d.kv_head_count >= 1 && d.kv_head_count <= 65535;
+}
+
+uint32_t seam_route_splits(const cf_kv_paged_attention_desc &d) {
+  // about two pages per wavefront, within one round of workgroups (three per CU)
+  const uint32_t per_head = (d.page_count + d.kv_head_count - 1) / d.kv_head_count;
+  uint32_t s = std::max<uint32_t>(1, per_head / (2 * kWavesNarrow));
+  s = std::min<uint32_t>(s, std::max<uint32_t>(1, 3 * cu_count() / d.kv_head_count));
+  return std::min<uint32_t>(s, 64);
+}
+
+uint64_t seam_route_scratch_words(const cf_kv_paged_attention_desc &d) {
+  return static_cast<uint64_t>(d.kv_head_count) * d.page_count + 2ull * d.kv_head_count;
+}
+
+cf_status seam_route_launch(const cf_kv_paged_attention_desc &d, uint32_t splits, float *partial, uint32_t *scratch,
+                            hipStream_t s) {
+  uint32_t *lists = scratch;
+  uint32_t *counts = scratch + static_cast<uint64_t>(d.kv_head_count) * d.page_count;
+  uint32_t *taken = counts + d.kv_head_count;
+  seam_list_kernel<<<d.kv_head_count, kListThreads, 0, s>>>(d, lists, counts, taken);
+  const dim3 grid(splits, d.kv_head_count);
+  if (d.head_dim == 128)
+    seam_group_kernel<128><<<grid, 64 * kWavesNarrow, 0, s>>>(d, splits, lists, counts, taken, partial);
+  else
+    seam_group_kernel<64><<<grid, 64 * kWavesNarrow, 0, s>>>(d, splits, lists, counts, taken, partial);
+  return cfd::launch_status();
+}
+
+}  // namespace cfkv

@@ -44,6 +44,7 @@
 #include "chromofold/kv_codec_ext.h"
 #include "chromofold/kv_cuda.h"
 #include "kv_group_decode.hpp"
+#include "kv_seam_route.hpp"
 
 namespace {
 
@@ -210,11 +211,13 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Split s of the (vectors, KV head) unit writes slot s of `partial`: [split][kv head][vector][head_dim + 2] = acc,
-// m, l.
+// Split s of the (vectors, KV head) unit writes slot slot0 + s of `partial`: [slot][kv head][vector][head_dim + 2] =
+// acc, m, l; with no `partial` (one split) the workgroup writes the output itself. `route_taken` (the decode-shape
+// route's per-head flags, kv_seam_route.hpp, or NULL): a head the route took gets an empty slot here.
 template <int D>  // staged query dims: desc head_dim <= D (64 or 128)
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void seam_kernel(cf_kv_paged_attention_desc d, uint32_t splits,
-                                                        float *__restrict__ partial) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void seam_kernel(
+    cf_kv_paged_attention_desc d, uint32_t splits, float *__restrict__ partial, const uint32_t *__restrict__ route_taken,
+    uint32_t slot0) {
   constexpr int KS = D / 16;  // 16-dim k-steps of QK^T, 16-dim tiles of the output
   __shared__ __align__(16) uint8_t s_k[kChunk * kKStride];
   __shared__ __align__(16) uint8_t s_vt[kMaxD * kVStride];
@@ -240,6 +243,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   const uint32_t wv0 = blockIdx.x * kVecs + wave * 16;       // this wavefront's first vector
   const bool wave_active = wv0 < M;
   const float scale = d.softmax_scale;
+  if (route_taken && route_taken[kvh]) {  // the decode-shape route covered this head: an empty slot
+    for (uint32_t i = static_cast<uint32_t>(tid); i < kVecs * (HD + 2); i += kThreads) {
+      const uint32_t v = blockIdx.x * kVecs + i / (HD + 2), k = i % (HD + 2);
+      if (v < M)
+        partial[((static_cast<size_t>(slot0 + split) * d.kv_head_count + kvh) * M + v) * (HD + 2) + k] =
+            k == HD ? -INFINITY : 0.0f;
+    }
+    return;
+  }
 
   auto row_of = [&](uint32_t v) { return v / gqa; };
   auto qtok_of = [&](uint32_t r) { return d.query_token_begin + r; };
@@ -843,7 +855,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   for (int i = 0; i < 4; ++i) {
     const uint32_t v = wv0 + 4 * (lane >> 4) + i;
     if (v >= M) continue;
-    if (splits == 1) {
+    if (!partial) {
       const float inv = l_run[i] > 0.0f ? 1.0f / l_run[i] : 0.0f;
       float *out = d.output + (static_cast<size_t>(row_of(v)) * d.query_head_count + kvh * gqa + v % gqa) * HD;
 #pragma unroll
@@ -852,7 +864,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
         if (dd < HD) out[dd] = bad ? __builtin_nanf("") : acc[t][i] * inv;
       }
     } else {
-      float *pp = partial + ((static_cast<size_t>(split) * d.kv_head_count + kvh) * M + v) * (HD + 2);
+      float *pp = partial + ((static_cast<size_t>(slot0 + split) * d.kv_head_count + kvh) * M + v) * (HD + 2);
 #pragma unroll
       for (int t = 0; t < KS; ++t) {
         const uint32_t dd = 16 * t + (lane & 15);
@@ -871,22 +883,31 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 // once into LDS; each thread then streams its dim of every split with 8 loads in flight.
 __global__ __launch_bounds__(kMaxD) void seam_merge_kernel(cf_kv_paged_attention_desc d, uint32_t splits,
                                                            const float *__restrict__ partial) {
-  __shared__ float s_sc[64];  // e^(m_s - m) per split (0 for splits that saw nothing)
+  __shared__ float s_sc[cfkv::kSeamMergeMaxSlots];  // e^(m_s - m) per split (0 for splits that saw nothing)
   __shared__ float s_l, s_m;
   __shared__ int s_nan;
   const uint32_t v = blockIdx.x, kvh = blockIdx.y, dd = threadIdx.x;
   const uint32_t gqa = d.gqa_group_size, HD = d.head_dim, M = d.query_count * gqa;
   const size_t stride = static_cast<size_t>(d.kv_head_count) * M * (HD + 2);
   const float *base = partial + (static_cast<size_t>(kvh) * M + v) * (HD + 2);
-  if (dd < 64) {  // one wavefront: the splits' maxima, their merge, the scales and l
-    const float ms = dd < splits ? base[dd * stride + HD] : -INFINITY;
-    const float ls = dd < splits ? base[dd * stride + HD + 1] : 0.0f;
-    const bool nan = __builtin_amdgcn_ballot_w64(ms != ms) != 0;
-    float m = (ms != ms) ? -INFINITY : ms;
+  if (dd < 64) {  // one wavefront: the splits' maxima (two per lane), their merge, the scales and l
+    float ms[2], ls[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const uint32_t sp = dd + 64u * k;
+      ms[k] = sp < splits ? base[sp * stride + HD] : -INFINITY;
+      ls[k] = sp < splits ? base[sp * stride + HD + 1] : 0.0f;
+    }
+    const bool nan = __builtin_amdgcn_ballot_w64(ms[0] != ms[0] || ms[1] != ms[1]) != 0;
+    float m = fmaxf((ms[0] != ms[0]) ? -INFINITY : ms[0], (ms[1] != ms[1]) ? -INFINITY : ms[1]);
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    const float sc = (m == -INFINITY || ms == -INFINITY || ms != ms) ? 0.0f : __expf(ms - m);
-    s_sc[dd] = sc;
-    float l = ls * sc;
+    float l = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const float sc = (m == -INFINITY || ms[k] == -INFINITY || ms[k] != ms[k]) ? 0.0f : __expf(ms[k] - m);
+      s_sc[dd + 64 * k] = sc;
+      l += ls[k] * sc;
+    }
     for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
     if (dd == 0) {
       s_l = l;
@@ -1054,19 +1075,39 @@ extern "C" cf_status cf_kv_paged_attention_async(const cf_kv_paged_attention_des
   if (splits > 1 && part_bytes * splits > kSeamRegionBytes)
     splits = std::max<uint64_t>(1, kSeamRegionBytes / part_bytes);
   const hipStream_t s = cfd::as_stream(stream);
-  if (splits > 1 && stream_capturing(s)) splits = 1;
-  const auto launch = [&](float *partial) {
-    const dim3 grid(static_cast<uint32_t>(tiles), desc->kv_head_count, static_cast<uint32_t>(splits));
-    if (desc->head_dim <= 64) seam_kernel<64><<<grid, kThreads, 0, s>>>(*desc, static_cast<uint32_t>(splits), partial);
-    else seam_kernel<128><<<grid, kThreads, 0, s>>>(*desc, static_cast<uint32_t>(splits), partial);
-    if (splits > 1)
-      seam_merge_kernel<<<dim3(static_cast<uint32_t>(M), desc->kv_head_count), kMaxD, 0, s>>>(
-          *desc, static_cast<uint32_t>(splits), partial);
-  };
-  if (splits == 1) {
-    launch(nullptr);
-    return cfd::launch_status();
+  const bool capturing = stream_capturing(s);
+  if (splits > 1 && capturing) splits = 1;
+  // the decode-shape route (kv_seam_route.hpp) when a region can hold its page lists and both sets of slots
+  uint64_t route_splits = 0, route_words = 0;
+  if (!capturing && cfkv::seam_route_applies(*desc)) {
+    route_splits = cfkv::seam_route_splits(*desc);
+    route_words = cfkv::seam_route_scratch_words(*desc);
+    splits = std::min<uint64_t>(splits, cfkv::kSeamMergeMaxSlots - route_splits);
+    const uint64_t list_bytes = (route_words * 4 + 255) & ~uint64_t(255);
+    if (list_bytes + part_bytes * (route_splits + splits) > kSeamRegionBytes) route_splits = 0;
   }
+  const auto launch = [&](uint8_t *region) -> cf_status {
+    float *partial = reinterpret_cast<float *>(region);
+    const uint32_t *taken = nullptr;
+    if (route_splits) {
+      uint32_t *lists =
+          reinterpret_cast<uint32_t *>(region + kSeamRegionBytes - ((route_words * 4 + 255) & ~uint64_t(255)));
+      const cf_status rs = cfkv::seam_route_launch(*desc, static_cast<uint32_t>(route_splits), partial, lists, s);
+      if (rs != CF_OK) return rs;
+      taken = cfkv::seam_route_taken(*desc, lists);
+    }
+    const dim3 grid(static_cast<uint32_t>(tiles), desc->kv_head_count, static_cast<uint32_t>(splits));
+    const uint32_t slot0 = static_cast<uint32_t>(route_splits);
+    if (desc->head_dim <= 64)
+      seam_kernel<64><<<grid, kThreads, 0, s>>>(*desc, static_cast<uint32_t>(splits), partial, taken, slot0);
+    else
+      seam_kernel<128><<<grid, kThreads, 0, s>>>(*desc, static_cast<uint32_t>(splits), partial, taken, slot0);
+    if (partial)
+      seam_merge_kernel<<<dim3(static_cast<uint32_t>(M), desc->kv_head_count), kMaxD, 0, s>>>(
+          *desc, static_cast<uint32_t>(route_splits + splits), partial);
+    return cfd::launch_status();
+  };
+  if (splits == 1 && !route_splits) return launch(nullptr);
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return CF_ERR_CUDA;
   const StreamKey sid = stream_key(s);
@@ -1081,16 +1122,15 @@ extern "C" cf_status cf_kv_paged_attention_async(const cf_kv_paged_attention_des
   SeamRegion *r = seam_pick(sd, sid, wait);
   if (!r) {  // every region is owned by another stream that has not recorded an event yet
     splits = 1;
-    launch(nullptr);
-    return cfd::launch_status();
+    route_splits = 0;
+    return launch(nullptr);
   }
   if (wait && hipStreamWaitEvent(s, r->done, 0) != hipSuccess) return CF_ERR_CUDA;
   r->owner = sid;
   r->owned = true;
   r->done_valid = false;
   r->stamp = ++sd.calls;
-  launch(reinterpret_cast<float *>(sd.base + static_cast<uint64_t>(r - sd.r) * kSeamRegionBytes));
-  const cf_status st = cfd::launch_status();
+  const cf_status st = launch(sd.base + static_cast<uint64_t>(r - sd.r) * kSeamRegionBytes);
   if (sd.handover) {
     if (!r->done && hipEventCreateWithFlags(&r->done, hipEventDisableTiming) != hipSuccess) {
       r->done = nullptr;

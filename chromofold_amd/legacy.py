@@ -92,11 +92,22 @@ class PagedKv:
     device: str = "cuda"
     _keep: list = field(default_factory=list)
     descs: torch.Tensor | None = None
+    share_luts: bool = False  # pages whose k_lut / v_lut bytes are equal point at one device copy
 
     def __post_init__(self):
         arr = (A.cf_kv_device_page * max(1, len(self.pages)))()
+        shared = {}
+
+        def upload(k, a):
+            dt = np.int32 if k != "k_scales" and k != "v_scales" else np.float32
+            if not (self.share_luts and k in ("k_lut", "v_lut")):
+                return _dev(a, self.device, dt)
+            key = np.ascontiguousarray(a).tobytes()
+            if key not in shared:
+                shared[key] = _dev(a, self.device, dt)
+            return shared[key]
         for i, p in enumerate(self.pages):
-            t = {k: _dev(getattr(p, k), self.device, np.int32 if k != "k_scales" and k != "v_scales" else np.float32)
+            t = {k: upload(k, getattr(p, k))
                  for k in ["k_words", "k_block_offsets", "k_lut", "k_scales", "v_words", "v_block_offsets", "v_lut",
                            "v_scales"]}
             self._keep.append(t)

@@ -319,3 +319,118 @@ def test_scalar_route_head_dim_80_long_context_splits(dev):
     got, ref = _run(dev, deq, pages, q, kvh, gqa, T + 9 - 64, 1 / np.sqrt(hd), tail=(T, tail_k, tail_v))
     assert np.isfinite(got).all()
     assert np.abs(got - ref).max() <= ABS_TOL
+
+
+def _route_case(rng, kvh, hd, T, int8_at=None):
+    """rANS pages of 64 tokens (the last one ragged) for every KV head, one table pair per head shared by all its
+    pages, in shuffled descriptor order."""
+    from chromofold_amd import kv
+    from legacy_helpers import rans_page
+    pages, deq = [], []
+    for h in range(kvh):
+        K = rng.standard_normal((T, hd)).astype(np.float32)
+        V = (rng.standard_normal((T, hd)) * (0.5 + h)).astype(np.float32)
+        n = min(T, 1024)
+        tables = np.concatenate([kv.build_table(K[:n - n % 16].reshape(-1, 16, hd)),
+                                 kv.build_table(V[:n - n % 16].reshape(-1, 16, hd))])
+        for p0 in range(0, T, 64):
+            k, v = K[p0:p0 + 64].copy(), V[p0:p0 + 64].copy()
+            if int8_at is not None and (h, p0) == int8_at:
+                k[1, 2] = np.nan  # -128 after quantisation: the encoder stores this group as INT8
+            page, kd, vd = rans_page(k, v, h, p0, tables=tables)
+            pages.append(page)
+            deq.append((h, p0, kd, vd))
+    order = rng.permutation(len(pages))
+    return [pages[i] for i in order], [deq[i] for i in order]
+
+
+def _run_shared(dev, deq, pages, q, kvh, gqa, qtok, scale, window=0):
+    import torch
+    from chromofold_amd.legacy import PagedKv
+    pk = PagedKv(pages, str(dev), share_luts=True)
+    got = pk.attention(torch.from_numpy(q).to(dev), kvh, gqa, qtok, scale, window).cpu().numpy()
+    ref = np.zeros_like(q)
+    ref[0], _ = O.paged_attention_f64(q[0], q.shape[1], kvh, q.shape[2], gqa, qtok, window, scale, deq, None)
+    return got, ref
+
+
+@pytest.mark.parametrize("hd,gqa,kvh,T", [(128, 4, 8, 4000), (64, 1, 3, 2500), (128, 3, 2, 700), (64, 4, 1, 64)])
+def test_decode_route_rans_pages(dev, hd, gqa, kvh, T):
+    """A decode call (one query row, at most 4 query heads per KV head) over rANS pages whose KV heads each share one
+    table pair: the seam's decode-shape route (a page list per head, whole pages per wavefront through the batched
+    decode's group body, the seam's merge). Against the fp64 oracle at the seam's 2e-4 bar: the query at the end of
+    the context, in the middle of it (later pages wholly invisible, one page partly visible), and with a causal
+    window; a group stored as INT8 (it holds -128) among the rANS groups."""
+    rng = np.random.default_rng(7000 + hd + T)
+    pages, deq = _route_case(rng, kvh, hd, T, int8_at=(0, 64) if T > 64 else None)
+    q = rng.standard_normal((1, kvh * gqa, hd)).astype(np.float32)
+    sc = 1 / np.sqrt(hd)
+    for qtok, window in ((T - 1, 0), (T // 2 + 5, 0), (T - 1, 300), (T // 3, 100)):
+        got, ref = _run_shared(dev, deq, pages, q, kvh, gqa, qtok, sc, window)
+        assert np.isfinite(got).all(), (qtok, window)
+        assert np.abs(got - ref).max() <= ABS_TOL, (qtok, window, float(np.abs(got - ref).max()))
+
+
+def test_decode_route_mixed_heads(dev):
+    """One decode call where the route takes KV head 0 (rANS pages, one table pair) and leaves KV head 1 to the seam
+    kernel (a fixed-width page among its rANS pages) and KV head 2 too (its rANS pages carry two different table
+    pairs): every head against the fp64 oracle."""
+    from chromofold_amd import kv
+    from legacy_helpers import rans_page
+    rng = np.random.default_rng(7100)
+    hd, gqa, kvh, T = 128, 4, 3, 640
+    pages, deq = _route_case(rng, 1, hd, T)
+    for h in (1, 2):
+        K = rng.standard_normal((T, hd)).astype(np.float32)
+        V = rng.standard_normal((T, hd)).astype(np.float32)
+        tabs = [np.concatenate([kv.build_table(K[:256].reshape(-1, 16, hd)), kv.build_table(V[:256].reshape(-1, 16, hd))]),
+                np.concatenate([kv.build_table(K[256:512].reshape(-1, 16, hd)),
+                                kv.build_table(V[256:512].reshape(-1, 16, hd))])]
+        for p0 in range(0, T, 64):
+            if h == 1 and p0 == 128:
+                page, kd, vd = fixed_page(K[p0:p0 + 64], V[p0:p0 + 64], h, p0, 8)
+            else:
+                page, kd, vd = rans_page(K[p0:p0 + 64], V[p0:p0 + 64], h, p0,
+                                         tables=tabs[(p0 // 64) % 2 if h == 2 else 0])
+            pages.append(page)
+            deq.append((h, p0, kd, vd))
+    q = rng.standard_normal((1, kvh * gqa, hd)).astype(np.float32)
+    got, ref = _run_shared(dev, deq, pages, q, kvh, gqa, T - 1, 1 / np.sqrt(hd))
+    assert np.isfinite(got).all()
+    assert np.abs(got - ref).max() <= ABS_TOL
+
+
+def test_decode_route_refused_pages_nan(dev):
+    """Pages the route refuses make their KV head's outputs NaN, as the seam kernel does, and leave the other heads
+    untouched: a group that continues a chain, a descriptor whose token_count disagrees with its blob, and a blob
+    whose word stream was altered (the chain no longer ends where the encoder started)."""
+    from legacy_helpers import rans_page
+    rng = np.random.default_rng(7200)
+    hd, gqa, kvh, T = 64, 2, 2, 256
+    pages, deq = _route_case(rng, kvh, hd, T)
+    q = rng.standard_normal((1, kvh * gqa, hd)).astype(np.float32)
+    h0 = [i for i, p in enumerate(pages) if p.kv_head == 0]
+    k0 = rng.standard_normal((64, hd)).astype(np.float32)
+    v0 = rng.standard_normal((64, hd)).astype(np.float32)
+    for how in ("continues", "count", "stream"):
+        bad = list(pages)
+        i = h0[1]
+        p = pages[i]
+        if how == "continues":
+            cont, _, _ = rans_page(k0, v0, 0, p.token_begin, continues=True, second=(k0, v0), tables=None)
+            cont.k_lut, cont.v_lut = p.k_lut, p.v_lut  # the head's table pair, so that the route still takes the head
+            bad[i] = cont
+        elif how == "count":
+            q2, _, _ = rans_page(k0, v0, 0, p.token_begin)
+            q2.k_lut, q2.v_lut = p.k_lut, p.v_lut
+            q2.token_count = 60
+            bad[i] = q2
+        else:
+            q2, _, _ = rans_page(k0, v0, 0, p.token_begin, tables=np.concatenate([p.k_lut, p.v_lut]))
+            blob = q2.k_words.copy()
+            blob[-20] ^= 0x5A  # a byte of the word streams
+            q2.k_words = blob
+            bad[i] = q2
+        got, ref = _run_shared(dev, deq, bad, q, kvh, gqa, T - 1, 0.125)
+        assert np.isnan(got[:, :gqa]).all(), how                      # KV head 0: the refused page
+        assert np.abs(got[:, gqa:] - ref[:, gqa:]).max() <= ABS_TOL, how  # KV head 1: decoded normally
