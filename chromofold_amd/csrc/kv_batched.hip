@@ -944,78 +944,106 @@ __global__ __launch_bounds__(kGqa * D) void kv_merge_kernel(cf_kv_batched_desc d
 // ---- decode-shape route of the reference seam (kv_seam_route.hpp)
 
 constexpr unsigned kListThreads = 1024;
+constexpr unsigned kListPer = CF_KV_CUDA_MAX_PAGES_PER_LAUNCH / kListThreads;  // descriptors per thread
 
 // One workgroup per KV head: the head's pages in descriptor order (lists[head][0 .. counts[head])) and whether the
 // route takes the head (taken[head]): every page of the head a rANS page of the call's head_dim with 1..64 tokens,
-// all with the same K and V table pointers (compared as the minimum and maximum of each pointer's two halves).
+// all with the same K and V table pointers. Thread t looks at descriptors t + 1024 k (all its loads issued
+// together). Each wavefront compares the table pointers of its matching pages with those of its first one;
+// wavefront 0 then compares the wavefronts' first pointers, scans the 64 per-(k, wavefront) match counts into list
+// offsets and sets the verdict. The list is written only for a head the route takes.
 __global__ __launch_bounds__(kListThreads) void seam_list_kernel(cf_kv_paged_attention_desc d,
                                                                  uint32_t *__restrict__ lists,
                                                                  uint32_t *__restrict__ counts,
                                                                  uint32_t *__restrict__ taken) {
-  __shared__ uint32_t s_wc[kListThreads / 64];
-  __shared__ uint32_t s_base, s_bad;
-  __shared__ uint32_t s_lo[4], s_hi[4];  // min / max of k_lut and v_lut, low and high words
+  constexpr unsigned kW = kListThreads / 64;
+  static_assert(kListPer * kW == 64, "one wavefront scans the per-(chunk, wavefront) counts");
+  __shared__ uint32_t s_cnt[kListPer * kW];  // matches per (chunk, wavefront), then their exclusive prefix
+  __shared__ uint64_t s_kl[kW], s_vl[kW];    // per wavefront: the tables of its first matching page
+  __shared__ uint32_t s_flag[kW];            // per wavefront: bit 0 a match, bit 1 a refused page or other tables
+  __shared__ uint32_t s_ok;
   const uint32_t head = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
-  if (t < 4) {
-    s_lo[t] = 0xFFFFFFFFu;
-    s_hi[t] = 0u;
-  }
-  if (t == 0) {
-    s_base = 0;
-    s_bad = 0;
-  }
-  __syncthreads();
-  uint32_t *list = lists + static_cast<size_t>(head) * d.page_count;
-  for (uint32_t c0 = 0; c0 < d.page_count; c0 += kListThreads) {
-    const uint32_t p = c0 + t;
-    bool match = false;
+  bool match[kListPer], badp = false;
+  uint64_t kl[kListPer], vl[kListPer];
+#pragma unroll
+  for (unsigned k = 0; k < kListPer; ++k) {
+    const uint32_t p = t + kListThreads * k;
+    match[k] = false;
+    kl[k] = vl[k] = 0;
     if (p < d.page_count) {
       const cf_kv_device_page &pg = d.pages[p];
-      match = pg.kv_head == head;
-      if (match) {
-        const bool rans = pg.fixed_code_length == 0 && pg.k_max_code_length == 0;
-        if (!rans || pg.head_dim != d.head_dim || pg.token_count == 0 || pg.token_count > 64 || !pg.k_words ||
-            !pg.k_lut || !pg.v_lut)
-          s_bad = 1u;  // every writer stores the same value
-        const uint64_t k = reinterpret_cast<uintptr_t>(pg.k_lut), v = reinterpret_cast<uintptr_t>(pg.v_lut);
-        const uint32_t w[4] = {static_cast<uint32_t>(k), static_cast<uint32_t>(k >> 32), static_cast<uint32_t>(v),
-                               static_cast<uint32_t>(v >> 32)};
+      match[k] = pg.kv_head == head;
+      kl[k] = reinterpret_cast<uintptr_t>(pg.k_lut);
+      vl[k] = reinterpret_cast<uintptr_t>(pg.v_lut);
+      const bool rans = pg.fixed_code_length == 0 && pg.k_max_code_length == 0;
+      badp |= match[k] && (!rans || pg.head_dim != d.head_dim || pg.token_count == 0 || pg.token_count > 64 ||
+                           !pg.k_words || !kl[k] || !vl[k]);
+    }
+  }
+  uint64_t bal[kListPer], ck = 0, cv = 0;
+  bool has = false;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          atomicMin(&s_lo[i], w[i]);
-          atomicMax(&s_hi[i], w[i]);
-        }
-      }
+  for (unsigned k = 0; k < kListPer; ++k) {
+    bal[k] = __builtin_amdgcn_ballot_w64(match[k]);
+    if (lane == 0) s_cnt[k * kW + wave] = static_cast<uint32_t>(__builtin_popcountll(bal[k]));
+    if (!has && bal[k] != 0) {  // wave-uniform
+      const int f = __builtin_ctzll(bal[k]);
+      ck = __shfl(kl[k], f);
+      cv = __shfl(vl[k], f);
+      has = true;
     }
-    const uint64_t m = __builtin_amdgcn_ballot_w64(match);
-    if (lane == 0) s_wc[wave] = static_cast<uint32_t>(__builtin_popcountll(m));
-    __syncthreads();
-    uint32_t at = s_base;
-    for (uint32_t w = 0; w < wave; ++w) at += s_wc[w];
-    if (match)
-      list[at + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
-                                          __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0u))] = p;
-    __syncthreads();  // every thread has read s_base and s_wc
-    if (t == 0) {
-      uint32_t nn = 0;
-      for (uint32_t w = 0; w < kListThreads / 64; ++w) nn += s_wc[w];
-      s_base += nn;
+  }
+#pragma unroll
+  for (unsigned k = 0; k < kListPer; ++k) badp |= match[k] && (kl[k] != ck || vl[k] != cv);
+  const bool wbad = __builtin_amdgcn_ballot_w64(badp) != 0;
+  if (lane == 0) {
+    s_flag[wave] = (has ? 1u : 0u) | (wbad ? 2u : 0u);
+    s_kl[wave] = ck;
+    s_vl[wave] = cv;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const uint32_t c = s_cnt[lane];
+    uint32_t inc = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(inc, o);
+      if (lane >= static_cast<uint32_t>(o)) inc += y;
     }
-    __syncthreads();
+    s_cnt[lane] = inc - c;
+    const uint32_t total = __shfl(inc, 63);
+    const uint32_t f = lane < kW ? s_flag[lane] : 0u;
+    const uint64_t hb = __builtin_amdgcn_ballot_w64(f & 1u);
+    bool ok = __builtin_amdgcn_ballot_w64(f & 2u) == 0;
+    if (hb != 0) {
+      const int w0 = __builtin_ctzll(hb);
+      const uint64_t k0 = s_kl[w0], v0 = s_vl[w0];
+      const uint64_t kw = lane < kW ? s_kl[lane] : k0, vw = lane < kW ? s_vl[lane] : v0;
+      ok &= __builtin_amdgcn_ballot_w64((f & 1u) && (kw != k0 || vw != v0)) == 0;
+    }
+    if (lane == 0) {
+      counts[head] = total;
+      taken[head] = ok ? 1u : 0u;
+      s_ok = ok ? 1u : 0u;
+    }
   }
-  if (t == 0) {
-    bool same = true;
-    for (int i = 0; i < 4; ++i) same &= s_base == 0 || s_lo[i] == s_hi[i];
-    counts[head] = s_base;
-    taken[head] = (s_bad == 0 && same) ? 1u : 0u;
-  }
+  __syncthreads();
+  if (!s_ok) return;  // the seam kernel serves the head; nothing reads its list
+  uint32_t *list = lists + static_cast<size_t>(head) * d.page_count;
+#pragma unroll
+  for (unsigned k = 0; k < kListPer; ++k)
+    if (match[k])
+      list[s_cnt[k * kW + wave] + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal[k] >> 32),
+                                                            __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal[k]), 0u))] =
+          t + kListThreads * k;
 }
 
 // One (context split, KV head) per 4-wavefront workgroup for the heads seam_list_kernel took: wavefront w decodes the
 // head's listed pages of ordinals split + splits * (w + 4 k), each page one self-contained group (RANS_HYBRID chain
 // start or INT8 fallback) run through group_body with the page's token positions, then the workgroup writes slot
 // `split` of the seam's partials ([slot][kv head][vector][head_dim + 2] = acc, m, l; m NaN when a page was
-// refused). Heads the route did not take, and splits without pages, get empty slots (m = -inf, l = 0).
+// refused). Heads the route did not take are left alone (the seam kernel serves them and the merge reads its
+// slots); splits without pages get empty slots (m = -inf, l = 0).
 template <int D>
 __global__ CF_KV_OCC __launch_bounds__(64 * kWavesNarrow) void seam_group_kernel(cf_kv_paged_attention_desc d, uint32_t splits,
                                                                        const uint32_t *__restrict__ lists,
@@ -1032,7 +1060,8 @@ __global__ CF_KV_OCC __launch_bounds__(64 * kWavesNarrow) void seam_group_kernel
   const uint32_t split = blockIdx.x, head = blockIdx.y, gqa = d.gqa_group_size;
   const uint32_t n = counts[head];
   float *pp = partial + (static_cast<size_t>(split) * d.kv_head_count + head) * gqa * (D + 2);
-  if (!taken[head] || split >= n) {
+  if (!taken[head]) return;  // the seam kernel serves this head (the merge reads its slots instead)
+  if (split >= n) {
     for (uint32_t i = threadIdx.x; i < gqa * (D + 2); i += kThreads) pp[i] = i % (D + 2) == D ? -INFINITY : 0.0f;
     return;
   }

@@ -213,7 +213,7 @@ __device__ __forceinline__ void wave_sync() {
 
 // Split s of the (vectors, KV head) unit writes slot slot0 + s of `partial`: [slot][kv head][vector][head_dim + 2] =
 // acc, m, l; with no `partial` (one split) the workgroup writes the output itself. `route_taken` (the decode-shape
-// route's per-head flags, kv_seam_route.hpp, or NULL): a head the route took gets an empty slot here.
+// route's per-head flags, kv_seam_route.hpp, or NULL): a head the route took is left to it.
 template <int D>  // staged query dims: desc head_dim <= D (64 or 128)
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void seam_kernel(
     cf_kv_paged_attention_desc d, uint32_t splits, float *__restrict__ partial, const uint32_t *__restrict__ route_taken,
@@ -243,15 +243,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   const uint32_t wv0 = blockIdx.x * kVecs + wave * 16;       // this wavefront's first vector
   const bool wave_active = wv0 < M;
   const float scale = d.softmax_scale;
-  if (route_taken && route_taken[kvh]) {  // the decode-shape route covered this head: an empty slot
-    for (uint32_t i = static_cast<uint32_t>(tid); i < kVecs * (HD + 2); i += kThreads) {
-      const uint32_t v = blockIdx.x * kVecs + i / (HD + 2), k = i % (HD + 2);
-      if (v < M)
-        partial[((static_cast<size_t>(slot0 + split) * d.kv_head_count + kvh) * M + v) * (HD + 2) + k] =
-            k == HD ? -INFINITY : 0.0f;
-    }
-    return;
-  }
+  if (route_taken && route_taken[kvh]) return;  // the decode-shape route covers this head (the merge knows)
 
   auto row_of = [&](uint32_t v) { return v / gqa; };
   auto qtok_of = [&](uint32_t r) { return d.query_token_begin + r; };
@@ -881,8 +873,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 // Merge the split partials of one (vector, KV head) per workgroup: out = sum_s acc_s e^(m_s - m) / sum_s l_s
 // e^(m_s - m); zeros when nothing was visible; NaN when a split saw a refused page. The splits' (m, l) pairs are read
 // once into LDS; each thread then streams its dim of every split with 8 loads in flight.
+// With the decode-shape route (`taken` not NULL), a head it took has its slots at [0, route_slots), the others at
+// [route_slots, splits).
 __global__ __launch_bounds__(kMaxD) void seam_merge_kernel(cf_kv_paged_attention_desc d, uint32_t splits,
-                                                           const float *__restrict__ partial) {
+                                                           const float *__restrict__ partial,
+                                                           const uint32_t *__restrict__ taken, uint32_t route_slots) {
   __shared__ float s_sc[cfkv::kSeamMergeMaxSlots];  // e^(m_s - m) per split (0 for splits that saw nothing)
   __shared__ float s_l, s_m;
   __shared__ int s_nan;
@@ -890,6 +885,14 @@ __global__ __launch_bounds__(kMaxD) void seam_merge_kernel(cf_kv_paged_attention
   const uint32_t gqa = d.gqa_group_size, HD = d.head_dim, M = d.query_count * gqa;
   const size_t stride = static_cast<size_t>(d.kv_head_count) * M * (HD + 2);
   const float *base = partial + (static_cast<size_t>(kvh) * M + v) * (HD + 2);
+  if (taken) {
+    if (taken[kvh]) {
+      splits = route_slots;
+    } else {
+      base += route_slots * stride;
+      splits -= route_slots;
+    }
+  }
   if (dd < 64) {  // one wavefront: the splits' maxima (two per lane), their merge, the scales and l
     float ms[2], ls[2];
 #pragma unroll
@@ -1104,7 +1107,7 @@ extern "C" cf_status cf_kv_paged_attention_async(const cf_kv_paged_attention_des
       seam_kernel<128><<<grid, kThreads, 0, s>>>(*desc, static_cast<uint32_t>(splits), partial, taken, slot0);
     if (partial)
       seam_merge_kernel<<<dim3(static_cast<uint32_t>(M), desc->kv_head_count), kMaxD, 0, s>>>(
-          *desc, static_cast<uint32_t>(route_splits + splits), partial);
+          *desc, static_cast<uint32_t>(route_splits + splits), partial, taken, slot0);
     return cfd::launch_status();
   };
   if (splits == 1 && !route_splits) return launch(nullptr);
