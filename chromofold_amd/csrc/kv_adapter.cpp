@@ -1,6 +1,6 @@
 // kv_adapter.cpp — the llama.cpp paged-KV adapter (include/chromofold/chromofold_kv_adapter.h) and the host encoder
-// of the reference's fixed-width page format. Host C++ over the HIP runtime; attention goes through
-// cf_kv_paged_attention_async (kv_legacy.hip).
+// of the reference's fixed-width page format. Host C++ over the HIP runtime; attention goes through the seam
+// cf_kv_paged_attention_async (kv_legacy.hip) with its decode-shape route off (that route takes rANS pages only).
 //
 // Behaviour follows reference integrations/llama.cpp/chromofold_kv_adapter.cpp:21-236 and
 // src/runtime/compressed_kv_cache.cu:66-210: per (layer, kv head) a host fp32 active tail that must grow
@@ -26,6 +26,7 @@
 
 #include "chromofold/chromofold_kv_adapter.h"
 #include "chromofold/kv_codec_ext.h"
+#include "kv_seam_route.hpp"
 #include "chromofold/kv_cuda.h"
 
 extern "C" cf_status cf_kv_encode_fixed_page(uint32_t bits, const float *keys, const float *values,
@@ -397,7 +398,7 @@ extern "C" int cf_llama_kv_attention(cf_llama_kv_adapter *a, uint32_t layer, con
     d.head_dim = a->opt.head_dim;
     d.causal_window = causal_window;
     d.softmax_scale = softmax_scale;
-    if (cf_kv_paged_attention_async(&d, stream) != CF_OK)
+    if (cfkv::seam_paged_attention(&d, stream, false) != CF_OK)  // fixed-width pages: the route never takes them
       throw std::runtime_error("ChromoFold paged attention launch rejected");
   });
 }

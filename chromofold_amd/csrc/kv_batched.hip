@@ -943,112 +943,105 @@ __global__ __launch_bounds__(kGqa * D) void kv_merge_kernel(cf_kv_batched_desc d
 
 // ---- decode-shape route of the reference seam (kv_seam_route.hpp)
 
-constexpr unsigned kListThreads = 1024;
-constexpr unsigned kListPer = CF_KV_CUDA_MAX_PAGES_PER_LAUNCH / kListThreads;  // descriptors per thread
+using cfkv::kRouteChunk;
+using cfkv::kRouteInfoWords;
+using cfkv::kRouteMaxHeads;
+using cfkv::seam_route_chunks;
+static_assert(CF_KV_CUDA_MAX_PAGES_PER_LAUNCH / kRouteChunk <= 64, "a wavefront holds a head's chunk records");
 
-// One workgroup per KV head: the head's pages in descriptor order (lists[head][0 .. counts[head])) and whether the
-// route takes the head (taken[head]): every page of the head a rANS page of the call's head_dim with 1..64 tokens,
-// all with the same K and V table pointers. Thread t looks at descriptors t + 1024 k (all its loads issued
-// together). Each wavefront compares the table pointers of its matching pages with those of its first one;
-// wavefront 0 then compares the wavefronts' first pointers, scans the 64 per-(k, wavefront) match counts into list
-// offsets and sets the verdict. The list is written only for a head the route takes.
-__global__ __launch_bounds__(kListThreads) void seam_list_kernel(cf_kv_paged_attention_desc d,
-                                                                 uint32_t *__restrict__ lists,
-                                                                 uint32_t *__restrict__ counts,
-                                                                 uint32_t *__restrict__ taken) {
-  constexpr unsigned kW = kListThreads / 64;
-  static_assert(kListPer * kW == 64, "one wavefront scans the per-(chunk, wavefront) counts");
-  __shared__ uint32_t s_cnt[kListPer * kW];  // matches per (chunk, wavefront), then their exclusive prefix
-  __shared__ uint64_t s_kl[kW], s_vl[kW];    // per wavefront: the tables of its first matching page
-  __shared__ uint32_t s_flag[kW];            // per wavefront: bit 0 a match, bit 1 a refused page or other tables
-  __shared__ uint32_t s_ok;
-  const uint32_t head = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
-  bool match[kListPer], badp = false;
-  uint64_t kl[kListPer], vl[kListPer];
-#pragma unroll
-  for (unsigned k = 0; k < kListPer; ++k) {
-    const uint32_t p = t + kListThreads * k;
-    match[k] = false;
-    kl[k] = vl[k] = 0;
-    if (p < d.page_count) {
-      const cf_kv_device_page &pg = d.pages[p];
-      match[k] = pg.kv_head == head;
-      kl[k] = reinterpret_cast<uintptr_t>(pg.k_lut);
-      vl[k] = reinterpret_cast<uintptr_t>(pg.v_lut);
-      const bool rans = pg.fixed_code_length == 0 && pg.k_max_code_length == 0;
-      badp |= match[k] && (!rans || pg.head_dim != d.head_dim || pg.token_count == 0 || pg.token_count > 64 ||
-                           !pg.k_words || !kl[k] || !vl[k]);
-    }
-  }
-  uint64_t bal[kListPer], ck = 0, cv = 0;
-  bool has = false;
-#pragma unroll
-  for (unsigned k = 0; k < kListPer; ++k) {
-    bal[k] = __builtin_amdgcn_ballot_w64(match[k]);
-    if (lane == 0) s_cnt[k * kW + wave] = static_cast<uint32_t>(__builtin_popcountll(bal[k]));
-    if (!has && bal[k] != 0) {  // wave-uniform
-      const int f = __builtin_ctzll(bal[k]);
-      ck = __shfl(kl[k], f);
-      cv = __shfl(vl[k], f);
-      has = true;
-    }
-  }
-#pragma unroll
-  for (unsigned k = 0; k < kListPer; ++k) badp |= match[k] && (kl[k] != ck || vl[k] != cv);
-  const bool wbad = __builtin_amdgcn_ballot_w64(badp) != 0;
-  if (lane == 0) {
-    s_flag[wave] = (has ? 1u : 0u) | (wbad ? 2u : 0u);
-    s_kl[wave] = ck;
-    s_vl[wave] = cv;
+// One workgroup per chunk of 256 descriptors (thread t: descriptor 256 chunk + t). Each wavefront walks the KV
+// heads present among its 64 descriptors (one ballot per head) and notes per (head, wavefront) the match count,
+// whether a match is refused or names other tables than the wavefront's first match, and those tables; thread h
+// then combines the four wavefronts of head h into the (head, chunk) record and the wavefronts' offsets, and every
+// thread writes its descriptor index to lists[kv_head][256 chunk + offset] (descriptor order within the chunk).
+// Descriptors whose kv_head is not below the call's KV head count belong to no head (the seam kernel skips them).
+__global__ __launch_bounds__(kRouteChunk) void seam_list_kernel(cf_kv_paged_attention_desc d,
+                                                                uint32_t *__restrict__ lists,
+                                                                uint32_t *__restrict__ info) {
+  constexpr unsigned W = kRouteChunk / 64;
+  static_assert(kRouteMaxHeads * W == kRouteChunk, "one counter per thread to clear");
+  __shared__ uint32_t s_cnt[kRouteMaxHeads][W];  // matches per (head, wavefront), then their offsets
+  __shared__ uint32_t s_bad[kRouteMaxHeads][W];
+  __shared__ uint64_t s_kl[kRouteMaxHeads][W], s_vl[kRouteMaxHeads][W];
+  const uint32_t chunk = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const uint32_t H = d.kv_head_count, p = chunk * kRouteChunk + t;
+  s_cnt[t / W][t % W] = 0;
+  uint32_t hp = 0xFFFFFFFFu;
+  uint64_t kl = 0, vl = 0;
+  bool badp = false;
+  if (p < d.page_count) {
+    const cf_kv_device_page &pg = d.pages[p];
+    hp = pg.kv_head;
+    kl = reinterpret_cast<uintptr_t>(pg.k_lut);
+    vl = reinterpret_cast<uintptr_t>(pg.v_lut);
+    const bool rans = pg.fixed_code_length == 0 && pg.k_max_code_length == 0;
+    badp = !rans || pg.head_dim != d.head_dim || pg.token_count == 0 || pg.token_count > 64 || !pg.k_words || !kl ||
+           !vl;
   }
   __syncthreads();
-  if (wave == 0) {
-    const uint32_t c = s_cnt[lane];
-    uint32_t inc = c;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t y = __shfl_up(inc, o);
-      if (lane >= static_cast<uint32_t>(o)) inc += y;
-    }
-    s_cnt[lane] = inc - c;
-    const uint32_t total = __shfl(inc, 63);
-    const uint32_t f = lane < kW ? s_flag[lane] : 0u;
-    const uint64_t hb = __builtin_amdgcn_ballot_w64(f & 1u);
-    bool ok = __builtin_amdgcn_ballot_w64(f & 2u) == 0;
-    if (hb != 0) {
-      const int w0 = __builtin_ctzll(hb);
-      const uint64_t k0 = s_kl[w0], v0 = s_vl[w0];
-      const uint64_t kw = lane < kW ? s_kl[lane] : k0, vw = lane < kW ? s_vl[lane] : v0;
-      ok &= __builtin_amdgcn_ballot_w64((f & 1u) && (kw != k0 || vw != v0)) == 0;
-    }
+  const bool mine_ok = hp < H;
+  uint64_t mine = 0, left = __builtin_amdgcn_ballot_w64(mine_ok);
+  while (left != 0) {  // wave-uniform: one head per pass
+    const int f = __builtin_ctzll(left);
+    const uint32_t h = __shfl(hp, f);
+    const uint64_t k0 = __shfl(kl, f), v0 = __shfl(vl, f);
+    const uint64_t bal = __builtin_amdgcn_ballot_w64(hp == h);
+    if (hp == h) mine = bal;
+    const bool wb = __builtin_amdgcn_ballot_w64(hp == h && (badp || kl != k0 || vl != v0)) != 0;
     if (lane == 0) {
-      counts[head] = total;
-      taken[head] = ok ? 1u : 0u;
-      s_ok = ok ? 1u : 0u;
+      s_cnt[h][wave] = static_cast<uint32_t>(__builtin_popcountll(bal));
+      s_bad[h][wave] = wb ? 1u : 0u;
+      s_kl[h][wave] = k0;
+      s_vl[h][wave] = v0;
     }
+    left &= ~bal;
   }
   __syncthreads();
-  if (!s_ok) return;  // the seam kernel serves the head; nothing reads its list
-  uint32_t *list = lists + static_cast<size_t>(head) * d.page_count;
+  if (t < H) {  // head t's record for this chunk
+    uint32_t run = 0, bad = 0;
+    bool seen = false;
+    uint64_t k0 = 0, v0 = 0;
 #pragma unroll
-  for (unsigned k = 0; k < kListPer; ++k)
-    if (match[k])
-      list[s_cnt[k * kW + wave] + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal[k] >> 32),
-                                                            __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal[k]), 0u))] =
-          t + kListThreads * k;
+    for (unsigned w = 0; w < W; ++w) {
+      const uint32_t c = s_cnt[t][w];
+      if (c) {
+        bad |= s_bad[t][w];
+        if (!seen) {
+          k0 = s_kl[t][w];
+          v0 = s_vl[t][w];
+          seen = true;
+        } else if (s_kl[t][w] != k0 || s_vl[t][w] != v0) {
+          bad = 1u;
+        }
+      }
+      s_cnt[t][w] = run;
+      run += c;
+    }
+    uint4 *e = reinterpret_cast<uint4 *>(info + (static_cast<size_t>(t) * gridDim.x + chunk) * kRouteInfoWords);
+    e[0] = uint4{run, bad, static_cast<uint32_t>(k0), static_cast<uint32_t>(k0 >> 32)};
+    e[1] = uint4{static_cast<uint32_t>(v0), static_cast<uint32_t>(v0 >> 32), 0u, 0u};
+  }
+  __syncthreads();
+  if (mine_ok)
+    lists[static_cast<size_t>(hp) * d.page_count + chunk * kRouteChunk + s_cnt[hp][wave] +
+          __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mine >> 32),
+                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mine), 0u))] = p;
 }
 
-// One (context split, KV head) per 4-wavefront workgroup for the heads seam_list_kernel took: wavefront w decodes the
-// head's listed pages of ordinals split + splits * (w + 4 k), each page one self-contained group (RANS_HYBRID chain
-// start or INT8 fallback) run through group_body with the page's token positions, then the workgroup writes slot
-// `split` of the seam's partials ([slot][kv head][vector][head_dim + 2] = acc, m, l; m NaN when a page was
-// refused). Heads the route did not take are left alone (the seam kernel serves them and the merge reads its
-// slots); splits without pages get empty slots (m = -inf, l = 0).
+// One (context split, KV head) per 4-wavefront workgroup. Each wavefront reads the head's chunk records (lane c:
+// chunk c) and decides whether the route takes the head: no refused page and one pair of table pointers over all
+// chunks with pages; workgroup (0, head) publishes that in taken[head]. For a head it takes, wavefront w decodes
+// the head's pages of ordinals split + splits * (w + 4 k) (ordinal o: chunk = number of chunks whose inclusive
+// page prefix is at most o, then its list entry o - exclusive prefix), each page one self-contained group
+// (RANS_HYBRID chain start or INT8 fallback) run through group_body with the page's token positions, then the
+// workgroup writes slot `split` of the seam's partials ([slot][kv head][vector][head_dim + 2] = acc, m, l; m NaN
+// when a page was refused). Heads the route did not take are left alone (the seam kernel serves them and the merge
+// reads its slots); splits without pages get empty slots (m = -inf, l = 0).
 template <int D>
 __global__ CF_KV_OCC __launch_bounds__(64 * kWavesNarrow) void seam_group_kernel(cf_kv_paged_attention_desc d, uint32_t splits,
+                                                                       const uint32_t *__restrict__ info,
                                                                        const uint32_t *__restrict__ lists,
-                                                                       const uint32_t *__restrict__ counts,
-                                                                       const uint32_t *__restrict__ taken,
+                                                                       uint32_t *__restrict__ taken,
                                                                        float *__restrict__ partial) {
   constexpr int W = kWavesNarrow, NQ = D / 4, RAW = raw_words<D>(), BUF = buf_u32<D>(), kThreads = 64 * W;
   __shared__ uint2 s_tab[2][kSlots];
@@ -1058,17 +1051,46 @@ __global__ CF_KV_OCC __launch_bounds__(64 * kWavesNarrow) void seam_group_kernel
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int G = lane >> 4, t = lane & 15;
   const uint32_t split = blockIdx.x, head = blockIdx.y, gqa = d.gqa_group_size;
-  const uint32_t n = counts[head];
+  // the head's chunk records, lane c holding chunk c
+  const uint32_t chunks = seam_route_chunks(d.page_count);
+  uint32_t ccount = 0, cbad = 0;
+  uint64_t ckl = 0, cvl = 0;
+  if (static_cast<uint32_t>(lane) < chunks) {
+    const uint4 *e = reinterpret_cast<const uint4 *>(
+        info + (static_cast<size_t>(head) * chunks + static_cast<uint32_t>(lane)) * kRouteInfoWords);
+    const uint4 a = e[0], b = e[1];
+    ccount = a.x;
+    cbad = a.y;
+    ckl = a.z | (static_cast<uint64_t>(a.w) << 32);
+    cvl = b.x | (static_cast<uint64_t>(b.y) << 32);
+  }
+  const uint64_t with = __builtin_amdgcn_ballot_w64(ccount != 0);
+  bool ok = __builtin_amdgcn_ballot_w64(ccount != 0 && cbad != 0) == 0;
+  uint64_t tkl = 0, tvl = 0;
+  if (with != 0) {
+    const int f = __builtin_ctzll(with);
+    tkl = __shfl(ckl, f);
+    tvl = __shfl(cvl, f);
+    ok &= __builtin_amdgcn_ballot_w64(ccount != 0 && (ckl != tkl || cvl != tvl)) == 0;
+  }
+  uint32_t cinc = ccount;  // inclusive prefix of the chunks' page counts
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(cinc, o);
+    if (lane >= o) cinc += y;
+  }
+  const uint32_t n = __shfl(cinc, 63);
+  if (split == 0 && threadIdx.x == 0) taken[head] = ok ? 1u : 0u;
   float *pp = partial + (static_cast<size_t>(split) * d.kv_head_count + head) * gqa * (D + 2);
-  if (!taken[head]) return;  // the seam kernel serves this head (the merge reads its slots instead)
+  if (!ok) return;  // the seam kernel serves this head (the merge reads its slots instead)
   if (split >= n) {
     for (uint32_t i = threadIdx.x; i < gqa * (D + 2); i += kThreads) pp[i] = i % (D + 2) == D ? -INFINITY : 0.0f;
     return;
   }
   const uint32_t *list = lists + static_cast<size_t>(head) * d.page_count;
+  const uint32_t cexc = cinc - ccount;
   {  // the head's tables (every listed page has these), as the decoder reads them
-    const cf_kv_device_page &p0 = d.pages[list[0]];
-    const uint2 *tk = reinterpret_cast<const uint2 *>(p0.k_lut), *tv = reinterpret_cast<const uint2 *>(p0.v_lut);
+    const uint2 *tk = reinterpret_cast<const uint2 *>(tkl), *tv = reinterpret_cast<const uint2 *>(tvl);
     for (uint32_t i = threadIdx.x; i < kSlots; i += kThreads) {
       const uint2 a = tk[i], b = tv[i];
       s_tab[0][i] = uint2{(a.x & 2047u) | (((a.x >> 11) & 2047u) << 16), a.y};
@@ -1125,7 +1147,8 @@ __global__ CF_KV_OCC __launch_bounds__(64 * kWavesNarrow) void seam_group_kernel
   uint32_t pre[14];
   auto noop = []() {};
   for (uint32_t o = split + splits * static_cast<uint32_t>(wave); o < n; o += splits * W) {
-    const cf_kv_device_page &pg = d.pages[list[o]];
+    const uint32_t oc = static_cast<uint32_t>(__builtin_popcountll(__builtin_amdgcn_ballot_w64(cinc <= o)));
+    const cf_kv_device_page &pg = d.pages[list[oc * kRouteChunk + o - __shfl(cexc, static_cast<int>(oc))]];
     const uint32_t tb = pg.token_begin, tcnt = pg.token_count;
     if (tb > qtok || tb + tcnt <= wlo) continue;  // wholly outside the visible range: skipped unread
     const uint8_t *blob = reinterpret_cast<const uint8_t *>(pg.k_words);
@@ -1470,7 +1493,7 @@ namespace cfkv {
 bool seam_route_applies(const cf_kv_paged_attention_desc &d) {
   return d.query_count == 1 && d.gqa_group_size >= 1 && d.gqa_group_size <= static_cast<uint32_t>(kGqa) &&
          (d.head_dim == 64 || d.head_dim == 128) && d.active_token_count == 0 && d.page_count > 0 && d.pages &&
-         d.kv_head_count >= 1 && d.kv_head_count <= 65535;
+         d.kv_head_count >= 1 && d.kv_head_count <= kRouteMaxHeads;
 }
 
 uint32_t seam_route_splits(const cf_kv_paged_attention_desc &d) {
@@ -1482,20 +1505,23 @@ uint32_t seam_route_splits(const cf_kv_paged_attention_desc &d) {
 }
 
 uint64_t seam_route_scratch_words(const cf_kv_paged_attention_desc &d) {
-  return static_cast<uint64_t>(d.kv_head_count) * d.page_count + 2ull * d.kv_head_count;
+  const uint64_t h = d.kv_head_count;
+  return h * seam_route_chunks(d.page_count) * kRouteInfoWords + h + h * d.page_count;
 }
 
 cf_status seam_route_launch(const cf_kv_paged_attention_desc &d, uint32_t splits, float *partial, uint32_t *scratch,
                             hipStream_t s) {
-  uint32_t *lists = scratch;
-  uint32_t *counts = scratch + static_cast<uint64_t>(d.kv_head_count) * d.page_count;
-  uint32_t *taken = counts + d.kv_head_count;
-  seam_list_kernel<<<d.kv_head_count, kListThreads, 0, s>>>(d, lists, counts, taken);
+  const uint32_t chunks = seam_route_chunks(d.page_count);
+  uint32_t *info = scratch;
+  uint32_t *taken = info + static_cast<uint64_t>(d.kv_head_count) * chunks * kRouteInfoWords;
+  uint32_t *lists = taken + d.kv_head_count;
+  if ((reinterpret_cast<uintptr_t>(scratch) & 15u) != 0 || chunks > 64) return CF_ERR_INVALID_ARGUMENT;
+  seam_list_kernel<<<chunks, kRouteChunk, 0, s>>>(d, lists, info);
   const dim3 grid(splits, d.kv_head_count);
   if (d.head_dim == 128)
-    seam_group_kernel<128><<<grid, 64 * kWavesNarrow, 0, s>>>(d, splits, lists, counts, taken, partial);
+    seam_group_kernel<128><<<grid, 64 * kWavesNarrow, 0, s>>>(d, splits, info, lists, taken, partial);
   else
-    seam_group_kernel<64><<<grid, 64 * kWavesNarrow, 0, s>>>(d, splits, lists, counts, taken, partial);
+    seam_group_kernel<64><<<grid, 64 * kWavesNarrow, 0, s>>>(d, splits, info, lists, taken, partial);
   return cfd::launch_status();
 }
 

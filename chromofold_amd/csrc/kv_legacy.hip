@@ -1062,6 +1062,10 @@ extern "C" cf_status cf_kv_validate_paged_attention_desc(const cf_kv_paged_atten
 // per split, at most 64 splits, and no more partials than one scratch region holds (one split writes the output
 // directly and uses no region).
 extern "C" cf_status cf_kv_paged_attention_async(const cf_kv_paged_attention_desc *desc, void *stream) {
+  return cfkv::seam_paged_attention(desc, stream, true);
+}
+
+cf_status cfkv::seam_paged_attention(const cf_kv_paged_attention_desc *desc, void *stream, bool allow_route) {
   const cf_status valid = cf_kv_validate_paged_attention_desc(desc);
   if (valid != CF_OK) return valid;
   if (desc->kv_head_count > 65535) return CF_ERR_UNSUPPORTED;
@@ -1082,7 +1086,7 @@ extern "C" cf_status cf_kv_paged_attention_async(const cf_kv_paged_attention_des
   if (splits > 1 && capturing) splits = 1;
   // the decode-shape route (kv_seam_route.hpp) when a region can hold its page lists and both sets of slots
   uint64_t route_splits = 0, route_words = 0;
-  if (!capturing && cfkv::seam_route_applies(*desc)) {
+  if (allow_route && !capturing && cfkv::seam_route_applies(*desc)) {
     route_splits = cfkv::seam_route_splits(*desc);
     route_words = cfkv::seam_route_scratch_words(*desc);
     splits = std::min<uint64_t>(splits, cfkv::kSeamMergeMaxSlots - route_splits);

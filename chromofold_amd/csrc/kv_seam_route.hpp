@@ -4,12 +4,14 @@
 // A seam call with one query row and at most four query heads per KV head (a decode step) has four query vectors
 // per KV head. The seam kernel's 64-vector tiles then carry 60 padding vectors, and its workgroups decode each
 // page's two rANS chains one after another with nothing to overlap them. The route instead:
-//   1. seam_list_kernel: one workgroup per KV head lists the head's pages in descriptor order and decides whether
-//      the route takes the head: every page a rANS page (the seam's tag) of the call's head_dim with 1..64 tokens
-//      and one shared pair of K/V tables;
-//   2. seam_group_kernel: for the heads it takes, each wavefront decodes whole pages with the batched decode's
-//      group body (both chains interleaved in one wavefront, QK^T on the GQA heads' MFMA broadcast, P.V on
-//      v_mfma_f32_16x16x32_f16) and writes split partials in the seam's layout, slots [0, splits);
+//   1. seam_list_kernel: one workgroup per chunk of 256 descriptors lists, for every KV head, the head's pages of
+//      the chunk in descriptor order and records per (head, chunk) the page count, whether every such page is a
+//      rANS page (the seam's tag) of the call's head_dim with 1..64 tokens, and the K/V table pointers of the first;
+//   2. seam_group_kernel: each workgroup combines its head's chunk records (the route takes the head when every
+//      page qualifies and all share one pair of K/V tables; the first split's workgroup publishes the verdict); for
+//      a head it takes, each wavefront decodes whole pages with the batched decode's group body (both chains
+//      interleaved in one wavefront, QK^T on the GQA heads' MFMA broadcast, P.V on v_mfma_f32_16x16x32_f16) and
+//      writes split partials in the seam's layout, slots [0, splits);
 //   3. the seam kernel runs for the heads the route did not take (its slots follow), and the seam's merge kernel
 //      combines all slots.
 // Results follow the seam's rules: tokens in [window begin, query token] of every page; a page whose blob does not
@@ -27,19 +29,32 @@ namespace cfkv {
 
 // Split slots the seam's merge kernel combines at most (the route's slots plus the seam kernel's).
 constexpr uint32_t kSeamMergeMaxSlots = 128;
+// Descriptors per list workgroup, KV heads the route serves at most, words of a (head, chunk) record
+// (count, refused, K table lo/hi, V table lo/hi, 2 unused).
+constexpr uint32_t kRouteChunk = 256;
+constexpr uint32_t kRouteMaxHeads = 64;
+constexpr uint32_t kRouteInfoWords = 8;
+__host__ __device__ inline uint32_t seam_route_chunks(uint32_t page_count) {
+  return (page_count + kRouteChunk - 1) / kRouteChunk;
+}
+
+// cf_kv_paged_attention_async with the route allowed or not. A caller that knows its pages carry another tag than
+// the route takes (the llama adapter seals fixed-width pages) passes false and saves the route's two launches.
+cf_status seam_paged_attention(const cf_kv_paged_attention_desc *desc, void *stream, bool allow_route);
 
 // Host-side conditions of the route (the device side decides per KV head).
 bool seam_route_applies(const cf_kv_paged_attention_desc &d);
 // Context splits the route uses per KV head.
 uint32_t seam_route_splits(const cf_kv_paged_attention_desc &d);
-// Scratch (u32 words) the route needs: page lists [kv_heads][page_count], counts [kv_heads], taken [kv_heads].
+// Scratch (u32 words) the route needs: records [kv_heads][chunks][8], taken [kv_heads], lists
+// [kv_heads][page_count] (chunk c's pages of a head from c * 256). The scratch is 16-byte aligned.
 uint64_t seam_route_scratch_words(const cf_kv_paged_attention_desc &d);
 // Launches steps 1 and 2 on `s`. `taken` (inside `scratch`) is what the seam kernel then reads.
 cf_status seam_route_launch(const cf_kv_paged_attention_desc &d, uint32_t splits, float *partial, uint32_t *scratch,
                             hipStream_t s);
 // The per-head "taken" flags inside the scratch.
 inline const uint32_t *seam_route_taken(const cf_kv_paged_attention_desc &d, const uint32_t *scratch) {
-  return scratch + static_cast<uint64_t>(d.kv_head_count) * d.page_count + d.kv_head_count;
+  return scratch + static_cast<uint64_t>(d.kv_head_count) * seam_route_chunks(d.page_count) * kRouteInfoWords;
 }
 
 }  // namespace cfkv
