@@ -406,7 +406,8 @@ __global__ CF_KV_OCC __launch_bounds__(64 * W) void kv_batched_kernel(cf_kv_batc
   constexpr int kThreads = 64 * W;
   constexpr bool kWide = W == kWavesWide;           // contiguous weighted pair blocks (else strided pairs)
   constexpr int KL = kWide && RANS ? 16 : 0;        // V quads parked in LDS (see group_body)
-  __shared__ uint2 s_tab[RANS ? 2 : 1][kSlots];     // {f | c << 16, spread big bits} per slot, K and V tables
+  __shared__ __attribute__((aligned(16))) uint2 s_tab[RANS ? 2 : 1][kSlots];  // {f | c << 16, spread big bits} per
+                                                                              // slot, K and V tables
   __shared__ __attribute__((aligned(16))) _Float16 s_p[W][2][4][kGqa][16];  // per wave: [hi, lo][page][head][token]
                                                                           // probability * v_scale
   __shared__ uint32_t s_buf[W][BUF];                // per wave: staged words; query staging and partials alias it
@@ -422,10 +423,21 @@ __global__ CF_KV_OCC __launch_bounds__(64 * W) void kv_batched_kernel(cf_kv_batc
 
   // ---- stage tables and queries
   if constexpr (RANS) {
-    const uint2 *tk = reinterpret_cast<const uint2 *>(d.tables + static_cast<size_t>(2 * head) * CF_KV_RANS_TABLE_BYTES);
-    for (uint32_t i = threadIdx.x; i < 2 * kSlots; i += kThreads) {
-      const uint2 e = tk[i];  // K table then V table (adjacent blobs)
-      s_tab[i / kSlots][i % kSlots] = uint2{(e.x & 2047u) | (((e.x >> 11) & 2047u) << 16), e.y};
+    // K table then V table (adjacent blobs), two entries per 16-byte load; every load of a thread is issued before
+    // its first LDS write (one memory latency instead of one per loop step; the tail loads repeat the last pair)
+    const uint4 *tk = reinterpret_cast<const uint4 *>(d.tables + static_cast<size_t>(2 * head) * CF_KV_RANS_TABLE_BYTES);
+    constexpr uint32_t kPairs = kSlots;  // 2 * kSlots entries
+    constexpr int kIt = static_cast<int>((kPairs + kThreads - 1) / kThreads);
+    uint4 e[kIt];
+#pragma unroll
+    for (int k = 0; k < kIt; ++k) e[k] = tk[min(threadIdx.x + static_cast<uint32_t>(k * kThreads), kPairs - 1)];
+#pragma unroll
+    for (int k = 0; k < kIt; ++k) {
+      const uint32_t i = threadIdx.x + static_cast<uint32_t>(k * kThreads), j = 2 * i;
+      if (i < kPairs)
+        *reinterpret_cast<uint4 *>(&s_tab[j / kSlots][j % kSlots]) =
+            uint4{(e[k].x & 2047u) | (((e[k].x >> 11) & 2047u) << 16), e[k].y,
+                  (e[k].z & 2047u) | (((e[k].z >> 11) & 2047u) << 16), e[k].w};
     }
   }
   for (int i = threadIdx.x; i < kGqa * D; i += kThreads) {
@@ -976,7 +988,7 @@ __global__ __launch_bounds__(kRouteChunk) void seam_list_kernel(cf_kv_paged_atte
     vl = reinterpret_cast<uintptr_t>(pg.v_lut);
     const bool rans = pg.fixed_code_length == 0 && pg.k_max_code_length == 0;
     badp = !rans || pg.head_dim != d.head_dim || pg.token_count == 0 || pg.token_count > 64 || !pg.k_words || !kl ||
-           !vl;
+           !vl || ((kl | vl) & 15u) != 0;  // tables staged by 16-byte loads
   }
   __syncthreads();
   const bool mine_ok = hp < H;
@@ -1044,7 +1056,7 @@ __global__ CF_KV_OCC __launch_bounds__(64 * kWavesNarrow) void seam_group_kernel
                                                                        uint32_t *__restrict__ taken,
                                                                        float *__restrict__ partial) {
   constexpr int W = kWavesNarrow, NQ = D / 4, RAW = raw_words<D>(), BUF = buf_u32<D>(), kThreads = 64 * W;
-  __shared__ uint2 s_tab[2][kSlots];
+  __shared__ __attribute__((aligned(16))) uint2 s_tab[2][kSlots];
   __shared__ __attribute__((aligned(16))) _Float16 s_p[W][2][4][kGqa][16];
   __shared__ uint32_t s_buf[W][BUF];  // per wave: staged words; query staging and partials alias it
   // (no other shared variable: with 53,760 bytes or less three workgroups fit a CU)
@@ -1089,12 +1101,24 @@ __global__ CF_KV_OCC __launch_bounds__(64 * kWavesNarrow) void seam_group_kernel
   }
   const uint32_t *list = lists + static_cast<size_t>(head) * d.page_count;
   const uint32_t cexc = cinc - ccount;
-  {  // the head's tables (every listed page has these), as the decoder reads them
-    const uint2 *tk = reinterpret_cast<const uint2 *>(tkl), *tv = reinterpret_cast<const uint2 *>(tvl);
-    for (uint32_t i = threadIdx.x; i < kSlots; i += kThreads) {
-      const uint2 a = tk[i], b = tv[i];
-      s_tab[0][i] = uint2{(a.x & 2047u) | (((a.x >> 11) & 2047u) << 16), a.y};
-      s_tab[1][i] = uint2{(b.x & 2047u) | (((b.x >> 11) & 2047u) << 16), b.y};
+  {  // the head's tables (every listed page has these), as the decoder reads them: two entries per 16-byte load,
+     // all of a thread's loads issued before its first LDS write
+    constexpr int kIt = static_cast<int>(kSlots / 2 / kThreads);
+    static_assert(kIt * kThreads * 2 == static_cast<int>(kSlots), "whole 16-byte pairs per thread");
+    const uint4 *tk = reinterpret_cast<const uint4 *>(tkl), *tv = reinterpret_cast<const uint4 *>(tvl);
+    uint4 a[kIt], b[kIt];
+#pragma unroll
+    for (int k = 0; k < kIt; ++k) {
+      a[k] = tk[threadIdx.x + k * kThreads];
+      b[k] = tv[threadIdx.x + k * kThreads];
+    }
+#pragma unroll
+    for (int k = 0; k < kIt; ++k) {
+      const uint32_t j = 2 * (threadIdx.x + k * kThreads);
+      *reinterpret_cast<uint4 *>(&s_tab[0][j]) = uint4{(a[k].x & 2047u) | (((a[k].x >> 11) & 2047u) << 16), a[k].y,
+                                                       (a[k].z & 2047u) | (((a[k].z >> 11) & 2047u) << 16), a[k].w};
+      *reinterpret_cast<uint4 *>(&s_tab[1][j]) = uint4{(b[k].x & 2047u) | (((b[k].x >> 11) & 2047u) << 16), b[k].y,
+                                                       (b[k].z & 2047u) | (((b[k].z >> 11) & 2047u) << 16), b[k].w};
     }
   }
   static_assert(2 * kGqa * D * 2 <= W * BUF * 4, "query staging must fit the word buffers");
@@ -1363,6 +1387,9 @@ extern "C" cf_status cf_kv_validate_batched_desc(const cf_kv_batched_desc *d) {
     return CF_ERR_INVALID_ARGUMENT;
   if (d->codec != CF_KV_CODEC_INT8 && d->codec != CF_KV_CODEC_RANS_HYBRID) return CF_ERR_UNSUPPORTED;
   if (d->codec == CF_KV_CODEC_RANS_HYBRID && !d->tables) return CF_ERR_INVALID_ARGUMENT;
+  // blobs are copied in 16-byte chunks and tables read two entries per 16-byte load
+  if ((reinterpret_cast<uintptr_t>(d->pool) & 15u) != 0 || (reinterpret_cast<uintptr_t>(d->tables) & 15u) != 0)
+    return CF_ERR_INVALID_ARGUMENT;
   if (d->query_head_count / d->kv_head_count > kGqa) return CF_ERR_UNSUPPORTED;
   if (d->head_dim != 64 && d->head_dim != 128) return CF_ERR_UNSUPPORTED;
   if (d->seq_count > 65535 || d->kv_head_count > 65535) return CF_ERR_UNSUPPORTED;

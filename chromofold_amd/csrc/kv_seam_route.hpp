@@ -6,7 +6,8 @@
 // page's two rANS chains one after another with nothing to overlap them. The route instead:
 //   1. seam_list_kernel: one workgroup per chunk of 256 descriptors lists, for every KV head, the head's pages of
 //      the chunk in descriptor order and records per (head, chunk) the page count, whether every such page is a
-//      rANS page (the seam's tag) of the call's head_dim with 1..64 tokens, and the K/V table pointers of the first;
+//      rANS page (the seam's tag) of the call's head_dim with 1..64 tokens and 16-byte aligned tables, and the K/V
+//      table pointers of the first;
 //   2. seam_group_kernel: each workgroup combines its head's chunk records (the route takes the head when every
 //      page qualifies and all share one pair of K/V tables; the first split's workgroup publishes the verdict); for
 //      a head it takes, each wavefront decodes whole pages with the batched decode's group body (both chains

@@ -131,7 +131,7 @@ typedef struct cf_kv_batched_desc {
     const uint32_t *group_offsets;
     const uint32_t *seq_tokens;
     const uint32_t *query_pos;
-    const uint8_t *tables;       /* RANS_HYBRID: table blobs, CF_KV_RANS_TABLE_BYTES each */
+    const uint8_t *tables;       /* RANS_HYBRID: table blobs, CF_KV_RANS_TABLE_BYTES each, 16-byte aligned */
     const float *queries;
     float *output;
     float softmax_scale;
@@ -143,7 +143,8 @@ typedef struct cf_kv_batched_desc {
 /* Bytes of workspace the launch needs for this descriptor (0 when no split is used). Host only. */
 uint64_t cf_kv_batched_workspace_bytes(const cf_kv_batched_desc *desc);
 
-/* Host-only validation of a batched descriptor (no device dereference). */
+/* Host-only validation of a batched descriptor (no device dereference). A pool or table pointer that is not
+ * 16-byte aligned is CF_ERR_INVALID_ARGUMENT. */
 cf_status cf_kv_validate_batched_desc(const cf_kv_batched_desc *desc);
 
 /* Batched paged attention decode over INT8 or RANS_HYBRID pages. No counterpart in the reference (see above);

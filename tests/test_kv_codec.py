@@ -245,6 +245,30 @@ def test_device_encoder_rejects_bad_arguments_before_any_device_call(kv):
     assert call(D=20) == 2 and call(D=256) == 2 and call(codec=7) == 2
 
 
+def test_batched_desc_validation(kv):
+    """cf_kv_validate_batched_desc is host-only (fake, never dereferenced addresses): a well-formed descriptor is
+    accepted; NULL pointers, a RANS_HYBRID descriptor without tables, pool or table pointers off 16-byte alignment,
+    and heads or head_dims the kernels do not take are refused."""
+    import ctypes as C
+    L = kv.A.lib()
+    A = 1 << 20
+
+    def desc(**kw):
+        d = kv.cf_kv_batched_desc()
+        d.struct_size, d.abi_version, d.codec = C.sizeof(kv.cf_kv_batched_desc), kv.EXT_ABI_VERSION, 2
+        d.seq_count, d.kv_head_count, d.query_head_count, d.head_dim, d.max_groups = 2, 8, 32, 128, 4
+        d.pool = d.group_offsets = d.seq_tokens = d.query_pos = d.tables = d.queries = d.output = A
+        d.softmax_scale = 0.125
+        for k, v in kw.items():
+            setattr(d, k, v)
+        return L.cf_kv_validate_batched_desc(C.byref(d))
+
+    assert desc() == 0 and desc(codec=1, tables=None) == 0
+    assert desc(pool=None) == 1 and desc(tables=None) == 1 and desc(queries=None) == 1
+    assert desc(pool=A + 8) == 1 and desc(tables=A + 4) == 1 and desc(tables=A + 8) == 1
+    assert desc(query_head_count=40) == 2 and desc(head_dim=96) == 2 and desc(codec=3) == 2
+
+
 def test_mixed_pool_raw_prefix(kv):
     """build_batched(raw_groups=...) on the host: a sequence's leading groups are INT8 blobs inside a RANS_HYBRID
     pool. Every group decodes (oracle decoder) to the same symbols and scales as in an all-INT8 and an all-rANS pool,
