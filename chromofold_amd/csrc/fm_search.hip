@@ -252,8 +252,14 @@ __device__ __forceinline__ void lines_step(const cf_fm_view &v, const LinesArgs 
   const int L = LEVELS > 0 ? LEVELS : v.w.bits;
   uint32_t a = static_cast<uint32_t>(lo), b = static_cast<uint32_t>(hi);
   for (int lvl = 0; lvl < L; ++lvl) {
-    const int ra = cfl::rank1<false>(la.rec, la.nrec, lvl, a, nullptr);
-    const int rb = cfl::rank1<false>(la.rec, la.nrec, lvl, b, nullptr);
+    // both records' loads issued before either rank is counted (two latencies per level would serialise)
+    const uint32_t *lv = la.rec + static_cast<size_t>(lvl) * la.nrec * cfl::kRecWords;
+    const uint32_t ra_rec = min(a / cfl::kLineBits, la.nrec - 1u), rb_rec = min(b / cfl::kLineBits, la.nrec - 1u);
+    uint32_t wa[16], wb[16];
+    cfl::load_record(lv + ra_rec * cfl::kRecWords, wa);
+    cfl::load_record(lv + rb_rec * cfl::kRecWords, wb);
+    const int ra = cfl::record_rank<false>(wa, a - ra_rec * cfl::kLineBits, nullptr);
+    const int rb = cfl::record_rank<false>(wb, b - rb_rec * cfl::kLineBits, nullptr);
     if ((c >> (L - 1 - lvl)) & 1) {
       const uint32_t z = static_cast<uint32_t>(v.w.zeros[lvl]);
       a = z + ra;
