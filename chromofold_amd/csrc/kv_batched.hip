@@ -965,10 +965,12 @@ static_assert(CF_KV_CUDA_MAX_PAGES_PER_LAUNCH / kRouteChunk <= 64, "a wavefront 
 // heads present among its 64 descriptors (one ballot per head) and notes per (head, wavefront) the match count,
 // whether a match is refused or names other tables than the wavefront's first match, and those tables; thread h
 // then combines the four wavefronts of head h into the (head, chunk) record and the wavefronts' offsets, and every
-// thread writes its descriptor index to lists[kv_head][256 chunk + offset] (descriptor order within the chunk).
+// thread writes its page's entry to lists[kv_head][256 chunk + offset] (descriptor order within the chunk): the
+// blob pointer's two halves, token_begin and token_count, so that the group kernel reads one 16-byte entry per page
+// instead of an index and then the descriptor.
 // Descriptors whose kv_head is not below the call's KV head count belong to no head (the seam kernel skips them).
 __global__ __launch_bounds__(kRouteChunk) void seam_list_kernel(cf_kv_paged_attention_desc d,
-                                                                uint32_t *__restrict__ lists,
+                                                                uint4 *__restrict__ lists,
                                                                 uint32_t *__restrict__ info) {
   constexpr unsigned W = kRouteChunk / 64;
   static_assert(kRouteMaxHeads * W == kRouteChunk, "one counter per thread to clear");
@@ -978,12 +980,15 @@ __global__ __launch_bounds__(kRouteChunk) void seam_list_kernel(cf_kv_paged_atte
   const uint32_t chunk = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
   const uint32_t H = d.kv_head_count, p = chunk * kRouteChunk + t;
   s_cnt[t / W][t % W] = 0;
-  uint32_t hp = 0xFFFFFFFFu;
-  uint64_t kl = 0, vl = 0;
+  uint32_t hp = 0xFFFFFFFFu, tbeg = 0, tcnt = 0;
+  uint64_t kl = 0, vl = 0, kw = 0;
   bool badp = false;
   if (p < d.page_count) {
     const cf_kv_device_page &pg = d.pages[p];
     hp = pg.kv_head;
+    tbeg = pg.token_begin;
+    tcnt = pg.token_count;
+    kw = reinterpret_cast<uintptr_t>(pg.k_words);
     kl = reinterpret_cast<uintptr_t>(pg.k_lut);
     vl = reinterpret_cast<uintptr_t>(pg.v_lut);
     const bool rans = pg.fixed_code_length == 0 && pg.k_max_code_length == 0;
@@ -1037,7 +1042,8 @@ __global__ __launch_bounds__(kRouteChunk) void seam_list_kernel(cf_kv_paged_atte
   if (mine_ok)
     lists[static_cast<size_t>(hp) * d.page_count + chunk * kRouteChunk + s_cnt[hp][wave] +
           __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mine >> 32),
-                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mine), 0u))] = p;
+                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mine), 0u))] =
+        uint4{static_cast<uint32_t>(kw), static_cast<uint32_t>(kw >> 32), tbeg, tcnt};
 }
 
 // One (context split, KV head) per 4-wavefront workgroup. Each wavefront reads the head's chunk records (lane c:
@@ -1052,7 +1058,7 @@ __global__ __launch_bounds__(kRouteChunk) void seam_list_kernel(cf_kv_paged_atte
 template <int D>
 __global__ CF_KV_OCC __launch_bounds__(64 * kWavesNarrow) void seam_group_kernel(cf_kv_paged_attention_desc d, uint32_t splits,
                                                                        const uint32_t *__restrict__ info,
-                                                                       const uint32_t *__restrict__ lists,
+                                                                       const uint4 *__restrict__ lists,
                                                                        uint32_t *__restrict__ taken,
                                                                        float *__restrict__ partial) {
   constexpr int W = kWavesNarrow, NQ = D / 4, RAW = raw_words<D>(), BUF = buf_u32<D>(), kThreads = 64 * W;
@@ -1099,7 +1105,7 @@ __global__ CF_KV_OCC __launch_bounds__(64 * kWavesNarrow) void seam_group_kernel
     for (uint32_t i = threadIdx.x; i < gqa * (D + 2); i += kThreads) pp[i] = i % (D + 2) == D ? -INFINITY : 0.0f;
     return;
   }
-  const uint32_t *list = lists + static_cast<size_t>(head) * d.page_count;
+  const uint4 *list = lists + static_cast<size_t>(head) * d.page_count;
   const uint32_t cexc = cinc - ccount;
   {  // the head's tables (every listed page has these), as the decoder reads them: two entries per 16-byte load,
      // all of a thread's loads issued before its first LDS write
@@ -1170,12 +1176,22 @@ __global__ CF_KV_OCC __launch_bounds__(64 * kWavesNarrow) void seam_group_kernel
   bool bad = false;
   uint32_t pre[14];
   auto noop = []() {};
-  for (uint32_t o = split + splits * static_cast<uint32_t>(wave); o < n; o += splits * W) {
+  // the page entry of ordinal o (wave-uniform: a scalar load), the next one loaded while the current page is decoded
+  auto entry_of = [&](uint32_t o) {
     const uint32_t oc = static_cast<uint32_t>(__builtin_popcountll(__builtin_amdgcn_ballot_w64(cinc <= o)));
-    const cf_kv_device_page &pg = d.pages[list[oc * kRouteChunk + o - __shfl(cexc, static_cast<int>(oc))]];
-    const uint32_t tb = pg.token_begin, tcnt = pg.token_count;
+    const uint32_t li = __builtin_amdgcn_readfirstlane(oc * kRouteChunk + o - __shfl(cexc, static_cast<int>(oc)));
+    return list[li];
+  };
+  const uint32_t ostep = splits * static_cast<uint32_t>(W);
+  uint32_t o = split + splits * static_cast<uint32_t>(wave);
+  uint4 ent = o < n ? entry_of(o) : uint4{0, 0, 0, 0};
+  for (uint32_t on; o < n; o = on) {
+    on = o + ostep;
+    const uint4 e = ent;
+    if (on < n) ent = entry_of(on);
+    const uint32_t tb = e.z, tcnt = e.w;
     if (tb > qtok || tb + tcnt <= wlo) continue;  // wholly outside the visible range: skipped unread
-    const uint8_t *blob = reinterpret_cast<const uint8_t *>(pg.k_words);
+    const uint8_t *blob = reinterpret_cast<const uint8_t *>(e.x | (static_cast<uint64_t>(e.y) << 32));
     const uint32_t codec = *reinterpret_cast<const uint32_t *>(blob);
     const uint32_t cnt = *reinterpret_cast<const uint32_t *>(blob + 4);
     const uint32_t chain = *reinterpret_cast<const uint16_t *>(blob + 8);
@@ -1533,15 +1549,15 @@ uint32_t seam_route_splits(const cf_kv_paged_attention_desc &d) {
 
 uint64_t seam_route_scratch_words(const cf_kv_paged_attention_desc &d) {
   const uint64_t h = d.kv_head_count;
-  return h * seam_route_chunks(d.page_count) * kRouteInfoWords + h + h * d.page_count;
+  return h * seam_route_chunks(d.page_count) * kRouteInfoWords + 4 * h * d.page_count + h;
 }
 
 cf_status seam_route_launch(const cf_kv_paged_attention_desc &d, uint32_t splits, float *partial, uint32_t *scratch,
                             hipStream_t s) {
   const uint32_t chunks = seam_route_chunks(d.page_count);
   uint32_t *info = scratch;
-  uint32_t *taken = info + static_cast<uint64_t>(d.kv_head_count) * chunks * kRouteInfoWords;
-  uint32_t *lists = taken + d.kv_head_count;
+  uint4 *lists = reinterpret_cast<uint4 *>(info + static_cast<uint64_t>(d.kv_head_count) * chunks * kRouteInfoWords);
+  uint32_t *taken = reinterpret_cast<uint32_t *>(lists + static_cast<uint64_t>(d.kv_head_count) * d.page_count);
   if ((reinterpret_cast<uintptr_t>(scratch) & 15u) != 0 || chunks > 64) return CF_ERR_INVALID_ARGUMENT;
   seam_list_kernel<<<chunks, kRouteChunk, 0, s>>>(d, lists, info);
   const dim3 grid(splits, d.kv_head_count);

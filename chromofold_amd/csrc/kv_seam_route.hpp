@@ -47,15 +47,16 @@ cf_status seam_paged_attention(const cf_kv_paged_attention_desc *desc, void *str
 bool seam_route_applies(const cf_kv_paged_attention_desc &d);
 // Context splits the route uses per KV head.
 uint32_t seam_route_splits(const cf_kv_paged_attention_desc &d);
-// Scratch (u32 words) the route needs: records [kv_heads][chunks][8], taken [kv_heads], lists
-// [kv_heads][page_count] (chunk c's pages of a head from c * 256). The scratch is 16-byte aligned.
+// Scratch (u32 words) the route needs: records [kv_heads][chunks][8], lists [kv_heads][page_count] of 16-byte page
+// entries (chunk c's pages of a head from c * 256), taken [kv_heads]. The scratch is 16-byte aligned.
 uint64_t seam_route_scratch_words(const cf_kv_paged_attention_desc &d);
 // Launches steps 1 and 2 on `s`. `taken` (inside `scratch`) is what the seam kernel then reads.
 cf_status seam_route_launch(const cf_kv_paged_attention_desc &d, uint32_t splits, float *partial, uint32_t *scratch,
                             hipStream_t s);
 // The per-head "taken" flags inside the scratch.
 inline const uint32_t *seam_route_taken(const cf_kv_paged_attention_desc &d, const uint32_t *scratch) {
-  return scratch + static_cast<uint64_t>(d.kv_head_count) * seam_route_chunks(d.page_count) * kRouteInfoWords;
+  const uint64_t h = d.kv_head_count;
+  return scratch + h * seam_route_chunks(d.page_count) * kRouteInfoWords + 4 * h * d.page_count;
 }
 
 }  // namespace cfkv
