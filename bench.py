@@ -589,6 +589,9 @@ def bench_gather(steps: int, warmup: int, dim: int = 128, nq: int = 1 << 20) -> 
         A.check(L.cf_sparse_gather_fused_async(v, emb.data_ptr(), dim, dpos.data_ptr(), out.data_ptr(), nq, s),
                 "cf_sparse_gather_fused_async")
 
+    def fused_lines():
+        idx.gather_fused_lines_into(emb, dpos, out, stream=torch.cuda.current_stream())
+
     def via_ids():
         A.check(L.cf_sparse_gather_async(ids.data_ptr(), emb.data_ptr(), dim, dpos.data_ptr(), out.data_ptr(), nq, s),
                 "cf_sparse_gather_async")
@@ -599,17 +602,24 @@ def bench_gather(steps: int, warmup: int, dim: int = 128, nq: int = 1 << 20) -> 
     ref = emb[torch.from_numpy(tok[pos[chk]].astype(np.int64)).to("cuda:0")]
     assert torch.equal(out[torch.from_numpy(chk).to("cuda:0")], ref), "fused gather != emb[tok[pos]]"
     _, per_f = _events_time(fused, steps, warmup)
+    out.fill_(float("nan"))
+    fused_lines()
+    torch.cuda.synchronize()
+    assert torch.equal(out[torch.from_numpy(chk).to("cuda:0")], ref), "fused gather (lines) != emb[tok[pos]]"
+    _, per_fl = _events_time(fused_lines, steps, warmup)
     A.check(L.cf_sparse_decode_all_async(v, ids.data_ptr(), n, s), "cf_sparse_decode_all_async")
     _, per_d = _events_time(lambda: A.check(L.cf_sparse_decode_all_async(v, ids.data_ptr(), n, s), "decode_all"),
                             steps, warmup)
     _, per_g = _events_time(via_ids, steps, warmup)
     torch.cuda.synchronize()
     assert torch.equal(out[torch.from_numpy(chk).to("cuda:0")], ref), "gather via ids != emb[tok[pos]]"
-    tf, td, tg = (float(np.mean(p)) * 1e-3 for p in (per_f, per_d, per_g))
+    tf, tfl, td, tg = (float(np.mean(p)) * 1e-3 for p in (per_f, per_fl, per_d, per_g))
     step_bytes = nq * 4 + nq * dim * 4
     return {"workload": f"{nq} positions into the C1 index, rows of {dim} fp32 from a {vocab}-row table",
             "fused_ms": tf * 1e3, "fused_mqs": nq / tf / 1e6, "fused_gbs": step_bytes / tf / 1e9,
             "fused_roofline_frac": step_bytes / tf / 1e9 / HBM_PEAK_GBS,
+            "fused_lines_ms": tfl * 1e3, "fused_lines_gbs": step_bytes / tfl / 1e9,
+            "fused_lines_roofline_frac": step_bytes / tfl / 1e9 / HBM_PEAK_GBS,
             "decode_all_ms": td * 1e3, "gather_via_ids_ms": tg * 1e3,
             "decode_all_plus_gather_ms": (td + tg) * 1e3}
 

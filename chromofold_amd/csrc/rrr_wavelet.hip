@@ -17,6 +17,7 @@
 #include "cf_device.hpp"
 #include "rrr_core.hpp"
 #include "lines_core.hpp"
+#include "gather_core.hpp"
 #include "chromofold/chromofold_index.h"
 
 namespace {
@@ -89,6 +90,28 @@ __global__ __launch_bounds__(kThreads) void rrrw_access_lines_kernel(cf_rrrw_vie
   out[t] = val;
 }
 
+// cf_sparse_gather_fused_async over the line layout: lane = query (its access walk, one record per level), then the
+// wave copies its 64 rows (gather_core.hpp).
+template <int LEVELS, bool VEC>
+__global__ __launch_bounds__(kThreads) void sparse_fused_lines_kernel(cf_rrrw_view v, const uint32_t *__restrict__ lines,
+                                                                      uint32_t nrec, const float *__restrict__ emb,
+                                                                      int dim, const uint32_t *__restrict__ pos,
+                                                                      float *__restrict__ out, size_t count) {
+  const size_t q0 = (blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x) & ~size_t(63);
+  if (q0 >= count) return;  // wave-uniform
+  const size_t t = q0 + (threadIdx.x & 63u);
+  const int L = LEVELS > 0 ? LEVELS : v.bits;
+  uint32_t a = t < count ? pos[t] : 0u, id = 0;
+  for (int lvl = 0; lvl < L; ++lvl) {
+    int bit;
+    const int r = cfl::rank1<true>(lines, nrec, lvl, a, &bit);
+    id = (id << 1) | static_cast<uint32_t>(bit);
+    a = bit ? static_cast<uint32_t>(v.zeros[lvl] + r) : a - static_cast<uint32_t>(r);
+  }
+  const int nq = static_cast<int>(count - q0 < 64 ? count - q0 : 64);
+  cfg::copy_rows<VEC>(id, nq, emb, static_cast<uint64_t>(dim), out, q0);
+}
+
 template <int LEVELS>
 __global__ __launch_bounds__(kThreads) void rrrw_rank_lines_kernel(cf_rrrw_view v, const uint32_t *__restrict__ lines,
                                                                    uint32_t nrec, const uint32_t *__restrict__ sym,
@@ -144,6 +167,25 @@ extern "C" cf_status cf_rrrw_access_lines_async(cf_rrrw_view v, const uint32_t *
     case 16: rrrw_access_lines_kernel<16><<<g, kThreads, 0, s>>>(v, lines, nrec, positions, out, count); break;
     default: rrrw_access_lines_kernel<0><<<g, kThreads, 0, s>>>(v, lines, nrec, positions, out, count); break;
   }
+  return cfd::launch_status();
+}
+
+extern "C" cf_status cf_sparse_gather_fused_lines_async(cf_rrrw_view v, const uint32_t *lines, const float *emb,
+                                                        int dim, const uint32_t *pos, float *out, size_t count,
+                                                        void *stream) {
+  if (!rrrw_lines_ok(v, lines) || !emb || !pos || !out) return CF_ERR_INVALID_ARGUMENT;
+  if (count == 0 || dim <= 0) return CF_OK;
+  const hipStream_t s = cfd::as_stream(stream);
+  const unsigned g = cfd::grid_for(count, kThreads);
+  const uint32_t nrec = rrrw_nrec(v);
+  const bool vec = cfg::vec4_ok(emb, out, static_cast<uint64_t>(dim));
+#define CF_FUSED(L, V) sparse_fused_lines_kernel<L, V><<<g, kThreads, 0, s>>>(v, lines, nrec, emb, dim, pos, out, count)
+  switch (v.bits) {
+    case 15: if (vec) CF_FUSED(15, true); else CF_FUSED(15, false); break;
+    case 16: if (vec) CF_FUSED(16, true); else CF_FUSED(16, false); break;
+    default: if (vec) CF_FUSED(0, true); else CF_FUSED(0, false); break;
+  }
+#undef CF_FUSED
   return cfd::launch_status();
 }
 

@@ -113,6 +113,14 @@ class RrrWaveletIndex:
                                                  _ptr(positions), _ptr(out), positions.numel(), stream_ptr(stream)),
                 "cf_rrrw_rank_lines_async")
 
+    def gather_fused_lines_into(self, emb: torch.Tensor, positions: torch.Tensor, out: torch.Tensor,
+                                stream=None) -> None:
+        """out[t, :] = emb[access(positions[t]), :] (cf_sparse_gather_fused_lines_async)."""
+        A.check(A.lib().cf_sparse_gather_fused_lines_async(self.view(), _ptr(self.build_lines(stream)), _ptr(emb),
+                                                           emb.shape[1], _ptr(positions), _ptr(out), positions.numel(),
+                                                           stream_ptr(stream)),
+                "cf_sparse_gather_fused_lines_async")
+
     def rank(self, symbols: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
         out = torch.empty_like(positions, dtype=torch.int32)
         self.rank_into(symbols, positions, out)
@@ -241,6 +249,7 @@ A.declare("cf_rrrw_lines_bytes", A.U64, [A.cf_rrrw_view])
 A.declare("cf_rrrw_lines_build_async", A.I32, [A.cf_rrrw_view, A.P, A.U64, A.P])
 A.declare("cf_rrrw_access_lines_async", A.I32, [A.cf_rrrw_view, A.P, A.P, A.P, A.SZ, A.P])
 A.declare("cf_rrrw_rank_lines_async", A.I32, [A.cf_rrrw_view, A.P, A.P, A.P, A.P, A.SZ, A.P])
+A.declare("cf_sparse_gather_fused_lines_async", A.I32, [A.cf_rrrw_view, A.P, A.P, C.c_int, A.P, A.P, A.SZ, A.P])
 A.declare("cf_fm_lines_bytes", A.U64, [A.cf_fm_view])
 A.declare("cf_fm_lines_build_async", A.I32, [A.cf_fm_view, A.P, A.U64, A.P])
 A.declare("cf_fm_count_lines_async", A.I32, [A.cf_fm_view, A.P, A.P, A.P, A.P, A.P, A.SZ, A.P])

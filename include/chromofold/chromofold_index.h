@@ -91,6 +91,11 @@ cf_status cf_rrrw_access_lines_async(cf_rrrw_view v, const uint32_t *lines, cons
                                      size_t count, void *stream);
 cf_status cf_rrrw_rank_lines_async(cf_rrrw_view v, const uint32_t *lines, const uint32_t *symbols,
                                    const uint32_t *positions, uint32_t *out, size_t count, void *stream);
+/* cf_sparse_gather_fused_async (chromofold_extra.h, reference src/cuda/sparse_gather.cu:55-66) over the line layout:
+ * out[t, :] = emb[access(pos[t]), :] for t < count, the same bytes, each query's access walk reading one 64-byte
+ * line per level. Same argument rules (count 0 or dim <= 0: nothing to do). */
+cf_status cf_sparse_gather_fused_lines_async(cf_rrrw_view v, const uint32_t *lines, const float *emb, int dim,
+                                             const uint32_t *pos, float *out, size_t count, void *stream);
 
 /* ---- derived on-device line layout for FM search (no counterpart in the reference; the .cffm on disk and the
  * cf_fm_view arrays are unchanged). Built once per loaded index from its cf_fm_view; the search entry points below

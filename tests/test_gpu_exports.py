@@ -180,7 +180,9 @@ def test_rrr_sparse_gathers(dev, bits, n):
     _ok(_lib().cf_sparse_decode_all_async(v, ids.data_ptr(), n, None), "decode_all")
     assert np.array_equal(_np(ids, np.uint32), tok)
     V = 1 << bits
-    for dim, K in ((32, 700), (5, 200)):
+    # row lengths: 16-byte rows of 8 and 32 units, float rows of 5 units (one unit per lane and pass) and of 300
+    # units (several per lane)
+    for dim, K in ((32, 700), (5, 200), (128, 333), (300, 130)):
         E = rng.standard_normal((V, dim)).astype(np.float32)
         dE = torch.from_numpy(E).to(dev)
         pos = rng.integers(0, n, K).astype(np.uint32)
@@ -188,6 +190,9 @@ def test_rrr_sparse_gathers(dev, bits, n):
         g = torch.full((K, dim), float("nan"), device=dev)
         _ok(_lib().cf_sparse_gather_fused_async(v, dE.data_ptr(), dim, dp.data_ptr(), g.data_ptr(), K, None), "fused")
         assert np.array_equal(g.cpu().numpy(), E[tok[pos]])
+        g3 = torch.full((K, dim), float("nan"), device=dev)
+        idx.gather_fused_lines_into(dE, dp, g3)  # the same gather over the line layout
+        assert np.array_equal(g3.cpu().numpy(), E[tok[pos]])
         g2 = torch.full((K, dim), float("nan"), device=dev)
         _ok(_lib().cf_sparse_gather_async(ids.data_ptr(), dE.data_ptr(), dim, dp.data_ptr(), g2.data_ptr(), K, None),
             "gather")
