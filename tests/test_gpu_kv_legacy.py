@@ -434,3 +434,55 @@ def test_decode_route_refused_pages_nan(dev):
         got, ref = _run_shared(dev, deq, bad, q, kvh, gqa, T - 1, 0.125)
         assert np.isnan(got[:, :gqa]).all(), how                      # KV head 0: the refused page
         assert np.abs(got[:, gqa:] - ref[:, gqa:]).max() <= ABS_TOL, how  # KV head 1: decoded normally
+
+
+def test_decode_route_many_heads_full_page_list(dev):
+    """The route at its limits: 64 KV heads (the most it serves) x 64 rANS pages = 4096 descriptors (the seam's
+    per-launch limit), so every one of the 16 list workgroups sees all 64 heads and every head's pages span all 16
+    chunk records; plus a descriptor whose kv_head lies past the call's KV heads, which the route and the seam
+    kernel both leave out. Against the fp64 oracle, which only ever reads pages of the call's heads."""
+    import copy
+    rng = np.random.default_rng(7300)
+    hd, gqa, kvh, T = 64, 1, 64, 4096
+    pages, deq = _route_case(rng, kvh, hd, T)
+    assert len(pages) == 4096
+    q = rng.standard_normal((1, kvh * gqa, hd)).astype(np.float32)
+    got, ref = _run_shared(dev, deq, pages, q, kvh, gqa, T - 1, 0.125)
+    assert np.isfinite(got).all()
+    assert np.abs(got - ref).max() <= ABS_TOL
+    stray = copy.copy(pages[5])
+    stray.kv_head = kvh  # not a KV head of this call
+    more = pages[:100] + [stray] + pages[100:-1]  # 4096 descriptors again; the dropped page's head loses a page
+    kept = [d for d in deq if not (d[0] == pages[-1].kv_head and d[1] == pages[-1].token_begin)]
+    got2, ref2 = _run_shared(dev, kept, more, q, kvh, gqa, T - 1, 0.125)
+    assert np.isfinite(got2).all()
+    assert np.abs(got2 - ref2).max() <= ABS_TOL
+
+
+def test_decode_route_unaligned_tables_fall_back(dev):
+    """Table pointers off 16-byte alignment: the route leaves the head to the seam kernel (which reads tables at
+    any 4-byte alignment), with the same results within the bar."""
+    import torch
+    from chromofold_amd.legacy import PagedKv
+    rng = np.random.default_rng(7400)
+    hd, gqa, kvh, T = 128, 4, 2, 512
+    pages, deq = _route_case(rng, kvh, hd, T)
+    q = rng.standard_normal((1, kvh * gqa, hd)).astype(np.float32)
+    got, ref = _run_shared(dev, deq, pages, q, kvh, gqa, T - 1, 0.125)
+    assert np.abs(got - ref).max() <= ABS_TOL
+    import ctypes as C
+    from chromofold_amd import _abi as A
+    pk = PagedKv(pages, str(dev), share_luts=True)
+    arr = (A.cf_kv_device_page * len(pages)).from_buffer_copy(pk.descs.cpu().numpy().tobytes())
+    copies = {}
+    for i, p in enumerate(pages):  # every table re-pointed 4 bytes into a copy of the same contents
+        for f in ("k_lut", "v_lut"):
+            a = np.ascontiguousarray(getattr(p, f)).view(np.int32)
+            key = a.tobytes()
+            if key not in copies:
+                copies[key] = torch.from_numpy(np.concatenate([[0], a]).astype(np.int32)).to(dev)
+            setattr(arr[i], f, copies[key].data_ptr() + 4)
+            assert getattr(arr[i], f) % 16 == 4
+    pk.descs = torch.from_numpy(np.frombuffer(bytes(arr), np.uint8).copy()).to(dev)
+    got2 = pk.attention(torch.from_numpy(q).to(dev), kvh, gqa, T - 1, 0.125).cpu().numpy()
+    assert np.abs(got2 - ref).max() <= ABS_TOL
