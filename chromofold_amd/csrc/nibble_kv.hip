@@ -430,10 +430,18 @@ __global__ __launch_bounds__(64) void nib_merge_kernel(const AttnItem *__restric
   const uint32_t D = sh.head_dim, stride = D + 4u;
   const float *row0 = ws + it.ws_offset + (uint64_t(qt) * sh.q_heads + qh) * stride;
   const uint64_t split_stride = uint64_t(it.q_tokens) * sh.q_heads * stride;
+  const uint32_t ns = it.nsplit;
+  constexpr uint32_t kB = 8;  // splits whose loads are in flight together
   float M = kNegInf;
-  for (uint32_t s = 0; s < it.nsplit; ++s) M = fmaxf(M, row0[s * split_stride + D]);
+  for (uint32_t s0 = 0; s0 < ns; s0 += kB) {  // the maxima, kB loads at a time (past the end: the last split again)
+    float mv[kB];
+#pragma unroll
+    for (uint32_t u = 0; u < kB; ++u) mv[u] = row0[min(s0 + u, ns - 1u) * split_stride + D];
+#pragma unroll
+    for (uint32_t u = 0; u < kB; ++u) M = fmaxf(M, mv[u]);
+  }
   float L = 0.0f, o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  // splits in ascending order (the same sums in the same order for any grouping); four splits' loads are issued
+  // splits in ascending order (the same sums in the same order for any grouping); kB splits' loads are issued
   // together so that their latencies overlap, and a split with nothing attended (m = -inf) changes nothing
   auto add = [&](float ms, float ls, const float (&v)[4]) {
     if (ms == kNegInf) return;
@@ -453,18 +461,13 @@ __global__ __launch_bounds__(64) void nib_merge_kernel(const AttnItem *__restric
     }
   };
   if (M != kNegInf) {
-    uint32_t s = 0;
-    for (; s + 4u <= it.nsplit; s += 4u) {
-      float ms[4], ls[4], v[4][4];
+    for (uint32_t s0 = 0; s0 < ns; s0 += kB) {
+      float ms[kB], ls[kB], v[kB][4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) load(s + u, ms[u], ls[u], v[u]);
+      for (uint32_t u = 0; u < kB; ++u) load(min(s0 + u, ns - 1u), ms[u], ls[u], v[u]);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) add(ms[u], ls[u], v[u]);
-    }
-    for (; s < it.nsplit; ++s) {
-      float ms, ls, v[4];
-      load(s, ms, ls, v);
-      add(ms, ls, v);
+      for (uint32_t u = 0; u < kB; ++u)
+        if (s0 + u < ns) add(ms[u], ls[u], v[u]);
     }
   }
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
