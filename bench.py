@@ -102,16 +102,30 @@ def bench_rrr(steps: int, warmup: int, cpu: bool = True) -> dict:
     idx.access_lines_into(dpos, out_l)
     assert np.array_equal(to_u32(out_l), tok[pos]), "line-layout access mismatch"
 
-    wall_r, per_r = _events_time(lambda: idx.rank_lines_into(dc, di, out_l), steps, warmup)
-    _, per_a = _events_time(lambda: idx.access_lines_into(dpos, out_l), steps, warmup)
+    # the derived 4-ary layout (built once at load): 8 records per query instead of 15; the C1 figures
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    idx.build_quads(n)
+    torch.cuda.synchronize()
+    t_quads = time.perf_counter() - t0
+    idx.rank_quads_into(dc, di, out_l)
+    assert np.array_equal(to_u32(out_l), rank_gpu), "4-ary layout rank != RRR rank"
+    idx.access_quads_into(dpos, out_l)
+    assert np.array_equal(to_u32(out_l), tok[pos]), "4-ary layout access mismatch"
+    wall_r, per_r = _events_time(lambda: idx.rank_quads_into(dc, di, out_l), steps, warmup)
+    _, per_a = _events_time(lambda: idx.access_quads_into(dpos, out_l), steps, warmup)
+    _, per_lr = _events_time(lambda: idx.rank_lines_into(dc, di, out_l), steps, warmup)
+    _, per_la = _events_time(lambda: idx.access_lines_into(dpos, out_l), steps, warmup)
     _, per_rr = _events_time(lambda: idx.rank_into(dc, di, out), steps, warmup)
     _, per_ra = _events_time(lambda: idx.access_into(dpos, out), steps, warmup)
-    t_rank, t_acc, t_rrank, t_racc = (float(np.mean(x)) * 1e-3 for x in (per_r, per_a, per_rr, per_ra))
-    # algorithmic bytes: line layout = 15 levels x one 64-B record per query (rank and access alike) + the query
-    # words + the result; RRR = 15 levels x 32 B per rank1 (samples 12 + class scan 16 + offset 4), 2 rank1 per level
-    # for rank (960 B), 1 for access (480 B)
-    bytes_rank = nq * (15 * 64 + 12.0)
-    bytes_acc = nq * (15 * 64 + 8.0)
+    t_rank, t_acc, t_lrank, t_lacc, t_rrank, t_racc = (float(np.mean(x)) * 1e-3 for x in
+                                                       (per_r, per_a, per_lr, per_la, per_rr, per_ra))
+    # algorithmic bytes: 4-ary layout = 8 levels x one 64-B record per query (rank and access alike) + the query
+    # words + the result; line layout = 15 levels x 64 B; RRR = 15 levels x 32 B per rank1 (samples 12 + class scan
+    # 16 + offset 4), 2 rank1 per level for rank (960 B), 1 for access (480 B)
+    L4 = (15 + 1) // 2
+    bytes_rank = nq * (L4 * 64 + 12.0)
+    bytes_acc = nq * (L4 * 64 + 8.0)
     res = {
         "rank_mqs": nq / t_rank / 1e6, "access_mqs": nq / t_acc / 1e6,
         "rank_ms": t_rank * 1e3, "access_ms": t_acc * 1e3,
@@ -120,6 +134,9 @@ def bench_rrr(steps: int, warmup: int, cpu: bool = True) -> dict:
                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": bytes_rank / t_rank / 1e9 / HBM_PEAK_GBS,
                           "traffic": None},
         "access_gbs": bytes_acc / t_acc / 1e9,
+        "lines_rank_mqs": nq / t_lrank / 1e6, "lines_access_mqs": nq / t_lacc / 1e6,
+        "lines_rank_ms": t_lrank * 1e3, "lines_access_ms": t_lacc * 1e3,
+        "quads_bytes": idx.quads.numel(), "quads_build_ms": t_quads * 1e3,
         "rrr_rank_mqs": nq / t_rrank / 1e6, "rrr_access_mqs": nq / t_racc / 1e6,
         "rrr_rank_ms": t_rrank * 1e3, "rrr_access_ms": t_racc * 1e3,
         "rrr_rank_gbs": 960.0 * nq / t_rrank / 1e9,

@@ -17,6 +17,7 @@
 #include "cf_device.hpp"
 #include "rrr_core.hpp"
 #include "lines_core.hpp"
+#include "quads_core.hpp"
 #include "gather_core.hpp"
 #include "chromofold/chromofold_index.h"
 
@@ -112,6 +113,41 @@ __global__ __launch_bounds__(kThreads) void sparse_fused_lines_kernel(cf_rrrw_vi
   cfg::copy_rows<VEC>(id, nq, emb, static_cast<uint64_t>(dim), out, q0);
 }
 
+// Access and rank over the 4-ary layout (quads_core.hpp): L4 records per query.
+template <int L4>
+__global__ __launch_bounds__(kThreads) void rrrw_access_quads_kernel(const uint32_t *__restrict__ quads, uint32_t nrec,
+                                                                     uint32_t nlev, const uint32_t *__restrict__ pos,
+                                                                     uint32_t *__restrict__ out, size_t count) {
+  const size_t t = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x;
+  if (t >= count) return;
+  const uint32_t L = L4 > 0 ? static_cast<uint32_t>(L4) : nlev;
+  const uint32_t *Z = quads + static_cast<size_t>(L) * nrec * cfq::kRecWords;
+  uint32_t a = pos[t], val = 0;
+  for (uint32_t l = 0; l < L; ++l) {
+    uint32_t d;
+    a = cfq::step<true>(quads, nrec, Z, l, a, 0u, &d);
+    val = (val << 2) | d;
+  }
+  out[t] = val;
+}
+
+template <int L4>
+__global__ __launch_bounds__(kThreads) void rrrw_rank_quads_kernel(const uint32_t *__restrict__ quads, uint32_t nrec,
+                                                                   uint32_t nlev, uint32_t mask,
+                                                                   const uint32_t *__restrict__ sym,
+                                                                   const uint32_t *__restrict__ pos,
+                                                                   uint32_t *__restrict__ out, size_t count) {
+  const size_t t = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x;
+  if (t >= count) return;
+  const uint32_t L = L4 > 0 ? static_cast<uint32_t>(L4) : nlev;
+  const uint32_t *Z = quads + static_cast<size_t>(L) * nrec * cfq::kRecWords;
+  const uint32_t c = sym[t] & mask;  // the RRR walk reads the symbol's low `bits` bits only
+  uint32_t a = pos[t];
+  for (uint32_t l = 0; l < L; ++l) a = cfq::step<false>(quads, nrec, Z, l, a, (c >> (2u * (L - 1u - l))) & 3u, nullptr);
+  const int32_t *base = reinterpret_cast<const int32_t *>(Z + 4u * L);
+  out[t] = static_cast<uint32_t>(static_cast<int32_t>(a) + base[c]);
+}
+
 template <int LEVELS>
 __global__ __launch_bounds__(kThreads) void rrrw_rank_lines_kernel(cf_rrrw_view v, const uint32_t *__restrict__ lines,
                                                                    uint32_t nrec, const uint32_t *__restrict__ sym,
@@ -167,6 +203,68 @@ extern "C" cf_status cf_rrrw_access_lines_async(cf_rrrw_view v, const uint32_t *
     case 16: rrrw_access_lines_kernel<16><<<g, kThreads, 0, s>>>(v, lines, nrec, positions, out, count); break;
     default: rrrw_access_lines_kernel<0><<<g, kThreads, 0, s>>>(v, lines, nrec, positions, out, count); break;
   }
+  return cfd::launch_status();
+}
+
+// ---- the 4-ary layout (quads_core.hpp): n is the sequence's length (the view does not hold it)
+static bool rrrw_ok(const cf_rrrw_view &v) {  // the arrays the binary access walk reads
+  return v.classes && v.offsets && v.rank_a && v.rank_d && v.off_a && v.off_d && v.offbase && v.zeros;
+}
+
+static bool quads_view_ok(const cf_rrrw_view &v, uint64_t n) {
+  return v.bits > 0 && v.bits <= kLinesMaxBits && v.nsb >= 0 && n < (uint64_t{1} << 31) &&
+         n <= static_cast<uint64_t>(v.nsb) * 960u;
+}
+
+extern "C" uint64_t cf_rrrw_quads_bytes(cf_rrrw_view v, uint64_t n) {
+  if (!quads_view_ok(v, n)) return 0;
+  return cfq::layout(v.bits, n, int32_t{1} << v.bits).bytes();
+}
+
+extern "C" uint64_t cf_rrrw_quads_workspace_bytes(cf_rrrw_view v, uint64_t n) {
+  if (!quads_view_ok(v, n)) return 0;
+  return cfq::workspace_bytes(n, cfq::nrec_for(n));
+}
+
+extern "C" cf_status cf_rrrw_quads_build_async(cf_rrrw_view v, uint64_t n, uint32_t *quads, uint64_t bytes,
+                                               void *workspace, uint64_t workspace_bytes, void *stream) {
+  if (!quads_view_ok(v, n) || !quads || (reinterpret_cast<uintptr_t>(quads) & 15u) != 0 || !workspace ||
+      (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0 || !rrrw_ok(v))
+    return CF_ERR_INVALID_ARGUMENT;
+  if (bytes < cf_rrrw_quads_bytes(v, n) || workspace_bytes < cf_rrrw_quads_workspace_bytes(v, n))
+    return CF_ERR_INVALID_ARGUMENT;
+  return cfq::build(v, n, int32_t{1} << v.bits, nullptr, quads, workspace, cfd::as_stream(stream));
+}
+
+extern "C" cf_status cf_rrrw_access_quads_async(cf_rrrw_view v, uint64_t n, const uint32_t *quads,
+                                                const uint32_t *positions, uint32_t *out, size_t count, void *stream) {
+  if (!quads_view_ok(v, n) || !quads || (reinterpret_cast<uintptr_t>(quads) & 15u) != 0 || !positions || !out)
+    return CF_ERR_INVALID_ARGUMENT;
+  if (count == 0) return CF_OK;
+  const hipStream_t s = cfd::as_stream(stream);
+  const unsigned g = cfd::grid_for(count, kThreads);
+  const uint32_t nrec = cfq::nrec_for(n), L4 = cfq::levels_for(v.bits);
+  if (L4 == 8)
+    rrrw_access_quads_kernel<8><<<g, kThreads, 0, s>>>(quads, nrec, L4, positions, out, count);
+  else
+    rrrw_access_quads_kernel<0><<<g, kThreads, 0, s>>>(quads, nrec, L4, positions, out, count);
+  return cfd::launch_status();
+}
+
+extern "C" cf_status cf_rrrw_rank_quads_async(cf_rrrw_view v, uint64_t n, const uint32_t *quads,
+                                              const uint32_t *symbols, const uint32_t *positions, uint32_t *out,
+                                              size_t count, void *stream) {
+  if (!quads_view_ok(v, n) || !quads || (reinterpret_cast<uintptr_t>(quads) & 15u) != 0 || !symbols || !positions ||
+      !out)
+    return CF_ERR_INVALID_ARGUMENT;
+  if (count == 0) return CF_OK;
+  const hipStream_t s = cfd::as_stream(stream);
+  const unsigned g = cfd::grid_for(count, kThreads);
+  const uint32_t nrec = cfq::nrec_for(n), L4 = cfq::levels_for(v.bits), mask = (1u << v.bits) - 1u;
+  if (L4 == 8)
+    rrrw_rank_quads_kernel<8><<<g, kThreads, 0, s>>>(quads, nrec, L4, mask, symbols, positions, out, count);
+  else
+    rrrw_rank_quads_kernel<0><<<g, kThreads, 0, s>>>(quads, nrec, L4, mask, symbols, positions, out, count);
   return cfd::launch_status();
 }
 

@@ -52,6 +52,8 @@ class RrrWaveletIndex:
     na: int
     tensors: dict
     lines: "torch.Tensor | None" = None  # the derived line layout, built on first use (build_lines)
+    quads: "torch.Tensor | None" = None  # the derived 4-ary layout (build_quads), over quads_n symbols
+    quads_n: int = 0
 
     @classmethod
     def from_host(cls, arrays, device="cuda") -> "RrrWaveletIndex":
@@ -112,6 +114,34 @@ class RrrWaveletIndex:
         A.check(A.lib().cf_rrrw_rank_lines_async(self.view(), _ptr(self.build_lines(stream)), _ptr(symbols),
                                                  _ptr(positions), _ptr(out), positions.numel(), stream_ptr(stream)),
                 "cf_rrrw_rank_lines_async")
+
+    # ---- the derived 4-ary layout (cf_rrrw_quads_*): same results, ceil(bits / 2) records per query
+    def build_quads(self, n: int, stream=None) -> torch.Tensor:
+        """Builds (once) the 4-ary layout of the matrix's n symbols."""
+        if self.quads is None or self.quads_n != n:
+            v = self.view()
+            L = A.lib()
+            nb, nw = int(L.cf_rrrw_quads_bytes(v, n)), int(L.cf_rrrw_quads_workspace_bytes(v, n))
+            if nb == 0:
+                raise A.CfError(A.CF_ERR_UNSUPPORTED, "cf_rrrw_quads_bytes")
+            dev = self.tensors["classes"].device
+            quads = torch.empty(nb, dtype=torch.uint8, device=dev)
+            ws = torch.empty(nw, dtype=torch.uint8, device=dev)
+            A.check(L.cf_rrrw_quads_build_async(v, n, _ptr(quads), nb, _ptr(ws), nw, stream_ptr(stream)),
+                    "cf_rrrw_quads_build_async")
+            torch.cuda.current_stream(dev).synchronize() if stream is None else stream.synchronize()  # ws is freed
+            self.quads, self.quads_n = quads, n
+        return self.quads
+
+    def access_quads_into(self, positions: torch.Tensor, out: torch.Tensor, stream=None) -> None:
+        A.check(A.lib().cf_rrrw_access_quads_async(self.view(), self.quads_n, _ptr(self.quads), _ptr(positions),
+                                                   _ptr(out), positions.numel(), stream_ptr(stream)),
+                "cf_rrrw_access_quads_async")
+
+    def rank_quads_into(self, symbols: torch.Tensor, positions: torch.Tensor, out: torch.Tensor, stream=None) -> None:
+        A.check(A.lib().cf_rrrw_rank_quads_async(self.view(), self.quads_n, _ptr(self.quads), _ptr(symbols),
+                                                 _ptr(positions), _ptr(out), positions.numel(), stream_ptr(stream)),
+                "cf_rrrw_rank_quads_async")
 
     def gather_fused_lines_into(self, emb: torch.Tensor, positions: torch.Tensor, out: torch.Tensor,
                                 stream=None) -> None:
@@ -249,6 +279,11 @@ A.declare("cf_rrrw_lines_bytes", A.U64, [A.cf_rrrw_view])
 A.declare("cf_rrrw_lines_build_async", A.I32, [A.cf_rrrw_view, A.P, A.U64, A.P])
 A.declare("cf_rrrw_access_lines_async", A.I32, [A.cf_rrrw_view, A.P, A.P, A.P, A.SZ, A.P])
 A.declare("cf_rrrw_rank_lines_async", A.I32, [A.cf_rrrw_view, A.P, A.P, A.P, A.P, A.SZ, A.P])
+A.declare("cf_rrrw_quads_bytes", A.U64, [A.cf_rrrw_view, A.U64])
+A.declare("cf_rrrw_quads_workspace_bytes", A.U64, [A.cf_rrrw_view, A.U64])
+A.declare("cf_rrrw_quads_build_async", A.I32, [A.cf_rrrw_view, A.U64, A.P, A.U64, A.P, A.U64, A.P])
+A.declare("cf_rrrw_access_quads_async", A.I32, [A.cf_rrrw_view, A.U64, A.P, A.P, A.P, A.SZ, A.P])
+A.declare("cf_rrrw_rank_quads_async", A.I32, [A.cf_rrrw_view, A.U64, A.P, A.P, A.P, A.P, A.SZ, A.P])
 A.declare("cf_sparse_gather_fused_lines_async", A.I32, [A.cf_rrrw_view, A.P, A.P, C.c_int, A.P, A.P, A.SZ, A.P])
 A.declare("cf_fm_lines_bytes", A.U64, [A.cf_fm_view])
 A.declare("cf_fm_lines_build_async", A.I32, [A.cf_fm_view, A.P, A.U64, A.P])

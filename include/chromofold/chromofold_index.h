@@ -91,6 +91,30 @@ cf_status cf_rrrw_access_lines_async(cf_rrrw_view v, const uint32_t *lines, cons
                                      size_t count, void *stream);
 cf_status cf_rrrw_rank_lines_async(cf_rrrw_view v, const uint32_t *lines, const uint32_t *symbols,
                                    const uint32_t *positions, uint32_t *out, size_t count, void *stream);
+
+/* ---- derived on-device 4-ary layout of an RRR wavelet matrix (no counterpart in the reference; the .cfrw on disk
+ * and the cf_rrrw_view arrays are unchanged). The sequence (n symbols: the view does not hold n) read as base-4
+ * digits, most significant first, in L4 = ceil(bits / 2) levels of a 4-ary wavelet matrix: access and rank read L4
+ * 64-byte records per query (8 at bits 15) instead of the binary layouts' `bits`. Results equal cf_rrrw_access_async
+ * / cf_rrrw_rank_async for positions in [0, n] (past n: unspecified values, never an out-of-bounds read). Level 0
+ * holds every position's top digit in sequence order; level l + 1 the positions of level l stably sorted by their
+ * digit l. Layout of `quads` (u32 words, 16-byte aligned):
+ *   [L4][nrec][16] records, nrec = n / 208 + 1: words 0..2 = how many of digits 0, 1, 2 the level holds before
+ *   position 208 r, words 3..15 = the level's digits at positions [208 r, 208 r + 208), 16 two-bit digits per word,
+ *   LSB-first;
+ *   then Z [L4][4] u32 (Z[l][d] = positions of level l whose digit is below d);
+ *   then [2^bits] int32 base[c] = -(where the walk of symbol c from position 0 ends), rank(c, i) = walk(i) + base[c].
+ * bits <= 24 and n < 2^31 (the byte counts are 0 otherwise). The build decodes the sequence from the view into
+ * `workspace` (cf_rrrw_quads_workspace_bytes, 256-byte aligned) and sorts it level by level there. */
+uint64_t cf_rrrw_quads_bytes(cf_rrrw_view v, uint64_t n);
+uint64_t cf_rrrw_quads_workspace_bytes(cf_rrrw_view v, uint64_t n);
+cf_status cf_rrrw_quads_build_async(cf_rrrw_view v, uint64_t n, uint32_t *quads, uint64_t bytes, void *workspace,
+                                    uint64_t workspace_bytes, void *stream);
+cf_status cf_rrrw_access_quads_async(cf_rrrw_view v, uint64_t n, const uint32_t *quads, const uint32_t *positions,
+                                     uint32_t *out, size_t count, void *stream);
+cf_status cf_rrrw_rank_quads_async(cf_rrrw_view v, uint64_t n, const uint32_t *quads, const uint32_t *symbols,
+                                   const uint32_t *positions, uint32_t *out, size_t count, void *stream);
+
 /* cf_sparse_gather_fused_async (chromofold_extra.h, reference src/cuda/sparse_gather.cu:55-66) over the line layout:
  * out[t, :] = emb[access(pos[t]), :] for t < count, the same bytes, each query's access walk reading one 64-byte
  * line per level. Same argument rules (count 0 or dim <= 0: nothing to do). */
