@@ -206,25 +206,48 @@ def bench_fm(steps: int, warmup: int, cpu: bool = True) -> dict:
     fm.locate_lines(rows, pos_l)
     assert torch.equal(cnt_l, cnt) and torch.equal(lo_l, lo) and torch.equal(hi_l, hi), "line layout != RRR search"
     assert torch.equal(pos_l, pos), "line layout != RRR locate"
+    # the derived 4-ary layout (built once at load): 8 records per walk instead of 15; the C2 figures
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    fm.build_quads()
+    torch.cuda.synchronize()
+    t_quads_build = time.perf_counter() - t0
+    cnt_q = fm.count_quads(dpat, dps, dpl)
+    lo_q, hi_q = fm.ranges_quads(dpat, dps, dpl)
+    pos_q = torch.empty_like(rows)
+    fm.locate_quads(rows, pos_q)
+    assert torch.equal(cnt_q, cnt) and torch.equal(lo_q, lo) and torch.equal(hi_q, hi), "4-ary layout != RRR search"
+    assert torch.equal(pos_q, pos), "4-ary layout != RRR locate"
     _, per_c = _events_time(lambda: fm.count(dpat, dps, dpl), steps, warmup)
     _, per_l = _events_time(lambda: fm.locate(rows, pos), steps, warmup)
     _, per_cl = _events_time(lambda: fm.count_lines(dpat, dps, dpl, out=cnt_l), steps, warmup)
     _, per_ll = _events_time(lambda: fm.locate_lines(rows, pos_l), steps, warmup)
-    t_c, t_l, t_cl, t_ll = (float(np.mean(x)) * 1e-3 for x in (per_c, per_l, per_cl, per_ll))
-    res = {"count_mpats": pstart.size / t_cl / 1e6, "count_ms": t_cl * 1e3, "occurrences": occ,
-           "locate_mocc": occ / t_ll / 1e6, "locate_ms": t_ll * 1e3,
+    _, per_cq = _events_time(lambda: fm.count_quads(dpat, dps, dpl, out=cnt_q), steps, warmup)
+    _, per_lq = _events_time(lambda: fm.locate_quads(rows, pos_q), steps, warmup)
+    t_c, t_l, t_cl, t_ll, t_cq, t_lq = (float(np.mean(x)) * 1e-3 for x in (per_c, per_l, per_cl, per_ll, per_cq,
+                                                                          per_lq))
+    res = {"count_mpats": pstart.size / t_cq / 1e6, "count_ms": t_cq * 1e3, "occurrences": occ,
+           "locate_mocc": occ / t_lq / 1e6, "locate_ms": t_lq * 1e3,
+           "lines_count_mpats": pstart.size / t_cl / 1e6, "lines_count_ms": t_cl * 1e3,
+           "lines_locate_mocc": occ / t_ll / 1e6, "lines_locate_ms": t_ll * 1e3,
            "rrr_count_mpats": pstart.size / t_c / 1e6, "rrr_count_ms": t_c * 1e3,
            "rrr_locate_mocc": occ / t_l / 1e6, "rrr_locate_ms": t_l * 1e3,
            "gpu_sa_build_s": info["sa_s"], "gpu_index_build_s": info["build_s"], "lines_build_s": t_lines_build,
-           "index_bytes": fm.w.device_bytes(), "lines_bytes": fm.lines.numel()}
+           "quads_build_s": t_quads_build, "index_bytes": fm.w.device_bytes(), "lines_bytes": fm.lines.numel(),
+           "quads_bytes": fm.quads.numel()}
     # cost models (algorithmic bytes), symbols = pattern symbols per launch:
     #   RRR count: 1928 B per symbol (rank(c, lo) and rank(c, hi), each 2 rank1 per level x 15 levels x 32 B, + 8 B
     #   of C[]); RRR locate: 15.5 expected LF steps x (access 480 + rank 960 + mark word 4) + sval 4 + msb 4;
     #   line count: 1928 B per symbol (2 rank1 per level x 15 levels x one 64-B record, + lfb 4 B + the symbol 4 B);
-    #   line locate: 15.5 LF steps x (15 records x 64 B + lfb 4 + mark word 4) + sval 4 + msb 4.
+    #   line locate: 15.5 LF steps x (15 records x 64 B + lfb 4 + mark word 4) + sval 4 + msb 4;
+    #   4-ary count: 1032 B per symbol (2 walks x 8 levels x one 64-B record + lfb 4 + the symbol 4); 4-ary locate:
+    #   15.5 LF steps x (8 records x 64 B + lfb 4 + mark word 4) + sval 4 + msb 4.
     syms = float(plen.astype(np.int64).sum())
-    models = {"count_roofline": (syms * (2 * 15 * 64 + 8), t_cl, ("fm_count_lines", n, pstart.size)),
-              "locate_roofline": (occ * (15.5 * (15 * 64 + 8) + 8), t_ll, ("fm_locate_lines", n, occ)),
+    L4 = (fm.w.bits + 1) // 2
+    models = {"count_roofline": (syms * (2 * L4 * 64 + 8), t_cq, ("fm_count_quads", n, pstart.size)),
+              "locate_roofline": (occ * (15.5 * (L4 * 64 + 8) + 8), t_lq, ("fm_locate_quads", n, occ)),
+              "lines_count_roofline": (syms * (2 * 15 * 64 + 8), t_cl, ("fm_count_lines", n, pstart.size)),
+              "lines_locate_roofline": (occ * (15.5 * (15 * 64 + 8) + 8), t_ll, ("fm_locate_lines", n, occ)),
               "rrr_count_roofline": (syms * (1920 + 8), t_c, ("fm_count", n, pstart.size)),
               "rrr_locate_roofline": (occ * (15.5 * (480 + 960 + 4) + 8), t_l, ("fm_locate", n, occ))}
     for key, (b, t, tk) in models.items():
@@ -1217,7 +1240,8 @@ def main() -> int:
             secondary["cache_peaks"] = peaks
             l2 = peaks["l2_read_gbs"]
             secondary["c1_rrr"]["rank_frac_of_l2"] = rrr["rank_roofline"]["achieved"] / l2
-            for k in ("count_roofline", "locate_roofline", "rrr_count_roofline", "rrr_locate_roofline"):
+            for k in ("count_roofline", "locate_roofline", "lines_count_roofline", "lines_locate_roofline",
+                      "rrr_count_roofline", "rrr_locate_roofline"):
                 r = secondary["c2_fm"][k]
                 r["frac_of_l2"] = r["achieved"] / l2
                 if r["traffic_gbs"]:  # L2-miss traffic against the Infinity Cache's read rate

@@ -13,6 +13,7 @@
 #include "packed_core.hpp"
 #include "rrr_core.hpp"
 #include "lines_core.hpp"
+#include "quads_core.hpp"
 
 namespace {
 
@@ -229,62 +230,118 @@ __global__ __launch_bounds__(kStagedThreads) void fm_locate_staged_kernel(cf_fm_
     }                                                                                                         \
   } while (0)
 
-// ---- the line layout (lines_core.hpp, chromofold_index.h cf_fm_lines_*): with base[c] = C[c] - e(c) an LF step is
-// LF(i) = a_L(i) + base[c], so backward search takes 2 rank1 per level (lo and hi) and the LF step of locate 1 (the
-// access walk of i is the rank walk of i for c = BWT[i]), one 64-byte record each; every result equals the RRR
-// kernels' above.
-struct LinesArgs {
-  const uint32_t *rec;   // level records, [bits][nrec][16]
-  const int32_t *lfb;    // [sigma]
+// ---- the derived layouts (chromofold_index.h cf_fm_lines_*, cf_fm_quads_*). With lfb[c] = C[c] - e(c), e(c) the end
+// of the walk of c from position 0, an LF step is LF(i) = walk(i) + lfb[c], so backward search walks lo and hi
+// (one record per level each) and an LF step of locate walks once (the access walk of i is the rank walk of i for
+// c = BWT[i]); every result equals the RRR kernels' above.
+//   line layout (lines_core.hpp): the binary levels, `bits` records per walk;
+//   4-ary layout (quads_core.hpp): base-4 digits, ceil(bits / 2) records per walk.
+struct WalkArgs {
+  const uint32_t *rec;  // level records, [levels][nrec][16]
+  const int32_t *lfb;   // [sigma]
+  const uint32_t *Z;    // 4-ary layout: digit bucket starts [levels][4]
   uint32_t nrec;
 };
 
-__host__ inline LinesArgs lines_args(const cf_fm_view &v, const uint32_t *lines) {
+__host__ inline WalkArgs lines_args(const cf_fm_view &v, const uint32_t *lines) {
   const uint32_t nrec = cfl::nrec_for(static_cast<uint64_t>(v.n));
   return {lines, reinterpret_cast<const int32_t *>(lines + static_cast<size_t>(v.w.bits) * nrec * cfl::kRecWords),
-          nrec};
+          nullptr, nrec};
 }
 
-// One backward-search step on the line layout: [lo, hi) -> [lfb[c] + a_L, lfb[c] + b_L). When a and b fall in
-// the same record (most steps once the interval is narrow) the second load hits the line the first brought in.
+__host__ inline WalkArgs quads_args(const cf_fm_view &v, const uint32_t *quads) {
+  const cfq::Layout L = cfq::layout(v.w.bits, static_cast<uint64_t>(v.n), v.sigma);
+  const uint32_t *Z = quads + L.rec_words;
+  return {quads, reinterpret_cast<const int32_t *>(Z + L.z_words), Z, L.nrec};
+}
+
 template <int LEVELS>
-__device__ __forceinline__ void lines_step(const cf_fm_view &v, const LinesArgs &la, int c, int &lo, int &hi) {
-  const int L = LEVELS > 0 ? LEVELS : v.w.bits;
-  uint32_t a = static_cast<uint32_t>(lo), b = static_cast<uint32_t>(hi);
-  for (int lvl = 0; lvl < L; ++lvl) {
-    // both records' loads issued before either rank is counted (two latencies per level would serialise)
-    const uint32_t *lv = la.rec + static_cast<size_t>(lvl) * la.nrec * cfl::kRecWords;
-    const uint32_t ra_rec = min(a / cfl::kLineBits, la.nrec - 1u), rb_rec = min(b / cfl::kLineBits, la.nrec - 1u);
-    uint32_t wa[16], wb[16];
-    cfl::load_record(lv + ra_rec * cfl::kRecWords, wa);
-    cfl::load_record(lv + rb_rec * cfl::kRecWords, wb);
-    const int ra = cfl::record_rank<false>(wa, a - ra_rec * cfl::kLineBits, nullptr);
-    const int rb = cfl::record_rank<false>(wb, b - rb_rec * cfl::kLineBits, nullptr);
-    if ((c >> (L - 1 - lvl)) & 1) {
-      const uint32_t z = static_cast<uint32_t>(v.w.zeros[lvl]);
-      a = z + ra;
-      b = z + rb;
-    } else {
-      a -= ra;
-      b -= rb;
+struct LinesWalk {
+  // One backward-search step: [lo, hi) -> [lfb[c] + a_L, lfb[c] + b_L). When a and b fall in the same record (most
+  // steps once the interval is narrow) the second load hits the line the first brought in.
+  __device__ static __forceinline__ void range(const cf_fm_view &v, const WalkArgs &la, int c, int &lo, int &hi) {
+    const int L = LEVELS > 0 ? LEVELS : v.w.bits;
+    uint32_t a = static_cast<uint32_t>(lo), b = static_cast<uint32_t>(hi);
+    for (int lvl = 0; lvl < L; ++lvl) {
+      // both records' loads issued before either rank is counted (two latencies per level would serialise)
+      const uint32_t *lv = la.rec + static_cast<size_t>(lvl) * la.nrec * cfl::kRecWords;
+      const uint32_t ra_rec = min(a / cfl::kLineBits, la.nrec - 1u), rb_rec = min(b / cfl::kLineBits, la.nrec - 1u);
+      uint32_t wa[16], wb[16];
+      cfl::load_record(lv + ra_rec * cfl::kRecWords, wa);
+      cfl::load_record(lv + rb_rec * cfl::kRecWords, wb);
+      const int ra = cfl::record_rank<false>(wa, a - ra_rec * cfl::kLineBits, nullptr);
+      const int rb = cfl::record_rank<false>(wb, b - rb_rec * cfl::kLineBits, nullptr);
+      if ((c >> (L - 1 - lvl)) & 1) {
+        const uint32_t z = static_cast<uint32_t>(v.w.zeros[lvl]);
+        a = z + ra;
+        b = z + rb;
+      } else {
+        a -= ra;
+        b -= rb;
+      }
     }
+    const int f = la.lfb[c];
+    lo = f + static_cast<int>(a);
+    hi = f + static_cast<int>(b);
   }
-  const int f = la.lfb[c];
-  lo = f + static_cast<int>(a);
-  hi = f + static_cast<int>(b);
-}
+  // LF(p): c's bits and the next position from one walk of p (each record's bit at the position).
+  __device__ static __forceinline__ int lf(const cf_fm_view &v, const WalkArgs &la, int p) {
+    const int L = LEVELS > 0 ? LEVELS : v.w.bits;
+    uint32_t a = static_cast<uint32_t>(p);
+    int c = 0;
+    for (int lvl = 0; lvl < L; ++lvl) {
+      int bit;
+      const int r = cfl::rank1<true>(la.rec, la.nrec, lvl, a, &bit);
+      c = (c << 1) | bit;
+      a = bit ? static_cast<uint32_t>(v.w.zeros[lvl] + r) : a - static_cast<uint32_t>(r);
+    }
+    return static_cast<int>(a) + la.lfb[c];
+  }
+};
 
-// Backward search on the line layout. A workgroup owns `per` consecutive patterns and its lanes take the next one
+template <int L4>
+struct QuadsWalk {
+  __device__ static __forceinline__ void range(const cf_fm_view &v, const WalkArgs &la, int c, int &lo, int &hi) {
+    const uint32_t L = L4 > 0 ? static_cast<uint32_t>(L4) : cfq::levels_for(v.w.bits);
+    uint32_t a = static_cast<uint32_t>(lo), b = static_cast<uint32_t>(hi);
+    for (uint32_t l = 0; l < L; ++l) {
+      const uint32_t d = (static_cast<uint32_t>(c) >> (2u * (L - 1u - l))) & 3u;
+      const uint32_t *lv = la.rec + static_cast<size_t>(l) * la.nrec * cfq::kRecWords;
+      const uint32_t ra_rec = min(a / cfq::kDigits, la.nrec - 1u), rb_rec = min(b / cfq::kDigits, la.nrec - 1u);
+      uint32_t wa[16], wb[16];
+      cfq::load_record(lv + ra_rec * cfq::kRecWords, wa);
+      cfq::load_record(lv + rb_rec * cfq::kRecWords, wb);
+      const uint32_t z = la.Z[4 * l + d];
+      a = z + cfq::record_rank(wa, ra_rec * cfq::kDigits, min(a - ra_rec * cfq::kDigits, cfq::kDigits), d);
+      b = z + cfq::record_rank(wb, rb_rec * cfq::kDigits, min(b - rb_rec * cfq::kDigits, cfq::kDigits), d);
+    }
+    const int f = la.lfb[c];
+    lo = f + static_cast<int>(a);
+    hi = f + static_cast<int>(b);
+  }
+  __device__ static __forceinline__ int lf(const cf_fm_view &v, const WalkArgs &la, int p) {
+    const uint32_t L = L4 > 0 ? static_cast<uint32_t>(L4) : cfq::levels_for(v.w.bits);
+    uint32_t a = static_cast<uint32_t>(p), c = 0;
+    for (uint32_t l = 0; l < L; ++l) {
+      uint32_t d;
+      a = cfq::step<true>(la.rec, la.nrec, la.Z, l, a, 0u, &d);
+      c = (c << 2) | d;
+    }
+    return static_cast<int>(a) + la.lfb[c];
+  }
+};
+
+// Backward search on a derived layout. A workgroup owns `per` consecutive patterns and its lanes take the next one
 // from an LDS counter whenever they finish one (pattern lengths vary); each loop iteration consumes one symbol
 // (right to left, reference fm_search_device.cuh:31-48) or stores a result.
-template <int LEVELS>
-__global__ __launch_bounds__(kThreads) void fm_search_lines_kernel(cf_fm_view v, LinesArgs la,
-                                                                   const int32_t *__restrict__ pat,
-                                                                   const int32_t *__restrict__ pstart,
-                                                                   const int32_t *__restrict__ plen, size_t npat,
-                                                                   uint32_t *__restrict__ cnt_out,
-                                                                   int32_t *__restrict__ lo_out,
-                                                                   int32_t *__restrict__ hi_out) {
+template <typename Walk>
+__global__ __launch_bounds__(kThreads) void fm_search_walk_kernel(cf_fm_view v, WalkArgs la,
+                                                                  const int32_t *__restrict__ pat,
+                                                                  const int32_t *__restrict__ pstart,
+                                                                  const int32_t *__restrict__ plen, size_t npat,
+                                                                  uint32_t *__restrict__ cnt_out,
+                                                                  int32_t *__restrict__ lo_out,
+                                                                  int32_t *__restrict__ hi_out) {
   __shared__ uint32_t s_next;
   const ItemQueue q = item_queue(npat, &s_next);
   size_t t = q.take();
@@ -303,7 +360,7 @@ __global__ __launch_bounds__(kThreads) void fm_search_lines_kernel(cf_fm_view v,
         if (c < 0 || c >= v.sigma) {
           lo = hi = 0;
         } else if (lo < hi) {
-          lines_step<LEVELS>(v, la, c, lo, hi);
+          Walk::range(v, la, c, lo, hi);
         }
       } else {
         if (cnt_out) cnt_out[t] = static_cast<uint32_t>(hi - lo);
@@ -324,15 +381,13 @@ __global__ __launch_bounds__(kThreads) void fm_search_lines_kernel(cf_fm_view v,
   }
 }
 
-// Locate on the line layout (reference fm_search_device.cuh:52-62): one LF step per loop iteration, c and LF(p)
-// from one walk of p (the record's bit gives c's next bit, its rank the next position).
-template <int LEVELS>
-__global__ __launch_bounds__(kThreads) void fm_locate_lines_kernel(cf_fm_view v, LinesArgs la,
-                                                                   const int32_t *__restrict__ rows,
-                                                                   int32_t *__restrict__ out, size_t nocc) {
+// Locate on a derived layout (reference fm_search_device.cuh:52-62): one LF step per loop iteration.
+template <typename Walk>
+__global__ __launch_bounds__(kThreads) void fm_locate_walk_kernel(cf_fm_view v, WalkArgs la,
+                                                                  const int32_t *__restrict__ rows,
+                                                                  int32_t *__restrict__ out, size_t nocc) {
   __shared__ uint32_t s_next;
   const ItemQueue q = item_queue(nocc, &s_next);
-  const int L = LEVELS > 0 ? LEVELS : v.w.bits;
   size_t t = q.take();
   bool active = t < q.end;
   int p = active ? rows[t] : 0, steps = 0;
@@ -348,15 +403,7 @@ __global__ __launch_bounds__(kThreads) void fm_locate_lines_kernel(cf_fm_view v,
           steps = 0;
         }
       } else {
-        uint32_t a = static_cast<uint32_t>(p);
-        int c = 0;
-        for (int lvl = 0; lvl < L; ++lvl) {
-          int bit;
-          const int r = cfl::rank1<true>(la.rec, la.nrec, lvl, a, &bit);
-          c = (c << 1) | bit;
-          a = bit ? static_cast<uint32_t>(v.w.zeros[lvl] + r) : a - static_cast<uint32_t>(r);
-        }
-        p = static_cast<int>(a) + la.lfb[c];
+        p = Walk::lf(v, la, p);
         ++steps;
       }
     }
@@ -458,10 +505,10 @@ extern "C" cf_status cf_fm_count_lines_async(cf_fm_view v, const uint32_t *lines
   if (npat == 0) return CF_OK;
   if (npat > (static_cast<size_t>(1) << 40)) return CF_ERR_INVALID_ARGUMENT;
   const hipStream_t s = cfd::as_stream(stream);
-  const LinesArgs la = lines_args(v, lines);
+  const WalkArgs la = lines_args(v, lines);
   const unsigned g = lines_grid(npat);
 #define CF_LAUNCH(L) \
-  fm_search_lines_kernel<L><<<g, kThreads, 0, s>>>(v, la, pat, pstart, plen, npat, out, nullptr, nullptr)
+  fm_search_walk_kernel<LinesWalk<L>><<<g, kThreads, 0, s>>>(v, la, pat, pstart, plen, npat, out, nullptr, nullptr)
   CF_FM_DISPATCH(CF_LAUNCH)
 #undef CF_LAUNCH
   return cfd::launch_status();
@@ -474,10 +521,10 @@ extern "C" cf_status cf_fm_ranges_lines_async(cf_fm_view v, const uint32_t *line
   if (npat == 0) return CF_OK;
   if (npat > (static_cast<size_t>(1) << 40)) return CF_ERR_INVALID_ARGUMENT;
   const hipStream_t s = cfd::as_stream(stream);
-  const LinesArgs la = lines_args(v, lines);
+  const WalkArgs la = lines_args(v, lines);
   const unsigned g = lines_grid(npat);
 #define CF_LAUNCH(L) \
-  fm_search_lines_kernel<L><<<g, kThreads, 0, s>>>(v, la, pat, pstart, plen, npat, nullptr, lo_out, hi_out)
+  fm_search_walk_kernel<LinesWalk<L>><<<g, kThreads, 0, s>>>(v, la, pat, pstart, plen, npat, nullptr, lo_out, hi_out)
   CF_FM_DISPATCH(CF_LAUNCH)
 #undef CF_LAUNCH
   return cfd::launch_status();
@@ -489,10 +536,92 @@ extern "C" cf_status cf_fm_locate_lines_async(cf_fm_view v, const uint32_t *line
   if (nocc == 0) return CF_OK;
   if (nocc > (static_cast<size_t>(1) << 40)) return CF_ERR_INVALID_ARGUMENT;
   const hipStream_t s = cfd::as_stream(stream);
-  const LinesArgs la = lines_args(v, lines);
+  const WalkArgs la = lines_args(v, lines);
   const unsigned g = lines_grid(nocc);
-#define CF_LAUNCH(L) fm_locate_lines_kernel<L><<<g, kThreads, 0, s>>>(v, la, r_in, out, nocc)
+#define CF_LAUNCH(L) fm_locate_walk_kernel<LinesWalk<L>><<<g, kThreads, 0, s>>>(v, la, r_in, out, nocc)
   CF_FM_DISPATCH(CF_LAUNCH)
+#undef CF_LAUNCH
+  return cfd::launch_status();
+}
+
+// ---- 4-ary layout entry points (chromofold_index.h) ----
+static bool quads_fm_ok(const cf_fm_view &v) {
+  return v.w.classes && v.w.bits > 0 && v.w.bits <= 24 && v.n > 0 && v.sigma > 0 && v.C && v.w.zeros &&
+         (v.sigma - 1) >> v.w.bits == 0 && static_cast<uint64_t>(v.n) <= static_cast<uint64_t>(v.w.nsb) * 960u;
+}
+
+extern "C" uint64_t cf_fm_quads_bytes(cf_fm_view v) {
+  if (!quads_fm_ok(v)) return 0;
+  return cfq::layout(v.w.bits, static_cast<uint64_t>(v.n), v.sigma).bytes();
+}
+
+extern "C" uint64_t cf_fm_quads_workspace_bytes(cf_fm_view v) {
+  if (!quads_fm_ok(v)) return 0;
+  return cfq::workspace_bytes(static_cast<uint64_t>(v.n), cfq::nrec_for(static_cast<uint64_t>(v.n)));
+}
+
+extern "C" cf_status cf_fm_quads_build_async(cf_fm_view v, uint32_t *quads, uint64_t bytes, void *workspace,
+                                             uint64_t workspace_bytes, void *stream) {
+  if (!quads_fm_ok(v) || !quads || (reinterpret_cast<uintptr_t>(quads) & 15u) != 0 || !workspace ||
+      (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0 || !v.w.offsets || !v.w.rank_a || !v.w.rank_d ||
+      !v.w.off_a || !v.w.off_d || !v.w.offbase)
+    return CF_ERR_INVALID_ARGUMENT;
+  if (bytes < cf_fm_quads_bytes(v) || workspace_bytes < cf_fm_quads_workspace_bytes(v)) return CF_ERR_INVALID_ARGUMENT;
+  return cfq::build(v.w, static_cast<uint64_t>(v.n), v.sigma, v.C, quads, workspace, cfd::as_stream(stream));
+}
+
+static bool quads_ptr_ok(const cf_fm_view &v, const uint32_t *quads) {
+  return quads && (reinterpret_cast<uintptr_t>(quads) & 15u) == 0 && quads_fm_ok(v);
+}
+
+#define CF_QUADS_DISPATCH(LAUNCH)           \
+  if (cfq::levels_for(v.w.bits) == 8) {     \
+    LAUNCH(QuadsWalk<8>);                   \
+  } else {                                  \
+    LAUNCH(QuadsWalk<0>);                   \
+  }
+
+extern "C" cf_status cf_fm_count_quads_async(cf_fm_view v, const uint32_t *quads, const int32_t *pat,
+                                             const int32_t *pstart, const int32_t *plen, uint32_t *out, size_t npat,
+                                             void *stream) {
+  if (!pat || !pstart || !plen || !out || !quads_ptr_ok(v, quads)) return CF_ERR_INVALID_ARGUMENT;
+  if (npat == 0) return CF_OK;
+  if (npat > (static_cast<size_t>(1) << 40)) return CF_ERR_INVALID_ARGUMENT;
+  const hipStream_t s = cfd::as_stream(stream);
+  const WalkArgs la = quads_args(v, quads);
+  const unsigned g = lines_grid(npat);
+#define CF_LAUNCH(W) fm_search_walk_kernel<W><<<g, kThreads, 0, s>>>(v, la, pat, pstart, plen, npat, out, nullptr, nullptr)
+  CF_QUADS_DISPATCH(CF_LAUNCH)
+#undef CF_LAUNCH
+  return cfd::launch_status();
+}
+
+extern "C" cf_status cf_fm_ranges_quads_async(cf_fm_view v, const uint32_t *quads, const int32_t *pat,
+                                              const int32_t *pstart, const int32_t *plen, int32_t *lo_out,
+                                              int32_t *hi_out, size_t npat, void *stream) {
+  if (!pat || !pstart || !plen || !lo_out || !hi_out || !quads_ptr_ok(v, quads)) return CF_ERR_INVALID_ARGUMENT;
+  if (npat == 0) return CF_OK;
+  if (npat > (static_cast<size_t>(1) << 40)) return CF_ERR_INVALID_ARGUMENT;
+  const hipStream_t s = cfd::as_stream(stream);
+  const WalkArgs la = quads_args(v, quads);
+  const unsigned g = lines_grid(npat);
+#define CF_LAUNCH(W) \
+  fm_search_walk_kernel<W><<<g, kThreads, 0, s>>>(v, la, pat, pstart, plen, npat, nullptr, lo_out, hi_out)
+  CF_QUADS_DISPATCH(CF_LAUNCH)
+#undef CF_LAUNCH
+  return cfd::launch_status();
+}
+
+extern "C" cf_status cf_fm_locate_quads_async(cf_fm_view v, const uint32_t *quads, const int32_t *r_in, int32_t *out,
+                                              size_t nocc, void *stream) {
+  if (!r_in || !out || !quads_ptr_ok(v, quads) || !v.mwords || !v.msb || !v.sval) return CF_ERR_INVALID_ARGUMENT;
+  if (nocc == 0) return CF_OK;
+  if (nocc > (static_cast<size_t>(1) << 40)) return CF_ERR_INVALID_ARGUMENT;
+  const hipStream_t s = cfd::as_stream(stream);
+  const WalkArgs la = quads_args(v, quads);
+  const unsigned g = lines_grid(nocc);
+#define CF_LAUNCH(W) fm_locate_walk_kernel<W><<<g, kThreads, 0, s>>>(v, la, r_in, out, nocc)
+  CF_QUADS_DISPATCH(CF_LAUNCH)
 #undef CF_LAUNCH
   return cfd::launch_status();
 }

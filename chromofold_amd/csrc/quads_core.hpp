@@ -91,7 +91,7 @@ __global__ __launch_bounds__(256) void tokens_kernel(cf_rrrw_view w, uint32_t *_
 
 // Per record r of the level whose digit is (seq >> shift) & 3: the count of each digit, into cnt[d][r]
 // (cnt rows of nrec + 1 entries; entry nrec stays 0 so that an exclusive scan leaves the totals there).
-__global__ __launch_bounds__(kBuildThreads) void count_kernel(const uint32_t *__restrict__ seq, uint32_t n,
+static __global__ __launch_bounds__(kBuildThreads) void count_kernel(const uint32_t *__restrict__ seq, uint32_t n,
                                                               uint32_t nrec, uint32_t shift, uint32_t *__restrict__ cnt) {
   __shared__ uint32_t s_c[kBuildThreads / 64][4];
   const uint32_t r = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63u;
@@ -116,7 +116,7 @@ __global__ __launch_bounds__(kBuildThreads) void count_kernel(const uint32_t *__
 // The level's records from the exclusive prefix counts pre[d][r] (totals at pre[d][nrec]), and the stable partition
 // of the sequence by the digit into `next`: position i of record r goes to Z[d] + pre[d][r] + (its rank among the
 // record's d digits). Workgroup 0 writes Z.
-__global__ __launch_bounds__(kBuildThreads) void write_kernel(const uint32_t *__restrict__ seq, uint32_t *__restrict__ next,
+static __global__ __launch_bounds__(kBuildThreads) void write_kernel(const uint32_t *__restrict__ seq, uint32_t *__restrict__ next,
                                                               uint32_t n, uint32_t nrec, uint32_t shift,
                                                               const uint32_t *__restrict__ pre,
                                                               uint32_t *__restrict__ level, uint32_t *__restrict__ Z) {
@@ -159,7 +159,7 @@ __global__ __launch_bounds__(kBuildThreads) void write_kernel(const uint32_t *__
 }
 
 // base[c] = (X ? X[c] : 0) - e(c) for c < nsym, one thread per symbol.
-__global__ __launch_bounds__(256) void base_kernel(const uint32_t *__restrict__ quads, uint32_t nrec,
+static __global__ __launch_bounds__(256) void base_kernel(const uint32_t *__restrict__ quads, uint32_t nrec,
                                                    const uint32_t *__restrict__ Z, uint32_t L4, int32_t nsym,
                                                    const int32_t *__restrict__ X, int32_t *__restrict__ base) {
   const int c = static_cast<int>(blockIdx.x * 256u + threadIdx.x);

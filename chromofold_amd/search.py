@@ -179,6 +179,7 @@ class FmIndex:
     sa_sample: int
     tensors: dict
     lines: "torch.Tensor | None" = None  # the derived line layout, built on first use (build_lines)
+    quads: "torch.Tensor | None" = None  # the derived 4-ary layout, built on first use (build_quads)
 
     @classmethod
     def from_host(cls, arrays, device="cuda") -> "FmIndex":
@@ -247,6 +248,44 @@ class FmIndex:
                                                  rows.numel(), stream_ptr(stream)), "cf_fm_locate_lines_async")
         return out
 
+    # ---- the derived 4-ary layout (cf_fm_quads_*): same results, ceil(bits / 2) records per walk
+    def build_quads(self, stream=None) -> torch.Tensor:
+        if self.quads is None:
+            v = self.view()
+            L = A.lib()
+            nb, nw = int(L.cf_fm_quads_bytes(v)), int(L.cf_fm_quads_workspace_bytes(v))
+            if nb == 0:
+                raise A.CfError(A.CF_ERR_INVALID_ARGUMENT, "cf_fm_quads_bytes")
+            dev = self.tensors["C"].device
+            quads = torch.empty(nb, dtype=torch.uint8, device=dev)
+            ws = torch.empty(nw, dtype=torch.uint8, device=dev)
+            A.check(L.cf_fm_quads_build_async(v, _ptr(quads), nb, _ptr(ws), nw, stream_ptr(stream)),
+                    "cf_fm_quads_build_async")
+            torch.cuda.current_stream(dev).synchronize() if stream is None else stream.synchronize()  # ws is freed
+            self.quads = quads
+        return self.quads
+
+    def count_quads(self, pat, pstart, plen, out=None, stream=None) -> torch.Tensor:
+        out = torch.empty(pstart.numel(), dtype=torch.int32, device=pstart.device) if out is None else out
+        A.check(A.lib().cf_fm_count_quads_async(self.view(), _ptr(self.build_quads(stream)), _ptr(pat), _ptr(pstart),
+                                                _ptr(plen), _ptr(out), pstart.numel(), stream_ptr(stream)),
+                "cf_fm_count_quads_async")
+        return out
+
+    def ranges_quads(self, pat, pstart, plen, stream=None):
+        lo = torch.empty(pstart.numel(), dtype=torch.int32, device=pstart.device)
+        hi = torch.empty_like(lo)
+        A.check(A.lib().cf_fm_ranges_quads_async(self.view(), _ptr(self.build_quads(stream)), _ptr(pat), _ptr(pstart),
+                                                 _ptr(plen), _ptr(lo), _ptr(hi), pstart.numel(), stream_ptr(stream)),
+                "cf_fm_ranges_quads_async")
+        return lo, hi
+
+    def locate_quads(self, rows: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+        out = torch.empty_like(rows, dtype=torch.int32) if out is None else out
+        A.check(A.lib().cf_fm_locate_quads_async(self.view(), _ptr(self.build_quads(stream)), _ptr(rows), _ptr(out),
+                                                 rows.numel(), stream_ptr(stream)), "cf_fm_locate_quads_async")
+        return out
+
 
 def gpu_suffix_array(s: torch.Tensor, stream=None) -> torch.Tensor:
     """Suffix array of the int32 device text `s` (sentinel-terminated) via cf_suffix_array."""
@@ -279,6 +318,12 @@ A.declare("cf_rrrw_lines_bytes", A.U64, [A.cf_rrrw_view])
 A.declare("cf_rrrw_lines_build_async", A.I32, [A.cf_rrrw_view, A.P, A.U64, A.P])
 A.declare("cf_rrrw_access_lines_async", A.I32, [A.cf_rrrw_view, A.P, A.P, A.P, A.SZ, A.P])
 A.declare("cf_rrrw_rank_lines_async", A.I32, [A.cf_rrrw_view, A.P, A.P, A.P, A.P, A.SZ, A.P])
+A.declare("cf_fm_quads_bytes", A.U64, [A.cf_fm_view])
+A.declare("cf_fm_quads_workspace_bytes", A.U64, [A.cf_fm_view])
+A.declare("cf_fm_quads_build_async", A.I32, [A.cf_fm_view, A.P, A.U64, A.P, A.U64, A.P])
+A.declare("cf_fm_count_quads_async", A.I32, [A.cf_fm_view, A.P, A.P, A.P, A.P, A.P, A.SZ, A.P])
+A.declare("cf_fm_ranges_quads_async", A.I32, [A.cf_fm_view, A.P, A.P, A.P, A.P, A.P, A.P, A.SZ, A.P])
+A.declare("cf_fm_locate_quads_async", A.I32, [A.cf_fm_view, A.P, A.P, A.P, A.SZ, A.P])
 A.declare("cf_rrrw_quads_bytes", A.U64, [A.cf_rrrw_view, A.U64])
 A.declare("cf_rrrw_quads_workspace_bytes", A.U64, [A.cf_rrrw_view, A.U64])
 A.declare("cf_rrrw_quads_build_async", A.I32, [A.cf_rrrw_view, A.U64, A.P, A.U64, A.P, A.U64, A.P])

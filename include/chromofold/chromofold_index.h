@@ -145,6 +145,25 @@ cf_status cf_fm_ranges_lines_async(cf_fm_view v, const uint32_t *lines, const in
 cf_status cf_fm_locate_lines_async(cf_fm_view v, const uint32_t *lines, const int32_t *r_in, int32_t *out,
                                    size_t nocc, void *stream);
 
+/* ---- derived on-device 4-ary layout for FM search (no counterpart in the reference; the .cffm on disk and the
+ * cf_fm_view arrays are unchanged): the 4-ary layout of cf_rrrw_quads_* (above) of the BWT (n = view.n), with the
+ * per-symbol table holding lfb[c] = C[c] - (where the walk of c from position 0 ends) for c < sigma instead of
+ * base[]. Backward search then walks lo and hi through ceil(bits / 2) records per pattern symbol (the line layout:
+ * bits), and an LF step of locate one walk; results equal cf_fm_count_async / cf_fm_ranges_async /
+ * cf_fm_locate_async for the same view. Layout of `quads`: [L4][nrec][16] records, nrec = n / 208 + 1, then
+ * Z [L4][4], then [sigma] int32 lfb. bits <= 24, sigma <= 2^bits (the byte counts are 0 otherwise). The build decodes
+ * the BWT from the view into `workspace` (cf_fm_quads_workspace_bytes, 256-byte aligned). */
+uint64_t cf_fm_quads_bytes(cf_fm_view v);
+uint64_t cf_fm_quads_workspace_bytes(cf_fm_view v);
+cf_status cf_fm_quads_build_async(cf_fm_view v, uint32_t *quads, uint64_t bytes, void *workspace,
+                                  uint64_t workspace_bytes, void *stream);
+cf_status cf_fm_count_quads_async(cf_fm_view v, const uint32_t *quads, const int32_t *pat, const int32_t *pstart,
+                                  const int32_t *plen, uint32_t *out, size_t npat, void *stream);
+cf_status cf_fm_ranges_quads_async(cf_fm_view v, const uint32_t *quads, const int32_t *pat, const int32_t *pstart,
+                                   const int32_t *plen, int32_t *lo_out, int32_t *hi_out, size_t npat, void *stream);
+cf_status cf_fm_locate_quads_async(cf_fm_view v, const uint32_t *quads, const int32_t *r_in, int32_t *out,
+                                   size_t nocc, void *stream);
+
 /* ---- on-disk formats: .cfrw v1 and .cffm v1 (host files; host arrays) ----
  * Byte-compatible with the reference writer (tools/build_index.cpp:413-438 and 496-526; exporter docstrings
  * tools/export_rrr_wavelet.py:11-19, tools/export_fm_index.py:19-29): magic, version 1, little-endian header

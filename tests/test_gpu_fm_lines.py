@@ -1,5 +1,6 @@
 """GPU parity of the derived line layout of the FM-index (cf_fm_lines_build_async and the cf_fm_*_lines_async search
-entry points, chromofold_index.h).
+entry points, chromofold_index.h) and of the derived 4-ary layout (cf_fm_quads_*), checked the same way (its records,
+bucket starts and lfb against a 4-ary wavelet matrix of the BWT built here by stable sorts).
 
 The layout has no counterpart in the reference: it is built on the device from the same cf_fm_view, and the search
 entry points over it must return exactly what the RRR entry points return. Anchors:
@@ -85,9 +86,18 @@ def check_layout(lines, bits, recs, base):
 
 
 def _check_layout(idx, bwt):
+    from test_gpu_rrr_wavelet import expected_quads
     bits = idx.w.bits
-    recs, lfb = expected_lines(bwt, bits, idx.tensors["C"].cpu().numpy())
+    C = idx.tensors["C"].cpu().numpy()
+    recs, lfb = expected_lines(bwt, bits, C)
     check_layout(idx.build_lines(), bits, recs, lfb)
+    q = idx.build_quads().cpu().numpy().view(np.uint32)
+    qrecs, Z, qlfb = expected_quads(bwt, bits, C)
+    nw = qrecs.size
+    assert q.size == nw + Z.size + qlfb.size
+    assert np.array_equal(q[:nw].reshape(qrecs.shape), qrecs)
+    assert np.array_equal(q[nw:nw + Z.size].reshape(Z.shape), Z)
+    assert np.array_equal(q[nw + Z.size:].view(np.int32), qlfb)
 
 
 def _search_both(idx, pat, ps, pl, dev):
@@ -98,6 +108,10 @@ def _search_both(idx, pat, ps, pl, dev):
     rlo, rhi = (x.cpu().numpy() for x in idx.ranges(dp, ds, dl))
     assert np.array_equal(cnt, rcnt)
     assert np.array_equal(lo, rlo) and np.array_equal(hi, rhi)
+    qcnt = idx.count_quads(dp, ds, dl).cpu().numpy().view(np.uint32)
+    qlo, qhi = (x.cpu().numpy() for x in idx.ranges_quads(dp, ds, dl))
+    assert np.array_equal(qcnt, rcnt)
+    assert np.array_equal(qlo, rlo) and np.array_equal(qhi, rhi)
     return cnt, lo, hi
 
 
@@ -113,6 +127,7 @@ def test_tiny_cffm_fixture(dev):
     assert np.array_equal(cnt, d["count_golden"])
     rows = np.concatenate([np.arange(a, b, dtype=np.int32) for a, b in zip(lo, hi)])
     pos = idx.locate_lines(_i32(rows, dev)).cpu().numpy()
+    assert np.array_equal(idx.locate_quads(_i32(rows, dev)).cpu().numpy(), pos)
     at = 0
     for t, (a, b) in enumerate(zip(lo, hi)):
         got = np.sort(pos[at:at + (b - a)])
@@ -168,6 +183,7 @@ def test_random_text_vs_oracle(dev, ntok, vocab, sample, seed):
     got = idx.locate_lines(_i32(rows, dev)).cpu().numpy()
     assert np.array_equal(got, O.fm_locate(f, rows))
     assert np.array_equal(got, idx.locate(_i32(rows, dev)).cpu().numpy())
+    assert np.array_equal(idx.locate_quads(_i32(rows, dev)).cpu().numpy(), got)
 
 
 def test_fm_c2_index_lines_vs_rrr(dev):
@@ -190,6 +206,7 @@ def test_fm_c2_index_lines_vs_rrr(dev):
     dr = _i32(rows, dev)
     got = fm.locate_lines(dr).cpu().numpy()
     assert np.array_equal(got, fm.locate(dr).cpu().numpy())
+    assert np.array_equal(fm.locate_quads(dr).cpu().numpy(), got)
     assert np.array_equal(got[:50_000], O.fm_locate(f, rows[:50_000]))
 
 

@@ -51,10 +51,11 @@ def _check_lines_layout(idx, tok, bits):
     check_layout(idx.build_lines(), bits, recs, base)
 
 
-def expected_quads(tok, bits):
+def expected_quads(tok, bits, X=None):
     """The 4-ary wavelet matrix of `tok` as the layout stores it: records [L4][nrec][16] (counts of digits 0..2
-    before the record, then 13 words of 16 two-bit digits), Z [L4][4] and base [2^bits] = -(end of the walk of c
-    from 0), built with numpy stable sorts and cumulative counts."""
+    before the record, then 13 words of 16 two-bit digits), Z [L4][4] and base[c] = X[c] - (end of the walk of c
+    from 0) for c < X.size (X = zeros of 2^bits when not given), built with numpy stable sorts and cumulative
+    counts."""
     tok = np.asarray(tok, np.uint32)
     L4, n = (bits + 1) // 2, tok.size
     nrec = n // 208 + 1
@@ -76,12 +77,13 @@ def expected_quads(tok, bits):
         tot = [int(cl[v][n]) for v in range(4)]
         Z[lvl] = [0, tot[0], tot[0] + tot[1], tot[0] + tot[1] + tot[2]]
         S = S[np.argsort(d, kind="stable")]
-    cs = np.arange(1 << bits, dtype=np.int64)
+    X = np.zeros(1 << bits, np.int64) if X is None else np.asarray(X, np.int64)
+    cs = np.arange(X.size, dtype=np.int64)
     pw = np.zeros(cs.size, np.int64)
     for lvl in range(L4):
         d = (cs >> (2 * (L4 - 1 - lvl))) & 3
         pw = Z[lvl][d].astype(np.int64) + np.choose(d, [cums[lvl][v][pw] for v in range(4)])
-    return recs, Z, (-pw).astype(np.int32)
+    return recs, Z, (X - pw).astype(np.int32)
 
 
 def _quads(idx, tok, bits):
