@@ -34,7 +34,8 @@ HBM_PEAK_GBS = 8000.0
 # Infinity Cache (or HBM) serves (profiles/fm_c2.md).
 MEASURED_TRAFFIC = {("kv", 32768, 32): 2.0848e9, ("fm_count", 1 << 24, 1_000_000): 95.537e9,
                     ("fm_locate", 1 << 24, 900_000): 49.336e9, ("fm_count_lines", 1 << 24, 1_000_000): 32.44e9,
-                    ("fm_locate_lines", 1 << 24, 900_000): 25.99e9}
+                    ("fm_locate_lines", 1 << 24, 900_000): 25.99e9, ("fm_count_quads", 1 << 24, 1_000_000): 18.82e9,
+                    ("fm_locate_quads", 1 << 24, 900_000): 14.84e9}
 METRIC = "compressed-KV attn decode tokens/s + HBM GB/s fraction; wavelet rank Mq/s"
 
 
