@@ -390,8 +390,8 @@ def _sustained_time(fn, steps: int, warmup: int, warm_s: float):
 
 
 def bench_stream_read(buf, steps: int = 20, warmup: int = 3) -> dict:
-    """The device's achievable HBM read bandwidth: cf_stream_read_async (16-byte loads, each byte read once) over
-    `buf` (a uint8 device tensor of >= 2 GB, e.g. the KV pool itself)."""
+    """The device's achievable HBM read bandwidth: cf_stream_read_async (one workgroup per 64 KiB chunk, 16-byte
+    non-temporal loads, each byte read once) over `buf` (a uint8 device tensor of >= 2 GB, e.g. the KV pool itself)."""
     import torch
     from chromofold_amd import _abi as A
     A.declare("cf_stream_read_async", A.I32, [A.P, A.U64, A.P, A.P])

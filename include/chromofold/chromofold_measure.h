@@ -13,10 +13,11 @@
 extern "C" {
 #endif
 
-/* Read `bytes` bytes of device memory at `src` once (16-byte loads, every byte read exactly once, no writes but one
- * 32-bit XOR of all data per workgroup into *sink, which keeps the loads alive). src 16-byte aligned, bytes a
- * multiple of 16; sink device memory. Asynchronous on `stream`; allocates nothing. The achieved read bandwidth is
- * bytes / kernel time. */
+/* Read `bytes` bytes of device memory at `src` once (16-byte non-temporal loads, one workgroup per 64 KiB chunk,
+ * every byte read exactly once). Each workgroup folds its data into a 32-bit XOR and stores it to *sink only when it
+ * equals a fixed key: that keeps the loads alive without an atomic per workgroup, and the sink's value carries no
+ * meaning. src 16-byte aligned, bytes a multiple of 16; sink device memory. Asynchronous on `stream`; allocates
+ * nothing. The achieved read bandwidth is bytes / kernel time. */
 cf_status cf_stream_read_async(const void *src, uint64_t bytes, uint32_t *sink, void *stream);
 
 /* Cache bandwidth: `passes` passes over `bytes` at `src` with ordinary 16-byte loads, each pass giving every
