@@ -115,6 +115,30 @@ constexpr int buf_u32() {
   return words > red ? words : red;
 }
 
+// Max over the 64 lanes of four values at once, as wave-uniform values: v_max_f32_dpp within each row (quad_perm
+// [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror), then row_bcast:15 (rows 1, 3) and row_bcast:31 (rows 2, 3)
+// fold the rows into lane 63, which is read. One asm statement, so that nothing the compiler emits lands between
+// the steps: the four chains are interleaved, so each DPP source was written three VALU instructions earlier, and
+// the leading s_nop 1 gives the two wait states a DPP read needs after the write of its source before the block.
+// Replaces six rounds of ds_bpermute (an LDS round trip each) on the softmax's dependency chain: -2 to -3 % per
+// launch at C4.
+__device__ __forceinline__ void wave64_max4(float (&x)[4]) {
+#define CF_DPP4(CTL)                                                                                                \
+  "v_max_f32_dpp %0, %0, %0 " CTL "\n\tv_max_f32_dpp %1, %1, %1 " CTL "\n\tv_max_f32_dpp %2, %2, %2 " CTL        \
+  "\n\tv_max_f32_dpp %3, %3, %3 " CTL "\n\t"
+  asm volatile("s_nop 1\n\t"
+               CF_DPP4("quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf")
+               CF_DPP4("quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf")
+               CF_DPP4("row_half_mirror row_mask:0xf bank_mask:0xf")
+               CF_DPP4("row_mirror row_mask:0xf bank_mask:0xf")
+               CF_DPP4("row_bcast:15 row_mask:0xa bank_mask:0xf")
+               CF_DPP4("row_bcast:31 row_mask:0xc bank_mask:0xf")
+               : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]));
+#undef CF_DPP4
+#pragma unroll
+  for (int h = 0; h < 4; ++h) x[h] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x[h]), 63));
+}
+
 // Decode one page group (K scores, softmax, V accumulation).
 // RANS groups: `st` holds the chain's lane states on entry (K, V) and the states the group ends with on return;
 // the word streams are read through `wk` (the wave's LDS staging buffer, K stream then V); `raw` points at the
@@ -254,10 +278,8 @@ __device__ __forceinline__ void group_body(const Hook &after_decode, uint32_t (&
     s[h] = tok_ok ? (RANS ? (sa[h] + sb[h]) : (sa[h] + sb[h] - kOffset * qsum[h])) * ksc : -INFINITY;
     mx[h] = s[h];
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1)
-#pragma unroll
-    for (int h = 0; h < kGqa; ++h) mx[h] = fmaxf(mx[h], __shfl_xor(mx[h], o));
+  static_assert(kGqa == 4, "wave64_max4 reduces four heads");
+  wave64_max4(mx);
   // P.V runs on v_mfma_f32_16x16x32_f16 with k = 8 tokens of each of the 4 pages (page G's from lane group G), so
   // one MFMA sums all four pages: rows 0-3 are the 4 heads' hi parts of the weights p * v_scale, rows 4-7 their lo
   // parts (rows 8-15 repeat rows 0-7 and are dropped), 16 dims per MFMA. The lane's accumulators acc_v hold rows
