@@ -135,6 +135,29 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x + dpp_row<0x140>(x);
 }
 
+// Max / sum over the lanes {l, l ^ 16, l ^ 32, l ^ 48} (the same position in the four rows; every lane gets the
+// result) with gfx950's v_permlane16_swap / v_permlane32_swap, VALU exchanges that keep an LDS round trip
+// (ds_bpermute) off a softmax's dependency chain. Bit-identical to the xor-16 / xor-32 shuffle reductions: each
+// step combines the same pair of values in every lane. The max is a plain v_max_f32 (fmaxf would first canonicalise
+// both operands).
+__device__ __forceinline__ float vmax_f32(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float rows4_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = vmax_f32(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return vmax_f32(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows4_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // Global-address-space view of a generic pointer (one read from a struct or from LDS): its loads become global_load
 // (vmcnt only) instead of flat_load, which also counts in lgkmcnt, so that every wait for an LDS access would wait
 // for those loads too.

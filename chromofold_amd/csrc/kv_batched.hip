@@ -872,8 +872,7 @@ __global__ __launch_bounds__(kPfxThreads) void kv_prefix_kernel(cf_kv_batched_de
     for (int G = 0; G < 4; ++G)
 #pragma unroll
       for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[G][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = cfd::rows4_max(mx);
     const float mn = fmaxf(m, mx);
     const float alpha = m == -INFINITY ? 0.0f : __expf(m - mn);
     m = mn;
@@ -886,8 +885,7 @@ __global__ __launch_bounds__(kPfxThreads) void kv_prefix_kernel(cf_kv_batched_de
         st[G][r] = p;
         psum += p;
       }
-    psum += __shfl_xor(psum, 16);
-    psum += __shfl_xor(psum, 32);
+    psum = cfd::rows4_sum(psum);
     l = l * alpha + psum;
     // P V units: O is kept in units of 2^e with e = (exponent of the group's largest present-page V scale) - 15,
     // so the f16 operand p * v_scale * 2^-e stays below 2^15 whatever the V magnitude and weights down to 2^-29
