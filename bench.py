@@ -633,6 +633,9 @@ def bench_gather(steps: int, warmup: int, dim: int = 128, nq: int = 1 << 20) -> 
     def fused_lines():
         idx.gather_fused_lines_into(emb, dpos, out, stream=torch.cuda.current_stream())
 
+    def fused_quads():
+        idx.gather_fused_quads_into(emb, dpos, out, stream=torch.cuda.current_stream())
+
     def via_ids():
         A.check(L.cf_sparse_gather_async(ids.data_ptr(), emb.data_ptr(), dim, dpos.data_ptr(), out.data_ptr(), nq, s),
                 "cf_sparse_gather_async")
@@ -648,19 +651,27 @@ def bench_gather(steps: int, warmup: int, dim: int = 128, nq: int = 1 << 20) -> 
     torch.cuda.synchronize()
     assert torch.equal(out[torch.from_numpy(chk).to("cuda:0")], ref), "fused gather (lines) != emb[tok[pos]]"
     _, per_fl = _events_time(fused_lines, steps, warmup)
+    idx.build_quads(n)
+    out.fill_(float("nan"))
+    fused_quads()
+    torch.cuda.synchronize()
+    assert torch.equal(out[torch.from_numpy(chk).to("cuda:0")], ref), "fused gather (quads) != emb[tok[pos]]"
+    _, per_fq = _events_time(fused_quads, steps, warmup)
     A.check(L.cf_sparse_decode_all_async(v, ids.data_ptr(), n, s), "cf_sparse_decode_all_async")
     _, per_d = _events_time(lambda: A.check(L.cf_sparse_decode_all_async(v, ids.data_ptr(), n, s), "decode_all"),
                             steps, warmup)
     _, per_g = _events_time(via_ids, steps, warmup)
     torch.cuda.synchronize()
     assert torch.equal(out[torch.from_numpy(chk).to("cuda:0")], ref), "gather via ids != emb[tok[pos]]"
-    tf, tfl, td, tg = (float(np.mean(p)) * 1e-3 for p in (per_f, per_fl, per_d, per_g))
+    tf, tfl, tfq, td, tg = (float(np.mean(p)) * 1e-3 for p in (per_f, per_fl, per_fq, per_d, per_g))
     step_bytes = nq * 4 + nq * dim * 4
     return {"workload": f"{nq} positions into the C1 index, rows of {dim} fp32 from a {vocab}-row table",
             "fused_ms": tf * 1e3, "fused_mqs": nq / tf / 1e6, "fused_gbs": step_bytes / tf / 1e9,
             "fused_roofline_frac": step_bytes / tf / 1e9 / HBM_PEAK_GBS,
             "fused_lines_ms": tfl * 1e3, "fused_lines_gbs": step_bytes / tfl / 1e9,
             "fused_lines_roofline_frac": step_bytes / tfl / 1e9 / HBM_PEAK_GBS,
+            "fused_quads_ms": tfq * 1e3, "fused_quads_gbs": step_bytes / tfq / 1e9,
+            "fused_quads_roofline_frac": step_bytes / tfq / 1e9 / HBM_PEAK_GBS,
             "decode_all_ms": td * 1e3, "gather_via_ids_ms": tg * 1e3,
             "decode_all_plus_gather_ms": (td + tg) * 1e3}
 

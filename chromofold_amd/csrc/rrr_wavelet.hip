@@ -148,6 +148,28 @@ __global__ __launch_bounds__(kThreads) void rrrw_rank_quads_kernel(const uint32_
   out[t] = static_cast<uint32_t>(static_cast<int32_t>(a) + base[c]);
 }
 
+// cf_sparse_gather_fused_async over the 4-ary layout: lane = query (its access walk, one record per 4-ary level),
+// then the wave copies its 64 rows (gather_core.hpp).
+template <int L4, bool VEC>
+__global__ __launch_bounds__(kThreads) void sparse_fused_quads_kernel(const uint32_t *__restrict__ quads, uint32_t nrec,
+                                                                      uint32_t nlev, const float *__restrict__ emb,
+                                                                      int dim, const uint32_t *__restrict__ pos,
+                                                                      float *__restrict__ out, size_t count) {
+  const size_t q0 = (blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x) & ~size_t(63);
+  if (q0 >= count) return;  // wave-uniform
+  const size_t t = q0 + (threadIdx.x & 63u);
+  const uint32_t L = L4 > 0 ? static_cast<uint32_t>(L4) : nlev;
+  const uint32_t *Z = quads + static_cast<size_t>(L) * nrec * cfq::kRecWords;
+  uint32_t a = t < count ? pos[t] : 0u, id = 0;
+  for (uint32_t l = 0; l < L; ++l) {
+    uint32_t d;
+    a = cfq::step<true>(quads, nrec, Z, l, a, 0u, &d);
+    id = (id << 2) | d;
+  }
+  const int nq = static_cast<int>(count - q0 < 64 ? count - q0 : 64);
+  cfg::copy_rows<VEC>(id, nq, emb, static_cast<uint64_t>(dim), out, q0);
+}
+
 template <int LEVELS>
 __global__ __launch_bounds__(kThreads) void rrrw_rank_lines_kernel(cf_rrrw_view v, const uint32_t *__restrict__ lines,
                                                                    uint32_t nrec, const uint32_t *__restrict__ sym,
@@ -265,6 +287,26 @@ extern "C" cf_status cf_rrrw_rank_quads_async(cf_rrrw_view v, uint64_t n, const 
     rrrw_rank_quads_kernel<8><<<g, kThreads, 0, s>>>(quads, nrec, L4, mask, symbols, positions, out, count);
   else
     rrrw_rank_quads_kernel<0><<<g, kThreads, 0, s>>>(quads, nrec, L4, mask, symbols, positions, out, count);
+  return cfd::launch_status();
+}
+
+extern "C" cf_status cf_sparse_gather_fused_quads_async(cf_rrrw_view v, uint64_t n, const uint32_t *quads,
+                                                        const float *emb, int dim, const uint32_t *pos, float *out,
+                                                        size_t count, void *stream) {
+  if (!quads_view_ok(v, n) || !quads || (reinterpret_cast<uintptr_t>(quads) & 15u) != 0 || !emb || !pos || !out)
+    return CF_ERR_INVALID_ARGUMENT;
+  if (count == 0 || dim <= 0) return CF_OK;
+  const hipStream_t s = cfd::as_stream(stream);
+  const unsigned g = cfd::grid_for(count, kThreads);
+  const uint32_t nrec = cfq::nrec_for(n), L4 = cfq::levels_for(v.bits);
+  const bool vec = cfg::vec4_ok(emb, out, static_cast<uint64_t>(dim));
+#define CF_FUSED(L, V) sparse_fused_quads_kernel<L, V><<<g, kThreads, 0, s>>>(quads, nrec, L4, emb, dim, pos, out, count)
+  if (L4 == 8) {
+    if (vec) CF_FUSED(8, true); else CF_FUSED(8, false);
+  } else {
+    if (vec) CF_FUSED(0, true); else CF_FUSED(0, false);
+  }
+#undef CF_FUSED
   return cfd::launch_status();
 }
 

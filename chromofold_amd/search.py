@@ -151,6 +151,17 @@ class RrrWaveletIndex:
                                                            stream_ptr(stream)),
                 "cf_sparse_gather_fused_lines_async")
 
+    def gather_fused_quads_into(self, emb: torch.Tensor, positions: torch.Tensor, out: torch.Tensor,
+                                stream=None) -> None:
+        """out[t, :] = emb[access(positions[t]), :] over the 4-ary layout (cf_sparse_gather_fused_quads_async);
+        build_quads(n) first."""
+        if self.quads is None:
+            raise A.CfError(A.CF_ERR_INVALID_ARGUMENT, "cf_sparse_gather_fused_quads_async: build_quads(n) first")
+        A.check(A.lib().cf_sparse_gather_fused_quads_async(self.view(), self.quads_n, _ptr(self.quads), _ptr(emb),
+                                                           emb.shape[1], _ptr(positions), _ptr(out), positions.numel(),
+                                                           stream_ptr(stream)),
+                "cf_sparse_gather_fused_quads_async")
+
     def rank(self, symbols: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
         out = torch.empty_like(positions, dtype=torch.int32)
         self.rank_into(symbols, positions, out)
@@ -330,6 +341,8 @@ A.declare("cf_rrrw_quads_build_async", A.I32, [A.cf_rrrw_view, A.U64, A.P, A.U64
 A.declare("cf_rrrw_access_quads_async", A.I32, [A.cf_rrrw_view, A.U64, A.P, A.P, A.P, A.SZ, A.P])
 A.declare("cf_rrrw_rank_quads_async", A.I32, [A.cf_rrrw_view, A.U64, A.P, A.P, A.P, A.P, A.SZ, A.P])
 A.declare("cf_sparse_gather_fused_lines_async", A.I32, [A.cf_rrrw_view, A.P, A.P, C.c_int, A.P, A.P, A.SZ, A.P])
+A.declare("cf_sparse_gather_fused_quads_async", A.I32,
+          [A.cf_rrrw_view, A.U64, A.P, A.P, C.c_int, A.P, A.P, A.SZ, A.P])
 A.declare("cf_fm_lines_bytes", A.U64, [A.cf_fm_view])
 A.declare("cf_fm_lines_build_async", A.I32, [A.cf_fm_view, A.P, A.U64, A.P])
 A.declare("cf_fm_count_lines_async", A.I32, [A.cf_fm_view, A.P, A.P, A.P, A.P, A.P, A.SZ, A.P])

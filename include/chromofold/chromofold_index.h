@@ -121,6 +121,12 @@ cf_status cf_rrrw_rank_quads_async(cf_rrrw_view v, uint64_t n, const uint32_t *q
 cf_status cf_sparse_gather_fused_lines_async(cf_rrrw_view v, const uint32_t *lines, const float *emb, int dim,
                                              const uint32_t *pos, float *out, size_t count, void *stream);
 
+/* The same gather over the 4-ary layout (cf_rrrw_quads_build_async, n the sequence's length): each query's access
+ * walk reads one 64-byte record per 4-ary level (8 at 15 bits instead of the line layout's 15). Same bytes out, same
+ * argument rules; quads 16-byte aligned. */
+cf_status cf_sparse_gather_fused_quads_async(cf_rrrw_view v, uint64_t n, const uint32_t *quads, const float *emb,
+                                             int dim, const uint32_t *pos, float *out, size_t count, void *stream);
+
 /* ---- derived on-device line layout for FM search (no counterpart in the reference; the .cffm on disk and the
  * cf_fm_view arrays are unchanged). Built once per loaded index from its cf_fm_view; the search entry points below
  * return exactly what cf_fm_count_async / cf_fm_ranges_async / cf_fm_locate_async return for the same view, with one

@@ -193,6 +193,10 @@ def test_rrr_sparse_gathers(dev, bits, n):
         g3 = torch.full((K, dim), float("nan"), device=dev)
         idx.gather_fused_lines_into(dE, dp, g3)  # the same gather over the line layout
         assert np.array_equal(g3.cpu().numpy(), E[tok[pos]])
+        g4 = torch.full((K, dim), float("nan"), device=dev)
+        idx.build_quads(n)
+        idx.gather_fused_quads_into(dE, dp, g4)  # and over the 4-ary layout
+        assert np.array_equal(g4.cpu().numpy(), E[tok[pos]])
         g2 = torch.full((K, dim), float("nan"), device=dev)
         _ok(_lib().cf_sparse_gather_async(ids.data_ptr(), dE.data_ptr(), dim, dp.data_ptr(), g2.data_ptr(), K, None),
             "gather")
