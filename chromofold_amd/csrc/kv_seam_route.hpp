@@ -9,7 +9,7 @@
 //      rANS page (the seam's tag) of the call's head_dim with 1..64 tokens and 16-byte aligned tables, and the K/V
 //      table pointers of the first;
 //   2. seam_group_kernel: each workgroup combines its head's chunk records (the route takes the head when every
-//      page qualifies and all share one pair of K/V tables; the first split's workgroup publishes the verdict); for
+//      page qualifies and all share one pair of K/V tables; the first split's workgroup publishes the decision); for
 //      a head it takes, each wavefront decodes whole pages with the batched decode's group body (both chains
 //      interleaved in one wavefront, QK^T on the GQA heads' MFMA broadcast, P.V on v_mfma_f32_16x16x32_f16) and
 //      writes split partials in the seam's layout, slots [0, splits);
