@@ -14,7 +14,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr uint64_t kChunk16 = 4096;  // 16-byte units per chunk (64 KiB)
-constexpr uint32_t kKey = 0x2545F491u;  // a workgroup fold equal to this is stored (keeps the loads alive)
+constexpr uint32_t kKey = CF_MEASURE_FOLD_KEY;  // a workgroup fold equal to this is stored (keeps the loads alive)
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // The workgroup's XOR of `acc`, stored to *sink if it equals kKey.

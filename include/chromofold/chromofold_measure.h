@@ -13,10 +13,13 @@
 extern "C" {
 #endif
 
+/* The fixed key of the measurement kernels' folds (below). */
+#define CF_MEASURE_FOLD_KEY 0x2545F491u
+
 /* Read `bytes` bytes of device memory at `src` once (16-byte non-temporal loads, one workgroup per 64 KiB chunk,
- * every byte read exactly once). Each workgroup folds its data into a 32-bit XOR and stores it to *sink only when it
- * equals a fixed key: that keeps the loads alive without an atomic per workgroup, and the sink's value carries no
- * meaning. src 16-byte aligned, bytes a multiple of 16; sink device memory. Asynchronous on `stream`; allocates
+ * every byte read exactly once). Each workgroup folds its chunk into a 32-bit XOR of its 32-bit words and stores it
+ * to *sink only when it equals CF_MEASURE_FOLD_KEY: that keeps the loads alive without an atomic per workgroup, and
+ * for ordinary data the sink is left as it was. src 16-byte aligned, bytes a multiple of 16; sink device memory. Asynchronous on `stream`; allocates
  * nothing. The achieved read bandwidth is bytes / kernel time. */
 cf_status cf_stream_read_async(const void *src, uint64_t bytes, uint32_t *sink, void *stream);
 
