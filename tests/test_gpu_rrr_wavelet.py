@@ -135,8 +135,11 @@ def test_tiny_cfrw_fixture(dev):
     assert np.array_equal(_quads_rank(idx, d["rank_c"], d["rank_i"]), d["rank_golden"])
 
 
+# sizes at and just past the 4-ary layout's 208-digit records (208, 209, 416, 624), and 22 / 24 bits (the layouts'
+# widest symbols)
 @pytest.mark.parametrize("n,bits,seed", [(1, 1, 1), (15, 3, 2), (16, 4, 3), (961, 5, 4), (4095, 9, 5),
-                                         (65536, 15, 6), (100003, 16, 7), (30000, 17, 8)])
+                                         (65536, 15, 6), (100003, 16, 7), (30000, 17, 8), (208, 2, 9), (416, 6, 10),
+                                         (209, 7, 11), (624, 8, 12), (20000, 22, 13), (3000, 24, 14)])
 def test_random_shapes_vs_closed_form(dev, n, bits, seed):
     from chromofold_amd.search import to_u32, u32_dev
     rng = np.random.default_rng(seed)
