@@ -1202,91 +1202,149 @@ __global__ CF_KV_OCC __launch_bounds__(64 * kWavesNarrow) void seam_group_kernel
   uint32_t *buf = s_buf[__builtin_amdgcn_readfirstlane(wave)];
   bool bad = false;
   uint32_t pre[14];
-  auto noop = []() {};
-  // the page entry of ordinal o (wave-uniform: a scalar load), the next one loaded while the current page is decoded
+#pragma unroll
+  for (int w = 0; w < 14; ++w) pre[w] = 0;
+  // the page entry of ordinal o (wave-uniform: a scalar load)
   auto entry_of = [&](uint32_t o) {
     const uint32_t oc = static_cast<uint32_t>(__builtin_popcountll(__builtin_amdgcn_ballot_w64(cinc <= o)));
     const uint32_t li = __builtin_amdgcn_readfirstlane(oc * kRouteChunk + o - __shfl(cexc, static_cast<int>(oc)));
     return list[li];
   };
   const uint32_t ostep = splits * static_cast<uint32_t>(W);
-  uint32_t o = split + splits * static_cast<uint32_t>(wave);
-  uint4 ent = o < n ? entry_of(o) : uint4{0, 0, 0, 0};
-  for (uint32_t on; o < n; o = on) {
-    on = o + ostep;
-    const uint4 e = ent;
-    if (on < n) ent = entry_of(on);
-    const uint32_t tb = e.z, tcnt = e.w;
-    if (tb > qtok || tb + tcnt <= wlo) continue;  // wholly outside the visible range: skipped unread
-    const uint8_t *blob = reinterpret_cast<const uint8_t *>(e.x | (static_cast<uint64_t>(e.y) << 32));
-    const uint32_t codec = *reinterpret_cast<const uint32_t *>(blob);
-    const uint32_t cnt = *reinterpret_cast<const uint32_t *>(blob + 4);
-    const uint32_t chain = *reinterpret_cast<const uint16_t *>(blob + 8);
-    const uint32_t bd = *reinterpret_cast<const uint16_t *>(blob + 20);
-    const uint16_t *tch = reinterpret_cast<const uint16_t *>(blob + 12);
-    // a self-contained group of this head_dim whose token counts match the page: full 16-token pages, then at most
-    // one partial page, then empty ones (the seam's rule, kv_legacy.hip rans_stream_to_lds)
+  // the first ordinal from o on (in steps of ostep) whose page has a token in [window begin, query token], and its
+  // entry; pages wholly outside that range are skipped unread
+  auto next_visible = [&](uint32_t o, uint4 &e) {
+    for (; o < n; o += ostep) {
+      e = entry_of(o);
+      if (!(e.z > qtok || e.z + e.w <= wlo)) break;
+    }
+    return o;
+  };
+  // A page's header: loaded one page ahead (while the page before it is decoded). Its lane states, first raw words
+  // and word streams are loaded only once the header has passed the checks, during the previous page's softmax / V
+  // phase (its raw words through group_body's next-group refill).
+  struct Hdr {
+    const uint8_t *blob;
+    uint32_t tb, tcnt, codec, cnt, chain, bd, tc01, tc23;
+    float ks, vs;
+  };
+  auto load_hdr = [&](const uint4 &e) {
+    Hdr h;
+    h.blob = reinterpret_cast<const uint8_t *>(e.x | (static_cast<uint64_t>(e.y) << 32));
+    h.tb = e.z;
+    h.tcnt = e.w;
+    h.codec = *reinterpret_cast<const uint32_t *>(h.blob);
+    h.cnt = *reinterpret_cast<const uint32_t *>(h.blob + 4);
+    h.chain = *reinterpret_cast<const uint16_t *>(h.blob + 8);
+    h.tc01 = *reinterpret_cast<const uint32_t *>(h.blob + 12);
+    h.tc23 = *reinterpret_cast<const uint32_t *>(h.blob + 16);
+    h.bd = *reinterpret_cast<const uint16_t *>(h.blob + 20);
+    h.ks = reinterpret_cast<const float *>(h.blob + 32)[G];
+    h.vs = reinterpret_cast<const float *>(h.blob + 48)[G];
+    return h;
+  };
+  // a self-contained group of this head_dim whose token counts match the page: full 16-token pages, then at most one
+  // partial page, then empty ones (the seam's rule, kv_legacy.hip rans_stream_to_lds)
+  auto page_ok = [&](const Hdr &h) {
+    bool valid = h.bd == static_cast<uint32_t>(D) &&
+                 (h.codec == CF_KV_CODEC_INT8 || (h.codec == CF_KV_CODEC_RANS_HYBRID && h.chain == 1));
     uint32_t total = 0;
-    bool valid = bd == static_cast<uint32_t>(D) &&
-                 (codec == CF_KV_CODEC_INT8 || (codec == CF_KV_CODEC_RANS_HYBRID && chain == 1));
     bool open = true;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const uint32_t c = tch[g];
+      const uint32_t c = ((g < 2 ? h.tc01 : h.tc23) >> (16 * (g & 1))) & 0xFFFFu;
       valid &= c <= 16u && (c == 0 || open);
       open &= c == 16u;
       total += c;
     }
-    const uint32_t nk = cnt & 0xFFFFu, nv = cnt >> 16;
-    valid &= total == tcnt && (codec != CF_KV_CODEC_RANS_HYBRID || nk + nv <= kCapWords);
-    if (!valid) {
+    const uint32_t nk = h.cnt & 0xFFFFu, nv = h.cnt >> 16;
+    return valid && total == h.tcnt && (h.codec != CF_KV_CODEC_RANS_HYBRID || nk + nv <= kCapWords);
+  };
+  auto raw_of = [&](const Hdr &h) { return reinterpret_cast<const uint32_t *>(h.blob + kHdr + kStateBytes); };
+  uint32_t st_next[2] = {0, 0};
+  // lane states and word streams of a checked RANS page into registers / the wave's buffer (whole 16-byte chunks:
+  // blobs are padded to 16 bytes)
+  auto stage_page = [&](const Hdr &h) {
+    const uint32_t *hs = reinterpret_cast<const uint32_t *>(h.blob + kHdr);
+    st_next[0] = hs[lane];
+    st_next[1] = hs[64 + lane];
+    constexpr int kStage16 = ((kCapWords * 2) + 1023) / 1024;
+    const uint32_t nbytes = (((h.cnt & 0xFFFFu) + (h.cnt >> 16)) * 2u + 15u) & ~15u;
+    const uint8_t *src = reinterpret_cast<const uint8_t *>(raw_of(h) + 2 * RAW) + 16u * lane;
+#pragma unroll
+    for (int k = 0; k < kStage16; ++k)
+      if (1024u * k + 16u * lane < nbytes)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t *>(src + 1024 * k),
+                                         (__attribute__((address_space(3))) void *)(buf + 256 * k), 16, 0, 0);
+  };
+  uint4 ec = {0, 0, 0, 0};
+  uint32_t o = next_visible(split + splits * static_cast<uint32_t>(wave), ec);
+  Hdr cur = o < n ? load_hdr(ec) : Hdr{};
+  bool cur_ok = o < n && page_ok(cur);
+  if (cur_ok && cur.codec == CF_KV_CODEC_RANS_HYBRID) {  // the wave's first page: nothing to overlap it with
+    const uint32_t *raw = raw_of(cur);
+#pragma unroll
+    for (int w = 0; w < 7; ++w) {
+      pre[w] = raw[w * 64 + lane];
+      pre[7 + w] = raw[RAW + w * 64 + lane];
+    }
+    stage_page(cur);
+  }
+  uint4 en = {0, 0, 0, 0};
+  uint32_t on = o < n ? next_visible(o + ostep, en) : n;
+  while (o < n) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this page's states and word streams have landed
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    uint32_t st[2] = {st_next[0], st_next[1]};
+    const Hdr nx = on < n ? load_hdr(en) : Hdr{};
+    uint4 en2 = {0, 0, 0, 0};
+    const uint32_t on2 = on < n ? next_visible(on + ostep, en2) : n;
+    const bool nx_ok = on < n && page_ok(nx);
+    const bool next_rans = nx_ok && nx.codec == CF_KV_CODEC_RANS_HYBRID;
+    const uint32_t *nlw = next_rans ? raw_of(nx) : nullptr;
+    auto stage_next = [&]() {  // the word buffer is free: the next page's states and word streams
+      if (next_rans) stage_page(nx);
+    };
+    if (!cur_ok) {
       bad = true;
-      continue;
-    }
-    const uint32_t tcG = tch[G];
-    const float ks = reinterpret_cast<const float *>(blob + 32)[G];
-    const float vs = reinterpret_cast<const float *>(blob + 48)[G];
-    const uint32_t pos = tb + 16u * static_cast<uint32_t>(G) + static_cast<uint32_t>(t);
-    const bool tok_ok = static_cast<uint32_t>(t) < tcG && pos >= wlo && pos <= qtok;
-    // any token of the lane's 16-token page visible (behind a window the visible tokens can be a page's suffix)
-    const uint32_t pg0 = tb + 16u * static_cast<uint32_t>(G);
-    const bool page_vis = tcG > 0 && pg0 <= qtok && pg0 + tcG - 1 >= wlo;
-    if (codec == CF_KV_CODEC_RANS_HYBRID) {
-      const uint32_t *hs = reinterpret_cast<const uint32_t *>(blob + kHdr);
-      uint32_t st[2] = {hs[lane], hs[64 + lane]};
-      const uint32_t *raw = reinterpret_cast<const uint32_t *>(blob + kHdr + kStateBytes);
+      if (next_rans) {
 #pragma unroll
-      for (int w = 0; w < 7; ++w) {
-        pre[w] = raw[w * 64 + lane];
-        pre[7 + w] = raw[RAW + w * 64 + lane];
+        for (int w = 0; w < 7; ++w) {
+          pre[w] = nlw[w * 64 + lane];
+          pre[7 + w] = nlw[RAW + w * 64 + lane];
+        }
       }
-      // the word streams into the wave's buffer (whole 16-byte chunks: blobs are padded to 16 bytes)
-      constexpr int kStage16 = ((kCapWords * 2) + 1023) / 1024;
-      const uint32_t nbytes = ((nk + nv) * 2u + 15u) & ~15u;
-      const uint8_t *src = reinterpret_cast<const uint8_t *>(raw + 2 * RAW) + 16u * lane;
-#pragma unroll
-      for (int k = 0; k < kStage16; ++k)
-        if (1024u * k + 16u * lane < nbytes)
-          __builtin_amdgcn_global_load_lds(reinterpret_cast<const uint32_t *>(src + 1024 * k),
-                                           (__attribute__((address_space(3))) void *)(buf + 256 * k), 16, 0, 0);
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      uint32_t ends[2];
-      group_body<D, CF_KV_CODEC_RANS_HYBRID, 0, const uint16_t *, decltype(noop), true, true>(
-          noop, pre, nullptr, st, raw, reinterpret_cast<const uint16_t *>(buf), cnt, s_tab, qhi, qlo, qsum,
-          s_p[wave], nullptr, lane, tok_ok, ks, vs, e_run, m_run, l_run, acc_v, ends, page_vis);
-      // a group coded on its own ends where the encoder started (2^16 in every lane) and consumed exactly its words
-      const bool ok = st[0] == 65536u && st[1] == 65536u && ends[0] == nk && ends[1] == nk + nv;
-      bad |= __builtin_amdgcn_ballot_w64(!ok) != 0;
+      stage_next();
     } else {
-      uint32_t st[2] = {0, 0};
-      group_body<D, CF_KV_CODEC_INT8, 0, const uint16_t *, decltype(noop), false, true>(
-          noop, pre, nullptr, st, reinterpret_cast<const uint32_t *>(blob + kHdr),
-          static_cast<const uint16_t *>(nullptr), 0, s_tab, qhi, qlo, qsum, s_p[wave], nullptr, lane, tok_ok, ks, vs,
-          e_run, m_run, l_run, acc_v, nullptr, page_vis);
+      const uint32_t tcG = ((G < 2 ? cur.tc01 : cur.tc23) >> (16 * (G & 1))) & 0xFFFFu;
+      const uint32_t pos = cur.tb + 16u * static_cast<uint32_t>(G) + static_cast<uint32_t>(t);
+      const bool tok_ok = static_cast<uint32_t>(t) < tcG && pos >= wlo && pos <= qtok;
+      // any token of the lane's 16-token page visible (behind a window the visible tokens can be a page's suffix)
+      const uint32_t pg0 = cur.tb + 16u * static_cast<uint32_t>(G);
+      const bool page_vis = tcG > 0 && pg0 <= qtok && pg0 + tcG - 1 >= wlo;
+      if (cur.codec == CF_KV_CODEC_RANS_HYBRID) {
+        uint32_t ends[2];
+        group_body<D, CF_KV_CODEC_RANS_HYBRID, 0, const uint16_t *, decltype(stage_next), true, true>(
+            stage_next, pre, nlw, st, raw_of(cur), reinterpret_cast<const uint16_t *>(buf), cur.cnt, s_tab, qhi, qlo,
+            qsum, s_p[wave], nullptr, lane, tok_ok, cur.ks, cur.vs, e_run, m_run, l_run, acc_v, ends, page_vis);
+        // a group coded on its own ends where the encoder started (2^16 in every lane) and consumed exactly its words
+        const uint32_t nk = cur.cnt & 0xFFFFu, nv = cur.cnt >> 16;
+        const bool ok = st[0] == 65536u && st[1] == 65536u && ends[0] == nk && ends[1] == nk + nv;
+        bad |= __builtin_amdgcn_ballot_w64(!ok) != 0;
+      } else {
+        group_body<D, CF_KV_CODEC_INT8, 0, const uint16_t *, decltype(stage_next), false, true>(
+            stage_next, pre, nlw, st, reinterpret_cast<const uint32_t *>(cur.blob + kHdr),
+            static_cast<const uint16_t *>(nullptr), 0, s_tab, qhi, qlo, qsum, s_p[wave], nullptr, lane, tok_ok,
+            cur.ks, cur.vs, e_run, m_run, l_run, acc_v, nullptr, page_vis);
+      }
     }
+    cur = nx;
+    cur_ok = nx_ok;
+    o = on;
+    on = on2;
+    en = en2;
   }
 
   // ---- reduce the wavefront (as kv_batched_kernel), then merge the wavefronts into the slot
