@@ -920,8 +920,17 @@ __global__ __launch_bounds__(kMaxD) void seam_merge_kernel(cf_kv_paged_attention
   }
   __syncthreads();
   if (dd >= HD) return;
+  // the splits' rows in batches of 32, then 8, then one at a time: each batch's loads are in flight together (one
+  // L2 round trip per batch, not per 8 splits), and the sum keeps the ascending split order
   float o = 0.0f;
   uint32_t s = 0;
+  for (; s + 32 <= splits; s += 32) {
+    float x[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) x[j] = base[(s + j) * stride + dd];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) o += x[j] * s_sc[s + j];
+  }
   for (; s + 8 <= splits; s += 8) {
     float x[8];
 #pragma unroll
