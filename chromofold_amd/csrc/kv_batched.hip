@@ -959,21 +959,39 @@ __global__ __launch_bounds__(kGqa * D) void kv_merge_kernel(cf_kv_batched_desc d
   const uint32_t gqa = d.query_head_count / d.kv_head_count;
   if (static_cast<uint32_t>(h) >= gqa) return;
   const float *pp = partial + (static_cast<size_t>(seq) * d.kv_head_count + head) * splits * (kGqa * (D + 2));
+  // eight splits' values loaded at a time (indices clamped to the last split), combined in ascending split order
+  constexpr uint32_t kB = 8;
   float m = -INFINITY;
   bool nan = false;  // a NaN partial (a coded prefix group, see kv_prefix_kernel) makes the row NaN
-  for (uint32_t s = 0; s < splits; ++s) {
-    const float ms = pp[s * (kGqa * (D + 2)) + h * (D + 2) + D];
-    nan |= ms != ms;
-    m = fmaxf(m, ms);  // fmaxf drops a NaN, hence the flag
+  for (uint32_t s0 = 0; s0 < splits; s0 += kB) {
+    float ms[kB];
+#pragma unroll
+    for (uint32_t u = 0; u < kB; ++u) ms[u] = pp[min(s0 + u, splits - 1u) * (kGqa * (D + 2)) + h * (D + 2) + D];
+#pragma unroll
+    for (uint32_t u = 0; u < kB; ++u)
+      if (s0 + u < splits) {
+        nan |= ms[u] != ms[u];
+        m = fmaxf(m, ms[u]);  // fmaxf drops a NaN, hence the flag
+      }
   }
   float l = 0.0f, o = 0.0f;
   if (m != -INFINITY)
-    for (uint32_t s = 0; s < splits; ++s) {
-      const float *q = pp + s * (kGqa * (D + 2)) + h * (D + 2);
-      if (q[D] == -INFINITY) continue;
-      const float sc = __expf(q[D] - m);
-      l += q[D + 1] * sc;
-      o += q[dd] * sc;
+    for (uint32_t s0 = 0; s0 < splits; s0 += kB) {
+      float mq[kB], lq[kB], oq[kB];
+#pragma unroll
+      for (uint32_t u = 0; u < kB; ++u) {
+        const float *q = pp + min(s0 + u, splits - 1u) * (kGqa * (D + 2)) + h * (D + 2);
+        mq[u] = q[D];
+        lq[u] = q[D + 1];
+        oq[u] = q[dd];
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < kB; ++u) {
+        if (s0 + u >= splits || mq[u] == -INFINITY) continue;
+        const float sc = __expf(mq[u] - m);
+        l += lq[u] * sc;
+        o += oq[u] * sc;
+      }
     }
   // 0 when no token is visible
   d.output[(static_cast<size_t>(seq) * d.query_head_count + head * gqa + h) * D + dd] =
